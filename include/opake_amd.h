@@ -1,0 +1,183 @@
+/*
+ * opake_amd — C ABI of the MI355X (gfx950) DP-SGD clip -> sum -> noise step.
+ *
+ * Conventions for every entry point:
+ *   - all pointers are device pointers owned by the caller (inputs are
+ *     borrowed and never written, outputs are written in full);
+ *   - work is enqueued asynchronously on `stream` (a hipStream_t passed as
+ *     void*; NULL is the default stream); nothing blocks the host;
+ *   - the library allocates no device memory: scratch comes in through the
+ *     `ws` / `ws_bytes` pair, sized with the matching *_workspace_bytes query;
+ *   - the return value is DPC_OK or a negative status:
+ *       DPC_EINVAL  bad shape, dtype, pointer or argument,
+ *       DPC_ENOTSUP a valid call this build does not implement,
+ *       DPC_ENOSPC  workspace too small,
+ *       DPC_EHIP    the HIP runtime reported an error at launch.
+ *   - tensors are dense row-major; `dtype` values are enum dpc_dtype.
+ *
+ * Reference interfaces named below are files of JetBrains-Research/opake.
+ */
+#ifndef OPAKE_AMD_H
+#define OPAKE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DPC_OK 0
+#define DPC_EINVAL (-22)
+#define DPC_ENOTSUP (-95)
+#define DPC_ENOSPC (-28)
+#define DPC_EHIP (-1000)
+
+enum dpc_dtype { DPC_F32 = 0, DPC_BF16 = 1 };
+enum dpc_scale_kind { DPC_SCALE_FIXED = 0, DPC_SCALE_AUTO_S = 1 };
+enum dpc_noise_mode { DPC_NOISE_NONE = 0, DPC_NOISE_INJECTED = 1, DPC_NOISE_PHILOX = 2 };
+
+/* Library ABI version (major * 100 + minor). */
+int dpc_version(void);
+
+/* Last HIP error string recorded by a failing call on this thread. */
+const char* dpc_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * Per-example squared gradient norms of linear layers (ghost / Gram norm).
+ *
+ * Replaces the norm pass over materialised per-example weight gradients:
+ * `vmap(grad)` in packages/opake-engine/src/opake/api/engine/clipping/
+ * _clipped_grad.py:278-296 followed by the per-leaf sum of squares of
+ * _streaming.py:70-82 (`_leaf_sq_sum`, _pytree.py:286-314).  For a layer
+ * with inputs A_i [T, din] and output gradients G_i [T, dout] the
+ * per-example weight gradient is G_i^T A_i, and
+ *     ||G_i^T A_i||_F^2 = <A_i A_i^T, G_i G_i^T>.
+ *
+ * dpc_gram_sqnorms: A [B, T, din], G [B, T, dout] in `dtype`.  Adds (or, if
+ * accumulate == 0, writes) ||G_i^T A_i||^2 to sqnorm[i] (float64, [B]).  A
+ * layer bias adds ||sum_t G_i[t]||^2 when with_bias != 0.  Examples whose
+ * A_i or G_i hold NaN/Inf produce a non-finite value (their clip factor
+ * becomes 0).
+ * -------------------------------------------------------------------------*/
+size_t dpc_gram_workspace_bytes(int B, int T);
+int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int din, int dout, int dtype,
+                     int with_bias, int accumulate, double* sqnorm, void* ws, size_t ws_bytes,
+                     void* stream);
+
+/* Flat inputs (T == 1): a [B, din], g [B, dout];
+ * sqnorm[i] (+)= ||a_i||^2 ||g_i||^2 (+ ||g_i||^2 with a bias). */
+int dpc_flat_sqnorms(const void* a, const void* g, int B, int din, int dout, int dtype,
+                     int with_bias, int accumulate, double* sqnorm, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Clip factors from squared norms.
+ *
+ * Replaces the ratio and scale computation of _streaming.py:84-108 and
+ * _pytree.py:111-157 (`_guard_scale` / `_finalize_scale`), evaluated in
+ * float64:
+ *   norm   = sqrt(sqnorm[i])
+ *   ratio  = max(C, 0) / norm                      (kind FIXED)
+ *          = max(C, 0) / (norm + gamma)            (kind AUTO_S)
+ *   s      = ratio * guard_rel[g] - guard_abs[g]
+ *   s      = min(1, s)                             (FIXED only)
+ *   s      = isfinite(s) ? max(s, 0) : 0
+ *   scale[g * B + i] = (float)s                    for each guard g < n_guards
+ * norms_out[i] = (float)norm; *nclipped = #{i : (float)norm > count_threshold}
+ * (the reference's strict `norms > clipping_norm`, _clipped_fun.py:348-396).
+ * guard_rel / guard_abs are HOST arrays of n_guards (1..4) values, one
+ * pair per storage dtype.  sqnorm and all outputs are device pointers.
+ * Any output pointer may be NULL.  `plan` (nullable, device memory of
+ * dpc_clip_plan_bytes(B) bytes) receives the ordered list of examples whose
+ * guard-0 scale is positive; the clipped-sum GEMM walks only those.
+ * -------------------------------------------------------------------------*/
+size_t dpc_clip_plan_bytes(int B);
+int dpc_clip_factors(const double* sqnorm, int B, double C, int kind, double gamma,
+                     const double* guard_rel, const double* guard_abs, int n_guards,
+                     float count_threshold, float* scale, float* norms_out, int* nclipped,
+                     void* plan, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Clipped batch sum of a linear layer with the noise epilogue fused.
+ *
+ * Replaces the apply pass of _streaming.py:137-167 (scale, store, batch sum
+ * via `reduce_leaf`), the `x / normalize_by` of _clipped_fun.py:880-883 and
+ * the per-leaf Gaussian draw + add of packages/opake-dpsgd/src/opake/api/
+ * dpsgd/noise/_gaussian.py:188-229:
+ *   acc[m, n] = sum_i scale[i] * sum_t G[i, t, m] * A[i, t, n]   (fp32)
+ *   v = to_out(acc); if normalize_by != 1: v = to_out(float(v) / normalize_by)
+ *   if sigma != 0: v = to_out(float(v) + (float)sigma * z[m, n])
+ *   out[m, n] = v             (out is [dout, din], dtype out_dtype)
+ * z comes from `noise` (float32 [dout, din], mode INJECTED; bit-exact with a
+ * host-drawn tensor) or from the Philox stream (mode PHILOX) keyed by
+ * (seed, leaf_id).  `plan` is the dpc_clip_factors plan built from the same
+ * `scale` (nullable: the generic kernel then scans every example).  On the
+ * bf16 MFMA path (T % 64 == 0, din and dout multiples of 8) each G element
+ * is scaled in fp32 and rounded to bf16 once before the product.  With
+ * with_bias, bias_out[m] = same recipe over
+ * sum_i scale[i] * sum_t G[i, t, m], its noise keyed by (seed, bias_leaf_id)
+ * under the [dout, 1] view.
+ * -------------------------------------------------------------------------*/
+size_t dpc_clipped_sum_workspace_bytes(int B, int T, int din, int dout, int dtype);
+int dpc_clipped_sum(const void* A, const void* G, const float* scale, const void* plan, int B,
+                    int T, int din, int dout, int dtype, double normalize_by, int noise_mode,
+                    const float* noise, const float* bias_noise, uint64_t seed, uint32_t leaf_id,
+                    uint32_t bias_leaf_id, double sigma, int out_dtype, void* out, int with_bias,
+                    void* bias_out, void* ws, size_t ws_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Gaussian noise on an arbitrary leaf (out-of-place).
+ *
+ * Replaces `_sample` of _gaussian.py:188-204:
+ *   y = to_dtype(float(x) + (float)sigma * z),   z as in dpc_clipped_sum.
+ * The leaf is viewed as [rows, cols] for the Philox stream (rows = size of
+ * dim 0, cols = numel / rows).  sigma == 0 copies x.
+ * -------------------------------------------------------------------------*/
+int dpc_add_noise(const void* x, void* y, int64_t rows, int64_t cols, int dtype, double sigma,
+                  int noise_mode, const float* noise, uint64_t seed, uint32_t leaf_id,
+                  void* stream);
+
+/* Known-answer hook: n Philox4x32-10 blocks for counters (c0 + j, c1, c2, c3),
+ * key (k0, k1), written as out[4 j + w]. */
+int dpc_philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
+                      uint32_t k1, int n, uint32_t* out, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Materialised-leaf clip-and-sum (multi-tensor apply).
+ *
+ * The HIP counterpart of the fused backend seam
+ * (_kernel_backend.py:9-17, registered like patches/__init__.py:106-117;
+ * kernels of packages/opake-patches/src/opake/api/patches/kernels/
+ * _clip_sum.py:74-152).  Leaves are stacked per-example values
+ * [B, n_l] of one storage dtype; `ptrs` (device int64 [L]) holds their
+ * addresses, `sizes` (device int64 [L]) their per-example element counts.
+ * The tile table (tile_leaf / tile_local, device int32 [n_tiles]) splits each
+ * leaf into 2048-element tiles.
+ *
+ * dpc_leaves_sqnorm: partial[b, t] = float64 sum over tile t of example b of
+ *   (float)sanitise(x)^2 (fp32 square, fp64 sum), then
+ *   leaf_sq[b, leaf_col[l]] = sum of leaf l's tiles (tile_start [L + 1]).
+ * dpc_leaves_apply: out[off_l + j] = sum_b stored(b, l, j) in fp32, where
+ *   stored = to_dtype(float(sanitise(x)) * scale[b]) with bf16 subnormals
+ *   that rounded up zeroed (_pytree.py:160-204); post_sq[b, t] (nullable) =
+ *   sum over the tile of stored^2 (fp32).  out_dtype is the storage dtype or
+ *   float32.
+ * -------------------------------------------------------------------------*/
+int dpc_leaves_sqnorm(const int64_t* ptrs, const int64_t* sizes, const int32_t* tile_leaf,
+                      const int32_t* tile_local, const int64_t* tile_start,
+                      const int32_t* leaf_col, int n_leaves, int n_tiles, int B, int dtype,
+                      double* partial, double* leaf_sq, int leaf_sq_stride, void* stream);
+int dpc_leaves_apply(const int64_t* ptrs, const int64_t* sizes, const int32_t* tile_leaf,
+                     const int32_t* tile_local, const int64_t* out_offs, int n_tiles, int B,
+                     int dtype, const float* scale, void* out, int out_dtype, float* post_sq,
+                     void* stream);
+
+/* Row sums: out[b] (+)= sum_j x[b, j] (float64), used to fold per-leaf
+ * squared norms into per-example totals in a fixed order. */
+int dpc_row_sum_f64(const double* x, int B, int n, int accumulate, double* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OPAKE_AMD_H */

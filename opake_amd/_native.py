@@ -1,0 +1,178 @@
+"""ctypes binding of ``libopake_amd.so`` (the C ABI in ``include/opake_amd.h``).
+
+The library is loaded from this package directory.  There is no fallback:
+if it is missing, or the tensors are not on a ROCm device, calls raise
+:class:`~opake_amd.exceptions.OperationError` / ``ConfigurationError``.
+Status codes map to the reference's error classes: ``DPC_EINVAL`` ->
+``ConfigurationError`` (a ``ValueError``), anything else -> ``OperationError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+from opake_amd.exceptions import ConfigurationError, OperationError
+
+LIB_PATH = Path(__file__).resolve().parent / "libopake_amd.so"
+
+DPC_OK = 0
+DPC_EINVAL = -22
+DPC_ENOTSUP = -95
+DPC_ENOSPC = -28
+DPC_EHIP = -1000
+
+DPC_F32 = 0
+DPC_BF16 = 1
+SCALE_FIXED = 0
+SCALE_AUTO_S = 1
+NOISE_NONE = 0
+NOISE_INJECTED = 1
+NOISE_PHILOX = 2
+
+_c_void_p = ctypes.c_void_p
+_c_int = ctypes.c_int
+_c_double = ctypes.c_double
+_c_float = ctypes.c_float
+_c_size_t = ctypes.c_size_t
+_c_u32 = ctypes.c_uint32
+_c_u64 = ctypes.c_uint64
+_c_i64 = ctypes.c_int64
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "dpc_version": (_c_int, []),
+    "dpc_last_error": (ctypes.c_char_p, []),
+    "dpc_gram_workspace_bytes": (_c_size_t, [_c_int, _c_int]),
+    "dpc_gram_sqnorms": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_void_p, _c_void_p, _c_size_t, _c_void_p],
+    ),
+    "dpc_flat_sqnorms": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,
+         _c_void_p],
+    ),
+    "dpc_clip_plan_bytes": (_c_size_t, [_c_int]),
+    "dpc_clip_factors": (
+        _c_int,
+        [_c_void_p, _c_int, _c_double, _c_int, _c_double, ctypes.POINTER(_c_double),
+         ctypes.POINTER(_c_double), _c_int, _c_float, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p],
+    ),
+    "dpc_clipped_sum_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "dpc_clipped_sum": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_double, _c_int, _c_void_p, _c_void_p, _c_u64, _c_u32, _c_u32, _c_double, _c_int,
+         _c_void_p, _c_int, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
+    ),
+    "dpc_add_noise": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_int, _c_double, _c_int, _c_void_p, _c_u64,
+         _c_u32, _c_void_p],
+    ),
+    "dpc_philox4x32_10": (
+        _c_int,
+        [_c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _c_int, _c_void_p, _c_void_p],
+    ),
+    "dpc_leaves_sqnorm": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+         _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p],
+    ),
+    "dpc_leaves_apply": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_void_p,
+         _c_void_p, _c_int, _c_void_p, _c_void_p],
+    ),
+    "dpc_row_sum_f64": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_void_p]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the native library; raise if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise OperationError(
+                f"native library {LIB_PATH} is missing; build it with "
+                "`python -c 'import __graft_entry__ as g; g.build()'` (needs hipcc)"
+            )
+        try:
+            lib = ctypes.CDLL(str(LIB_PATH))
+        except OSError as exc:
+            raise OperationError(f"cannot load {LIB_PATH}: {exc}") from exc
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+        return lib
+
+
+def call(name: str, *args) -> None:
+    """Call a status-returning entry point and raise on failure."""
+    lib = load()
+    status = getattr(lib, name)(*args)
+    if status == DPC_OK:
+        return
+    if status == DPC_EINVAL:
+        raise ConfigurationError(f"{name}: invalid argument (DPC_EINVAL)")
+    if status == DPC_ENOSPC:
+        raise OperationError(f"{name}: workspace too small (DPC_ENOSPC)")
+    if status == DPC_ENOTSUP:
+        raise OperationError(f"{name}: unsupported configuration (DPC_ENOTSUP)")
+    detail = lib.dpc_last_error().decode(errors="replace")
+    raise OperationError(f"{name}: HIP error ({status}): {detail}")
+
+
+def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def stream_handle(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return DPC_F32
+    if dtype == torch.bfloat16:
+        return DPC_BF16
+    raise ConfigurationError(f"unsupported dtype {dtype} (supported: float32, bfloat16)")
+
+
+def require_device(*tensors: torch.Tensor) -> torch.device:
+    """All tensors on one ROCm device; returns it."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ConfigurationError(
+                f"opake_amd kernels need tensors on a ROCm device, got {t.device}"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ConfigurationError("tensors span more than one device")
+    if dev is None:
+        raise ConfigurationError("no tensor argument to infer the device from")
+    if torch.version.hip is None:
+        raise OperationError("opake_amd requires a ROCm build of PyTorch")
+    return dev
+
+
+__all__ = ["LIB_PATH", "SIGNATURES", "call", "load", "ptr", "stream_handle"]

@@ -1,0 +1,206 @@
+"""Per-example clip -> sum (-> noise) of linear layers without per-example gradients.
+
+The reference materialises every per-example gradient with ``vmap(grad)`` and
+then runs the streaming clip-and-sum over them
+(packages/opake-engine/src/opake/api/engine/clipping/_clipped_fun.py:676-695,
+_streaming.py:39-185).  For a linear layer with inputs ``A`` [B, T, din] and
+output gradients ``G`` [B, T, dout] the per-example weight gradient is
+``G_i^T A_i``; this module computes the same clipped sum from ``A`` and ``G``:
+
+1. per-example squared norms through the Gram identity
+   ``||G_i^T A_i||^2 = <A_i A_i^T, G_i G_i^T>`` (``dpc_gram_sqnorms``; flat
+   inputs use ``||a_i||^2 ||g_i||^2``);
+2. guarded clip factors, the reference's ``_finalize_scale`` in float64
+   (``dpc_clip_factors``) with the guard constants the reference would use for
+   the materialised leaves (storage = leaf dtype, multiply = float32,
+   roundoff from the leaf sizes);
+3. one GEMM ``sum_i c_i G_i^T A_i`` with ``/ normalize_by`` and, optionally,
+   the Gaussian noise fused into its epilogue (``dpc_clipped_sum``).
+
+Outputs use the reference's types: a ``ClippedPytree`` (or ``NoisedPytree``)
+over ``{"weight": [dout, din]}`` (plus ``"bias": [dout]``) with
+``max_norm = C / normalize_by``.
+
+Differences from the materialised reference, all documented in tests:
+* the norm is that of the exact product ``G_i^T A_i`` of the given values,
+  not of its bf16-rounded copy (they agree to the bf16 rounding of the entries);
+* on the bf16 MFMA path each ``c_i G_i`` entry is rounded to bf16 once
+  before the product instead of each ``c_i (G_i^T A_i)`` entry;
+* an example whose ``A_i`` or ``G_i`` holds NaN/Inf gets a non-finite norm
+  and clip factor 0 (the whole example is dropped); the reference instead
+  zeroes the non-finite gradient entries and keeps the rest.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+from torch.autograd.profiler import record_function
+
+from opake_amd import _native as nat
+from opake_amd import ops
+from opake_amd.clipping import _numerics as num
+from opake_amd.exceptions import ConfigurationError, InputTypeError
+from opake_amd.noise import GaussianNoiseState, step_key_for
+from opake_amd.random import generator_from_key
+from opake_amd.types import ClippedPytree, NoisedPytree, PerGroup, clipped
+
+_DEFAULT_GAMMA = 0.01
+
+
+@dataclass(frozen=True)
+class GhostClipAux:
+    """Per-example diagnostics (device tensors; nothing is synchronised).
+
+    ``grad_norms``: per-example gradient norms before clipping (float32, the
+    reference's accumulation dtype).  ``clip_scales``: the guarded factors that
+    were applied.  ``num_clipped``: int32 [1], examples with norm > C.
+    """
+
+    grad_norms: torch.Tensor
+    clip_scales: torch.Tensor
+    num_clipped: torch.Tensor
+    batch_size: int
+
+    @property
+    def clipping_rate(self) -> float:
+        """Fraction of clipped examples (synchronises the host)."""
+        if self.batch_size == 0:
+            return 0.0
+        return float(self.num_clipped.item()) / float(self.batch_size)
+
+
+def _check_inputs(A, G, bias):
+    if not isinstance(A, torch.Tensor) or not isinstance(G, torch.Tensor):
+        raise InputTypeError("A and G must be tensors")
+    if A.dim() == 2 and G.dim() == 2:
+        A, G = A.unsqueeze(1), G.unsqueeze(1)
+    if A.dim() != 3 or G.dim() != 3 or A.shape[:2] != G.shape[:2]:
+        raise ConfigurationError(
+            "expected A [B, T, din] and G [B, T, dout] (or [B, din] / [B, dout]), got "
+            f"{tuple(A.shape)} and {tuple(G.shape)}"
+        )
+    if A.dtype != G.dtype or A.dtype not in (torch.float32, torch.bfloat16):
+        raise ConfigurationError("A and G must share a dtype: float32 or bfloat16")
+    return A, G
+
+
+def guard_for_linear(dtype: torch.dtype, din: int, dout: int, bias: bool):
+    """(rel, abs) guard of the materialised weight (+ bias) leaves."""
+    acc = num.compute_dtype_for_reduction([dtype])
+    sizes = [dout * din] + ([dout] if bias else [])
+    roundoff = num.norm_roundoff(acc, torch.float64, len(sizes), num.reduction_terms(sizes))
+    multiply = torch.promote_types(dtype, acc)
+    return num.guard_constants(dtype, multiply, roundoff)
+
+
+def ghost_sqnorms(A: torch.Tensor, G: torch.Tensor, *, bias: bool = False,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-example squared gradient norms of one linear layer (float64 [B])."""
+    A, G = _check_inputs(A, G, bias)
+    if A.shape[1] == 1:
+        return ops.flat_sqnorms(A[:, 0], G[:, 0], with_bias=bias, out=out)
+    return ops.gram_sqnorms(A, G, with_bias=bias, out=out)
+
+
+def _scale_kind(auto_s_gamma):
+    if auto_s_gamma is None:
+        return nat.SCALE_FIXED, 0.0
+    if auto_s_gamma <= 0:
+        raise ConfigurationError(f"gamma must be positive, got {auto_s_gamma}")
+    return nat.SCALE_AUTO_S, float(auto_s_gamma)
+
+
+def ghost_clip_sum(
+    A: torch.Tensor,
+    G: torch.Tensor,
+    *,
+    clipping_norm: float,
+    normalize_by: float = 1.0,
+    bias: bool = False,
+    auto_s_gamma: float | None = None,
+    dtype: torch.dtype | None = None,
+    return_aux: bool = False,
+    noise_fn=None,
+    noise_state: GaussianNoiseState | None = None,
+):
+    """Clipped (and optionally noised) sum of a linear layer's per-example gradients.
+
+    Without ``noise_fn``: returns ``ClippedPytree`` (or ``(ClippedPytree, aux)``).
+    With ``noise_fn``/``noise_state`` from :func:`opake_amd.noise.gaussian_noise`:
+    the noise is added in the GEMM epilogue and the call returns
+    ``(NoisedPytree, next_state)`` (or ``((NoisedPytree, aux), next_state)``),
+    bit-identical to ``noise_fn(ghost_clip_sum(...), noise_state)``.
+    ``auto_s_gamma`` selects AUTO-S scaling ``C / (||g|| + gamma)``.
+    """
+    if isinstance(clipping_norm, PerGroup):
+        raise ConfigurationError("per-group clipping is not supported by ghost_clip_sum")
+    if clipping_norm <= 0:
+        raise ConfigurationError(f"clipping_norm must be positive, got {clipping_norm}")
+    if normalize_by <= 0.0:
+        raise ConfigurationError(f"normalize_by must be > 0, got {normalize_by}.")
+    A, G = _check_inputs(A, G, bias)
+    B, T, din = A.shape
+    dout = G.shape[2]
+    out_dtype = dtype or A.dtype
+    kind, gamma = _scale_kind(auto_s_gamma)
+    max_norm = clipping_norm / normalize_by
+
+    with record_function("opake::ghost_clip_sum"):
+        sq = ghost_sqnorms(A, G, bias=bias)
+        cf = ops.clip_factors(
+            sq,
+            num.conservative_bound(clipping_norm),
+            [guard_for_linear(A.dtype, din, dout, bias)],
+            kind=kind,
+            gamma=gamma,
+            count_threshold=num.float32_of(clipping_norm),
+        )
+        spec = None
+        next_state = None
+        std = 0.0
+        if noise_fn is not None:
+            if noise_state is None:
+                raise ConfigurationError("noise_state is required with noise_fn")
+            std = noise_fn.clipped_stddev(clipped(None, max_norm=max_norm))
+            if std != 0.0:
+                if noise_fn.compute_dtype != torch.float32:
+                    raise ConfigurationError("fused noise supports compute_dtype float32 only")
+                step_key = step_key_for(noise_state)
+                # Flatten order of {"bias", "weight"}: bias first when present.
+                w_leaf, b_leaf = (1, 0) if bias else (0, 0)
+                if noise_fn.stream == "reference":
+                    gen = generator_from_key(step_key)
+                    b_draw = torch.randn(dout, dtype=torch.float32, generator=gen) if bias else None
+                    w_draw = torch.randn((dout, din), dtype=torch.float32, generator=gen)
+                    dev = A.device
+                    spec = ops.NoiseSpec(
+                        sigma=std,
+                        mode=nat.NOISE_INJECTED,
+                        noise=w_draw.pin_memory().to(dev, non_blocking=True),
+                        bias_noise=(b_draw.pin_memory().to(dev, non_blocking=True)
+                                    if bias else None),
+                    )
+                else:
+                    spec = ops.NoiseSpec(sigma=std, mode=nat.NOISE_PHILOX, seed=step_key.seed,
+                                         leaf_id=w_leaf, bias_leaf_id=b_leaf)
+            next_state = GaussianNoiseState(
+                _step_counter=noise_state._step_counter + 1, _rng_key=noise_state._rng_key)
+        w, b = ops.clipped_sum(
+            A, G, cf.scale[0], plan=cf.plan, normalize_by=normalize_by, noise=spec,
+            out_dtype=out_dtype, with_bias=bias,
+        )
+    tree = {"weight": w}
+    if bias:
+        tree["bias"] = b
+    aux = GhostClipAux(grad_norms=cf.norms, clip_scales=cf.scale[0], num_clipped=cf.nclipped,
+                       batch_size=B)
+    if noise_fn is None:
+        result = clipped(tree, max_norm=max_norm)
+        return (result, aux) if return_aux else result
+    result = NoisedPytree(pytree=tree, max_norm=max_norm, noise_stddev=std)
+    return ((result, aux) if return_aux else result), next_state
+
+
+__all__ = ["GhostClipAux", "ghost_clip_sum", "ghost_sqnorms", "guard_for_linear"]

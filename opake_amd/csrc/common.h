@@ -1,0 +1,124 @@
+// Shared device/host helpers for the DP clip-and-aggregate kernels (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "opake_amd.h"
+
+#define DPC_HOST_DEVICE __host__ __device__ __forceinline__
+#define DPC_DEVICE __device__ __forceinline__
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// bfloat16 <-> float.  bf16 is the upper half of an IEEE binary32; the
+// narrowing conversion rounds to nearest-even and keeps NaN a NaN.
+// ---------------------------------------------------------------------------
+DPC_HOST_DEVICE float bf16_bits_to_f32(uint16_t b) {
+  union { uint32_t u; float f; } v;
+  v.u = (uint32_t)b << 16;
+  return v.f;
+}
+
+DPC_HOST_DEVICE uint16_t f32_to_bf16_bits(float f) {
+  union { uint32_t u; float f; } v;
+  v.f = f;
+  uint32_t u = v.u;
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
+    return (uint16_t)((u >> 16) | 0x0040u);  // quiet NaN
+  }
+  uint32_t rounding = 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)((u + rounding) >> 16);
+}
+
+// Round a float to the nearest bf16 and widen it back (one rounding).
+DPC_HOST_DEVICE float round_to_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+// ---------------------------------------------------------------------------
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy
+// as 1, 2, 3", SC'11).  Counter (c0..c3), key (k0, k1); ten rounds of the
+// 4x32 S-box with multipliers 0xD2511F53 / 0xCD9E8D57 and Weyl key increments
+// 0x9E3779B9 / 0xBB67AE85.
+// ---------------------------------------------------------------------------
+struct Philox4 {
+  uint32_t v[4];
+};
+
+DPC_HOST_DEVICE void philox_mulhilo(uint32_t a, uint32_t b, uint32_t* hi, uint32_t* lo) {
+  uint64_t p = (uint64_t)a * (uint64_t)b;
+  *hi = (uint32_t)(p >> 32);
+  *lo = (uint32_t)p;
+}
+
+DPC_HOST_DEVICE Philox4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
+                                      uint32_t k0, uint32_t k1) {
+  const uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
+  const uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+  for (int round = 0; round < 10; ++round) {
+    uint32_t hi0, lo0, hi1, lo1;
+    philox_mulhilo(M0, c0, &hi0, &lo0);
+    philox_mulhilo(M1, c2, &hi1, &lo1);
+    uint32_t n0 = hi1 ^ c1 ^ k0;
+    uint32_t n1 = lo1;
+    uint32_t n2 = hi0 ^ c3 ^ k1;
+    uint32_t n3 = lo0;
+    c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+    k0 += W0;
+    k1 += W1;
+  }
+  Philox4 r;
+  r.v[0] = c0; r.v[1] = c1; r.v[2] = c2; r.v[3] = c3;
+  return r;
+}
+
+// Device-stream standard normals.  A leaf is viewed as a matrix
+// [rows, cols] (rows = size of dim 0, cols = numel / rows; 1-D leaves are
+// [n, 1]).  Element (r, c) takes normal (r & 1) of the Box-Muller pair drawn
+// from Philox block ((r >> 1) * cols + c, leaf):
+//   u1 = (k + 1/2) 2^-53 with k the top 53 bits of (w0 << 32 | w1)  (in (0,1))
+//   u2 = (w2 + 1/2) 2^-32
+//   radius = sqrt(-2 ln u1) in double, angle = 2 pi u2,
+//   z0 = radius cos(angle), z1 = radius sin(angle).
+// The 53-bit radius keeps the tail out to |z| = 8.57 (a 24-bit uniform would
+// cut it at 5.9).  The function of (seed, leaf, r, c) does not depend on how a
+// kernel tiles the leaf, so every kernel that writes a leaf draws the same
+// stream.
+DPC_DEVICE void philox_normal_pair(uint64_t seed, uint32_t leaf, uint64_t block, float* z0,
+                                   float* z1) {
+  Philox4 w = philox4x32_10((uint32_t)block, (uint32_t)(block >> 32), leaf, 0u,
+                            (uint32_t)seed, (uint32_t)(seed >> 32));
+  uint64_t bits = ((uint64_t)w.v[0] << 32) | (uint64_t)w.v[1];
+  double u1 = ((double)(bits >> 11) + 0.5) * 0x1.0p-53;
+  float u2 = (float)(((double)w.v[2] + 0.5) * 0x1.0p-32);
+  double radius = sqrt(-2.0 * log(u1));
+  float s, c;
+  sincospif(2.0f * u2, &s, &c);
+  *z0 = (float)(radius * (double)c);
+  *z1 = (float)(radius * (double)s);
+}
+
+// Sanitise a float like torch.nan_to_num(nan=0, posinf=0, neginf=0).
+DPC_HOST_DEVICE float finite_or_zero(float x) {
+  union { uint32_t u; float f; } v;
+  v.f = x;
+  return ((v.u & 0x7f800000u) == 0x7f800000u) ? 0.0f : x;
+}
+
+DPC_HOST_DEVICE int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Remembers the last failing HIP status of the calling thread (abi.hip).
+void dpc_record_error(hipError_t e);
+
+#define DPC_HIP_CHECK(expr)          \
+  do {                               \
+    hipError_t _e = (expr);          \
+    if (_e != hipSuccess) {          \
+      dpc_record_error(_e);          \
+      return DPC_EHIP;               \
+    }                                \
+  } while (0)

@@ -1,0 +1,105 @@
+// Gaussian noise on one leaf, out of place:
+//   y = to_dtype(float(x) + (float)sigma * z)
+// with z injected (float32, same shape) or drawn from the Philox stream of
+// (seed, leaf) under the [rows, cols] view described in common.h.  Each thread
+// produces one even/odd row pair of one column, so consecutive threads touch
+// consecutive columns.
+#include "common.h"
+
+namespace {
+
+constexpr int kNoiseThreads = 256;
+
+#pragma clang fp contract(off)
+template <bool kBf16>
+__device__ __forceinline__ float add_scaled(float x, float sigma, float z) {
+  float t = sigma * z;
+  float v = x + t;
+  return kBf16 ? round_to_bf16(v) : v;
+}
+#pragma clang fp contract(on)
+
+template <bool kBf16>
+__global__ void __launch_bounds__(kNoiseThreads)
+add_noise_kernel(const void* __restrict__ x, void* __restrict__ y, int64_t rows, int64_t cols,
+                 float sigma, int mode, const float* __restrict__ noise, uint64_t seed,
+                 uint32_t leaf) {
+  const int64_t pairs = (rows + 1) >> 1;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= pairs * cols) return;
+  const int64_t pr = t / cols, c = t - pr * cols;
+  const int64_t r0 = pr * 2;
+  float z0, z1;
+  if (mode == DPC_NOISE_PHILOX) {
+    philox_normal_pair(seed, leaf, (uint64_t)t, &z0, &z1);
+  } else {
+    z0 = noise[r0 * cols + c];
+    z1 = (r0 + 1 < rows) ? noise[(r0 + 1) * cols + c] : 0.0f;
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t r = r0 + h;
+    if (r >= rows) break;
+    const int64_t idx = r * cols + c;
+    const float z = h ? z1 : z0;
+    if (kBf16) {
+      float xv = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(x)[idx]);
+      reinterpret_cast<uint16_t*>(y)[idx] = f32_to_bf16_bits(add_scaled<true>(xv, sigma, z));
+    } else {
+      float xv = reinterpret_cast<const float*>(x)[idx];
+      reinterpret_cast<float*>(y)[idx] = add_scaled<false>(xv, sigma, z);
+    }
+  }
+}
+
+__global__ void philox_kat_kernel(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
+                                  uint32_t k1, int n, uint32_t* __restrict__ out) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  Philox4 r = philox4x32_10(c0 + (uint32_t)j, c1, c2, c3, k0, k1);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) out[4 * j + w] = r.v[w];
+}
+
+}  // namespace
+
+extern "C" int dpc_add_noise(const void* x, void* y, int64_t rows, int64_t cols, int dtype,
+                             double sigma, int noise_mode, const float* noise, uint64_t seed,
+                             uint32_t leaf_id, void* stream) {
+  if (rows < 0 || cols < 0 || !(sigma >= 0.0)) return DPC_EINVAL;
+  if (dtype != DPC_F32 && dtype != DPC_BF16) return DPC_EINVAL;
+  if (rows == 0 || cols == 0) return DPC_OK;
+  if (!x || !y) return DPC_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  const size_t esize = dtype == DPC_BF16 ? 2 : 4;
+  if (sigma == 0.0) {
+    if (x != y) {
+      DPC_HIP_CHECK(hipMemcpyAsync(y, x, (size_t)rows * cols * esize, hipMemcpyDeviceToDevice, s));
+    }
+    return DPC_OK;
+  }
+  if (noise_mode != DPC_NOISE_INJECTED && noise_mode != DPC_NOISE_PHILOX) return DPC_EINVAL;
+  if (noise_mode == DPC_NOISE_INJECTED && !noise) return DPC_EINVAL;
+  const int64_t work = ((rows + 1) >> 1) * cols;
+  const int64_t blocks = (work + kNoiseThreads - 1) / kNoiseThreads;
+  if (blocks > 0x7fffffffLL) return DPC_ENOTSUP;
+  if (dtype == DPC_BF16) {
+    hipLaunchKernelGGL(add_noise_kernel<true>, dim3((unsigned)blocks), dim3(kNoiseThreads), 0, s,
+                       x, y, rows, cols, (float)sigma, noise_mode, noise, seed, leaf_id);
+  } else {
+    hipLaunchKernelGGL(add_noise_kernel<false>, dim3((unsigned)blocks), dim3(kNoiseThreads), 0, s,
+                       x, y, rows, cols, (float)sigma, noise_mode, noise, seed, leaf_id);
+  }
+  DPC_HIP_CHECK(hipGetLastError());
+  return DPC_OK;
+}
+
+extern "C" int dpc_philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
+                                 uint32_t k1, int n, uint32_t* out, void* stream) {
+  if (n < 0 || (n > 0 && !out)) return DPC_EINVAL;
+  if (n == 0) return DPC_OK;
+  hipLaunchKernelGGL(philox_kat_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, (hipStream_t)stream,
+                     c0, c1, c2, c3, k0, k1, n, out);
+  DPC_HIP_CHECK(hipGetLastError());
+  return DPC_OK;
+}

@@ -1,0 +1,314 @@
+"""Parity of each HIP kernel with the CPU oracle (GPU tests, called through the C ABI)."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from opake_amd import _native as nat
+from opake_amd import ops
+from opake_amd.clipping import _numerics as num
+from oracle import c_oracle, clip_oracle, ghost_oracle
+
+pytestmark = pytest.mark.gpu
+
+RANDOM123_KAT = [
+    ((0, 0, 0, 0), (0, 0), (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+    ((0xFFFFFFFF,) * 4, (0xFFFFFFFF,) * 2, (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+    ((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0),
+     (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)),
+]
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# --- Philox stream ---------------------------------------------------------
+
+
+@pytest.mark.parametrize("ctr,key,expected", RANDOM123_KAT)
+def test_philox_known_answers(dev, ctr, key, expected):
+    got = ops.philox4x32_10(ctr, key, 1, dev).cpu().numpy()[0]
+    assert tuple(int(x) for x in got) == expected
+
+
+def test_philox_matches_c_oracle(dev):
+    got = ops.philox4x32_10((7, 1, 2, 3), (0xDEADBEEF, 0x12345678), 4096, dev).cpu().numpy()
+    want = c_oracle.philox((7, 1, 2, 3), (0xDEADBEEF, 0x12345678), 4096)
+    assert np.array_equal(got.astype(np.uint32), want)
+
+
+# --- squared norms -----------------------------------------------------------
+
+
+def _exact_sqnorms(A, G, bias=False):
+    w = torch.einsum("btm,btn->bmn", G.double(), A.double())
+    sq = (w * w).sum(dim=(1, 2))
+    if bias:
+        sq = sq + (G.double().sum(dim=1) ** 2).sum(dim=1)
+    return sq
+
+
+@pytest.mark.parametrize(
+    "B,T,din,dout",
+    [(3, 128, 64, 64), (2, 200, 136, 72), (2, 512, 256, 128), (1, 1, 8, 8), (4, 130, 64, 40)],
+)
+@pytest.mark.parametrize("bias", [False, True])
+def test_gram_sqnorms_bf16(dev, B, T, din, dout, bias):
+    g = _gen(B * 1000 + T)
+    A = torch.randn(B, T, din, generator=g).to(torch.bfloat16)
+    G = torch.randn(B, T, dout, generator=g).to(torch.bfloat16)
+    got = ops.gram_sqnorms(A.to(dev), G.to(dev), with_bias=bias).cpu()
+    want = _exact_sqnorms(A, G, bias)
+    # fp32 MFMA accumulation of exact bf16 products, fp64 combination.
+    torch.testing.assert_close(got, want, rtol=1e-4, atol=0)
+
+
+@pytest.mark.parametrize("B,T,din,dout", [(3, 17, 33, 9), (2, 70, 64, 65)])
+def test_gram_sqnorms_fp32_generic(dev, B, T, din, dout):
+    g = _gen(7)
+    A = torch.randn(B, T, din, generator=g)
+    G = torch.randn(B, T, dout, generator=g)
+    got = ops.gram_sqnorms(A.to(dev), G.to(dev), with_bias=True).cpu()
+    torch.testing.assert_close(got, _exact_sqnorms(A, G, True), rtol=1e-5, atol=0)
+
+
+def test_gram_sqnorms_accumulate(dev):
+    g = _gen(3)
+    A1, G1 = torch.randn(2, 64, 32, generator=g), torch.randn(2, 64, 16, generator=g)
+    A2, G2 = torch.randn(2, 64, 24, generator=g), torch.randn(2, 64, 8, generator=g)
+    out = ops.gram_sqnorms(A1.to(dev), G1.to(dev))
+    ops.gram_sqnorms(A2.to(dev), G2.to(dev), out=out)
+    torch.testing.assert_close(out.cpu(), _exact_sqnorms(A1, G1) + _exact_sqnorms(A2, G2),
+                               rtol=1e-5, atol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_flat_sqnorms(dev, dtype):
+    g = _gen(5)
+    a = torch.randn(6, 784, generator=g).to(dtype)
+    gg = torch.randn(6, 512, generator=g).to(dtype)
+    got = ops.flat_sqnorms(a.to(dev), gg.to(dev), with_bias=True).cpu()
+    want = (a.double() ** 2).sum(1) * (gg.double() ** 2).sum(1) + (gg.double() ** 2).sum(1)
+    torch.testing.assert_close(got, want, rtol=1e-12, atol=0)
+
+
+def test_gram_nonfinite_example_is_nonfinite(dev):
+    g = _gen(9)
+    A = torch.randn(3, 128, 64, generator=g).to(torch.bfloat16)
+    G = torch.randn(3, 128, 64, generator=g).to(torch.bfloat16)
+    A[1, 5, 7] = float("nan")
+    G[2, 3, 1] = float("inf")
+    got = ops.gram_sqnorms(A.to(dev), G.to(dev)).cpu()
+    assert math.isfinite(got[0].item())
+    assert not math.isfinite(got[1].item())
+    assert not math.isfinite(got[2].item())
+
+
+# --- clip factors ---------------------------------------------------------------
+
+
+def _oracle_scales(sq, C, rel_abs_storage, kind="fixed", gamma=0.0):
+    storage, mult, roundoff = rel_abs_storage
+    norm = torch.sqrt(sq)
+    bound = torch.clamp(torch.as_tensor(C, dtype=torch.float64), min=0.0)
+    ratio = bound / (norm + gamma) if kind == "auto_s" else bound / norm
+    return clip_oracle.finalize_scale(ratio, storage, mult, roundoff, clamp_to_one=kind != "auto_s")
+
+
+@pytest.mark.parametrize("kind", ["fixed", "auto_s"])
+def test_clip_factors_bit_exact(dev, kind):
+    g = _gen(11)
+    sq = torch.exp(torch.randn(3000, generator=g, dtype=torch.float64) * 3)
+    sq[:6] = torch.tensor([0.0, math.inf, math.nan, 1.0, 0.25, 1e300], dtype=torch.float64)
+    C = clip_oracle.conservative_bound(1.0)
+    gamma = 0.01 if kind == "auto_s" else 0.0
+    guards = []
+    expect = []
+    for storage in (torch.bfloat16, torch.float32):
+        mult = torch.promote_types(storage, torch.float32)
+        roundoff = clip_oracle.norm_roundoff(torch.float32, torch.float64, 1, 10240)
+        guards.append(num.guard_constants(storage, mult, roundoff))
+        expect.append(_oracle_scales(sq, C, (storage, mult, roundoff), kind, gamma).to(torch.float32))
+    cf = ops.clip_factors(sq.to(dev), C, guards, kind=nat.SCALE_AUTO_S if kind == "auto_s"
+                          else nat.SCALE_FIXED, gamma=gamma, count_threshold=1.0)
+    for gi in range(2):
+        assert torch.equal(cf.scale[gi].cpu(), expect[gi]), gi
+    norms = torch.sqrt(sq).to(torch.float32)
+    torch.testing.assert_close(cf.norms.cpu(), norms, rtol=0, atol=0, equal_nan=True)
+    assert int(cf.nclipped.item()) == int((norms > 1.0).sum().item())
+    # Plan: examples with a positive guard-0 scale, in order.
+    active = [i for i in range(sq.numel()) if expect[0][i] > 0]
+    plan = cf.plan.cpu().numpy().view(np.int32)
+    assert plan[0] == len(active)
+    assert list(plan[4:4 + len(active)]) == active
+
+
+def test_clip_factors_boundary_example(dev):
+    # The reference's own boundary pin: [[3,4],[0.6,0.8]], C=1 -> [1.2, 1.6]
+    # (an example at ||g|| == C is still scaled by rel < 1).
+    sq = torch.tensor([25.0, 1.0], dtype=torch.float64)
+    roundoff = clip_oracle.norm_roundoff(torch.float32, torch.float64, 1, 2)
+    guard = num.guard_constants(torch.float32, torch.float32, roundoff)
+    cf = ops.clip_factors(sq.to(dev), 1.0, [guard], count_threshold=1.0)
+    s = cf.scale[0].cpu().double()
+    vals = torch.tensor([[3.0, 4.0], [0.6, 0.8]], dtype=torch.float32)
+    out = (vals * s.float().view(2, 1)).sum(0)
+    torch.testing.assert_close(out, torch.tensor([1.2, 1.6]))
+    assert s[1] < 1.0
+    assert int(cf.nclipped.item()) == 1
+
+
+# --- clipped sum -----------------------------------------------------------------
+
+
+def _oracle_clipped_sum(A, G, C, nb=1.0, bias=False, out_dtype=None, kind="fixed", gamma=0.0):
+    leaves = ghost_oracle.linear_per_example_grads(A, G, with_bias=bias)
+    red = {A.dtype: out_dtype} if out_dtype is not None else None
+    res = clip_oracle.stream_clip_and_sum(leaves, clip_oracle.conservative_bound(C), kind=kind,
+                                          gamma=gamma, reduce_dtype=red)
+    return [clip_oracle.normalize(r, nb) for r in res.reduced], res
+
+
+def _run_clipped_sum(dev, A, G, C, nb=1.0, bias=False, out_dtype=None, use_plan=True):
+    B, T, din = A.shape
+    dout = G.shape[2]
+    sq = ops.gram_sqnorms(A.to(dev), G.to(dev), with_bias=bias) if T > 1 else ops.flat_sqnorms(
+        A[:, 0].to(dev), G[:, 0].to(dev), with_bias=bias)
+    from opake_amd.clipping import guard_for_linear
+    cf = ops.clip_factors(sq, num.conservative_bound(C), [guard_for_linear(A.dtype, din, dout, bias)],
+                          count_threshold=num.float32_of(C))
+    w, b = ops.clipped_sum(A.to(dev), G.to(dev), cf.scale[0], plan=cf.plan if use_plan else None,
+                           normalize_by=nb, out_dtype=out_dtype, with_bias=bias)
+    return w, b, cf
+
+
+def _rel_err(got, want):
+    got, want = got.double(), want.double()
+    return ((got - want).norm() / want.norm().clamp_min(1e-300)).item()
+
+
+@pytest.mark.parametrize(
+    "B,T,din,dout",
+    [(4, 128, 256, 256), (3, 64, 320, 264), (5, 192, 512, 136), (2, 64, 8, 8)],
+)
+def test_clipped_sum_bf16_mfma(dev, B, T, din, dout):
+    g = _gen(B + T + din)
+    A = torch.randn(B, T, din, generator=g).to(torch.bfloat16)
+    G = (torch.randn(B, T, dout, generator=g) * 0.01 *
+         torch.exp(torch.randn(B, 1, 1, generator=g))).to(torch.bfloat16)
+    w, _, cf = _run_clipped_sum(dev, A, G, 1.0, nb=float(B), out_dtype=torch.float32)
+    (want,), res = _oracle_clipped_sum(A, G, 1.0, nb=float(B), out_dtype=torch.float32)
+    assert _rel_err(w.cpu(), want) < 2e-2
+    torch.testing.assert_close(cf.norms.cpu().double(), res.norms, rtol=2e-2, atol=0)
+
+
+def test_clipped_sum_bf16_out_and_bias(dev):
+    g = _gen(21)
+    A = torch.randn(3, 128, 256, generator=g).to(torch.bfloat16)
+    G = (torch.randn(3, 128, 128, generator=g) * 0.02).to(torch.bfloat16)
+    w, b, _ = _run_clipped_sum(dev, A, G, 0.5, nb=2.0, bias=True)
+    (wb, ww), _ = _oracle_clipped_sum(A, G, 0.5, nb=2.0, bias=True)
+    assert w.dtype == torch.bfloat16 and b.dtype == torch.bfloat16
+    assert _rel_err(w.cpu(), ww) < 2e-2
+    assert _rel_err(b.cpu(), wb) < 2e-2
+
+
+@pytest.mark.parametrize("B,T,din,dout", [(6, 1, 784, 512), (3, 5, 33, 17), (4, 3, 64, 10)])
+def test_clipped_sum_fp32_generic(dev, B, T, din, dout):
+    g = _gen(31)
+    A = torch.randn(B, T, din, generator=g)
+    G = torch.randn(B, T, dout, generator=g) * 0.05
+    w, b, cf = _run_clipped_sum(dev, A, G, 1.0, nb=float(B), bias=True)
+    (wb, ww), res = _oracle_clipped_sum(A, G, 1.0, nb=float(B), bias=True)
+    torch.testing.assert_close(cf.norms.cpu().double(), res.norms, rtol=1e-5, atol=0)
+    assert _rel_err(w.cpu(), ww) < 1e-5
+    assert _rel_err(b.cpu(), wb) < 1e-5
+
+
+def test_clipped_sum_plan_skips_nonfinite_examples(dev):
+    g = _gen(41)
+    A = torch.randn(3, 64, 64, generator=g).to(torch.bfloat16)
+    G = (torch.randn(3, 64, 64, generator=g) * 0.01).to(torch.bfloat16)
+    A[1, 0, 0] = float("nan")
+    w, _, cf = _run_clipped_sum(dev, A, G, 1.0, out_dtype=torch.float32)
+    assert torch.isfinite(w).all()
+    assert cf.scale[0, 1].item() == 0.0
+    keep = torch.tensor([0, 2])
+    (want,), _ = _oracle_clipped_sum(A[keep], G[keep], 1.0, out_dtype=torch.float32)
+    assert _rel_err(w.cpu(), want) < 2e-2
+
+
+def test_clipped_sum_fast_and_generic_agree(dev):
+    g = _gen(51)
+    A = torch.randn(4, 128, 256, generator=g).to(torch.bfloat16)
+    G = (torch.randn(4, 128, 256, generator=g) * 0.01).to(torch.bfloat16)
+    w_fast, _, _ = _run_clipped_sum(dev, A, G, 1.0, out_dtype=torch.float32, use_plan=True)
+    w_gen, _, _ = _run_clipped_sum(dev, A, G, 1.0, out_dtype=torch.float32, use_plan=False)
+    assert _rel_err(w_fast.cpu(), w_gen.cpu()) < 5e-3
+
+
+# --- noise ---------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_add_noise_injected_bit_exact(dev, dtype):
+    from oracle import noise_oracle
+
+    g = _gen(61)
+    x = torch.randn(37, 19, generator=g).to(dtype)
+    z = torch.randn(37, 19, generator=g)
+    y = ops.add_noise(x.to(dev), 0.7, mode=nat.NOISE_INJECTED, noise=z.to(dev)).cpu()
+    assert torch.equal(y, noise_oracle.sample(x, 0.7, z))
+
+
+@pytest.mark.parametrize("shape", [(64, 33), (7,), (5, 3, 4)])
+def test_add_noise_device_stream_matches_c_oracle(dev, shape):
+    x = torch.zeros(shape)
+    seed = 0x0123456789ABCDEF
+    y = ops.add_noise(x.to(dev), 1.0, mode=nat.NOISE_PHILOX, seed=seed, leaf_id=3).cpu()
+    rows, cols = ops.leaf_view(x)
+    want = torch.from_numpy(c_oracle.leaf_normals(seed, 3, rows, cols)).reshape(shape)
+    torch.testing.assert_close(y.double(), want, rtol=0, atol=2e-5)
+
+
+def test_clipped_sum_epilogue_noise_injected_bit_exact(dev):
+    from oracle import noise_oracle
+
+    g = _gen(71)
+    A = torch.randn(2, 64, 256, generator=g).to(torch.bfloat16)
+    G = (torch.randn(2, 64, 256, generator=g) * 0.01).to(torch.bfloat16)
+    sq = ops.gram_sqnorms(A.to(dev), G.to(dev))
+    from opake_amd.clipping import guard_for_linear
+    cf = ops.clip_factors(sq, 1.0, [guard_for_linear(torch.bfloat16, 256, 256, False)],
+                          count_threshold=1.0)
+    for out_dtype in (torch.float32, torch.bfloat16):
+        center, _ = ops.clipped_sum(A.to(dev), G.to(dev), cf.scale[0], plan=cf.plan,
+                                    normalize_by=4.0, out_dtype=out_dtype)
+        z = torch.randn(256, 256, generator=g)
+        noisy, _ = ops.clipped_sum(
+            A.to(dev), G.to(dev), cf.scale[0], plan=cf.plan, normalize_by=4.0, out_dtype=out_dtype,
+            noise=ops.NoiseSpec(sigma=0.25, mode=nat.NOISE_INJECTED, noise=z.to(dev)))
+        assert torch.equal(noisy.cpu(), noise_oracle.sample(center.cpu(), 0.25, z))
+
+
+def test_clipped_sum_epilogue_noise_philox_matches_add_noise(dev):
+    g = _gen(81)
+    A = torch.randn(2, 64, 264, generator=g).to(torch.bfloat16)
+    G = (torch.randn(2, 64, 136, generator=g) * 0.01).to(torch.bfloat16)
+    sq = ops.gram_sqnorms(A.to(dev), G.to(dev))
+    from opake_amd.clipping import guard_for_linear
+    cf = ops.clip_factors(sq, 1.0, [guard_for_linear(torch.bfloat16, 264, 136, True)],
+                          count_threshold=1.0)
+    kw = dict(plan=cf.plan, normalize_by=2.0, out_dtype=torch.float32, with_bias=True)
+    cw, cb = ops.clipped_sum(A.to(dev), G.to(dev), cf.scale[0], **kw)
+    spec = ops.NoiseSpec(sigma=0.5, mode=nat.NOISE_PHILOX, seed=99, leaf_id=1, bias_leaf_id=0)
+    nw, nbias = ops.clipped_sum(A.to(dev), G.to(dev), cf.scale[0], noise=spec, **kw)
+    ew = ops.add_noise(cw, 0.5, mode=nat.NOISE_PHILOX, seed=99, leaf_id=1)
+    eb = ops.add_noise(cb, 0.5, mode=nat.NOISE_PHILOX, seed=99, leaf_id=0)
+    assert torch.equal(nw, ew)
+    assert torch.equal(nbias, eb)
