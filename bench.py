@@ -1,0 +1,221 @@
+"""DP-SGD clip -> sum -> noise step throughput on one MI355X.
+
+Workload: one sequence linear layer, d_in = d_out = 4096,
+bf16 activations A [B=32, T=512, 4096] ~ N(0, 1) and output gradients G of the
+same batch/sequence shape.  G is N(0, sigma_G) with sigma_G = C / sqrt(T * d_in
+* d_out) and each example scaled by a lognormal(0, 1) factor, so that about half
+of the examples are clipped (at the configuration's literal N(0, 1e-2) every
+example would be clipped by ~900x).  C = 1.0, noise multiplier 1.0,
+normalize_by = 1 (the reference default), noise from the device (Philox)
+stream fused into the clipped-sum epilogue.
+
+A step is one ``ghost_clip_sum`` call: Gram norms -> clip factors -> clipped-sum
+GEMM with the fused noise epilogue, inputs resident in HBM.  The timed region
+is bracketed by ``torch.cuda.synchronize()``.  The dominant kernel (the
+clipped-sum GEMM) is timed with HIP events recorded on the stream it is
+launched on, inside the timed steps.
+
+``cpu_baseline``: the reference algorithm restated on the CPU (``vmap(grad)``
+of the linear surrogate loss, the streaming clip-and-sum, the CPU-generator
+noise draw) on a bounded sample of the same workload: the full layer with a
+reduced batch, timed on the host cores of the box.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "DP-step examples/sec at 1 MI355X; TFLOP/s and % of MFMA/HBM roofline"
+B, T, DIN, DOUT = 32, 512, 4096, 4096
+C, NM = 1.0, 1.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+HBM_PEAK_GBS = 8000.0
+
+
+def algorithmic_flops(b=B, t=T, din=DIN, dout=DOUT):
+    """Gram norms (SYRK convention T(T+1)(din+dout)), inner products 2T^2, GEMM 2BTdin dout."""
+    gram = b * (t * (t + 1) * (din + dout) + 2 * t * t)
+    gemm = 2 * b * t * din * dout
+    return gram, gemm
+
+
+def make_inputs(device, b=B, t=T, din=DIN, dout=DOUT, seed=0):
+    import torch
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    A = torch.randn(b, t, din, generator=g, device=device, dtype=torch.float32).to(torch.bfloat16)
+    sigma_g = C / math.sqrt(t * din * dout)
+    lognormal = torch.exp(torch.randn(b, 1, 1, generator=g, device=device))
+    G = (torch.randn(b, t, dout, generator=g, device=device) * sigma_g * lognormal).to(
+        torch.bfloat16)
+    return A, G
+
+
+def cpu_baseline(sample_b: int, threads: int):
+    """Reference restatement on the CPU (oracle package), examples/s."""
+    import torch
+
+    from oracle import clip_oracle, ghost_oracle, noise_oracle
+
+    torch.set_num_threads(threads)
+    A, G = make_inputs(torch.device("cpu"), b=sample_b, seed=1)
+
+    def step():
+        leaves = [ghost_oracle.surrogate_per_example_grads(A, G)]
+        res = clip_oracle.stream_clip_and_sum(leaves, clip_oracle.conservative_bound(C))
+        center = clip_oracle.normalize(res.reduced[0], 1.0)
+        seed = noise_oracle.step_seed(0, 0)
+        draw = noise_oracle.draws_for([center], seed)[0]
+        return noise_oracle.sample(center, NM * C, draw)
+
+    step()  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return sample_b / times[len(times) // 2]
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, default=8, help="examples in the CPU sample")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the step shards by examples with one all-reduce; not built here).",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+
+    from opake_amd import _native
+    from opake_amd.clipping import ghost_clip_sum
+    from opake_amd.noise import gaussian_noise
+    from opake_amd.random import key
+
+    _native.load()
+    dev = torch.device("cuda:0")
+    A, G = make_inputs(dev)
+    noise_fn, state = gaussian_noise(noise_multiplier=NM, key=key(0), stream="device")
+
+    gemm_events = []
+
+    def step(st, record):
+        (res, aux), st = ghost_clip_sum(A, G, clipping_norm=C, return_aux=True, noise_fn=noise_fn,
+                                        noise_state=st, gemm_events=record)
+        return res, aux, st
+
+    for _ in range(args.warmup):
+        _, aux, state = step(state, None)
+    torch.cuda.synchronize()
+    clipped_frac = int(aux.num_clipped.item()) / B
+    print(f"[bench] warmup done, clipped fraction {clipped_frac:.3f}", file=sys.stderr, flush=True)
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        pair = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        gemm_events.append(pair)
+        _, aux, state = step(state, pair)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    print(f"[bench] {args.steps} timed steps in {elapsed:.4f} s", file=sys.stderr, flush=True)
+
+    gemm_ms = sum(a.elapsed_time(b) for a, b in gemm_events) / len(gemm_events)
+    gram_f, gemm_f = algorithmic_flops()
+    total_f = gram_f + gemm_f
+    ms_per_step = 1e3 * elapsed / args.steps
+    examples_per_s = B * args.steps / elapsed
+    step_tflops = total_f / (ms_per_step * 1e-3) / 1e12
+    gemm_tflops = gemm_f / (gemm_ms * 1e-3) / 1e12
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = min(len(os.sched_getaffinity(0)), 16)
+        print(f"[bench] cpu baseline: {args.cpu_sample} examples on {threads} threads",
+              file=sys.stderr, flush=True)
+        rate = cpu_baseline(args.cpu_sample, threads)
+        cpu = {
+            "value": rate,
+            "unit": "examples/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": (f"config 2 layer (4096x4096, T=512, bf16) at B={args.cpu_sample}: "
+                       "vmap(grad) of the linear surrogate loss + streaming clip-and-sum + "
+                       f"CPU randn noise; median of 3 steps after 1 warm-up; {cpu_model()}"),
+        }
+
+    line = {
+        "metric": METRIC,
+        "value": examples_per_s,
+        "unit": "examples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "linear 4096x4096, B=32, T=512, bf16; ghost-norm clip + sum + fused "
+                        "device-stream noise (BASELINE configs[1])",
+            "global_batch": B,
+            "seq_len": T,
+            "clipping_norm": C,
+            "noise_multiplier": NM,
+            "normalize_by": 1.0,
+            "G_scale": "N(0, C/sqrt(T*din*dout)) x lognormal(0,1) per example",
+            "clipped_fraction": clipped_frac,
+            "step_tflops": step_tflops,
+            "step_frac_of_bf16_peak": step_tflops / MFMA_BF16_PEAK_TFLOPS,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "clipped_sum_bf16_kernel",
+            "achieved": gemm_tflops,
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": gemm_tflops / MFMA_BF16_PEAK_TFLOPS,
+            "avg_launch_ms": gemm_ms,
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -124,6 +124,7 @@ def ghost_clip_sum(
     return_aux: bool = False,
     noise_fn=None,
     noise_state: GaussianNoiseState | None = None,
+    gemm_events=None,
 ):
     """Clipped (and optionally noised) sum of a linear layer's per-example gradients.
 
@@ -133,6 +134,8 @@ def ghost_clip_sum(
     ``(NoisedPytree, next_state)`` (or ``((NoisedPytree, aux), next_state)``),
     bit-identical to ``noise_fn(ghost_clip_sum(...), noise_state)``.
     ``auto_s_gamma`` selects AUTO-S scaling ``C / (||g|| + gamma)``.
+    ``gemm_events``: optional ``(start, end)`` pair of ``torch.cuda.Event``
+    recorded on the current stream around the clipped-sum launch (timing hook).
     """
     if isinstance(clipping_norm, PerGroup):
         raise ConfigurationError("per-group clipping is not supported by ghost_clip_sum")
@@ -187,10 +190,14 @@ def ghost_clip_sum(
                                          leaf_id=w_leaf, bias_leaf_id=b_leaf)
             next_state = GaussianNoiseState(
                 _step_counter=noise_state._step_counter + 1, _rng_key=noise_state._rng_key)
+        if gemm_events is not None:
+            gemm_events[0].record()
         w, b = ops.clipped_sum(
             A, G, cf.scale[0], plan=cf.plan, normalize_by=normalize_by, noise=spec,
             out_dtype=out_dtype, with_bias=bias,
         )
+        if gemm_events is not None:
+            gemm_events[1].record()
     tree = {"weight": w}
     if bias:
         tree["bias"] = b
