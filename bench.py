@@ -87,6 +87,20 @@ def cpu_baseline(sample_b: int, threads: int):
     return sample_b / times[len(times) // 2]
 
 
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed counter summary
+    (FETCH_SIZE / WRITE_SIZE runs scaled by a copy-kernel calibration), or None."""
+    path = os.path.join(ROOT, "profiles", "clipped_sum_cfg2_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(f"traffic_bytes_per_launch {kernel}:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -105,6 +119,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=8, help="examples in the CPU sample")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 5 device-to-device copies of MIB MiB (a plain copy kernel of "
+                         "known size, for scaling the FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -117,6 +134,16 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
+
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.randn(n, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n * 4, "copies": 5}), flush=True)
+        return 0
 
     from opake_amd import _native
     from opake_amd.clipping import ghost_clip_sum
@@ -209,7 +236,9 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": gemm_tflops / MFMA_BF16_PEAK_TFLOPS,
             "avg_launch_ms": gemm_ms,
-            "traffic": None,
+            "traffic": measured_traffic("clipped_sum_bf16_kernel"),
+            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1, "
+                            "copy-calibrated; profiles/clipped_sum_cfg2_traffic.md)",
         },
         "cpu_baseline": cpu,
     }

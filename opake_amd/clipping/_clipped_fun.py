@@ -1,0 +1,387 @@
+"""``clipped_fun`` / ``clipped_grad`` / ``auto_clipped_grad`` on the GPU.
+
+Same call sites, return shapes and error classes as the reference
+(packages/opake-engine/src/opake/api/engine/clipping/_clipped_fun.py:492-944,
+_clipped_grad.py:86-362, _auto.py:211-367):
+
+* per-example values come from ``torch.func.vmap`` over the batch arguments
+  (for ``clipped_grad``: ``vmap(grad_and_value(loss_fn))``, the reference's
+  ``_vmap_values``, _clipped_fun.py:476-489) on PyTorch-ROCm;
+* the clip-and-sum of the stacked values runs in the HIP leaf kernels
+  (``fused_stream_clip_and_sum``, the reference's streaming semantics,
+  _streaming.py:39-185);
+* ``x / normalize_by`` (_clipped_fun.py:880-883) and the ``ClippedPytree``
+  metadata ``max_norm = C / normalize_by`` (_clipped_grad.py:220);
+* ``microbatch_size`` accumulates chunk sums in float32 and casts once
+  (``_microbatch_accumulate_reduced``, _clipped_fun.py:252-345);
+* statistics count ``norm > C`` on the unguarded norms (:348-396).
+
+Not covered (``OperationError``): per-group norms, ``second_moment``, an
+explicit ``compute_dtype``, custom scale functions.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any, Callable
+
+import torch
+from torch.autograd.profiler import record_function
+from torch.func import grad_and_value, vmap
+
+from opake_amd.clipping._leaves import leaves_clip_sum, unsupported_reason
+from opake_amd.exceptions import ConfigurationError, InputTypeError, OperationError
+from opake_amd.pytree import tree_flatten, tree_leaves, tree_map, tree_unflatten
+from opake_amd.types import ClippedPytree, ClipState, PerGroup, clipped
+
+_DEFAULT_GAMMA = 0.01
+
+
+@dataclass(frozen=True)
+class FixedClipState(ClipState):
+    """Marker state for fixed clipping (``_clipped_fun.py:36-42``)."""
+
+
+@dataclass(frozen=True)
+class AutoClipState(ClipState):
+    """Marker state for AUTO-S scaling (``_auto.py``)."""
+
+
+@dataclass(frozen=True)
+class ClippedFunAux:
+    """Per-example diagnostics of :func:`clipped_fun` (``_clipped_fun.py:52-80``)."""
+
+    values: Any | None = None
+    norms: Any | None = None
+    clipped_norms: Any | None = None
+    value_aux: Any | None = None
+    clipping_rate: float | None = None
+    batch_size: int = 0
+    group_norms: dict | None = None
+
+
+@dataclass(frozen=True)
+class ClippingStats:
+    """Aggregated statistics (``_clipped_fun.py:83-88``)."""
+
+    num_clipped: float
+    clipping_rate: float | None
+    batch_size: int = 0
+
+
+@dataclass(frozen=True)
+class ClippedGradAux:
+    """Diagnostics of :func:`clipped_grad` (``_clipped_grad.py:34-61``)."""
+
+    loss_values: Any | None = None
+    grad_norms: Any | None = None
+    clipped_grad_norms: Any | None = None
+    loss_aux: Any | None = None
+    clipping_rate: float | None = None
+    batch_size: int = 0
+    group_norms: dict | None = None
+
+
+@dataclass(frozen=True)
+class _Scale:
+    kind: str
+    gamma: float = 0.0
+
+
+def _to_tuple(x) -> tuple:
+    return tuple(x) if isinstance(x, (tuple, list)) else (x,)
+
+
+def _validate_clipping_norm(clipping_norm) -> None:
+    if isinstance(clipping_norm, PerGroup):
+        raise OperationError("per-group clipping is not implemented by the HIP clip-and-sum")
+    if isinstance(clipping_norm, bool) or not isinstance(clipping_norm, (int, float)):
+        raise InputTypeError(f"clipping_norm must be a float, got {type(clipping_norm)}")
+    if clipping_norm <= 0:
+        raise ConfigurationError(f"clipping_norm must be positive, got {clipping_norm}")
+
+
+def _validate_static_args(argnums, batch_argnums, normalize_by) -> None:
+    """``_clipped_grad.py:64-83``."""
+    if normalize_by <= 0.0:
+        raise ConfigurationError(f"normalize_by must be > 0, got {normalize_by}.")
+    argnums, batch_argnums = _to_tuple(argnums), _to_tuple(batch_argnums)
+    if not batch_argnums:
+        raise ConfigurationError("Batch argnums must not be empty.")
+    if min(argnums + batch_argnums) < 0:
+        raise ConfigurationError(
+            f"argnums={argnums} and batch_argnums={batch_argnums} must be >= 0.")
+    shared = set(argnums) & set(batch_argnums)
+    if shared:
+        raise ConfigurationError(
+            "Cannot compute clipped gradients for argnums that have a batch axis. "
+            f"argnums={argnums} and batch_argnums={batch_argnums} with overlap {list(shared)}.")
+
+
+def _batch_size(args, batch_argnums) -> int:
+    for leaf in tree_leaves(args[batch_argnums[0]]):
+        return int(leaf.shape[0])
+    raise ConfigurationError("Could not determine the batch size from the batch arguments")
+
+
+def _slice_args(args, batch_argnums, start, stop):
+    return tuple(
+        tree_map(lambda x: x[start:stop], a) if i in batch_argnums else a
+        for i, a in enumerate(args)
+    )
+
+
+def _clip_sum_values(values, clipping_norm, scale, *, dtype, with_postsq):
+    """HIP clip-and-sum of a stacked pytree.
+
+    Returns ``(reduced, norms, post_sq, nclipped, storage_dtypes)``; the last is
+    a tree of the leaves' storage dtypes.
+    """
+    leaves, treedef = tree_flatten(values)
+    if not leaves:
+        raise ConfigurationError("the clipped function returned no tensor leaves")
+    B = leaves[0].shape[0]
+    reason = unsupported_reason(leaves, clipping_norm, scale, compute_dtype=None,
+                                second_moment=False, batch_size=B)
+    if reason is not None:
+        raise OperationError(f"HIP clip-and-sum cannot serve this call: {reason}")
+    out_dtypes = None
+    if dtype is not None:
+        if dtype != torch.float32:
+            raise OperationError(f"output dtype {dtype} is not supported (float32 or the leaf dtype)")
+        out_dtypes = {torch.bfloat16: torch.float32, torch.float32: torch.float32}
+    reduced, norms, post_sq, nclipped, _ = leaves_clip_sum(
+        [l.detach() for l in leaves], float(clipping_norm), kind=scale.kind, gamma=scale.gamma,
+        with_postsq=with_postsq, out_dtypes=out_dtypes)
+    return (tree_unflatten(treedef, reduced), norms, post_sq, nclipped,
+            tree_unflatten(treedef, [l.dtype for l in leaves]))
+
+
+def _make_clipped_fun(fun, has_aux, *, batch_argnums, clipping_norm, normalize_by, return_aux,
+                      return_stats, microbatch_size, dtype, scale, state):
+    batch_argnums = _to_tuple(batch_argnums)
+    if microbatch_size is not None and microbatch_size <= 0:
+        raise ConfigurationError(f"microbatch_size must be positive, got {microbatch_size}")
+    output_max_norm = clipping_norm / normalize_by
+
+    def run_chunk(args, kwargs, out_dtype):
+        in_dims = tuple(0 if i in batch_argnums else None for i in range(len(args)))
+        if has_aux:
+            values, aux = vmap(fun, in_dims=in_dims, out_dims=(0, 0), randomness="same")(
+                *args, **kwargs)
+        else:
+            values = vmap(fun, in_dims=in_dims, out_dims=0, randomness="same")(*args, **kwargs)
+            aux = None
+        return _clip_sum_values(values, clipping_norm, scale, dtype=out_dtype,
+                                with_postsq=return_aux) + (aux,)
+
+    def clipped_fn(*args, state, **kwargs):
+        if len(args) <= max(batch_argnums):
+            raise ConfigurationError("batch_argnums refers to a missing positional argument")
+        B = _batch_size(args, batch_argnums)
+        if B == 0:
+            raise ConfigurationError(
+                "Function-output clipping requires a non-empty batch because the output "
+                "pytree cannot be inferred otherwise.")
+        with torch.no_grad():
+            if microbatch_size is None:
+                reduced, norms, post_sq, nclipped, _, aux = run_chunk(args, kwargs, dtype)
+            else:
+                # Chunk sums are accumulated in float32 and cast once at the end.
+                acc, parts = None, []
+                for start in range(0, B, microbatch_size):
+                    chunk = _slice_args(args, batch_argnums, start, min(B, start + microbatch_size))
+                    r, n, p, c, storage, a = run_chunk(chunk, kwargs, torch.float32)
+                    acc = r if acc is None else tree_map(torch.add, acc, r)
+                    parts.append((n, p, c, a))
+                target = storage if dtype is None else tree_map(lambda _: dtype, storage)
+                reduced = tree_map(lambda x, dt: x.to(dt), acc, target)
+                norms = torch.cat([p[0] for p in parts])
+                post_sq = torch.cat([p[1] for p in parts]) if return_aux else None
+                nclipped = torch.stack([p[2] for p in parts]).sum()
+                aux = None
+                if parts[0][3] is not None:
+                    aux = tree_map(lambda *xs: torch.cat(xs), *[p[3] for p in parts])
+            if normalize_by != 1.0:
+                reduced = tree_map(lambda x: x / normalize_by, reduced)
+        output = clipped(reduced, max_norm=output_max_norm)
+        if not (return_aux or return_stats):
+            return output, state
+        num_clipped = float(nclipped.sum().item())
+        rate = num_clipped / float(B)
+        if return_aux:
+            fun_aux = ClippedFunAux(
+                values=aux, norms=norms, clipped_norms=torch.sqrt(post_sq),
+                clipping_rate=rate, batch_size=B)
+            return (output, fun_aux), state
+        return (output, ClippingStats(num_clipped=num_clipped, clipping_rate=rate,
+                                      batch_size=B)), state
+
+    return clipped_fn
+
+
+def clipped_fun(
+    fun: Callable[..., Any],
+    has_aux: bool = False,
+    *,
+    batch_argnums: int | tuple[int, ...] = 0,
+    clipping_norm: float = 1.0,
+    normalize_by: float = 1.0,
+    return_aux: bool = False,
+    return_stats: bool = False,
+    second_moment: bool = False,
+    microbatch_size: int | None = None,
+    dtype: torch.dtype | None = None,
+    compute_dtype: torch.dtype | None = None,
+):
+    """Clip each example's output of ``fun`` to L2 norm ``clipping_norm`` and sum.
+
+    Returns ``(clipped_fn, FixedClipState())``; ``clipped_fn(*args, state=)``
+    returns ``(ClippedPytree, state)`` (``((ClippedPytree, aux), state)`` with
+    ``return_aux`` / ``return_stats``).
+    """
+    if normalize_by <= 0.0:
+        raise ConfigurationError(f"normalize_by must be > 0, got {normalize_by}.")
+    if return_aux and return_stats:
+        raise ConfigurationError("return_stats cannot be combined with return_aux=True")
+    if second_moment:
+        raise OperationError("second_moment=True is not implemented by the HIP clip-and-sum")
+    if compute_dtype is not None:
+        raise OperationError("an explicit compute_dtype is not implemented by the HIP clip-and-sum")
+    _validate_clipping_norm(clipping_norm)
+    state = FixedClipState()
+    fn = _make_clipped_fun(fun, has_aux, batch_argnums=batch_argnums, clipping_norm=clipping_norm,
+                           normalize_by=normalize_by, return_aux=return_aux,
+                           return_stats=return_stats, microbatch_size=microbatch_size,
+                           dtype=dtype, scale=_Scale("fixed"), state=state)
+    return fn, state
+
+
+def _grad_wrapper(loss_fn, argnums, has_aux, return_aux):
+    """Per-example ``grad_and_value`` returning ``g`` or ``(g, {"values", "value_aux"})``."""
+    gv = grad_and_value(loss_fn, argnums=argnums, has_aux=has_aux)
+
+    def grad_fn(*args, **kwargs):
+        g, out = gv(*args, **kwargs)
+        if not return_aux:
+            return g
+        if has_aux:
+            value, value_aux = out
+            return g, {"values": value, "value_aux": value_aux}
+        return g, {"values": out}
+
+    return grad_fn
+
+
+def _make_grad(loss_fn, argnums, has_aux, *, clipping_norm, normalize_by, batch_argnums,
+               return_aux, return_stats, microbatch_size, dtype, scale, state):
+    _validate_static_args(argnums, batch_argnums, normalize_by)
+    if return_aux and return_stats:
+        raise ConfigurationError("return_stats cannot be combined with return_aux=True")
+    argnums_t = argnums if isinstance(argnums, int) else tuple(argnums)
+    grad_fn = _grad_wrapper(loss_fn, argnums_t, has_aux, return_aux)
+    inner = _make_clipped_fun(grad_fn, return_aux, batch_argnums=batch_argnums,
+                              clipping_norm=clipping_norm, normalize_by=normalize_by,
+                              return_aux=return_aux, return_stats=return_stats,
+                              microbatch_size=microbatch_size, dtype=dtype, scale=scale,
+                              state=state)
+    batch_t = _to_tuple(batch_argnums)
+    max_norm = clipping_norm / normalize_by
+
+    def wrapper(*args, state, **kwargs):
+        if _batch_size(args, batch_t) == 0:
+            zeros = tree_map(torch.zeros_like, args[argnums_t] if isinstance(argnums_t, int)
+                             else tuple(args[i] for i in argnums_t))
+            grads = clipped(zeros, max_norm=max_norm)
+            if return_aux:
+                empty = torch.empty(0)
+                return (grads, ClippedGradAux(loss_values=empty, grad_norms=empty,
+                                              clipped_grad_norms=empty, clipping_rate=0.0,
+                                              batch_size=0)), state
+            if return_stats:
+                return (grads, ClippingStats(num_clipped=0.0, clipping_rate=0.0,
+                                             batch_size=0)), state
+            return grads, state
+        with record_function("opake::clipped_grad"):
+            result, st = inner(*args, state=state, **kwargs)
+        if not return_aux:
+            return result, st
+        grads, aux = result
+        values = aux.values or {}
+        return (grads, ClippedGradAux(
+            loss_values=values.get("values"), grad_norms=aux.norms,
+            clipped_grad_norms=aux.clipped_norms, loss_aux=values.get("value_aux"),
+            clipping_rate=aux.clipping_rate, batch_size=aux.batch_size)), st
+
+    return wrapper
+
+
+def clipped_grad(
+    loss_fn: Callable,
+    argnums: int | tuple[int, ...] = 0,
+    has_aux: bool = False,
+    *,
+    clipping_norm: float,
+    normalize_by: float = 1.0,
+    batch_argnums: int | tuple[int, ...] = 1,
+    return_aux: bool = False,
+    return_stats: bool = False,
+    second_moment: bool = False,
+    microbatch_size: int | None = None,
+    dtype: torch.dtype | None = None,
+    compute_dtype: torch.dtype | None = None,
+):
+    """Sum of per-example clipped gradients of ``loss_fn`` (``_clipped_grad.py:86-362``)."""
+    if second_moment:
+        raise OperationError("second_moment=True is not implemented by the HIP clip-and-sum")
+    if compute_dtype is not None:
+        raise OperationError("an explicit compute_dtype is not implemented by the HIP clip-and-sum")
+    _validate_clipping_norm(clipping_norm)
+    state = FixedClipState()
+    fn = _make_grad(loss_fn, argnums, has_aux, clipping_norm=clipping_norm,
+                    normalize_by=normalize_by, batch_argnums=batch_argnums,
+                    return_aux=return_aux, return_stats=return_stats,
+                    microbatch_size=microbatch_size, dtype=dtype, scale=_Scale("fixed"),
+                    state=state)
+    return fn, state
+
+
+def auto_clipped_grad(
+    loss_fn: Callable,
+    argnums: int | tuple[int, ...] = 0,
+    has_aux: bool = False,
+    *,
+    R: float = 1.0,
+    gamma: float = _DEFAULT_GAMMA,
+    normalize_by: float = 1.0,
+    batch_argnums: int | tuple[int, ...] = 1,
+    return_aux: bool = False,
+    return_stats: bool = False,
+    microbatch_size: int | None = None,
+    dtype: Any = None,
+    second_moment: bool = False,
+):
+    """AUTO-S: ``R * g_i / (||g_i|| + gamma)`` per example, summed (``_auto.py:211-367``)."""
+    if second_moment:
+        raise OperationError("second_moment=True is not implemented by the HIP clip-and-sum")
+    if isinstance(gamma, bool) or not isinstance(gamma, (int, float)) or not gamma > 0:
+        raise ConfigurationError(f"gamma must be a positive float, got {gamma!r}")
+    _validate_clipping_norm(R)
+    state = AutoClipState()
+    fn = _make_grad(loss_fn, argnums, has_aux, clipping_norm=R, normalize_by=normalize_by,
+                    batch_argnums=batch_argnums, return_aux=return_aux,
+                    return_stats=return_stats, microbatch_size=microbatch_size, dtype=dtype,
+                    scale=_Scale("auto_s", float(gamma)), state=state)
+    return fn, state
+
+
+__all__ = [
+    "AutoClipState",
+    "ClippedFunAux",
+    "ClippedGradAux",
+    "ClippingStats",
+    "FixedClipState",
+    "auto_clipped_grad",
+    "clipped_fun",
+    "clipped_grad",
+]

@@ -1,0 +1,282 @@
+"""Materialised-leaf clip-and-sum on the GPU: the fused-backend seam.
+
+``fused_stream_clip_and_sum`` has the signature and return value of the
+reference's streaming clip-and-sum
+(packages/opake-engine/src/opake/api/engine/clipping/_streaming.py:39-185) and
+of the backend that ``register_fused_clip_backend`` accepts
+(``_kernel_backend.py:9-17``, consulted at ``_clipped_fun.py:442-467,680-692``).
+It takes stacked per-example values ``[B, *P]`` and does the work in a fixed
+number of HIP launches per storage dtype, whatever the number of leaves:
+
+1. ``dpc_leaves_sqnorm``: per (example, leaf) fp64 sums of fp32 squares of the
+   sanitised values, 2048-element tiles, then ``dpc_row_sum_f64`` folds the
+   leaves in flatten order (the reference's ``sq_norm = sq_0 + sq_1 + ...``);
+2. ``dpc_clip_factors``: the guarded scale per storage dtype (fixed or AUTO-S);
+3. ``dpc_leaves_apply``: scale in fp32, one cast to the storage dtype, bf16
+   subnormals that rounded up zeroed, fp32 sum over the batch in example order.
+
+A call the kernels do not cover (per-group norms, ``second_moment``, an
+explicit ``compute_dtype``, dtypes other than float32 / bfloat16, leaves that
+need grad) goes to the ``fallback`` the caller registered with
+:func:`make_fused_backend` -- in the reference that is its own PyTorch
+streaming path -- and raises ``OperationError`` when there is none.
+"""
+
+from __future__ import annotations
+
+import math
+from collections import OrderedDict
+
+import numpy as np
+import torch
+
+from opake_amd import _native as nat
+from opake_amd import ops
+from opake_amd.clipping import _numerics as num
+from opake_amd.exceptions import OperationError
+from opake_amd.pytree import tree_flatten, tree_unflatten
+
+TILE = 2048  # elements per tile: the reference's blocked-reduction width
+_MAX_BATCH = 65535
+_SUPPORTED = (torch.float32, torch.bfloat16)
+_MAX_PLANS = 64
+
+_fused_clip_backend = None
+
+
+def register_fused_clip_backend(backend) -> None:
+    """Register the fused clip-and-sum implementation (``_kernel_backend.py:9-12``)."""
+    global _fused_clip_backend
+    _fused_clip_backend = backend
+
+
+def get_fused_clip_backend():
+    """The registered implementation, if any (``_kernel_backend.py:15-17``)."""
+    return _fused_clip_backend
+
+
+def unsupported_reason(leaves, clipping_norm, scale, *, compute_dtype, second_moment,
+                       batch_size) -> str | None:
+    """Why the kernels cannot serve this call, or ``None``."""
+    if hasattr(clipping_norm, "groups"):
+        return "per-group clipping norms are not supported by the leaf kernels"
+    if getattr(scale, "kind", "fixed") not in ("fixed", "auto_s"):
+        return f"unknown scale kind {scale.kind!r}"
+    if second_moment:
+        return "second_moment=True is not supported"
+    if compute_dtype is not None:
+        return "an explicit compute_dtype is not supported"
+    if batch_size > _MAX_BATCH:
+        return f"batch size {batch_size} exceeds {_MAX_BATCH}"
+    grad_mode = torch.is_grad_enabled()
+    for leaf in leaves:
+        if not isinstance(leaf, torch.Tensor):
+            return f"non-tensor leaf of type {type(leaf).__name__}"
+        if not leaf.is_cuda:
+            return f"leaf on device {leaf.device}, not a ROCm device"
+        if leaf.device != leaves[0].device:
+            return "the leaves span more than one device"
+        if leaf.dtype not in _SUPPORTED:
+            return f"leaf dtype {leaf.dtype} (supported: float32, bfloat16)"
+        if grad_mode and leaf.requires_grad:
+            return "a leaf requires grad"
+        if leaf.dim() == 0 or leaf.shape[0] != batch_size:
+            return "a leaf's leading dimension is not the batch"
+    return None
+
+
+def _output_dtypes(leaves, reduce_leaf):
+    """Output dtype of ``reduce_leaf`` per storage dtype (the storage dtype or float32)."""
+    out = {}
+    for dtype in {leaf.dtype for leaf in leaves}:
+        probe = reduce_leaf(torch.zeros((1,), dtype=dtype, device=leaves[0].device))
+        if probe.dtype not in (dtype, torch.float32):
+            return None
+        out[dtype] = probe.dtype
+    return out
+
+
+_PLANS: OrderedDict = OrderedDict()
+
+
+def _plan(leaves, device):
+    """Tile tables per storage dtype, built on the host and copied once;
+    cached by device and per-example shapes (bounded LRU)."""
+    key = (device, tuple((leaf.dtype, tuple(leaf.shape[1:])) for leaf in leaves))
+    plan = _PLANS.get(key)
+    if plan is not None:
+        _PLANS.move_to_end(key)
+        return plan
+    groups = []
+    for dtype in (torch.bfloat16, torch.float32):
+        idx = [i for i, leaf in enumerate(leaves) if leaf.dtype == dtype]
+        if not idx:
+            continue
+        sizes = np.array([math.prod(leaves[i].shape[1:]) for i in idx], dtype=np.int64)
+        tiles = (sizes + TILE - 1) // TILE
+        tile_start = np.concatenate([[0], np.cumsum(tiles)]).astype(np.int64)
+        tile_leaf = np.repeat(np.arange(len(idx), dtype=np.int32), tiles)
+        tile_local = (np.arange(int(tile_start[-1]), dtype=np.int64) - tile_start[tile_leaf]).astype(
+            np.int32)
+        offsets = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+
+        def dev(a):
+            return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+        groups.append({
+            "dtype": dtype,
+            "idx": idx,
+            "sizes_host": sizes.tolist(),
+            "offsets_host": offsets.tolist(),
+            "total": int(sizes.sum()),
+            "n_tiles": int(tile_start[-1]),
+            "sizes": dev(sizes),
+            "out_offs": dev(offsets),
+            "leaf_col": dev(np.array(idx, dtype=np.int32)),
+            "tile_start": dev(tile_start),
+            "tile_leaf": dev(tile_leaf),
+            "tile_local": dev(tile_local),
+        })
+    plan = {"groups": groups, "n_leaves": len(leaves)}
+    _PLANS[key] = plan
+    if len(_PLANS) > _MAX_PLANS:
+        _PLANS.popitem(last=False)
+    return plan
+
+
+_MARKERS: dict = {}
+
+
+def _dtype_marker(leaf):
+    key = (leaf.dtype, leaf.device)
+    marker = _MARKERS.get(key)
+    if marker is None:
+        marker = _MARKERS[key] = leaf.new_zeros(())
+    return marker
+
+
+def leaves_clip_sum(leaves, clipping_norm: float, *, kind: str = "fixed", gamma: float = 0.0,
+                    with_postsq: bool = False, out_dtypes=None):
+    """Clip-and-sum of stacked leaves with the HIP kernels.
+
+    Returns ``(reduced, norms, post_sq, nclipped, scales)``: per-leaf batch sums
+    (in ``out_dtypes[dtype]``, default the leaf dtype), float32 norms [B],
+    float32 ``||stored||^2`` per example (or ``None``), int32 [1] count of
+    ``norm > C`` and the float32 scale rows ``{dtype: [B]}``.
+    """
+    device = leaves[0].device
+    B = leaves[0].shape[0]
+    L = len(leaves)
+    contiguous = [l if l.is_contiguous() else l.contiguous() for l in leaves]
+    plan = _plan(contiguous, device)
+    stream = nat.stream_handle(device)
+    acc = torch.float32
+    roundoff = num.norm_roundoff(acc, torch.float64, L,
+                                 num.reduction_terms([math.prod(l.shape[1:]) for l in leaves]))
+    leaf_sq = torch.empty((B, L), dtype=torch.float64, device=device)
+    groups = plan["groups"]
+    ptr_tables = []
+    for g in groups:
+        ptrs = torch.tensor([contiguous[i].data_ptr() for i in g["idx"]], dtype=torch.int64)
+        ptr_tables.append(ptrs.pin_memory().to(device, non_blocking=True))
+        partial = torch.empty((B, max(g["n_tiles"], 1)), dtype=torch.float64, device=device)
+        nat.call("dpc_leaves_sqnorm", nat.ptr(ptr_tables[-1]), nat.ptr(g["sizes"]),
+                 nat.ptr(g["tile_leaf"]), nat.ptr(g["tile_local"]), nat.ptr(g["tile_start"]),
+                 nat.ptr(g["leaf_col"]), len(g["idx"]), g["n_tiles"], B,
+                 nat.dtype_code(g["dtype"]), nat.ptr(partial), nat.ptr(leaf_sq), L, stream)
+    sq = torch.empty(B, dtype=torch.float64, device=device)
+    nat.call("dpc_row_sum_f64", nat.ptr(leaf_sq), B, L, 0, nat.ptr(sq), stream)
+    guards = [num.guard_constants(g["dtype"], torch.promote_types(g["dtype"], acc), roundoff)
+              for g in groups]
+    cf = ops.clip_factors(sq, num.conservative_bound(clipping_norm), guards,
+                          kind=nat.SCALE_AUTO_S if kind == "auto_s" else nat.SCALE_FIXED,
+                          gamma=gamma, count_threshold=num.float32_of(clipping_norm))
+    reduced = [None] * L
+    post_sq = None
+    if with_postsq:
+        post_sq = torch.zeros(B, dtype=torch.float32, device=device)
+    scales = {}
+    for gi, g in enumerate(groups):
+        dtype = g["dtype"]
+        out_dtype = (out_dtypes or {}).get(dtype, dtype)
+        flat = torch.empty(g["total"], dtype=out_dtype, device=device)
+        tile_sq = (torch.empty((B, g["n_tiles"]), dtype=torch.float32, device=device)
+                   if with_postsq else None)
+        scale_row = cf.scale[gi]
+        scales[dtype] = scale_row
+        nat.call("dpc_leaves_apply", nat.ptr(ptr_tables[gi]), nat.ptr(g["sizes"]),
+                 nat.ptr(g["tile_leaf"]), nat.ptr(g["tile_local"]), nat.ptr(g["out_offs"]),
+                 g["n_tiles"], B, nat.dtype_code(dtype), nat.ptr(scale_row), nat.ptr(flat),
+                 nat.dtype_code(out_dtype), nat.ptr(tile_sq), stream)
+        if with_postsq:
+            post_sq += tile_sq.sum(dim=1)
+        for j, i in enumerate(g["idx"]):
+            off, n = g["offsets_host"][j], g["sizes_host"][j]
+            reduced[i] = flat[off:off + n].view(leaves[i].shape[1:])
+    return reduced, cf.norms, post_sq, cf.nclipped, scales
+
+
+def make_fused_backend(fallback=None):
+    """A backend for :func:`register_fused_clip_backend`.
+
+    ``fallback`` (the caller's own streaming implementation, same signature)
+    serves calls the kernels do not support; without one they raise
+    ``OperationError``.
+    """
+
+    def backend(values, clipping_norm, *, scale, batch_size, reduce_leaf, compute_dtype,
+                second_moment, return_aux, return_stats):
+        leaves, treedef = tree_flatten(values)
+        reason = unsupported_reason(leaves, clipping_norm, scale, compute_dtype=compute_dtype,
+                                    second_moment=second_moment, batch_size=batch_size)
+        out_dtypes = None
+        if reason is None and leaves and batch_size > 0:
+            out_dtypes = _output_dtypes(leaves, reduce_leaf)
+            if out_dtypes is None:
+                reason = "the requested output dtype is not supported"
+        if reason is not None:
+            if fallback is None:
+                raise OperationError(f"HIP clip-and-sum cannot serve this call: {reason}")
+            return fallback(values, clipping_norm, scale=scale, batch_size=batch_size,
+                            reduce_leaf=reduce_leaf, compute_dtype=compute_dtype,
+                            second_moment=second_moment, return_aux=return_aux,
+                            return_stats=return_stats)
+        C = float(clipping_norm)
+        kind = getattr(scale, "kind", "fixed")
+        gamma = float(getattr(scale, "gamma", 0.0))
+        if not leaves or batch_size == 0:
+            device = leaves[0].device if leaves else torch.device("cuda")
+            reduced = [reduce_leaf(l) for l in leaves]
+            norms = torch.zeros(batch_size, dtype=torch.float32, device=device)
+            post = norms.clone()
+        else:
+            reduced, norms, post, _, _ = leaves_clip_sum(
+                leaves, C, kind=kind, gamma=gamma, with_postsq=return_aux, out_dtypes=out_dtypes)
+        diagnostics = {}
+        if return_aux or return_stats:
+            diagnostics["norms"] = norms.detach()
+        if return_aux:
+            diagnostics["clipped_norms"] = torch.sqrt(post).detach()
+        markers = [_dtype_marker(l) for l in leaves]
+        return (
+            tree_unflatten(treedef, reduced),
+            tree_unflatten(treedef, markers),
+            (),
+            (),
+            diagnostics if (return_aux or return_stats) else (),
+        )
+
+    return backend
+
+
+fused_stream_clip_and_sum = make_fused_backend()
+
+
+__all__ = [
+    "fused_stream_clip_and_sum",
+    "get_fused_clip_backend",
+    "leaves_clip_sum",
+    "make_fused_backend",
+    "register_fused_clip_backend",
+    "unsupported_reason",
+]
