@@ -1,12 +1,19 @@
 // Per-example squared gradient norms of linear layers via the Gram identity
 //   ||G_i^T A_i||_F^2 = <A_i A_i^T, G_i G_i^T>
 // (no per-example gradient is ever formed).  The T x T Gram matrices are
-// split into 128 x 128 tiles; a workgroup owns one (example, tile pair p <= q)
-// and computes the (p, q) tile of both A A^T and G G^T with bf16 MFMA
-// (fp32 accumulate), then their element-wise inner product in fp64.  Pairs
-// with p < q count twice (both Gram matrices are symmetric).  One fp64
-// partial per (example, pair) lands in the workspace; dpc_row_sum_f64 folds
-// them into sqnorm in a fixed order, so results are deterministic.
+// split into 128 x 128 tiles; a workgroup owns one (example, tile pair p <= q).
+// Its 8 waves form two groups of 4: group 0 computes the (p, q) tile of
+// A A^T while group 1 computes the same tile of G G^T, concurrently, with
+// bf16 MFMA and fp32 accumulators (each wave 64 x 64 of the tile).  Group 1
+// then hands its tile to group 0 through LDS for the element-wise inner
+// product in fp64.  Pairs with p < q count twice (both Gram matrices are
+// symmetric).  One fp64 partial per (example, pair) lands in the workspace;
+// dpc_row_sum_f64 folds them into sqnorm in a fixed order, so results are
+// deterministic.
+//
+// Workgroups are placed so that all pairs of one example run on one XCD
+// (hardware dispatch is round-robin over the 8 XCDs): the pairs re-read the
+// example's tiles from that XCD's L2 instead of from HBM.
 #include "common.h"
 
 namespace {
@@ -14,9 +21,15 @@ namespace {
 constexpr int kGramTile = 128;  // rows of a T-tile
 constexpr int kGramK = 64;      // reduction depth staged per LDS buffer
 constexpr int kGramThreads = 256;
+constexpr int kGramGroupThreads = 256;                   // one group = 4 waves
+constexpr int kGramMfmaThreads = 2 * kGramGroupThreads;  // A group + G group
+constexpr int kTileBytes = kGramTile * kGramK * 2;       // 16 KiB per staged tile
+constexpr int kStageBytes = 2 * kTileBytes;              // p tile + q tile
+constexpr int kGroupBytes = 2 * kStageBytes;             // two stages
+constexpr int kXcds = 8;
 
 // Byte offset of 16-byte chunk `c` of row `r` in a [rows][64] bf16 LDS tile.
-// The XOR swizzle spreads both the transposed writes and the MFMA fragment
+// The XOR swizzle spreads both the row-chunk writes and the MFMA fragment
 // reads (32 consecutive rows, one chunk) over all 32 banks.
 __device__ __forceinline__ int lds_off(int r, int c) {
   return r * 128 + ((c ^ ((r ^ (r >> 3)) & 7)) << 4);
@@ -29,14 +42,13 @@ __device__ __forceinline__ void pair_from_index(int pair, int* p, int* q) {
   *p = pair - qq * (qq + 1) / 2;
 }
 
-// Load a [128 x 64] bf16 tile (rows row0.., columns k0..) of one example into
-// registers: four 16-byte chunks per thread, zero outside [T) x [d).
+// Load 128 rows x 64 columns (bf16) starting at (row0, k0) of X [T, d]:
+// four 16-byte chunks per group thread, zero outside [T) x [d).
 __device__ __forceinline__ void gram_load(const uint16_t* __restrict__ X, int T, int d, int row0,
-                                          int k0, u32x4_t regs[4]) {
-  const int tid = threadIdx.x;
+                                          int k0, int gt, u32x4_t regs[4]) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    int q = tid + kGramThreads * j;
+    int q = gt + kGramGroupThreads * j;
     int r = q >> 3, c = q & 7;
     int row = row0 + r, col = k0 + c * 8;
     if (row < T && col < d) {
@@ -47,19 +59,20 @@ __device__ __forceinline__ void gram_load(const uint16_t* __restrict__ X, int T,
   }
 }
 
-__device__ __forceinline__ void gram_store(uint8_t* lds, const u32x4_t regs[4]) {
-  const int tid = threadIdx.x;
+__device__ __forceinline__ void gram_store(uint8_t* tile, int gt, const u32x4_t regs[4]) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    int q = tid + kGramThreads * j;
-    *reinterpret_cast<u32x4_t*>(lds + lds_off(q >> 3, q & 7)) = regs[j];
+    int q = gt + kGramGroupThreads * j;
+    *reinterpret_cast<u32x4_t*>(tile + lds_off(q >> 3, q & 7)) = regs[j];
   }
 }
 
-// acc[bi][bj] += X[p rows] X[q rows]^T over one staged K slab.
-__device__ __forceinline__ void gram_mma(const uint8_t* lp, const uint8_t* lq, f32x16_t acc[2][2]) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int wr = w >> 1, wc = w & 1;
+// acc[bi][bj] += X[p rows] X[q rows]^T over one staged 64-deep slab; wave wg
+// of the group owns rows wr * 64.. of p and wr * 64.. of q.
+__device__ __forceinline__ void gram_mma(const uint8_t* lp, const uint8_t* lq, int wg,
+                                         f32x16_t acc[2][2]) {
+  const int lane = threadIdx.x & 63;
+  const int wr = wg >> 1, wc = wg & 1;
 #pragma unroll
   for (int kk = 0; kk < kGramK / 16; ++kk) {
     const int c = kk * 2 + (lane >> 5);
@@ -77,41 +90,6 @@ __device__ __forceinline__ void gram_mma(const uint8_t* lp, const uint8_t* lq, f
   }
 }
 
-// One Gram tile (p, q) of X X^T for example-base pointer X ([T, d]).
-__device__ __forceinline__ void gram_tile(const uint16_t* __restrict__ X, int T, int d, int p,
-                                          int q, uint8_t* lds, f32x16_t acc[2][2]) {
-  const bool diag = (p == q);
-  constexpr int kTileBytes = kGramTile * kGramK * 2;  // 16 KiB
-  uint8_t* buf[2] = {lds, lds + 2 * kTileBytes};
-  u32x4_t rp[4], rq[4];
-  const int nk = ceil_div(d, kGramK);
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
-
-  gram_load(X, T, d, p * kGramTile, 0, rp);
-  if (!diag) gram_load(X, T, d, q * kGramTile, 0, rq);
-  gram_store(buf[0], rp);
-  if (!diag) gram_store(buf[0] + kTileBytes, rq);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    uint8_t* cur = buf[kt & 1];
-    uint8_t* nxt = buf[(kt + 1) & 1];
-    const bool more = kt + 1 < nk;
-    if (more) {
-      gram_load(X, T, d, p * kGramTile, (kt + 1) * kGramK, rp);
-      if (!diag) gram_load(X, T, d, q * kGramTile, (kt + 1) * kGramK, rq);
-    }
-    gram_mma(cur, diag ? cur : cur + kTileBytes, acc);
-    if (more) {
-      gram_store(nxt, rp);
-      if (!diag) gram_store(nxt + kTileBytes, rq);
-    }
-    __syncthreads();
-  }
-}
-
 __device__ __forceinline__ double block_sum_f64(double v, double* red) {
   for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -125,31 +103,104 @@ __device__ __forceinline__ double block_sum_f64(double v, double* red) {
   return total;
 }
 
-__global__ void __launch_bounds__(kGramThreads)
+// Linear workgroup id -> logical (example, pair) index so that each XCD
+// receives a contiguous range of logical indices.  `padded` is the grid size
+// (a multiple of kXcds); returns -1 for padding workgroups.
+__device__ __forceinline__ int xcd_logical_block(int padded, int nblocks) {
+  const int b = blockIdx.x;
+  const int per = padded / kXcds;
+  const int l = (b % kXcds) * per + b / kXcds;
+  return l < nblocks ? l : -1;
+}
+
+__global__ void __launch_bounds__(kGramMfmaThreads, 1)
 gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ G, int T,
-                      int din, int dout, int npairs, double* __restrict__ partial) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kGramTile * kGramK * 2];
-  __shared__ double red[kGramThreads / 64];
-  const int pair = blockIdx.x, ex = blockIdx.y;
+                      int din, int dout, int npairs, int nblocks, double* __restrict__ partial) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kGroupBytes];
+  __shared__ double red[kGramMfmaThreads / 64];
+  const int l = xcd_logical_block(gridDim.x, nblocks);
+  if (l < 0) return;  // padding workgroup: exits before any barrier
+  const int ex = l / npairs, pair = l % npairs;
   int p, q;
   pair_from_index(pair, &p, &q);
+  const bool diag = (p == q);
 
-  f32x16_t pa[2][2], pg[2][2];
-  gram_tile(A + (size_t)ex * T * din, T, din, p, q, lds, pa);
-  gram_tile(G + (size_t)ex * T * dout, T, dout, p, q, lds, pg);
+  const int group = threadIdx.x / kGramGroupThreads;
+  const int gt = threadIdx.x % kGramGroupThreads;
+  const int wg = gt >> 6;
+  const int d = group ? dout : din;
+  const uint16_t* X = group ? G + (size_t)ex * T * dout : A + (size_t)ex * T * din;
+  uint8_t* mine = lds + group * kGroupBytes;
+  const int nk_mine = ceil_div(d, kGramK);
+  const int nk = max(ceil_div(din, kGramK), ceil_div(dout, kGramK));
 
-  // Both tiles share the MFMA output layout, so the element-wise product
-  // needs no knowledge of which (s, t) a register holds.
-  double s = 0.0;
+  f32x16_t acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
+
+  // Register double buffer: step s + 1 is in flight while step s is multiplied
+  // and step s + 2 is requested.
+  u32x4_t rp0[4], rq0[4], rp1[4], rq1[4];
+  auto load = [&](int step, u32x4_t* rp, u32x4_t* rq) {
+    gram_load(X, T, d, p * kGramTile, step * kGramK, gt, rp);
+    if (!diag) gram_load(X, T, d, q * kGramTile, step * kGramK, gt, rq);
+  };
+  auto store = [&](int stage, const u32x4_t* rp, const u32x4_t* rq) {
+    uint8_t* st = mine + stage * kStageBytes;
+    gram_store(st, gt, rp);
+    if (!diag) gram_store(st + kTileBytes, gt, rq);
+  };
+  auto body = [&](int s, u32x4_t* rp_next, u32x4_t* rq_next, u32x4_t* rp_free,
+                  u32x4_t* rq_free) {
+    // rp_next/rq_next hold step s + 1; rp_free/rq_free receive step s + 2.
+    if (s + 2 < nk_mine) load(s + 2, rp_free, rq_free);
+    if (s < nk_mine) {
+      const uint8_t* st = mine + (s & 1) * kStageBytes;
+      gram_mma(st, diag ? st : st + kTileBytes, wg, acc);
+    }
+    if (s + 1 < nk_mine) store((s + 1) & 1, rp_next, rq_next);
+    __syncthreads();
+  };
+
+  if (nk_mine > 0) load(0, rp0, rq0);
+  if (nk_mine > 1) load(1, rp1, rq1);
+  if (nk_mine > 0) store(0, rp0, rq0);
+  __syncthreads();
+  int s = 0;
+  for (; s + 1 < nk; s += 2) {
+    body(s, rp1, rq1, rp0, rq0);
+    body(s + 1, rp0, rq0, rp1, rq1);
+  }
+  if (s < nk) body(s, rp1, rq1, rp0, rq0);
+
+  // Group 1 hands its G G^T tile to group 0 through LDS (same fragment order,
+  // element e of thread gt at float index e * 256 + gt).
+  float* xfer = reinterpret_cast<float*>(lds);
+  if (group == 1) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s += (double)pa[i][j][r] * (double)pg[i][j][r];
-  double total = block_sum_f64(s, red);
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xfer[((i * 2 + j) * 16 + r) * kGramGroupThreads + gt] = acc[i][j][r];
+  }
+  __syncthreads();
+  double sum = 0.0;
+  if (group == 0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          sum += (double)acc[i][j][r] *
+                 (double)xfer[((i * 2 + j) * 16 + r) * kGramGroupThreads + gt];
+  }
+  double total = block_sum_f64(sum, red);
   if (threadIdx.x == 0) {
-    partial[(size_t)ex * npairs + pair] = (p == q) ? total : 2.0 * total;
+    partial[(size_t)ex * npairs + pair] = diag ? total : 2.0 * total;
   }
 }
 
@@ -301,8 +352,11 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
   if (mfma) {
     int nt = ceil_div(T, kGramTile);
     npairs = nt * (nt + 1) / 2;
-    hipLaunchKernelGGL(gram_mfma_bf16_kernel, dim3(npairs, B), dim3(kGramThreads), 0, s,
-                       (const uint16_t*)A, (const uint16_t*)G, T, din, dout, npairs, partial);
+    const int nblocks = npairs * B;
+    const int padded = ceil_div(nblocks, kXcds) * kXcds;
+    hipLaunchKernelGGL(gram_mfma_bf16_kernel, dim3(padded), dim3(kGramMfmaThreads), 0, s,
+                       (const uint16_t*)A, (const uint16_t*)G, T, din, dout, npairs, nblocks,
+                       partial);
   } else {
     int nt = ceil_div(T, kGenTile);
     npairs = nt * (nt + 1) / 2;
