@@ -4,22 +4,25 @@
 // fused into the epilogue.
 //
 // Fast path (bf16, T % 64 == 0, din % 8 == 0, dout % 8 == 0):
-//   * 256 x 256 output tile per workgroup, 4 waves of 128 x 128, bf16 MFMA
-//     32x32x16 with fp32 accumulators (16 blocks per wave);
-//   * operands are stored m- (n-) contiguous in HBM; each thread loads an
-//     8 (k) x 8 (m) block with 16-byte loads, transposes it in registers and
-//     writes 8 k-contiguous rows into an XOR-swizzled LDS tile, so the MFMA
-//     fragment reads are single 16-byte LDS loads without bank conflicts;
-//   * two LDS stages (128 KiB), one barrier per 64-deep K step, the next
-//     step's global loads in flight during the current step's MFMAs;
-//   * a K step never straddles two examples, so the per-example scale is one
-//     scalar per step: it multiplies the G operand in fp32 during the
-//     register transpose and the product is rounded to bf16 once
-//     (v_cvt_pk_bf16_f32, round-to-nearest-even) -- the same single rounding
-//     of a scaled value that the reference applies when it stores a scaled
-//     bf16 per-example gradient.  The accumulators never leave the AGPRs.
-//     Examples with scale 0 are skipped through the clip plan, so their data
-//     (including any NaN/Inf) is never read;
+//   * 256 x 256 output tile per workgroup, 8 waves (2 per SIMD) of 128 x 64,
+//     bf16 MFMA 32x32x16 with fp32 accumulators (8 blocks per wave);
+//   * both operands are m- (n-) contiguous in HBM and are staged into LDS in
+//     that natural [k][m] layout (16-byte loads, 16-byte LDS stores, 64-byte
+//     blocks XOR-swizzled by the k row).  The MFMA fragments, which need 8
+//     consecutive k per lane, come out of LDS through the gfx950 transposing
+//     read ds_read_b64_tr_b16 (two per fragment), so no data is transposed
+//     in registers; all LDS accesses are free of bank conflicts;
+//   * a K step is 64 deep and never straddles two examples, so the
+//     per-example scale is one scalar per step: the G chunks are multiplied
+//     by it in fp32 between the global load and the LDS store and rounded to
+//     bf16 once (v_cvt_pk_bf16_f32, round-to-nearest-even) -- the same single
+//     rounding of a scaled value that the reference applies when it stores a
+//     scaled bf16 per-example gradient.  The accumulators never leave the
+//     AGPRs.  Examples with scale 0 are skipped through the clip plan, so
+//     their data (including any NaN/Inf) is never read;
+//   * two LDS stages (128 KiB), one barrier per K step; the scale + store of
+//     step s + 1 is interleaved with the MFMAs of step s, after which the
+//     registers are refilled with step s + 2 (loads in flight for a step);
 //   * workgroup ids are remapped so that each of the 8 XCDs owns a compact
 //     block of output tiles and re-reads operand tiles from its own L2.
 #include "common.h"
@@ -28,20 +31,24 @@
 namespace {
 
 constexpr int kBM = 256, kBN = 256, kBK = 64, kThreads = 256;
+constexpr int kFastThreads = 512;  // 8 waves
 
-// LDS layout of one 256-row operand tile for a 64-deep K step.  A 16-byte
-// chunk holds 8 consecutive k of one row; chunk kb (0..7) of row r lives at
-//   (kb >> 1) * kSlice + (kb & 1) * kHalf + 16 * (r + (r >> 3)).
-// MFMA fragment reads (32 consecutive rows, one chunk) are then contiguous
-// 16-byte runs, and fragment (i, kk) sits at a constant offset from a
-// per-lane base; the transposed writes (rows 8 apart across lanes) land
-// 144 bytes apart, which spreads 8 lanes over all 32 banks.
-constexpr int kHalf = (kBM + kBM / 8) * 16;      // 4608 bytes
-constexpr int kSlice = 2 * kHalf;                // 16 k per slice
-constexpr int kOperandBytes = 4 * kSlice;        // 36 KiB
+// LDS layout of one operand tile for a 64-deep K step: 64 rows (k) of 256
+// bf16 (512 bytes), the row's eight 64-byte blocks permuted by XOR with
+// (k & 7).  A 16-lane group of a 16-byte store covers 4 consecutive blocks
+// of one row, and a 32-lane half of a transposing read covers one block in 4
+// consecutive rows: both land on 64 distinct banks.
+constexpr int kRowBytes = 512;
+constexpr int kOperandBytes = kBK * kRowBytes;   // 32 KiB
 constexpr int kStageBytes = 2 * kOperandBytes;   // G tile + A tile
+constexpr int kEpilogueBytes = 128 * (kBN + 4) * 4;
+constexpr int kLdsBytes = 2 * kStageBytes > kEpilogueBytes ? 2 * kStageBytes : kEpilogueBytes;
 
-__device__ __forceinline__ int row_off(int r) { return 16 * (r + (r >> 3)); }
+// Byte offset of bf16 element (k, col) (col < 256, byte offset within the
+// 64-byte block preserved).
+__device__ __forceinline__ int tile_off(int k, int col) {
+  return k * kRowBytes + ((((col >> 5) ^ (k & 7)) << 6) | ((col & 31) << 1));
+}
 
 struct Epilogue {
   int M, N;
@@ -99,81 +106,36 @@ __device__ __forceinline__ void emit_pair(const Epilogue& ep, int m, int n, floa
   if (m + 1 < ep.M) store_value(ep, (size_t)(m + 1) * ep.N + n, finish_value(v1, ep, z1));
 }
 
-// 8 rows (k) x 8 columns of bf16 at byte offset `off` -> regs[k]; the row
-// stride enters as a scalar offset.  A chunk outside the matrix columns is
-// given an offset past the buffer's range, which the hardware reads as zero.
+// A 16-byte chunk outside the matrix columns is given an offset past the
+// buffer's range, which the hardware reads as zero.
 constexpr int kOutOfRange = 0x7ff00000;
-
-__device__ __forceinline__ void load_block(__amdgpu_buffer_rsrc_t rsrc, int off, int row_bytes,
-                                           u32x4_t regs[8]) {
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    regs[r] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, r * row_bytes, 0);
-  }
-}
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 
-// The same transpose with every element multiplied by `s` in fp32 and
-// rounded to bf16 (RNE) on the way.
-__device__ __forceinline__ void store_block_t_scaled(uint8_t* tile, int mb, int kb,
-                                                     const u32x4_t in[8], float s) {
-  uint8_t* base = tile + (kb >> 1) * kSlice + (kb & 1) * kHalf + row_off(mb * 8);
+// 8 bf16 multiplied by `s` in fp32, rounded to bf16 (RNE) once.
+__device__ __forceinline__ u32x4_t scale_chunk(u32x4_t x, float s) {
+  u32x4_t o;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int c = j >> 1;
-    u32x4_t o;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      uint32_t x = in[2 * t][c], y = in[2 * t + 1][c];
-      uint32_t xb = (j & 1) ? (x & 0xffff0000u) : (x << 16);
-      uint32_t yb = (j & 1) ? (y & 0xffff0000u) : (y << 16);
-      f32x2_t v = {__builtin_bit_cast(float, xb) * s, __builtin_bit_cast(float, yb) * s};
-      o[t] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
-    }
-    *reinterpret_cast<u32x4_t*>(base + 16 * j) = o;
+  for (int t = 0; t < 4; ++t) {
+    f32x2_t v = {__builtin_bit_cast(float, x[t] << 16) * s,
+                 __builtin_bit_cast(float, x[t] & 0xffff0000u) * s};
+    o[t] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
   }
+  return o;
 }
 
-// Transpose the 8 x 8 bf16 block in registers and store row j (operand row
-// mb * 8 + j, k-chunk kb) of the LDS tile.
-__device__ __forceinline__ void store_block_t(uint8_t* tile, int mb, int kb, const u32x4_t in[8]) {
-  uint8_t* base = tile + (kb >> 1) * kSlice + (kb & 1) * kHalf + row_off(mb * 8);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int c = j >> 1;
-    u32x4_t o;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      uint32_t x = in[2 * t][c], y = in[2 * t + 1][c];
-      o[t] = (j & 1) ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
-    }
-    *reinterpret_cast<u32x4_t*>(base + 16 * j) = o;
-  }
+// Transposing read of 4 k-consecutive bf16 per lane (see the fragment
+// addressing in the kernel).
+__device__ __forceinline__ i16x4_t read_tr(const uint8_t* lds_base, int off) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4_t*)((__attribute__((address_space(3))) uint8_t*)lds_base + off));
 }
 
-// One 64-deep K step of MFMAs over the staged G and A tiles.
-__device__ __forceinline__ void mma_stage(const uint8_t* tg, const uint8_t* ta,
-                                          f32x16_t acc[4][4]) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int wm = w >> 1, wn = w & 1;
-  const uint8_t* ga = tg + (lane >> 5) * kHalf + row_off(wm * 128 + (lane & 31));
-  const uint8_t* aa = ta + (lane >> 5) * kHalf + row_off(wn * 128 + (lane & 31));
-#pragma unroll
-  for (int kk = 0; kk < kBK / 16; ++kk) {
-    bf16x8_t a[4], b[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      a[i] = *reinterpret_cast<const bf16x8_t*>(ga + kk * kSlice + i * row_off(32));
-      b[i] = *reinterpret_cast<const bf16x8_t*>(aa + kk * kSlice + i * row_off(32));
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-  }
+__device__ __forceinline__ bf16x8_t join_frag(i16x4_t lo, i16x4_t hi) {
+  return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 // blockIdx -> (tile_m, tile_n): contiguous id ranges per XCD (hardware
@@ -202,27 +164,37 @@ struct FastArgs {
   Epilogue ep;
 };
 
-__global__ void __launch_bounds__(kThreads, 1) clipped_sum_bf16_kernel(FastArgs args) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kStageBytes];
-  static_assert(128 * (kBN + 4) * 4 <= 2 * kStageBytes, "epilogue tile fits");
+// Per-lane LDS offsets of the transposing fragment reads.  For a 32 x 16
+// (rows x k) fragment at tile column c0 and K sub-step 0, half h (k 4h..4h+3
+// of the lane's 8): lane l of 16-lane group q = l / 16, L = l % 16 reads the 8
+// bytes at k = 8 (q >> 1) + 4 h + (L >> 2), col = c0 + 16 (q & 1) + 4 (L & 3);
+// after the transpose it holds k = 8 (l / 32) + 4 h + 0..3 of col c0 + l % 32,
+// which is the MFMA operand layout.  K sub-step kk adds kk * 16 rows.
+__device__ __forceinline__ int frag_off(int c0, int h, int lane) {
+  const int q = lane >> 4, L = lane & 15;
+  const int k = 8 * (q >> 1) + 4 * h + (L >> 2);
+  return tile_off(k, c0 + 16 * (q & 1) + 4 * (L & 3));
+}
+
+__global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastArgs args) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
   const int M = args.ep.M, N = args.ep.N, T = args.T;
   int tm, tn;
   tile_coords(ceil_div(M, kBM), ceil_div(N, kBN), &tm, &tn);
   const int m0 = tm * kBM, n0 = tn * kBN;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int mb = tid & 31, kb = tid >> 5;
-  const bool g_ok = m0 + mb * 8 < M, a_ok = n0 + mb * 8 < N;
+  const int wm = w >> 2, wn = w & 3;  // wave tile: rows wm * 128 of G^T, wn * 64 of A
 
   ClipPlanView plan = clip_plan_view(const_cast<void*>(args.plan), args.B);
   const int nactive = *plan.nactive;
   const int spe = T / kBK;
   const int nsteps = nactive * spe;
 
-  f32x16_t acc[4][4];
+  f32x16_t acc[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
 
   if (nsteps > 0) {
     const int total_rows = args.B * T;
@@ -230,50 +202,89 @@ __global__ void __launch_bounds__(kThreads, 1) clipped_sum_bf16_kernel(FastArgs 
         const_cast<uint16_t*>(args.G), (short)0, total_rows * M * 2, 0x00020000);
     __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(args.A), (short)0, total_rows * N * 2, 0x00020000);
-    const int g_col = (m0 + mb * 8) * 2, a_col = (n0 + mb * 8) * 2;
-    const int g_bad = g_ok ? 0 : kOutOfRange, a_bad = a_ok ? 0 : kOutOfRange;
-    u32x4_t rg[8], ra[8];
-    int slot = 0, kt = 0;
-    int ex = plan.active[0];
-    int row = ex * T + kb * 8;
-    load_block(g_rsrc, (row * M * 2 + g_col) | g_bad, M * 2, rg);
-    load_block(a_rsrc, (row * N * 2 + a_col) | a_bad, N * 2, ra);
-    store_block_t_scaled(lds, mb, kb, rg, args.scale[ex]);
-    store_block_t(lds + kOperandBytes, mb, kb, ra);
+    // Staging: chunk c = tid + 512 j (j < 4) of a tile is row c >> 5, columns
+    // (c & 31) * 8 .. +8.  Columns outside the matrix read as zero.
+    int g_voff[4], a_voff[4], g_bad[4], a_bad[4], st_off[4], row_of[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = tid + kFastThreads * j;
+      const int r = c >> 5, col = (c & 31) * 8;
+      row_of[j] = r;
+      st_off[j] = tile_off(r, col);
+      g_voff[j] = (m0 + col) * 2;
+      a_voff[j] = (n0 + col) * 2;
+      g_bad[j] = (m0 + col < M) ? 0 : kOutOfRange;
+      a_bad[j] = (n0 + col < N) ? 0 : kOutOfRange;
+    }
+    int goff[4][2], aoff[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) goff[i][h] = frag_off(wm * 128 + i * 32, h, lane);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) aoff[j][h] = frag_off(wn * 64 + j * 32, h, lane);
+    }
+
+    u32x4_t g[4], a[4];
+    float sc = 0.0f;
+    // Step t covers rows [active[t / spe] * T + (t % spe) * 64, +64).
+    auto load_step = [&](int t) {
+      const int ex = plan.active[t / spe];
+      sc = args.scale[ex];
+      const int row0 = ex * T + (t % spe) * kBK;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = row0 + row_of[j];
+        g[j] = __builtin_amdgcn_raw_buffer_load_b128(g_rsrc, (row * M * 2 + g_voff[j]) | g_bad[j],
+                                                     0, 0);
+        a[j] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (row * N * 2 + a_voff[j]) | a_bad[j],
+                                                     0, 0);
+      }
+    };
+    auto store_chunk = [&](uint8_t* stage, int j) {
+      *reinterpret_cast<u32x4_t*>(stage + st_off[j]) = scale_chunk(g[j], sc);
+      *reinterpret_cast<u32x4_t*>(stage + kOperandBytes + st_off[j]) = a[j];
+    };
+    auto mma_kk = [&](const uint8_t* stage, int kk) {
+      const int kofs = kk * 16 * kRowBytes;
+      bf16x8_t fa[4], fb[2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        fa[i] = join_frag(read_tr(stage, goff[i][0] + kofs), read_tr(stage, goff[i][1] + kofs));
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        fb[j] = join_frag(read_tr(stage + kOperandBytes, aoff[j][0] + kofs),
+                          read_tr(stage + kOperandBytes, aoff[j][1] + kofs));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    };
+
+    load_step(0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) store_chunk(lds, j);
+    if (nsteps > 1) load_step(1);
     __syncthreads();
     for (int s = 0; s < nsteps; ++s) {
-      uint8_t* cur = lds + (s & 1) * kStageBytes;
+      const uint8_t* cur = lds + (s & 1) * kStageBytes;
       uint8_t* nxt = lds + ((s + 1) & 1) * kStageBytes;
-      int nslot = slot, nkt = kt + 1;
-      if (nkt == spe) {
-        nkt = 0;
-        ++nslot;
-      }
       const bool more = s + 1 < nsteps;
-      float nscale = 0.0f;
-      if (more) {
-        const int nex = plan.active[nslot];
-        nscale = args.scale[nex];
-        const int nrow = nex * T + nkt * kBK + kb * 8;
-        load_block(g_rsrc, (nrow * M * 2 + g_col) | g_bad, M * 2, rg);
-        load_block(a_rsrc, (nrow * N * 2 + a_col) | a_bad, N * 2, ra);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        mma_kk(cur, kk);
+        if (more) store_chunk(nxt, kk);
       }
-      mma_stage(cur, cur + kOperandBytes, acc);
-      if (more) {
-        store_block_t_scaled(nxt, mb, kb, rg, nscale);
-        store_block_t(nxt + kOperandBytes, mb, kb, ra);
-      }
+      if (s + 2 < nsteps) load_step(s + 2);
       __syncthreads();
-      slot = nslot;
-      kt = nkt;
     }
   }
 
   // Epilogue: the 256 x 256 fp32 tile goes through LDS in two halves of 128
-  // rows (128 KiB + padding fits in the 160 KiB LDS), then each thread owns one
-  // column and walks its rows in even/odd pairs: coalesced stores, and one
-  // Philox block per pair in a rolled loop (no per-element code expansion).
-  const int wm = w >> 1, wn = w & 1;
+  // rows (128 KiB + padding fits in the 160 KiB LDS); each of the 512 threads
+  // owns one column and half of the half's rows, walked in even/odd pairs:
+  // coalesced stores, and one Philox block per pair in a rolled loop.
   float* tile = reinterpret_cast<float*>(lds);
   constexpr int kLd = kBN + 4;
   for (int half = 0; half < 2; ++half) {
@@ -281,19 +292,21 @@ __global__ void __launch_bounds__(kThreads, 1) clipped_sum_bf16_kernel(FastArgs 
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int ml = i * 32 + (r >> 2) * 8 + 4 * (lane >> 5) + (r & 3);
-            const int nl = wn * 128 + j * 32 + (lane & 31);
+            const int nl = wn * 64 + j * 32 + (lane & 31);
             tile[ml * kLd + nl] = acc[i][j][r];
           }
     }
     __syncthreads();
-    const int n = n0 + tid;
+    const int col = tid & (kBN - 1);
+    const int r0 = (tid >> 8) * 64;
+    const int n = n0 + col;
 #pragma unroll 2
-    for (int ml = 0; ml < 128; ml += 2) {
-      emit_pair(args.ep, m0 + half * 128 + ml, n, tile[ml * kLd + tid], tile[(ml + 1) * kLd + tid]);
+    for (int ml = r0; ml < r0 + 64; ml += 2) {
+      emit_pair(args.ep, m0 + half * 128 + ml, n, tile[ml * kLd + col], tile[(ml + 1) * kLd + col]);
     }
     __syncthreads();
   }
@@ -465,7 +478,7 @@ extern "C" int dpc_clipped_sum(const void* A, const void* G, const float* scale,
     args.scale = scale;
     args.ep = ep;
     const int ntiles = ceil_div(dout, kBM) * ceil_div(din, kBN);
-    hipLaunchKernelGGL(clipped_sum_bf16_kernel, dim3(ntiles), dim3(kThreads), 0, s, args);
+    hipLaunchKernelGGL(clipped_sum_bf16_kernel, dim3(ntiles), dim3(kFastThreads), 0, s, args);
   } else {
     dim3 grid(ceil_div(din, kGT), ceil_div(dout, kGT));
     if (dtype == DPC_BF16) {
