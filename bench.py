@@ -115,8 +115,9 @@ def cpu_model() -> str:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=200,
+                    help="untimed steps; ~0.15 s of work lets the GPU clocks settle")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=8, help="examples in the CPU sample")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",

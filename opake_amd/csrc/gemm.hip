@@ -21,8 +21,9 @@
 //     AGPRs.  Examples with scale 0 are skipped through the clip plan, so
 //     their data (including any NaN/Inf) is never read;
 //   * two LDS stages (128 KiB), one barrier per K step; the scale + store of
-//     step s + 1 is interleaved with the MFMAs of step s, after which the
-//     registers are refilled with step s + 2 (loads in flight for a step);
+//     step s + 1 is interleaved, chunk by chunk, with the MFMAs of step s, and
+//     each chunk's registers are refilled with step s + 2 right after its
+//     store, so every global load is in flight for a whole step;
 //   * workgroup ids are remapped so that each of the 8 XCDs owns a compact
 //     block of output tiles and re-reads operand tiles from its own L2.
 #include "common.h"
@@ -104,6 +105,42 @@ __device__ __forceinline__ void emit_pair(const Epilogue& ep, int m, int n, floa
   }
   store_value(ep, (size_t)m * ep.N + n, finish_value(v0, ep, z0));
   if (m + 1 < ep.M) store_value(ep, (size_t)(m + 1) * ep.N + n, finish_value(v1, ep, z1));
+}
+
+// Rows m, m + 1 (m even) of columns n, n + 1 (n even, N even): v[r][c].
+// Each row's two values go out in one 4-byte (bf16) or 8-byte (fp32) store.
+__device__ __forceinline__ void emit_quad(const Epilogue& ep, int m, int n, const float v[2][2]) {
+  if (n >= ep.N || m >= ep.M) return;
+  float z[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+  if (ep.sigma != 0.0f) {
+    if (ep.noise_mode == DPC_NOISE_PHILOX) {
+      const uint64_t blk = (uint64_t)(m >> 1) * (uint64_t)ep.N + (uint64_t)n;
+      philox_normal_pair(ep.seed, ep.leaf, blk, &z[0][0], &z[1][0]);
+      philox_normal_pair(ep.seed, ep.leaf, blk + 1, &z[0][1], &z[1][1]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        if (m + r < ep.M) {
+          const float2 zz = *reinterpret_cast<const float2*>(ep.noise + (size_t)(m + r) * ep.N + n);
+          z[r][0] = zz.x;
+          z[r][1] = zz.y;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    if (m + r >= ep.M) break;
+    const float a = finish_value(v[r][0], ep, z[r][0]);
+    const float b = finish_value(v[r][1], ep, z[r][1]);
+    const size_t idx = (size_t)(m + r) * ep.N + n;
+    if (ep.out_bf16) {
+      const uint32_t packed = (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+      *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(ep.out) + idx) = packed;
+    } else {
+      *reinterpret_cast<float2*>(reinterpret_cast<float*>(ep.out) + idx) = make_float2(a, b);
+    }
+  }
 }
 
 // A 16-byte chunk outside the matrix columns is given an offset past the
@@ -226,22 +263,20 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
     }
 
     u32x4_t g[4], a[4];
-    float sc = 0.0f;
     // Step t covers rows [active[t / spe] * T + (t % spe) * 64, +64).
-    auto load_step = [&](int t) {
+    auto step_row0 = [&](int t, float* sc) {
       const int ex = plan.active[t / spe];
-      sc = args.scale[ex];
-      const int row0 = ex * T + (t % spe) * kBK;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int row = row0 + row_of[j];
-        g[j] = __builtin_amdgcn_raw_buffer_load_b128(g_rsrc, (row * M * 2 + g_voff[j]) | g_bad[j],
-                                                     0, 0);
-        a[j] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (row * N * 2 + a_voff[j]) | a_bad[j],
-                                                     0, 0);
-      }
+      *sc = args.scale[ex];
+      return ex * T + (t % spe) * kBK;
     };
-    auto store_chunk = [&](uint8_t* stage, int j) {
+    auto load_chunk = [&](int row0, int j) {
+      const int row = row0 + row_of[j];
+      g[j] = __builtin_amdgcn_raw_buffer_load_b128(g_rsrc, (row * M * 2 + g_voff[j]) | g_bad[j], 0,
+                                                   0);
+      a[j] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (row * N * 2 + a_voff[j]) | a_bad[j], 0,
+                                                   0);
+    };
+    auto store_chunk = [&](uint8_t* stage, int j, float sc) {
       *reinterpret_cast<u32x4_t*>(stage + st_off[j]) = scale_chunk(g[j], sc);
       *reinterpret_cast<u32x4_t*>(stage + kOperandBytes + st_off[j]) = a[j];
     };
@@ -262,29 +297,47 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
     };
 
-    load_step(0);
+    // Prologue: step 0 into stage 0, step 1 into the registers.
+    float sc_next = 0.0f, sc_after = 0.0f;
+    int row0 = step_row0(0, &sc_next);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) store_chunk(lds, j);
-    if (nsteps > 1) load_step(1);
+    for (int j = 0; j < 4; ++j) load_chunk(row0, j);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) store_chunk(lds, j, sc_next);
+    row0 = step_row0(min(1, nsteps - 1), &sc_next);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) load_chunk(row0, j);
     __syncthreads();
+    // Step s: K sub-step kk's MFMAs, then chunk kk of step s + 1 goes from the
+    // registers (scaled) into the other stage and the same registers are
+    // refilled with chunk kk of step s + 2 -- each load is in flight for a
+    // whole step before its data is stored.  Past the last step the stores
+    // and loads repeat the last step's (in-range) rows into the unused stage:
+    // every path then issues the same loads, which keeps the compiler's
+    // memory-counter waits exact.
     for (int s = 0; s < nsteps; ++s) {
       const uint8_t* cur = lds + (s & 1) * kStageBytes;
       uint8_t* nxt = lds + ((s + 1) & 1) * kStageBytes;
-      const bool more = s + 1 < nsteps;
+      const int row2 = step_row0(min(s + 2, nsteps - 1), &sc_after);
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         mma_kk(cur, kk);
-        if (more) store_chunk(nxt, kk);
+        store_chunk(nxt, kk, sc_next);
+        load_chunk(row2, kk);
+        // Keep each chunk's store and reload inside its K sub-step: the
+        // scheduler would otherwise sink all loads to the end of the step.
+        __builtin_amdgcn_sched_barrier(0);
       }
-      if (s + 2 < nsteps) load_step(s + 2);
+      sc_next = sc_after;
       __syncthreads();
     }
   }
 
   // Epilogue: the 256 x 256 fp32 tile goes through LDS in two halves of 128
   // rows (128 KiB + padding fits in the 160 KiB LDS); each of the 512 threads
-  // owns one column and half of the half's rows, walked in even/odd pairs:
-  // coalesced stores, and one Philox block per pair in a rolled loop.
+  // owns a pair of adjacent columns and a quarter of the half's rows, walked
+  // in even/odd row pairs: coalesced 4- or 8-byte stores, and one Philox block
+  // per (row pair, column) in a rolled loop.
   float* tile = reinterpret_cast<float*>(lds);
   constexpr int kLd = kBN + 4;
   for (int half = 0; half < 2; ++half) {
@@ -301,12 +354,14 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
           }
     }
     __syncthreads();
-    const int col = tid & (kBN - 1);
-    const int r0 = (tid >> 8) * 64;
-    const int n = n0 + col;
+    const int cl = 2 * (tid & 127);
+    const int r0 = (tid >> 7) * 32;
 #pragma unroll 2
-    for (int ml = r0; ml < r0 + 64; ml += 2) {
-      emit_pair(args.ep, m0 + half * 128 + ml, n, tile[ml * kLd + col], tile[(ml + 1) * kLd + col]);
+    for (int ml = r0; ml < r0 + 32; ml += 2) {
+      const float2 t0 = *reinterpret_cast<const float2*>(tile + ml * kLd + cl);
+      const float2 t1 = *reinterpret_cast<const float2*>(tile + (ml + 1) * kLd + cl);
+      const float v[2][2] = {{t0.x, t0.y}, {t1.x, t1.y}};
+      emit_quad(args.ep, m0 + half * 128 + ml, n0 + cl, v);
     }
     __syncthreads();
   }

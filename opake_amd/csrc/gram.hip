@@ -1,38 +1,40 @@
 // Per-example squared gradient norms of linear layers via the Gram identity
 //   ||G_i^T A_i||_F^2 = <A_i A_i^T, G_i G_i^T>
 // (no per-example gradient is ever formed).  The T x T Gram matrices are
-// split into 128 x 128 tiles; a workgroup owns one (example, tile pair p <= q).
-// Its 8 waves form two groups of 4: group 0 computes the (p, q) tile of
-// A A^T while group 1 computes the same tile of G G^T, concurrently, with
-// bf16 MFMA and fp32 accumulators (each wave 64 x 64 of the tile).  Group 1
-// then hands its tile to group 0 through LDS for the element-wise inner
-// product in fp64.  Pairs with p < q count twice (both Gram matrices are
-// symmetric).  One fp64 partial per (example, pair) lands in the workspace;
-// dpc_row_sum_f64 folds them into sqnorm in a fixed order, so results are
-// deterministic.
+// split into 128 x 128 tiles; a workgroup of 4 waves owns one (example, tile
+// pair p <= q) and computes the (p, q) tile of both A A^T and G G^T with bf16
+// MFMA and fp32 accumulators.  Each wave holds the same 64 x 64 block of both
+// tiles, so the element-wise inner product (fp64) needs no data exchange.
+// Pairs with p < q count twice (both Gram matrices are symmetric).  One fp64
+// partial per (example, pair) lands in the workspace; dpc_row_sum_f64 folds
+// them into sqnorm in a fixed order, so results are deterministic.
 //
-// Workgroups are placed so that all pairs of one example run on one XCD
-// (hardware dispatch is round-robin over the 8 XCDs): the pairs re-read the
-// example's tiles from that XCD's L2 instead of from HBM.
+// Two workgroups fit on a CU (64 KiB of LDS, <= 256 registers per lane at 2
+// waves per SIMD), so the 10 pairs x B examples of a typical call are all
+// resident at once.  Workgroups are placed so that all pairs of one example
+// run on one XCD (hardware dispatch is round-robin over the 8 XCDs): the pairs
+// re-read the example's rows from that XCD's L2 instead of from HBM.
 #include "common.h"
 
 namespace {
 
 constexpr int kGramTile = 128;  // rows of a T-tile
-constexpr int kGramK = 64;      // reduction depth staged per LDS buffer
 constexpr int kGramThreads = 256;
-constexpr int kGramGroupThreads = 256;                   // one group = 4 waves
-constexpr int kGramMfmaThreads = 2 * kGramGroupThreads;  // A group + G group
-constexpr int kTileBytes = kGramTile * kGramK * 2;       // 16 KiB per staged tile
-constexpr int kStageBytes = 2 * kTileBytes;              // p tile + q tile
-constexpr int kGroupBytes = 2 * kStageBytes;             // two stages
+constexpr int kGramMfmaThreads = 256;
+constexpr int kGK = 32;                              // reduction depth per K step
+constexpr int kGTileBytes = kGramTile * kGK * 2;     // 8 KiB per staged tile
+constexpr int kGStageBytes = 4 * kGTileBytes;        // A_p, A_q, G_p, G_q
 constexpr int kXcds = 8;
+// A 16-byte chunk whose columns lie outside the row is given an offset past
+// the buffer's range, which the hardware reads as zero.
+constexpr int kGramOutOfRange = 0x7ff00000;
 
-// Byte offset of 16-byte chunk `c` of row `r` in a [rows][64] bf16 LDS tile.
-// The XOR swizzle spreads both the row-chunk writes and the MFMA fragment
-// reads (32 consecutive rows, one chunk) over all 32 banks.
-__device__ __forceinline__ int lds_off(int r, int c) {
-  return r * 128 + ((c ^ ((r ^ (r >> 3)) & 7)) << 4);
+// Byte offset of 16-byte chunk c (4 per 64-byte row) of row r in a staged
+// tile.  A fragment read (16 lanes = 16 consecutive rows, one chunk) and a
+// staging write (16 lanes = 4 rows x 4 chunks) both touch 16 distinct 16-byte
+// bank groups of the 64 four-byte banks.
+__device__ __forceinline__ int gtile_off(int r, int c) {
+  return r * 64 + ((c ^ ((r >> 2) & 3)) << 4);
 }
 
 __device__ __forceinline__ void pair_from_index(int pair, int* p, int* q) {
@@ -40,54 +42,6 @@ __device__ __forceinline__ void pair_from_index(int pair, int* p, int* q) {
   while ((qq + 1) * (qq + 2) / 2 <= pair) ++qq;
   *q = qq;
   *p = pair - qq * (qq + 1) / 2;
-}
-
-// Load 128 rows x 64 columns (bf16) starting at (row0, k0) of X [T, d]:
-// four 16-byte chunks per group thread, zero outside [T) x [d).
-__device__ __forceinline__ void gram_load(const uint16_t* __restrict__ X, int T, int d, int row0,
-                                          int k0, int gt, u32x4_t regs[4]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    int q = gt + kGramGroupThreads * j;
-    int r = q >> 3, c = q & 7;
-    int row = row0 + r, col = k0 + c * 8;
-    if (row < T && col < d) {
-      regs[j] = *reinterpret_cast<const u32x4_t*>(X + (size_t)row * d + col);
-    } else {
-      regs[j] = u32x4_t{0u, 0u, 0u, 0u};
-    }
-  }
-}
-
-__device__ __forceinline__ void gram_store(uint8_t* tile, int gt, const u32x4_t regs[4]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    int q = gt + kGramGroupThreads * j;
-    *reinterpret_cast<u32x4_t*>(tile + lds_off(q >> 3, q & 7)) = regs[j];
-  }
-}
-
-// acc[bi][bj] += X[p rows] X[q rows]^T over one staged 64-deep slab; wave wg
-// of the group owns rows wr * 64.. of p and wr * 64.. of q.
-__device__ __forceinline__ void gram_mma(const uint8_t* lp, const uint8_t* lq, int wg,
-                                         f32x16_t acc[2][2]) {
-  const int lane = threadIdx.x & 63;
-  const int wr = wg >> 1, wc = wg & 1;
-#pragma unroll
-  for (int kk = 0; kk < kGramK / 16; ++kk) {
-    const int c = kk * 2 + (lane >> 5);
-    bf16x8_t a[2], b[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      a[i] = *reinterpret_cast<const bf16x8_t*>(lp + lds_off(wr * 64 + i * 32 + (lane & 31), c));
-      b[i] = *reinterpret_cast<const bf16x8_t*>(lq + lds_off(wc * 64 + i * 32 + (lane & 31), c));
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-  }
 }
 
 __device__ __forceinline__ double block_sum_f64(double v, double* red) {
@@ -113,10 +67,72 @@ __device__ __forceinline__ int xcd_logical_block(int padded, int nblocks) {
   return l < nblocks ? l : -1;
 }
 
-__global__ void __launch_bounds__(kGramMfmaThreads, 1)
+// One staged operand (rows row0.. of X [T, d], a 32-deep K step): per thread
+// two 16-byte chunks, chunk id q = tid + 256 j -> row q >> 2, chunk q & 3.
+struct GramOperand {
+  __amdgpu_buffer_rsrc_t rsrc;
+  int row_bytes;   // d * 2
+  int voff[2];     // byte offset of the thread's chunks at K step 0
+  int col[2];      // first column of the chunks
+  int d;
+};
+
+__device__ __forceinline__ GramOperand make_operand(const uint16_t* X, int T, int d, int row0) {
+  GramOperand o;
+  o.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(X), (short)0, T * d * 2,
+                                             0x00020000);
+  o.row_bytes = d * 2;
+  o.d = d;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int q = threadIdx.x + kGramMfmaThreads * j;
+    o.col[j] = (q & 3) * 8;
+    o.voff[j] = (row0 + (q >> 2)) * o.row_bytes + o.col[j] * 2;
+  }
+  return o;
+}
+
+__device__ __forceinline__ void load_operand(const GramOperand& o, int step, u32x4_t r[2]) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int k = step * kGK + o.col[j];
+    const int bad = k < o.d ? 0 : kGramOutOfRange;
+    r[j] = __builtin_amdgcn_raw_buffer_load_b128(o.rsrc, (o.voff[j] + step * kGK * 2) | bad, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void store_operand(uint8_t* tile, const u32x4_t r[2]) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int q = threadIdx.x + kGramMfmaThreads * j;
+    *reinterpret_cast<u32x4_t*>(tile + gtile_off(q >> 2, q & 3)) = r[j];
+  }
+}
+
+// acc[i][j] += X_p[rows wr*64 + i*32 ..] . X_q[rows wc*64 + j*32 ..] over the
+// 16-deep sub-step kk of a staged K step.
+__device__ __forceinline__ void gram_mma(const uint8_t* tp, const uint8_t* tq, int kk,
+                                         f32x16_t acc[2][2]) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wr = w >> 1, wc = w & 1;
+  const int c = kk * 2 + (lane >> 5);
+  bf16x8_t a[2], b[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    a[i] = *reinterpret_cast<const bf16x8_t*>(tp + gtile_off(wr * 64 + i * 32 + (lane & 31), c));
+    b[i] = *reinterpret_cast<const bf16x8_t*>(tq + gtile_off(wc * 64 + i * 32 + (lane & 31), c));
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+}
+
+__global__ void __launch_bounds__(kGramMfmaThreads, 2)
 gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ G, int T,
                       int din, int dout, int npairs, int nblocks, double* __restrict__ partial) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kGroupBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kGStageBytes];
   __shared__ double red[kGramMfmaThreads / 64];
   const int l = xcd_logical_block(gridDim.x, nblocks);
   if (l < 0) return;  // padding workgroup: exits before any barrier
@@ -125,79 +141,87 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
   pair_from_index(pair, &p, &q);
   const bool diag = (p == q);
 
-  const int group = threadIdx.x / kGramGroupThreads;
-  const int gt = threadIdx.x % kGramGroupThreads;
-  const int wg = gt >> 6;
-  const int d = group ? dout : din;
-  const uint16_t* X = group ? G + (size_t)ex * T * dout : A + (size_t)ex * T * din;
-  uint8_t* mine = lds + group * kGroupBytes;
-  const int nk_mine = ceil_div(d, kGramK);
-  const int nk = max(ceil_div(din, kGramK), ceil_div(dout, kGramK));
+  const uint16_t* Xa = A + (size_t)ex * T * din;
+  const uint16_t* Xg = G + (size_t)ex * T * dout;
+  const GramOperand ap = make_operand(Xa, T, din, p * kGramTile);
+  const GramOperand aq = make_operand(Xa, T, din, q * kGramTile);
+  const GramOperand gp = make_operand(Xg, T, dout, p * kGramTile);
+  const GramOperand gq = make_operand(Xg, T, dout, q * kGramTile);
+  const int nka = ceil_div(din, kGK), nkg = ceil_div(dout, kGK);
+  const int nk = max(nka, nkg);
 
-  f32x16_t acc[2][2];
+  f32x16_t pa[2][2], pg[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
+    for (int j = 0; j < 2; ++j) pa[i][j] = pg[i][j] = f32x16_t{};
 
-  // Register double buffer: step s + 1 is in flight while step s is multiplied
-  // and step s + 2 is requested.
-  u32x4_t rp0[4], rq0[4], rp1[4], rq1[4];
-  auto load = [&](int step, u32x4_t* rp, u32x4_t* rq) {
-    gram_load(X, T, d, p * kGramTile, step * kGramK, gt, rp);
-    if (!diag) gram_load(X, T, d, q * kGramTile, step * kGramK, gt, rq);
+  // Registers hold the next K step of the four operands (the q operands are
+  // not loaded on diagonal pairs).  Past an operand's last step the loads
+  // repeat its last step, so every path issues the same loads.
+  u32x4_t rap[2], raq[2], rgp[2], rgq[2];
+  auto load_a = [&](int step) {
+    const int t = min(step, nka - 1);
+    load_operand(ap, t, rap);
+    if (!diag) load_operand(aq, t, raq);
   };
-  auto store = [&](int stage, const u32x4_t* rp, const u32x4_t* rq) {
-    uint8_t* st = mine + stage * kStageBytes;
-    gram_store(st, gt, rp);
-    if (!diag) gram_store(st + kTileBytes, gt, rq);
+  auto load_g = [&](int step) {
+    const int t = min(step, nkg - 1);
+    load_operand(gp, t, rgp);
+    if (!diag) load_operand(gq, t, rgq);
   };
-  auto body = [&](int s, u32x4_t* rp_next, u32x4_t* rq_next, u32x4_t* rp_free,
-                  u32x4_t* rq_free) {
-    // rp_next/rq_next hold step s + 1; rp_free/rq_free receive step s + 2.
-    if (s + 2 < nk_mine) load(s + 2, rp_free, rq_free);
-    if (s < nk_mine) {
-      const uint8_t* st = mine + (s & 1) * kStageBytes;
-      gram_mma(st, diag ? st : st + kTileBytes, wg, acc);
+  auto store_a = [&](uint8_t* stage) {
+    store_operand(stage, rap);
+    if (!diag) store_operand(stage + kGTileBytes, raq);
+  };
+  auto store_g = [&](uint8_t* stage) {
+    store_operand(stage + 2 * kGTileBytes, rgp);
+    if (!diag) store_operand(stage + 3 * kGTileBytes, rgq);
+  };
+
+  load_a(0);
+  load_g(0);
+  store_a(lds);
+  store_g(lds);
+  load_a(1);
+  load_g(1);
+  __syncthreads();
+  // Step s: sub-step 0 multiplies A (and then stores A's step s + 1 and
+  // reloads A's step s + 2), sub-step 1 multiplies G likewise, both on the
+  // current stage; each load is in flight for a whole step.
+  for (int s = 0; s < nk; ++s) {
+    const uint8_t* cur = lds + (s & 1) * kGStageBytes;
+    uint8_t* nxt = lds + ((s + 1) & 1) * kGStageBytes;
+    const uint8_t* cap = cur;
+    const uint8_t* caq = diag ? cur : cur + kGTileBytes;
+    const uint8_t* cgp = cur + 2 * kGTileBytes;
+    const uint8_t* cgq = diag ? cgp : cur + 3 * kGTileBytes;
+    if (s < nka) {
+      gram_mma(cap, caq, 0, pa);
+      gram_mma(cap, caq, 1, pa);
     }
-    if (s + 1 < nk_mine) store((s + 1) & 1, rp_next, rq_next);
+    store_a(nxt);
+    load_a(s + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    if (s < nkg) {
+      gram_mma(cgp, cgq, 0, pg);
+      gram_mma(cgp, cgq, 1, pg);
+    }
+    store_g(nxt);
+    load_g(s + 2);
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
-  };
-
-  if (nk_mine > 0) load(0, rp0, rq0);
-  if (nk_mine > 1) load(1, rp1, rq1);
-  if (nk_mine > 0) store(0, rp0, rq0);
-  __syncthreads();
-  int s = 0;
-  for (; s + 1 < nk; s += 2) {
-    body(s, rp1, rq1, rp0, rq0);
-    body(s + 1, rp0, rq0, rp1, rq1);
   }
-  if (s < nk) body(s, rp1, rq1, rp0, rq0);
 
-  // Group 1 hands its G G^T tile to group 0 through LDS (same fragment order,
-  // element e of thread gt at float index e * 256 + gt).
-  float* xfer = reinterpret_cast<float*>(lds);
-  if (group == 1) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) xfer[((i * 2 + j) * 16 + r) * kGramGroupThreads + gt] = acc[i][j][r];
-  }
-  __syncthreads();
+  // Both tiles share the MFMA output layout, so the element-wise product
+  // needs no knowledge of which (s, t) a register holds.
   double sum = 0.0;
-  if (group == 0) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          sum += (double)acc[i][j][r] *
-                 (double)xfer[((i * 2 + j) * 16 + r) * kGramGroupThreads + gt];
-  }
+      for (int r = 0; r < 16; ++r) sum += (double)pa[i][j][r] * (double)pg[i][j][r];
   double total = block_sum_f64(sum, red);
   if (threadIdx.x == 0) {
     partial[(size_t)ex * npairs + pair] = diag ? total : 2.0 * total;
@@ -348,7 +372,11 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
   hipStream_t s = (hipStream_t)stream;
   double* partial = (double*)ws;
   int npairs;
-  const bool mfma = dtype == DPC_BF16 && din % 8 == 0 && dout % 8 == 0;
+  // Buffer offsets are 32-bit: one example's rows (plus a tile of padding)
+  // must stay below 2 GiB for the MFMA path.
+  const size_t dmax = (size_t)(din > dout ? din : dout);
+  const bool fits = ((size_t)T + kGramTile) * dmax * 2 < ((size_t)1 << 31);
+  const bool mfma = dtype == DPC_BF16 && din % 8 == 0 && dout % 8 == 0 && fits;
   if (mfma) {
     int nt = ceil_div(T, kGramTile);
     npairs = nt * (nt + 1) / 2;
