@@ -7,11 +7,12 @@
 //   * 256 x 256 output tile per workgroup, 8 waves (2 per SIMD) of 128 x 64,
 //     bf16 MFMA 32x32x16 with fp32 accumulators (8 blocks per wave);
 //   * both operands are m- (n-) contiguous in HBM and are staged into LDS in
-//     that natural [k][m] layout (16-byte loads, 16-byte LDS stores, 64-byte
-//     blocks XOR-swizzled by the k row).  The MFMA fragments, which need 8
-//     consecutive k per lane, come out of LDS through the gfx950 transposing
-//     read ds_read_b64_tr_b16 (two per fragment), so no data is transposed
-//     in registers; all LDS accesses are free of bank conflicts;
+//     that natural [k][m] layout (64-byte blocks XOR-swizzled by the k row):
+//     A straight from HBM (buffer_load ... lds), G through registers, where
+//     it is scaled.  The MFMA fragments, which need 8 consecutive k per lane,
+//     come out of LDS through the gfx950 transposing read ds_read_b64_tr_b16
+//     (two per fragment), so no data is transposed in registers; all LDS
+//     accesses are free of bank conflicts;
 //   * a K step is 64 deep and never straddles two examples, so the
 //     per-example scale is one scalar per step: the G chunks are multiplied
 //     by it in fp32 between the global load and the LDS store and rounded to
@@ -42,14 +43,13 @@ constexpr int kFastThreads = 512;  // 8 waves
 constexpr int kRowBytes = 512;
 constexpr int kOperandBytes = kBK * kRowBytes;   // 32 KiB
 constexpr int kStageBytes = 2 * kOperandBytes;   // G tile + A tile
-constexpr int kEpilogueBytes = 128 * (kBN + 4) * 4;
-constexpr int kLdsBytes = 2 * kStageBytes > kEpilogueBytes ? 2 * kStageBytes : kEpilogueBytes;
 
 // Byte offset of bf16 element (k, col) (col < 256, byte offset within the
 // 64-byte block preserved).
 __device__ __forceinline__ int tile_off(int k, int col) {
   return k * kRowBytes + ((((col >> 5) ^ (k & 7)) << 6) | ((col & 31) << 1));
 }
+
 
 struct Epilogue {
   int M, N;
@@ -213,8 +213,27 @@ __device__ __forceinline__ int frag_off(int c0, int h, int lane) {
   return tile_off(k, c0 + 16 * (q & 1) + 4 * (L & 3));
 }
 
+// LDS of the fast kernel: the G tiles of both stages (and, after the K loop,
+// a quarter of the output tile) in one array, each stage's A tile in an array
+// of its own.  A is filled by DMA (buffer_load ... lds); keeping its stages in
+// distinct objects lets the compiler see that a DMA into one stage does not
+// alias the reads of the other, so it inserts no memory-counter wait before
+// them.
+constexpr int kQuarterRows = 64;
+constexpr int kEpiLd = kBN + 4;
+constexpr int kGLdsBytes = (2 * kOperandBytes > kQuarterRows * kEpiLd * 4)
+                               ? 2 * kOperandBytes
+                               : kQuarterRows * kEpiLd * 4;
+
+// vmcnt(N) with the other counters left alone (gfx9 s_waitcnt encoding).
+#define DPC_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
+
 __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastArgs args) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_g[kGLdsBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_a0[kOperandBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_a1[kOperandBytes];
   const int M = args.ep.M, N = args.ep.N, T = args.T;
   int tm, tn;
   tile_coords(ceil_div(M, kBM), ceil_div(N, kBN), &tm, &tn);
@@ -239,20 +258,71 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
         const_cast<uint16_t*>(args.G), (short)0, total_rows * M * 2, 0x00020000);
     __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(args.A), (short)0, total_rows * N * 2, 0x00020000);
-    // Staging: chunk c = tid + 512 j (j < 4) of a tile is row c >> 5, columns
-    // (c & 31) * 8 .. +8.  Columns outside the matrix read as zero.
-    int g_voff[4], a_voff[4], g_bad[4], a_bad[4], st_off[4], row_of[4];
+
+    // The clip plan, 64 entries at a time in registers: lane l holds slot
+    // base + l (example index and scale).  A step reads its slot with
+    // v_readlane, so the K loop issues no memory operations besides the
+    // operand loads.
+    int plan_base = -64, plan_ex = 0;
+    float plan_sc = 0.0f;
+    auto refill_plan = [&](int slot) __attribute__((always_inline)) {
+      plan_base = slot & ~63;
+      const int sl = plan_base + lane;
+      plan_ex = sl < nactive ? plan.active[sl] : 0;
+      plan_sc = sl < nactive ? args.scale[plan_ex] : 0.0f;
+    };
+    // Step t covers rows [active[t / spe] * T + (t % spe) * 64, +64).
+    auto step_row0 = [&](int t, float* sc) __attribute__((always_inline)) {
+      const int slot = t / spe;
+      if (slot - plan_base >= 64) {
+        refill_plan(slot);
+        DPC_WAIT_VMCNT(0);  // keep the loop's memory-counter accounting exact
+      }
+      const int ex = __builtin_amdgcn_readlane(plan_ex, slot - plan_base);
+      *sc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                          __builtin_bit_cast(int, plan_sc), slot - plan_base));
+      return ex * T + (t % spe) * kBK;
+    };
+
+    // G staging: chunk j (< 4) of this thread is tile row r0 + 16 j, columns
+    // col .. col + 8; columns outside the matrix read as zero.  Row r0 + 16 j
+    // has the same swizzle as row r0, so chunk j is st_off + j * 16 rows.
+    const int r0 = tid >> 5, col = (tid & 31) * 8;
+    const int st_off = tile_off(r0, col);
+    const int g_voff = (m0 + col) * 2;
+    const int g_bad = (m0 + col < M) ? 0 : kOutOfRange;
+    u32x4_t g[4];
+    auto load_chunk = [&](int row0, int j) __attribute__((always_inline)) {
+      const int row = row0 + r0;
+      g[j] = __builtin_amdgcn_raw_buffer_load_b128(g_rsrc, (row * M * 2 + g_voff) | g_bad,
+                                                   j * 16 * M * 2, 0);
+    };
+    auto store_chunk = [&](uint8_t* gstage, int j, float sc) __attribute__((always_inline)) {
+      *reinterpret_cast<u32x4_t*>(gstage + st_off + j * 16 * kRowBytes) = scale_chunk(g[j], sc);
+    };
+    // A goes straight from memory into LDS (buffer_load ... lds): wave w's
+    // instruction j fills the 1 KiB at (w * 4 + j) * 1024 of the A tile, lane
+    // i the 16 bytes at i * 16 -- row (w * 4 + j) * 2 + i / 32, physical
+    // 16-byte slot i % 32, which holds logical columns
+    // (((i % 32) / 4) ^ (row & 7)) * 32 + (i % 4) * 8.
+    int dma_voff[4], dma_bad[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int c = tid + kFastThreads * j;
-      const int r = c >> 5, col = (c & 31) * 8;
-      row_of[j] = r;
-      st_off[j] = tile_off(r, col);
-      g_voff[j] = (m0 + col) * 2;
-      a_voff[j] = (n0 + col) * 2;
-      g_bad[j] = (m0 + col < M) ? 0 : kOutOfRange;
-      a_bad[j] = (n0 + col < N) ? 0 : kOutOfRange;
+      const int row = (w * 4 + j) * 2 + (lane >> 5);
+      const int slot = lane & 31;
+      const int acol = (((slot >> 2) ^ (row & 7)) << 5) + (slot & 3) * 8;
+      dma_voff[j] = row * N * 2 + (n0 + acol) * 2;
+      dma_bad[j] = (n0 + acol < N) ? 0 : kOutOfRange;
     }
+    auto dma_a = [&](uint8_t* astage, int row0) __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            a_rsrc, (__attribute__((address_space(3))) void*)((lds_u8_t*)astage + (w * 4 + j) * 1024),
+            16, (row0 * N * 2 + dma_voff[j]) | dma_bad[j], 0, 0, 0);
+      }
+    };
+
     int goff[4][2], aoff[2][2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -261,111 +331,135 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
 #pragma unroll
       for (int j = 0; j < 2; ++j) aoff[j][h] = frag_off(wn * 64 + j * 32, h, lane);
     }
-
-    u32x4_t g[4], a[4];
-    // Step t covers rows [active[t / spe] * T + (t % spe) * 64, +64).
-    auto step_row0 = [&](int t, float* sc) {
-      const int ex = plan.active[t / spe];
-      *sc = args.scale[ex];
-      return ex * T + (t % spe) * kBK;
+    // Fragments of K sub-step kk: 4 of G^T (rows) and 2 of A (columns).
+    struct Frags {
+      bf16x8_t a[4], b[2];
     };
-    auto load_chunk = [&](int row0, int j) {
-      const int row = row0 + row_of[j];
-      g[j] = __builtin_amdgcn_raw_buffer_load_b128(g_rsrc, (row * M * 2 + g_voff[j]) | g_bad[j], 0,
-                                                   0);
-      a[j] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, (row * N * 2 + a_voff[j]) | a_bad[j], 0,
-                                                   0);
-    };
-    auto store_chunk = [&](uint8_t* stage, int j, float sc) {
-      *reinterpret_cast<u32x4_t*>(stage + st_off[j]) = scale_chunk(g[j], sc);
-      *reinterpret_cast<u32x4_t*>(stage + kOperandBytes + st_off[j]) = a[j];
-    };
-    auto mma_kk = [&](const uint8_t* stage, int kk) {
+    auto read_frags = [&](const uint8_t* gstage, const uint8_t* astage, int kk, Frags& f) __attribute__((always_inline)) {
       const int kofs = kk * 16 * kRowBytes;
-      bf16x8_t fa[4], fb[2];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        fa[i] = join_frag(read_tr(stage, goff[i][0] + kofs), read_tr(stage, goff[i][1] + kofs));
+        f.a[i] = join_frag(read_tr(gstage, goff[i][0] + kofs), read_tr(gstage, goff[i][1] + kofs));
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-        fb[j] = join_frag(read_tr(stage + kOperandBytes, aoff[j][0] + kofs),
-                          read_tr(stage + kOperandBytes, aoff[j][1] + kofs));
+        f.b[j] = join_frag(read_tr(astage, aoff[j][0] + kofs), read_tr(astage, aoff[j][1] + kofs));
+    };
+    auto mma = [&](const Frags& f) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
     };
 
-    // Prologue: step 0 into stage 0, step 1 into the registers.
-    float sc_next = 0.0f, sc_after = 0.0f;
-    int row0 = step_row0(0, &sc_next);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) load_chunk(row0, j);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) store_chunk(lds, j, sc_next);
-    row0 = step_row0(min(1, nsteps - 1), &sc_next);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) load_chunk(row0, j);
-    __syncthreads();
-    // Step s: K sub-step kk's MFMAs, then chunk kk of step s + 1 goes from the
-    // registers (scaled) into the other stage and the same registers are
-    // refilled with chunk kk of step s + 2 -- each load is in flight for a
-    // whole step before its data is stored.  Past the last step the stores
-    // and loads repeat the last step's (in-range) rows into the unused stage:
-    // every path then issues the same loads, which keeps the compiler's
-    // memory-counter waits exact.
-    for (int s = 0; s < nsteps; ++s) {
-      const uint8_t* cur = lds + (s & 1) * kStageBytes;
-      uint8_t* nxt = lds + ((s + 1) & 1) * kStageBytes;
+    // One K step on stage (gcur, acur), staging step s + 1 into (gnxt, anxt):
+    // the DMA of A's step s + 1 is issued first; then K sub-step kk's MFMAs,
+    // after which chunk kk of G's step s + 1 goes from the registers (scaled)
+    // into the other stage and the same registers are refilled with chunk kk
+    // of step s + 2 -- each load is in flight for a whole step.  Fragments are
+    // double-buffered (sub-step kk + 1's reads are issued before sub-step kk's
+    // MFMAs), and the sched_barriers keep each chunk's store and reload inside
+    // its sub-step (the scheduler would otherwise sink all loads to the end of
+    // the step).  Before the barrier only the 4 G loads may still be
+    // outstanding.  Past the last step the stores and loads repeat the last
+    // step's (in-range) rows into the unused stage: every path issues the same
+    // memory operations, which keeps the counter waits exact.
+    float sc_next = 0.0f;
+    int row_next = 0;
+    auto k_step = [&](int s, const uint8_t* gcur, const uint8_t* acur, uint8_t* gnxt,
+                      uint8_t* anxt) __attribute__((always_inline)) {
+      dma_a(anxt, row_next);
+      float sc_after;
       const int row2 = step_row0(min(s + 2, nsteps - 1), &sc_after);
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        mma_kk(cur, kk);
-        store_chunk(nxt, kk, sc_next);
-        load_chunk(row2, kk);
-        // Keep each chunk's store and reload inside its K sub-step: the
-        // scheduler would otherwise sink all loads to the end of the step.
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      Frags f0, f1;
+      read_frags(gcur, acur, 0, f0);
+      read_frags(gcur, acur, 1, f1);
+      mma(f0);
+      store_chunk(gnxt, 0, sc_next);
+      load_chunk(row2, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(gcur, acur, 2, f0);
+      mma(f1);
+      store_chunk(gnxt, 1, sc_next);
+      load_chunk(row2, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(gcur, acur, 3, f1);
+      mma(f0);
+      store_chunk(gnxt, 2, sc_next);
+      load_chunk(row2, 2);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(f1);
+      store_chunk(gnxt, 3, sc_next);
+      load_chunk(row2, 3);
+      __builtin_amdgcn_sched_barrier(0);
       sc_next = sc_after;
+      row_next = row2;
+      DPC_WAIT_VMCNT(4);
       __syncthreads();
+    };
+
+    uint8_t* g0 = lds_g;
+    uint8_t* g1 = lds_g + kOperandBytes;
+    // Prologue: step 0 into stage 0 (A by DMA, G through registers), step 1
+    // of G into the registers.
+    int row0 = step_row0(0, &sc_next);
+    dma_a(lds_a0, row0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) load_chunk(row0, j);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) store_chunk(g0, j, sc_next);
+    row_next = step_row0(min(1, nsteps - 1), &sc_next);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) load_chunk(row_next, j);
+    DPC_WAIT_VMCNT(4);  // the A DMA of step 0 has landed (4 G loads may be in flight)
+    __syncthreads();
+    int s = 0;
+    for (; s + 1 < nsteps; s += 2) {
+      k_step(s, g0, lds_a0, g1, lds_a1);
+      k_step(s + 1, g1, lds_a1, g0, lds_a0);
     }
+    if (s < nsteps) k_step(s, g0, lds_a0, g1, lds_a1);
+    DPC_WAIT_VMCNT(0);
   }
 
-  // Epilogue: the 256 x 256 fp32 tile goes through LDS in two halves of 128
-  // rows (128 KiB + padding fits in the 160 KiB LDS); each of the 512 threads
-  // owns a pair of adjacent columns and a quarter of the half's rows, walked
-  // in even/odd row pairs: coalesced 4- or 8-byte stores, and one Philox block
-  // per (row pair, column) in a rolled loop.
-  float* tile = reinterpret_cast<float*>(lds);
-  constexpr int kLd = kBN + 4;
-  for (int half = 0; half < 2; ++half) {
-    if (wm == half) {
+  // Epilogue: the 256 x 256 fp32 tile goes through LDS in four quarters of 64
+  // rows; each of the 512 threads owns a pair of adjacent columns and 16 of
+  // the quarter's rows, walked in even/odd row pairs: coalesced 4- or 8-byte
+  // stores, and one Philox block per (row pair, column) in a rolled loop.
+  float* tile = reinterpret_cast<float*>(lds_g);
+  // Unrolled: the accumulator blocks are selected by compile-time indices
+  // (a runtime index would move them to scratch memory).
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+  for (int quarter = 0; quarter < 4; ++quarter) {
+    if (wm == (quarter >> 1)) {
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii) {
+        const int i = 2 * (quarter & 1) + ii;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int ml = i * 32 + (r >> 2) * 8 + 4 * (lane >> 5) + (r & 3);
+            const int ml = ii * 32 + (r >> 2) * 8 + 4 * (lane >> 5) + (r & 3);
             const int nl = wn * 64 + j * 32 + (lane & 31);
-            tile[ml * kLd + nl] = acc[i][j][r];
+            tile[ml * kEpiLd + nl] = acc[i][j][r];
           }
+      }
     }
     __syncthreads();
     const int cl = 2 * (tid & 127);
-    const int r0 = (tid >> 7) * 32;
+    const int rr = (tid >> 7) * 16;
 #pragma unroll 2
-    for (int ml = r0; ml < r0 + 32; ml += 2) {
-      const float2 t0 = *reinterpret_cast<const float2*>(tile + ml * kLd + cl);
-      const float2 t1 = *reinterpret_cast<const float2*>(tile + (ml + 1) * kLd + cl);
+    for (int ml = rr; ml < rr + 16; ml += 2) {
+      const float2 t0 = *reinterpret_cast<const float2*>(tile + ml * kEpiLd + cl);
+      const float2 t1 = *reinterpret_cast<const float2*>(tile + (ml + 1) * kEpiLd + cl);
       const float v[2][2] = {{t0.x, t0.y}, {t1.x, t1.y}};
-      emit_quad(args.ep, m0 + half * 128 + ml, n0 + cl, v);
+      emit_quad(args.ep, m0 + quarter * kQuarterRows + ml, n0 + cl, v);
     }
     __syncthreads();
   }
 }
+
+#undef DPC_WAIT_VMCNT
 
 // Generic path: any T, float32 or bf16 operands, scale applied to the G
 // operand in fp32; 64 x 64 tiles with a 4 x 4 FMA block per thread.
