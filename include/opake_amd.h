@@ -158,10 +158,12 @@ int dpc_philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32
  *   (float)sanitise(x)^2 (fp32 square, fp64 sum), then
  *   leaf_sq[b, leaf_col[l]] = sum of leaf l's tiles (tile_start [L + 1]).
  * dpc_leaves_apply: out[off_l + j] = sum_b stored(b, l, j) in fp32, where
- *   stored = to_dtype(float(sanitise(x)) * scale[b]) with bf16 subnormals
- *   that rounded up zeroed (_pytree.py:160-204); post_sq[b, t] (nullable) =
- *   sum over the tile of stored^2 (fp32).  out_dtype is the storage dtype or
- *   float32.
+ *   stored = to_dtype(float(sanitise(x)) * scale[row_l * B + b]) with bf16
+ *   subnormals that rounded up zeroed (_pytree.py:160-204); row_l =
+ *   leaf_scale_row[l] (device int32 [L]; NULL: every leaf uses row 0 -- the
+ *   per-group clipping of _streaming.py:63-104 gives each group its row);
+ *   post_sq[b, t] (nullable) = sum over the tile of stored^2 (fp32).
+ *   out_dtype is the storage dtype or float32.
  * -------------------------------------------------------------------------*/
 int dpc_leaves_sqnorm(const int64_t* ptrs, const int64_t* sizes, const int32_t* tile_leaf,
                       const int32_t* tile_local, const int64_t* tile_start,
@@ -169,8 +171,16 @@ int dpc_leaves_sqnorm(const int64_t* ptrs, const int64_t* sizes, const int32_t* 
                       double* partial, double* leaf_sq, int leaf_sq_stride, void* stream);
 int dpc_leaves_apply(const int64_t* ptrs, const int64_t* sizes, const int32_t* tile_leaf,
                      const int32_t* tile_local, const int64_t* out_offs, int n_tiles, int B,
-                     int dtype, const float* scale, void* out, int out_dtype, float* post_sq,
-                     void* stream);
+                     int dtype, const float* scale, const int32_t* leaf_scale_row, void* out,
+                     int out_dtype, float* post_sq, void* stream);
+
+/* Per-group sums of per-leaf squared norms: out[g * B + b] (float64) = sum of
+ * x[b * stride + j] over the columns j with col_group[j] == g, in column
+ * order -- the per-group accumulation in leaf order of
+ * packages/opake-engine/src/opake/api/engine/clipping/_streaming.py:71-80
+ * (_accumulate_group_value, _pytree.py:345-352). */
+int dpc_group_sum_f64(const double* x, int B, int n, int stride, const int32_t* col_group,
+                      int n_groups, double* out, void* stream);
 
 /* Row sums: out[b] (+)= sum_j x[b, j] (float64), used to fold per-leaf
  * squared norms into per-example totals in a fixed order. */

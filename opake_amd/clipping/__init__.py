@@ -13,22 +13,28 @@ from opake_amd.clipping._clipped_fun import (
 from opake_amd.clipping._ghost import GhostClipAux, ghost_clip_sum, ghost_sqnorms, guard_for_linear
 from opake_amd.clipping._model import GhostGradAux, ghost_clipped_grad
 from opake_amd.clipping._leaves import (
+    LeafClipResult,
     fused_stream_clip_and_sum,
     get_fused_clip_backend,
     leaves_clip_sum,
     make_fused_backend,
     register_fused_clip_backend,
 )
+from opake_amd.clipping._pytree_clip import ClipPytreeAux, auto_scale_pytree, clip_pytree
 
 __all__ = [
     "AutoClipState",
+    "ClipPytreeAux",
     "ClippedFunAux",
     "ClippedGradAux",
     "ClippingStats",
     "FixedClipState",
     "GhostClipAux",
     "GhostGradAux",
+    "LeafClipResult",
     "auto_clipped_grad",
+    "auto_scale_pytree",
+    "clip_pytree",
     "clipped_fun",
     "clipped_grad",
     "fused_stream_clip_and_sum",

@@ -16,8 +16,13 @@ _clipped_grad.py:86-362, _auto.py:211-367):
   (``_microbatch_accumulate_reduced``, _clipped_fun.py:252-345);
 * statistics count ``norm > C`` on the unguarded norms (:348-396).
 
-Not covered (``OperationError``): per-group norms, ``second_moment``, an
-explicit ``compute_dtype``, custom scale functions.
+* ``PerGroup`` clipping norms clip each group of leaves to its own bound by its
+  own norm (``_streaming.py:63-104``); statistics are then counted per group
+  (``_compute_clipping_stats``, :348-396) and ``clipping_rate`` in the aux is
+  ``None``.
+
+Not covered (``OperationError``): ``second_moment``, an explicit
+``compute_dtype``, custom scale functions.
 """
 
 from __future__ import annotations
@@ -29,9 +34,15 @@ import torch
 from torch.autograd.profiler import record_function
 from torch.func import grad_and_value, vmap
 
-from opake_amd.clipping._leaves import leaves_clip_sum, unsupported_reason
+from opake_amd.clipping._leaves import _group_layout, leaves_clip_sum, unsupported_reason
 from opake_amd.exceptions import ConfigurationError, InputTypeError, OperationError
-from opake_amd.pytree import tree_flatten, tree_leaves, tree_map, tree_unflatten
+from opake_amd.pytree import (
+    tree_flatten,
+    tree_flatten_with_paths,
+    tree_leaves,
+    tree_map,
+    tree_unflatten,
+)
 from opake_amd.types import ClippedPytree, ClipState, PerGroup, clipped
 
 _DEFAULT_GAMMA = 0.01
@@ -64,8 +75,8 @@ class ClippedFunAux:
 class ClippingStats:
     """Aggregated statistics (``_clipped_fun.py:83-88``)."""
 
-    num_clipped: float
-    clipping_rate: float | None
+    num_clipped: float | dict
+    clipping_rate: float | dict | None
     batch_size: int = 0
 
 
@@ -92,9 +103,15 @@ def _to_tuple(x) -> tuple:
     return tuple(x) if isinstance(x, (tuple, list)) else (x,)
 
 
-def _validate_clipping_norm(clipping_norm) -> None:
+def _validate_clipping_norm(clipping_norm, name: str = "clipping_norm") -> None:
+    """``_clipped_fun.py:194-207`` / ``_auto.py:99-108``."""
     if isinstance(clipping_norm, PerGroup):
-        raise OperationError("per-group clipping is not implemented by the HIP clip-and-sum")
+        for group_name, value in clipping_norm.values.items():
+            if value <= 0:
+                raise ConfigurationError(
+                    f"{name} must be positive for all groups, got {value} for group "
+                    f"'{group_name}'")
+        return
     if isinstance(clipping_norm, bool) or not isinstance(clipping_norm, (int, float)):
         raise InputTypeError(f"clipping_norm must be a float, got {type(clipping_norm)}")
     if clipping_norm <= 0:
@@ -131,13 +148,24 @@ def _slice_args(args, batch_argnums, start, stop):
     )
 
 
-def _clip_sum_values(values, clipping_norm, scale, *, dtype, with_postsq):
-    """HIP clip-and-sum of a stacked pytree.
+@dataclass
+class _ChunkResult:
+    reduced: Any
+    norms: torch.Tensor
+    post_sq: torch.Tensor | None
+    nclipped: torch.Tensor  # [1], or [G] per group in sorted name order
+    group_norms: dict | None
+    storage: Any
+    aux: Any = None
 
-    Returns ``(reduced, norms, post_sq, nclipped, storage_dtypes)``; the last is
-    a tree of the leaves' storage dtypes.
-    """
-    leaves, treedef = tree_flatten(values)
+
+def _clip_sum_values(values, clipping_norm, scale, *, dtype, with_postsq) -> _ChunkResult:
+    """HIP clip-and-sum of a stacked pytree (``_streaming.py:39-185``)."""
+    grouped = isinstance(clipping_norm, PerGroup)
+    if grouped:
+        paths, leaves, treedef = tree_flatten_with_paths(values)
+    else:
+        leaves, treedef = tree_flatten(values)
     if not leaves:
         raise ConfigurationError("the clipped function returned no tensor leaves")
     B = leaves[0].shape[0]
@@ -150,11 +178,34 @@ def _clip_sum_values(values, clipping_norm, scale, *, dtype, with_postsq):
         if dtype != torch.float32:
             raise OperationError(f"output dtype {dtype} is not supported (float32 or the leaf dtype)")
         out_dtypes = {torch.bfloat16: torch.float32, torch.float32: torch.float32}
-    reduced, norms, post_sq, nclipped, _ = leaves_clip_sum(
-        [l.detach() for l in leaves], float(clipping_norm), kind=scale.kind, gamma=scale.gamma,
-        with_postsq=with_postsq, out_dtypes=out_dtypes)
-    return (tree_unflatten(treedef, reduced), norms, post_sq, nclipped,
-            tree_unflatten(treedef, [l.dtype for l in leaves]))
+    detached = [l.detach() for l in leaves]
+    names = None
+    if grouped:
+        names, leaf_groups, bounds = _group_layout(paths, clipping_norm)
+        res = leaves_clip_sum(detached, bounds, kind=scale.kind, gamma=scale.gamma,
+                              with_postsq=with_postsq, out_dtypes=out_dtypes,
+                              leaf_groups=leaf_groups)
+    else:
+        res = leaves_clip_sum(detached, float(clipping_norm), kind=scale.kind,
+                              gamma=scale.gamma, with_postsq=with_postsq, out_dtypes=out_dtypes)
+    group_norms = None
+    if grouped:
+        group_norms = {n: res.group_norms[k] for k, n in enumerate(names)}
+    return _ChunkResult(reduced=tree_unflatten(treedef, res.reduced), norms=res.norms,
+                        post_sq=res.post_sq, nclipped=res.nclipped, group_norms=group_norms,
+                        storage=tree_unflatten(treedef, [l.dtype for l in leaves]))
+
+
+def _stats(nclipped: torch.Tensor, clipping_norm, batch_size: int):
+    """Counts and rates, per group (sorted names) for ``PerGroup`` (:348-396)."""
+    counts = nclipped.to(torch.float64).cpu().tolist()
+    if isinstance(clipping_norm, PerGroup):
+        names = sorted(clipping_norm.values)
+        num = {n: float(c) for n, c in zip(names, counts)}
+        rate = {n: c / max(1.0, float(batch_size)) for n, c in num.items()}
+        return num, rate
+    num = float(sum(counts))
+    return num, num / max(1.0, float(batch_size))
 
 
 def _make_clipped_fun(fun, has_aux, *, batch_argnums, clipping_norm, normalize_by, return_aux,
@@ -172,8 +223,10 @@ def _make_clipped_fun(fun, has_aux, *, batch_argnums, clipping_norm, normalize_b
         else:
             values = vmap(fun, in_dims=in_dims, out_dims=0, randomness="same")(*args, **kwargs)
             aux = None
-        return _clip_sum_values(values, clipping_norm, scale, dtype=out_dtype,
-                                with_postsq=return_aux) + (aux,)
+        res = _clip_sum_values(values, clipping_norm, scale, dtype=out_dtype,
+                               with_postsq=return_aux)
+        res.aux = aux
+        return res
 
     def clipped_fn(*args, state, **kwargs):
         if len(args) <= max(batch_argnums):
@@ -185,34 +238,43 @@ def _make_clipped_fun(fun, has_aux, *, batch_argnums, clipping_norm, normalize_b
                 "pytree cannot be inferred otherwise.")
         with torch.no_grad():
             if microbatch_size is None:
-                reduced, norms, post_sq, nclipped, _, aux = run_chunk(args, kwargs, dtype)
+                res = run_chunk(args, kwargs, dtype)
+                reduced = res.reduced
             else:
                 # Chunk sums are accumulated in float32 and cast once at the end.
                 acc, parts = None, []
                 for start in range(0, B, microbatch_size):
                     chunk = _slice_args(args, batch_argnums, start, min(B, start + microbatch_size))
-                    r, n, p, c, storage, a = run_chunk(chunk, kwargs, torch.float32)
-                    acc = r if acc is None else tree_map(torch.add, acc, r)
-                    parts.append((n, p, c, a))
-                target = storage if dtype is None else tree_map(lambda _: dtype, storage)
+                    r = run_chunk(chunk, kwargs, torch.float32)
+                    acc = r.reduced if acc is None else tree_map(torch.add, acc, r.reduced)
+                    r.reduced = None
+                    parts.append(r)
+                target = (parts[0].storage if dtype is None
+                          else tree_map(lambda _: dtype, parts[0].storage))
                 reduced = tree_map(lambda x, dt: x.to(dt), acc, target)
-                norms = torch.cat([p[0] for p in parts])
-                post_sq = torch.cat([p[1] for p in parts]) if return_aux else None
-                nclipped = torch.stack([p[2] for p in parts]).sum()
+                group_norms = None
+                if parts[0].group_norms is not None:
+                    group_norms = {n: torch.cat([p.group_norms[n] for p in parts])
+                                   for n in parts[0].group_norms}
                 aux = None
-                if parts[0][3] is not None:
-                    aux = tree_map(lambda *xs: torch.cat(xs), *[p[3] for p in parts])
+                if parts[0].aux is not None:
+                    aux = tree_map(lambda *xs: torch.cat(xs), *[p.aux for p in parts])
+                res = _ChunkResult(
+                    reduced=reduced, norms=torch.cat([p.norms for p in parts]),
+                    post_sq=torch.cat([p.post_sq for p in parts]) if return_aux else None,
+                    nclipped=torch.stack([p.nclipped for p in parts]).sum(dim=0),
+                    group_norms=group_norms, storage=parts[0].storage, aux=aux)
             if normalize_by != 1.0:
                 reduced = tree_map(lambda x: x / normalize_by, reduced)
         output = clipped(reduced, max_norm=output_max_norm)
         if not (return_aux or return_stats):
             return output, state
-        num_clipped = float(nclipped.sum().item())
-        rate = num_clipped / float(B)
+        num_clipped, rate = _stats(res.nclipped, clipping_norm, B)
         if return_aux:
             fun_aux = ClippedFunAux(
-                values=aux, norms=norms, clipped_norms=torch.sqrt(post_sq),
-                clipping_rate=rate, batch_size=B)
+                values=res.aux, norms=res.norms, clipped_norms=torch.sqrt(res.post_sq),
+                clipping_rate=rate if isinstance(rate, float) else None, batch_size=B,
+                group_norms=res.group_norms)
             return (output, fun_aux), state
         return (output, ClippingStats(num_clipped=num_clipped, clipping_rate=rate,
                                       batch_size=B)), state
@@ -293,12 +355,19 @@ def _make_grad(loss_fn, argnums, has_aux, *, clipping_norm, normalize_by, batch_
             zeros = tree_map(torch.zeros_like, args[argnums_t] if isinstance(argnums_t, int)
                              else tuple(args[i] for i in argnums_t))
             grads = clipped(zeros, max_norm=max_norm)
+            per_group = isinstance(clipping_norm, PerGroup)
             if return_aux:
                 empty = torch.empty(0)
                 return (grads, ClippedGradAux(loss_values=empty, grad_norms=empty,
-                                              clipped_grad_norms=empty, clipping_rate=0.0,
+                                              clipped_grad_norms=empty,
+                                              clipping_rate=None if per_group else 0.0,
                                               batch_size=0)), state
             if return_stats:
+                if per_group:
+                    zeros_by_group = dict.fromkeys(sorted(clipping_norm.values), 0.0)
+                    return (grads, ClippingStats(num_clipped=zeros_by_group,
+                                                 clipping_rate=dict(zeros_by_group),
+                                                 batch_size=0)), state
                 return (grads, ClippingStats(num_clipped=0.0, clipping_rate=0.0,
                                              batch_size=0)), state
             return grads, state
@@ -311,7 +380,8 @@ def _make_grad(loss_fn, argnums, has_aux, *, clipping_norm, normalize_by, batch_
         return (grads, ClippedGradAux(
             loss_values=values.get("values"), grad_norms=aux.norms,
             clipped_grad_norms=aux.clipped_norms, loss_aux=values.get("value_aux"),
-            clipping_rate=aux.clipping_rate, batch_size=aux.batch_size)), st
+            clipping_rate=aux.clipping_rate, batch_size=aux.batch_size,
+            group_norms=aux.group_norms)), st
 
     return wrapper
 
@@ -366,7 +436,7 @@ def auto_clipped_grad(
         raise OperationError("second_moment=True is not implemented by the HIP clip-and-sum")
     if isinstance(gamma, bool) or not isinstance(gamma, (int, float)) or not gamma > 0:
         raise ConfigurationError(f"gamma must be a positive float, got {gamma!r}")
-    _validate_clipping_norm(R)
+    _validate_clipping_norm(R, "R")
     state = AutoClipState()
     fn = _make_grad(loss_fn, argnums, has_aux, clipping_norm=R, normalize_by=normalize_by,
                     batch_argnums=batch_argnums, return_aux=return_aux,

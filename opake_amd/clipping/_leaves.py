@@ -15,9 +15,10 @@ number of HIP launches per storage dtype, whatever the number of leaves:
 3. ``dpc_leaves_apply``: scale in fp32, one cast to the storage dtype, bf16
    subnormals that rounded up zeroed, fp32 sum over the batch in example order.
 
-A call the kernels do not cover (per-group norms, ``second_moment``, an
-explicit ``compute_dtype``, dtypes other than float32 / bfloat16, leaves that
-need grad) goes to the ``fallback`` the caller registered with
+Per-group clipping norms (``PerGroup``) clip each group to its own bound by
+its own norm, with one scale row per group.  A call the kernels do not cover
+(``second_moment``, an explicit ``compute_dtype``, dtypes other than float32 /
+bfloat16, leaves that need grad) goes to the ``fallback`` the caller registered with
 :func:`make_fused_backend` -- in the reference that is its own PyTorch
 streaming path -- and raises ``OperationError`` when there is none.
 """
@@ -26,6 +27,7 @@ from __future__ import annotations
 
 import math
 from collections import OrderedDict
+from dataclasses import dataclass
 
 import numpy as np
 import torch
@@ -33,8 +35,15 @@ import torch
 from opake_amd import _native as nat
 from opake_amd import ops
 from opake_amd.clipping import _numerics as num
-from opake_amd.exceptions import OperationError
-from opake_amd.pytree import tree_flatten, tree_unflatten
+from opake_amd.exceptions import ConfigurationError, OperationError
+from opake_amd.pytree import (
+    param_path,
+    param_path_display,
+    tree_flatten,
+    tree_flatten_with_paths,
+    tree_unflatten,
+)
+from opake_amd.types import PerGroup
 
 TILE = 2048  # elements per tile: the reference's blocked-reduction width
 _MAX_BATCH = 65535
@@ -58,8 +67,6 @@ def get_fused_clip_backend():
 def unsupported_reason(leaves, clipping_norm, scale, *, compute_dtype, second_moment,
                        batch_size) -> str | None:
     """Why the kernels cannot serve this call, or ``None``."""
-    if hasattr(clipping_norm, "groups"):
-        return "per-group clipping norms are not supported by the leaf kernels"
     if getattr(scale, "kind", "fixed") not in ("fixed", "auto_s"):
         return f"unknown scale kind {scale.kind!r}"
     if second_moment:
@@ -155,18 +162,44 @@ def _dtype_marker(leaf):
     return marker
 
 
-def leaves_clip_sum(leaves, clipping_norm: float, *, kind: str = "fixed", gamma: float = 0.0,
-                    with_postsq: bool = False, out_dtypes=None):
-    """Clip-and-sum of stacked leaves with the HIP kernels.
+@dataclass
+class LeafClipResult:
+    """Outputs of :func:`leaves_clip_sum` (device tensors, nothing synchronised).
 
-    Returns ``(reduced, norms, post_sq, nclipped, scales)``: per-leaf batch sums
-    (in ``out_dtypes[dtype]``, default the leaf dtype), float32 norms [B],
-    float32 ``||stored||^2`` per example (or ``None``), int32 [1] count of
-    ``norm > C`` and the float32 scale rows ``{dtype: [B]}``.
+    ``reduced``: per-leaf batch sums.  ``norms``: float32 [B] global norms.
+    ``post_sq``: float32 [B] ``||stored||^2`` or ``None``.  ``nclipped``:
+    int32 [1] examples with norm > C (global clipping) or [G] per group.
+    ``group_norms``: float32 [G, B] (per-group clipping) or ``None``.
+    ``scales``: float32 scale rows per storage dtype, [G, B] (G = 1 without groups).
+    """
+
+    reduced: list
+    norms: torch.Tensor
+    post_sq: torch.Tensor | None
+    nclipped: torch.Tensor
+    group_norms: torch.Tensor | None
+    scales: dict
+
+
+def leaves_clip_sum(leaves, clipping_norm, *, kind: str = "fixed", gamma: float = 0.0,
+                    with_postsq: bool = False, out_dtypes=None, leaf_groups=None,
+                    conservative: bool = True):
+    """Clip-and-sum of stacked leaves ``[B, *P]`` with the HIP kernels.
+
+    ``clipping_norm`` is one bound, or -- with ``leaf_groups`` (group index of
+    each leaf) -- a list of per-group bounds: each group is clipped to its own
+    bound by its own norm (``_streaming.py:63-104``).  Batch sums come out in
+    ``out_dtypes[dtype]`` (default: the leaf dtype).  ``conservative`` rounds
+    each bound down to float32 first, as the reference's batch path does
+    (``_clipped_fun.py:211-216``); the single-pytree functions use the exact
+    bound (``_pytree.py:624-628``).  See :class:`LeafClipResult`.
     """
     device = leaves[0].device
     B = leaves[0].shape[0]
     L = len(leaves)
+    grouped = leaf_groups is not None
+    bounds = list(clipping_norm) if grouped else [clipping_norm]
+    n_groups = len(bounds)
     contiguous = [l if l.is_contiguous() else l.contiguous() for l in leaves]
     plan = _plan(contiguous, device)
     stream = nat.stream_handle(device)
@@ -188,9 +221,25 @@ def leaves_clip_sum(leaves, clipping_norm: float, *, kind: str = "fixed", gamma:
     nat.call("dpc_row_sum_f64", nat.ptr(leaf_sq), B, L, 0, nat.ptr(sq), stream)
     guards = [num.guard_constants(g["dtype"], torch.promote_types(g["dtype"], acc), roundoff)
               for g in groups]
-    cf = ops.clip_factors(sq, num.conservative_bound(clipping_norm), guards,
-                          kind=nat.SCALE_AUTO_S if kind == "auto_s" else nat.SCALE_FIXED,
-                          gamma=gamma, count_threshold=num.float32_of(clipping_norm))
+    scale_kind = nat.SCALE_AUTO_S if kind == "auto_s" else nat.SCALE_FIXED
+    bound_of = num.conservative_bound if conservative else float
+    if grouped:
+        col_group = _device_table(device, ("col_group", tuple(leaf_groups)), leaf_groups,
+                                  np.int32)
+        group_sq = torch.empty((n_groups, B), dtype=torch.float64, device=device)
+        nat.call("dpc_group_sum_f64", nat.ptr(leaf_sq), B, L, L, nat.ptr(col_group), n_groups,
+                 nat.ptr(group_sq), stream)
+        cfs = [ops.clip_factors(group_sq[k], bound_of(bounds[k]), guards,
+                                kind=scale_kind, gamma=gamma,
+                                count_threshold=num.float32_of(bounds[k]))
+               for k in range(n_groups)]
+        norms = torch.sqrt(sq).to(torch.float32)
+        group_norms = torch.stack([cf.norms for cf in cfs])
+        nclipped = torch.cat([cf.nclipped for cf in cfs])
+    else:
+        cfs = [ops.clip_factors(sq, bound_of(bounds[0]), guards, kind=scale_kind,
+                                gamma=gamma, count_threshold=num.float32_of(bounds[0]))]
+        norms, group_norms, nclipped = cfs[0].norms, None, cfs[0].nclipped
     reduced = [None] * L
     post_sq = None
     if with_postsq:
@@ -202,18 +251,65 @@ def leaves_clip_sum(leaves, clipping_norm: float, *, kind: str = "fixed", gamma:
         flat = torch.empty(g["total"], dtype=out_dtype, device=device)
         tile_sq = (torch.empty((B, g["n_tiles"]), dtype=torch.float32, device=device)
                    if with_postsq else None)
-        scale_row = cf.scale[gi]
-        scales[dtype] = scale_row
+        if grouped:
+            scale_rows = torch.stack([cf.scale[gi] for cf in cfs])
+            rows = [leaf_groups[i] for i in g["idx"]]
+            leaf_row = _device_table(device, ("leaf_row", dtype, tuple(rows)), rows, np.int32)
+        else:
+            scale_rows, leaf_row = cfs[0].scale[gi:gi + 1], None
+        scales[dtype] = scale_rows
         nat.call("dpc_leaves_apply", nat.ptr(ptr_tables[gi]), nat.ptr(g["sizes"]),
                  nat.ptr(g["tile_leaf"]), nat.ptr(g["tile_local"]), nat.ptr(g["out_offs"]),
-                 g["n_tiles"], B, nat.dtype_code(dtype), nat.ptr(scale_row), nat.ptr(flat),
-                 nat.dtype_code(out_dtype), nat.ptr(tile_sq), stream)
+                 g["n_tiles"], B, nat.dtype_code(dtype), nat.ptr(scale_rows), nat.ptr(leaf_row),
+                 nat.ptr(flat), nat.dtype_code(out_dtype), nat.ptr(tile_sq), stream)
         if with_postsq:
             post_sq += tile_sq.sum(dim=1)
         for j, i in enumerate(g["idx"]):
             off, n = g["offsets_host"][j], g["sizes_host"][j]
             reduced[i] = flat[off:off + n].view(leaves[i].shape[1:])
-    return reduced, cf.norms, post_sq, cf.nclipped, scales
+    return LeafClipResult(reduced=reduced, norms=norms, post_sq=post_sq, nclipped=nclipped,
+                          group_norms=group_norms, scales=scales)
+
+
+_TABLES: OrderedDict = OrderedDict()
+
+
+def _device_table(device, key, values, np_dtype):
+    """Small immutable index tables, copied to the device once (bounded LRU)."""
+    full = (device, key)
+    t = _TABLES.get(full)
+    if t is None:
+        t = torch.from_numpy(np.asarray(values, dtype=np_dtype)).to(device)
+        _TABLES[full] = t
+        if len(_TABLES) > 4 * _MAX_PLANS:
+            _TABLES.popitem(last=False)
+    else:
+        _TABLES.move_to_end(full)
+    return t
+
+
+def _group_layout(paths, clipping_norm):
+    """Leaf -> group index (groups in sorted name order) and the group bounds.
+
+    Requires a 1:1 match between leaf paths and the PerGroup's path keys
+    (``_pytree.py:56-74``).
+    """
+    leaf_set = {param_path(p) for p in paths}
+    group_set = set(clipping_norm.groups)
+    if leaf_set != group_set:
+        parts = ["PerGroup path keys must match the pytree tensor leaves exactly."]
+        missing = sorted(leaf_set - group_set, key=param_path_display)
+        extra = sorted(group_set - leaf_set, key=param_path_display)
+        if missing:
+            parts.append(f"Leaves with no group assignment: {missing}.")
+        if extra:
+            parts.append(f"Group paths with no matching leaf: {extra}.")
+        raise ConfigurationError(" ".join(parts))
+    names = sorted(clipping_norm.values)
+    index = {n: k for k, n in enumerate(names)}
+    leaf_groups = [index[clipping_norm.groups[param_path(p)]] for p in paths]
+    bounds = [float(clipping_norm.values[n]) for n in names]
+    return names, leaf_groups, bounds
 
 
 def make_fused_backend(fallback=None):
@@ -241,20 +337,32 @@ def make_fused_backend(fallback=None):
                             reduce_leaf=reduce_leaf, compute_dtype=compute_dtype,
                             second_moment=second_moment, return_aux=return_aux,
                             return_stats=return_stats)
-        C = float(clipping_norm)
         kind = getattr(scale, "kind", "fixed")
         gamma = float(getattr(scale, "gamma", 0.0))
+        grouped = isinstance(clipping_norm, PerGroup)
+        names = None
         if not leaves or batch_size == 0:
             device = leaves[0].device if leaves else torch.device("cuda")
             reduced = [reduce_leaf(l) for l in leaves]
             norms = torch.zeros(batch_size, dtype=torch.float32, device=device)
             post = norms.clone()
+            group_norms = None
         else:
-            reduced, norms, post, _, _ = leaves_clip_sum(
-                leaves, C, kind=kind, gamma=gamma, with_postsq=return_aux, out_dtypes=out_dtypes)
+            if grouped:
+                paths, _, _ = tree_flatten_with_paths(values)
+                names, leaf_groups, bounds = _group_layout(paths, clipping_norm)
+                res = leaves_clip_sum(leaves, bounds, kind=kind, gamma=gamma,
+                                      with_postsq=return_aux, out_dtypes=out_dtypes,
+                                      leaf_groups=leaf_groups)
+            else:
+                res = leaves_clip_sum(leaves, float(clipping_norm), kind=kind, gamma=gamma,
+                                      with_postsq=return_aux, out_dtypes=out_dtypes)
+            reduced, norms, post, group_norms = res.reduced, res.norms, res.post_sq, res.group_norms
         diagnostics = {}
         if return_aux or return_stats:
             diagnostics["norms"] = norms.detach()
+            if grouped and group_norms is not None:
+                diagnostics["group_norms"] = {n: group_norms[k].detach() for k, n in enumerate(names)}
         if return_aux:
             diagnostics["clipped_norms"] = torch.sqrt(post).detach()
         markers = [_dtype_marker(l) for l in leaves]
@@ -275,6 +383,7 @@ fused_stream_clip_and_sum = make_fused_backend()
 __all__ = [
     "fused_stream_clip_and_sum",
     "get_fused_clip_backend",
+    "LeafClipResult",
     "leaves_clip_sum",
     "make_fused_backend",
     "register_fused_clip_backend",

@@ -94,8 +94,8 @@ __global__ void __launch_bounds__(kThreads)
 apply_sum_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ sizes,
                  const int32_t* __restrict__ tile_leaf, const int32_t* __restrict__ tile_local,
                  const int64_t* __restrict__ out_offs, int n_tiles, int B,
-                 const float* __restrict__ scale, void* __restrict__ out,
-                 float* __restrict__ post_sq) {
+                 const float* __restrict__ scale, const int32_t* __restrict__ leaf_scale_row,
+                 void* __restrict__ out, float* __restrict__ post_sq) {
   __shared__ float red[kThreads / 64];
   const int t = blockIdx.x;
   const int leaf = tile_leaf[t];
@@ -106,8 +106,9 @@ apply_sum_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ s
   float acc[kPerThread];
 #pragma unroll
   for (int j = 0; j < kPerThread; ++j) acc[j] = 0.f;
+  const float* srow = scale + (size_t)(leaf_scale_row ? leaf_scale_row[leaf] : 0) * B;
   for (int b = 0; b < B; ++b) {
-    const float s = scale[b];
+    const float s = srow[b];
     float sq = 0.f;
 #pragma unroll
     for (int j = 0; j < kPerThread; ++j) {
@@ -145,7 +146,35 @@ apply_sum_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ s
 }
 #pragma clang fp contract(on)
 
+// out[g * B + b] = sum over columns j with col_group[j] == g of x[b, j], in
+// column order (fp64): the reference's per-group accumulation in leaf order.
+__global__ void __launch_bounds__(kThreads)
+group_sum_kernel(const double* __restrict__ x, int B, int n, int stride,
+                 const int32_t* __restrict__ col_group, int n_groups, double* __restrict__ out) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= B * n_groups) return;
+  const int g = idx / B, b = idx % B;
+  double s = 0.0;
+  for (int j = 0; j < n; ++j) {
+    if (col_group[j] == g) s += x[(size_t)b * stride + j];
+  }
+  out[(size_t)g * B + b] = s;
+}
+
 }  // namespace
+
+extern "C" int dpc_group_sum_f64(const double* x, int B, int n, int stride,
+                                 const int32_t* col_group, int n_groups, double* out,
+                                 void* stream) {
+  if (B < 0 || n < 0 || stride < n || n_groups < 1) return DPC_EINVAL;
+  if (B == 0) return DPC_OK;
+  if (!out || (n > 0 && (!x || !col_group))) return DPC_EINVAL;
+  const int total = B * n_groups;
+  hipLaunchKernelGGL(group_sum_kernel, dim3(ceil_div(total, kThreads)), dim3(kThreads), 0,
+                     (hipStream_t)stream, x, B, n, stride, col_group, n_groups, out);
+  DPC_HIP_CHECK(hipGetLastError());
+  return DPC_OK;
+}
 
 extern "C" int dpc_leaves_sqnorm(const int64_t* ptrs, const int64_t* sizes,
                                  const int32_t* tile_leaf, const int32_t* tile_local,
@@ -180,8 +209,8 @@ extern "C" int dpc_leaves_sqnorm(const int64_t* ptrs, const int64_t* sizes,
 extern "C" int dpc_leaves_apply(const int64_t* ptrs, const int64_t* sizes,
                                 const int32_t* tile_leaf, const int32_t* tile_local,
                                 const int64_t* out_offs, int n_tiles, int B, int dtype,
-                                const float* scale, void* out, int out_dtype, float* post_sq,
-                                void* stream) {
+                                const float* scale, const int32_t* leaf_scale_row, void* out,
+                                int out_dtype, float* post_sq, void* stream) {
   if (n_tiles < 0 || B < 0) return DPC_EINVAL;
   if (dtype != DPC_F32 && dtype != DPC_BF16) return DPC_EINVAL;
   if (out_dtype != DPC_F32 && out_dtype != dtype) return DPC_EINVAL;
@@ -191,15 +220,15 @@ extern "C" int dpc_leaves_apply(const int64_t* ptrs, const int64_t* sizes,
   hipStream_t s = (hipStream_t)stream;
   if (dtype == DPC_BF16 && out_dtype == DPC_BF16) {
     hipLaunchKernelGGL((apply_sum_kernel<true, true>), dim3(n_tiles), dim3(kThreads), 0, s, ptrs,
-                       sizes, tile_leaf, tile_local, out_offs, n_tiles, B, scale, out, post_sq);
+                       sizes, tile_leaf, tile_local, out_offs, n_tiles, B, scale, leaf_scale_row, out, post_sq);
   } else if (dtype == DPC_BF16) {
     hipLaunchKernelGGL((apply_sum_kernel<true, false>), dim3(n_tiles), dim3(kThreads), 0, s,
-                       ptrs, sizes, tile_leaf, tile_local, out_offs, n_tiles, B, scale, out,
-                       post_sq);
+                       ptrs, sizes, tile_leaf, tile_local, out_offs, n_tiles, B, scale,
+                       leaf_scale_row, out, post_sq);
   } else {
     hipLaunchKernelGGL((apply_sum_kernel<false, false>), dim3(n_tiles), dim3(kThreads), 0, s,
-                       ptrs, sizes, tile_leaf, tile_local, out_offs, n_tiles, B, scale, out,
-                       post_sq);
+                       ptrs, sizes, tile_leaf, tile_local, out_offs, n_tiles, B, scale,
+                       leaf_scale_row, out, post_sq);
   }
   DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;

@@ -278,3 +278,154 @@ def test_ghost_clipped_grad_sequence_bf16(dev):
     for i, n in enumerate(names):
         assert _rel(out.pytree[n], res.reduced[i]) < 2e-2, n
     torch.testing.assert_close(aux.grad_norms.cpu().double(), res.norms, rtol=2e-2, atol=0)
+
+
+# --- per-group clipping ------------------------------------------------------------------
+
+
+def _per_group(names, assignment, values):
+    from opake_amd.types import PerGroup
+    return PerGroup({n: assignment[n] for n in names}, values)
+
+
+@pytest.mark.parametrize("kind", ["fixed", "auto_s"])
+def test_leaf_backend_per_group_matches_streaming_oracle(dev, kind):
+    gen = torch.Generator().manual_seed(11 + (kind == "auto_s"))
+    B = 7
+    tree = _values(gen, B, [torch.float32, torch.bfloat16])
+    tree["p3"][1, 2, 5] = math.nan
+    names = sorted(tree)
+    assignment = {"p0": "attn", "p1": "mlp", "p2": "attn", "p3": "emb", "p4": "mlp"}
+    values = {"attn": 0.3, "mlp": 0.05, "emb": 2.0}
+    cons = {g: clip_oracle.conservative_bound(v) for g, v in values.items()}
+    gamma = 0.01 if kind == "auto_s" else 0.0
+    res = clip_oracle.stream_clip_and_sum(
+        [tree[n] for n in names], None, kind=kind, gamma=gamma,
+        groups=[assignment[n] for n in names], group_values=cons, return_aux=True)
+    pg = _per_group(names, assignment, values)
+    dev_tree = {k: v.to(dev) for k, v in tree.items()}
+    reduced, _, _, _, diag = cl.fused_stream_clip_and_sum(
+        dev_tree, pg, scale=_Scale(kind, gamma), batch_size=B, reduce_leaf=_reduce,
+        compute_dtype=None, second_moment=False, return_aux=True, return_stats=False)
+    for i, n in enumerate(names):
+        assert reduced[n].dtype == tree[n].dtype
+        torch.testing.assert_close(reduced[n].cpu(), res.reduced[i])
+    torch.testing.assert_close(diag["norms"].cpu().double(), res.norms, rtol=1e-6, atol=0)
+    assert set(diag["group_norms"]) == set(values)
+    for g in values:
+        torch.testing.assert_close(diag["group_norms"][g].cpu().double(), res.group_norms[g],
+                                   rtol=1e-6, atol=0)
+    torch.testing.assert_close(diag["clipped_norms"].cpu().double(),
+                               res.clipped_norms.double(), rtol=1e-5, atol=1e-7)
+
+
+def test_clip_pytree_per_group_closed_form(dev):
+    # attn = [3, 4] with C_attn = 1 -> [0.6, 0.8]; mlp = [0.3, 0.4] with C_mlp = 1 unchanged.
+    tree = {"attn": torch.tensor([3.0, 4.0], device=dev),
+            "mlp": torch.tensor([0.3, 0.4], device=dev)}
+    pg = _per_group(["attn", "mlp"], {"attn": "a", "mlp": "m"}, {"a": 1.0, "m": 1.0})
+    out, aux = cl.clip_pytree(tree, pg)
+    torch.testing.assert_close(out["attn"].cpu(), torch.tensor([0.6, 0.8]), rtol=1e-6, atol=0)
+    assert torch.equal(out["mlp"].cpu(), tree["mlp"].cpu())
+    assert aux.group_norms["a"].item() == pytest.approx(5.0)
+    assert aux.group_norms["m"].item() == pytest.approx(0.5)
+    assert aux.norm.item() == pytest.approx(math.sqrt(25.25))
+
+
+def test_per_group_path_mismatch_raises(dev):
+    from opake_amd.exceptions import ConfigurationError
+    tree = {"a": torch.ones(2, 3, device=dev), "b": torch.ones(2, 3, device=dev)}
+    pg = _per_group(["a"], {"a": "g"}, {"g": 1.0})
+    with pytest.raises(ConfigurationError, match="Leaves with no group assignment"):
+        cl.fused_stream_clip_and_sum(
+            tree, pg, scale=_Scale("fixed"), batch_size=2, reduce_leaf=_reduce,
+            compute_dtype=None, second_moment=False, return_aux=False, return_stats=False)
+
+
+@pytest.mark.parametrize("microbatch", [None, 3])
+def test_clipped_grad_per_group_stats_and_aux(dev, microbatch):
+    gen = torch.Generator().manual_seed(5)
+    B = 8
+    d_w, d_b = torch.randn(B, 6, generator=gen) * 2, torch.randn(B, 3, generator=gen) * 0.1
+
+    def loss(p, dw, db):  # per-example grads: w -> dw, b -> db
+        return (p["w"] * dw).sum() + (p["b"] * db).sum()
+
+    params = {"w": torch.zeros(6, device=dev), "b": torch.zeros(3, device=dev)}
+    pg = _per_group(["w", "b"], {"w": "weights", "b": "bias"}, {"weights": 1.5, "bias": 0.2})
+    cons = {"weights": clip_oracle.conservative_bound(1.5),
+            "bias": clip_oracle.conservative_bound(0.2)}
+    res = clip_oracle.stream_clip_and_sum([d_b, d_w], None, groups=["bias", "weights"],
+                                          group_values=cons, return_aux=True)
+    g, st = cl.clipped_grad(loss, clipping_norm=pg, normalize_by=2.0, batch_argnums=(1, 2),
+                            return_aux=True, microbatch_size=microbatch)
+    (out, aux), _ = g(params, d_w.to(dev), d_b.to(dev), state=st)
+    assert out.max_norm.values == {"weights": 0.75, "bias": 0.1}
+    torch.testing.assert_close(out.pytree["b"].cpu(), res.reduced[0] / 2.0)
+    torch.testing.assert_close(out.pytree["w"].cpu(), res.reduced[1] / 2.0)
+    assert aux.clipping_rate is None and aux.batch_size == B
+    for gname in ("weights", "bias"):
+        torch.testing.assert_close(aux.group_norms[gname].cpu().double(), res.group_norms[gname],
+                                   rtol=1e-6, atol=0)
+    g2, st2 = cl.clipped_grad(loss, clipping_norm=pg, batch_argnums=(1, 2), return_stats=True,
+                              microbatch_size=microbatch)
+    (_, stats), _ = g2(params, d_w.to(dev), d_b.to(dev), state=st2)
+    want = {gname: float((res.group_norms[gname].float() > v).sum())
+            for gname, v in (("weights", 1.5), ("bias", 0.2))}
+    assert stats.num_clipped == want
+    assert stats.clipping_rate == {k: v / B for k, v in want.items()}
+    assert stats.batch_size == B
+
+
+# --- single-pytree clipping ----------------------------------------------------------------
+
+
+def test_clip_pytree_closed_forms(dev):
+    x = {"w": torch.tensor([3.0, 4.0], device=dev)}
+    out, aux = cl.clip_pytree(x, 0.0)
+    assert torch.equal(out["w"].cpu(), torch.zeros(2)) and aux.norm.item() == 5.0
+    out, _ = cl.clip_pytree(x, float("inf"))
+    assert torch.equal(out["w"].cpu(), x["w"].cpu())
+    out, aux = cl.clip_pytree(x, 1.0)
+    assert float(out["w"].double().norm()) == pytest.approx(1.0, rel=1e-6)
+    assert float(out["w"].double().norm()) <= 1.0
+    small = {"w": torch.tensor([0.3, 0.4], device=dev)}
+    out, _ = cl.clip_pytree(small, 1.0)
+    assert torch.equal(out["w"].cpu(), small["w"].cpu())
+    bad = {"w": torch.tensor([math.nan, math.inf, 2.0], device=dev)}
+    out, aux = cl.clip_pytree(bad, 10.0)
+    assert torch.equal(out["w"].cpu(), torch.tensor([0.0, 0.0, 2.0])) and aux.norm.item() == 2.0
+    out, _ = cl.clip_pytree(x, 1.0, return_zero=True)
+    assert torch.equal(out["w"].cpu(), torch.zeros(2))
+    zero = {"w": torch.zeros(4, device=dev)}
+    out, _ = cl.clip_pytree(zero, 1.0)
+    assert torch.equal(out["w"].cpu(), torch.zeros(4))
+    # AUTO-S: [3,4], R=1, gamma=0.01 -> x / 5.01; zeros stay zeros (test_auto.py:24-62).
+    out, aux = cl.auto_scale_pytree(x, R=1.0, gamma=0.01)
+    torch.testing.assert_close(out["w"].cpu(), torch.tensor([3.0, 4.0]) / 5.01, rtol=1e-6,
+                               atol=0)
+    out, _ = cl.auto_scale_pytree(zero, R=1.0, gamma=0.01)
+    assert torch.equal(out["w"].cpu(), torch.zeros(4))
+    from opake_amd.exceptions import ConfigurationError
+    with pytest.raises(ConfigurationError):
+        cl.auto_scale_pytree(x, R=1.0, gamma=0.0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_clip_pytree_matches_oracle(dev, dtype):
+    gen = torch.Generator().manual_seed(21)
+    tree = {"a": (torch.randn(37, 5, generator=gen) * 3).to(dtype),
+            "b": (torch.randn(9000, generator=gen)).to(dtype), "c": 1.5}
+    names = ["a", "b"]
+    for C in (0.7, 1e6):
+        want, want_norm = clip_oracle.clip_pytree_scalar([tree[n] for n in names], C)
+        out, aux = cl.clip_pytree({k: (v.to(dev) if torch.is_tensor(v) else v)
+                                   for k, v in tree.items()}, C)
+        assert out["c"] == 1.5
+        for n, w in zip(names, want):
+            torch.testing.assert_close(out[n].cpu(), w)
+        torch.testing.assert_close(aux.norm.cpu(), want_norm, rtol=1e-6, atol=0)
+    want, _ = clip_oracle.auto_scale_scalar([tree[n] for n in names], 0.5, 0.01)
+    out, _ = cl.auto_scale_pytree({n: tree[n].to(dev) for n in names}, R=0.5, gamma=0.01)
+    for n, w in zip(names, want):
+        torch.testing.assert_close(out[n].cpu(), w)
