@@ -182,6 +182,52 @@ int dpc_leaves_apply(const int64_t* ptrs, const int64_t* sizes, const int32_t* t
 int dpc_group_sum_f64(const double* x, int B, int n, int stride, const int32_t* col_group,
                       int n_groups, double* out, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Grouped (segmented) linear layers: E problems of one shape, e.g. the same
+ * projection of E mixture-of-experts experts.  Problem e has operands A_e
+ * [rows_e, din] and G_e [rows_e, dout] (addresses in the device int64 tables
+ * a_ptrs / g_ptrs) whose rows are cut into segments, each segment the rows
+ * of one example -- the reference's "virtual experts" b * E + e of
+ * packages/opake-patches/src/opake/api/patches/kernels/fused_moe.py:20-27,
+ * whose per-sample weight gradient out[g] = A_g^T B_g over the segment's rows
+ * (_grouped_AtB, fused_moe.py:54-113) is never formed here.
+ *
+ * dpc_grouped_gram_sqnorms: seg_sq[v] = ||G_v^T A_v||^2 for every segment v
+ *   (float64, written), the per-sample norms of the virtual experts that
+ *   _streaming.py:70-82 would take of the materialised gradients.  `items`
+ *   (device int32 [n_items][4]) lists (problem, first row, rows, pair) for
+ *   every 128-row tile pair p <= q (pair = q (q + 1) / 2 + p) of every
+ *   segment, segment by segment; seg_item_start (device int32 [S + 1]) gives
+ *   each segment's item range.  max_rows bounds every segment's rows.
+ *   ws: n_items float64.
+ * dpc_segment_plan: the step table of dpc_grouped_clipped_sum.  Segment v
+ *   (rows seg_row0[v] .. + seg_len[v] of problem seg_group[v]; segments sorted
+ *   by problem) contributes ceil(seg_len / 64) steps (row0, v << 7 | rows)
+ *   when seg_scale[v] > 0; step_start[e] (device int32 [E + 1]) is problem
+ *   e's first step.  max_steps bounds the table (int32 [2 * max_steps]).
+ * dpc_grouped_clipped_sum: for each problem e, the dpc_clipped_sum recipe
+ *   over its segments, segment v scaled by seg_scale[v]:
+ *     acc[m, n] = sum_v seg_scale[v] * sum_{t in v} G_e[t, m] * A_e[t, n]
+ *   written to out_ptrs[e] ([dout, din], out_dtype) with / normalize_by and
+ *   noise sigmas[e] * z (z from noise_ptrs[e] or Philox (seed, leaf_ids[e])).
+ *   rows (device int32 [E]) bounds each problem's operand rows; max_rows
+ *   bounds rows.  Segments with scale 0 are never read.
+ * -------------------------------------------------------------------------*/
+int dpc_grouped_gram_sqnorms(const int64_t* a_ptrs, const int64_t* g_ptrs, int din, int dout,
+                             int dtype, const int32_t* items, int n_items, int max_rows,
+                             const int32_t* seg_item_start, int S, double* seg_sq, void* ws,
+                             size_t ws_bytes, void* stream);
+int dpc_segment_plan(const int32_t* seg_row0, const int32_t* seg_len, const int32_t* seg_group,
+                     const float* seg_scale, int S, int E, int max_steps, int32_t* steps,
+                     int32_t* step_start, void* stream);
+int dpc_grouped_clipped_sum(const int64_t* a_ptrs, const int64_t* g_ptrs, const int32_t* rows,
+                            int max_rows, int E, int din, int dout, int dtype,
+                            const int32_t* steps, const int32_t* step_start,
+                            const float* seg_scale, double normalize_by, int noise_mode,
+                            const int64_t* noise_ptrs, uint64_t seed, const uint32_t* leaf_ids,
+                            const float* sigmas, int out_dtype, const int64_t* out_ptrs,
+                            void* stream);
+
 /* Row sums: out[b] (+)= sum_j x[b, j] (float64), used to fold per-leaf
  * squared norms into per-example totals in a fixed order. */
 int dpc_row_sum_f64(const double* x, int B, int n, int accumulate, double* out, void* stream);

@@ -94,6 +94,22 @@ SIGNATURES = {
         _c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_void_p],
     ),
     "dpc_row_sum_f64": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_void_p]),
+    "dpc_grouped_gram_sqnorms": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_int, _c_void_p,
+         _c_int, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
+    ),
+    "dpc_segment_plan": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_void_p,
+         _c_void_p, _c_void_p],
+    ),
+    "dpc_grouped_clipped_sum": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,
+         _c_void_p, _c_void_p, _c_double, _c_int, _c_void_p, _c_u64, _c_void_p, _c_void_p, _c_int,
+         _c_void_p, _c_void_p],
+    ),
 }
 
 _lock = threading.Lock()

@@ -12,12 +12,27 @@ follows from each layer's inputs ``A`` and output gradients ``G`` alone:
    (``G_i`` is example ``i``'s own output gradient because ``loss_i`` depends on
    example ``i`` only; no weight-gradient GEMM runs);
 2. per-example squared norms summed over layers (``dpc_gram_sqnorms`` /
-   ``dpc_flat_sqnorms``, accumulated into one float64 [B] vector);
-3. one set of guarded clip factors for the whole parameter tree, with the
-   reference's roundoff for the materialised leaves (``_norm_roundoff`` over
-   all weights and biases);
+   ``dpc_flat_sqnorms``), one float64 [B] row per clipping group;
+3. guarded clip factors per group, with the reference's roundoff for the
+   materialised leaves (``_norm_roundoff`` over all weights and biases);
 4. one ``dpc_clipped_sum`` per layer (weight and bias), with ``/ normalize_by``
    and, optionally, the Gaussian noise fused into the epilogue.
+
+Row-segmented layers.  A module that feeds one linear layer with the rows of
+several examples -- the experts of a mixture-of-experts layer, whose input is
+the tokens routed to that expert -- sets ``linear.dpc_row_segments`` to the
+per-example row counts (a list of B ints, rows in example order) before it
+calls the layer.  Such a layer's per-example gradient is the sum over its
+segment (the reference's "virtual experts" ``b * E + e``,
+packages/opake-patches/src/opake/api/patches/kernels/fused_moe.py:20-27), and
+all segmented layers of one shape go through one grouped norm launch
+(``dpc_grouped_gram_sqnorms``) and one grouped clipped-sum launch
+(``dpc_grouped_clipped_sum``).
+
+``clipping_norm`` may be a ``PerGroup`` over the output leaves (keys
+``"<layer>.weight"`` / ``"<layer>.bias"``, the parameter names): each group is clipped to its own
+bound by its own per-example norm (_streaming.py:63-104), and the noise of a
+leaf uses its group's standard deviation.
 
 The output is the reference's ``ClippedPytree`` (``NoisedPytree`` with noise)
 over ``{parameter name: tensor}`` with ``max_norm = C / normalize_by``; noise
@@ -37,6 +52,7 @@ from opake_amd.clipping import _numerics as num
 from opake_amd.clipping._clipped_fun import FixedClipState
 from opake_amd.exceptions import ConfigurationError, InputTypeError
 from opake_amd.noise import GaussianNoiseState, step_key_for
+from opake_amd.pytree import param_path
 from opake_amd.random import generator_from_key
 from opake_amd.types import NoisedPytree, PerGroup, clipped
 
@@ -44,32 +60,43 @@ from opake_amd.types import NoisedPytree, PerGroup, clipped
 @dataclass(frozen=True)
 class GhostGradAux:
     """Per-example diagnostics (device tensors): loss values, norms before
-    clipping (float32), applied clip scales, ``num_clipped`` (int32 [1])."""
+    clipping (float32 [B]), applied clip scales (float32 [n_guards, B] per
+    group), ``num_clipped`` (int32 [1], or [G] per group), and per-group norms
+    ``{group: float32 [B]}`` with ``PerGroup`` clipping."""
 
     loss_values: torch.Tensor
     grad_norms: torch.Tensor
     clip_scales: torch.Tensor
     num_clipped: torch.Tensor
     batch_size: int
+    group_norms: dict | None = None
 
     @property
-    def clipping_rate(self) -> float:
+    def clipping_rate(self) -> float | None:
+        if self.group_norms is not None:
+            return None
         if self.batch_size == 0:
             return 0.0
-        return float(self.num_clipped.item()) / float(self.batch_size)
+        return float(self.num_clipped.sum().item()) / float(self.batch_size)
 
 
 class _Capture:
-    """Forward hook that keeps a linear layer's input and its (graph-attached) output."""
+    """Forward hook that keeps a linear layer's input, its (graph-attached)
+    output and the row segments the caller declared for this call."""
 
     def __init__(self, module: torch.nn.Linear):
         self.A = None
         self.out = None
+        self.segments = None
+        self.calls = 0
         self._handle = module.register_forward_hook(self._fwd)
 
     def _fwd(self, module, inputs, output):
+        self.calls += 1
         self.A = inputs[0].detach()
         self.out = output
+        seg = getattr(module, "dpc_row_segments", None)
+        self.segments = None if seg is None else [int(v) for v in seg]
 
     def remove(self):
         self._handle.remove()
@@ -83,6 +110,9 @@ def _linear_layers(model: torch.nn.Module):
             layers.append((name, mod))
             covered.add(id(mod.weight))
             if mod.bias is not None:
+                if not mod.bias.requires_grad:
+                    raise ConfigurationError(
+                        f"layer {name!r}: a frozen bias under a trainable weight is not supported")
                 covered.add(id(mod.bias))
     for pname, p in model.named_parameters():
         if p.requires_grad and id(p) not in covered:
@@ -101,11 +131,35 @@ def _as_btd(x: torch.Tensor, B: int) -> torch.Tensor:
     return x.reshape(B, -1, x.shape[-1])
 
 
+def _validate_bound(clipping_norm) -> None:
+    if isinstance(clipping_norm, PerGroup):
+        for gname, value in clipping_norm.values.items():
+            if value <= 0:
+                raise ConfigurationError(
+                    f"clipping_norm must be positive for all groups, got {value} for group "
+                    f"'{gname}'")
+        return
+    if isinstance(clipping_norm, bool) or not isinstance(clipping_norm, (int, float)):
+        raise InputTypeError(f"clipping_norm must be a float, got {type(clipping_norm)}")
+    if clipping_norm <= 0:
+        raise ConfigurationError(f"clipping_norm must be positive, got {clipping_norm}")
+
+
+@dataclass
+class _Layer:
+    name: str
+    mod: torch.nn.Linear
+    group: int
+    A: torch.Tensor  # dense [B, T, din]; segmented [rows, din]
+    G: torch.Tensor
+    segments: list | None = None
+
+
 def ghost_clipped_grad(
     model: torch.nn.Module,
     loss_fn,
     *,
-    clipping_norm: float,
+    clipping_norm,
     normalize_by: float = 1.0,
     return_aux: bool = False,
     dtype: torch.dtype | None = None,
@@ -113,17 +167,13 @@ def ghost_clipped_grad(
     """Create ``grad_fn(inputs, targets, *, state, noise_fn=None, noise_state=None)``.
 
     ``loss_fn(outputs, targets)`` must return per-example losses ``[B]``
-    (e.g. ``cross_entropy(..., reduction="none")``).  Without ``noise_fn`` the
+    (e.g. ``cross_entropy(..., reduction="none")``).  ``inputs`` is one tensor
+    or a tuple of positional arguments of ``model``.  Without ``noise_fn`` the
     call returns ``(ClippedPytree, state)``; with it, ``(NoisedPytree, state,
     noise_state')`` where the noise was fused into the clipped-sum epilogue.
     With ``return_aux`` the first element is ``(result, GhostGradAux)``.
     """
-    if isinstance(clipping_norm, PerGroup):
-        raise ConfigurationError("per-group clipping is not supported by ghost_clipped_grad")
-    if isinstance(clipping_norm, bool) or not isinstance(clipping_norm, (int, float)):
-        raise InputTypeError(f"clipping_norm must be a float, got {type(clipping_norm)}")
-    if clipping_norm <= 0:
-        raise ConfigurationError(f"clipping_norm must be positive, got {clipping_norm}")
+    _validate_bound(clipping_norm)
     if normalize_by <= 0.0:
         raise ConfigurationError(f"normalize_by must be > 0, got {normalize_by}.")
     layers = _linear_layers(model)
@@ -139,11 +189,41 @@ def ghost_clipped_grad(
     leaf_names.sort()
     leaf_index = {n: i for i, n in enumerate(leaf_names)}
 
+    # Clipping groups: one per PerGroup name (sorted), or a single group.
+    per_group = isinstance(clipping_norm, PerGroup)
+    if per_group:
+        group_names = sorted(clipping_norm.values)
+        keys = {param_path(n) for n in leaf_names}
+        mapped = set(clipping_norm.groups)
+        if keys != mapped:
+            missing = sorted(map(str, keys - mapped))
+            extra = sorted(map(str, mapped - keys))
+            raise ConfigurationError(
+                "PerGroup path keys must match the pytree tensor leaves exactly."
+                + (f" Leaves with no group assignment: {missing}." if missing else "")
+                + (f" Group paths with no matching leaf: {extra}." if extra else ""))
+        gidx = {n: k for k, n in enumerate(group_names)}
+        leaf_group = {n: gidx[clipping_norm.groups[param_path(n)]] for n in leaf_names}
+        bounds = [float(clipping_norm.values[n]) for n in group_names]
+    else:
+        group_names = None
+        leaf_group = dict.fromkeys(leaf_names, 0)
+        bounds = [float(clipping_norm)]
+    n_groups = len(bounds)
+    layer_group = {}
+    for name, mod in layers:
+        g = leaf_group[f"{name}.weight"]
+        if mod.bias is not None and leaf_group[f"{name}.bias"] != g:
+            raise ConfigurationError(
+                f"layer {name!r}: weight and bias must be in the same clipping group")
+        layer_group[name] = g
+
     def grad_fn(inputs, targets, *, state, noise_fn=None, noise_state=None):
         captures = [_Capture(mod) for _, mod in layers]
+        args = inputs if isinstance(inputs, tuple) else (inputs,)
         try:
             with record_function("opake::ghost_clipped_grad"), torch.enable_grad():
-                outputs = model(inputs)
+                outputs = model(*args)
                 losses = loss_fn(outputs, targets)
                 if losses.dim() != 1:
                     raise ConfigurationError("loss_fn must return per-example losses [B]")
@@ -151,6 +231,10 @@ def ghost_clipped_grad(
                 for (name, _), cap in zip(layers, captures):
                     if cap.out is None:
                         raise ConfigurationError(f"layer {name!r} was not used by the forward pass")
+                    if cap.calls != 1:
+                        raise ConfigurationError(
+                            f"layer {name!r} was called {cap.calls} times; ghost clipping needs "
+                            "one call per layer and step")
                 # Gradients with respect to the layer outputs only: autograd
                 # prunes the weight-gradient GEMMs, which the clipped sum replaces.
                 grads = torch.autograd.grad(losses.sum(), [c.out for c in captures],
@@ -158,36 +242,66 @@ def ghost_clipped_grad(
         finally:
             for c in captures:
                 c.remove()
-        pairs = []
+        dense, segmented = [], []
         for (name, mod), cap, g in zip(layers, captures, grads):
-            A = _as_btd(cap.A, B)
-            G = _as_btd(g.detach() if g is not None else torch.zeros_like(cap.out), B)
-            if A.dtype != G.dtype:
-                G = G.to(A.dtype)
-            pairs.append((name, mod, A.contiguous(), G.contiguous()))
-            cap.out = None
-
-        sq = None
-        for name, mod, A, G in pairs:
-            bias = mod.bias is not None
-            if A.shape[1] == 1:
-                sq = ops.flat_sqnorms(A[:, 0], G[:, 0], with_bias=bias, out=sq)
+            G = g.detach() if g is not None else torch.zeros_like(cap.out)
+            if cap.A.dtype != G.dtype:
+                G = G.to(cap.A.dtype)
+            if cap.segments is None:
+                layer = _Layer(name, mod, layer_group[name], _as_btd(cap.A, B).contiguous(),
+                               _as_btd(G, B).contiguous())
+                dense.append(layer)
             else:
-                sq = ops.gram_sqnorms(A, G, with_bias=bias, out=sq)
+                if mod.bias is not None:
+                    raise ConfigurationError(
+                        f"layer {name!r}: row-segmented layers with a bias are not supported")
+                if len(cap.segments) != B or sum(cap.segments) != cap.A.reshape(-1, cap.A.shape[-1]).shape[0]:
+                    raise ConfigurationError(
+                        f"layer {name!r}: dpc_row_segments must give B row counts that add up "
+                        "to the layer's input rows")
+                A2 = cap.A.reshape(-1, cap.A.shape[-1]).contiguous()
+                G2 = G.reshape(-1, G.shape[-1]).contiguous()
+                segmented.append(_Layer(name, mod, layer_group[name], A2, G2, cap.segments))
+            cap.out = None
+        device = losses.device
+
+        # Per-group, per-example squared norms.
+        sq = torch.zeros((n_groups, B), dtype=torch.float64, device=device)
+        for L in dense:
+            bias = L.mod.bias is not None
+            if L.A.shape[1] == 1:
+                ops.flat_sqnorms(L.A[:, 0], L.G[:, 0], with_bias=bias, out=sq[L.group])
+            else:
+                ops.gram_sqnorms(L.A, L.G, with_bias=bias, out=sq[L.group])
+        buckets = {}
+        for L in segmented:
+            key = (L.A.shape[1], L.G.shape[1], L.A.dtype)
+            buckets.setdefault(key, []).append(L)
+        bucket_layouts = []
+        for key, members in buckets.items():
+            layout = ops.SegmentLayout([L.segments for L in members], device)
+            seg_sq = ops.grouped_gram_sqnorms([L.A for L in members], [L.G for L in members],
+                                              layout)
+            for g in range(n_groups):
+                idx = [i for i, L in enumerate(members) if L.group == g]
+                if idx:
+                    sq[g] += seg_sq[idx].sum(dim=0)
+            bucket_layouts.append((members, layout))
 
         # Guards for the materialised leaves the reference would clip.
         sizes = []
-        for _, mod, _, _ in pairs:
+        for name, mod in layers:
             sizes.append(mod.weight.numel())
             if mod.bias is not None:
                 sizes.append(mod.bias.numel())
         roundoff = num.norm_roundoff(torch.float32, torch.float64, len(sizes),
                                      num.reduction_terms(sizes))
-        storage = sorted({A.dtype for _, _, A, _ in pairs}, key=str)
+        storage = sorted({L.A.dtype for L in dense + segmented}, key=str)
         guards = [num.guard_constants(dt, torch.promote_types(dt, torch.float32), roundoff)
                   for dt in storage]
-        cf = ops.clip_factors(sq, num.conservative_bound(clipping_norm), guards,
-                              count_threshold=num.float32_of(clipping_norm))
+        cfs = [ops.clip_factors(sq[g], num.conservative_bound(bounds[g]), guards,
+                                count_threshold=num.float32_of(bounds[g]))
+               for g in range(n_groups)]
 
         std = 0.0
         gen = None
@@ -197,57 +311,110 @@ def ghost_clipped_grad(
             if noise_state is None:
                 raise ConfigurationError("noise_state is required with noise_fn")
             std = noise_fn.clipped_stddev(clipped(None, max_norm=max_norm))
-            if std != 0.0 and noise_fn.compute_dtype != torch.float32:
+            noisy = any((std.for_path(param_path(n)) if isinstance(std, PerGroup) else std) != 0.0
+                        for n in leaf_names)
+            if noisy and noise_fn.compute_dtype != torch.float32:
                 raise ConfigurationError("fused noise supports compute_dtype float32 only")
             step_key = step_key_for(noise_state)
-            if std != 0.0 and noise_fn.stream == "reference":
+            if noisy and noise_fn.stream == "reference":
                 gen = generator_from_key(step_key)
             next_noise_state = GaussianNoiseState(
                 _step_counter=noise_state._step_counter + 1, _rng_key=noise_state._rng_key)
 
-        # Reference-stream draws, one generator, flatten order.
+        def leaf_std(leaf: str) -> float:
+            if isinstance(std, PerGroup):
+                return float(std.for_path(param_path(leaf)))
+            return float(std)
+
+        # Reference-stream draws: one generator, flatten order, no draw for a
+        # leaf whose standard deviation is 0.
         draws = {}
         if gen is not None:
             shapes = {}
-            for name, mod, _, _ in pairs:
+            for name, mod in layers:
                 shapes[f"{name}.weight"] = tuple(mod.weight.shape)
                 if mod.bias is not None:
                     shapes[f"{name}.bias"] = tuple(mod.bias.shape)
             for leaf in leaf_names:
-                draws[leaf] = torch.randn(shapes[leaf], dtype=torch.float32, generator=gen)
+                if leaf_std(leaf) != 0.0:
+                    draws[leaf] = torch.randn(shapes[leaf], dtype=torch.float32, generator=gen)
+
+        def to_dev(t):
+            return t.pin_memory().to(device, non_blocking=True)
 
         tree = {}
-        for name, mod, A, G in pairs:
-            si = storage.index(A.dtype)
+        for L in dense:
+            si = storage.index(L.A.dtype)
+            cf = cfs[L.group]
+            wn, bn = f"{L.name}.weight", f"{L.name}.bias"
             spec = None
-            if std != 0.0:
-                wn, bn = f"{name}.weight", f"{name}.bias"
+            s_w = leaf_std(wn) if noise_fn is not None else 0.0
+            s_b = leaf_std(bn) if (noise_fn is not None and L.mod.bias is not None) else s_w
+            if s_w != s_b:
+                raise ConfigurationError(
+                    f"layer {L.name!r}: weight and bias noise must share a standard deviation")
+            if s_w != 0.0:
                 if gen is not None:
-                    dev = A.device
                     spec = ops.NoiseSpec(
-                        sigma=std, mode=nat.NOISE_INJECTED,
-                        noise=draws[wn].pin_memory().to(dev, non_blocking=True),
-                        bias_noise=(draws[bn].pin_memory().to(dev, non_blocking=True)
-                                    if mod.bias is not None else None))
+                        sigma=s_w, mode=nat.NOISE_INJECTED, noise=to_dev(draws[wn]),
+                        bias_noise=to_dev(draws[bn]) if L.mod.bias is not None else None)
                 else:
-                    spec = ops.NoiseSpec(sigma=std, mode=nat.NOISE_PHILOX, seed=step_key.seed,
+                    spec = ops.NoiseSpec(sigma=s_w, mode=nat.NOISE_PHILOX, seed=step_key.seed,
                                          leaf_id=leaf_index[wn],
                                          bias_leaf_id=leaf_index.get(bn, 0))
-            w, b = ops.clipped_sum(A, G, cf.scale[si], plan=cf.plan if len(storage) == 1 else None,
+            w, b = ops.clipped_sum(L.A, L.G, cf.scale[si],
+                                   plan=cf.plan if len(storage) == 1 else None,
                                    normalize_by=normalize_by, noise=spec,
-                                   out_dtype=dtype or mod.weight.dtype,
-                                   with_bias=mod.bias is not None)
-            tree[f"{name}.weight"] = w
-            if mod.bias is not None:
-                tree[f"{name}.bias"] = b
+                                   out_dtype=dtype or L.mod.weight.dtype,
+                                   with_bias=L.mod.bias is not None)
+            tree[wn] = w
+            if L.mod.bias is not None:
+                tree[bn] = b
+        for members, layout in bucket_layouts:
+            si = storage.index(members[0].A.dtype)
+            seg_scale = torch.stack([cfs[L.group].scale[si] for L in members])
+            names = [f"{L.name}.weight" for L in members]
+            sigmas = [leaf_std(n) if noise_fn is not None else 0.0 for n in names]
+            gnoise = None
+            if any(s != 0.0 for s in sigmas):
+                if gen is not None:
+                    zero = None
+                    noise = []
+                    for n, L in zip(names, members):
+                        if n in draws:
+                            noise.append(to_dev(draws[n]))
+                        else:
+                            if zero is None:
+                                zero = torch.zeros(tuple(L.mod.weight.shape), dtype=torch.float32,
+                                                   device=device)
+                            noise.append(zero)
+                    gnoise = ops.GroupedNoise(sigmas=sigmas, mode=nat.NOISE_INJECTED, noise=noise)
+                else:
+                    gnoise = ops.GroupedNoise(sigmas=sigmas, mode=nat.NOISE_PHILOX,
+                                              seed=step_key.seed,
+                                              leaf_ids=[leaf_index[n] for n in names])
+            out_dtype = dtype or members[0].mod.weight.dtype
+            stacked = ops.grouped_clipped_sum([L.A for L in members], [L.G for L in members],
+                                              layout, seg_scale, normalize_by=normalize_by,
+                                              noise=gnoise, out_dtype=out_dtype)
+            for i, n in enumerate(names):
+                tree[n] = stacked[i]
         tree = {k: tree[k] for k in leaf_names}
         if noise_fn is None:
             result = clipped(tree, max_norm=max_norm)
         else:
             result = NoisedPytree(pytree=tree, max_norm=max_norm, noise_stddev=std)
         if return_aux:
-            aux = GhostGradAux(loss_values=losses.detach(), grad_norms=cf.norms,
-                               clip_scales=cf.scale, num_clipped=cf.nclipped, batch_size=B)
+            total = sq.sum(dim=0) if n_groups > 1 else sq[0]
+            group_norms = None
+            if per_group:
+                group_norms = {n: cfs[k].norms for k, n in enumerate(group_names)}
+            aux = GhostGradAux(
+                loss_values=losses.detach(),
+                grad_norms=torch.sqrt(total).to(torch.float32) if per_group else cfs[0].norms,
+                clip_scales=torch.stack([cf.scale for cf in cfs]) if per_group else cfs[0].scale,
+                num_clipped=torch.cat([cf.nclipped for cf in cfs]),
+                batch_size=B, group_norms=group_norms)
             result = (result, aux)
         if noise_fn is None:
             return result, state

@@ -175,13 +175,9 @@ __device__ __forceinline__ bf16x8_t join_frag(i16x4_t lo, i16x4_t hi) {
   return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-// blockIdx -> (tile_m, tile_n): contiguous id ranges per XCD (hardware
-// dispatch is round-robin over the 8 XCDs), then GROUP_M-ordered tiles so a
-// group of tile rows shares the activation tiles.
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int* tm, int* tn) {
-  const int ntiles = tiles_m * tiles_n;
-  int lin = blockIdx.x;
-  if (ntiles % 8 == 0) lin = (lin % 8) * (ntiles / 8) + lin / 8;
+// Linear workgroup id -> (tile_m, tile_n) in GROUP_M order, so a group of
+// tile rows shares the activation tiles.
+__device__ __forceinline__ void tile_coords(int lin, int tiles_m, int tiles_n, int* tm, int* tn) {
   constexpr int kGroupM = 4;
   const int per_group = kGroupM * tiles_n;
   const int group = lin / per_group;
@@ -192,13 +188,41 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int* tm, i
   *tn = in_group / gsize;
 }
 
+// Hardware dispatch is round-robin over the 8 XCDs: give each XCD a
+// contiguous range of linear ids, so it re-reads operand tiles from its own L2.
+__device__ __forceinline__ int xcd_linear_id(int nblocks) {
+  const int b = blockIdx.x;
+  return (nblocks % 8 == 0) ? (b % 8) * (nblocks / 8) + b / 8 : b;
+}
+
+// Grouped mode: E independent problems of one shape (dout x din), e.g. the
+// same layer of E experts.  Problem e reads rows of A_e / G_e (rows[e] rows
+// each) in 64-row K steps taken from a step table: entry (row0, seg << 7 |
+// valid) covers rows row0 .. row0 + valid - 1 of segment seg, whose clip
+// scale is seg_scale[seg]; rows past `valid` read as zero.  Problem e's steps
+// are entries step_start[e] .. step_start[e + 1] - 1.
+struct GroupedTables {
+  const int64_t* a_ptrs;
+  const int64_t* g_ptrs;
+  const int32_t* rows;
+  const int32_t* steps;
+  const int32_t* step_start;
+  const float* seg_scale;
+  const int64_t* out_ptrs;
+  const int64_t* noise_ptrs;  // nullable
+  const uint32_t* leaf_ids;
+  const float* sigmas;
+  int E;
+};
+
 struct FastArgs {
-  const uint16_t* A;  // [B * T, N]
+  const uint16_t* A;  // [B * T, N] (dense mode)
   const uint16_t* G;  // [B * T, M]
   int T, B;
   const void* plan;
   const float* scale;
   Epilogue ep;
+  GroupedTables grp;
 };
 
 // Per-lane LDS offsets of the transposing fragment reads.  For a 32 x 16
@@ -230,21 +254,55 @@ constexpr int kGLdsBytes = (2 * kOperandBytes > kQuarterRows * kEpiLd * 4)
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 
+template <bool kGrouped>
 __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastArgs args) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_g[kGLdsBytes];
   __shared__ __attribute__((aligned(16))) uint8_t lds_a0[kOperandBytes];
   __shared__ __attribute__((aligned(16))) uint8_t lds_a1[kOperandBytes];
   const int M = args.ep.M, N = args.ep.N, T = args.T;
+  const int tiles_m = ceil_div(M, kBM), tiles_n = ceil_div(N, kBN);
+  int lin = xcd_linear_id(gridDim.x);
+  int grp = 0;
+  if (kGrouped) {
+    grp = lin / (tiles_m * tiles_n);
+    lin -= grp * tiles_m * tiles_n;
+  }
   int tm, tn;
-  tile_coords(ceil_div(M, kBM), ceil_div(N, kBN), &tm, &tn);
+  tile_coords(lin, tiles_m, tiles_n, &tm, &tn);
   const int m0 = tm * kBM, n0 = tn * kBN;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wm = w >> 2, wn = w & 3;  // wave tile: rows wm * 128 of G^T, wn * 64 of A
 
-  ClipPlanView plan = clip_plan_view(const_cast<void*>(args.plan), args.B);
-  const int nactive = *plan.nactive;
+  Epilogue ep = args.ep;
+  const uint16_t* Abase = args.A;
+  const uint16_t* Gbase = args.G;
+  int total_rows, nsteps, step0 = 0, nactive = 0;
   const int spe = T / kBK;
-  const int nsteps = nactive * spe;
+  ClipPlanView plan = clip_plan_view(const_cast<void*>(args.plan), args.B);
+  if (kGrouped) {
+    Abase = reinterpret_cast<const uint16_t*>(args.grp.a_ptrs[grp]);
+    Gbase = reinterpret_cast<const uint16_t*>(args.grp.g_ptrs[grp]);
+    total_rows = args.grp.rows[grp];
+    step0 = args.grp.step_start[grp];
+    nsteps = args.grp.step_start[grp + 1] - step0;
+    ep.out = reinterpret_cast<void*>(args.grp.out_ptrs[grp]);
+    if (args.grp.noise_ptrs) ep.noise = reinterpret_cast<const float*>(args.grp.noise_ptrs[grp]);
+    ep.leaf = args.grp.leaf_ids[grp];
+    ep.sigma = ep.noise_mode == DPC_NOISE_NONE ? 0.0f : args.grp.sigmas[grp];
+    // Rows past a step's `valid` are fetched out of range (zero in the G tile);
+    // the A tile starts from zeros so that whatever such a fetch leaves in LDS
+    // is finite.
+    const u32x4_t zero = {0u, 0u, 0u, 0u};
+    for (int i = tid * 16; i < kOperandBytes; i += kFastThreads * 16) {
+      *reinterpret_cast<u32x4_t*>(lds_a0 + i) = zero;
+      *reinterpret_cast<u32x4_t*>(lds_a1 + i) = zero;
+    }
+    __syncthreads();
+  } else {
+    nactive = *plan.nactive;
+    nsteps = nactive * spe;
+    total_rows = args.B * T;
+  }
 
   f32x16_t acc[4][2];
 #pragma unroll
@@ -253,27 +311,35 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
 
   if (nsteps > 0) {
-    const int total_rows = args.B * T;
     __amdgpu_buffer_rsrc_t g_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(args.G), (short)0, total_rows * M * 2, 0x00020000);
+        const_cast<uint16_t*>(Gbase), (short)0, total_rows * M * 2, 0x00020000);
     __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(args.A), (short)0, total_rows * N * 2, 0x00020000);
+        const_cast<uint16_t*>(Abase), (short)0, total_rows * N * 2, 0x00020000);
 
     // The clip plan, 64 entries at a time in registers: lane l holds slot
-    // base + l (example index and scale).  A step reads its slot with
+    // base + l (dense: example index and scale; grouped: the step's first
+    // row, segment/valid word and scale).  A step reads its slot with
     // v_readlane, so the K loop issues no memory operations besides the
     // operand loads.
-    int plan_base = -64, plan_ex = 0;
+    int plan_base = -64, plan_ex = 0, plan_pack = 0;
     float plan_sc = 0.0f;
     auto refill_plan = [&](int slot) __attribute__((always_inline)) {
       plan_base = slot & ~63;
       const int sl = plan_base + lane;
-      plan_ex = sl < nactive ? plan.active[sl] : 0;
-      plan_sc = sl < nactive ? args.scale[plan_ex] : 0.0f;
+      if (kGrouped) {
+        const bool in = sl < nsteps;
+        plan_ex = in ? args.grp.steps[2 * (step0 + sl)] : 0;
+        plan_pack = in ? args.grp.steps[2 * (step0 + sl) + 1] : 0;
+        plan_sc = in ? args.grp.seg_scale[plan_pack >> 7] : 0.0f;
+      } else {
+        plan_ex = sl < nactive ? plan.active[sl] : 0;
+        plan_sc = sl < nactive ? args.scale[plan_ex] : 0.0f;
+      }
     };
-    // Step t covers rows [active[t / spe] * T + (t % spe) * 64, +64).
-    auto step_row0 = [&](int t, float* sc) __attribute__((always_inline)) {
-      const int slot = t / spe;
+    // Dense: step t covers rows [active[t / spe] * T + (t % spe) * 64, +64).
+    // Grouped: step t is table entry step0 + t.
+    auto step_row0 = [&](int t, float* sc, int* valid) __attribute__((always_inline)) {
+      const int slot = kGrouped ? t : t / spe;
       if (slot - plan_base >= 64) {
         refill_plan(slot);
         DPC_WAIT_VMCNT(0);  // keep the loop's memory-counter accounting exact
@@ -281,6 +347,11 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
       const int ex = __builtin_amdgcn_readlane(plan_ex, slot - plan_base);
       *sc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
                                           __builtin_bit_cast(int, plan_sc), slot - plan_base));
+      if (kGrouped) {
+        *valid = __builtin_amdgcn_readlane(plan_pack, slot - plan_base) & 127;
+        return ex;
+      }
+      *valid = kBK;
       return ex * T + (t % spe) * kBK;
     };
 
@@ -292,9 +363,10 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
     const int g_voff = (m0 + col) * 2;
     const int g_bad = (m0 + col < M) ? 0 : kOutOfRange;
     u32x4_t g[4];
-    auto load_chunk = [&](int row0, int j) __attribute__((always_inline)) {
+    auto load_chunk = [&](int row0, int valid, int j) __attribute__((always_inline)) {
       const int row = row0 + r0;
-      g[j] = __builtin_amdgcn_raw_buffer_load_b128(g_rsrc, (row * M * 2 + g_voff) | g_bad,
+      const int bad = (kGrouped && r0 + 16 * j >= valid) ? kOutOfRange : g_bad;
+      g[j] = __builtin_amdgcn_raw_buffer_load_b128(g_rsrc, (row * M * 2 + g_voff) | bad,
                                                    j * 16 * M * 2, 0);
     };
     auto store_chunk = [&](uint8_t* gstage, int j, float sc) __attribute__((always_inline)) {
@@ -305,21 +377,23 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
     // i the 16 bytes at i * 16 -- row (w * 4 + j) * 2 + i / 32, physical
     // 16-byte slot i % 32, which holds logical columns
     // (((i % 32) / 4) ^ (row & 7)) * 32 + (i % 4) * 8.
-    int dma_voff[4], dma_bad[4];
+    int dma_voff[4], dma_bad[4], dma_row[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int row = (w * 4 + j) * 2 + (lane >> 5);
       const int slot = lane & 31;
       const int acol = (((slot >> 2) ^ (row & 7)) << 5) + (slot & 3) * 8;
+      dma_row[j] = row;
       dma_voff[j] = row * N * 2 + (n0 + acol) * 2;
       dma_bad[j] = (n0 + acol < N) ? 0 : kOutOfRange;
     }
-    auto dma_a = [&](uint8_t* astage, int row0) __attribute__((always_inline)) {
+    auto dma_a = [&](uint8_t* astage, int row0, int valid) __attribute__((always_inline)) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
+        const int bad = (kGrouped && dma_row[j] >= valid) ? kOutOfRange : dma_bad[j];
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             a_rsrc, (__attribute__((address_space(3))) void*)((lds_u8_t*)astage + (w * 4 + j) * 1024),
-            16, (row0 * N * 2 + dma_voff[j]) | dma_bad[j], 0, 0, 0);
+            16, (row0 * N * 2 + dma_voff[j]) | bad, 0, 0, 0);
       }
     };
 
@@ -365,35 +439,37 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
     // step's (in-range) rows into the unused stage: every path issues the same
     // memory operations, which keeps the counter waits exact.
     float sc_next = 0.0f;
-    int row_next = 0;
+    int row_next = 0, valid_next = kBK;
     auto k_step = [&](int s, const uint8_t* gcur, const uint8_t* acur, uint8_t* gnxt,
                       uint8_t* anxt) __attribute__((always_inline)) {
-      dma_a(anxt, row_next);
+      dma_a(anxt, row_next, valid_next);
       float sc_after;
-      const int row2 = step_row0(min(s + 2, nsteps - 1), &sc_after);
+      int valid2;
+      const int row2 = step_row0(min(s + 2, nsteps - 1), &sc_after, &valid2);
       Frags f0, f1;
       read_frags(gcur, acur, 0, f0);
       read_frags(gcur, acur, 1, f1);
       mma(f0);
       store_chunk(gnxt, 0, sc_next);
-      load_chunk(row2, 0);
+      load_chunk(row2, valid2, 0);
       __builtin_amdgcn_sched_barrier(0);
       read_frags(gcur, acur, 2, f0);
       mma(f1);
       store_chunk(gnxt, 1, sc_next);
-      load_chunk(row2, 1);
+      load_chunk(row2, valid2, 1);
       __builtin_amdgcn_sched_barrier(0);
       read_frags(gcur, acur, 3, f1);
       mma(f0);
       store_chunk(gnxt, 2, sc_next);
-      load_chunk(row2, 2);
+      load_chunk(row2, valid2, 2);
       __builtin_amdgcn_sched_barrier(0);
       mma(f1);
       store_chunk(gnxt, 3, sc_next);
-      load_chunk(row2, 3);
+      load_chunk(row2, valid2, 3);
       __builtin_amdgcn_sched_barrier(0);
       sc_next = sc_after;
       row_next = row2;
+      valid_next = valid2;
       DPC_WAIT_VMCNT(4);
       __syncthreads();
     };
@@ -402,15 +478,16 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
     uint8_t* g1 = lds_g + kOperandBytes;
     // Prologue: step 0 into stage 0 (A by DMA, G through registers), step 1
     // of G into the registers.
-    int row0 = step_row0(0, &sc_next);
-    dma_a(lds_a0, row0);
+    int valid0;
+    int row0 = step_row0(0, &sc_next, &valid0);
+    dma_a(lds_a0, row0, valid0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) load_chunk(row0, j);
+    for (int j = 0; j < 4; ++j) load_chunk(row0, valid0, j);
 #pragma unroll
     for (int j = 0; j < 4; ++j) store_chunk(g0, j, sc_next);
-    row_next = step_row0(min(1, nsteps - 1), &sc_next);
+    row_next = step_row0(min(1, nsteps - 1), &sc_next, &valid_next);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) load_chunk(row_next, j);
+    for (int j = 0; j < 4; ++j) load_chunk(row_next, valid_next, j);
     DPC_WAIT_VMCNT(4);  // the A DMA of step 0 has landed (4 G loads may be in flight)
     __syncthreads();
     int s = 0;
@@ -453,7 +530,7 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
       const float2 t0 = *reinterpret_cast<const float2*>(tile + ml * kEpiLd + cl);
       const float2 t1 = *reinterpret_cast<const float2*>(tile + (ml + 1) * kEpiLd + cl);
       const float v[2][2] = {{t0.x, t0.y}, {t1.x, t1.y}};
-      emit_quad(args.ep, m0 + quarter * kQuarterRows + ml, n0 + cl, v);
+      emit_quad(ep, m0 + quarter * kQuarterRows + ml, n0 + cl, v);
     }
     __syncthreads();
   }
@@ -566,7 +643,218 @@ bias_finish_kernel(const float* __restrict__ partial, int nsplit, Epilogue ep) {
   emit_pair(ep, m, 0, v0, v1);
 }
 
+// Grouped generic path (float32, or bf16 of any shape): problem blockIdx.z,
+// 64 x 64 output tiles, the steps of the problem walked row by row.
+template <typename In>
+__global__ void __launch_bounds__(kThreads)
+grouped_generic_kernel(GroupedTables grp, Epilogue ep0) {
+  __shared__ float sg[kGK][kGT + 1];
+  __shared__ float sa[kGK][kGT + 1];
+  const int e = blockIdx.z;
+  Epilogue ep = ep0;
+  ep.out = reinterpret_cast<void*>(grp.out_ptrs[e]);
+  if (grp.noise_ptrs) ep.noise = reinterpret_cast<const float*>(grp.noise_ptrs[e]);
+  ep.leaf = grp.leaf_ids[e];
+  ep.sigma = ep.noise_mode == DPC_NOISE_NONE ? 0.0f : grp.sigmas[e];
+  const In* A = reinterpret_cast<const In*>(grp.a_ptrs[e]);
+  const In* G = reinterpret_cast<const In*>(grp.g_ptrs[e]);
+  const int M = ep.M, N = ep.N;
+  const int m0 = blockIdx.y * kGT, n0 = blockIdx.x * kGT;
+  const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+  const int s0 = grp.step_start[e], s1 = grp.step_start[e + 1];
+  for (int st = s0; st < s1; ++st) {
+    const int row0 = grp.steps[2 * st];
+    const int pack = grp.steps[2 * st + 1];
+    const int valid = pack & 127;
+    const float sc = grp.seg_scale[pack >> 7];
+    for (int k0 = 0; k0 < valid; k0 += kGK) {
+      for (int x = tid; x < kGK * kGT; x += kThreads) {
+        const int k = x / kGT, col = x % kGT;
+        float gv = 0.f, av = 0.f;
+        if (k0 + k < valid) {
+          const size_t row = (size_t)(row0 + k0 + k);
+          if (m0 + col < M) gv = sc * to_f32<In>(G[row * M + m0 + col]);
+          if (n0 + col < N) av = to_f32<In>(A[row * N + n0 + col]);
+        }
+        sg[k][col] = gv;
+        sa[k][col] = av;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < kGK; ++k) {
+        float a[4], b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          a[i] = sg[k][tr * 4 + i];
+          b[i] = sa[k][tc * 4 + i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+      }
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + tc * 4 + j;
+#pragma unroll
+    for (int i = 0; i < 4; i += 2) emit_pair(ep, m0 + tr * 4 + i, n, acc[i][j], acc[i + 1][j]);
+  }
+}
+
+// Step table of the grouped clipped sum: segments with a positive scale, in
+// segment order, cut into 64-row steps; group e's steps start at
+// step_start[e] (segments must be sorted by group).
+constexpr int kPlanThreads = 256;
+constexpr int kMaxPlanGroups = 4096;
+
+__global__ void __launch_bounds__(kPlanThreads)
+segment_plan_kernel(const int32_t* __restrict__ seg_row0, const int32_t* __restrict__ seg_len,
+                    const int32_t* __restrict__ seg_group, const float* __restrict__ seg_scale,
+                    int S, int E, int max_steps, int32_t* __restrict__ steps,
+                    int32_t* __restrict__ step_start) {
+  __shared__ int gcount[kMaxPlanGroups];
+  __shared__ int wave_total[kPlanThreads / 64];
+  __shared__ int base;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int g = tid; g < E; g += kPlanThreads) gcount[g] = 0;
+  if (tid == 0) base = 0;
+  __syncthreads();
+  for (int start = 0; start < S; start += kPlanThreads) {
+    const int v = start + tid;
+    int cnt = 0;
+    if (v < S && seg_scale[v] > 0.0f && seg_len[v] > 0) cnt = ceil_div(seg_len[v], kBK);
+    int incl = cnt;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    if (lane == 63) wave_total[w] = incl;
+    __syncthreads();
+    int pos = base + incl - cnt;
+    for (int u = 0; u < w; ++u) pos += wave_total[u];
+    for (int j = 0; j < cnt; ++j) {
+      const int idx = pos + j;
+      if (idx < max_steps) {
+        steps[2 * idx] = seg_row0[v] + j * kBK;
+        steps[2 * idx + 1] = (v << 7) | min(kBK, seg_len[v] - j * kBK);
+      }
+    }
+    if (cnt > 0) atomicAdd(&gcount[min(max(seg_group[v], 0), E - 1)], cnt);
+    __syncthreads();
+    if (tid == 0) {
+      int total = 0;
+      for (int u = 0; u < kPlanThreads / 64; ++u) total += wave_total[u];
+      base += total;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    int acc = 0;
+    for (int g = 0; g < E; ++g) {
+      step_start[g] = min(acc, max_steps);
+      acc += gcount[g];
+    }
+    step_start[E] = min(acc, max_steps);
+  }
+}
+
 }  // namespace
+
+extern "C" int dpc_segment_plan(const int32_t* seg_row0, const int32_t* seg_len,
+                                const int32_t* seg_group, const float* seg_scale, int S, int E,
+                                int max_steps, int32_t* steps, int32_t* step_start, void* stream) {
+  if (S < 0 || E < 1 || max_steps < 0) return DPC_EINVAL;
+  if (E > kMaxPlanGroups || S >= (1 << 24)) return DPC_ENOTSUP;
+  if (!step_start || (S > 0 && (!seg_row0 || !seg_len || !seg_group || !seg_scale)) ||
+      (max_steps > 0 && !steps))
+    return DPC_EINVAL;
+  hipLaunchKernelGGL(segment_plan_kernel, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream,
+                     seg_row0, seg_len, seg_group, seg_scale, S, E, max_steps, steps, step_start);
+  DPC_HIP_CHECK(hipGetLastError());
+  return DPC_OK;
+}
+
+extern "C" int dpc_grouped_clipped_sum(const int64_t* a_ptrs, const int64_t* g_ptrs,
+                                       const int32_t* rows, int max_rows, int E, int din, int dout,
+                                       int dtype, const int32_t* steps, const int32_t* step_start,
+                                       const float* seg_scale, double normalize_by, int noise_mode,
+                                       const int64_t* noise_ptrs, uint64_t seed,
+                                       const uint32_t* leaf_ids, const float* sigmas,
+                                       int out_dtype, const int64_t* out_ptrs, void* stream) {
+  if (E < 0 || max_rows < 0 || din <= 0 || dout <= 0) return DPC_EINVAL;
+  if (dtype != DPC_F32 && dtype != DPC_BF16) return DPC_EINVAL;
+  if (out_dtype != DPC_F32 && out_dtype != DPC_BF16) return DPC_EINVAL;
+  if (!(normalize_by > 0.0)) return DPC_EINVAL;
+  if (noise_mode < DPC_NOISE_NONE || noise_mode > DPC_NOISE_PHILOX) return DPC_EINVAL;
+  if (E == 0) return DPC_OK;
+  if (!a_ptrs || !g_ptrs || !rows || !step_start || !seg_scale || !leaf_ids || !sigmas ||
+      !out_ptrs || !steps)
+    return DPC_EINVAL;
+  if (noise_mode == DPC_NOISE_INJECTED && !noise_ptrs) return DPC_EINVAL;
+  if (E > 65535) return DPC_ENOTSUP;
+  hipStream_t s = (hipStream_t)stream;
+  Epilogue ep;
+  ep.M = dout;
+  ep.N = din;
+  ep.nb = (float)normalize_by;
+  ep.apply_nb = normalize_by != 1.0;
+  ep.noise_mode = noise_mode;
+  ep.noise = nullptr;
+  ep.seed = seed;
+  ep.leaf = 0;
+  ep.sigma = 0.0f;
+  ep.out_bf16 = out_dtype == DPC_BF16;
+  ep.out = nullptr;
+  GroupedTables grp;
+  grp.a_ptrs = a_ptrs;
+  grp.g_ptrs = g_ptrs;
+  grp.rows = rows;
+  grp.steps = steps;
+  grp.step_start = step_start;
+  grp.seg_scale = seg_scale;
+  grp.out_ptrs = out_ptrs;
+  grp.noise_ptrs = noise_mode == DPC_NOISE_INJECTED ? noise_ptrs : nullptr;
+  grp.leaf_ids = leaf_ids;
+  grp.sigmas = sigmas;
+  grp.E = E;
+  // Buffer offsets are 32-bit, and a row past a step's end is fetched at an
+  // offset >= kOutOfRange: each problem's operands must stay below that.
+  const size_t dmax = (size_t)(din > dout ? din : dout);
+  const bool fits = (size_t)max_rows * dmax * 2 < (size_t)kOutOfRange;
+  const bool fast = dtype == DPC_BF16 && din % 8 == 0 && dout % 8 == 0 && fits;
+  if (fast) {
+    FastArgs args;
+    args.A = nullptr;
+    args.G = nullptr;
+    args.T = 0;
+    args.B = 0;
+    args.plan = nullptr;
+    args.scale = nullptr;
+    args.ep = ep;
+    args.grp = grp;
+    const long long ntiles = (long long)ceil_div(dout, kBM) * ceil_div(din, kBN) * E;
+    if (ntiles > 0x7fffffff) return DPC_ENOTSUP;
+    hipLaunchKernelGGL(clipped_sum_bf16_kernel<true>, dim3((unsigned)ntiles), dim3(kFastThreads),
+                       0, s, args);
+  } else {
+    dim3 grid(ceil_div(din, kGT), ceil_div(dout, kGT), E);
+    if (dtype == DPC_BF16) {
+      hipLaunchKernelGGL(grouped_generic_kernel<uint16_t>, grid, dim3(kThreads), 0, s, grp, ep);
+    } else {
+      hipLaunchKernelGGL(grouped_generic_kernel<float>, grid, dim3(kThreads), 0, s, grp, ep);
+    }
+  }
+  DPC_HIP_CHECK(hipGetLastError());
+  return DPC_OK;
+}
 
 extern "C" size_t dpc_clipped_sum_workspace_bytes(int B, int T, int din, int dout, int dtype) {
   (void)B;
@@ -627,7 +915,7 @@ extern "C" int dpc_clipped_sum(const void* A, const void* G, const float* scale,
     args.scale = scale;
     args.ep = ep;
     const int ntiles = ceil_div(dout, kBM) * ceil_div(din, kBN);
-    hipLaunchKernelGGL(clipped_sum_bf16_kernel, dim3(ntiles), dim3(kFastThreads), 0, s, args);
+    hipLaunchKernelGGL(clipped_sum_bf16_kernel<false>, dim3(ntiles), dim3(kFastThreads), 0, s, args);
   } else {
     dim3 grid(ceil_div(din, kGT), ceil_div(dout, kGT));
     if (dtype == DPC_BF16) {

@@ -129,20 +129,44 @@ __device__ __forceinline__ void gram_mma(const uint8_t* tp, const uint8_t* tq, i
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
 }
 
+// Grouped mode: work item l is (problem, first row, rows, pair) -- the tile
+// pair `pair` of the rows-long segment starting at `first row` of problem
+// `problem`'s operands (a_ptrs / g_ptrs); rows past the segment read as zero.
+struct GramItems {
+  const int32_t* items;  // [n_items][4]
+  const int64_t* a_ptrs;
+  const int64_t* g_ptrs;
+};
+
+template <bool kGrouped>
 __global__ void __launch_bounds__(kGramMfmaThreads, 2)
 gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ G, int T,
-                      int din, int dout, int npairs, int nblocks, double* __restrict__ partial) {
+                      int din, int dout, int npairs, int nblocks, double* __restrict__ partial,
+                      GramItems work) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kGStageBytes];
   __shared__ double red[kGramMfmaThreads / 64];
   const int l = xcd_logical_block(gridDim.x, nblocks);
   if (l < 0) return;  // padding workgroup: exits before any barrier
-  const int ex = l / npairs, pair = l % npairs;
+  const uint16_t* Xa;
+  const uint16_t* Xg;
+  int pair;
+  if (kGrouped) {
+    const int32_t* it = work.items + 4 * (size_t)l;
+    const int problem = it[0], row0 = it[1];
+    T = it[2];
+    pair = it[3];
+    Xa = reinterpret_cast<const uint16_t*>(work.a_ptrs[problem]) + (size_t)row0 * din;
+    Xg = reinterpret_cast<const uint16_t*>(work.g_ptrs[problem]) + (size_t)row0 * dout;
+  } else {
+    const int ex = l / npairs;
+    pair = l % npairs;
+    Xa = A + (size_t)ex * T * din;
+    Xg = G + (size_t)ex * T * dout;
+  }
   int p, q;
   pair_from_index(pair, &p, &q);
   const bool diag = (p == q);
 
-  const uint16_t* Xa = A + (size_t)ex * T * din;
-  const uint16_t* Xg = G + (size_t)ex * T * dout;
   const GramOperand ap = make_operand(Xa, T, din, p * kGramTile);
   const GramOperand aq = make_operand(Xa, T, din, q * kGramTile);
   const GramOperand gp = make_operand(Xg, T, dout, p * kGramTile);
@@ -223,9 +247,7 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
 #pragma unroll
       for (int r = 0; r < 16; ++r) sum += (double)pa[i][j][r] * (double)pg[i][j][r];
   double total = block_sum_f64(sum, red);
-  if (threadIdx.x == 0) {
-    partial[(size_t)ex * npairs + pair] = diag ? total : 2.0 * total;
-  }
+  if (threadIdx.x == 0) partial[l] = diag ? total : 2.0 * total;  // dense: l = ex * npairs + pair
 }
 
 // Generic path (float32 inputs, or bf16 with d % 8 != 0): 64 x 64 tiles,
@@ -296,6 +318,47 @@ gram_generic_kernel(const In* __restrict__ A, const In* __restrict__ G, int T, i
     for (int j = 0; j < 4; ++j) s += (double)pa[i][j] * (double)pg[i][j];
   double total = block_sum_f64(s, red);
   if (threadIdx.x == 0) partial[(size_t)ex * npairs + pair] = (p == q) ? total : 2.0 * total;
+}
+
+// Grouped generic path: one 128-row tile pair (P, Q) as its four 64-row
+// sub-tile pairs; the inner products of the sub-tiles add up to the pair's.
+template <typename In>
+__global__ void __launch_bounds__(kGramThreads)
+gram_grouped_generic_kernel(GramItems work, int din, int dout, double* __restrict__ partial) {
+  __shared__ float sp[kGenK][kGenTile + 1];
+  __shared__ float sq[kGenK][kGenTile + 1];
+  __shared__ double red[kGramThreads / 64];
+  const int l = blockIdx.x;
+  const int32_t* it = work.items + 4 * (size_t)l;
+  const int problem = it[0], row0 = it[1], rows = it[2];
+  int P, Q;
+  pair_from_index(it[3], &P, &Q);
+  const In* Xa = reinterpret_cast<const In*>(work.a_ptrs[problem]) + (size_t)row0 * din;
+  const In* Xg = reinterpret_cast<const In*>(work.g_ptrs[problem]) + (size_t)row0 * dout;
+  double s = 0.0;
+  for (int sub = 0; sub < 4; ++sub) {
+    const int p = 2 * P + (sub >> 1), q = 2 * Q + (sub & 1);
+    float pa[4][4], pg[4][4];
+    gram_tile_generic<In>(Xa, rows, din, p, q, sp, sq, pa);
+    gram_tile_generic<In>(Xg, rows, dout, p, q, sp, sq, pg);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s += (double)pa[i][j] * (double)pg[i][j];
+  }
+  double total = block_sum_f64(s, red);
+  if (threadIdx.x == 0) partial[l] = (P == Q) ? total : 2.0 * total;
+}
+
+// seg_sq[v] = sum of the partials of segment v's items (fixed order).
+__global__ void __launch_bounds__(kGramThreads)
+segment_fold_kernel(const double* __restrict__ partial, const int32_t* __restrict__ item_start,
+                    int S, double* __restrict__ seg_sq) {
+  const int v = blockIdx.x * blockDim.x + threadIdx.x;
+  if (v >= S) return;
+  double s = 0.0;
+  for (int i = item_start[v]; i < item_start[v + 1]; ++i) s += partial[i];
+  seg_sq[v] = s;
 }
 
 // ||sum_t G_i[t]||^2 for a bias: one workgroup per example, columns strided
@@ -382,9 +445,10 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
     npairs = nt * (nt + 1) / 2;
     const int nblocks = npairs * B;
     const int padded = ceil_div(nblocks, kXcds) * kXcds;
-    hipLaunchKernelGGL(gram_mfma_bf16_kernel, dim3(padded), dim3(kGramMfmaThreads), 0, s,
+    GramItems none = {nullptr, nullptr, nullptr};
+    hipLaunchKernelGGL(gram_mfma_bf16_kernel<false>, dim3(padded), dim3(kGramMfmaThreads), 0, s,
                        (const uint16_t*)A, (const uint16_t*)G, T, din, dout, npairs, nblocks,
-                       partial);
+                       partial, none);
   } else {
     int nt = ceil_div(T, kGenTile);
     npairs = nt * (nt + 1) / 2;
@@ -415,6 +479,42 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
                        0, s, bias_sq, B, 1, 1, sqnorm);
     DPC_HIP_CHECK(hipGetLastError());
   }
+  return DPC_OK;
+}
+
+extern "C" int dpc_grouped_gram_sqnorms(const int64_t* a_ptrs, const int64_t* g_ptrs, int din,
+                                        int dout, int dtype, const int32_t* items, int n_items,
+                                        int max_rows, const int32_t* seg_item_start, int S,
+                                        double* seg_sq, void* ws, size_t ws_bytes,
+                                        void* stream) {
+  if (din <= 0 || dout <= 0 || n_items < 0 || S < 0 || max_rows < 0) return DPC_EINVAL;
+  if (dtype != DPC_F32 && dtype != DPC_BF16) return DPC_EINVAL;
+  if (S == 0) return DPC_OK;
+  if (!seg_item_start || !seg_sq || (n_items > 0 && (!a_ptrs || !g_ptrs || !items || !ws)))
+    return DPC_EINVAL;
+  if (ws_bytes < (size_t)n_items * sizeof(double)) return DPC_ENOSPC;
+  hipStream_t s = (hipStream_t)stream;
+  double* partial = (double*)ws;
+  if (n_items > 0) {
+    GramItems work = {items, a_ptrs, g_ptrs};
+    const size_t dmax = (size_t)(din > dout ? din : dout);
+    const bool fits = ((size_t)max_rows + kGramTile) * dmax * 2 < ((size_t)1 << 31);
+    if (dtype == DPC_BF16 && din % 8 == 0 && dout % 8 == 0 && fits) {
+      const int padded = ceil_div(n_items, kXcds) * kXcds;
+      hipLaunchKernelGGL(gram_mfma_bf16_kernel<true>, dim3(padded), dim3(kGramMfmaThreads), 0, s,
+                         nullptr, nullptr, 0, din, dout, 0, n_items, partial, work);
+    } else if (dtype == DPC_BF16) {
+      hipLaunchKernelGGL(gram_grouped_generic_kernel<uint16_t>, dim3(n_items), dim3(kGramThreads),
+                         0, s, work, din, dout, partial);
+    } else {
+      hipLaunchKernelGGL(gram_grouped_generic_kernel<float>, dim3(n_items), dim3(kGramThreads), 0,
+                         s, work, din, dout, partial);
+    }
+    DPC_HIP_CHECK(hipGetLastError());
+  }
+  hipLaunchKernelGGL(segment_fold_kernel, dim3(ceil_div(S, kGramThreads)), dim3(kGramThreads), 0,
+                     s, (const double*)partial, seg_item_start, S, seg_sq);
+  DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;
 }
 

@@ -191,6 +191,179 @@ def clipped_sum(
     return out, bias_out
 
 
+_GRAM_TILE = 128  # rows of a Gram tile of the grouped norm kernel
+_STEP_ROWS = 64  # rows of a K step of the grouped clipped sum
+
+
+class SegmentLayout:
+    """Rows of E problems cut into per-example segments, built on the host.
+
+    ``lengths[e][k]`` is the number of rows of segment k of problem e; problem
+    e's rows are its segments in order.  Segment ``v = e * K + k`` (K segments
+    per problem, e.g. K = batch size).  The device tables (segment first rows
+    and lengths, Gram work items) are built once per layout and copied in one
+    transfer.
+    """
+
+    def __init__(self, lengths, device):
+        import numpy as np
+
+        lens = np.asarray(lengths, dtype=np.int64)
+        if lens.ndim != 2 or (lens < 0).any():
+            raise ConfigurationError("segment lengths must be a non-negative [E, K] table")
+        self.E, self.K = lens.shape
+        self.S = self.E * self.K
+        self.lengths = lens
+        self.rows = lens.sum(axis=1)
+        self.max_rows = int(self.rows.max()) if self.E else 0
+        if self.max_rows >= 1 << 30:
+            raise ConfigurationError("too many rows in one problem")
+        flat = lens.reshape(-1)
+        row0 = (np.cumsum(lens, axis=1) - lens).reshape(-1)
+        group = np.repeat(np.arange(self.E, dtype=np.int64), self.K)
+        nt = (flat + _GRAM_TILE - 1) // _GRAM_TILE
+        npairs = nt * (nt + 1) // 2
+        item_start = np.concatenate([[0], np.cumsum(npairs)])
+        self.n_items = int(item_start[-1])
+        seg_of_item = np.repeat(np.arange(self.S), npairs)
+        pair = np.arange(self.n_items) - item_start[seg_of_item]
+        items = np.stack([group[seg_of_item], row0[seg_of_item], flat[seg_of_item], pair], axis=1)
+        self.max_steps = int(((flat + _STEP_ROWS - 1) // _STEP_ROWS).sum())
+        # One int32 buffer: row0 [S] | len [S] | group [S] | rows [E] |
+        # item_start [S + 1] | items [n_items * 4].
+        parts = [row0, flat, group, self.rows, item_start, items.reshape(-1)]
+        host = torch.from_numpy(np.concatenate(parts).astype(np.int32))
+        buf = host.pin_memory().to(device, non_blocking=True) if torch.device(device).type == "cuda" \
+            else host
+        offs = np.cumsum([0] + [len(p) for p in parts])
+        (self.seg_row0, self.seg_len, self.seg_group, self.rows_dev, self.item_start,
+         self.items) = [buf[offs[i]:offs[i + 1]] for i in range(len(parts))]
+        self._buf = buf
+        self.device = torch.device(device)
+
+    def example_of_segment(self):
+        """Column index k of every segment (int64 [S], on the device)."""
+        return torch.arange(self.S, device=self.device) % self.K
+
+
+def _ptr_table(tensors, device) -> torch.Tensor:
+    host = torch.tensor([t.data_ptr() for t in tensors], dtype=torch.int64)
+    return host.pin_memory().to(device, non_blocking=True)
+
+
+def _check_grouped(A_list, G_list, layout: SegmentLayout):
+    if len(A_list) != layout.E or len(G_list) != layout.E:
+        raise ConfigurationError("one A and one G per problem of the layout are required")
+    if layout.E == 0:
+        raise ConfigurationError("a grouped call needs at least one problem")
+    din, dout, dtype = A_list[0].shape[-1], G_list[0].shape[-1], A_list[0].dtype
+    for e, (A, G) in enumerate(zip(A_list, G_list)):
+        if A.dim() != 2 or G.dim() != 2 or A.shape[0] != G.shape[0]:
+            raise ConfigurationError("grouped operands must be A_e [rows, din], G_e [rows, dout]")
+        if A.shape[1] != din or G.shape[1] != dout or A.dtype != dtype or G.dtype != dtype:
+            raise ConfigurationError("grouped problems must share din, dout and dtype")
+        if A.shape[0] != int(layout.rows[e]):
+            raise ConfigurationError(
+                f"problem {e} has {A.shape[0]} rows, its segments {int(layout.rows[e])}")
+        if not (A.is_contiguous() and G.is_contiguous()):
+            raise ConfigurationError("grouped operands must be contiguous")
+    return din, dout, dtype
+
+
+def grouped_gram_sqnorms(A_list, G_list, layout: SegmentLayout) -> torch.Tensor:
+    """``||G_v^T A_v||^2`` for every segment v of the layout: float64 [E, K]."""
+    dev = nat.require_device(*A_list, *G_list)
+    din, dout, dtype = _check_grouped(A_list, G_list, layout)
+    seg_sq = torch.empty((layout.E, layout.K), dtype=torch.float64, device=dev)
+    ws = torch.empty(max(layout.n_items, 1), dtype=torch.float64, device=dev)
+    a_ptrs, g_ptrs = _ptr_table(A_list, dev), _ptr_table(G_list, dev)
+    nat.call(
+        "dpc_grouped_gram_sqnorms", nat.ptr(a_ptrs), nat.ptr(g_ptrs), din, dout,
+        nat.dtype_code(dtype), nat.ptr(layout.items), layout.n_items, layout.max_rows,
+        nat.ptr(layout.item_start), layout.S, nat.ptr(seg_sq), nat.ptr(ws),
+        ws.numel() * 8, nat.stream_handle(dev),
+    )
+    return seg_sq
+
+
+@dataclass
+class GroupedNoise:
+    """Noise of a grouped clipped sum: per-problem ``sigmas``; ``noise`` holds
+    float32 draws per problem (mode INJECTED) or ``leaf_ids`` name each
+    problem's Philox stream under ``seed`` (mode PHILOX)."""
+
+    sigmas: list
+    mode: int = nat.NOISE_PHILOX
+    noise: list | None = None
+    seed: int = 0
+    leaf_ids: list | None = None
+
+
+def grouped_clipped_sum(
+    A_list,
+    G_list,
+    layout: SegmentLayout,
+    seg_scale: torch.Tensor,
+    *,
+    normalize_by: float = 1.0,
+    noise: GroupedNoise | None = None,
+    out_dtype: torch.dtype | None = None,
+) -> torch.Tensor:
+    """``out[e] = sum_v seg_scale[v] G_v^T A_v`` over problem e's segments, with
+    ``/ normalize_by`` and noise in the epilogue: [E, dout, din].
+
+    ``seg_scale`` is float32 [E, K] (segment v = e * K + k); segments with
+    scale 0 are never read.
+    """
+    dev = nat.require_device(*A_list, *G_list, seg_scale)
+    din, dout, dtype = _check_grouped(A_list, G_list, layout)
+    if seg_scale.dtype != torch.float32 or tuple(seg_scale.shape) != (layout.E, layout.K):
+        raise ConfigurationError("seg_scale must be float32 [E, K]")
+    seg_scale = _contig(seg_scale)
+    out_dtype = out_dtype or dtype
+    E = layout.E
+    out = torch.empty((E, dout, din), dtype=out_dtype, device=dev)
+    steps = torch.empty(2 * max(layout.max_steps, 1), dtype=torch.int32, device=dev)
+    step_start = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    stream = nat.stream_handle(dev)
+    nat.call(
+        "dpc_segment_plan", nat.ptr(layout.seg_row0), nat.ptr(layout.seg_len),
+        nat.ptr(layout.seg_group), nat.ptr(seg_scale), layout.S, E, layout.max_steps,
+        nat.ptr(steps), nat.ptr(step_start), stream,
+    )
+    spec = noise or GroupedNoise(sigmas=[0.0] * E, mode=nat.NOISE_NONE)
+    if len(spec.sigmas) != E:
+        raise ConfigurationError("one noise sigma per problem is required")
+    active = any(s != 0.0 for s in spec.sigmas)
+    mode = spec.mode if active else nat.NOISE_NONE
+    noise_ptrs = None
+    if mode == nat.NOISE_INJECTED:
+        if spec.noise is None or len(spec.noise) != E:
+            raise ConfigurationError("injected noise needs one float32 tensor per problem")
+        for t in spec.noise:
+            if t.dtype != torch.float32 or tuple(t.shape) != (dout, din) or not t.is_contiguous() \
+                    or t.device != dev:
+                raise ConfigurationError(f"injected noise must be float32 {(dout, din)} on the device")
+        noise_ptrs = _ptr_table(spec.noise, dev)
+    leaf_ids = spec.leaf_ids if spec.leaf_ids is not None else list(range(E))
+    if len(leaf_ids) != E:
+        raise ConfigurationError("one leaf id per problem is required")
+    small = torch.tensor([v & 0xFFFFFFFF for v in leaf_ids], dtype=torch.int64).to(torch.int32)
+    sig = torch.tensor([float(v) for v in spec.sigmas], dtype=torch.float32)
+    leaf_dev = small.pin_memory().to(dev, non_blocking=True)
+    sig_dev = sig.pin_memory().to(dev, non_blocking=True)
+    a_ptrs, g_ptrs = _ptr_table(A_list, dev), _ptr_table(G_list, dev)
+    out_ptrs = _ptr_table([out[e] for e in range(E)], dev)
+    nat.call(
+        "dpc_grouped_clipped_sum", nat.ptr(a_ptrs), nat.ptr(g_ptrs), nat.ptr(layout.rows_dev),
+        layout.max_rows, E, din, dout, nat.dtype_code(dtype), nat.ptr(steps),
+        nat.ptr(step_start), nat.ptr(seg_scale), float(normalize_by), mode, nat.ptr(noise_ptrs),
+        spec.seed & ((1 << 64) - 1), nat.ptr(leaf_dev), nat.ptr(sig_dev),
+        nat.dtype_code(out_dtype), nat.ptr(out_ptrs), stream,
+    )
+    return out
+
+
 def leaf_view(t: torch.Tensor) -> tuple[int, int]:
     """The [rows, cols] view of a leaf for the device noise stream."""
     if t.dim() == 0:
@@ -239,12 +412,16 @@ def philox4x32_10(counter: tuple[int, int, int, int], key: tuple[int, int], n: i
 
 __all__ = [
     "ClipFactors",
+    "GroupedNoise",
     "NoiseSpec",
+    "SegmentLayout",
     "add_noise",
     "clip_factors",
     "clipped_sum",
     "flat_sqnorms",
     "gram_sqnorms",
+    "grouped_clipped_sum",
+    "grouped_gram_sqnorms",
     "leaf_view",
     "philox4x32_10",
 ]

@@ -69,8 +69,52 @@ def mlp_per_example_grads(model: torch.nn.Module, params: dict, x: torch.Tensor,
     return vmap(grad(loss_fn), in_dims=(None, 0, 0))(params, x, y)
 
 
+def segment_grads(A: torch.Tensor, G: torch.Tensor, lengths, *, dtype=None) -> torch.Tensor:
+    """Per-segment weight gradients of a row-segmented linear layer.
+
+    ``A`` [rows, din], ``G`` [rows, dout]; ``lengths`` are the consecutive
+    segments' row counts.  Segment v's gradient is ``G_v^T A_v`` over its rows
+    (the per-sample gradient of a "virtual expert", the reference's
+    ``_grouped_AtB`` out[g] = A_g^T B_g,
+    packages/opake-patches/src/opake/api/patches/kernels/fused_moe.py:54-113),
+    computed in float64 and rounded once to ``dtype``.  Returns [S, dout, din].
+    """
+    dtype = dtype or A.dtype
+    out = torch.zeros(len(lengths), G.shape[1], A.shape[1], dtype=torch.float64)
+    start = 0
+    for v, n in enumerate(lengths):
+        if n:
+            out[v] = G[start:start + n].double().T @ A[start:start + n].double()
+        start += n
+    return out.to(dtype)
+
+
+def per_example_grads_loop(model: torch.nn.Module, loss_fn, args: tuple, targets,
+                           batch_args=None) -> dict:
+    """Per-example gradients of every trainable parameter by brute force: one
+    forward and backward of ``model`` per example on its own slice.
+
+    ``loss_fn(outputs, targets)`` returns per-example losses; ``batch_args``
+    marks which positional args carry the batch (default: all).  Returns
+    ``{parameter name: [B, *shape]}`` in float64 of the parameter values.
+    """
+    params = {n: p for n, p in model.named_parameters() if p.requires_grad}
+    B = targets.shape[0]
+    batch_args = batch_args or tuple(range(len(args)))
+    out = {n: [] for n in params}
+    for i in range(B):
+        sl = tuple(a[i:i + 1] if j in batch_args else a for j, a in enumerate(args))
+        loss = loss_fn(model(*sl), targets[i:i + 1]).sum()
+        gs = torch.autograd.grad(loss, list(params.values()), allow_unused=True)
+        for (n, p), g in zip(params.items(), gs):
+            out[n].append(torch.zeros_like(p) if g is None else g.detach())
+    return {n: torch.stack(v) for n, v in out.items()}
+
+
 __all__ = [
     "MLP",
+    "per_example_grads_loop",
+    "segment_grads",
     "linear_per_example_grads",
     "mlp_per_example_grads",
     "surrogate_per_example_grads",

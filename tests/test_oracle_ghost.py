@@ -77,3 +77,80 @@ def test_mlp_vmap_grad_matches_loop():
         loss.backward()
         for k, p in model.named_parameters():
             torch.testing.assert_close(got[k][i], p.grad, rtol=1e-10, atol=1e-12)
+
+
+def test_per_example_loop_matches_vmap_grad_mlp():
+    torch.manual_seed(3)
+    model = ghost_oracle.MLP(12, 9, 4).double()
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(5, 12, generator=g, dtype=torch.float64)
+    y = torch.randint(0, 4, (5,), generator=g)
+    params = {k: v.detach() for k, v in model.named_parameters()}
+    vm = ghost_oracle.mlp_per_example_grads(model, params, x, y)
+    loop = ghost_oracle.per_example_grads_loop(
+        model, lambda out, t: torch.nn.functional.cross_entropy(out, t, reduction="none"),
+        (x,), y)
+    for k in vm:
+        torch.testing.assert_close(loop[k], vm[k], rtol=1e-12, atol=1e-12)
+
+
+def _moe_setup(seed=0, B=3, T=7, d=6, inter=5, E=4, k=2):
+    from opake_amd.moe import TopKMoE
+
+    torch.manual_seed(seed)
+    model = TopKMoE(d, inter, E, k, dtype=torch.float64)
+    g = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(B, T, d, generator=g, dtype=torch.float64)
+    logits = torch.randn(B, T, E, generator=g, dtype=torch.float64)
+    target = torch.randn(B, T, d, generator=g, dtype=torch.float64)
+    return model, x, logits, target
+
+
+def _mse(out, t):
+    return ((out - t) ** 2).sum(dim=(1, 2))
+
+
+def test_moe_matches_dense_reference_forward():
+    # moe.py:74-103 of the reference: dense loop over experts with route weights.
+    model, x, logits, _ = _moe_setup()
+    out = model(x, logits)
+    top_v, top_i = torch.topk(logits, model.top_k, dim=-1)
+    w = torch.softmax(top_v, dim=-1)
+    ref = torch.zeros_like(x)
+    for e, ex in enumerate(model.experts):
+        gu = x @ ex.gate_up.weight.T
+        h = torch.nn.functional.silu(gu[..., :model.inter]) * gu[..., model.inter:]
+        y = h @ ex.down.weight.T
+        route = torch.where(top_i == e, w, torch.zeros_like(w)).sum(-1, keepdim=True)
+        ref = ref + y * route
+    # The module (as the reference) accumulates the expert outputs and takes
+    # the SiLU in float32.
+    torch.testing.assert_close(out, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_segment_grads_are_the_per_example_expert_grads():
+    # The rows of expert e are its examples' tokens in example order, so the
+    # per-segment G_v^T A_v are the per-example gradients of that expert.
+    model, x, logits, target = _moe_setup(seed=5)
+    caps = {}
+
+    def hook(name):
+        def fn(mod, inp, out):
+            caps[name] = (inp[0].detach(), out, list(mod.dpc_row_segments))
+        return fn
+
+    handles = [m.register_forward_hook(hook(n)) for n, m in model.named_modules()
+               if isinstance(m, torch.nn.Linear) and m.weight.requires_grad]
+    losses = _mse(model(x, logits), target)
+    names = list(caps)
+    outs = torch.autograd.grad(losses.sum(), [caps[n][1] for n in names])
+    for h in handles:
+        h.remove()
+    loop = ghost_oracle.per_example_grads_loop(model, _mse, (x, logits), target)
+    for n, G in zip(names, outs):
+        A, _, seg = caps[n]
+        assert len(seg) == x.shape[0] and sum(seg) == A.shape[0]
+        got = ghost_oracle.segment_grads(A, G.detach(), seg)
+        # The forward takes the SiLU and the output sum in float32, so a batch
+        # of one and the full batch agree to float32 rounding.
+        torch.testing.assert_close(got, loop[f"{n}.weight"], rtol=1e-6, atol=1e-8)
