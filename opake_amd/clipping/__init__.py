@@ -11,7 +11,12 @@ from opake_amd.clipping._clipped_fun import (
     clipped_grad,
 )
 from opake_amd.clipping._ghost import GhostClipAux, ghost_clip_sum, ghost_sqnorms, guard_for_linear
-from opake_amd.clipping._model import GhostGradAux, ghost_clipped_grad
+from opake_amd.clipping._model import (
+    GhostGradAux,
+    LinearCapture,
+    ghost_clip_captured,
+    ghost_clipped_grad,
+)
 from opake_amd.clipping._leaves import (
     LeafClipResult,
     fused_stream_clip_and_sum,
@@ -32,6 +37,7 @@ __all__ = [
     "GhostClipAux",
     "GhostGradAux",
     "LeafClipResult",
+    "LinearCapture",
     "auto_clipped_grad",
     "auto_scale_pytree",
     "clip_pytree",
@@ -39,6 +45,7 @@ __all__ = [
     "clipped_grad",
     "fused_stream_clip_and_sum",
     "get_fused_clip_backend",
+    "ghost_clip_captured",
     "ghost_clip_sum",
     "ghost_clipped_grad",
     "ghost_sqnorms",

@@ -41,7 +41,8 @@ leaves are drawn in sorted-name (flatten) order.
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+import math
+from dataclasses import dataclass, replace
 
 import torch
 from torch.autograd.profiler import record_function
@@ -64,7 +65,7 @@ class GhostGradAux:
     group), ``num_clipped`` (int32 [1], or [G] per group), and per-group norms
     ``{group: float32 [B]}`` with ``PerGroup`` clipping."""
 
-    loss_values: torch.Tensor
+    loss_values: torch.Tensor | None
     grad_norms: torch.Tensor
     clip_scales: torch.Tensor
     num_clipped: torch.Tensor
@@ -146,13 +147,286 @@ def _validate_bound(clipping_norm) -> None:
 
 
 @dataclass
-class _Layer:
+class LinearCapture:
+    """One linear layer's operands for ghost clipping.
+
+    ``A`` / ``G``: the layer's inputs and output gradients, ``[B, T, d]`` or
+    ``[B, d]`` -- or, with ``segments`` (B per-example row counts), ``[rows,
+    d]`` rows of several examples in example order.  The output leaves are
+    ``"<name>.weight"`` (``[dout, din]``) and, with ``has_bias``,
+    ``"<name>.bias"``; ``param_dtype`` is their default dtype (the operand
+    dtype when ``None``).
+    """
+
     name: str
-    mod: torch.nn.Linear
+    A: torch.Tensor
+    G: torch.Tensor
+    has_bias: bool = False
+    segments: list | None = None
+    param_dtype: torch.dtype | None = None
+
+
+@dataclass
+class _Layer:
+    cap: LinearCapture
     group: int
     A: torch.Tensor  # dense [B, T, din]; segmented [rows, din]
     G: torch.Tensor
-    segments: list | None = None
+
+    @property
+    def name(self):
+        return self.cap.name
+
+
+def _groups_of(leaf_names, clipping_norm):
+    """Leaf -> group index, group names (sorted) and bounds."""
+    if not isinstance(clipping_norm, PerGroup):
+        return dict.fromkeys(leaf_names, 0), None, [float(clipping_norm)]
+    group_names = sorted(clipping_norm.values)
+    keys = {param_path(n) for n in leaf_names}
+    mapped = set(clipping_norm.groups)
+    if keys != mapped:
+        missing = sorted(map(str, keys - mapped))
+        extra = sorted(map(str, mapped - keys))
+        raise ConfigurationError(
+            "PerGroup path keys must match the pytree tensor leaves exactly."
+            + (f" Leaves with no group assignment: {missing}." if missing else "")
+            + (f" Group paths with no matching leaf: {extra}." if extra else ""))
+    gidx = {n: k for k, n in enumerate(group_names)}
+    leaf_group = {n: gidx[clipping_norm.groups[param_path(n)]] for n in leaf_names}
+    return leaf_group, group_names, [float(clipping_norm.values[n]) for n in group_names]
+
+
+def _event_pair(sink):
+    """Record a start event on the current stream (the one the kernels use)."""
+    if sink is None:
+        return None
+    pair = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+    pair[0].record()
+    sink.append(pair)
+    return pair
+
+
+def _close_pair(pair):
+    if pair is not None:
+        pair[1].record()
+
+
+def ghost_clip_captured(
+    captures,
+    *,
+    clipping_norm,
+    normalize_by: float = 1.0,
+    noise_fn=None,
+    noise_state=None,
+    dtype: torch.dtype | None = None,
+    return_aux: bool = False,
+    gemm_events: list | None = None,
+):
+    """Clip -> sum (-> noise) from the captured operands of linear layers.
+
+    ``captures``: a list of :class:`LinearCapture` (one per layer, all with
+    the same batch).  Returns what ``ghost_clipped_grad``'s step returns,
+    without the forward: ``ClippedPytree`` (``(NoisedPytree, noise_state')``
+    with ``noise_fn``), and with ``return_aux`` the first element is
+    ``(result, GhostGradAux)`` whose ``loss_values`` is ``None``.
+    ``gemm_events`` (timing hook): a list that receives one pair of recorded
+    ``torch.cuda.Event`` around each clipped-sum launch.
+    """
+    _validate_bound(clipping_norm)
+    if normalize_by <= 0.0:
+        raise ConfigurationError(f"normalize_by must be > 0, got {normalize_by}.")
+    if not captures:
+        raise ConfigurationError("no layers to clip")
+    max_norm = clipping_norm / normalize_by
+    per_group = isinstance(clipping_norm, PerGroup)
+    shapes = {}
+    for c in captures:
+        shapes[f"{c.name}.weight"] = (c.G.shape[-1], c.A.shape[-1])
+        if c.has_bias:
+            shapes[f"{c.name}.bias"] = (c.G.shape[-1],)
+    if len(shapes) != sum(1 + c.has_bias for c in captures):
+        raise ConfigurationError("layer names must be unique")
+    leaf_names = sorted(shapes)
+    leaf_index = {n: i for i, n in enumerate(leaf_names)}
+    leaf_group, group_names, bounds = _groups_of(leaf_names, clipping_norm)
+    n_groups = len(bounds)
+
+    B = None
+    dense, segmented = [], []
+    for c in captures:
+        g = leaf_group[f"{c.name}.weight"]
+        if c.has_bias and leaf_group[f"{c.name}.bias"] != g:
+            raise ConfigurationError(
+                f"layer {c.name!r}: weight and bias must be in the same clipping group")
+        G = c.G if c.G.dtype == c.A.dtype else c.G.to(c.A.dtype)
+        if c.segments is None:
+            nb = c.A.shape[0]
+            if B is None:
+                B = nb
+            A3, G3 = _as_btd(c.A, B), _as_btd(G, B)
+            if A3.shape[1] != G3.shape[1]:
+                raise ConfigurationError(f"layer {c.name!r}: A and G disagree on the token count")
+            dense.append(_Layer(c, g, A3.contiguous(), G3.contiguous()))
+        else:
+            if c.has_bias:
+                raise ConfigurationError(
+                    f"layer {c.name!r}: row-segmented layers with a bias are not supported")
+            A2 = c.A.reshape(-1, c.A.shape[-1]).contiguous()
+            G2 = G.reshape(-1, G.shape[-1]).contiguous()
+            if B is None:
+                B = len(c.segments)
+            if len(c.segments) != B or sum(c.segments) != A2.shape[0] or G2.shape[0] != A2.shape[0]:
+                raise ConfigurationError(
+                    f"layer {c.name!r}: the row segments must give B row counts that add up "
+                    "to the layer's input rows")
+            segmented.append(_Layer(c, g, A2, G2))
+    device = (dense + segmented)[0].A.device
+
+    # Per-group, per-example squared norms.
+    sq = torch.zeros((n_groups, B), dtype=torch.float64, device=device)
+    for L in dense:
+        if L.A.shape[1] == 1:
+            ops.flat_sqnorms(L.A[:, 0], L.G[:, 0], with_bias=L.cap.has_bias, out=sq[L.group])
+        else:
+            ops.gram_sqnorms(L.A, L.G, with_bias=L.cap.has_bias, out=sq[L.group])
+    buckets = {}
+    for L in segmented:
+        buckets.setdefault((L.A.shape[1], L.G.shape[1], L.A.dtype), []).append(L)
+    bucket_layouts = []
+    for members in buckets.values():
+        layout = ops.SegmentLayout([L.cap.segments for L in members], device)
+        seg_sq = ops.grouped_gram_sqnorms([L.A for L in members], [L.G for L in members], layout)
+        for g in range(n_groups):
+            idx = [i for i, L in enumerate(members) if L.group == g]
+            if idx:
+                sq[g] += seg_sq[idx].sum(dim=0)
+        bucket_layouts.append((members, layout))
+
+    # Guards for the materialised leaves the reference would clip.
+    sizes = [math.prod(shapes[n]) for n in leaf_names]
+    roundoff = num.norm_roundoff(torch.float32, torch.float64, len(sizes),
+                                 num.reduction_terms(sizes))
+    storage = sorted({L.A.dtype for L in dense + segmented}, key=str)
+    guards = [num.guard_constants(dt, torch.promote_types(dt, torch.float32), roundoff)
+              for dt in storage]
+    cfs = [ops.clip_factors(sq[g], num.conservative_bound(bounds[g]), guards,
+                            count_threshold=num.float32_of(bounds[g]))
+           for g in range(n_groups)]
+
+    std = 0.0
+    gen = None
+    step_key = None
+    next_noise_state = None
+    if noise_fn is not None:
+        if noise_state is None:
+            raise ConfigurationError("noise_state is required with noise_fn")
+        std = noise_fn.clipped_stddev(clipped(None, max_norm=max_norm))
+        noisy = any((std.for_path(param_path(n)) if isinstance(std, PerGroup) else std) != 0.0
+                    for n in leaf_names)
+        if noisy and noise_fn.compute_dtype != torch.float32:
+            raise ConfigurationError("fused noise supports compute_dtype float32 only")
+        step_key = step_key_for(noise_state)
+        if noisy and noise_fn.stream == "reference":
+            gen = generator_from_key(step_key)
+        next_noise_state = GaussianNoiseState(
+            _step_counter=noise_state._step_counter + 1, _rng_key=noise_state._rng_key)
+
+    def leaf_std(leaf: str) -> float:
+        if noise_fn is None:
+            return 0.0
+        if isinstance(std, PerGroup):
+            return float(std.for_path(param_path(leaf)))
+        return float(std)
+
+    # Reference-stream draws: one generator, flatten order, no draw for a
+    # leaf whose standard deviation is 0.
+    draws = {}
+    if gen is not None:
+        for leaf in leaf_names:
+            if leaf_std(leaf) != 0.0:
+                draws[leaf] = torch.randn(shapes[leaf], dtype=torch.float32, generator=gen)
+
+    def to_dev(t):
+        return t.pin_memory().to(device, non_blocking=True)
+
+    tree = {}
+    for L in dense:
+        si = storage.index(L.A.dtype)
+        cf = cfs[L.group]
+        wn, bn = f"{L.name}.weight", f"{L.name}.bias"
+        spec = None
+        s_w = leaf_std(wn)
+        s_b = leaf_std(bn) if L.cap.has_bias else s_w
+        if s_w != s_b:
+            raise ConfigurationError(
+                f"layer {L.name!r}: weight and bias noise must share a standard deviation")
+        if s_w != 0.0:
+            if gen is not None:
+                spec = ops.NoiseSpec(
+                    sigma=s_w, mode=nat.NOISE_INJECTED, noise=to_dev(draws[wn]),
+                    bias_noise=to_dev(draws[bn]) if L.cap.has_bias else None)
+            else:
+                spec = ops.NoiseSpec(sigma=s_w, mode=nat.NOISE_PHILOX, seed=step_key.seed,
+                                     leaf_id=leaf_index[wn], bias_leaf_id=leaf_index.get(bn, 0))
+        ev = _event_pair(gemm_events)
+        w, b = ops.clipped_sum(L.A, L.G, cf.scale[si], plan=cf.plan if len(storage) == 1 else None,
+                               normalize_by=normalize_by, noise=spec,
+                               out_dtype=dtype or L.cap.param_dtype or L.A.dtype,
+                               with_bias=L.cap.has_bias)
+        _close_pair(ev)
+        tree[wn] = w
+        if L.cap.has_bias:
+            tree[bn] = b
+    for members, layout in bucket_layouts:
+        si = storage.index(members[0].A.dtype)
+        seg_scale = torch.stack([cfs[L.group].scale[si] for L in members])
+        names = [f"{L.name}.weight" for L in members]
+        sigmas = [leaf_std(n) for n in names]
+        gnoise = None
+        if any(s != 0.0 for s in sigmas):
+            if gen is not None:
+                zero = None
+                noise = []
+                for n in names:
+                    if n in draws:
+                        noise.append(to_dev(draws[n]))
+                    else:
+                        if zero is None:
+                            zero = torch.zeros(shapes[n], dtype=torch.float32, device=device)
+                        noise.append(zero)
+                gnoise = ops.GroupedNoise(sigmas=sigmas, mode=nat.NOISE_INJECTED, noise=noise)
+            else:
+                gnoise = ops.GroupedNoise(sigmas=sigmas, mode=nat.NOISE_PHILOX, seed=step_key.seed,
+                                          leaf_ids=[leaf_index[n] for n in names])
+        out_dtype = dtype or members[0].cap.param_dtype or members[0].A.dtype
+        ev = _event_pair(gemm_events)
+        stacked = ops.grouped_clipped_sum([L.A for L in members], [L.G for L in members], layout,
+                                          seg_scale, normalize_by=normalize_by, noise=gnoise,
+                                          out_dtype=out_dtype)
+        _close_pair(ev)
+        for i, n in enumerate(names):
+            tree[n] = stacked[i]
+    tree = {k: tree[k] for k in leaf_names}
+    if noise_fn is None:
+        result = clipped(tree, max_norm=max_norm)
+    else:
+        result = NoisedPytree(pytree=tree, max_norm=max_norm, noise_stddev=std)
+    if return_aux:
+        total = sq.sum(dim=0) if n_groups > 1 else sq[0]
+        group_norms = None
+        if per_group:
+            group_norms = {n: cfs[k].norms for k, n in enumerate(group_names)}
+        aux = GhostGradAux(
+            loss_values=None,
+            grad_norms=torch.sqrt(total).to(torch.float32) if per_group else cfs[0].norms,
+            clip_scales=torch.stack([cf.scale for cf in cfs]) if per_group else cfs[0].scale,
+            num_clipped=torch.cat([cf.nclipped for cf in cfs]),
+            batch_size=B, group_norms=group_norms)
+        result = (result, aux)
+    if noise_fn is None:
+        return result
+    return result, next_noise_state
 
 
 def ghost_clipped_grad(
@@ -177,49 +451,16 @@ def ghost_clipped_grad(
     if normalize_by <= 0.0:
         raise ConfigurationError(f"normalize_by must be > 0, got {normalize_by}.")
     layers = _linear_layers(model)
-    max_norm = clipping_norm / normalize_by
-    state0 = FixedClipState()
-
-    # Output leaves, in flatten (sorted-name) order.
     leaf_names = []
     for name, mod in layers:
         leaf_names.append(f"{name}.weight")
         if mod.bias is not None:
             leaf_names.append(f"{name}.bias")
-    leaf_names.sort()
-    leaf_index = {n: i for i, n in enumerate(leaf_names)}
-
-    # Clipping groups: one per PerGroup name (sorted), or a single group.
-    per_group = isinstance(clipping_norm, PerGroup)
-    if per_group:
-        group_names = sorted(clipping_norm.values)
-        keys = {param_path(n) for n in leaf_names}
-        mapped = set(clipping_norm.groups)
-        if keys != mapped:
-            missing = sorted(map(str, keys - mapped))
-            extra = sorted(map(str, mapped - keys))
-            raise ConfigurationError(
-                "PerGroup path keys must match the pytree tensor leaves exactly."
-                + (f" Leaves with no group assignment: {missing}." if missing else "")
-                + (f" Group paths with no matching leaf: {extra}." if extra else ""))
-        gidx = {n: k for k, n in enumerate(group_names)}
-        leaf_group = {n: gidx[clipping_norm.groups[param_path(n)]] for n in leaf_names}
-        bounds = [float(clipping_norm.values[n]) for n in group_names]
-    else:
-        group_names = None
-        leaf_group = dict.fromkeys(leaf_names, 0)
-        bounds = [float(clipping_norm)]
-    n_groups = len(bounds)
-    layer_group = {}
-    for name, mod in layers:
-        g = leaf_group[f"{name}.weight"]
-        if mod.bias is not None and leaf_group[f"{name}.bias"] != g:
-            raise ConfigurationError(
-                f"layer {name!r}: weight and bias must be in the same clipping group")
-        layer_group[name] = g
+    _groups_of(leaf_names, clipping_norm)  # validates a PerGroup against the leaves
+    state0 = FixedClipState()
 
     def grad_fn(inputs, targets, *, state, noise_fn=None, noise_state=None):
-        captures = [_Capture(mod) for _, mod in layers]
+        hooks = [_Capture(mod) for _, mod in layers]
         args = inputs if isinstance(inputs, tuple) else (inputs,)
         try:
             with record_function("opake::ghost_clipped_grad"), torch.enable_grad():
@@ -227,8 +468,7 @@ def ghost_clipped_grad(
                 losses = loss_fn(outputs, targets)
                 if losses.dim() != 1:
                     raise ConfigurationError("loss_fn must return per-example losses [B]")
-                B = losses.shape[0]
-                for (name, _), cap in zip(layers, captures):
+                for (name, _), cap in zip(layers, hooks):
                     if cap.out is None:
                         raise ConfigurationError(f"layer {name!r} was not used by the forward pass")
                     if cap.calls != 1:
@@ -237,190 +477,35 @@ def ghost_clipped_grad(
                             "one call per layer and step")
                 # Gradients with respect to the layer outputs only: autograd
                 # prunes the weight-gradient GEMMs, which the clipped sum replaces.
-                grads = torch.autograd.grad(losses.sum(), [c.out for c in captures],
+                grads = torch.autograd.grad(losses.sum(), [c.out for c in hooks],
                                             allow_unused=True)
         finally:
-            for c in captures:
+            for c in hooks:
                 c.remove()
-        dense, segmented = [], []
-        for (name, mod), cap, g in zip(layers, captures, grads):
+        B = losses.shape[0]
+        captures = []
+        for (name, mod), cap, g in zip(layers, hooks, grads):
             G = g.detach() if g is not None else torch.zeros_like(cap.out)
-            if cap.A.dtype != G.dtype:
-                G = G.to(cap.A.dtype)
-            if cap.segments is None:
-                layer = _Layer(name, mod, layer_group[name], _as_btd(cap.A, B).contiguous(),
-                               _as_btd(G, B).contiguous())
-                dense.append(layer)
-            else:
-                if mod.bias is not None:
-                    raise ConfigurationError(
-                        f"layer {name!r}: row-segmented layers with a bias are not supported")
-                if len(cap.segments) != B or sum(cap.segments) != cap.A.reshape(-1, cap.A.shape[-1]).shape[0]:
-                    raise ConfigurationError(
-                        f"layer {name!r}: dpc_row_segments must give B row counts that add up "
-                        "to the layer's input rows")
-                A2 = cap.A.reshape(-1, cap.A.shape[-1]).contiguous()
-                G2 = G.reshape(-1, G.shape[-1]).contiguous()
-                segmented.append(_Layer(name, mod, layer_group[name], A2, G2, cap.segments))
-            cap.out = None
-        device = losses.device
-
-        # Per-group, per-example squared norms.
-        sq = torch.zeros((n_groups, B), dtype=torch.float64, device=device)
-        for L in dense:
-            bias = L.mod.bias is not None
-            if L.A.shape[1] == 1:
-                ops.flat_sqnorms(L.A[:, 0], L.G[:, 0], with_bias=bias, out=sq[L.group])
-            else:
-                ops.gram_sqnorms(L.A, L.G, with_bias=bias, out=sq[L.group])
-        buckets = {}
-        for L in segmented:
-            key = (L.A.shape[1], L.G.shape[1], L.A.dtype)
-            buckets.setdefault(key, []).append(L)
-        bucket_layouts = []
-        for key, members in buckets.items():
-            layout = ops.SegmentLayout([L.segments for L in members], device)
-            seg_sq = ops.grouped_gram_sqnorms([L.A for L in members], [L.G for L in members],
-                                              layout)
-            for g in range(n_groups):
-                idx = [i for i, L in enumerate(members) if L.group == g]
-                if idx:
-                    sq[g] += seg_sq[idx].sum(dim=0)
-            bucket_layouts.append((members, layout))
-
-        # Guards for the materialised leaves the reference would clip.
-        sizes = []
-        for name, mod in layers:
-            sizes.append(mod.weight.numel())
-            if mod.bias is not None:
-                sizes.append(mod.bias.numel())
-        roundoff = num.norm_roundoff(torch.float32, torch.float64, len(sizes),
-                                     num.reduction_terms(sizes))
-        storage = sorted({L.A.dtype for L in dense + segmented}, key=str)
-        guards = [num.guard_constants(dt, torch.promote_types(dt, torch.float32), roundoff)
-                  for dt in storage]
-        cfs = [ops.clip_factors(sq[g], num.conservative_bound(bounds[g]), guards,
-                                count_threshold=num.float32_of(bounds[g]))
-               for g in range(n_groups)]
-
-        std = 0.0
-        gen = None
-        step_key = None
-        next_noise_state = None
-        if noise_fn is not None:
-            if noise_state is None:
-                raise ConfigurationError("noise_state is required with noise_fn")
-            std = noise_fn.clipped_stddev(clipped(None, max_norm=max_norm))
-            noisy = any((std.for_path(param_path(n)) if isinstance(std, PerGroup) else std) != 0.0
-                        for n in leaf_names)
-            if noisy and noise_fn.compute_dtype != torch.float32:
-                raise ConfigurationError("fused noise supports compute_dtype float32 only")
-            step_key = step_key_for(noise_state)
-            if noisy and noise_fn.stream == "reference":
-                gen = generator_from_key(step_key)
-            next_noise_state = GaussianNoiseState(
-                _step_counter=noise_state._step_counter + 1, _rng_key=noise_state._rng_key)
-
-        def leaf_std(leaf: str) -> float:
-            if isinstance(std, PerGroup):
-                return float(std.for_path(param_path(leaf)))
-            return float(std)
-
-        # Reference-stream draws: one generator, flatten order, no draw for a
-        # leaf whose standard deviation is 0.
-        draws = {}
-        if gen is not None:
-            shapes = {}
-            for name, mod in layers:
-                shapes[f"{name}.weight"] = tuple(mod.weight.shape)
-                if mod.bias is not None:
-                    shapes[f"{name}.bias"] = tuple(mod.bias.shape)
-            for leaf in leaf_names:
-                if leaf_std(leaf) != 0.0:
-                    draws[leaf] = torch.randn(shapes[leaf], dtype=torch.float32, generator=gen)
-
-        def to_dev(t):
-            return t.pin_memory().to(device, non_blocking=True)
-
-        tree = {}
-        for L in dense:
-            si = storage.index(L.A.dtype)
-            cf = cfs[L.group]
-            wn, bn = f"{L.name}.weight", f"{L.name}.bias"
-            spec = None
-            s_w = leaf_std(wn) if noise_fn is not None else 0.0
-            s_b = leaf_std(bn) if (noise_fn is not None and L.mod.bias is not None) else s_w
-            if s_w != s_b:
+            if cap.segments is None and cap.A.shape[0] != B:
                 raise ConfigurationError(
-                    f"layer {L.name!r}: weight and bias noise must share a standard deviation")
-            if s_w != 0.0:
-                if gen is not None:
-                    spec = ops.NoiseSpec(
-                        sigma=s_w, mode=nat.NOISE_INJECTED, noise=to_dev(draws[wn]),
-                        bias_noise=to_dev(draws[bn]) if L.mod.bias is not None else None)
-                else:
-                    spec = ops.NoiseSpec(sigma=s_w, mode=nat.NOISE_PHILOX, seed=step_key.seed,
-                                         leaf_id=leaf_index[wn],
-                                         bias_leaf_id=leaf_index.get(bn, 0))
-            w, b = ops.clipped_sum(L.A, L.G, cf.scale[si],
-                                   plan=cf.plan if len(storage) == 1 else None,
-                                   normalize_by=normalize_by, noise=spec,
-                                   out_dtype=dtype or L.mod.weight.dtype,
-                                   with_bias=L.mod.bias is not None)
-            tree[wn] = w
-            if L.mod.bias is not None:
-                tree[bn] = b
-        for members, layout in bucket_layouts:
-            si = storage.index(members[0].A.dtype)
-            seg_scale = torch.stack([cfs[L.group].scale[si] for L in members])
-            names = [f"{L.name}.weight" for L in members]
-            sigmas = [leaf_std(n) if noise_fn is not None else 0.0 for n in names]
-            gnoise = None
-            if any(s != 0.0 for s in sigmas):
-                if gen is not None:
-                    zero = None
-                    noise = []
-                    for n, L in zip(names, members):
-                        if n in draws:
-                            noise.append(to_dev(draws[n]))
-                        else:
-                            if zero is None:
-                                zero = torch.zeros(tuple(L.mod.weight.shape), dtype=torch.float32,
-                                                   device=device)
-                            noise.append(zero)
-                    gnoise = ops.GroupedNoise(sigmas=sigmas, mode=nat.NOISE_INJECTED, noise=noise)
-                else:
-                    gnoise = ops.GroupedNoise(sigmas=sigmas, mode=nat.NOISE_PHILOX,
-                                              seed=step_key.seed,
-                                              leaf_ids=[leaf_index[n] for n in names])
-            out_dtype = dtype or members[0].mod.weight.dtype
-            stacked = ops.grouped_clipped_sum([L.A for L in members], [L.G for L in members],
-                                              layout, seg_scale, normalize_by=normalize_by,
-                                              noise=gnoise, out_dtype=out_dtype)
-            for i, n in enumerate(names):
-                tree[n] = stacked[i]
-        tree = {k: tree[k] for k in leaf_names}
-        if noise_fn is None:
-            result = clipped(tree, max_norm=max_norm)
-        else:
-            result = NoisedPytree(pytree=tree, max_norm=max_norm, noise_stddev=std)
+                    f"layer {name!r}: its input does not have the batch as dim 0 (a layer fed "
+                    "with the rows of several examples must set dpc_row_segments)")
+            captures.append(LinearCapture(name=name, A=cap.A, G=G, has_bias=mod.bias is not None,
+                                          segments=cap.segments, param_dtype=mod.weight.dtype))
+            cap.out = None
+        out = ghost_clip_captured(captures, clipping_norm=clipping_norm,
+                                  normalize_by=normalize_by, noise_fn=noise_fn,
+                                  noise_state=noise_state, dtype=dtype, return_aux=return_aux)
+        if noise_fn is not None:
+            out, next_state = out
         if return_aux:
-            total = sq.sum(dim=0) if n_groups > 1 else sq[0]
-            group_norms = None
-            if per_group:
-                group_norms = {n: cfs[k].norms for k, n in enumerate(group_names)}
-            aux = GhostGradAux(
-                loss_values=losses.detach(),
-                grad_norms=torch.sqrt(total).to(torch.float32) if per_group else cfs[0].norms,
-                clip_scales=torch.stack([cf.scale for cf in cfs]) if per_group else cfs[0].scale,
-                num_clipped=torch.cat([cf.nclipped for cf in cfs]),
-                batch_size=B, group_norms=group_norms)
-            result = (result, aux)
+            result, aux = out
+            out = (result, replace(aux, loss_values=losses.detach()))
         if noise_fn is None:
-            return result, state
-        return result, state, next_noise_state
+            return out, state
+        return out, state, next_state
 
     return grad_fn, state0
 
 
-__all__ = ["GhostGradAux", "ghost_clipped_grad"]
+__all__ = ["GhostGradAux", "LinearCapture", "ghost_clip_captured", "ghost_clipped_grad"]
