@@ -273,7 +273,9 @@ def test_add_noise_device_stream_matches_c_oracle(dev, shape):
     y = ops.add_noise(x.to(dev), 1.0, mode=nat.NOISE_PHILOX, seed=seed, leaf_id=3).cpu()
     rows, cols = ops.leaf_view(x)
     want = torch.from_numpy(c_oracle.leaf_normals(seed, 3, rows, cols)).reshape(shape)
-    torch.testing.assert_close(y.double(), want, rtol=0, atol=2e-5)
+    # The device evaluates the transform in float (normals within 1e-6 of the
+    # double-precision formulas).
+    torch.testing.assert_close(y.double(), want, rtol=0, atol=5e-6)
 
 
 def test_clipped_sum_epilogue_noise_injected_bit_exact(dev):
