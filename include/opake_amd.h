@@ -194,12 +194,16 @@ int dpc_group_sum_f64(const double* x, int B, int n, int stride, const int32_t* 
  *
  * dpc_grouped_gram_sqnorms: seg_sq[v] = ||G_v^T A_v||^2 for every segment v
  *   (float64, written), the per-sample norms of the virtual experts that
- *   _streaming.py:70-82 would take of the materialised gradients.  `items`
- *   (device int32 [n_items][4]) lists (problem, first row, rows, pair) for
- *   every 128-row tile pair p <= q (pair = q (q + 1) / 2 + p) of every
- *   segment, segment by segment; seg_item_start (device int32 [S + 1]) gives
- *   each segment's item range.  max_rows bounds every segment's rows.
- *   ws: n_items float64.
+ *   _streaming.py:70-82 would take of the materialised gradients.  Problems
+ *   may differ in shape: `dims` is a HOST int32 array [n_problems][2] of
+ *   (din, dout), n_problems <= 64.  `items` (device int32 [n_items][4])
+ *   lists (problem << 16 | pair, first row, rows, slot) for every 128-row
+ *   tile pair p <= q (pair = q (q + 1) / 2 + p) of every segment, in any
+ *   order; an item whose first field is negative is skipped (padding).  With
+ *   n_items a multiple of 8, item l runs on XCD l / (n_items / 8).  slot is
+ *   the item's index in segment-major order, and seg_item_start (device int32
+ *   [S + 1]) gives each segment's slot range.  max_rows bounds every
+ *   segment's rows.  ws: n_items float64.
  * dpc_segment_plan: the step table of dpc_grouped_clipped_sum.  Segment v
  *   (rows seg_row0[v] .. + seg_len[v] of problem seg_group[v]; segments sorted
  *   by problem) contributes ceil(seg_len / 64) steps (row0, v << 7 | rows)
@@ -213,10 +217,10 @@ int dpc_group_sum_f64(const double* x, int B, int n, int stride, const int32_t* 
  *   rows (device int32 [E]) bounds each problem's operand rows; max_rows
  *   bounds rows.  Segments with scale 0 are never read.
  * -------------------------------------------------------------------------*/
-int dpc_grouped_gram_sqnorms(const int64_t* a_ptrs, const int64_t* g_ptrs, int din, int dout,
-                             int dtype, const int32_t* items, int n_items, int max_rows,
-                             const int32_t* seg_item_start, int S, double* seg_sq, void* ws,
-                             size_t ws_bytes, void* stream);
+int dpc_grouped_gram_sqnorms(const int64_t* a_ptrs, const int64_t* g_ptrs, const int32_t* dims,
+                             int n_problems, int dtype, const int32_t* items, int n_items,
+                             int max_rows, const int32_t* seg_item_start, int S, double* seg_sq,
+                             void* ws, size_t ws_bytes, void* stream);
 int dpc_segment_plan(const int32_t* seg_row0, const int32_t* seg_len, const int32_t* seg_group,
                      const float* seg_scale, int S, int E, int max_steps, int32_t* steps,
                      int32_t* step_start, void* stream);

@@ -96,8 +96,8 @@ SIGNATURES = {
     "dpc_row_sum_f64": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_void_p]),
     "dpc_grouped_gram_sqnorms": (
         _c_int,
-        [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_int, _c_void_p,
-         _c_int, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
+        [_c_void_p, _c_void_p, ctypes.POINTER(_c_int), _c_int, _c_int, _c_void_p, _c_int, _c_int,
+         _c_void_p, _c_int, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
     ),
     "dpc_segment_plan": (
         _c_int,

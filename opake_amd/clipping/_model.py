@@ -290,18 +290,29 @@ def ghost_clip_captured(
             ops.flat_sqnorms(L.A[:, 0], L.G[:, 0], with_bias=L.cap.has_bias, out=sq[L.group])
         else:
             ops.gram_sqnorms(L.A, L.G, with_bias=L.cap.has_bias, out=sq[L.group])
+    # The norms of all segmented layers of one dtype in one grouped launch
+    # (up to 64 layers each; mixed shapes, most expensive tile pairs first).
+    by_dtype = {}
+    for L in segmented:
+        by_dtype.setdefault(L.A.dtype, []).append(L)
+    cap = ops.SegmentLayout.MAX_GRAM_PROBLEMS
+    for members_all in by_dtype.values():
+        for c0 in range(0, len(members_all), cap):
+            members = members_all[c0:c0 + cap]
+            layout = ops.SegmentLayout([L.cap.segments for L in members], device,
+                                       gram_weights=[L.A.shape[1] + L.G.shape[1] for L in members])
+            seg_sq = ops.grouped_gram_sqnorms([L.A for L in members], [L.G for L in members],
+                                              layout)
+            for g in range(n_groups):
+                idx = [i for i, L in enumerate(members) if L.group == g]
+                if idx:
+                    sq[g] += seg_sq[idx].sum(dim=0)
+    # The clipped sums: one grouped launch per layer shape.
     buckets = {}
     for L in segmented:
         buckets.setdefault((L.A.shape[1], L.G.shape[1], L.A.dtype), []).append(L)
-    bucket_layouts = []
-    for members in buckets.values():
-        layout = ops.SegmentLayout([L.cap.segments for L in members], device)
-        seg_sq = ops.grouped_gram_sqnorms([L.A for L in members], [L.G for L in members], layout)
-        for g in range(n_groups):
-            idx = [i for i, L in enumerate(members) if L.group == g]
-            if idx:
-                sq[g] += seg_sq[idx].sum(dim=0)
-        bucket_layouts.append((members, layout))
+    bucket_layouts = [(members, ops.SegmentLayout([L.cap.segments for L in members], device))
+                      for members in buckets.values()]
 
     # Guards for the materialised leaves the reference would clip.
     sizes = [math.prod(shapes[n]) for n in leaf_names]

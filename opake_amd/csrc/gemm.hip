@@ -439,13 +439,16 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
     // step's (in-range) rows into the unused stage: every path issues the same
     // memory operations, which keeps the counter waits exact.
     float sc_next = 0.0f;
-    int row_next = 0, valid_next = kBK;
+    int row_next = 0, valid_next = kBK, valid_cur = kBK;
     auto k_step = [&](int s, const uint8_t* gcur, const uint8_t* acur, uint8_t* gnxt,
                       uint8_t* anxt) __attribute__((always_inline)) {
       dma_a(anxt, row_next, valid_next);
       float sc_after;
       int valid2;
       const int row2 = step_row0(min(s + 2, nsteps - 1), &sc_after, &valid2);
+      // Grouped mode: a segment's last step may hold fewer than 64 rows; the
+      // MFMAs of 16-row sub-steps past them (all zeros) are skipped.
+      const int vcur = kGrouped ? valid_cur : kBK;
       Frags f0, f1;
       read_frags(gcur, acur, 0, f0);
       read_frags(gcur, acur, 1, f1);
@@ -454,21 +457,22 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
       load_chunk(row2, valid2, 0);
       __builtin_amdgcn_sched_barrier(0);
       read_frags(gcur, acur, 2, f0);
-      mma(f1);
+      if (vcur > 16) mma(f1);
       store_chunk(gnxt, 1, sc_next);
       load_chunk(row2, valid2, 1);
       __builtin_amdgcn_sched_barrier(0);
       read_frags(gcur, acur, 3, f1);
-      mma(f0);
+      if (vcur > 32) mma(f0);
       store_chunk(gnxt, 2, sc_next);
       load_chunk(row2, valid2, 2);
       __builtin_amdgcn_sched_barrier(0);
-      mma(f1);
+      if (vcur > 48) mma(f1);
       store_chunk(gnxt, 3, sc_next);
       load_chunk(row2, valid2, 3);
       __builtin_amdgcn_sched_barrier(0);
       sc_next = sc_after;
       row_next = row2;
+      valid_cur = valid_next;
       valid_next = valid2;
       DPC_WAIT_VMCNT(4);
       __syncthreads();
@@ -480,6 +484,7 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
     // of G into the registers.
     int valid0;
     int row0 = step_row0(0, &sc_next, &valid0);
+    valid_cur = valid0;
     dma_a(lds_a0, row0, valid0);
 #pragma unroll
     for (int j = 0; j < 4; ++j) load_chunk(row0, valid0, j);

@@ -110,9 +110,11 @@ __device__ __forceinline__ void store_operand(uint8_t* tile, const u32x4_t r[2])
 }
 
 // acc[i][j] += X_p[rows wr*64 + i*32 ..] . X_q[rows wc*64 + j*32 ..] over the
-// 16-deep sub-step kk of a staged K step.
+// 16-deep sub-step kk of a staged K step.  `live` bit i (j + 2) says whether
+// the 32-row block i of the p tile (j of the q tile) holds rows of the
+// segment; blocks past its end are all zero, and their MFMAs are skipped.
 __device__ __forceinline__ void gram_mma(const uint8_t* tp, const uint8_t* tq, int kk,
-                                         f32x16_t acc[2][2]) {
+                                         f32x16_t acc[2][2], int live) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wr = w >> 1, wc = w & 1;
   const int c = kk * 2 + (lane >> 5);
@@ -122,20 +124,35 @@ __device__ __forceinline__ void gram_mma(const uint8_t* tp, const uint8_t* tq, i
     a[i] = *reinterpret_cast<const bf16x8_t*>(tp + gtile_off(wr * 64 + i * 32 + (lane & 31), c));
     b[i] = *reinterpret_cast<const bf16x8_t*>(tq + gtile_off(wc * 64 + i * 32 + (lane & 31), c));
   }
+  if (live == 15) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+      if ((live >> i & 1) && (live >> (j + 2) & 1))
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
 }
 
-// Grouped mode: work item l is (problem, first row, rows, pair) -- the tile
-// pair `pair` of the rows-long segment starting at `first row` of problem
-// `problem`'s operands (a_ptrs / g_ptrs); rows past the segment read as zero.
+// Grouped mode: work item l is (problem << 16 | pair, first row, rows, slot)
+// -- the tile pair `pair` of the rows-long segment starting at `first row` of
+// problem `problem`'s operands (a_ptrs / g_ptrs, widths din[problem] /
+// dout[problem]); rows past the segment read as zero; the result goes to
+// partial[slot].
+constexpr int kMaxGramProblems = 64;
+
 struct GramItems {
   const int32_t* items;  // [n_items][4]
   const int64_t* a_ptrs;
   const int64_t* g_ptrs;
+  int din[kMaxGramProblems];
+  int dout[kMaxGramProblems];
 };
 
 template <bool kGrouped>
@@ -149,12 +166,16 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
   if (l < 0) return;  // padding workgroup: exits before any barrier
   const uint16_t* Xa;
   const uint16_t* Xg;
-  int pair;
+  int pair, slot = l;
   if (kGrouped) {
     const int32_t* it = work.items + 4 * (size_t)l;
-    const int problem = it[0], row0 = it[1];
+    if (it[0] < 0) return;  // empty item: exits before any barrier
+    const int problem = it[0] >> 16, row0 = it[1];
+    pair = it[0] & 0xffff;
     T = it[2];
-    pair = it[3];
+    slot = it[3];
+    din = work.din[problem];
+    dout = work.dout[problem];
     Xa = reinterpret_cast<const uint16_t*>(work.a_ptrs[problem]) + (size_t)row0 * din;
     Xg = reinterpret_cast<const uint16_t*>(work.g_ptrs[problem]) + (size_t)row0 * dout;
   } else {
@@ -166,6 +187,15 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
   int p, q;
   pair_from_index(pair, &p, &q);
   const bool diag = (p == q);
+  int live = 0;
+  {
+    const int w = threadIdx.x >> 6, wr = w >> 1, wc = w & 1;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (p * kGramTile + wr * 64 + i * 32 < T) live |= 1 << i;
+      if (q * kGramTile + wc * 64 + i * 32 < T) live |= 1 << (i + 2);
+    }
+  }
 
   const GramOperand ap = make_operand(Xa, T, din, p * kGramTile);
   const GramOperand aq = make_operand(Xa, T, din, q * kGramTile);
@@ -221,15 +251,15 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
     const uint8_t* cgp = cur + 2 * kGTileBytes;
     const uint8_t* cgq = diag ? cgp : cur + 3 * kGTileBytes;
     if (s < nka) {
-      gram_mma(cap, caq, 0, pa);
-      gram_mma(cap, caq, 1, pa);
+      gram_mma(cap, caq, 0, pa, live);
+      gram_mma(cap, caq, 1, pa, live);
     }
     store_a(nxt);
     load_a(s + 2);
     __builtin_amdgcn_sched_barrier(0);
     if (s < nkg) {
-      gram_mma(cgp, cgq, 0, pg);
-      gram_mma(cgp, cgq, 1, pg);
+      gram_mma(cgp, cgq, 0, pg, live);
+      gram_mma(cgp, cgq, 1, pg, live);
     }
     store_g(nxt);
     load_g(s + 2);
@@ -247,7 +277,7 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
 #pragma unroll
       for (int r = 0; r < 16; ++r) sum += (double)pa[i][j][r] * (double)pg[i][j][r];
   double total = block_sum_f64(sum, red);
-  if (threadIdx.x == 0) partial[l] = diag ? total : 2.0 * total;  // dense: l = ex * npairs + pair
+  if (threadIdx.x == 0) partial[slot] = diag ? total : 2.0 * total;  // dense: slot = ex * npairs + pair
 }
 
 // Generic path (float32 inputs, or bf16 with d % 8 != 0): 64 x 64 tiles,
@@ -324,15 +354,17 @@ gram_generic_kernel(const In* __restrict__ A, const In* __restrict__ G, int T, i
 // sub-tile pairs; the inner products of the sub-tiles add up to the pair's.
 template <typename In>
 __global__ void __launch_bounds__(kGramThreads)
-gram_grouped_generic_kernel(GramItems work, int din, int dout, double* __restrict__ partial) {
+gram_grouped_generic_kernel(GramItems work, double* __restrict__ partial) {
   __shared__ float sp[kGenK][kGenTile + 1];
   __shared__ float sq[kGenK][kGenTile + 1];
   __shared__ double red[kGramThreads / 64];
   const int l = blockIdx.x;
   const int32_t* it = work.items + 4 * (size_t)l;
-  const int problem = it[0], row0 = it[1], rows = it[2];
+  if (it[0] < 0) return;  // empty item
+  const int problem = it[0] >> 16, row0 = it[1], rows = it[2], slot = it[3];
   int P, Q;
-  pair_from_index(it[3], &P, &Q);
+  pair_from_index(it[0] & 0xffff, &P, &Q);
+  const int din = work.din[problem], dout = work.dout[problem];
   const In* Xa = reinterpret_cast<const In*>(work.a_ptrs[problem]) + (size_t)row0 * din;
   const In* Xg = reinterpret_cast<const In*>(work.g_ptrs[problem]) + (size_t)row0 * dout;
   double s = 0.0;
@@ -347,7 +379,7 @@ gram_grouped_generic_kernel(GramItems work, int din, int dout, double* __restric
       for (int j = 0; j < 4; ++j) s += (double)pa[i][j] * (double)pg[i][j];
   }
   double total = block_sum_f64(s, red);
-  if (threadIdx.x == 0) partial[l] = (P == Q) ? total : 2.0 * total;
+  if (threadIdx.x == 0) partial[slot] = (P == Q) ? total : 2.0 * total;
 }
 
 // seg_sq[v] = sum of the partials of segment v's items (fixed order).
@@ -445,7 +477,7 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
     npairs = nt * (nt + 1) / 2;
     const int nblocks = npairs * B;
     const int padded = ceil_div(nblocks, kXcds) * kXcds;
-    GramItems none = {nullptr, nullptr, nullptr};
+    GramItems none = {};
     hipLaunchKernelGGL(gram_mfma_bf16_kernel<false>, dim3(padded), dim3(kGramMfmaThreads), 0, s,
                        (const uint16_t*)A, (const uint16_t*)G, T, din, dout, npairs, nblocks,
                        partial, none);
@@ -482,33 +514,46 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
   return DPC_OK;
 }
 
-extern "C" int dpc_grouped_gram_sqnorms(const int64_t* a_ptrs, const int64_t* g_ptrs, int din,
-                                        int dout, int dtype, const int32_t* items, int n_items,
-                                        int max_rows, const int32_t* seg_item_start, int S,
-                                        double* seg_sq, void* ws, size_t ws_bytes,
-                                        void* stream) {
-  if (din <= 0 || dout <= 0 || n_items < 0 || S < 0 || max_rows < 0) return DPC_EINVAL;
+extern "C" int dpc_grouped_gram_sqnorms(const int64_t* a_ptrs, const int64_t* g_ptrs,
+                                        const int32_t* dims, int n_problems, int dtype,
+                                        const int32_t* items, int n_items, int max_rows,
+                                        const int32_t* seg_item_start, int S, double* seg_sq,
+                                        void* ws, size_t ws_bytes, void* stream) {
+  if (n_problems < 1 || !dims || n_items < 0 || S < 0 || max_rows < 0) return DPC_EINVAL;
   if (dtype != DPC_F32 && dtype != DPC_BF16) return DPC_EINVAL;
+  if (n_problems > kMaxGramProblems) return DPC_ENOTSUP;
   if (S == 0) return DPC_OK;
   if (!seg_item_start || !seg_sq || (n_items > 0 && (!a_ptrs || !g_ptrs || !items || !ws)))
     return DPC_EINVAL;
   if (ws_bytes < (size_t)n_items * sizeof(double)) return DPC_ENOSPC;
+  GramItems work;
+  work.items = items;
+  work.a_ptrs = a_ptrs;
+  work.g_ptrs = g_ptrs;
+  bool aligned = true;
+  int dmax = 0;
+  for (int p = 0; p < kMaxGramProblems; ++p) {
+    work.din[p] = p < n_problems ? dims[2 * p] : 0;
+    work.dout[p] = p < n_problems ? dims[2 * p + 1] : 0;
+    if (p >= n_problems) continue;
+    if (work.din[p] <= 0 || work.dout[p] <= 0) return DPC_EINVAL;
+    aligned = aligned && work.din[p] % 8 == 0 && work.dout[p] % 8 == 0;
+    dmax = max(dmax, max(work.din[p], work.dout[p]));
+  }
   hipStream_t s = (hipStream_t)stream;
   double* partial = (double*)ws;
   if (n_items > 0) {
-    GramItems work = {items, a_ptrs, g_ptrs};
-    const size_t dmax = (size_t)(din > dout ? din : dout);
-    const bool fits = ((size_t)max_rows + kGramTile) * dmax * 2 < ((size_t)1 << 31);
-    if (dtype == DPC_BF16 && din % 8 == 0 && dout % 8 == 0 && fits) {
+    const bool fits = ((size_t)max_rows + kGramTile) * (size_t)dmax * 2 < ((size_t)1 << 31);
+    if (dtype == DPC_BF16 && aligned && fits) {
       const int padded = ceil_div(n_items, kXcds) * kXcds;
       hipLaunchKernelGGL(gram_mfma_bf16_kernel<true>, dim3(padded), dim3(kGramMfmaThreads), 0, s,
-                         nullptr, nullptr, 0, din, dout, 0, n_items, partial, work);
+                         nullptr, nullptr, 0, 0, 0, 0, n_items, partial, work);
     } else if (dtype == DPC_BF16) {
       hipLaunchKernelGGL(gram_grouped_generic_kernel<uint16_t>, dim3(n_items), dim3(kGramThreads),
-                         0, s, work, din, dout, partial);
+                         0, s, work, partial);
     } else {
       hipLaunchKernelGGL(gram_grouped_generic_kernel<float>, dim3(n_items), dim3(kGramThreads), 0,
-                         s, work, din, dout, partial);
+                         s, work, partial);
     }
     DPC_HIP_CHECK(hipGetLastError());
   }

@@ -200,12 +200,48 @@ class SegmentLayout:
 
     ``lengths[e][k]`` is the number of rows of segment k of problem e; problem
     e's rows are its segments in order.  Segment ``v = e * K + k`` (K segments
-    per problem, e.g. K = batch size).  The device tables (segment first rows
-    and lengths, Gram work items) are built once per layout and copied in one
-    transfer.
+    per problem, e.g. K = batch size).  ``gram_weights[e]`` (default 1) is the
+    relative cost of a Gram tile pair of problem e (its din + dout): the Gram
+    work items are issued most expensive first, so that a launch over problems
+    of different widths ends evenly.  The device tables (segment first rows and
+    lengths, Gram work items) are copied in one transfer.
     """
 
-    def __init__(self, lengths, device):
+    MAX_GRAM_PROBLEMS = 64
+    XCDS = 8
+
+    @classmethod
+    def _xcd_schedule(cls, items, cost, seg_of_item, item_start):
+        """Order Gram items for the kernel's XCD placement (item l of a launch of
+        8 * per runs on XCD l // per): segments go whole to the least loaded of
+        8 bins, most expensive first, so each XCD gets a balanced share, works
+        through it most expensive first and keeps a segment's tile pairs (which
+        re-read the same rows) together in its L2.  Bins are padded to equal
+        length with empty items (problem field -1)."""
+        import numpy as np
+
+        n_seg = len(item_start) - 1
+        seg_cost = np.zeros(n_seg)
+        np.add.at(seg_cost, seg_of_item, cost)
+        bins = [[] for _ in range(cls.XCDS)]
+        load = np.zeros(cls.XCDS)
+        for v in np.argsort(-seg_cost, kind="stable"):
+            if item_start[v + 1] == item_start[v]:
+                continue
+            b = int(np.argmin(load))
+            bins[b].append(v)
+            load[b] += seg_cost[v]
+        per = max((sum(int(item_start[v + 1] - item_start[v]) for v in b) for b in bins), default=0)
+        out = np.zeros((cls.XCDS * per, 4), dtype=np.int64)
+        out[:, 0] = -1
+        for x, b in enumerate(bins):
+            rows = [items[item_start[v]:item_start[v + 1]] for v in b]
+            if rows:
+                chunk = np.concatenate(rows)
+                out[x * per:x * per + len(chunk)] = chunk
+        return out
+
+    def __init__(self, lengths, device, gram_weights=None):
         import numpy as np
 
         lens = np.asarray(lengths, dtype=np.int64)
@@ -218,32 +254,49 @@ class SegmentLayout:
         self.max_rows = int(self.rows.max()) if self.E else 0
         if self.max_rows >= 1 << 30:
             raise ConfigurationError("too many rows in one problem")
+        weights = np.ones(self.E) if gram_weights is None else np.asarray(gram_weights, float)
         flat = lens.reshape(-1)
         row0 = (np.cumsum(lens, axis=1) - lens).reshape(-1)
         group = np.repeat(np.arange(self.E, dtype=np.int64), self.K)
         nt = (flat + _GRAM_TILE - 1) // _GRAM_TILE
         npairs = nt * (nt + 1) // 2
+        if npairs.size and npairs.max() >= 1 << 16:
+            raise ConfigurationError("a segment is too long for the grouped Gram kernel")
         item_start = np.concatenate([[0], np.cumsum(npairs)])
         self.n_items = int(item_start[-1])
         seg_of_item = np.repeat(np.arange(self.S), npairs)
         pair = np.arange(self.n_items) - item_start[seg_of_item]
-        items = np.stack([group[seg_of_item], row0[seg_of_item], flat[seg_of_item], pair], axis=1)
+        # Cost of a pair: the problem's weight times the live 32-row blocks of
+        # both tiles (blocks past the segment's end are skipped).
+        q = ((np.sqrt(8 * pair + 1) - 1) // 2).astype(np.int64)
+        q = np.where((q + 1) * (q + 2) // 2 <= pair, q + 1, q)
+        pp = pair - q * (q + 1) // 2
+        seg_len = flat[seg_of_item]
+
+        def live_rows(t):
+            rows = np.clip(seg_len - t * _GRAM_TILE, 0, _GRAM_TILE)
+            return (rows + 31) // 32
+
+        cost = weights[group[seg_of_item]] * live_rows(pp) * live_rows(q)
+        slot = np.arange(self.n_items)
+        items = np.stack([(group[seg_of_item] << 16) | pair, row0[seg_of_item], seg_len, slot],
+                         axis=1)
+        items = self._xcd_schedule(items, cost, seg_of_item, item_start)
         self.max_steps = int(((flat + _STEP_ROWS - 1) // _STEP_ROWS).sum())
         # One int32 buffer: row0 [S] | len [S] | group [S] | rows [E] |
         # item_start [S + 1] | items [n_items * 4].
         parts = [row0, flat, group, self.rows, item_start, items.reshape(-1)]
         host = torch.from_numpy(np.concatenate(parts).astype(np.int32))
-        buf = host.pin_memory().to(device, non_blocking=True) if torch.device(device).type == "cuda" \
-            else host
+        if torch.device(device).type == "cuda":
+            buf = host.pin_memory().to(device, non_blocking=True)
+        else:
+            buf = host
         offs = np.cumsum([0] + [len(p) for p in parts])
         (self.seg_row0, self.seg_len, self.seg_group, self.rows_dev, self.item_start,
          self.items) = [buf[offs[i]:offs[i + 1]] for i in range(len(parts))]
+        self.n_launch_items = len(items)
         self._buf = buf
         self.device = torch.device(device)
-
-    def example_of_segment(self):
-        """Column index k of every segment (int64 [S], on the device)."""
-        return torch.arange(self.S, device=self.device) % self.K
 
 
 def _ptr_table(tensors, device) -> torch.Tensor:
@@ -251,7 +304,7 @@ def _ptr_table(tensors, device) -> torch.Tensor:
     return host.pin_memory().to(device, non_blocking=True)
 
 
-def _check_grouped(A_list, G_list, layout: SegmentLayout):
+def _check_grouped(A_list, G_list, layout: SegmentLayout, *, same_shape: bool):
     if len(A_list) != layout.E or len(G_list) != layout.E:
         raise ConfigurationError("one A and one G per problem of the layout are required")
     if layout.E == 0:
@@ -260,8 +313,10 @@ def _check_grouped(A_list, G_list, layout: SegmentLayout):
     for e, (A, G) in enumerate(zip(A_list, G_list)):
         if A.dim() != 2 or G.dim() != 2 or A.shape[0] != G.shape[0]:
             raise ConfigurationError("grouped operands must be A_e [rows, din], G_e [rows, dout]")
-        if A.shape[1] != din or G.shape[1] != dout or A.dtype != dtype or G.dtype != dtype:
-            raise ConfigurationError("grouped problems must share din, dout and dtype")
+        if A.dtype != dtype or G.dtype != dtype:
+            raise ConfigurationError("grouped problems must share a dtype")
+        if same_shape and (A.shape[1] != din or G.shape[1] != dout):
+            raise ConfigurationError("grouped problems must share din and dout")
         if A.shape[0] != int(layout.rows[e]):
             raise ConfigurationError(
                 f"problem {e} has {A.shape[0]} rows, its segments {int(layout.rows[e])}")
@@ -271,15 +326,21 @@ def _check_grouped(A_list, G_list, layout: SegmentLayout):
 
 
 def grouped_gram_sqnorms(A_list, G_list, layout: SegmentLayout) -> torch.Tensor:
-    """``||G_v^T A_v||^2`` for every segment v of the layout: float64 [E, K]."""
+    """``||G_v^T A_v||^2`` for every segment v of the layout: float64 [E, K].
+
+    Problems may differ in din / dout (at most 64 problems per call)."""
     dev = nat.require_device(*A_list, *G_list)
-    din, dout, dtype = _check_grouped(A_list, G_list, layout)
+    _, _, dtype = _check_grouped(A_list, G_list, layout, same_shape=False)
+    if layout.E > SegmentLayout.MAX_GRAM_PROBLEMS:
+        raise ConfigurationError("at most 64 problems per grouped Gram call")
+    dims = (ctypes.c_int * (2 * layout.E))(
+        *[v for A, G in zip(A_list, G_list) for v in (A.shape[1], G.shape[1])])
     seg_sq = torch.empty((layout.E, layout.K), dtype=torch.float64, device=dev)
-    ws = torch.empty(max(layout.n_items, 1), dtype=torch.float64, device=dev)
+    ws = torch.empty(max(layout.n_launch_items, 1), dtype=torch.float64, device=dev)
     a_ptrs, g_ptrs = _ptr_table(A_list, dev), _ptr_table(G_list, dev)
     nat.call(
-        "dpc_grouped_gram_sqnorms", nat.ptr(a_ptrs), nat.ptr(g_ptrs), din, dout,
-        nat.dtype_code(dtype), nat.ptr(layout.items), layout.n_items, layout.max_rows,
+        "dpc_grouped_gram_sqnorms", nat.ptr(a_ptrs), nat.ptr(g_ptrs), dims, layout.E,
+        nat.dtype_code(dtype), nat.ptr(layout.items), layout.n_launch_items, layout.max_rows,
         nat.ptr(layout.item_start), layout.S, nat.ptr(seg_sq), nat.ptr(ws),
         ws.numel() * 8, nat.stream_handle(dev),
     )
@@ -316,7 +377,7 @@ def grouped_clipped_sum(
     scale 0 are never read.
     """
     dev = nat.require_device(*A_list, *G_list, seg_scale)
-    din, dout, dtype = _check_grouped(A_list, G_list, layout)
+    din, dout, dtype = _check_grouped(A_list, G_list, layout, same_shape=True)
     if seg_scale.dtype != torch.float32 or tuple(seg_scale.shape) != (layout.E, layout.K):
         raise ConfigurationError("seg_scale must be float32 [E, K]")
     seg_scale = _contig(seg_scale)

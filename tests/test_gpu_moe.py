@@ -71,6 +71,28 @@ def test_grouped_gram_sqnorms_match_segment_grads(dev, dtype, din, dout):
                 assert abs(got[e, k].item() - sq[k].item()) <= tol * sq[k].item(), (e, k)
 
 
+@pytest.mark.parametrize("dtype,shapes", [
+    (torch.bfloat16, [(64, 96), (128, 40), (32, 256)]),
+    (torch.bfloat16, [(64, 96), (36, 40), (32, 256)]),  # one misaligned width: generic kernel
+    (torch.float32, [(24, 16), (40, 8), (8, 48)]),
+])
+def test_grouped_gram_mixed_shapes_cost_ordered(dev, dtype, shapes):
+    gen = torch.Generator().manual_seed(17)
+    As, Gs = [], []
+    for lens, (din, dout) in zip(LENGTHS, shapes):
+        rows = sum(lens)
+        As.append(torch.randn(rows, din, generator=gen).to(dtype))
+        Gs.append((torch.randn(rows, dout, generator=gen) * 0.1).to(dtype))
+    layout = ops.SegmentLayout(LENGTHS, dev, gram_weights=[a + b for a, b in shapes])
+    got = ops.grouped_gram_sqnorms([a.to(dev) for a in As], [g.to(dev) for g in Gs], layout)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    for e, lens in enumerate(LENGTHS):
+        want = (ghost_oracle.segment_grads(As[e], Gs[e], lens, dtype=torch.float64) ** 2).sum(
+            dim=(1, 2))
+        for k in range(len(lens)):
+            assert abs(got[e, k].item() - want[k].item()) <= tol * want[k].item(), (e, k)
+
+
 @pytest.mark.parametrize("dtype,din,dout", [(torch.float32, 40, 24), (torch.bfloat16, 264, 136),
                                             (torch.bfloat16, 36, 20)])
 @pytest.mark.parametrize("out_dtype", [None, torch.float32])
