@@ -33,7 +33,7 @@
 namespace {
 
 constexpr int kBM = 256, kBN = 256, kBK = 64, kThreads = 256;
-constexpr int kFastThreads = 512;  // 8 waves
+constexpr int kFastWaves = 8;
 
 // LDS layout of one operand tile for a 64-deep K step: 64 rows (k) of 256
 // bf16 (512 bytes), the row's eight 64-byte blocks permuted by XOR with
@@ -254,8 +254,19 @@ constexpr int kGLdsBytes = (2 * kOperandBytes > kQuarterRows * kEpiLd * 4)
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 
-template <bool kGrouped>
-__global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastArgs args) {
+// The body of the fast kernel for one 256 x 256 output tile.  kWaves = 8:
+// waves of 128 x 64 (2 per SIMD); kWaves = 4: waves of 128 x 128 (1 per SIMD,
+// accumulators in AGPRs; half the LDS fragment traffic per MFMA).
+template <bool kGrouped, int kWaves>
+__device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
+  constexpr int kT = kWaves * 64;           // threads
+  constexpr int kWavesN = kWaves / 2;       // waves along the tile columns
+  constexpr int kWC = kBN / kWavesN;        // columns of a wave tile
+  constexpr int kNB = kWC / 32;             // 32-column MFMA blocks of a wave tile
+  constexpr int kRowsPerPass = kT / 32;     // G rows staged per pass of all threads
+  constexpr int kGC = kBK / kRowsPerPass;   // G chunks per thread per K step
+  constexpr int kGCSub = kGC / 4;           // ... stored per 16-deep sub-step
+  constexpr int kDma = 32 / kWaves;         // 1 KiB A transfers per wave per K step
   __shared__ __attribute__((aligned(16))) uint8_t lds_g[kGLdsBytes];
   __shared__ __attribute__((aligned(16))) uint8_t lds_a0[kOperandBytes];
   __shared__ __attribute__((aligned(16))) uint8_t lds_a1[kOperandBytes];
@@ -271,7 +282,7 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
   tile_coords(lin, tiles_m, tiles_n, &tm, &tn);
   const int m0 = tm * kBM, n0 = tn * kBN;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int wm = w >> 2, wn = w & 3;  // wave tile: rows wm * 128 of G^T, wn * 64 of A
+  const int wm = w / kWavesN, wn = w % kWavesN;  // wave tile: rows wm * 128, columns wn * kWC
 
   Epilogue ep = args.ep;
   const uint16_t* Abase = args.A;
@@ -293,7 +304,7 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
     // the A tile starts from zeros so that whatever such a fetch leaves in LDS
     // is finite.
     const u32x4_t zero = {0u, 0u, 0u, 0u};
-    for (int i = tid * 16; i < kOperandBytes; i += kFastThreads * 16) {
+    for (int i = tid * 16; i < kOperandBytes; i += kT * 16) {
       *reinterpret_cast<u32x4_t*>(lds_a0 + i) = zero;
       *reinterpret_cast<u32x4_t*>(lds_a1 + i) = zero;
     }
@@ -304,11 +315,11 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
     total_rows = args.B * T;
   }
 
-  f32x16_t acc[4][2];
+  f32x16_t acc[4][kNB];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
+    for (int j = 0; j < kNB; ++j) acc[i][j] = f32x16_t{};
 
   if (nsteps > 0) {
     __amdgpu_buffer_rsrc_t g_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -355,32 +366,34 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
       return ex * T + (t % spe) * kBK;
     };
 
-    // G staging: chunk j (< 4) of this thread is tile row r0 + 16 j, columns
-    // col .. col + 8; columns outside the matrix read as zero.  Row r0 + 16 j
-    // has the same swizzle as row r0, so chunk j is st_off + j * 16 rows.
+    // G staging: chunk j (< kGC) of this thread is tile row r0 + kRowsPerPass j,
+    // columns col .. col + 8; columns outside the matrix read as zero.  That
+    // row has the same swizzle as row r0 (kRowsPerPass is a multiple of 8), so
+    // chunk j is st_off + j * kRowsPerPass rows.
     const int r0 = tid >> 5, col = (tid & 31) * 8;
     const int st_off = tile_off(r0, col);
     const int g_voff = (m0 + col) * 2;
     const int g_bad = (m0 + col < M) ? 0 : kOutOfRange;
-    u32x4_t g[4];
+    u32x4_t g[kGC];
     auto load_chunk = [&](int row0, int valid, int j) __attribute__((always_inline)) {
       const int row = row0 + r0;
-      const int bad = (kGrouped && r0 + 16 * j >= valid) ? kOutOfRange : g_bad;
+      const int bad = (kGrouped && r0 + kRowsPerPass * j >= valid) ? kOutOfRange : g_bad;
       g[j] = __builtin_amdgcn_raw_buffer_load_b128(g_rsrc, (row * M * 2 + g_voff) | bad,
-                                                   j * 16 * M * 2, 0);
+                                                   j * kRowsPerPass * M * 2, 0);
     };
     auto store_chunk = [&](uint8_t* gstage, int j, float sc) __attribute__((always_inline)) {
-      *reinterpret_cast<u32x4_t*>(gstage + st_off + j * 16 * kRowBytes) = scale_chunk(g[j], sc);
+      *reinterpret_cast<u32x4_t*>(gstage + st_off + j * kRowsPerPass * kRowBytes) =
+          scale_chunk(g[j], sc);
     };
     // A goes straight from memory into LDS (buffer_load ... lds): wave w's
-    // instruction j fills the 1 KiB at (w * 4 + j) * 1024 of the A tile, lane
-    // i the 16 bytes at i * 16 -- row (w * 4 + j) * 2 + i / 32, physical
-    // 16-byte slot i % 32, which holds logical columns
+    // instruction j fills the 1 KiB at (w * kDma + j) * 1024 of the A tile,
+    // lane i the 16 bytes at i * 16 -- row (w * kDma + j) * 2 + i / 32,
+    // physical 16-byte slot i % 32, which holds logical columns
     // (((i % 32) / 4) ^ (row & 7)) * 32 + (i % 4) * 8.
-    int dma_voff[4], dma_bad[4], dma_row[4];
+    int dma_voff[kDma], dma_bad[kDma], dma_row[kDma];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = (w * 4 + j) * 2 + (lane >> 5);
+    for (int j = 0; j < kDma; ++j) {
+      const int row = (w * kDma + j) * 2 + (lane >> 5);
       const int slot = lane & 31;
       const int acol = (((slot >> 2) ^ (row & 7)) << 5) + (slot & 3) * 8;
       dma_row[j] = row;
@@ -389,25 +402,26 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
     }
     auto dma_a = [&](uint8_t* astage, int row0, int valid) __attribute__((always_inline)) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < kDma; ++j) {
         const int bad = (kGrouped && dma_row[j] >= valid) ? kOutOfRange : dma_bad[j];
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            a_rsrc, (__attribute__((address_space(3))) void*)((lds_u8_t*)astage + (w * 4 + j) * 1024),
+            a_rsrc,
+            (__attribute__((address_space(3))) void*)((lds_u8_t*)astage + (w * kDma + j) * 1024),
             16, (row0 * N * 2 + dma_voff[j]) | bad, 0, 0, 0);
       }
     };
 
-    int goff[4][2], aoff[2][2];
+    int goff[4][2], aoff[kNB][2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) goff[i][h] = frag_off(wm * 128 + i * 32, h, lane);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) aoff[j][h] = frag_off(wn * 64 + j * 32, h, lane);
+      for (int j = 0; j < kNB; ++j) aoff[j][h] = frag_off(wn * kWC + j * 32, h, lane);
     }
-    // Fragments of K sub-step kk: 4 of G^T (rows) and 2 of A (columns).
+    // Fragments of K sub-step kk: 4 of G^T (rows) and kNB of A (columns).
     struct Frags {
-      bf16x8_t a[4], b[2];
+      bf16x8_t a[4], b[kNB];
     };
     auto read_frags = [&](const uint8_t* gstage, const uint8_t* astage, int kk, Frags& f) __attribute__((always_inline)) {
       const int kofs = kk * 16 * kRowBytes;
@@ -415,26 +429,26 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
       for (int i = 0; i < 4; ++i)
         f.a[i] = join_frag(read_tr(gstage, goff[i][0] + kofs), read_tr(gstage, goff[i][1] + kofs));
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < kNB; ++j)
         f.b[j] = join_frag(read_tr(astage, aoff[j][0] + kofs), read_tr(astage, aoff[j][1] + kofs));
     };
     auto mma = [&](const Frags& f) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < kNB; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
     };
 
     // One K step on stage (gcur, acur), staging step s + 1 into (gnxt, anxt):
     // the DMA of A's step s + 1 is issued first; then K sub-step kk's MFMAs,
-    // after which chunk kk of G's step s + 1 goes from the registers (scaled)
-    // into the other stage and the same registers are refilled with chunk kk
-    // of step s + 2 -- each load is in flight for a whole step.  Fragments are
+    // after which G chunks kk * kGCSub .. of step s + 1 go from the registers
+    // (scaled) into the other stage and the same registers are refilled with
+    // those chunks of step s + 2 -- each load is in flight for a whole step.  Fragments are
     // double-buffered (sub-step kk + 1's reads are issued before sub-step kk's
     // MFMAs), and the sched_barriers keep each chunk's store and reload inside
     // its sub-step (the scheduler would otherwise sink all loads to the end of
-    // the step).  Before the barrier only the 4 G loads may still be
+    // the step).  Before the barrier only the kGC G loads may still be
     // outstanding.  Past the last step the stores and loads repeat the last
     // step's (in-range) rows into the unused stage: every path issues the same
     // memory operations, which keeps the counter waits exact.
@@ -450,31 +464,33 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
       // MFMAs of 16-row sub-steps past them (all zeros) are skipped.
       const int vcur = kGrouped ? valid_cur : kBK;
       Frags f0, f1;
+      auto stage_g = [&](int kk) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < kGCSub; ++c) store_chunk(gnxt, kk * kGCSub + c, sc_next);
+#pragma unroll
+        for (int c = 0; c < kGCSub; ++c) load_chunk(row2, valid2, kk * kGCSub + c);
+      };
       read_frags(gcur, acur, 0, f0);
       read_frags(gcur, acur, 1, f1);
       mma(f0);
-      store_chunk(gnxt, 0, sc_next);
-      load_chunk(row2, valid2, 0);
+      stage_g(0);
       __builtin_amdgcn_sched_barrier(0);
       read_frags(gcur, acur, 2, f0);
       if (vcur > 16) mma(f1);
-      store_chunk(gnxt, 1, sc_next);
-      load_chunk(row2, valid2, 1);
+      stage_g(1);
       __builtin_amdgcn_sched_barrier(0);
       read_frags(gcur, acur, 3, f1);
       if (vcur > 32) mma(f0);
-      store_chunk(gnxt, 2, sc_next);
-      load_chunk(row2, valid2, 2);
+      stage_g(2);
       __builtin_amdgcn_sched_barrier(0);
       if (vcur > 48) mma(f1);
-      store_chunk(gnxt, 3, sc_next);
-      load_chunk(row2, valid2, 3);
+      stage_g(3);
       __builtin_amdgcn_sched_barrier(0);
       sc_next = sc_after;
       row_next = row2;
       valid_cur = valid_next;
       valid_next = valid2;
-      DPC_WAIT_VMCNT(4);
+      DPC_WAIT_VMCNT(kGC);
       __syncthreads();
     };
 
@@ -487,13 +503,13 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
     valid_cur = valid0;
     dma_a(lds_a0, row0, valid0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) load_chunk(row0, valid0, j);
+    for (int j = 0; j < kGC; ++j) load_chunk(row0, valid0, j);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) store_chunk(g0, j, sc_next);
+    for (int j = 0; j < kGC; ++j) store_chunk(g0, j, sc_next);
     row_next = step_row0(min(1, nsteps - 1), &sc_next, &valid_next);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) load_chunk(row_next, valid_next, j);
-    DPC_WAIT_VMCNT(4);  // the A DMA of step 0 has landed (4 G loads may be in flight)
+    for (int j = 0; j < kGC; ++j) load_chunk(row_next, valid_next, j);
+    DPC_WAIT_VMCNT(kGC);  // the A DMA of step 0 has landed (kGC G loads may be in flight)
     __syncthreads();
     int s = 0;
     for (; s + 1 < nsteps; s += 2) {
@@ -505,10 +521,11 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
   }
 
   // Epilogue: the 256 x 256 fp32 tile goes through LDS in four quarters of 64
-  // rows; each of the 512 threads owns a pair of adjacent columns and 16 of
+  // rows; each thread owns a pair of adjacent columns and 64 / (kT / 128) of
   // the quarter's rows, walked in even/odd row pairs: coalesced 4- or 8-byte
   // stores, and one Philox block per (row pair, column) in a rolled loop.
   float* tile = reinterpret_cast<float*>(lds_g);
+  constexpr int kEpiRows = kQuarterRows / (kT / 128);
   // Unrolled: the accumulator blocks are selected by compile-time indices
   // (a runtime index would move them to scratch memory).
 #pragma unroll
@@ -518,20 +535,20 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
       for (int ii = 0; ii < 2; ++ii) {
         const int i = 2 * (quarter & 1) + ii;
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < kNB; ++j)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int ml = ii * 32 + (r >> 2) * 8 + 4 * (lane >> 5) + (r & 3);
-            const int nl = wn * 64 + j * 32 + (lane & 31);
+            const int nl = wn * kWC + j * 32 + (lane & 31);
             tile[ml * kEpiLd + nl] = acc[i][j][r];
           }
       }
     }
     __syncthreads();
     const int cl = 2 * (tid & 127);
-    const int rr = (tid >> 7) * 16;
+    const int rr = (tid >> 7) * kEpiRows;
 #pragma unroll 2
-    for (int ml = rr; ml < rr + 16; ml += 2) {
+    for (int ml = rr; ml < rr + kEpiRows; ml += 2) {
       const float2 t0 = *reinterpret_cast<const float2*>(tile + ml * kEpiLd + cl);
       const float2 t1 = *reinterpret_cast<const float2*>(tile + (ml + 1) * kEpiLd + cl);
       const float v[2][2] = {{t0.x, t0.y}, {t1.x, t1.y}};
@@ -539,6 +556,19 @@ __global__ void __launch_bounds__(kFastThreads, 1) clipped_sum_bf16_kernel(FastA
     }
     __syncthreads();
   }
+}
+
+// 8 waves (2 per SIMD) measure faster than the 4-wave 128 x 128 layout on
+// both the dense and the grouped workloads.  (Launch bounds must not depend on
+// a template parameter: the host stub of such a kernel is not emitted.)
+template <bool kGrouped>
+__global__ void __launch_bounds__(kFastWaves * 64, 1) clipped_sum_bf16_kernel(FastArgs args) {
+  clipped_sum_tile<kGrouped, kFastWaves>(args);
+}
+
+template <bool kGrouped>
+void launch_fast(dim3 grid, hipStream_t s, const FastArgs& args) {
+  hipLaunchKernelGGL(clipped_sum_bf16_kernel<kGrouped>, grid, dim3(kFastWaves * 64), 0, s, args);
 }
 
 #undef DPC_WAIT_VMCNT
@@ -847,8 +877,7 @@ extern "C" int dpc_grouped_clipped_sum(const int64_t* a_ptrs, const int64_t* g_p
     args.grp = grp;
     const long long ntiles = (long long)ceil_div(dout, kBM) * ceil_div(din, kBN) * E;
     if (ntiles > 0x7fffffff) return DPC_ENOTSUP;
-    hipLaunchKernelGGL(clipped_sum_bf16_kernel<true>, dim3((unsigned)ntiles), dim3(kFastThreads),
-                       0, s, args);
+    launch_fast<true>(dim3((unsigned)ntiles), s, args);
   } else {
     dim3 grid(ceil_div(din, kGT), ceil_div(dout, kGT), E);
     if (dtype == DPC_BF16) {
@@ -920,7 +949,7 @@ extern "C" int dpc_clipped_sum(const void* A, const void* G, const float* scale,
     args.scale = scale;
     args.ep = ep;
     const int ntiles = ceil_div(dout, kBM) * ceil_div(din, kBN);
-    hipLaunchKernelGGL(clipped_sum_bf16_kernel<false>, dim3(ntiles), dim3(kFastThreads), 0, s, args);
+    launch_fast<false>(dim3(ntiles), s, args);
   } else {
     dim3 grid(ceil_div(din, kGT), ceil_div(dout, kGT));
     if (dtype == DPC_BF16) {
