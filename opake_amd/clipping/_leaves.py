@@ -181,6 +181,72 @@ class LeafClipResult:
     scales: dict
 
 
+class LeafBatch:
+    """Stacked per-example leaves ``[B, *P]`` prepared for the leaf kernels:
+    the tile tables per storage dtype and the device pointer tables.  The
+    leaves must stay alive (and unchanged) while the batch is in use."""
+
+    def __init__(self, leaves):
+        self.leaves = [l if l.is_contiguous() else l.contiguous() for l in leaves]
+        self.device = self.leaves[0].device
+        self.B = self.leaves[0].shape[0]
+        self.L = len(self.leaves)
+        self.plan = _plan(self.leaves, self.device)
+        self.ptr_tables = []
+        for g in self.plan["groups"]:
+            ptrs = torch.tensor([self.leaves[i].data_ptr() for i in g["idx"]], dtype=torch.int64)
+            self.ptr_tables.append(ptrs.pin_memory().to(self.device, non_blocking=True))
+
+    @property
+    def dtypes(self):
+        return [g["dtype"] for g in self.plan["groups"]]
+
+    def sqnorms(self) -> torch.Tensor:
+        """Per-leaf squared norms float64 [B, L] (``_leaf_sq_sum``: sanitised,
+        squared in float32, summed in float64 per 2048-element tile)."""
+        B, L = self.B, self.L
+        stream = nat.stream_handle(self.device)
+        leaf_sq = torch.empty((B, L), dtype=torch.float64, device=self.device)
+        for g, ptrs in zip(self.plan["groups"], self.ptr_tables):
+            partial = torch.empty((B, max(g["n_tiles"], 1)), dtype=torch.float64, device=self.device)
+            nat.call("dpc_leaves_sqnorm", nat.ptr(ptrs), nat.ptr(g["sizes"]),
+                     nat.ptr(g["tile_leaf"]), nat.ptr(g["tile_local"]), nat.ptr(g["tile_start"]),
+                     nat.ptr(g["leaf_col"]), len(g["idx"]), g["n_tiles"], B,
+                     nat.dtype_code(g["dtype"]), nat.ptr(partial), nat.ptr(leaf_sq), L, stream)
+        return leaf_sq
+
+    def apply(self, scale_rows: dict, leaf_rows=None, out_dtypes=None, with_postsq=False):
+        """Scale-store-sum over the batch: leaf l of storage dtype t uses row
+        ``leaf_rows[l]`` (default 0) of ``scale_rows[t]`` (float32 [R, B]).
+        Returns ``(reduced, post_sq)``; ``post_sq`` is float32 [B] or None."""
+        B = self.B
+        stream = nat.stream_handle(self.device)
+        reduced = [None] * self.L
+        post_sq = torch.zeros(B, dtype=torch.float32, device=self.device) if with_postsq else None
+        for g, ptrs in zip(self.plan["groups"], self.ptr_tables):
+            dtype = g["dtype"]
+            out_dtype = (out_dtypes or {}).get(dtype, dtype)
+            flat = torch.empty(g["total"], dtype=out_dtype, device=self.device)
+            tile_sq = (torch.empty((B, g["n_tiles"]), dtype=torch.float32, device=self.device)
+                       if with_postsq else None)
+            rows = scale_rows[dtype]
+            leaf_row = None
+            if leaf_rows is not None:
+                idx_rows = [leaf_rows[i] for i in g["idx"]]
+                leaf_row = _device_table(self.device, ("leaf_row", dtype, tuple(idx_rows)),
+                                         idx_rows, np.int32)
+            nat.call("dpc_leaves_apply", nat.ptr(ptrs), nat.ptr(g["sizes"]),
+                     nat.ptr(g["tile_leaf"]), nat.ptr(g["tile_local"]), nat.ptr(g["out_offs"]),
+                     g["n_tiles"], B, nat.dtype_code(dtype), nat.ptr(rows), nat.ptr(leaf_row),
+                     nat.ptr(flat), nat.dtype_code(out_dtype), nat.ptr(tile_sq), stream)
+            if with_postsq:
+                post_sq += tile_sq.sum(dim=1)
+            for j, i in enumerate(g["idx"]):
+                off, n = g["offsets_host"][j], g["sizes_host"][j]
+                reduced[i] = flat[off:off + n].view(self.leaves[i].shape[1:])
+        return reduced, post_sq
+
+
 def leaves_clip_sum(leaves, clipping_norm, *, kind: str = "fixed", gamma: float = 0.0,
                     with_postsq: bool = False, out_dtypes=None, leaf_groups=None,
                     conservative: bool = True):
@@ -194,33 +260,20 @@ def leaves_clip_sum(leaves, clipping_norm, *, kind: str = "fixed", gamma: float 
     (``_clipped_fun.py:211-216``); the single-pytree functions use the exact
     bound (``_pytree.py:624-628``).  See :class:`LeafClipResult`.
     """
-    device = leaves[0].device
-    B = leaves[0].shape[0]
-    L = len(leaves)
+    batch = LeafBatch(leaves)
+    device, B, L = batch.device, batch.B, batch.L
     grouped = leaf_groups is not None
     bounds = list(clipping_norm) if grouped else [clipping_norm]
     n_groups = len(bounds)
-    contiguous = [l if l.is_contiguous() else l.contiguous() for l in leaves]
-    plan = _plan(contiguous, device)
     stream = nat.stream_handle(device)
     acc = torch.float32
     roundoff = num.norm_roundoff(acc, torch.float64, L,
                                  num.reduction_terms([math.prod(l.shape[1:]) for l in leaves]))
-    leaf_sq = torch.empty((B, L), dtype=torch.float64, device=device)
-    groups = plan["groups"]
-    ptr_tables = []
-    for g in groups:
-        ptrs = torch.tensor([contiguous[i].data_ptr() for i in g["idx"]], dtype=torch.int64)
-        ptr_tables.append(ptrs.pin_memory().to(device, non_blocking=True))
-        partial = torch.empty((B, max(g["n_tiles"], 1)), dtype=torch.float64, device=device)
-        nat.call("dpc_leaves_sqnorm", nat.ptr(ptr_tables[-1]), nat.ptr(g["sizes"]),
-                 nat.ptr(g["tile_leaf"]), nat.ptr(g["tile_local"]), nat.ptr(g["tile_start"]),
-                 nat.ptr(g["leaf_col"]), len(g["idx"]), g["n_tiles"], B,
-                 nat.dtype_code(g["dtype"]), nat.ptr(partial), nat.ptr(leaf_sq), L, stream)
+    leaf_sq = batch.sqnorms()
     sq = torch.empty(B, dtype=torch.float64, device=device)
     nat.call("dpc_row_sum_f64", nat.ptr(leaf_sq), B, L, 0, nat.ptr(sq), stream)
-    guards = [num.guard_constants(g["dtype"], torch.promote_types(g["dtype"], acc), roundoff)
-              for g in groups]
+    guards = [num.guard_constants(dt, torch.promote_types(dt, acc), roundoff)
+              for dt in batch.dtypes]
     scale_kind = nat.SCALE_AUTO_S if kind == "auto_s" else nat.SCALE_FIXED
     bound_of = num.conservative_bound if conservative else float
     if grouped:
@@ -240,33 +293,12 @@ def leaves_clip_sum(leaves, clipping_norm, *, kind: str = "fixed", gamma: float 
         cfs = [ops.clip_factors(sq, bound_of(bounds[0]), guards, kind=scale_kind,
                                 gamma=gamma, count_threshold=num.float32_of(bounds[0]))]
         norms, group_norms, nclipped = cfs[0].norms, None, cfs[0].nclipped
-    reduced = [None] * L
-    post_sq = None
-    if with_postsq:
-        post_sq = torch.zeros(B, dtype=torch.float32, device=device)
     scales = {}
-    for gi, g in enumerate(groups):
-        dtype = g["dtype"]
-        out_dtype = (out_dtypes or {}).get(dtype, dtype)
-        flat = torch.empty(g["total"], dtype=out_dtype, device=device)
-        tile_sq = (torch.empty((B, g["n_tiles"]), dtype=torch.float32, device=device)
-                   if with_postsq else None)
-        if grouped:
-            scale_rows = torch.stack([cf.scale[gi] for cf in cfs])
-            rows = [leaf_groups[i] for i in g["idx"]]
-            leaf_row = _device_table(device, ("leaf_row", dtype, tuple(rows)), rows, np.int32)
-        else:
-            scale_rows, leaf_row = cfs[0].scale[gi:gi + 1], None
-        scales[dtype] = scale_rows
-        nat.call("dpc_leaves_apply", nat.ptr(ptr_tables[gi]), nat.ptr(g["sizes"]),
-                 nat.ptr(g["tile_leaf"]), nat.ptr(g["tile_local"]), nat.ptr(g["out_offs"]),
-                 g["n_tiles"], B, nat.dtype_code(dtype), nat.ptr(scale_rows), nat.ptr(leaf_row),
-                 nat.ptr(flat), nat.dtype_code(out_dtype), nat.ptr(tile_sq), stream)
-        if with_postsq:
-            post_sq += tile_sq.sum(dim=1)
-        for j, i in enumerate(g["idx"]):
-            off, n = g["offsets_host"][j], g["sizes_host"][j]
-            reduced[i] = flat[off:off + n].view(leaves[i].shape[1:])
+    for gi, dtype in enumerate(batch.dtypes):
+        scales[dtype] = (torch.stack([cf.scale[gi] for cf in cfs]) if grouped
+                         else cfs[0].scale[gi:gi + 1])
+    reduced, post_sq = batch.apply(scales, leaf_groups if grouped else None, out_dtypes,
+                                   with_postsq)
     return LeafClipResult(reduced=reduced, norms=norms, post_sq=post_sq, nclipped=nclipped,
                           group_norms=group_norms, scales=scales)
 

@@ -1,4 +1,4 @@
-"""Model-level ghost clipping: clip -> sum (-> noise) over every linear layer.
+"""Model-level ghost clipping: clip -> sum (-> noise) over a model's parameters.
 
 The reference differentiates ``loss_fn`` per example with ``vmap(grad)``
 (packages/opake-engine/src/opake/api/engine/clipping/_clipped_grad.py:278-296)
@@ -34,6 +34,12 @@ all segmented layers of one shape go through one grouped norm launch
 bound by its own per-example norm (_streaming.py:63-104), and the noise of a
 leaf uses its group's standard deviation.
 
+Other modules that own trainable parameters (RMSNorm / LayerNorm weights,
+...) get their per-example gradients materialised -- ``vmap`` over the batch
+of the module's own ``vjp`` from its captured inputs and output gradients,
+which for such parameters is a few values per example -- and clipped with the
+rest by the leaf kernels.
+
 The output is the reference's ``ClippedPytree`` (``NoisedPytree`` with noise)
 over ``{parameter name: tensor}`` with ``max_norm = C / normalize_by``; noise
 leaves are drawn in sorted-name (flatten) order.
@@ -51,6 +57,7 @@ from opake_amd import _native as nat
 from opake_amd import ops
 from opake_amd.clipping import _numerics as num
 from opake_amd.clipping._clipped_fun import FixedClipState
+from opake_amd.clipping._leaves import LeafBatch
 from opake_amd.exceptions import ConfigurationError, InputTypeError
 from opake_amd.noise import GaussianNoiseState, step_key_for
 from opake_amd.pytree import param_path
@@ -103,26 +110,74 @@ class _Capture:
         self._handle.remove()
 
 
-def _linear_layers(model: torch.nn.Module):
-    layers = []
-    covered = set()
+def _trainable_modules(model: torch.nn.Module):
+    """Linear layers with a trainable weight, and the other modules that own
+    trainable parameters directly (``[(name, module, [(param name, param)])]``)."""
+    linears, others = [], []
+    seen = set()
     for name, mod in model.named_modules():
+        own = [(pn, p) for pn, p in mod.named_parameters(recurse=False) if p.requires_grad]
+        if not own:
+            continue
+        for _, p in own:
+            if id(p) in seen:
+                raise ConfigurationError(
+                    f"module {name!r} shares a trainable parameter with another module")
+            seen.add(id(p))
         if isinstance(mod, torch.nn.Linear) and mod.weight.requires_grad:
-            layers.append((name, mod))
-            covered.add(id(mod.weight))
-            if mod.bias is not None:
-                if not mod.bias.requires_grad:
-                    raise ConfigurationError(
-                        f"layer {name!r}: a frozen bias under a trainable weight is not supported")
-                covered.add(id(mod.bias))
-    for pname, p in model.named_parameters():
-        if p.requires_grad and id(p) not in covered:
-            raise ConfigurationError(
-                f"parameter {pname!r} is trainable but not part of an nn.Linear layer; "
-                "ghost clipping covers linear layers only (freeze it or use clipped_grad)")
-    if not layers:
-        raise ConfigurationError("the model has no trainable nn.Linear layer")
-    return layers
+            if mod.bias is not None and not mod.bias.requires_grad:
+                raise ConfigurationError(
+                    f"layer {name!r}: a frozen bias under a trainable weight is not supported")
+            linears.append((name, mod))
+        else:
+            others.append((name, mod, own))
+    if not linears and not others:
+        raise ConfigurationError("the model has no trainable parameter")
+    return linears, others
+
+
+class _DirectHook:
+    """Forward hook of a module with its own trainable parameters (not a
+    linear layer): keeps its positional inputs and its output."""
+
+    def __init__(self, module: torch.nn.Module):
+        self.args = None
+        self.out = None
+        self.calls = 0
+        self._handle = module.register_forward_hook(self._fwd)
+
+    def _fwd(self, module, inputs, output):
+        self.calls += 1
+        self.args = tuple(x.detach() if isinstance(x, torch.Tensor) else x for x in inputs)
+        self.out = output
+
+    def remove(self):
+        self._handle.remove()
+
+
+def _per_example_param_grads(mod, own, args, G):
+    """Per-example gradients of ``mod``'s own parameters from its inputs and
+    output gradients: ``vmap`` over the batch of the module's ``vjp`` (the
+    reference's per-example ``grad``, restricted to this module).  Returns
+    ``{param name: [B, *shape]}`` in the parameters' dtype."""
+    from torch.func import functional_call, vjp, vmap
+
+    params = {pn: p.detach() for pn, p in own}
+    tensor_pos = [i for i, a in enumerate(args) if isinstance(a, torch.Tensor)]
+
+    def single(p, g, *xs):
+        full = list(args)
+        for i, x in zip(tensor_pos, xs):
+            full[i] = x.unsqueeze(0)
+
+        def f(pp):
+            return functional_call(mod, pp, tuple(full))
+
+        _, fn = vjp(f, p)
+        return fn(g.unsqueeze(0))[0]
+
+    xs = [args[i] for i in tensor_pos]
+    return vmap(single, in_dims=(None, 0) + (0,) * len(xs))(params, G, *xs)
 
 
 def _as_btd(x: torch.Tensor, B: int) -> torch.Tensor:
@@ -164,6 +219,17 @@ class LinearCapture:
     has_bias: bool = False
     segments: list | None = None
     param_dtype: torch.dtype | None = None
+
+
+@dataclass
+class DirectCapture:
+    """Materialised per-example gradients of parameters outside linear layers
+    (norm weights, biases of other modules, ...): ``{leaf name: [B, *shape]}``.
+    They are clipped with the linear layers' leaves by the leaf kernels
+    (``dpc_leaves_sqnorm`` / ``dpc_leaves_apply``), the reference's own path
+    for materialised values (_streaming.py:39-185)."""
+
+    grads: dict
 
 
 @dataclass
@@ -240,6 +306,14 @@ def ghost_clip_captured(
         raise ConfigurationError("no layers to clip")
     max_norm = clipping_norm / normalize_by
     per_group = isinstance(clipping_norm, PerGroup)
+    direct = {}
+    for c in captures:
+        if isinstance(c, DirectCapture):
+            for n, t in c.grads.items():
+                if n in direct:
+                    raise ConfigurationError(f"leaf {n!r} is given twice")
+                direct[n] = t
+    captures = [c for c in captures if not isinstance(c, DirectCapture)]
     shapes = {}
     for c in captures:
         shapes[f"{c.name}.weight"] = (c.G.shape[-1], c.A.shape[-1])
@@ -247,6 +321,12 @@ def ghost_clip_captured(
             shapes[f"{c.name}.bias"] = (c.G.shape[-1],)
     if len(shapes) != sum(1 + c.has_bias for c in captures):
         raise ConfigurationError("layer names must be unique")
+    for n, t in direct.items():
+        if n in shapes:
+            raise ConfigurationError(f"leaf {n!r} is given twice")
+        shapes[n] = tuple(t.shape[1:])
+    if not shapes:
+        raise ConfigurationError("no layers to clip")
     leaf_names = sorted(shapes)
     leaf_index = {n: i for i, n in enumerate(leaf_names)}
     leaf_group, group_names, bounds = _groups_of(leaf_names, clipping_norm)
@@ -281,7 +361,15 @@ def ghost_clip_captured(
                     f"layer {c.name!r}: the row segments must give B row counts that add up "
                     "to the layer's input rows")
             segmented.append(_Layer(c, g, A2, G2))
-    device = (dense + segmented)[0].A.device
+    direct_names = sorted(direct)
+    if direct_names:
+        nb = direct[direct_names[0]].shape[0]
+        if B is None:
+            B = nb
+        if any(direct[n].shape[0] != B for n in direct_names):
+            raise ConfigurationError("the per-example gradients do not share the batch size")
+    device = (dense + segmented)[0].A.device if (dense or segmented) else \
+        direct[direct_names[0]].device
 
     # Per-group, per-example squared norms.
     sq = torch.zeros((n_groups, B), dtype=torch.float64, device=device)
@@ -314,11 +402,25 @@ def ghost_clip_captured(
     bucket_layouts = [(members, ops.SegmentLayout([L.cap.segments for L in members], device))
                       for members in buckets.values()]
 
+    # Materialised per-example gradients: per-leaf squared norms, summed into
+    # their groups in leaf order.
+    direct_batch = None
+    if direct_names:
+        direct_batch = LeafBatch([direct[n].detach() for n in direct_names])
+        leaf_sq = direct_batch.sqnorms()
+        cols = [leaf_group[n] for n in direct_names]
+        col_group = torch.tensor(cols, dtype=torch.int32).to(device)
+        gsq = torch.empty((n_groups, B), dtype=torch.float64, device=device)
+        nat.call("dpc_group_sum_f64", nat.ptr(leaf_sq), B, len(cols), len(cols),
+                 nat.ptr(col_group), n_groups, nat.ptr(gsq), nat.stream_handle(device))
+        sq += gsq
+
     # Guards for the materialised leaves the reference would clip.
     sizes = [math.prod(shapes[n]) for n in leaf_names]
     roundoff = num.norm_roundoff(torch.float32, torch.float64, len(sizes),
                                  num.reduction_terms(sizes))
-    storage = sorted({L.A.dtype for L in dense + segmented}, key=str)
+    storage = sorted({L.A.dtype for L in dense + segmented} | {direct[n].dtype for n in direct},
+                     key=str)
     guards = [num.guard_constants(dt, torch.promote_types(dt, torch.float32), roundoff)
               for dt in storage]
     cfs = [ops.clip_factors(sq[g], num.conservative_bound(bounds[g]), guards,
@@ -418,6 +520,23 @@ def ghost_clip_captured(
         _close_pair(ev)
         for i, n in enumerate(names):
             tree[n] = stacked[i]
+    if direct_batch is not None:
+        scale_rows = {dt: torch.stack([cf.scale[storage.index(dt)] for cf in cfs])
+                      for dt in direct_batch.dtypes}
+        out_dtypes = {dt: dtype for dt in direct_batch.dtypes} if dtype is not None else None
+        reduced, _ = direct_batch.apply(scale_rows, [leaf_group[n] for n in direct_names],
+                                        out_dtypes)
+        for n, x in zip(direct_names, reduced):
+            if normalize_by != 1.0:
+                x = x / normalize_by
+            s_n = leaf_std(n)
+            if s_n != 0.0:
+                if gen is not None:
+                    x = ops.add_noise(x, s_n, mode=nat.NOISE_INJECTED, noise=to_dev(draws[n]))
+                else:
+                    x = ops.add_noise(x, s_n, mode=nat.NOISE_PHILOX, seed=step_key.seed,
+                                      leaf_id=leaf_index[n])
+            tree[n] = x
     tree = {k: tree[k] for k in leaf_names}
     if noise_fn is None:
         result = clipped(tree, max_norm=max_norm)
@@ -461,17 +580,20 @@ def ghost_clipped_grad(
     _validate_bound(clipping_norm)
     if normalize_by <= 0.0:
         raise ConfigurationError(f"normalize_by must be > 0, got {normalize_by}.")
-    layers = _linear_layers(model)
+    layers, others = _trainable_modules(model)
     leaf_names = []
     for name, mod in layers:
         leaf_names.append(f"{name}.weight")
         if mod.bias is not None:
             leaf_names.append(f"{name}.bias")
+    for name, _, own in others:
+        leaf_names.extend(f"{name}.{pn}" if name else pn for pn, _ in own)
     _groups_of(leaf_names, clipping_norm)  # validates a PerGroup against the leaves
     state0 = FixedClipState()
 
     def grad_fn(inputs, targets, *, state, noise_fn=None, noise_state=None):
         hooks = [_Capture(mod) for _, mod in layers]
+        dhooks = [_DirectHook(mod) for _, mod, _ in others]
         args = inputs if isinstance(inputs, tuple) else (inputs,)
         try:
             with record_function("opake::ghost_clipped_grad"), torch.enable_grad():
@@ -479,23 +601,25 @@ def ghost_clipped_grad(
                 losses = loss_fn(outputs, targets)
                 if losses.dim() != 1:
                     raise ConfigurationError("loss_fn must return per-example losses [B]")
-                for (name, _), cap in zip(layers, hooks):
+                named = [(n, c) for (n, _), c in zip(layers, hooks)]
+                named += [(n, c) for (n, _, _), c in zip(others, dhooks)]
+                for name, cap in named:
                     if cap.out is None:
-                        raise ConfigurationError(f"layer {name!r} was not used by the forward pass")
+                        raise ConfigurationError(f"module {name!r} was not used by the forward pass")
                     if cap.calls != 1:
                         raise ConfigurationError(
-                            f"layer {name!r} was called {cap.calls} times; ghost clipping needs "
-                            "one call per layer and step")
-                # Gradients with respect to the layer outputs only: autograd
+                            f"module {name!r} was called {cap.calls} times; ghost clipping needs "
+                            "one call per module and step")
+                # Gradients with respect to the module outputs only: autograd
                 # prunes the weight-gradient GEMMs, which the clipped sum replaces.
-                grads = torch.autograd.grad(losses.sum(), [c.out for c in hooks],
+                grads = torch.autograd.grad(losses.sum(), [c.out for _, c in named],
                                             allow_unused=True)
         finally:
-            for c in hooks:
+            for c in hooks + dhooks:
                 c.remove()
         B = losses.shape[0]
         captures = []
-        for (name, mod), cap, g in zip(layers, hooks, grads):
+        for (name, mod), cap, g in zip(layers, hooks, grads[:len(layers)]):
             G = g.detach() if g is not None else torch.zeros_like(cap.out)
             if cap.segments is None and cap.A.shape[0] != B:
                 raise ConfigurationError(
@@ -504,6 +628,19 @@ def ghost_clipped_grad(
             captures.append(LinearCapture(name=name, A=cap.A, G=G, has_bias=mod.bias is not None,
                                           segments=cap.segments, param_dtype=mod.weight.dtype))
             cap.out = None
+        per_ex = {}
+        for (name, mod, own), cap, g in zip(others, dhooks, grads[len(layers):]):
+            G = g.detach() if g is not None else torch.zeros_like(cap.out)
+            if G.shape[0] != B:
+                raise ConfigurationError(f"module {name!r}: its output does not have the batch "
+                                         "as dim 0")
+            with torch.enable_grad():
+                pg = _per_example_param_grads(mod, own, cap.args, G)
+            for pn, t in pg.items():
+                per_ex[f"{name}.{pn}" if name else pn] = t.detach()
+            cap.out = None
+        if per_ex:
+            captures.append(DirectCapture(per_ex))
         out = ghost_clip_captured(captures, clipping_norm=clipping_norm,
                                   normalize_by=normalize_by, noise_fn=noise_fn,
                                   noise_state=noise_state, dtype=dtype, return_aux=return_aux)
@@ -519,4 +656,10 @@ def ghost_clipped_grad(
     return grad_fn, state0
 
 
-__all__ = ["GhostGradAux", "LinearCapture", "ghost_clip_captured", "ghost_clipped_grad"]
+__all__ = [
+    "DirectCapture",
+    "GhostGradAux",
+    "LinearCapture",
+    "ghost_clip_captured",
+    "ghost_clipped_grad",
+]

@@ -1,0 +1,77 @@
+"""Per-example gradients of modules outside linear layers (CPU).
+
+``ghost_clipped_grad`` materialises the per-example gradients of parameters
+that do not sit in a linear layer (RMSNorm / LayerNorm weights and biases) as
+``vmap`` over the batch of the module's own ``vjp``.  Pinned here against the
+brute-force oracle -- one forward and backward per example -- on the modules
+alone and inside a transformer block, in float64.  The block's linear-layer
+gradients are pinned too: ``G_i^T A_i`` from the captured operands equals the
+per-example gradient of the loop.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from opake_amd.clipping._model import _per_example_param_grads
+from opake_amd.transformer import BlockLM, per_example_lm_loss
+from oracle import ghost_oracle
+
+
+def _sq(out, t):
+    return ((out - t) ** 2).sum(dim=tuple(range(1, out.dim())))
+
+
+def test_norm_modules_match_the_per_example_loop():
+    torch.manual_seed(0)
+    B, T, d = 4, 6, 10
+    for mod in (torch.nn.RMSNorm(d, eps=1e-5), torch.nn.LayerNorm(d)):
+        mod = mod.double()
+        with torch.no_grad():
+            for p in mod.parameters():
+                p.normal_()
+        x = torch.randn(B, T, d, dtype=torch.float64)
+        t = torch.randn(B, T, d, dtype=torch.float64)
+        G = 2 * (mod(x) - t)
+        own = [(n, p) for n, p in mod.named_parameters(recurse=False)]
+        got = _per_example_param_grads(mod, own, (x,), G.detach())
+        want = ghost_oracle.per_example_grads_loop(mod, _sq, (x,), t)
+        for n in want:
+            torch.testing.assert_close(got[n].detach(), want[n], rtol=1e-12, atol=1e-12)
+
+
+def test_block_captures_give_the_per_example_grads():
+    torch.manual_seed(1)
+    model = BlockLM(vocab=50, d=32, n_heads=4, ffn=48, dtype=torch.float64)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.normal_(0.0, 0.2)
+    g = torch.Generator().manual_seed(2)
+    ids = torch.randint(0, 50, (3, 9), generator=g)
+    tgt = torch.randint(0, 50, (3, 9), generator=g)
+    caps = {}
+
+    def hook(name):
+        def fn(mod, inp, out):
+            caps[name] = (mod, inp[0].detach(), out)
+        return fn
+
+    handles = [m.register_forward_hook(hook(n)) for n, m in model.named_modules()
+               if any(p.requires_grad for p in m.parameters(recurse=False))]
+    losses = per_example_lm_loss(model(ids), tgt)
+    names = list(caps)
+    outs = torch.autograd.grad(losses.sum(), [caps[n][2] for n in names])
+    for h in handles:
+        h.remove()
+    loop = ghost_oracle.per_example_grads_loop(model, per_example_lm_loss, (ids,), tgt)
+    assert sorted(loop) == sorted(f"{n}.weight" for n in names)
+    for n, G in zip(names, outs):
+        mod, A, _ = caps[n]
+        if isinstance(mod, torch.nn.Linear):
+            got = ghost_oracle.linear_per_example_grads(A, G.detach())[0]
+        else:
+            got = _per_example_param_grads(mod, [("weight", mod.weight)], (A,), G.detach())[
+                "weight"].detach()
+        # The block takes its SiLU, rotary and attention core in float32, so a
+        # batch of one and the full batch agree to float32 rounding.
+        torch.testing.assert_close(got, loop[f"{n}.weight"], rtol=1e-6, atol=1e-9)
