@@ -20,6 +20,13 @@ of the linear surrogate loss, the streaming clip-and-sum, the CPU-generator
 noise draw) on a bounded sample of the same workload: the full layer with a
 reduced batch, timed on the host cores of the box.
 
+``--config 3`` (not the default line) measures BASELINE configs[2]: a
+Llama-style block (d = 2048, 16 heads, SwiGLU 8192, RMSNorm, RoPE, bf16, B =
+16, T = 1024, vocab 32000, embedding and head frozen); ``value`` is the ghost
+clip -> sum -> noise of the block's parameters from one step's captured
+operands, and ``config.full_step_ms`` the whole step with the forward and the
+backward to the module outputs on PyTorch-ROCm.
+
 ``--config 5`` (not the default line) measures BASELINE configs[4] the same
 way: a top-2 MoE FFN with 8 SwiGLU experts (d = 2048, expert width 5632),
 bf16, B = 16, T = 1024, routing from N(0, 1) router logits; the step is the
@@ -298,10 +305,165 @@ def run_moe(args) -> dict:
     }
 
 
+BLK_B, BLK_T, BLK_D, BLK_H, BLK_F, BLK_V = 16, 1024, 2048, 16, 8192, 32000
+
+
+def block_model(device, dtype, seed=0):
+    import torch
+
+    from opake_amd.transformer import BlockLM
+
+    torch.manual_seed(seed)
+    model = BlockLM(BLK_V, BLK_D, BLK_H, BLK_F, dtype=dtype, device=device)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.normal_(0.0, 0.02)
+    return model
+
+
+def block_flops(b=BLK_B, t=BLK_T):
+    """Gram norms (SYRK convention) and clipped-sum FLOPs of the block's four
+    projections (qkv d->3d, o d->d, gate_up d->2F, down F->d)."""
+    shapes = [(BLK_D, 3 * BLK_D), (BLK_D, BLK_D), (BLK_D, 2 * BLK_F), (BLK_F, BLK_D)]
+    gram = b * sum(t * (t + 1) * (din + dout) + 2 * t * t for din, dout in shapes)
+    gemm = b * sum(2 * t * din * dout for din, dout in shapes)
+    return gram, gemm
+
+
+def block_cpu_baseline(threads: int):
+    """One example of the config-3 step on the CPU: per-example gradients of
+    the block's parameters (forward and backward of the example alone), the
+    streaming clip-and-sum and the CPU-generator noise.  Examples/s."""
+    import torch
+
+    from opake_amd.transformer import per_example_lm_loss
+    from oracle import clip_oracle, ghost_oracle, noise_oracle
+
+    torch.set_num_threads(threads)
+    model = block_model(torch.device("cpu"), torch.float32, seed=1)
+    g = torch.Generator().manual_seed(2)
+    ids = torch.randint(0, BLK_V, (1, BLK_T), generator=g)
+    tgt = torch.randint(0, BLK_V, (1, BLK_T), generator=g)
+    t0 = time.perf_counter()
+    per = ghost_oracle.per_example_grads_loop(model, per_example_lm_loss, (ids,), tgt)
+    names = sorted(per)
+    res = clip_oracle.stream_clip_and_sum([per[n] for n in names],
+                                          clip_oracle.conservative_bound(C))
+    draws = noise_oracle.draws_for(res.reduced, noise_oracle.step_seed(0, 0))
+    [noise_oracle.sample(x, NM * C, z) for x, z in zip(res.reduced, draws)]
+    return 1.0 / (time.perf_counter() - t0)
+
+
+def run_block(args) -> dict:
+    import torch
+
+    from opake_amd import _native
+    from opake_amd.clipping import ghost_capture, ghost_clip_captured, ghost_clipped_grad
+    from opake_amd.noise import gaussian_noise
+    from opake_amd.random import key
+    from opake_amd.transformer import per_example_lm_loss
+
+    _native.load()
+    dev = torch.device("cuda:0")
+    model = block_model(dev, torch.bfloat16)
+    g = torch.Generator(device=dev).manual_seed(0)
+    ids = torch.randint(0, BLK_V, (BLK_B, BLK_T), generator=g, device=dev)
+    tgt = torch.randint(0, BLK_V, (BLK_B, BLK_T), generator=g, device=dev)
+    noise_fn, state = gaussian_noise(noise_multiplier=NM, key=key(0), stream="device")
+
+    # Full step: forward, backward to the module outputs, clip + sum + noise.
+    fn, st = ghost_clipped_grad(model, per_example_lm_loss, clipping_norm=C, return_aux=True)
+    full_steps = max(1, args.steps // 20)
+    for _ in range(max(1, args.warmup // 40)):
+        (_, aux), _, state = fn(ids, tgt, state=st, noise_fn=noise_fn, noise_state=state)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(full_steps):
+        (_, aux), _, state = fn(ids, tgt, state=st, noise_fn=noise_fn, noise_state=state)
+    torch.cuda.synchronize()
+    full_s = (time.perf_counter() - t0) / full_steps
+    clipped_frac = int(aux.num_clipped.sum().item()) / BLK_B
+    print(f"[bench] full step {1e3 * full_s:.2f} ms, clipped fraction {clipped_frac:.3f}",
+          file=sys.stderr, flush=True)
+
+    # The clip -> sum -> noise part alone, on one step's captured operands.
+    caps, _ = ghost_capture(model, per_example_lm_loss, ids, tgt)
+
+    def step(st_, record):
+        return ghost_clip_captured(caps, clipping_norm=C, noise_fn=noise_fn, noise_state=st_,
+                                   gemm_events=record)
+
+    for _ in range(max(1, args.warmup // 8)):
+        _, state = step(state, None)
+    steps = max(1, args.steps // 8)
+    events = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        _, state = step(state, events)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    print(f"[bench] {steps} timed clip steps in {elapsed:.4f} s", file=sys.stderr, flush=True)
+    gemm_ms = sum(a.elapsed_time(b) for a, b in events) / steps
+    gram_f, gemm_f = block_flops()
+    ms_per_step = 1e3 * elapsed / steps
+    step_tflops = (gram_f + gemm_f) / (ms_per_step * 1e-3) / 1e12
+    gemm_tflops = gemm_f / (gemm_ms * 1e-3) / 1e12
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = min(len(os.sched_getaffinity(0)), 16)
+        print(f"[bench] cpu baseline: 1 example on {threads} threads", file=sys.stderr, flush=True)
+        cpu = {
+            "value": block_cpu_baseline(threads),
+            "unit": "examples/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": ("config 3 at B=1 (float32): the example's per-parameter gradients by its "
+                       "own forward and backward (67.1M block parameters), streaming "
+                       f"clip-and-sum, CPU randn noise; one step; {cpu_model()}"),
+        }
+    return {
+        "steps": steps,
+        "warmup": max(1, args.warmup // 8),
+        "ms_per_step": ms_per_step,
+        "value": BLK_B * steps / elapsed,
+        "config": {
+            "workload": "Llama-style block d=2048, 16 heads, SwiGLU 8192, RMSNorm, RoPE, bf16, "
+                        "B=16, T=1024, vocab 32000 (embedding and head frozen); ghost clipping "
+                        "of the 67.1M block parameters from captured operands + fused "
+                        "device-stream noise (BASELINE configs[2])",
+            "global_batch": BLK_B,
+            "seq_len": BLK_T,
+            "clipping_norm": C,
+            "noise_multiplier": NM,
+            "normalize_by": 1.0,
+            "clipped_fraction": clipped_frac,
+            "step_tflops": step_tflops,
+            "step_frac_of_bf16_peak": step_tflops / MFMA_BF16_PEAK_TFLOPS,
+            "full_step_ms": 1e3 * full_s,
+            "full_step_examples_per_s": BLK_B / full_s,
+            "full_step": "forward + backward to the module outputs (PyTorch-ROCm, attention core "
+                         "in float32) + ghost clip + sum + noise",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "clipped_sum_bf16_kernel<false> (4 launches per step)",
+            "achieved": gemm_tflops,
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": gemm_tflops / MFMA_BF16_PEAK_TFLOPS,
+            "avg_launch_ms": gemm_ms / 4,
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--config", type=int, choices=(2, 5), default=2,
-                    help="BASELINE configuration: 2 (default line) or 5 (MoE)")
+    ap.add_argument("--config", type=int, choices=(2, 3, 5), default=2,
+                    help="BASELINE configuration: 2 (default line), 3 (transformer block) or "
+                         "5 (MoE)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=200,
@@ -334,8 +496,8 @@ def main() -> int:
         print(json.dumps({"copy_calibration_bytes": n * 4, "copies": 5}), flush=True)
         return 0
 
-    if args.config == 5:
-        out = run_moe(args)
+    if args.config in (3, 5):
+        out = run_moe(args) if args.config == 5 else run_block(args)
         line = {"metric": METRIC, "value": out["value"], "unit": "examples/s", "n_gpus": 1,
                 "steps": out["steps"], "warmup": out["warmup"], "ms_per_step": out["ms_per_step"],
                 "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",

@@ -12,8 +12,10 @@ from opake_amd.clipping._clipped_fun import (
 )
 from opake_amd.clipping._ghost import GhostClipAux, ghost_clip_sum, ghost_sqnorms, guard_for_linear
 from opake_amd.clipping._model import (
+    DirectCapture,
     GhostGradAux,
     LinearCapture,
+    ghost_capture,
     ghost_clip_captured,
     ghost_clipped_grad,
 )
@@ -32,6 +34,7 @@ __all__ = [
     "ClipPytreeAux",
     "ClippedFunAux",
     "ClippedGradAux",
+    "DirectCapture",
     "ClippingStats",
     "FixedClipState",
     "GhostClipAux",
@@ -45,6 +48,7 @@ __all__ = [
     "clipped_grad",
     "fused_stream_clip_and_sum",
     "get_fused_clip_backend",
+    "ghost_capture",
     "ghost_clip_captured",
     "ghost_clip_sum",
     "ghost_clipped_grad",

@@ -559,6 +559,72 @@ def ghost_clip_captured(
     return result, next_noise_state
 
 
+def _capture(model, layers, others, loss_fn, inputs, targets):
+    hooks = [_Capture(mod) for _, mod in layers]
+    dhooks = [_DirectHook(mod) for _, mod, _ in others]
+    args = inputs if isinstance(inputs, tuple) else (inputs,)
+    try:
+        with record_function("opake::ghost_capture"), torch.enable_grad():
+            outputs = model(*args)
+            losses = loss_fn(outputs, targets)
+            if losses.dim() != 1:
+                raise ConfigurationError("loss_fn must return per-example losses [B]")
+            named = [(n, c) for (n, _), c in zip(layers, hooks)]
+            named += [(n, c) for (n, _, _), c in zip(others, dhooks)]
+            for name, cap in named:
+                if cap.out is None:
+                    raise ConfigurationError(f"module {name!r} was not used by the forward pass")
+                if cap.calls != 1:
+                    raise ConfigurationError(
+                        f"module {name!r} was called {cap.calls} times; ghost clipping needs "
+                        "one call per module and step")
+            # Gradients with respect to the module outputs only: autograd
+            # prunes the weight-gradient GEMMs, which the clipped sum replaces.
+            grads = torch.autograd.grad(losses.sum(), [c.out for _, c in named],
+                                        allow_unused=True)
+    finally:
+        for c in hooks + dhooks:
+            c.remove()
+    B = losses.shape[0]
+    captures = []
+    for (name, mod), cap, g in zip(layers, hooks, grads[:len(layers)]):
+        G = g.detach() if g is not None else torch.zeros_like(cap.out)
+        if cap.segments is None and cap.A.shape[0] != B:
+            raise ConfigurationError(
+                f"layer {name!r}: its input does not have the batch as dim 0 (a layer fed "
+                "with the rows of several examples must set dpc_row_segments)")
+        captures.append(LinearCapture(name=name, A=cap.A, G=G, has_bias=mod.bias is not None,
+                                      segments=cap.segments, param_dtype=mod.weight.dtype))
+        cap.out = None
+    per_ex = {}
+    for (name, mod, own), cap, g in zip(others, dhooks, grads[len(layers):]):
+        G = g.detach() if g is not None else torch.zeros_like(cap.out)
+        if G.shape[0] != B:
+            raise ConfigurationError(f"module {name!r}: its output does not have the batch "
+                                     "as dim 0")
+        with torch.enable_grad():
+            pg = _per_example_param_grads(mod, own, cap.args, G)
+        for pn, t in pg.items():
+            per_ex[f"{name}.{pn}" if name else pn] = t.detach()
+        cap.out = None
+    if per_ex:
+        captures.append(DirectCapture(per_ex))
+    return captures, losses.detach()
+
+
+def ghost_capture(model: torch.nn.Module, loss_fn, inputs, targets):
+    """One forward of ``model`` and the backward to its trainable modules'
+    outputs: the operands ghost clipping needs, without clipping them.
+
+    Returns ``(captures, losses)``: a :class:`LinearCapture` per linear layer
+    and one :class:`DirectCapture` with the materialised per-example gradients
+    of the other trainable parameters; ``ghost_clip_captured(captures, ...)``
+    then gives ``ghost_clipped_grad``'s result.
+    """
+    layers, others = _trainable_modules(model)
+    return _capture(model, layers, others, loss_fn, inputs, targets)
+
+
 def ghost_clipped_grad(
     model: torch.nn.Module,
     loss_fn,
@@ -592,55 +658,7 @@ def ghost_clipped_grad(
     state0 = FixedClipState()
 
     def grad_fn(inputs, targets, *, state, noise_fn=None, noise_state=None):
-        hooks = [_Capture(mod) for _, mod in layers]
-        dhooks = [_DirectHook(mod) for _, mod, _ in others]
-        args = inputs if isinstance(inputs, tuple) else (inputs,)
-        try:
-            with record_function("opake::ghost_clipped_grad"), torch.enable_grad():
-                outputs = model(*args)
-                losses = loss_fn(outputs, targets)
-                if losses.dim() != 1:
-                    raise ConfigurationError("loss_fn must return per-example losses [B]")
-                named = [(n, c) for (n, _), c in zip(layers, hooks)]
-                named += [(n, c) for (n, _, _), c in zip(others, dhooks)]
-                for name, cap in named:
-                    if cap.out is None:
-                        raise ConfigurationError(f"module {name!r} was not used by the forward pass")
-                    if cap.calls != 1:
-                        raise ConfigurationError(
-                            f"module {name!r} was called {cap.calls} times; ghost clipping needs "
-                            "one call per module and step")
-                # Gradients with respect to the module outputs only: autograd
-                # prunes the weight-gradient GEMMs, which the clipped sum replaces.
-                grads = torch.autograd.grad(losses.sum(), [c.out for _, c in named],
-                                            allow_unused=True)
-        finally:
-            for c in hooks + dhooks:
-                c.remove()
-        B = losses.shape[0]
-        captures = []
-        for (name, mod), cap, g in zip(layers, hooks, grads[:len(layers)]):
-            G = g.detach() if g is not None else torch.zeros_like(cap.out)
-            if cap.segments is None and cap.A.shape[0] != B:
-                raise ConfigurationError(
-                    f"layer {name!r}: its input does not have the batch as dim 0 (a layer fed "
-                    "with the rows of several examples must set dpc_row_segments)")
-            captures.append(LinearCapture(name=name, A=cap.A, G=G, has_bias=mod.bias is not None,
-                                          segments=cap.segments, param_dtype=mod.weight.dtype))
-            cap.out = None
-        per_ex = {}
-        for (name, mod, own), cap, g in zip(others, dhooks, grads[len(layers):]):
-            G = g.detach() if g is not None else torch.zeros_like(cap.out)
-            if G.shape[0] != B:
-                raise ConfigurationError(f"module {name!r}: its output does not have the batch "
-                                         "as dim 0")
-            with torch.enable_grad():
-                pg = _per_example_param_grads(mod, own, cap.args, G)
-            for pn, t in pg.items():
-                per_ex[f"{name}.{pn}" if name else pn] = t.detach()
-            cap.out = None
-        if per_ex:
-            captures.append(DirectCapture(per_ex))
+        captures, losses = _capture(model, layers, others, loss_fn, inputs, targets)
         out = ghost_clip_captured(captures, clipping_norm=clipping_norm,
                                   normalize_by=normalize_by, noise_fn=noise_fn,
                                   noise_state=noise_state, dtype=dtype, return_aux=return_aux)
@@ -660,6 +678,7 @@ __all__ = [
     "DirectCapture",
     "GhostGradAux",
     "LinearCapture",
+    "ghost_capture",
     "ghost_clip_captured",
     "ghost_clipped_grad",
 ]
