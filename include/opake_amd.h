@@ -232,6 +232,25 @@ int dpc_grouped_clipped_sum(const int64_t* a_ptrs, const int64_t* g_ptrs, const 
                             const float* sigmas, int out_dtype, const int64_t* out_ptrs,
                             void* stream);
 
+/* ------------------------------------------------------------------------
+ * Per-example weight gradients of a narrow linear layer (LoRA adapters).
+ *
+ * Replaces the per-sample adapter gradients of packages/opake-patches/src/
+ * opake/api/patches/kernels/lora.py:687-701 (`_per_sample_lora_adapter_grads`:
+ * dA = X^T (G B^T) s, dB = (X A)^T G s per example) and, generally, the
+ * vmap(grad) materialisation (_clipped_grad.py:278-296) of a linear layer
+ * whose din or dout is at most 32:
+ *   out[b, m, n] = sum_t G[b, t, m] * A[b, t, n]   (fp32 sums; out [B, dout, din]
+ *   in out_dtype, rounded once).
+ * A [B, T, din], G [B, T, dout] in `dtype`.  The gradients are then clipped as
+ * materialised leaves (dpc_leaves_sqnorm / dpc_leaves_apply).  Wider layers:
+ * DPC_ENOTSUP (use the Gram path).  ws: dpc_per_example_grads_workspace_bytes.
+ * -------------------------------------------------------------------------*/
+size_t dpc_per_example_grads_workspace_bytes(int B, int T, int din, int dout);
+int dpc_per_example_grads(const void* A, const void* G, int B, int T, int din, int dout,
+                          int dtype, void* out, int out_dtype, void* ws, size_t ws_bytes,
+                          void* stream);
+
 /* Row sums: out[b] (+)= sum_j x[b, j] (float64), used to fold per-leaf
  * squared norms into per-example totals in a fixed order. */
 int dpc_row_sum_f64(const double* x, int B, int n, int accumulate, double* out, void* stream);

@@ -94,6 +94,12 @@ SIGNATURES = {
         _c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_void_p],
     ),
     "dpc_row_sum_f64": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_void_p]),
+    "dpc_per_example_grads_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int]),
+    "dpc_per_example_grads": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_int,
+         _c_void_p, _c_size_t, _c_void_p],
+    ),
     "dpc_grouped_gram_sqnorms": (
         _c_int,
         [_c_void_p, _c_void_p, ctypes.POINTER(_c_int), _c_int, _c_int, _c_void_p, _c_int, _c_int,

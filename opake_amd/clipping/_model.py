@@ -219,6 +219,13 @@ class LinearCapture:
     has_bias: bool = False
     segments: list | None = None
     param_dtype: torch.dtype | None = None
+    norm_method: str = "auto"
+
+
+def _direct_is_cheaper(T: int, din: int, dout: int) -> bool:
+    """Per-example gradients (2 T din dout FLOP, kept for a layer with a side of
+    at most 32, e.g. a LoRA adapter) against the Gram norm (T^2 (din + dout))."""
+    return min(din, dout) <= ops.NARROW_MAX and 2 * din * dout < T * (din + dout)
 
 
 @dataclass
@@ -340,6 +347,8 @@ def ghost_clip_captured(
             raise ConfigurationError(
                 f"layer {c.name!r}: weight and bias must be in the same clipping group")
         G = c.G if c.G.dtype == c.A.dtype else c.G.to(c.A.dtype)
+        if c.norm_method not in ("auto", "gram", "direct"):
+            raise ConfigurationError(f"layer {c.name!r}: unknown norm_method {c.norm_method!r}")
         if c.segments is None:
             nb = c.A.shape[0]
             if B is None:
@@ -347,6 +356,19 @@ def ghost_clip_captured(
             A3, G3 = _as_btd(c.A, B), _as_btd(G, B)
             if A3.shape[1] != G3.shape[1]:
                 raise ConfigurationError(f"layer {c.name!r}: A and G disagree on the token count")
+            T_, din_, dout_ = A3.shape[1], A3.shape[2], G3.shape[2]
+            direct_ok = min(din_, dout_) <= ops.NARROW_MAX and T_ > 1
+            if c.norm_method == "direct" and not direct_ok:
+                raise ConfigurationError(
+                    f"layer {c.name!r}: the direct method needs din or dout <= {ops.NARROW_MAX}")
+            if direct_ok and (c.norm_method == "direct" or (
+                    c.norm_method == "auto" and _direct_is_cheaper(T_, din_, dout_))):
+                # Materialised per-example gradients, clipped as leaves.
+                pdt = c.param_dtype or A3.dtype
+                direct[f"{c.name}.weight"] = ops.per_example_grads(A3, G3, out_dtype=pdt)
+                if c.has_bias:
+                    direct[f"{c.name}.bias"] = G3.float().sum(dim=1).to(pdt)
+                continue
             dense.append(_Layer(c, g, A3.contiguous(), G3.contiguous()))
         else:
             if c.has_bias:

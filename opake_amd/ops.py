@@ -425,6 +425,34 @@ def grouped_clipped_sum(
     return out
 
 
+NARROW_MAX = 32  # widest narrow side of dpc_per_example_grads
+
+
+def per_example_grads(A: torch.Tensor, G: torch.Tensor, *,
+                      out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Per-example weight gradients ``G_i^T A_i`` of a linear layer whose din or
+    dout is at most 32: [B, dout, din] in ``out_dtype`` (default: the input
+    dtype), summed in float32."""
+    dev = nat.require_device(A, G)
+    if A.dim() != 3 or G.dim() != 3 or A.shape[:2] != G.shape[:2] or A.dtype != G.dtype:
+        raise ConfigurationError("expected A [B, T, din], G [B, T, dout] of one dtype")
+    B, T, din = A.shape
+    dout = G.shape[2]
+    if min(din, dout) > NARROW_MAX:
+        raise ConfigurationError(f"per_example_grads needs din or dout <= {NARROW_MAX}")
+    out_dtype = out_dtype or A.dtype
+    out = torch.empty((B, dout, din), dtype=out_dtype, device=dev)
+    if B == 0:
+        return out
+    A, G = _contig(A), _contig(G)
+    ws_bytes = nat.load().dpc_per_example_grads_workspace_bytes(B, T, din, dout)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    nat.call("dpc_per_example_grads", nat.ptr(A), nat.ptr(G), B, T, din, dout,
+             nat.dtype_code(A.dtype), nat.ptr(out), nat.dtype_code(out_dtype), nat.ptr(ws),
+             ws_bytes, nat.stream_handle(dev))
+    return out
+
+
 def leaf_view(t: torch.Tensor) -> tuple[int, int]:
     """The [rows, cols] view of a leaf for the device noise stream."""
     if t.dim() == 0:
@@ -484,5 +512,6 @@ __all__ = [
     "grouped_clipped_sum",
     "grouped_gram_sqnorms",
     "leaf_view",
+    "per_example_grads",
     "philox4x32_10",
 ]

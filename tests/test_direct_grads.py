@@ -75,3 +75,38 @@ def test_block_captures_give_the_per_example_grads():
         # The block takes its SiLU, rotary and attention core in float32, so a
         # batch of one and the full batch agree to float32 rounding.
         torch.testing.assert_close(got, loop[f"{n}.weight"], rtol=1e-6, atol=1e-9)
+
+
+def test_lora_block_adapter_captures_give_the_per_example_grads():
+    from opake_amd.lora import LoRABlock
+
+    torch.manual_seed(5)
+    model = LoRABlock(d=32, n_heads=4, n_kv_heads=2, ffn=40, r=4, dtype=torch.float64)
+    with torch.no_grad():
+        for n, p in model.named_parameters():
+            p.normal_(0.0, 0.2)
+    trainable = sorted(n for n, p in model.named_parameters() if p.requires_grad)
+    assert all(".lora_" in n for n in trainable) and len(trainable) == 14
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(3, 10, 32, generator=g, dtype=torch.float64)
+    t = torch.randn(3, 10, 32, generator=g, dtype=torch.float64)
+    caps = {}
+
+    def hook(name):
+        def fn(mod, inp, out):
+            caps[name] = (inp[0].detach(), out)
+        return fn
+
+    handles = [m.register_forward_hook(hook(n)) for n, m in model.named_modules()
+               if isinstance(m, torch.nn.Linear) and m.weight.requires_grad]
+    losses = _sq(model(x), t)
+    names = list(caps)
+    outs = torch.autograd.grad(losses.sum(), [caps[n][1] for n in names])
+    for h in handles:
+        h.remove()
+    loop = ghost_oracle.per_example_grads_loop(model, _sq, (x,), t)
+    for n, G in zip(names, outs):
+        A = caps[n][0]
+        got = ghost_oracle.linear_per_example_grads(A, G.detach())[0]
+        # float32 internals of the block (SiLU, rotary, attention core)
+        torch.testing.assert_close(got, loop[f"{n}.weight"], rtol=1e-5, atol=1e-7)
