@@ -27,6 +27,12 @@ clip -> sum -> noise of the block's parameters from one step's captured
 operands, and ``config.full_step_ms`` the whole step with the forward and the
 backward to the module outputs on PyTorch-ROCm.
 
+``--config 4`` measures BASELINE configs[3]: LoRA r = 16 adapters on the seven
+projections of an 8B-shaped block, B = 8, T = 2048, bf16; the adapters'
+per-example gradients are formed directly (the Gram norm would cost 64x
+more), then clipped, summed and noised as materialised leaves; the roofline
+is HBM bandwidth of the per-example gradient kernel.
+
 ``--config 5`` (not the default line) measures BASELINE configs[4] the same
 way: a top-2 MoE FFN with 8 SwiGLU experts (d = 2048, expert width 5632),
 bf16, B = 16, T = 1024, routing from N(0, 1) router logits; the step is the
@@ -459,11 +465,174 @@ def run_block(args) -> dict:
     }
 
 
+LORA_B, LORA_T, LORA_D, LORA_H, LORA_KV, LORA_F, LORA_R = 8, 2048, 4096, 32, 8, 14336, 16
+
+
+def lora_model(device, dtype, seed=0):
+    import torch
+
+    from opake_amd.lora import LoRABlock
+
+    torch.manual_seed(seed)
+    model = LoRABlock(LORA_D, LORA_H, LORA_KV, LORA_F, LORA_R, 32.0, dtype=dtype, device=device)
+    with torch.no_grad():
+        for n, p in model.named_parameters():
+            if ".lora_A." not in n:  # base weights, norms and lora_B: N(0, 0.02)
+                p.normal_(0.0, 0.02) if p.dim() > 1 else p.fill_(1.0)
+    return model
+
+
+def lora_work(b=LORA_B, t=LORA_T):
+    """Per-example adapter gradients: FLOPs (2 T din r per adapter side) and the
+    algorithmic HBM bytes of their kernel (read A and G, write the [B, dout,
+    din] gradients in bf16), summed over the 14 adapters."""
+    kv = LORA_D // LORA_H * LORA_KV
+    projs = [(LORA_D, LORA_D), (LORA_D, kv), (LORA_D, kv), (LORA_D, LORA_D),
+             (LORA_D, LORA_F), (LORA_D, LORA_F), (LORA_F, LORA_D)]
+    flops = nbytes = 0
+    for din, dout in projs:
+        for a, g in ((din, LORA_R), (LORA_R, dout)):
+            flops += b * 2 * t * a * g
+            nbytes += b * (t * (a + g) * 2 + a * g * 2)
+    return flops, nbytes
+
+
+def _mse_loss(out, target):
+    return ((out.float() - target.float()) ** 2).mean(dim=(1, 2))
+
+
+def lora_cpu_baseline(threads: int):
+    """One example of the config-4 step on the CPU: the adapters' per-example
+    gradients by the example's own forward and backward, the streaming
+    clip-and-sum and the CPU-generator noise.  Examples/s."""
+    import torch
+
+    from oracle import clip_oracle, ghost_oracle, noise_oracle
+
+    torch.set_num_threads(threads)
+    model = lora_model(torch.device("cpu"), torch.float32, seed=1)
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(1, LORA_T, LORA_D, generator=g)
+    tgt = torch.randn(1, LORA_T, LORA_D, generator=g)
+    t0 = time.perf_counter()
+    per = ghost_oracle.per_example_grads_loop(model, _mse_loss, (x,), tgt)
+    names = sorted(per)
+    res = clip_oracle.stream_clip_and_sum([per[n] for n in names],
+                                          clip_oracle.conservative_bound(C))
+    draws = noise_oracle.draws_for(res.reduced, noise_oracle.step_seed(0, 0))
+    [noise_oracle.sample(v, NM * C, z) for v, z in zip(res.reduced, draws)]
+    return 1.0 / (time.perf_counter() - t0)
+
+
+def run_lora(args) -> dict:
+    import torch
+
+    from opake_amd import _native
+    from opake_amd.clipping import ghost_capture, ghost_clip_captured, ghost_clipped_grad
+    from opake_amd.noise import gaussian_noise
+    from opake_amd.random import key
+
+    _native.load()
+    dev = torch.device("cuda:0")
+    model = lora_model(dev, torch.bfloat16)
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(LORA_B, LORA_T, LORA_D, generator=g, device=dev).to(torch.bfloat16)
+    tgt = torch.randn(LORA_B, LORA_T, LORA_D, generator=g, device=dev)
+    noise_fn, state = gaussian_noise(noise_multiplier=NM, key=key(0), stream="device")
+
+    fn, st = ghost_clipped_grad(model, _mse_loss, clipping_norm=C, return_aux=True)
+    full_steps = max(1, args.steps // 20)
+    for _ in range(max(1, args.warmup // 40)):
+        (_, aux), _, state = fn(x, tgt, state=st, noise_fn=noise_fn, noise_state=state)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(full_steps):
+        (_, aux), _, state = fn(x, tgt, state=st, noise_fn=noise_fn, noise_state=state)
+    torch.cuda.synchronize()
+    full_s = (time.perf_counter() - t0) / full_steps
+    clipped_frac = int(aux.num_clipped.sum().item()) / LORA_B
+    print(f"[bench] full step {1e3 * full_s:.2f} ms, clipped fraction {clipped_frac:.3f}",
+          file=sys.stderr, flush=True)
+
+    caps, _ = ghost_capture(model, _mse_loss, x, tgt)
+
+    def step(st_, record):
+        return ghost_clip_captured(caps, clipping_norm=C, noise_fn=noise_fn, noise_state=st_,
+                                   gemm_events=record)
+
+    for _ in range(max(1, args.warmup // 4)):
+        _, state = step(state, None)
+    steps = max(1, args.steps // 4)
+    events = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        _, state = step(state, events)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    print(f"[bench] {steps} timed clip steps in {elapsed:.4f} s", file=sys.stderr, flush=True)
+    kern_ms = sum(a.elapsed_time(b) for a, b in events) / steps
+    flops, nbytes = lora_work()
+    ms_per_step = 1e3 * elapsed / steps
+    gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = min(len(os.sched_getaffinity(0)), 16)
+        print(f"[bench] cpu baseline: 1 example on {threads} threads", file=sys.stderr, flush=True)
+        cpu = {
+            "value": lora_cpu_baseline(threads),
+            "unit": "examples/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": ("config 4 at B=1 (float32): the 14 adapters' gradients by the example's "
+                       "own forward and backward, streaming clip-and-sum, CPU randn noise; one "
+                       f"step; {cpu_model()}"),
+        }
+    return {
+        "steps": steps,
+        "warmup": max(1, args.warmup // 4),
+        "ms_per_step": ms_per_step,
+        "value": LORA_B * steps / elapsed,
+        "config": {
+            "workload": "LoRA r=16 (alpha 32) on q/k/v/o/gate/up/down of an 8B-shaped block "
+                        "(d=4096, FFN 14336, 32 heads / 8 KV heads), bf16, B=8, T=2048, base "
+                        "frozen N(0,0.02), lora_A Kaiming-uniform, lora_B N(0,0.02); clipping "
+                        "of the 1,310,720 adapter parameters from captured operands (direct "
+                        "per-example gradients) + fused device-stream noise (BASELINE "
+                        "configs[3])",
+            "global_batch": LORA_B,
+            "seq_len": LORA_T,
+            "clipping_norm": C,
+            "noise_multiplier": NM,
+            "normalize_by": 1.0,
+            "clipped_fraction": clipped_frac,
+            "loss": "mean squared error to a N(0,1) target",
+            "direct_tflops": flops / (kern_ms * 1e-3) / 1e12,
+            "full_step_ms": 1e3 * full_s,
+            "full_step_examples_per_s": LORA_B / full_s,
+            "full_step": "forward + backward to the adapter outputs (PyTorch-ROCm, attention "
+                         "core in float32) + clip + sum + noise",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "narrow_partial_bf16_kernel + narrow_finish_kernel (dpc_per_example_grads, 14 "
+                      "launches per step)",
+            "achieved": gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": gbs / HBM_PEAK_GBS,
+            "avg_launch_ms": kern_ms / 14,
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--config", type=int, choices=(2, 3, 5), default=2,
-                    help="BASELINE configuration: 2 (default line), 3 (transformer block) or "
-                         "5 (MoE)")
+    ap.add_argument("--config", type=int, choices=(2, 3, 4, 5), default=2,
+                    help="BASELINE configuration: 2 (default line), 3 (transformer block), "
+                         "4 (LoRA) or 5 (MoE)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=200,
@@ -496,8 +665,8 @@ def main() -> int:
         print(json.dumps({"copy_calibration_bytes": n * 4, "copies": 5}), flush=True)
         return 0
 
-    if args.config in (3, 5):
-        out = run_moe(args) if args.config == 5 else run_block(args)
+    if args.config in (3, 4, 5):
+        out = {3: run_block, 4: run_lora, 5: run_moe}[args.config](args)
         line = {"metric": METRIC, "value": out["value"], "unit": "examples/s", "n_gpus": 1,
                 "steps": out["steps"], "warmup": out["warmup"], "ms_per_step": out["ms_per_step"],
                 "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",

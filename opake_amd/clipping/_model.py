@@ -304,7 +304,8 @@ def ghost_clip_captured(
     with ``noise_fn``), and with ``return_aux`` the first element is
     ``(result, GhostGradAux)`` whose ``loss_values`` is ``None``.
     ``gemm_events`` (timing hook): a list that receives one pair of recorded
-    ``torch.cuda.Event`` around each clipped-sum launch.
+    ``torch.cuda.Event`` around each clipped-sum launch (and each per-example
+    gradient launch of a layer that takes the direct method).
     """
     _validate_bound(clipping_norm)
     if normalize_by <= 0.0:
@@ -365,7 +366,9 @@ def ghost_clip_captured(
                     c.norm_method == "auto" and _direct_is_cheaper(T_, din_, dout_))):
                 # Materialised per-example gradients, clipped as leaves.
                 pdt = c.param_dtype or A3.dtype
+                ev = _event_pair(gemm_events)
                 direct[f"{c.name}.weight"] = ops.per_example_grads(A3, G3, out_dtype=pdt)
+                _close_pair(ev)
                 if c.has_bias:
                     direct[f"{c.name}.bias"] = G3.float().sum(dim=1).to(pdt)
                 continue

@@ -444,7 +444,11 @@ def per_example_grads(A: torch.Tensor, G: torch.Tensor, *,
     out = torch.empty((B, dout, din), dtype=out_dtype, device=dev)
     if B == 0:
         return out
-    A, G = _contig(A), _contig(G)
+    # The kernel reads rows with aligned vector loads.
+    A = A.contiguous() if (A.is_contiguous() and A.data_ptr() % 16 == 0) else A.clone(
+        memory_format=torch.contiguous_format)
+    G = G.contiguous() if (G.is_contiguous() and G.data_ptr() % 16 == 0) else G.clone(
+        memory_format=torch.contiguous_format)
     ws_bytes = nat.load().dpc_per_example_grads_workspace_bytes(B, T, din, dout)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     nat.call("dpc_per_example_grads", nat.ptr(A), nat.ptr(G), B, T, din, dout,
