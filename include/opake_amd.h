@@ -162,8 +162,10 @@ int dpc_philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32
  *   subnormals that rounded up zeroed (_pytree.py:160-204); row_l =
  *   leaf_scale_row[l] (device int32 [L]; NULL: every leaf uses row 0 -- the
  *   per-group clipping of _streaming.py:63-104 gives each group its row);
- *   post_sq[b, t] (nullable) = sum over the tile of stored^2 (fp32).
- *   out_dtype is the storage dtype or float32.
+ *   out_sq (nullable, same layout and dtype as out) = sum_b to_dtype(stored^2),
+ *   the second moment of _streaming.py:167-172; post_sq[b, t] (nullable) =
+ *   sum over the tile of stored^2 (fp32).  out_dtype is the storage dtype or
+ *   float32.
  * -------------------------------------------------------------------------*/
 int dpc_leaves_sqnorm(const int64_t* ptrs, const int64_t* sizes, const int32_t* tile_leaf,
                       const int32_t* tile_local, const int64_t* tile_start,
@@ -172,7 +174,7 @@ int dpc_leaves_sqnorm(const int64_t* ptrs, const int64_t* sizes, const int32_t* 
 int dpc_leaves_apply(const int64_t* ptrs, const int64_t* sizes, const int32_t* tile_leaf,
                      const int32_t* tile_local, const int64_t* out_offs, int n_tiles, int B,
                      int dtype, const float* scale, const int32_t* leaf_scale_row, void* out,
-                     int out_dtype, float* post_sq, void* stream);
+                     void* out_sq, int out_dtype, float* post_sq, void* stream);
 
 /* Per-group sums of per-leaf squared norms: out[g * B + b] (float64) = sum of
  * x[b * stride + j] over the columns j with col_group[j] == g, in column

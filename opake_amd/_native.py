@@ -88,7 +88,7 @@ SIGNATURES = {
     "dpc_leaves_apply": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_void_p,
-         _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p],
+         _c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p],
     ),
     "dpc_group_sum_f64": (
         _c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_void_p],

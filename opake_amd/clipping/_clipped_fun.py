@@ -21,8 +21,13 @@ _clipped_grad.py:86-362, _auto.py:211-367):
   (``_compute_clipping_stats``, :348-396) and ``clipping_rate`` in the aux is
   ``None``.
 
-Not covered (``OperationError``): ``second_moment``, an explicit
-``compute_dtype``, custom scale functions.
+* ``second_moment=True`` adds the batch sum of the squared stored per-example
+  values (``_streaming.py:167-172``) as a ``SecondMomentClippingOutput`` with
+  ``max_norm = C^2 / normalize_by`` for the squared stream
+  (``_clipped_fun.py:414-423``).
+
+Not covered (``OperationError``): an explicit ``compute_dtype``, custom scale
+functions.
 """
 
 from __future__ import annotations
@@ -43,7 +48,13 @@ from opake_amd.pytree import (
     tree_map,
     tree_unflatten,
 )
-from opake_amd.types import ClippedPytree, ClipState, PerGroup, clipped
+from opake_amd.types import (
+    ClippedPytree,
+    ClipState,
+    PerGroup,
+    SecondMomentClippingOutput,
+    clipped,
+)
 
 _DEFAULT_GAMMA = 0.01
 
@@ -157,9 +168,11 @@ class _ChunkResult:
     group_norms: dict | None
     storage: Any
     aux: Any = None
+    squared: Any = None  # second moment: batch sums of the squared stored values
 
 
-def _clip_sum_values(values, clipping_norm, scale, *, dtype, with_postsq) -> _ChunkResult:
+def _clip_sum_values(values, clipping_norm, scale, *, dtype, with_postsq,
+                     second_moment=False) -> _ChunkResult:
     """HIP clip-and-sum of a stacked pytree (``_streaming.py:39-185``)."""
     grouped = isinstance(clipping_norm, PerGroup)
     if grouped:
@@ -184,16 +197,19 @@ def _clip_sum_values(values, clipping_norm, scale, *, dtype, with_postsq) -> _Ch
         names, leaf_groups, bounds = _group_layout(paths, clipping_norm)
         res = leaves_clip_sum(detached, bounds, kind=scale.kind, gamma=scale.gamma,
                               with_postsq=with_postsq, out_dtypes=out_dtypes,
-                              leaf_groups=leaf_groups)
+                              leaf_groups=leaf_groups, second_moment=second_moment)
     else:
         res = leaves_clip_sum(detached, float(clipping_norm), kind=scale.kind,
-                              gamma=scale.gamma, with_postsq=with_postsq, out_dtypes=out_dtypes)
+                              gamma=scale.gamma, with_postsq=with_postsq, out_dtypes=out_dtypes,
+                              second_moment=second_moment)
     group_norms = None
     if grouped:
         group_norms = {n: res.group_norms[k] for k, n in enumerate(names)}
     return _ChunkResult(reduced=tree_unflatten(treedef, res.reduced), norms=res.norms,
                         post_sq=res.post_sq, nclipped=res.nclipped, group_norms=group_norms,
-                        storage=tree_unflatten(treedef, [l.dtype for l in leaves]))
+                        storage=tree_unflatten(treedef, [l.dtype for l in leaves]),
+                        squared=(tree_unflatten(treedef, res.squared) if second_moment
+                                 else None))
 
 
 def _stats(nclipped: torch.Tensor, clipping_norm, batch_size: int):
@@ -209,11 +225,12 @@ def _stats(nclipped: torch.Tensor, clipping_norm, batch_size: int):
 
 
 def _make_clipped_fun(fun, has_aux, *, batch_argnums, clipping_norm, normalize_by, return_aux,
-                      return_stats, microbatch_size, dtype, scale, state):
+                      return_stats, microbatch_size, dtype, scale, state, second_moment=False):
     batch_argnums = _to_tuple(batch_argnums)
     if microbatch_size is not None and microbatch_size <= 0:
         raise ConfigurationError(f"microbatch_size must be positive, got {microbatch_size}")
     output_max_norm = clipping_norm / normalize_by
+    squared_max_norm = (clipping_norm * clipping_norm) / normalize_by if second_moment else None
 
     def run_chunk(args, kwargs, out_dtype):
         in_dims = tuple(0 if i in batch_argnums else None for i in range(len(args)))
@@ -224,7 +241,7 @@ def _make_clipped_fun(fun, has_aux, *, batch_argnums, clipping_norm, normalize_b
             values = vmap(fun, in_dims=in_dims, out_dims=0, randomness="same")(*args, **kwargs)
             aux = None
         res = _clip_sum_values(values, clipping_norm, scale, dtype=out_dtype,
-                               with_postsq=return_aux)
+                               with_postsq=return_aux, second_moment=second_moment)
         res.aux = aux
         return res
 
@@ -239,19 +256,25 @@ def _make_clipped_fun(fun, has_aux, *, batch_argnums, clipping_norm, normalize_b
         with torch.no_grad():
             if microbatch_size is None:
                 res = run_chunk(args, kwargs, dtype)
-                reduced = res.reduced
+                reduced, squared = res.reduced, res.squared
             else:
-                # Chunk sums are accumulated in float32 and cast once at the end.
-                acc, parts = None, []
+                # Chunk sums are accumulated in float32 and cast once at the end
+                # (_microbatch_accumulate_reduced, _clipped_fun.py:252-345).
+                acc, acc_sq, parts = None, None, []
                 for start in range(0, B, microbatch_size):
                     chunk = _slice_args(args, batch_argnums, start, min(B, start + microbatch_size))
                     r = run_chunk(chunk, kwargs, torch.float32)
                     acc = r.reduced if acc is None else tree_map(torch.add, acc, r.reduced)
-                    r.reduced = None
+                    if second_moment:
+                        acc_sq = (r.squared if acc_sq is None
+                                  else tree_map(torch.add, acc_sq, r.squared))
+                    r.reduced = r.squared = None
                     parts.append(r)
                 target = (parts[0].storage if dtype is None
                           else tree_map(lambda _: dtype, parts[0].storage))
                 reduced = tree_map(lambda x, dt: x.to(dt), acc, target)
+                squared = (tree_map(lambda x, dt: x.to(dt), acc_sq, target) if second_moment
+                           else None)
                 group_norms = None
                 if parts[0].group_norms is not None:
                     group_norms = {n: torch.cat([p.group_norms[n] for p in parts])
@@ -266,7 +289,12 @@ def _make_clipped_fun(fun, has_aux, *, batch_argnums, clipping_norm, normalize_b
                     group_norms=group_norms, storage=parts[0].storage, aux=aux)
             if normalize_by != 1.0:
                 reduced = tree_map(lambda x: x / normalize_by, reduced)
+                if second_moment:
+                    squared = tree_map(lambda x: x / normalize_by, squared)
         output = clipped(reduced, max_norm=output_max_norm)
+        if second_moment:
+            output = SecondMomentClippingOutput(
+                grads=output, squared_grads=clipped(squared, max_norm=squared_max_norm))
         if not (return_aux or return_stats):
             return output, state
         num_clipped, rate = _stats(res.nclipped, clipping_norm, B)
@@ -306,8 +334,6 @@ def clipped_fun(
         raise ConfigurationError(f"normalize_by must be > 0, got {normalize_by}.")
     if return_aux and return_stats:
         raise ConfigurationError("return_stats cannot be combined with return_aux=True")
-    if second_moment:
-        raise OperationError("second_moment=True is not implemented by the HIP clip-and-sum")
     if compute_dtype is not None:
         raise OperationError("an explicit compute_dtype is not implemented by the HIP clip-and-sum")
     _validate_clipping_norm(clipping_norm)
@@ -315,7 +341,8 @@ def clipped_fun(
     fn = _make_clipped_fun(fun, has_aux, batch_argnums=batch_argnums, clipping_norm=clipping_norm,
                            normalize_by=normalize_by, return_aux=return_aux,
                            return_stats=return_stats, microbatch_size=microbatch_size,
-                           dtype=dtype, scale=_Scale("fixed"), state=state)
+                           dtype=dtype, scale=_Scale("fixed"), state=state,
+                           second_moment=second_moment)
     return fn, state
 
 
@@ -336,7 +363,8 @@ def _grad_wrapper(loss_fn, argnums, has_aux, return_aux):
 
 
 def _make_grad(loss_fn, argnums, has_aux, *, clipping_norm, normalize_by, batch_argnums,
-               return_aux, return_stats, microbatch_size, dtype, scale, state):
+               return_aux, return_stats, microbatch_size, dtype, scale, state,
+               second_moment=False):
     _validate_static_args(argnums, batch_argnums, normalize_by)
     if return_aux and return_stats:
         raise ConfigurationError("return_stats cannot be combined with return_aux=True")
@@ -346,7 +374,7 @@ def _make_grad(loss_fn, argnums, has_aux, *, clipping_norm, normalize_by, batch_
                               clipping_norm=clipping_norm, normalize_by=normalize_by,
                               return_aux=return_aux, return_stats=return_stats,
                               microbatch_size=microbatch_size, dtype=dtype, scale=scale,
-                              state=state)
+                              state=state, second_moment=second_moment)
     batch_t = _to_tuple(batch_argnums)
     max_norm = clipping_norm / normalize_by
 
@@ -355,6 +383,11 @@ def _make_grad(loss_fn, argnums, has_aux, *, clipping_norm, normalize_by, batch_
             zeros = tree_map(torch.zeros_like, args[argnums_t] if isinstance(argnums_t, int)
                              else tuple(args[i] for i in argnums_t))
             grads = clipped(zeros, max_norm=max_norm)
+            if second_moment:
+                grads = SecondMomentClippingOutput(
+                    grads=grads, squared_grads=clipped(
+                        tree_map(torch.zeros_like, zeros),
+                        max_norm=(clipping_norm * clipping_norm) / normalize_by))
             per_group = isinstance(clipping_norm, PerGroup)
             if return_aux:
                 empty = torch.empty(0)
@@ -401,9 +434,12 @@ def clipped_grad(
     dtype: torch.dtype | None = None,
     compute_dtype: torch.dtype | None = None,
 ):
-    """Sum of per-example clipped gradients of ``loss_fn`` (``_clipped_grad.py:86-362``)."""
-    if second_moment:
-        raise OperationError("second_moment=True is not implemented by the HIP clip-and-sum")
+    """Sum of per-example clipped gradients of ``loss_fn`` (``_clipped_grad.py:86-362``).
+
+    With ``second_moment`` the result is a ``SecondMomentClippingOutput``: the
+    clipped sum and the sum of the squared clipped per-example gradients, with
+    ``max_norm`` ``C / normalize_by`` and ``C^2 / normalize_by``.
+    """
     if compute_dtype is not None:
         raise OperationError("an explicit compute_dtype is not implemented by the HIP clip-and-sum")
     _validate_clipping_norm(clipping_norm)
@@ -412,7 +448,7 @@ def clipped_grad(
                     normalize_by=normalize_by, batch_argnums=batch_argnums,
                     return_aux=return_aux, return_stats=return_stats,
                     microbatch_size=microbatch_size, dtype=dtype, scale=_Scale("fixed"),
-                    state=state)
+                    state=state, second_moment=second_moment)
     return fn, state
 
 
@@ -432,8 +468,6 @@ def auto_clipped_grad(
     second_moment: bool = False,
 ):
     """AUTO-S: ``R * g_i / (||g_i|| + gamma)`` per example, summed (``_auto.py:211-367``)."""
-    if second_moment:
-        raise OperationError("second_moment=True is not implemented by the HIP clip-and-sum")
     if isinstance(gamma, bool) or not isinstance(gamma, (int, float)) or not gamma > 0:
         raise ConfigurationError(f"gamma must be a positive float, got {gamma!r}")
     _validate_clipping_norm(R, "R")
@@ -441,7 +475,8 @@ def auto_clipped_grad(
     fn = _make_grad(loss_fn, argnums, has_aux, clipping_norm=R, normalize_by=normalize_by,
                     batch_argnums=batch_argnums, return_aux=return_aux,
                     return_stats=return_stats, microbatch_size=microbatch_size, dtype=dtype,
-                    scale=_Scale("auto_s", float(gamma)), state=state)
+                    scale=_Scale("auto_s", float(gamma)), state=state,
+                    second_moment=second_moment)
     return fn, state
 
 

@@ -16,9 +16,10 @@ number of HIP launches per storage dtype, whatever the number of leaves:
    subnormals that rounded up zeroed, fp32 sum over the batch in example order.
 
 Per-group clipping norms (``PerGroup``) clip each group to its own bound by
-its own norm, with one scale row per group.  A call the kernels do not cover
-(``second_moment``, an explicit ``compute_dtype``, dtypes other than float32 /
-bfloat16, leaves that need grad) goes to the ``fallback`` the caller registered with
+its own norm, with one scale row per group; ``second_moment`` adds the batch
+sums of the squared stored values.  A call the kernels do not cover (an
+explicit ``compute_dtype``, dtypes other than float32 / bfloat16, leaves that
+need grad) goes to the ``fallback`` the caller registered with
 :func:`make_fused_backend` -- in the reference that is its own PyTorch
 streaming path -- and raises ``OperationError`` when there is none.
 """
@@ -69,8 +70,6 @@ def unsupported_reason(leaves, clipping_norm, scale, *, compute_dtype, second_mo
     """Why the kernels cannot serve this call, or ``None``."""
     if getattr(scale, "kind", "fixed") not in ("fixed", "auto_s"):
         return f"unknown scale kind {scale.kind!r}"
-    if second_moment:
-        return "second_moment=True is not supported"
     if compute_dtype is not None:
         return "an explicit compute_dtype is not supported"
     if batch_size > _MAX_BATCH:
@@ -171,6 +170,8 @@ class LeafClipResult:
     int32 [1] examples with norm > C (global clipping) or [G] per group.
     ``group_norms``: float32 [G, B] (per-group clipping) or ``None``.
     ``scales``: float32 scale rows per storage dtype, [G, B] (G = 1 without groups).
+    ``squared``: per-leaf batch sums of the squared stored values (second
+    moment) or ``None``.
     """
 
     reduced: list
@@ -179,6 +180,7 @@ class LeafClipResult:
     nclipped: torch.Tensor
     group_norms: torch.Tensor | None
     scales: dict
+    squared: list | None = None
 
 
 class LeafBatch:
@@ -215,18 +217,23 @@ class LeafBatch:
                      nat.dtype_code(g["dtype"]), nat.ptr(partial), nat.ptr(leaf_sq), L, stream)
         return leaf_sq
 
-    def apply(self, scale_rows: dict, leaf_rows=None, out_dtypes=None, with_postsq=False):
+    def apply(self, scale_rows: dict, leaf_rows=None, out_dtypes=None, with_postsq=False,
+              second_moment=False):
         """Scale-store-sum over the batch: leaf l of storage dtype t uses row
         ``leaf_rows[l]`` (default 0) of ``scale_rows[t]`` (float32 [R, B]).
-        Returns ``(reduced, post_sq)``; ``post_sq`` is float32 [B] or None."""
+        Returns ``(reduced, post_sq)``; ``post_sq`` is float32 [B] or None.
+        With ``second_moment`` also the batch sums of the squared stored values:
+        ``(reduced, post_sq, squared)``."""
         B = self.B
         stream = nat.stream_handle(self.device)
         reduced = [None] * self.L
+        squared = [None] * self.L
         post_sq = torch.zeros(B, dtype=torch.float32, device=self.device) if with_postsq else None
         for g, ptrs in zip(self.plan["groups"], self.ptr_tables):
             dtype = g["dtype"]
             out_dtype = (out_dtypes or {}).get(dtype, dtype)
             flat = torch.empty(g["total"], dtype=out_dtype, device=self.device)
+            flat_sq = torch.empty_like(flat) if second_moment else None
             tile_sq = (torch.empty((B, g["n_tiles"]), dtype=torch.float32, device=self.device)
                        if with_postsq else None)
             rows = scale_rows[dtype]
@@ -238,18 +245,23 @@ class LeafBatch:
             nat.call("dpc_leaves_apply", nat.ptr(ptrs), nat.ptr(g["sizes"]),
                      nat.ptr(g["tile_leaf"]), nat.ptr(g["tile_local"]), nat.ptr(g["out_offs"]),
                      g["n_tiles"], B, nat.dtype_code(dtype), nat.ptr(rows), nat.ptr(leaf_row),
-                     nat.ptr(flat), nat.dtype_code(out_dtype), nat.ptr(tile_sq), stream)
+                     nat.ptr(flat), nat.ptr(flat_sq), nat.dtype_code(out_dtype), nat.ptr(tile_sq),
+                     stream)
             if with_postsq:
                 post_sq += tile_sq.sum(dim=1)
             for j, i in enumerate(g["idx"]):
                 off, n = g["offsets_host"][j], g["sizes_host"][j]
                 reduced[i] = flat[off:off + n].view(self.leaves[i].shape[1:])
+                if second_moment:
+                    squared[i] = flat_sq[off:off + n].view(self.leaves[i].shape[1:])
+        if second_moment:
+            return reduced, post_sq, squared
         return reduced, post_sq
 
 
 def leaves_clip_sum(leaves, clipping_norm, *, kind: str = "fixed", gamma: float = 0.0,
                     with_postsq: bool = False, out_dtypes=None, leaf_groups=None,
-                    conservative: bool = True):
+                    conservative: bool = True, second_moment: bool = False):
     """Clip-and-sum of stacked leaves ``[B, *P]`` with the HIP kernels.
 
     ``clipping_norm`` is one bound, or -- with ``leaf_groups`` (group index of
@@ -297,10 +309,12 @@ def leaves_clip_sum(leaves, clipping_norm, *, kind: str = "fixed", gamma: float 
     for gi, dtype in enumerate(batch.dtypes):
         scales[dtype] = (torch.stack([cf.scale[gi] for cf in cfs]) if grouped
                          else cfs[0].scale[gi:gi + 1])
-    reduced, post_sq = batch.apply(scales, leaf_groups if grouped else None, out_dtypes,
-                                   with_postsq)
+    out = batch.apply(scales, leaf_groups if grouped else None, out_dtypes, with_postsq,
+                      second_moment=second_moment)
+    reduced, post_sq = out[0], out[1]
     return LeafClipResult(reduced=reduced, norms=norms, post_sq=post_sq, nclipped=nclipped,
-                          group_norms=group_norms, scales=scales)
+                          group_norms=group_norms, scales=scales,
+                          squared=out[2] if second_moment else None)
 
 
 _TABLES: OrderedDict = OrderedDict()
@@ -376,6 +390,7 @@ def make_fused_backend(fallback=None):
         if not leaves or batch_size == 0:
             device = leaves[0].device if leaves else torch.device("cuda")
             reduced = [reduce_leaf(l) for l in leaves]
+            squared = [reduce_leaf(l) for l in leaves] if second_moment else None
             norms = torch.zeros(batch_size, dtype=torch.float32, device=device)
             post = norms.clone()
             group_norms = None
@@ -385,11 +400,13 @@ def make_fused_backend(fallback=None):
                 names, leaf_groups, bounds = _group_layout(paths, clipping_norm)
                 res = leaves_clip_sum(leaves, bounds, kind=kind, gamma=gamma,
                                       with_postsq=return_aux, out_dtypes=out_dtypes,
-                                      leaf_groups=leaf_groups)
+                                      leaf_groups=leaf_groups, second_moment=second_moment)
             else:
                 res = leaves_clip_sum(leaves, float(clipping_norm), kind=kind, gamma=gamma,
-                                      with_postsq=return_aux, out_dtypes=out_dtypes)
+                                      with_postsq=return_aux, out_dtypes=out_dtypes,
+                                      second_moment=second_moment)
             reduced, norms, post, group_norms = res.reduced, res.norms, res.post_sq, res.group_norms
+            squared = res.squared
         diagnostics = {}
         if return_aux or return_stats:
             diagnostics["norms"] = norms.detach()
@@ -401,8 +418,8 @@ def make_fused_backend(fallback=None):
         return (
             tree_unflatten(treedef, reduced),
             tree_unflatten(treedef, markers),
-            (),
-            (),
+            tree_unflatten(treedef, squared) if second_moment else (),
+            tree_unflatten(treedef, markers) if second_moment else (),
             diagnostics if (return_aux or return_stats) else (),
         )
 

@@ -8,7 +8,8 @@
 //               2048-element tile, tiles summed per leaf;
 //   apply pass: stored = to_dtype(float(x) * scale[b]) with bf16 results that
 //               rounded up into the subnormal range zeroed; summed over the
-//               batch in fp32 in order b = 0..B-1.
+//               batch in fp32 in order b = 0..B-1; optionally the second
+//               moment, to_dtype(stored^2) summed the same way.
 #include "common.h"
 
 namespace {
@@ -95,7 +96,7 @@ apply_sum_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ s
                  const int32_t* __restrict__ tile_leaf, const int32_t* __restrict__ tile_local,
                  const int64_t* __restrict__ out_offs, int n_tiles, int B,
                  const float* __restrict__ scale, const int32_t* __restrict__ leaf_scale_row,
-                 void* __restrict__ out, float* __restrict__ post_sq) {
+                 void* __restrict__ out, void* __restrict__ out_sq, float* __restrict__ post_sq) {
   __shared__ float red[kThreads / 64];
   const int t = blockIdx.x;
   const int leaf = tile_leaf[t];
@@ -103,9 +104,9 @@ apply_sum_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ s
   const int64_t base = ptrs[leaf];
   const int64_t off0 = (int64_t)tile_local[t] * kTile;
   const float smallest_normal = 1.17549435e-38f;  // bf16 shares float32's exponent range
-  float acc[kPerThread];
+  float acc[kPerThread], acc2[kPerThread];
 #pragma unroll
-  for (int j = 0; j < kPerThread; ++j) acc[j] = 0.f;
+  for (int j = 0; j < kPerThread; ++j) acc[j] = acc2[j] = 0.f;
   const float* srow = scale + (size_t)(leaf_scale_row ? leaf_scale_row[leaf] : 0) * B;
   for (int b = 0; b < B; ++b) {
     const float s = srow[b];
@@ -123,6 +124,12 @@ apply_sum_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ s
           if (sa <= smallest_normal && sa > fabsf(prod)) stored = 0.f;
         }
         acc[j] = acc[j] + stored;
+        if (out_sq) {
+          // Second moment: the stored value squared in its dtype, then summed.
+          float s2 = stored * stored;
+          if (kBf16) s2 = round_to_bf16(s2);
+          acc2[j] = acc2[j] + s2;
+        }
         if (post_sq) sq = sq + stored * stored;
       }
     }
@@ -138,8 +145,10 @@ apply_sum_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ s
     if (off < n) {
       if (kOutBf16) {
         reinterpret_cast<uint16_t*>(out)[obase + off] = f32_to_bf16_bits(acc[j]);
+        if (out_sq) reinterpret_cast<uint16_t*>(out_sq)[obase + off] = f32_to_bf16_bits(acc2[j]);
       } else {
         reinterpret_cast<float*>(out)[obase + off] = acc[j];
+        if (out_sq) reinterpret_cast<float*>(out_sq)[obase + off] = acc2[j];
       }
     }
   }
@@ -210,7 +219,7 @@ extern "C" int dpc_leaves_apply(const int64_t* ptrs, const int64_t* sizes,
                                 const int32_t* tile_leaf, const int32_t* tile_local,
                                 const int64_t* out_offs, int n_tiles, int B, int dtype,
                                 const float* scale, const int32_t* leaf_scale_row, void* out,
-                                int out_dtype, float* post_sq, void* stream) {
+                                void* out_sq, int out_dtype, float* post_sq, void* stream) {
   if (n_tiles < 0 || B < 0) return DPC_EINVAL;
   if (dtype != DPC_F32 && dtype != DPC_BF16) return DPC_EINVAL;
   if (out_dtype != DPC_F32 && out_dtype != dtype) return DPC_EINVAL;
@@ -220,15 +229,16 @@ extern "C" int dpc_leaves_apply(const int64_t* ptrs, const int64_t* sizes,
   hipStream_t s = (hipStream_t)stream;
   if (dtype == DPC_BF16 && out_dtype == DPC_BF16) {
     hipLaunchKernelGGL((apply_sum_kernel<true, true>), dim3(n_tiles), dim3(kThreads), 0, s, ptrs,
-                       sizes, tile_leaf, tile_local, out_offs, n_tiles, B, scale, leaf_scale_row, out, post_sq);
+                       sizes, tile_leaf, tile_local, out_offs, n_tiles, B, scale, leaf_scale_row, out, out_sq,
+                       post_sq);
   } else if (dtype == DPC_BF16) {
     hipLaunchKernelGGL((apply_sum_kernel<true, false>), dim3(n_tiles), dim3(kThreads), 0, s,
                        ptrs, sizes, tile_leaf, tile_local, out_offs, n_tiles, B, scale,
-                       leaf_scale_row, out, post_sq);
+                       leaf_scale_row, out, out_sq, post_sq);
   } else {
     hipLaunchKernelGGL((apply_sum_kernel<false, false>), dim3(n_tiles), dim3(kThreads), 0, s,
                        ptrs, sizes, tile_leaf, tile_local, out_offs, n_tiles, B, scale,
-                       leaf_scale_row, out, post_sq);
+                       leaf_scale_row, out, out_sq, post_sq);
   }
   DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;

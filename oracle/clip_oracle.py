@@ -149,11 +149,12 @@ class StreamResult:
     clipped_norms: torch.Tensor | None
     group_norms: dict | None
     scales: dict  # storage dtype -> float64 scale [B]
+    squared: list | None = None  # second moment: sum_b stored_b^2 per leaf
 
 
 def stream_clip_and_sum(leaves, clipping_norm, *, kind="fixed", gamma=0.0, groups=None,
                         group_values=None, compute_dtype=None, reduce_dtype=None,
-                        return_aux=False) -> StreamResult:
+                        return_aux=False, second_moment=False) -> StreamResult:
     """_streaming.py:39-185 on a list of stacked leaves [B, *P].
 
     ``clipping_norm`` is the (already conservative) bound as a float; for
@@ -161,7 +162,8 @@ def stream_clip_and_sum(leaves, clipping_norm, *, kind="fixed", gamma=0.0, group
     ``group_values`` (group name -> bound).  ``reduce_dtype`` maps a leaf dtype
     to the batch-sum output dtype (``_sum_clipped_tensor``,
     _clipped_fun.py:112-131): default keeps the leaf dtype with fp32
-    accumulation for bf16/fp16.
+    accumulation for bf16/fp16.  ``second_moment`` also sums ``stored.square()``
+    (squared in the leaf dtype, _streaming.py:167-172) into ``squared``.
     """
     B = leaves[0].shape[0] if leaves else 0
     acc = resolve_compute_dtype_for_reduction([l.dtype for l in leaves], compute_dtype)
@@ -196,6 +198,7 @@ def stream_clip_and_sum(leaves, clipping_norm, *, kind="fixed", gamma=0.0, group
 
     post_sq = torch.zeros(B, dtype=acc) if return_aux else None
     reduced = []
+    squared = []
     scales = {}
     for i, leaf in enumerate(leaves):
         r = ratios[groups[i]] if groups is not None else ratio
@@ -210,6 +213,8 @@ def stream_clip_and_sum(leaves, clipping_norm, *, kind="fixed", gamma=0.0, group
         accum = torch.float32 if leaf.dtype in (torch.float16, torch.bfloat16) else None
         summed = torch.sum(stored, dim=0, dtype=accum)
         reduced.append(summed.to(out_dtype))
+        if second_moment:
+            squared.append(torch.sum(stored.square(), dim=0, dtype=accum).to(out_dtype))
     return StreamResult(
         reduced=reduced,
         norms=norm,
@@ -217,6 +222,7 @@ def stream_clip_and_sum(leaves, clipping_norm, *, kind="fixed", gamma=0.0, group
         clipped_norms=torch.sqrt(post_sq) if return_aux else None,
         group_norms=group_norms,
         scales=scales,
+        squared=squared if second_moment else None,
     )
 
 

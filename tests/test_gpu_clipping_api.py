@@ -429,3 +429,60 @@ def test_clip_pytree_matches_oracle(dev, dtype):
     out, _ = cl.auto_scale_pytree({n: tree[n].to(dev) for n in names}, R=0.5, gamma=0.01)
     for n, w in zip(names, want):
         torch.testing.assert_close(out[n].cpu(), w)
+
+
+# --- second moment ----------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("per_group", [False, True])
+def test_leaf_backend_second_moment_matches_oracle(dev, per_group):
+    gen = torch.Generator().manual_seed(31 + per_group)
+    B = 6
+    tree = _values(gen, B, [torch.float32, torch.bfloat16])
+    names = sorted(tree)
+    if per_group:
+        assignment = {"p0": "a", "p1": "b", "p2": "a", "p3": "b", "p4": "a"}
+        values = {"a": 0.4, "b": 0.1}
+        C = _per_group(names, assignment, values)
+        res = clip_oracle.stream_clip_and_sum(
+            [tree[n] for n in names], None, groups=[assignment[n] for n in names],
+            group_values={g: clip_oracle.conservative_bound(v) for g, v in values.items()},
+            second_moment=True)
+    else:
+        C = torch.tensor(clip_oracle.conservative_bound(0.3), device=dev)
+        res = clip_oracle.stream_clip_and_sum([tree[n] for n in names], float(C),
+                                              second_moment=True)
+    reduced, markers, squared, sq_markers, _ = cl.fused_stream_clip_and_sum(
+        {k: v.to(dev) for k, v in tree.items()}, C, scale=_Scale("fixed"), batch_size=B,
+        reduce_leaf=_reduce, compute_dtype=None, second_moment=True, return_aux=False,
+        return_stats=False)
+    for i, n in enumerate(names):
+        assert squared[n].dtype == tree[n].dtype and sq_markers[n].dtype == tree[n].dtype
+        torch.testing.assert_close(reduced[n].cpu(), res.reduced[i])
+        torch.testing.assert_close(squared[n].cpu(), res.squared[i])
+
+
+@pytest.mark.parametrize("microbatch", [None, 2])
+def test_clipped_grad_second_moment_and_paired_noise(dev, microbatch):
+    from opake_amd.types import SecondMomentClippingOutput, SecondMomentNoiseOutput
+
+    gen = torch.Generator().manual_seed(41)
+    d = torch.randn(5, 12, generator=gen) * 0.7
+
+    def loss(p, db):  # per-example gradient = db
+        return (p * db).sum()
+
+    g, st = cl.clipped_grad(loss, clipping_norm=1.5, normalize_by=5.0, batch_argnums=1,
+                            second_moment=True, microbatch_size=microbatch)
+    out, _ = g(torch.zeros(12, device=dev), d.to(dev), state=st)
+    assert isinstance(out, SecondMomentClippingOutput)
+    assert out.grads.max_norm == pytest.approx(1.5 / 5.0)
+    assert out.squared_grads.max_norm == pytest.approx(1.5 * 1.5 / 5.0)
+    res = clip_oracle.stream_clip_and_sum([d], clip_oracle.conservative_bound(1.5),
+                                          second_moment=True)
+    assert _rel(out.grads.pytree, res.reduced[0] / 5.0) < 1e-6
+    assert _rel(out.squared_grads.pytree, res.squared[0] / 5.0) < 1e-6
+    noise_fn, nstate = gaussian_noise(noise_multiplier=1.0, key=key(3), stream="device")
+    noisy, _ = noise_fn(out, nstate)
+    assert isinstance(noisy, SecondMomentNoiseOutput)
+    assert not torch.equal(noisy.noisy_grads.pytree, out.grads.pytree)

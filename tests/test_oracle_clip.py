@@ -251,3 +251,24 @@ def test_stream_auto_s_and_nonfinite():
     want = (xs * (1.0 / (n + 0.01)).float().unsqueeze(1)).sum(0)
     torch.testing.assert_close(res.reduced[0], want, rtol=1e-6, atol=1e-7)
     assert torch.isfinite(res.reduced[0]).all()
+
+
+def test_second_moment_closed_form_and_per_example_identity():
+    # [[3, 4], [0.6, 0.8]] with C = 1: both examples store ~[0.6, 0.8], so the
+    # second moment is ~[0.72, 1.28]; it equals the sum of the squares of the
+    # single-example clip (clip_pytree) of each example.
+    x = torch.tensor([[3.0, 4.0], [0.6, 0.8]])
+    res = co.stream_clip_and_sum([x], 1.0, second_moment=True)
+    torch.testing.assert_close(res.squared[0], torch.tensor([0.72, 1.28]), rtol=1e-6, atol=0)
+    g = torch.Generator().manual_seed(4)
+    for dtype in (torch.float32, torch.bfloat16):
+        leaves = [(torch.randn(5, 7, generator=g) * 3).to(dtype),
+                  (torch.randn(5, 300, generator=g)).to(dtype)]
+        res = co.stream_clip_and_sum(leaves, 2.0, second_moment=True)
+        for i in range(2):
+            want = torch.zeros(leaves[i].shape[1:], dtype=torch.float32)
+            for b in range(5):
+                one, _ = co.clip_pytree_scalar([l[b] for l in leaves], 2.0)
+                want += one[i].square().float()
+            torch.testing.assert_close(res.squared[i].float(), want.to(dtype).float(),
+                                       rtol=1e-6 if dtype == torch.float32 else 1e-2, atol=0)
