@@ -43,6 +43,13 @@ int dpc_version(void);
 /* Last HIP error string recorded by a failing call on this thread. */
 const char* dpc_last_error(void);
 
+/* Writes n 32-bit words from HOST memory `host_words` to device memory `dst`
+ * with kernels that carry the words as arguments: no host buffer has to
+ * outlive the call, so it may be recorded into a HIP graph.  Used for the
+ * small index and pointer tables the other entry points take (no reference
+ * counterpart: plumbing of this build). */
+int dpc_write_words(void* dst, const uint32_t* host_words, int n, void* stream);
+
 /* ------------------------------------------------------------------------
  * Per-example squared gradient norms of linear layers (ghost / Gram norm).
  *

@@ -46,6 +46,7 @@ _c_i64 = ctypes.c_int64
 SIGNATURES = {
     "dpc_version": (_c_int, []),
     "dpc_last_error": (ctypes.c_char_p, []),
+    "dpc_write_words": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_void_p]),
     "dpc_gram_workspace_bytes": (_c_size_t, [_c_int, _c_int]),
     "dpc_gram_sqnorms": (
         _c_int,

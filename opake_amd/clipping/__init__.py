@@ -28,6 +28,7 @@ from opake_amd.clipping._leaves import (
     register_fused_clip_backend,
 )
 from opake_amd.clipping._pytree_clip import ClipPytreeAux, auto_scale_pytree, clip_pytree
+from opake_amd.clipping._graph import GraphedGhostClip
 
 __all__ = [
     "AutoClipState",
@@ -39,6 +40,7 @@ __all__ = [
     "FixedClipState",
     "GhostClipAux",
     "GhostGradAux",
+    "GraphedGhostClip",
     "LeafClipResult",
     "LinearCapture",
     "auto_clipped_grad",

@@ -34,6 +34,7 @@ import numpy as np
 import torch
 
 from opake_amd import _native as nat
+from opake_amd._tables import device_table, pointer_table
 from opake_amd import ops
 from opake_amd.clipping import _numerics as num
 from opake_amd.exceptions import ConfigurationError, OperationError
@@ -194,10 +195,8 @@ class LeafBatch:
         self.B = self.leaves[0].shape[0]
         self.L = len(self.leaves)
         self.plan = _plan(self.leaves, self.device)
-        self.ptr_tables = []
-        for g in self.plan["groups"]:
-            ptrs = torch.tensor([self.leaves[i].data_ptr() for i in g["idx"]], dtype=torch.int64)
-            self.ptr_tables.append(ptrs.pin_memory().to(self.device, non_blocking=True))
+        self.ptr_tables = [pointer_table([self.leaves[i] for i in g["idx"]], self.device)
+                           for g in self.plan["groups"]]
 
     @property
     def dtypes(self):
@@ -317,21 +316,9 @@ def leaves_clip_sum(leaves, clipping_norm, *, kind: str = "fixed", gamma: float 
                           squared=out[2] if second_moment else None)
 
 
-_TABLES: OrderedDict = OrderedDict()
-
-
 def _device_table(device, key, values, np_dtype):
-    """Small immutable index tables, copied to the device once (bounded LRU)."""
-    full = (device, key)
-    t = _TABLES.get(full)
-    if t is None:
-        t = torch.from_numpy(np.asarray(values, dtype=np_dtype)).to(device)
-        _TABLES[full] = t
-        if len(_TABLES) > 4 * _MAX_PLANS:
-            _TABLES.popitem(last=False)
-    else:
-        _TABLES.move_to_end(full)
-    return t
+    """Small immutable index tables on the device (cached by content)."""
+    return device_table(values, np_dtype, device)
 
 
 def _group_layout(paths, clipping_norm):

@@ -50,11 +50,13 @@ from __future__ import annotations
 import math
 from dataclasses import dataclass, replace
 
+import numpy as np
 import torch
 from torch.autograd.profiler import record_function
 
 from opake_amd import _native as nat
 from opake_amd import ops
+from opake_amd._tables import device_table
 from opake_amd.clipping import _numerics as num
 from opake_amd.clipping._clipped_fun import FixedClipState
 from opake_amd.clipping._leaves import LeafBatch
@@ -416,10 +418,14 @@ def ghost_clip_captured(
                                        gram_weights=[L.A.shape[1] + L.G.shape[1] for L in members])
             seg_sq = ops.grouped_gram_sqnorms([L.A for L in members], [L.G for L in members],
                                               layout)
-            for g in range(n_groups):
-                idx = [i for i, L in enumerate(members) if L.group == g]
-                if idx:
-                    sq[g] += seg_sq[idx].sum(dim=0)
+            # Per-group sums over the layers, in layer order: [B, E] columns
+            # folded by group.
+            cols = device_table([L.group for L in members], np.int32, device)
+            by_example = seg_sq.t().contiguous()
+            gsq = torch.empty((n_groups, B), dtype=torch.float64, device=device)
+            nat.call("dpc_group_sum_f64", nat.ptr(by_example), B, len(members), len(members),
+                     nat.ptr(cols), n_groups, nat.ptr(gsq), nat.stream_handle(device))
+            sq += gsq
     # The clipped sums: one grouped launch per layer shape.
     buckets = {}
     for L in segmented:
@@ -434,7 +440,7 @@ def ghost_clip_captured(
         direct_batch = LeafBatch([direct[n].detach() for n in direct_names])
         leaf_sq = direct_batch.sqnorms()
         cols = [leaf_group[n] for n in direct_names]
-        col_group = torch.tensor(cols, dtype=torch.int32).to(device)
+        col_group = device_table(cols, np.int32, device)
         gsq = torch.empty((n_groups, B), dtype=torch.float64, device=device)
         nat.call("dpc_group_sum_f64", nat.ptr(leaf_sq), B, len(cols), len(cols),
                  nat.ptr(col_group), n_groups, nat.ptr(gsq), nat.stream_handle(device))
@@ -650,6 +656,25 @@ def ghost_capture(model: torch.nn.Module, loss_fn, inputs, targets):
     return _capture(model, layers, others, loss_fn, inputs, targets)
 
 
+def _slice_batch(x, start, stop):
+    if isinstance(x, tuple):
+        return tuple(_slice_batch(v, start, stop) for v in x)
+    return x[start:stop] if isinstance(x, torch.Tensor) else x
+
+
+def _merge_aux(parts):
+    group_norms = None
+    if parts[0].group_norms is not None:
+        group_norms = {k: torch.cat([p.group_norms[k] for p in parts]) for k in parts[0].group_norms}
+    return GhostGradAux(
+        loss_values=torch.cat([p.loss_values for p in parts]),
+        grad_norms=torch.cat([p.grad_norms for p in parts]),
+        clip_scales=torch.cat([p.clip_scales for p in parts], dim=-1),
+        num_clipped=torch.stack([p.num_clipped for p in parts]).sum(dim=0),
+        batch_size=sum(p.batch_size for p in parts),
+        group_norms=group_norms)
+
+
 def ghost_clipped_grad(
     model: torch.nn.Module,
     loss_fn,
@@ -658,6 +683,7 @@ def ghost_clipped_grad(
     normalize_by: float = 1.0,
     return_aux: bool = False,
     dtype: torch.dtype | None = None,
+    microbatch_size: int | None = None,
 ):
     """Create ``grad_fn(inputs, targets, *, state, noise_fn=None, noise_state=None)``.
 
@@ -667,10 +693,19 @@ def ghost_clipped_grad(
     call returns ``(ClippedPytree, state)``; with it, ``(NoisedPytree, state,
     noise_state')`` where the noise was fused into the clipped-sum epilogue.
     With ``return_aux`` the first element is ``(result, GhostGradAux)``.
+
+    ``microbatch_size`` runs the forward, backward and clipped sum chunk by
+    chunk (chunk sums accumulated in float32 and cast once, as
+    ``_microbatch_accumulate_reduced``, _clipped_fun.py:252-345); the noise is
+    then added to the total by ``noise_fn`` (not fused).
     """
     _validate_bound(clipping_norm)
     if normalize_by <= 0.0:
         raise ConfigurationError(f"normalize_by must be > 0, got {normalize_by}.")
+    if microbatch_size is not None and (isinstance(microbatch_size, bool)
+                                        or not isinstance(microbatch_size, int)
+                                        or microbatch_size <= 0):
+        raise ConfigurationError(f"microbatch_size must be a positive int, got {microbatch_size}")
     layers, others = _trainable_modules(model)
     leaf_names = []
     for name, mod in layers:
@@ -682,7 +717,39 @@ def ghost_clipped_grad(
     _groups_of(leaf_names, clipping_norm)  # validates a PerGroup against the leaves
     state0 = FixedClipState()
 
+    def microbatched(inputs, targets, *, state, noise_fn=None, noise_state=None):
+        B = targets.shape[0]
+        acc, auxes, max_norm = None, [], None
+        for start in range(0, B, microbatch_size):
+            stop = min(B, start + microbatch_size)
+            captures, losses = _capture(model, layers, others, loss_fn,
+                                        _slice_batch(inputs, start, stop), targets[start:stop])
+            out = ghost_clip_captured(captures, clipping_norm=clipping_norm,
+                                      normalize_by=normalize_by, dtype=torch.float32,
+                                      return_aux=return_aux)
+            if return_aux:
+                out, aux = out
+                auxes.append(replace(aux, loss_values=losses.detach()))
+            max_norm = out.max_norm
+            acc = out.pytree if acc is None else {k: acc[k] + v for k, v in out.pytree.items()}
+        param_dtype = {n: p.dtype for n, p in model.named_parameters()}
+        tree = {k: v.to(dtype or param_dtype.get(k, v.dtype)) for k, v in acc.items()}
+        result = clipped(tree, max_norm=max_norm)
+        next_state = None
+        if noise_fn is not None:
+            if noise_state is None:
+                raise ConfigurationError("noise_state is required with noise_fn")
+            result, next_state = noise_fn(result, noise_state)
+        if return_aux:
+            result = (result, _merge_aux(auxes))
+        if noise_fn is None:
+            return result, state
+        return result, state, next_state
+
     def grad_fn(inputs, targets, *, state, noise_fn=None, noise_state=None):
+        if microbatch_size is not None and targets.shape[0] > microbatch_size:
+            return microbatched(inputs, targets, state=state, noise_fn=noise_fn,
+                                noise_state=noise_state)
         captures, losses = _capture(model, layers, others, loss_fn, inputs, targets)
         out = ghost_clip_captured(captures, clipping_norm=clipping_norm,
                                   normalize_by=normalize_by, noise_fn=noise_fn,

@@ -12,7 +12,10 @@ from dataclasses import dataclass
 
 import torch
 
+import numpy as np
+
 from opake_amd import _native as nat
+from opake_amd._tables import device_table, pointer_table
 from opake_amd.exceptions import ConfigurationError
 
 
@@ -286,11 +289,7 @@ class SegmentLayout:
         # One int32 buffer: row0 [S] | len [S] | group [S] | rows [E] |
         # item_start [S + 1] | items [n_items * 4].
         parts = [row0, flat, group, self.rows, item_start, items.reshape(-1)]
-        host = torch.from_numpy(np.concatenate(parts).astype(np.int32))
-        if torch.device(device).type == "cuda":
-            buf = host.pin_memory().to(device, non_blocking=True)
-        else:
-            buf = host
+        buf = device_table(np.concatenate(parts), np.int32, device)
         offs = np.cumsum([0] + [len(p) for p in parts])
         (self.seg_row0, self.seg_len, self.seg_group, self.rows_dev, self.item_start,
          self.items) = [buf[offs[i]:offs[i + 1]] for i in range(len(parts))]
@@ -300,8 +299,7 @@ class SegmentLayout:
 
 
 def _ptr_table(tensors, device) -> torch.Tensor:
-    host = torch.tensor([t.data_ptr() for t in tensors], dtype=torch.int64)
-    return host.pin_memory().to(device, non_blocking=True)
+    return pointer_table(tensors, device)
 
 
 def _check_grouped(A_list, G_list, layout: SegmentLayout, *, same_shape: bool):
@@ -409,10 +407,8 @@ def grouped_clipped_sum(
     leaf_ids = spec.leaf_ids if spec.leaf_ids is not None else list(range(E))
     if len(leaf_ids) != E:
         raise ConfigurationError("one leaf id per problem is required")
-    small = torch.tensor([v & 0xFFFFFFFF for v in leaf_ids], dtype=torch.int64).to(torch.int32)
-    sig = torch.tensor([float(v) for v in spec.sigmas], dtype=torch.float32)
-    leaf_dev = small.pin_memory().to(dev, non_blocking=True)
-    sig_dev = sig.pin_memory().to(dev, non_blocking=True)
+    leaf_dev = device_table([v & 0xFFFFFFFF for v in leaf_ids], np.uint32, dev)
+    sig_dev = device_table([float(v) for v in spec.sigmas], np.float32, dev)
     a_ptrs, g_ptrs = _ptr_table(A_list, dev), _ptr_table(G_list, dev)
     out_ptrs = _ptr_table([out[e] for e in range(E)], dev)
     nat.call(

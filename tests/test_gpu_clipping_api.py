@@ -486,3 +486,30 @@ def test_clipped_grad_second_moment_and_paired_noise(dev, microbatch):
     noisy, _ = noise_fn(out, nstate)
     assert isinstance(noisy, SecondMomentNoiseOutput)
     assert not torch.equal(noisy.noisy_grads.pytree, out.grads.pytree)
+
+
+# --- microbatching in ghost_clipped_grad ---------------------------------------------------
+
+
+def test_ghost_clipped_grad_microbatch_matches_full_batch(dev):
+    torch.manual_seed(0)
+    model = ghost_oracle.MLP()
+    gen = torch.Generator().manual_seed(2)
+    B = 256
+    x = torch.randn(B, 784, generator=gen)
+    y = torch.randint(0, 10, (B,), generator=gen)
+    names, want, res = _mlp_oracle(model, x, y, 1.0, float(B))
+    dmodel = ghost_oracle.MLP().to(dev)
+    dmodel.load_state_dict(model.state_dict())
+    loss = lambda out, t: torch.nn.functional.cross_entropy(out, t, reduction="none")  # noqa: E731
+    g, st = cl.ghost_clipped_grad(dmodel, loss, clipping_norm=1.0, normalize_by=float(B),
+                                  return_aux=True, microbatch_size=100)
+    (out, aux), _ = g(x.to(dev), y.to(dev), state=st)
+    for i, n in enumerate(names):
+        assert _rel(out.pytree[n], want[i]) < 1e-5, n
+    assert aux.batch_size == B and aux.loss_values.shape == (B,)
+    torch.testing.assert_close(aux.grad_norms.cpu().double(), res.norms, rtol=1e-5, atol=0)
+    assert int(aux.num_clipped.item()) == clip_oracle.num_clipped(res.norms.float(), 1.0)
+    noise_fn, nstate = gaussian_noise(noise_multiplier=1.0, key=key(4), stream="device")
+    noisy, st2, nstate2 = g(x.to(dev), y.to(dev), state=st, noise_fn=noise_fn, noise_state=nstate)
+    assert isinstance(noisy[0], NoisedPytree) and nstate2._step_counter == 1
