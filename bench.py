@@ -20,6 +20,11 @@ of the linear surrogate loss, the streaming clip-and-sum, the CPU-generator
 noise draw) on a bounded sample of the same workload: the full layer with a
 reduced batch, timed on the host cores of the box.
 
+``--config 1`` measures BASELINE configs[0], the reference's CPU-runnable
+MLP (784-512-10, fp32, B = 256): the whole DP step on the GPU, eagerly and with
+the clip part replayed from a HIP graph; ``cpu_baseline`` there is the full
+configuration on the CPU.
+
 ``--config 3`` (not the default line) measures BASELINE configs[2]: a
 Llama-style block (d = 2048, 16 heads, SwiGLU 8192, RMSNorm, RoPE, bf16, B =
 16, T = 1024, vocab 32000, embedding and head frozen); ``value`` is the ghost
@@ -465,6 +470,150 @@ def run_block(args) -> dict:
     }
 
 
+MLP_B = 256
+
+
+def _mlp_ce(out, target):
+    import torch
+
+    return torch.nn.functional.cross_entropy(out, target, reduction="none")
+
+
+def mlp_cpu_baseline(threads: int, repeats: int = 3):
+    """The config-1 step as the reference runs it on the CPU: vmap(grad) of the
+    per-example cross-entropy, the streaming clip-and-sum and the CPU-generator
+    noise, at the full batch of 256.  Examples/s (median of ``repeats``)."""
+    import torch
+
+    from oracle import clip_oracle, ghost_oracle, noise_oracle
+
+    torch.set_num_threads(threads)
+    torch.manual_seed(0)
+    model = ghost_oracle.MLP()
+    params = {k: v.detach() for k, v in model.named_parameters()}
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(MLP_B, 784, generator=g)
+    y = torch.randint(0, 10, (MLP_B,), generator=g)
+
+    def step():
+        per = ghost_oracle.mlp_per_example_grads(model, params, x, y)
+        names = sorted(per)
+        res = clip_oracle.stream_clip_and_sum([per[n] for n in names],
+                                              clip_oracle.conservative_bound(C))
+        draws = noise_oracle.draws_for(res.reduced, noise_oracle.step_seed(0, 0))
+        return [noise_oracle.sample(v, NM * C, z) for v, z in zip(res.reduced, draws)]
+
+    step()
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return MLP_B / times[len(times) // 2]
+
+
+def run_mlp(args) -> dict:
+    import torch
+
+    from opake_amd import _native
+    from opake_amd.clipping import (
+        GraphedGhostClip,
+        ghost_capture,
+        ghost_clip_captured,
+        ghost_clipped_grad,
+    )
+    from opake_amd.noise import gaussian_noise
+    from opake_amd.random import key
+    from oracle import ghost_oracle
+
+    _native.load()
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    model = ghost_oracle.MLP().to(dev)
+    g = torch.Generator(device=dev).manual_seed(1)
+    x = torch.randn(MLP_B, 784, generator=g, device=dev)
+    y = torch.randint(0, 10, (MLP_B,), generator=g, device=dev)
+    noise_fn, state = gaussian_noise(noise_multiplier=NM, key=key(0), stream="device")
+    fn, st = ghost_clipped_grad(model, _mlp_ce, clipping_norm=C)
+    graphed = GraphedGhostClip(clipping_norm=C)
+
+    def timed(step, n, warm):
+        for _ in range(warm):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n
+
+    holder = {"state": state}
+
+    def full_eager():
+        _, _, holder["state"] = fn(x, y, state=st, noise_fn=noise_fn, noise_state=holder["state"])
+
+    def full_graphed():
+        caps, _ = ghost_capture(model, _mlp_ce, x, y)
+        _, holder["state"] = noise_fn(graphed(caps), holder["state"])
+
+    caps, _ = ghost_capture(model, _mlp_ce, x, y)
+    clip_eager_s = timed(lambda: ghost_clip_captured(caps, clipping_norm=C), args.steps,
+                         args.warmup)
+    clip_graph_s = timed(lambda: graphed(caps), args.steps, args.warmup)
+    eager_s = timed(full_eager, args.steps, args.warmup)
+    graph_s = timed(full_graphed, args.steps, args.warmup)
+    print(f"[bench] clip eager {1e3 * clip_eager_s:.3f} ms, graphed {1e3 * clip_graph_s:.3f} ms; "
+          f"full step eager {1e3 * eager_s:.3f} ms, graphed {1e3 * graph_s:.3f} ms",
+          file=sys.stderr, flush=True)
+    best = min(eager_s, graph_s)
+    flops = 2 * MLP_B * (784 * 512 + 512 * 10)  # clipped sums (flat layers)
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = min(len(os.sched_getaffinity(0)), 16)
+        cpu = {
+            "value": mlp_cpu_baseline(threads),
+            "unit": "examples/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": ("config 1 in full (B=256, float32): vmap(grad) of the per-example "
+                       "cross-entropy, streaming clip-and-sum, CPU randn noise; median of 3 "
+                       f"steps after 1 warm-up; {cpu_model()}"),
+        }
+    return {
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": 1e3 * best,
+        "value": MLP_B / best,
+        "dtype": "fp32",
+        "config": {
+            "workload": "MLP 784-512-10 (ReLU), fp32, B=256 flat inputs, per-example "
+                        "cross-entropy; full DP step on the GPU: forward, backward to the layer "
+                        "outputs, ghost clip + sum (flat norms) and device-stream noise "
+                        "(BASELINE configs[0])",
+            "global_batch": MLP_B,
+            "clipping_norm": C,
+            "noise_multiplier": NM,
+            "normalize_by": 1.0,
+            "full_step_eager_ms": 1e3 * eager_s,
+            "full_step_graphed_ms": 1e3 * graph_s,
+            "clip_eager_ms": 1e3 * clip_eager_s,
+            "clip_graphed_ms": 1e3 * clip_graph_s,
+            "value_from": "graphed" if graph_s <= eager_s else "eager",
+        },
+        "roofline": {
+            "bound": "latency",
+            "kernel": "whole step (launch-bound at this size)",
+            "achieved": flops / (clip_graph_s * 1e12),
+            "peak": 157.3,
+            "unit": "TFLOP/s",
+            "frac": flops / (clip_graph_s * 1e12) / 157.3,
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+
+
 LORA_B, LORA_T, LORA_D, LORA_H, LORA_KV, LORA_F, LORA_R = 8, 2048, 4096, 32, 8, 14336, 16
 
 
@@ -630,9 +779,9 @@ def run_lora(args) -> dict:
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--config", type=int, choices=(2, 3, 4, 5), default=2,
-                    help="BASELINE configuration: 2 (default line), 3 (transformer block), "
-                         "4 (LoRA) or 5 (MoE)")
+    ap.add_argument("--config", type=int, choices=(1, 2, 3, 4, 5), default=2,
+                    help="BASELINE configuration: 2 (default line), 1 (MLP), 3 (transformer "
+                         "block), 4 (LoRA) or 5 (MoE)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=200,
@@ -665,11 +814,12 @@ def main() -> int:
         print(json.dumps({"copy_calibration_bytes": n * 4, "copies": 5}), flush=True)
         return 0
 
-    if args.config in (3, 4, 5):
-        out = {3: run_block, 4: run_lora, 5: run_moe}[args.config](args)
+    if args.config in (1, 3, 4, 5):
+        out = {1: run_mlp, 3: run_block, 4: run_lora, 5: run_moe}[args.config](args)
         line = {"metric": METRIC, "value": out["value"], "unit": "examples/s", "n_gpus": 1,
                 "steps": out["steps"], "warmup": out["warmup"], "ms_per_step": out["ms_per_step"],
-                "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+                "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                "dtype": out.get("dtype", "bf16"),
                 "data": "synthetic", "config": out["config"], "roofline": out["roofline"],
                 "cpu_baseline": out["cpu_baseline"]}
         print(json.dumps(line), flush=True)
