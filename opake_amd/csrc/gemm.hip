@@ -440,20 +440,55 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
     };
 
-    // One K step on stage (gcur, acur), staging step s + 1 into (gnxt, anxt):
-    // the DMA of A's step s + 1 is issued first; then K sub-step kk's MFMAs,
-    // after which G chunks kk * kGCSub .. of step s + 1 go from the registers
-    // (scaled) into the other stage and the same registers are refilled with
-    // those chunks of step s + 2 -- each load is in flight for a whole step.  Fragments are
-    // double-buffered (sub-step kk + 1's reads are issued before sub-step kk's
-    // MFMAs), and the sched_barriers keep each chunk's store and reload inside
-    // its sub-step (the scheduler would otherwise sink all loads to the end of
-    // the step).  Before the barrier only the kGC G loads may still be
-    // outstanding.  Past the last step the stores and loads repeat the last
-    // step's (in-range) rows into the unused stage: every path issues the same
-    // memory operations, which keeps the counter waits exact.
+    // One K step on stage (gcur, acur), staging step s + 1 into (gnxt, anxt).
+    // On entry the fragments of sub-step 0 are in flight into `fa`.
+    //   * The DMA of A's step s + 1 is issued first.
+    //   * Sub-steps 0..2: the MFMAs of sub-step kk run while the fragments of
+    //     sub-step kk + 1 are read (fragments alternate between fa and fb); G
+    //     chunks of step s + 1 go from the registers (scaled) into the other
+    //     stage, and their registers are refilled with step s + 2, so each
+    //     load is in flight for a whole step.
+    //   * Barrier: the other stage is complete (the DMA has landed, every G
+    //     store is done), and this stage's last fragments are in registers.
+    //   * Sub-step 3: its MFMAs run while the fragments of sub-step 0 of step
+    //     s + 1 are read from the other stage.
+    // So the MFMAs of every sub-step, across step boundaries too, overlap the
+    // reads of the next, and the barrier is the only place a wave waits for
+    // the others.  With 8 waves the sched_group_barriers interleave each
+    // sub-step's 8 MFMAs with the 12 reads of the next (the scheduler would
+    // otherwise bunch them); with the sched_barriers they also keep each G
+    // chunk's store and reload inside its sub-step.  Before the barrier only
+    // the kGC G loads may still be outstanding.  Past the last step the stores
+    // and loads repeat the last step's (in-range) rows into the unused stage:
+    // every path issues the same memory operations, which keeps the counter
+    // waits exact.
     float sc_next = 0.0f;
     int row_next = 0, valid_next = kBK, valid_cur = kBK;
+    auto interleave = [&]() __attribute__((always_inline)) {
+      if constexpr (kWaves == 8) {
+#define DPC_SG(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
+#define DPC_SG_PAIR(reads) \
+  DPC_SG(0x008, 1);        \
+  DPC_SG(0x100, reads);    \
+  DPC_SG(0x002, 3)
+        // 0x008 MFMA, 0x100 LDS read, 0x002 VALU.
+        DPC_SG_PAIR(2); DPC_SG_PAIR(1); DPC_SG_PAIR(2); DPC_SG_PAIR(1);
+        DPC_SG_PAIR(2); DPC_SG_PAIR(1); DPC_SG_PAIR(2); DPC_SG_PAIR(1);
+#undef DPC_SG_PAIR
+      }
+    };
+    // LDS writes and global loads of the G chunks staged in a sub-step.
+    auto order_stores = [&](int chunks) __attribute__((always_inline)) {
+      if constexpr (kWaves == 8) {
+        if (chunks == 1) {
+          DPC_SG(0x200, 1); DPC_SG(0x020, 1);
+        } else {
+          DPC_SG(0x200, 2); DPC_SG(0x020, 2);
+        }
+#undef DPC_SG
+      }
+    };
+    Frags fa, fb;
     auto k_step = [&](int s, const uint8_t* gcur, const uint8_t* acur, uint8_t* gnxt,
                       uint8_t* anxt) __attribute__((always_inline)) {
       dma_a(anxt, row_next, valid_next);
@@ -463,28 +498,31 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       // Grouped mode: a segment's last step may hold fewer than 64 rows; the
       // MFMAs of 16-row sub-steps past them (all zeros) are skipped.
       const int vcur = kGrouped ? valid_cur : kBK;
-      Frags f0, f1;
       auto stage_g = [&](int kk) __attribute__((always_inline)) {
 #pragma unroll
         for (int c = 0; c < kGCSub; ++c) store_chunk(gnxt, kk * kGCSub + c, sc_next);
 #pragma unroll
         for (int c = 0; c < kGCSub; ++c) load_chunk(row2, valid2, kk * kGCSub + c);
       };
-      read_frags(gcur, acur, 0, f0);
-      read_frags(gcur, acur, 1, f1);
-      mma(f0);
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(gcur, acur, 1, fb);
+      mma(fa);
       stage_g(0);
+      interleave();
+      order_stores(1);
       __builtin_amdgcn_sched_barrier(0);
-      read_frags(gcur, acur, 2, f0);
-      if (vcur > 16) mma(f1);
+      read_frags(gcur, acur, 2, fa);
+      if (vcur > 16) mma(fb);
       stage_g(1);
+      interleave();
+      order_stores(1);
       __builtin_amdgcn_sched_barrier(0);
-      read_frags(gcur, acur, 3, f1);
-      if (vcur > 32) mma(f0);
+      read_frags(gcur, acur, 3, fb);
+      if (vcur > 32) mma(fa);
       stage_g(2);
-      __builtin_amdgcn_sched_barrier(0);
-      if (vcur > 48) mma(f1);
       stage_g(3);
+      interleave();
+      order_stores(2);
       __builtin_amdgcn_sched_barrier(0);
       sc_next = sc_after;
       row_next = row2;
@@ -492,12 +530,16 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       valid_next = valid2;
       DPC_WAIT_VMCNT(kGC);
       __syncthreads();
+      read_frags(gnxt, anxt, 0, fa);
+      if (vcur > 48) mma(fb);
+      interleave();
+      __builtin_amdgcn_sched_barrier(0);
     };
 
     uint8_t* g0 = lds_g;
     uint8_t* g1 = lds_g + kOperandBytes;
     // Prologue: step 0 into stage 0 (A by DMA, G through registers), step 1
-    // of G into the registers.
+    // of G into the registers, the fragments of step 0's first sub-step.
     int valid0;
     int row0 = step_row0(0, &sc_next, &valid0);
     valid_cur = valid0;
@@ -511,6 +553,7 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     for (int j = 0; j < kGC; ++j) load_chunk(row_next, valid_next, j);
     DPC_WAIT_VMCNT(kGC);  // the A DMA of step 0 has landed (kGC G loads may be in flight)
     __syncthreads();
+    read_frags(g0, lds_a0, 0, fa);
     int s = 0;
     for (; s + 1 < nsteps; s += 2) {
       k_step(s, g0, lds_a0, g1, lds_a1);
@@ -518,6 +561,9 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     }
     if (s < nsteps) k_step(s, g0, lds_a0, g1, lds_a1);
     DPC_WAIT_VMCNT(0);
+    // The last step's reads of the unused stage are done before the
+    // epilogue reuses the G stages.
+    __syncthreads();
   }
 
   // Epilogue: the 256 x 256 fp32 tile goes through LDS in four quarters of 64
