@@ -14,6 +14,13 @@
 // resident at once.  Workgroups are placed so that all pairs of one example
 // run on one XCD (hardware dispatch is round-robin over the 8 XCDs): the pairs
 // re-read the example's rows from that XCD's L2 instead of from HBM.
+//
+// A lone workgroup has one wave per SIMD, so the K loop hides LDS latency
+// itself: every group of four MFMAs runs while the next group's fragments
+// are read, the barrier sits before a step's last group (which overlaps the
+// next step's first reads), and the loop body has no branch around the
+// accumulators (operands ordered so that din <= dout: the loop is the
+// "both Gram matrices" body for A's K range, then a "G G^T only" body).
 #include "common.h"
 
 namespace {
@@ -109,35 +116,33 @@ __device__ __forceinline__ void store_operand(uint8_t* tile, const u32x4_t r[2])
   }
 }
 
-// acc[i][j] += X_p[rows wr*64 + i*32 ..] . X_q[rows wc*64 + j*32 ..] over the
-// 16-deep sub-step kk of a staged K step.  `live` bit i (j + 2) says whether
-// the 32-row block i of the p tile (j of the q tile) holds rows of the
-// segment; blocks past its end are all zero, and their MFMAs are skipped.
-__device__ __forceinline__ void gram_mma(const uint8_t* tp, const uint8_t* tq, int kk,
-                                         f32x16_t acc[2][2], int live) {
+// Fragments of the 16-deep sub-step kk of a staged K step for this wave's
+// 64 x 64 block: a = X_p rows wr*64 + i*32 .., b = X_q rows wc*64 + j*32 ...
+struct GramFrags {
+  bf16x8_t a[2], b[2];
+};
+
+__device__ __forceinline__ void gram_read(const uint8_t* tp, const uint8_t* tq, int kk,
+                                          GramFrags& f) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wr = w >> 1, wc = w & 1;
   const int c = kk * 2 + (lane >> 5);
-  bf16x8_t a[2], b[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    a[i] = *reinterpret_cast<const bf16x8_t*>(tp + gtile_off(wr * 64 + i * 32 + (lane & 31), c));
-    b[i] = *reinterpret_cast<const bf16x8_t*>(tq + gtile_off(wc * 64 + i * 32 + (lane & 31), c));
+    f.a[i] = *reinterpret_cast<const bf16x8_t*>(tp + gtile_off(wr * 64 + i * 32 + (lane & 31), c));
+    f.b[i] = *reinterpret_cast<const bf16x8_t*>(tq + gtile_off(wc * 64 + i * 32 + (lane & 31), c));
   }
-  if (live == 15) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-    return;
-  }
+}
+
+// acc[i][j] += a[i] . b[j].  Rows past the segment's end read as zero, so
+// the blocks they fill add nothing (their MFMAs are not skipped: a branch
+// per block would put the accumulators behind control flow).
+__device__ __forceinline__ void gram_mma(const GramFrags& f, f32x16_t acc[2][2]) {
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-      if ((live >> i & 1) && (live >> (j + 2) & 1))
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
 }
 
 // Grouped mode: work item l is (problem << 16 | pair, first row, rows, slot)
@@ -187,14 +192,15 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
   int p, q;
   pair_from_index(pair, &p, &q);
   const bool diag = (p == q);
-  int live = 0;
-  {
-    const int w = threadIdx.x >> 6, wr = w >> 1, wc = w & 1;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      if (p * kGramTile + wr * 64 + i * 32 < T) live |= 1 << i;
-      if (q * kGramTile + wc * 64 + i * 32 < T) live |= 1 << (i + 2);
-    }
+  // <A A^T, G G^T> is symmetric in A and G: order them so that din <= dout;
+  // the K loop then has one shape (both Gram matrices, then G G^T alone).
+  if (din > dout) {
+    const uint16_t* t = Xa;
+    Xa = Xg;
+    Xg = t;
+    const int d = din;
+    din = dout;
+    dout = d;
   }
 
   const GramOperand ap = make_operand(Xa, T, din, p * kGramTile);
@@ -211,18 +217,16 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
     for (int j = 0; j < 2; ++j) pa[i][j] = pg[i][j] = f32x16_t{};
 
   // Registers hold the next K step of the four operands (the q operands are
-  // not loaded on diagonal pairs).  Past an operand's last step the loads
-  // repeat its last step, so every path issues the same loads.
+  // not loaded on diagonal pairs).  Past an operand's K range the loads read
+  // zeros, so every path issues the same loads.
   u32x4_t rap[2], raq[2], rgp[2], rgq[2];
   auto load_a = [&](int step) {
-    const int t = min(step, nka - 1);
-    load_operand(ap, t, rap);
-    if (!diag) load_operand(aq, t, raq);
+    load_operand(ap, step, rap);
+    if (!diag) load_operand(aq, step, raq);
   };
   auto load_g = [&](int step) {
-    const int t = min(step, nkg - 1);
-    load_operand(gp, t, rgp);
-    if (!diag) load_operand(gq, t, rgq);
+    load_operand(gp, step, rgp);
+    if (!diag) load_operand(gq, step, rgq);
   };
   auto store_a = [&](uint8_t* stage) {
     store_operand(stage, rap);
@@ -240,32 +244,81 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
   load_a(1);
   load_g(1);
   __syncthreads();
-  // Step s: sub-step 0 multiplies A (and then stores A's step s + 1 and
-  // reloads A's step s + 2), sub-step 1 multiplies G likewise, both on the
-  // current stage; each load is in flight for a whole step.
-  for (int s = 0; s < nk; ++s) {
+  // A K step is four groups of MFMAs on the current stage -- A sub-steps 0
+  // and 1, then G sub-steps 0 and 1 -- and each group's fragments are read
+  // before the previous group's MFMAs (two fragment sets, fx and fy), so the
+  // LDS latency overlaps MFMA work even with one wave per SIMD.  A's step
+  // s + 1 is stored into the other stage (and its registers reloaded with
+  // step s + 2) after A's MFMAs, G's after G's; each load is in flight for a
+  // whole step.  The barrier before the last group completes the other
+  // stage, so the next step's first fragments are read from it while that
+  // group's MFMAs run.  (Every wave's reads of the current stage are done at
+  // the barrier -- it waits for the wave's LDS operations -- so the next step
+  // may overwrite it.)
+  auto stage_ptrs = [&](const uint8_t* st, const uint8_t** tap, const uint8_t** taq,
+                        const uint8_t** tgp, const uint8_t** tgq) __attribute__((always_inline)) {
+    *tap = st;
+    *taq = diag ? st : st + kGTileBytes;
+    *tgp = st + 2 * kGTileBytes;
+    *tgq = diag ? *tgp : st + 3 * kGTileBytes;
+  };
+  GramFrags fx, fy;
+  {
+    const uint8_t *tap, *taq, *tgp, *tgq;
+    stage_ptrs(lds, &tap, &taq, &tgp, &tgq);
+    gram_read(tap, taq, 0, fx);
+  }
+  // Steps inside A's K range (nka <= nkg): on entry fx holds (in flight) A's
+  // sub-step 0 fragments of the current stage.
+  auto step_ag = [&](int s) __attribute__((always_inline)) {
     const uint8_t* cur = lds + (s & 1) * kGStageBytes;
     uint8_t* nxt = lds + ((s + 1) & 1) * kGStageBytes;
-    const uint8_t* cap = cur;
-    const uint8_t* caq = diag ? cur : cur + kGTileBytes;
-    const uint8_t* cgp = cur + 2 * kGTileBytes;
-    const uint8_t* cgq = diag ? cgp : cur + 3 * kGTileBytes;
-    if (s < nka) {
-      gram_mma(cap, caq, 0, pa, live);
-      gram_mma(cap, caq, 1, pa, live);
-    }
+    const uint8_t *cap, *caq, *cgp, *cgq, *nap, *naq, *ngp, *ngq;
+    stage_ptrs(cur, &cap, &caq, &cgp, &cgq);
+    stage_ptrs(nxt, &nap, &naq, &ngp, &ngq);
+    gram_read(cap, caq, 1, fy);
+    gram_mma(fx, pa);
     store_a(nxt);
     load_a(s + 2);
     __builtin_amdgcn_sched_barrier(0);
-    if (s < nkg) {
-      gram_mma(cgp, cgq, 0, pg, live);
-      gram_mma(cgp, cgq, 1, pg, live);
-    }
+    gram_read(cgp, cgq, 0, fx);
+    gram_mma(fy, pa);
+    gram_read(cgp, cgq, 1, fy);
+    gram_mma(fx, pg);
     store_g(nxt);
     load_g(s + 2);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
-  }
+    // The next step's first fragments: A's sub-step 0, or G's past A's range.
+    if (s + 1 < nka) gram_read(nap, naq, 0, fx);
+    else gram_read(ngp, ngq, 0, fx);
+    gram_mma(fy, pg);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Steps past A's K range: on entry fx holds G's sub-step 0 fragments.  (A's
+  // loads, past its range, read zeros: every step issues the same loads.)
+  auto step_g = [&](int s) __attribute__((always_inline)) {
+    const uint8_t* cur = lds + (s & 1) * kGStageBytes;
+    uint8_t* nxt = lds + ((s + 1) & 1) * kGStageBytes;
+    const uint8_t *cap, *caq, *cgp, *cgq, *nap, *naq, *ngp, *ngq;
+    stage_ptrs(cur, &cap, &caq, &cgp, &cgq);
+    stage_ptrs(nxt, &nap, &naq, &ngp, &ngq);
+    gram_read(cgp, cgq, 1, fy);
+    gram_mma(fx, pg);
+    store_a(nxt);
+    load_a(s + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    store_g(nxt);
+    load_g(s + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    gram_read(ngp, ngq, 0, fx);
+    gram_mma(fy, pg);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int s = 0;
+  for (; s < nka; ++s) step_ag(s);
+  for (; s < nkg; ++s) step_g(s);
 
   // Both tiles share the MFMA output layout, so the element-wise product
   // needs no knowledge of which (s, t) a register holds.
