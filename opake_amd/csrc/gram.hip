@@ -160,15 +160,67 @@ struct GramItems {
   int dout[kMaxGramProblems];
 };
 
+// Dense mode: the order in which an XCD's work items are dispatched.
+// Hardware hands an XCD's workgroups to its CUs in turn, so when an XCD has
+// n items and C CUs (C < n <= 2 C), the items at positions k and C + k share
+// CU k.  Diagonal pairs (p == q: two operand tiles instead of four) are the
+// light items, so they go first and last -- the CUs that run two items run
+// two light ones -- and the off-diagonal pairs fill the middle.  All items of
+// the XCD's range stay on it (its L2 holds their examples).
+
+// Diagonal pairs (pair index q (q + 3) / 2) of an example below pair index r.
+__device__ __forceinline__ int diag_below(int r, int nt) {
+  int c = 0;
+  while (c < nt && c * (c + 3) / 2 < r) ++c;
+  return c;
+}
+
+// Diagonal items among items 0 .. L - 1 (example-major order).
+__device__ __forceinline__ int diag_before(int L, int npairs, int nt) {
+  return (L / npairs) * nt + diag_below(L % npairs, nt);
+}
+
+// Pair index of the j-th off-diagonal pair (p < q) of an example.
+__device__ __forceinline__ int offdiag_pair(int j) {
+  int q = 1;
+  while (j >= q) {
+    j -= q;
+    ++q;
+  }
+  return q * (q + 1) / 2 + j;
+}
+
+// Item (example-major index) at dispatch position pos of the range
+// L0 .. L0 + n - 1 of an XCD with `cus` CUs.
+__device__ __forceinline__ int dense_item(int pos, int L0, int n, int npairs, int nt, int cus) {
+  const int f0 = diag_before(L0, npairs, nt);
+  const int nd = diag_before(L0 + n, npairs, nt) - f0;
+  const int no = n - nd;
+  const int a = min(nd, max(0, n - cus));
+  if (pos < a || pos >= a + no) {
+    const int r = f0 + (pos < a ? pos : pos - no);
+    const int qd = r % nt;
+    return (r / nt) * npairs + qd * (qd + 3) / 2;
+  }
+  const int noff = npairs - nt;
+  const int r = (L0 - f0) + (pos - a);
+  return (r / noff) * npairs + offdiag_pair(r % noff);
+}
+
 template <bool kGrouped>
 __global__ void __launch_bounds__(kGramMfmaThreads, 2)
 gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ G, int T,
                       int din, int dout, int npairs, int nblocks, double* __restrict__ partial,
-                      GramItems work) {
+                      GramItems work, int xcd_cus) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kGStageBytes];
   __shared__ double red[kGramMfmaThreads / 64];
-  const int l = xcd_logical_block(gridDim.x, nblocks);
+  int l = xcd_logical_block(gridDim.x, nblocks);
   if (l < 0) return;  // padding workgroup: exits before any barrier
+  if (!kGrouped) {
+    const int per = gridDim.x / kXcds, x = blockIdx.x % kXcds, L0 = x * per;
+    const int nt = ceil_div(T, kGramTile);
+    l = dense_item(blockIdx.x / kXcds, L0, min(per, nblocks - L0), npairs, nt, xcd_cus);
+  }
   const uint16_t* Xa;
   const uint16_t* Xg;
   int pair, slot = l;
@@ -498,6 +550,21 @@ row_sum_f64_kernel(const double* __restrict__ x, int B, int n, int accumulate,
   out[b] = accumulate ? out[b] + s : s;
 }
 
+// CUs per XCD of the current device (cached per device; 32 on MI355X).
+int xcd_cus() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 32;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n < kXcds)
+      n = 256;
+    cached[dev] = n / kXcds;
+  }
+  return cached[dev];
+}
+
 }  // namespace
 
 extern "C" size_t dpc_gram_workspace_bytes(int B, int T) {
@@ -533,7 +600,7 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
     GramItems none = {};
     hipLaunchKernelGGL(gram_mfma_bf16_kernel<false>, dim3(padded), dim3(kGramMfmaThreads), 0, s,
                        (const uint16_t*)A, (const uint16_t*)G, T, din, dout, npairs, nblocks,
-                       partial, none);
+                       partial, none, xcd_cus());
   } else {
     int nt = ceil_div(T, kGenTile);
     npairs = nt * (nt + 1) / 2;
@@ -600,7 +667,7 @@ extern "C" int dpc_grouped_gram_sqnorms(const int64_t* a_ptrs, const int64_t* g_
     if (dtype == DPC_BF16 && aligned && fits) {
       const int padded = ceil_div(n_items, kXcds) * kXcds;
       hipLaunchKernelGGL(gram_mfma_bf16_kernel<true>, dim3(padded), dim3(kGramMfmaThreads), 0, s,
-                         nullptr, nullptr, 0, 0, 0, 0, n_items, partial, work);
+                         nullptr, nullptr, 0, 0, 0, 0, n_items, partial, work, 0);
     } else if (dtype == DPC_BF16) {
       hipLaunchKernelGGL(gram_grouped_generic_kernel<uint16_t>, dim3(n_items), dim3(kGramThreads),
                          0, s, work, partial);

@@ -198,6 +198,14 @@ _GRAM_TILE = 128  # rows of a Gram tile of the grouped norm kernel
 _STEP_ROWS = 64  # rows of a K step of the grouped clipped sum
 
 
+def _xcd_cus(device) -> int:
+    """CUs per XCD of a ROCm device (8 XCDs; 32 CUs each on MI355X)."""
+    dev = torch.device(device)
+    if dev.type != "cuda" or not torch.cuda.is_available():
+        return 32
+    return max(1, torch.cuda.get_device_properties(dev).multi_processor_count // 8)
+
+
 class SegmentLayout:
     """Rows of E problems cut into per-example segments, built on the host.
 
@@ -214,34 +222,48 @@ class SegmentLayout:
     XCDS = 8
 
     @classmethod
-    def _xcd_schedule(cls, items, cost, seg_of_item, item_start):
+    def _xcd_schedule(cls, items, cost, seg_of_item, item_start, xcd_cus=32):
         """Order Gram items for the kernel's XCD placement (item l of a launch of
-        8 * per runs on XCD l // per): segments go whole to the least loaded of
-        8 bins, most expensive first, so each XCD gets a balanced share, works
-        through it most expensive first and keeps a segment's tile pairs (which
-        re-read the same rows) together in its L2.  Bins are padded to equal
-        length with empty items (problem field -1)."""
+        8 * per runs on XCD l // per): segments go whole to the 8 bins, most
+        expensive first in snake order, so each XCD gets a balanced share and
+        keeps a segment's tile pairs (which re-read the same rows) together in
+        its L2.
+        Within a bin, hardware hands the items to the XCD's CUs in turn, so
+        with n items on C CUs (C < n <= 2 C) the items at positions k and C + k
+        share CU k: the 2 (n - C) lightest items take those positions (first
+        and last) and the rest the middle; otherwise the bin runs segment by
+        segment.  Bins are padded to equal length with empty items (problem
+        field -1)."""
         import numpy as np
 
         n_seg = len(item_start) - 1
-        seg_cost = np.zeros(n_seg)
-        np.add.at(seg_cost, seg_of_item, cost)
-        bins = [[] for _ in range(cls.XCDS)]
-        load = np.zeros(cls.XCDS)
-        for v in np.argsort(-seg_cost, kind="stable"):
-            if item_start[v + 1] == item_start[v]:
-                continue
-            b = int(np.argmin(load))
-            bins[b].append(v)
-            load[b] += seg_cost[v]
-        per = max((sum(int(item_start[v + 1] - item_start[v]) for v in b) for b in bins), default=0)
+        counts = np.diff(item_start)
+        seg_cost = np.bincount(seg_of_item, weights=cost, minlength=n_seg)
+        # Segments with items, most expensive first, dealt to the bins in
+        # snake order (0..7, 7..0, ...): balanced to within one segment.
+        order = np.argsort(-seg_cost, kind="stable")
+        order = order[counts[order] > 0]
+        r = np.arange(len(order))
+        lap, pos = r // cls.XCDS, r % cls.XCDS
+        seg_bin = np.where(lap % 2 == 0, pos, cls.XCDS - 1 - pos)
+        per = int(np.bincount(seg_bin, weights=counts[order], minlength=cls.XCDS).max()) \
+            if len(order) else 0
         out = np.zeros((cls.XCDS * per, 4), dtype=np.int64)
         out[:, 0] = -1
-        for x, b in enumerate(bins):
-            rows = [items[item_start[v]:item_start[v + 1]] for v in b]
-            if rows:
-                chunk = np.concatenate(rows)
-                out[x * per:x * per + len(chunk)] = chunk
+        for x in range(cls.XCDS):
+            segs = order[seg_bin == x]  # most expensive first
+            if not len(segs):
+                continue
+            lens = counts[segs]
+            first = np.repeat(item_start[segs] - (np.cumsum(lens) - lens), lens)
+            idx = first + np.arange(int(lens.sum()))
+            n = len(idx)
+            a = n - xcd_cus
+            if 0 < a and n <= 2 * xcd_cus:
+                by_cost = idx[np.argsort(cost[idx], kind="stable")]
+                light, heavy = by_cost[:2 * a], by_cost[2 * a:][::-1]
+                idx = np.concatenate([light[:a], heavy, light[a:]])
+            out[x * per:x * per + n] = items[idx]
         return out
 
     def __init__(self, lengths, device, gram_weights=None):
@@ -284,7 +306,7 @@ class SegmentLayout:
         slot = np.arange(self.n_items)
         items = np.stack([(group[seg_of_item] << 16) | pair, row0[seg_of_item], seg_len, slot],
                          axis=1)
-        items = self._xcd_schedule(items, cost, seg_of_item, item_start)
+        items = self._xcd_schedule(items, cost, seg_of_item, item_start, _xcd_cus(device))
         self.max_steps = int(((flat + _STEP_ROWS - 1) // _STEP_ROWS).sum())
         # One int32 buffer: row0 [S] | len [S] | group [S] | rows [E] |
         # item_start [S + 1] | items [n_items * 4].
