@@ -123,7 +123,10 @@ int dpc_clip_factors(const double* sqnorm, int B, double C, int kind, double gam
  * is scaled in fp32 and rounded to bf16 once before the product.  With
  * with_bias, bias_out[m] = same recipe over
  * sum_i scale[i] * sum_t G[i, t, m], its noise keyed by (seed, bias_leaf_id)
- * under the [dout, 1] view.
+ * under the [dout, 1] view.  ws (dpc_clipped_sum_workspace_bytes) holds the
+ * bias partials and, on the MFMA path for layers of fewer than 192 256 x 256
+ * output tiles, the fp32 K-slices of a split-K launch (summed in a fixed
+ * order); with a smaller ws (or none, without bias) the launch is one pass.
  * -------------------------------------------------------------------------*/
 size_t dpc_clipped_sum_workspace_bytes(int B, int T, int din, int dout, int dtype);
 int dpc_clipped_sum(const void* A, const void* G, const float* scale, const void* plan, int B,

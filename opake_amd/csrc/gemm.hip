@@ -223,6 +223,12 @@ struct FastArgs {
   const float* scale;
   Epilogue ep;
   GroupedTables grp;
+  // Dense split-K: workgroup (split, tile) takes steps
+  // [split * n / splits, (split + 1) * n / splits) of the n steps and, for
+  // splits > 1, writes its raw fp32 tile to partial[split] ([M][N]); the
+  // reduce kernel adds the splits in order and applies the epilogue.
+  int splits;
+  float* partial;
 };
 
 // Per-lane LDS offsets of the transposing fragment reads.  For a 32 x 16
@@ -273,10 +279,13 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
   const int M = args.ep.M, N = args.ep.N, T = args.T;
   const int tiles_m = ceil_div(M, kBM), tiles_n = ceil_div(N, kBN);
   int lin = xcd_linear_id(gridDim.x);
-  int grp = 0;
+  int grp = 0, split = 0;
   if (kGrouped) {
     grp = lin / (tiles_m * tiles_n);
     lin -= grp * tiles_m * tiles_n;
+  } else if (args.splits > 1) {
+    split = lin / (tiles_m * tiles_n);
+    lin -= split * tiles_m * tiles_n;
   }
   int tm, tn;
   tile_coords(lin, tiles_m, tiles_n, &tm, &tn);
@@ -287,7 +296,7 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
   Epilogue ep = args.ep;
   const uint16_t* Abase = args.A;
   const uint16_t* Gbase = args.G;
-  int total_rows, nsteps, step0 = 0, nactive = 0;
+  int total_rows, nsteps, step0 = 0, nactive = 0, step_base = 0;
   const int spe = T / kBK;
   ClipPlanView plan = clip_plan_view(const_cast<void*>(args.plan), args.B);
   if (kGrouped) {
@@ -311,7 +320,9 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     __syncthreads();
   } else {
     nactive = *plan.nactive;
-    nsteps = nactive * spe;
+    const long long all = (long long)nactive * spe;
+    step_base = (int)(all * split / args.splits);
+    nsteps = (int)(all * (split + 1) / args.splits) - step_base;
     total_rows = args.B * T;
   }
 
@@ -350,6 +361,7 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     // Dense: step t covers rows [active[t / spe] * T + (t % spe) * 64, +64).
     // Grouped: step t is table entry step0 + t.
     auto step_row0 = [&](int t, float* sc, int* valid) __attribute__((always_inline)) {
+      t += step_base;  // dense split-K: this workgroup's first step
       const int slot = kGrouped ? t : t / spe;
       if (slot - plan_base >= 64) {
         refill_plan(slot);
@@ -593,12 +605,24 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     __syncthreads();
     const int cl = 2 * (tid & 127);
     const int rr = (tid >> 7) * kEpiRows;
+    if (!kGrouped && args.splits > 1) {
+      // Split-K: the raw fp32 tile; the reduce kernel finishes it.
+      float* part = args.partial + (size_t)split * M * N;
 #pragma unroll 2
-    for (int ml = rr; ml < rr + kEpiRows; ml += 2) {
-      const float2 t0 = *reinterpret_cast<const float2*>(tile + ml * kEpiLd + cl);
-      const float2 t1 = *reinterpret_cast<const float2*>(tile + (ml + 1) * kEpiLd + cl);
-      const float v[2][2] = {{t0.x, t0.y}, {t1.x, t1.y}};
-      emit_quad(ep, m0 + quarter * kQuarterRows + ml, n0 + cl, v);
+      for (int ml = rr; ml < rr + kEpiRows; ++ml) {
+        const int m = m0 + quarter * kQuarterRows + ml, n = n0 + cl;
+        if (m < M && n < N)
+          *reinterpret_cast<float2*>(part + (size_t)m * N + n) =
+              *reinterpret_cast<const float2*>(tile + ml * kEpiLd + cl);
+      }
+    } else {
+#pragma unroll 2
+      for (int ml = rr; ml < rr + kEpiRows; ml += 2) {
+        const float2 t0 = *reinterpret_cast<const float2*>(tile + ml * kEpiLd + cl);
+        const float2 t1 = *reinterpret_cast<const float2*>(tile + (ml + 1) * kEpiLd + cl);
+        const float v[2][2] = {{t0.x, t0.y}, {t1.x, t1.y}};
+        emit_quad(ep, m0 + quarter * kQuarterRows + ml, n0 + cl, v);
+      }
     }
     __syncthreads();
   }
@@ -615,6 +639,40 @@ __global__ void __launch_bounds__(kFastWaves * 64, 1) clipped_sum_bf16_kernel(Fa
 template <bool kGrouped>
 void launch_fast(dim3 grid, hipStream_t s, const FastArgs& args) {
   hipLaunchKernelGGL(clipped_sum_bf16_kernel<kGrouped>, grid, dim3(kFastWaves * 64), 0, s, args);
+}
+
+// Split-K finish: out = epilogue(sum over splits of partial[split], in
+// order).  One thread per (row pair, column pair); M and N are even.
+__global__ void __launch_bounds__(kThreads)
+split_reduce_kernel(const float* __restrict__ partial, int splits, Epilogue ep) {
+  const int half_n = ep.N / 2;
+  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long long)(ep.M / 2) * half_n) return;
+  const int m = 2 * (int)(idx / half_n), n = 2 * (int)(idx % half_n);
+  const size_t plane = (size_t)ep.M * ep.N;
+  float v[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+  for (int sp = 0; sp < splits; ++sp) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const float2 t = *reinterpret_cast<const float2*>(partial + sp * plane +
+                                                        (size_t)(m + r) * ep.N + n);
+      v[r][0] += t.x;
+      v[r][1] += t.y;
+    }
+  }
+  emit_quad(ep, m, n, v);
+}
+
+// Split-K factor of a dense fast-path launch: launches of fewer than 192
+// output tiles (on 256 CUs) take their K steps in up to 8 slices so that the
+// grid fills the chip; the slices' fp32 tiles go through a workspace.
+int fast_splits(int B, int T, int din, int dout) {
+  const int ntiles = ceil_div(dout, kBM) * ceil_div(din, kBN);
+  if (ntiles >= 192) return 1;
+  int splits = 1;
+  const long long steps = (long long)B * (T / kBK);
+  while (splits < 8 && ntiles * splits * 2 <= 256 && steps >= 8LL * splits * 2) splits *= 2;
+  return splits;
 }
 
 #undef DPC_WAIT_VMCNT
@@ -921,6 +979,8 @@ extern "C" int dpc_grouped_clipped_sum(const int64_t* a_ptrs, const int64_t* g_p
     args.scale = nullptr;
     args.ep = ep;
     args.grp = grp;
+    args.splits = 1;
+    args.partial = nullptr;
     const long long ntiles = (long long)ceil_div(dout, kBM) * ceil_div(din, kBN) * E;
     if (ntiles > 0x7fffffff) return DPC_ENOTSUP;
     launch_fast<true>(dim3((unsigned)ntiles), s, args);
@@ -936,13 +996,27 @@ extern "C" int dpc_grouped_clipped_sum(const int64_t* a_ptrs, const int64_t* g_p
   return DPC_OK;
 }
 
+namespace {
+// Workspace layout: the bias split partials (kBiasSplits x dout floats), then,
+// 256-byte aligned, the split-K tiles of a dense fast-path launch.
+size_t bias_ws_bytes(int dout) {
+  return ((size_t)kBiasSplits * (size_t)dout * sizeof(float) + 255) & ~(size_t)255;
+}
+bool fast_shape(int B, int T, int din, int dout, int dtype) {
+  const size_t rows = (size_t)B * (size_t)T;
+  const bool small = rows * (size_t)(din > dout ? din : dout) * 2 < ((size_t)1 << 31);
+  return dtype == DPC_BF16 && T % kBK == 0 && din % 8 == 0 && dout % 8 == 0 && B > 0 && small;
+}
+}  // namespace
+
 extern "C" size_t dpc_clipped_sum_workspace_bytes(int B, int T, int din, int dout, int dtype) {
-  (void)B;
-  (void)T;
-  (void)din;
-  (void)dtype;
-  if (dout <= 0) return 0;
-  return (size_t)kBiasSplits * (size_t)dout * sizeof(float);
+  if (dout <= 0 || din <= 0 || T <= 0 || B < 0) return 0;
+  size_t bytes = bias_ws_bytes(dout);
+  if (fast_shape(B, T, din, dout, dtype)) {
+    const int splits = fast_splits(B, T, din, dout);
+    if (splits > 1) bytes += (size_t)splits * (size_t)dout * (size_t)din * sizeof(float);
+  }
+  return bytes;
 }
 
 extern "C" int dpc_clipped_sum(const void* A, const void* G, const float* scale, const void* plan,
@@ -963,7 +1037,7 @@ extern "C" int dpc_clipped_sum(const void* A, const void* G, const float* scale,
   if (sigma != 0.0 && noise_mode == DPC_NOISE_NONE) return DPC_EINVAL;
   if (sigma != 0.0 && noise_mode == DPC_NOISE_INJECTED && (!noise || (with_bias && !bias_noise)))
     return DPC_EINVAL;
-  if (with_bias && (!bias_out || !ws || ws_bytes < dpc_clipped_sum_workspace_bytes(B, T, din, dout, dtype)))
+  if (with_bias && (!bias_out || !ws || ws_bytes < bias_ws_bytes(dout)))
     return with_bias && !bias_out ? DPC_EINVAL : DPC_ENOSPC;
   hipStream_t s = (hipStream_t)stream;
 
@@ -981,10 +1055,7 @@ extern "C" int dpc_clipped_sum(const void* A, const void* G, const float* scale,
   ep.out = out;
 
   // Buffer offsets are 32-bit: each operand must stay below 2 GiB.
-  const size_t rows = (size_t)B * (size_t)T;
-  const bool small = rows * (size_t)(din > dout ? din : dout) * 2 < ((size_t)1 << 31);
-  const bool fast = dtype == DPC_BF16 && T % kBK == 0 && din % 8 == 0 && dout % 8 == 0 &&
-                    plan != nullptr && B > 0 && small;
+  const bool fast = fast_shape(B, T, din, dout, dtype) && plan != nullptr;
   if (fast) {
     FastArgs args;
     args.A = (const uint16_t*)A;
@@ -994,8 +1065,20 @@ extern "C" int dpc_clipped_sum(const void* A, const void* G, const float* scale,
     args.plan = plan;
     args.scale = scale;
     args.ep = ep;
+    // Split-K only with a workspace that holds the slices (else one pass).
+    int splits = fast_splits(B, T, din, dout);
+    const size_t need = bias_ws_bytes(dout) + (size_t)splits * dout * (size_t)din * sizeof(float);
+    if (splits > 1 && (!ws || ws_bytes < need)) splits = 1;
+    args.splits = splits;
+    args.partial = splits > 1 ? (float*)((uint8_t*)ws + bias_ws_bytes(dout)) : nullptr;
     const int ntiles = ceil_div(dout, kBM) * ceil_div(din, kBN);
-    launch_fast<false>(dim3(ntiles), s, args);
+    launch_fast<false>(dim3(ntiles * splits), s, args);
+    if (splits > 1) {
+      DPC_HIP_CHECK(hipGetLastError());
+      const long long quads = (long long)(dout / 2) * (din / 2);
+      hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((quads + kThreads - 1) / kThreads)),
+                         dim3(kThreads), 0, s, (const float*)args.partial, splits, ep);
+    }
   } else {
     dim3 grid(ceil_div(din, kGT), ceil_div(dout, kGT));
     if (dtype == DPC_BF16) {

@@ -175,7 +175,9 @@ def clipped_sum(
     out = torch.empty((dout, din), dtype=out_dtype, device=dev)
     bias_out = torch.empty(dout, dtype=out_dtype, device=dev) if with_bias else None
     ws_bytes = nat.load().dpc_clipped_sum_workspace_bytes(B, T, din, dout, nat.dtype_code(A.dtype))
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if with_bias else None
+    # The workspace holds the bias partials and, for launches of few output
+    # tiles, the split-K slices.
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
     spec = noise or NoiseSpec(sigma=0.0, mode=nat.NOISE_NONE)
     if spec.sigma != 0.0 and spec.mode == nat.NOISE_INJECTED:
         for t, shape in ((spec.noise, (dout, din)), (spec.bias_noise, (dout,))):
@@ -188,7 +190,7 @@ def clipped_sum(
         din, dout, nat.dtype_code(A.dtype), float(normalize_by), spec.mode,
         nat.ptr(spec.noise), nat.ptr(spec.bias_noise), spec.seed & ((1 << 64) - 1),
         spec.leaf_id & 0xFFFFFFFF, spec.bias_leaf_id & 0xFFFFFFFF, float(spec.sigma), nat.dtype_code(out_dtype), nat.ptr(out),
-        int(with_bias), nat.ptr(bias_out), nat.ptr(ws), ws_bytes if with_bias else 0,
+        int(with_bias), nat.ptr(bias_out), nat.ptr(ws), ws_bytes if ws is not None else 0,
         nat.stream_handle(dev),
     )
     return out, bias_out

@@ -207,6 +207,30 @@ def test_clipped_sum_bf16_mfma(dev, B, T, din, dout):
     torch.testing.assert_close(cf.norms.cpu().double(), res.norms, rtol=2e-2, atol=0)
 
 
+@pytest.mark.parametrize("B,T,din,dout", [(8, 256, 512, 264), (16, 128, 256, 256)])
+def test_clipped_sum_split_k(dev, B, T, din, dout):
+    """Launches of few output tiles split their K steps (2-8 slices through the
+    workspace, added in a fixed order): same result as the oracle, the same
+    bits on every run, and the fused Philox noise equal to the noise kernel's."""
+    assert nat.load().dpc_clipped_sum_workspace_bytes(B, T, din, dout, nat.DPC_BF16) > \
+        nat.load().dpc_clipped_sum_workspace_bytes(B, T, din, dout, nat.DPC_F32)
+    g = _gen(B * T + din)
+    A = torch.randn(B, T, din, generator=g).to(torch.bfloat16)
+    G = (torch.randn(B, T, dout, generator=g) * 0.01 *
+         torch.exp(torch.randn(B, 1, 1, generator=g))).to(torch.bfloat16)
+    w, b, cf = _run_clipped_sum(dev, A, G, 1.0, nb=2.0, bias=True, out_dtype=torch.float32)
+    (wb, ww), _ = _oracle_clipped_sum(A, G, 1.0, nb=2.0, bias=True, out_dtype=torch.float32)
+    assert _rel_err(w.cpu(), ww) < 2e-2
+    assert _rel_err(b.cpu(), wb) < 2e-2
+    w2, _, _ = _run_clipped_sum(dev, A, G, 1.0, nb=2.0, bias=True, out_dtype=torch.float32)
+    assert torch.equal(w, w2)
+    kw = dict(plan=cf.plan, normalize_by=2.0, out_dtype=torch.bfloat16)
+    center, _ = ops.clipped_sum(A.to(dev), G.to(dev), cf.scale[0], **kw)
+    spec = ops.NoiseSpec(sigma=0.5, mode=nat.NOISE_PHILOX, seed=7, leaf_id=3)
+    noisy, _ = ops.clipped_sum(A.to(dev), G.to(dev), cf.scale[0], noise=spec, **kw)
+    assert torch.equal(noisy, ops.add_noise(center, 0.5, mode=nat.NOISE_PHILOX, seed=7, leaf_id=3))
+
+
 def test_clipped_sum_bf16_out_and_bias(dev):
     g = _gen(21)
     A = torch.randn(3, 128, 256, generator=g).to(torch.bfloat16)
