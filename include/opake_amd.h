@@ -267,6 +267,15 @@ int dpc_per_example_grads(const void* A, const void* G, int B, int T, int din, i
  * squared norms into per-example totals in a fixed order. */
 int dpc_row_sum_f64(const double* x, int B, int n, int accumulate, double* out, void* stream);
 
+/* Measurement helper with no counterpart in the reference (used by bench.py
+ * to put the roofline in context): `grid` workgroups of 8 waves run `iters`
+ * rounds of 8 independent 32x32x16 bf16 MFMAs on operands taken from
+ * `operands` (device, grid * 512 * 128 bytes of caller-chosen bf16 bits);
+ * out (device float32, grid * 512) keeps the results live.  Timing the
+ * launch gives the bf16 MFMA throughput the chip sustains on such data:
+ * 2 * 32 * 32 * 16 * 8 * iters FLOP per wave. */
+int dpc_calib_mfma_bf16(const void* operands, int grid, int iters, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,7 @@ _c_i64 = ctypes.c_int64
 # name -> (restype, argtypes)
 SIGNATURES = {
     "dpc_version": (_c_int, []),
+    "dpc_calib_mfma_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_void_p]),
     "dpc_last_error": (ctypes.c_char_p, []),
     "dpc_write_words": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_void_p]),
     "dpc_gram_workspace_bytes": (_c_size_t, [_c_int, _c_int]),
