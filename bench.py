@@ -45,6 +45,13 @@ per-expert ghost clipping of the 16 expert projections from their captured
 inputs and output gradients (grouped Gram norms, per-expert clip factors with
 C_e = C / sqrt(8), grouped clipped-sum GEMMs with per-group noise fused), the
 model's forward and backward excluded.
+
+``--path leaves`` (config 2, not the default line) runs the materialised-leaf
+path -- the reference's own streaming clip-and-sum as the fused-backend seam
+runs it -- over the config-2 layer's per-example gradients ([32, 4096, 4096]
+bf16, synthetic, resident in HBM) and times each pass on its own (norm pass,
+clip factors, scale-store-sum pass, device-stream noise pass) with its bytes
+and GB/s against the HBM peak.
 """
 
 from __future__ import annotations
@@ -818,11 +825,116 @@ def run_lora(args) -> dict:
     }
 
 
+def run_leaves(args) -> dict:
+    """The materialised-leaf path (the reference's own streaming clip-and-sum,
+    ``_streaming.py:39-185``, as ``dpc_leaves_*``) on the config-2 layer's
+    per-example gradients, each HBM pass timed on its own: the norm pass, the
+    clip factors, the scale-store-sum pass and the device-stream noise pass."""
+    import math
+
+    import torch
+
+    from opake_amd import _native as nat
+    from opake_amd import ops
+    from opake_amd.clipping import _numerics as num
+    from opake_amd.clipping._leaves import LeafBatch
+
+    nat.load()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    # Per-example gradients [B, dout, din] in bf16, each example scaled so
+    # that its norm is C * lognormal(0, 1): about half are clipped.
+    P = DOUT * DIN
+    z = torch.randn(B, 1, 1, generator=g, device=dev)
+    leaf = (torch.randn(B, DOUT, DIN, generator=g, device=dev) * (C / math.sqrt(P)) *
+            torch.exp(z)).to(torch.bfloat16)
+    batch = LeafBatch([leaf])
+    roundoff = num.norm_roundoff(torch.float32, torch.float64, 1, num.reduction_terms([P]))
+    guards = [num.guard_constants(torch.bfloat16, torch.float32, roundoff)]
+    stream = nat.stream_handle(dev)
+    sq = torch.empty(B, dtype=torch.float64, device=dev)
+    seed = 12345
+
+    def step(ev):
+        ev[0].record()
+        leaf_sq = batch.sqnorms()
+        ev[1].record()
+        nat.call("dpc_row_sum_f64", nat.ptr(leaf_sq), B, 1, 0, nat.ptr(sq), stream)
+        cf = ops.clip_factors(sq, num.conservative_bound(C), guards,
+                              count_threshold=num.float32_of(C))
+        ev[2].record()
+        (center,), _ = batch.apply({torch.bfloat16: cf.scale[0:1]})
+        ev[3].record()
+        out = ops.add_noise(center, NM * C, mode=nat.NOISE_PHILOX, seed=seed, leaf_id=0)
+        ev[4].record()
+        return out, cf
+
+    def events():
+        return [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+
+    for _ in range(args.warmup):
+        _, cf = step(events())
+    torch.cuda.synchronize()
+    clipped_frac = int(cf.nclipped.item()) / B
+    evs = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        evs.append(events())
+        step(evs[-1])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = [sum(e[i].elapsed_time(e[i + 1]) for e in evs) / len(evs) for i in range(4)]
+    nbytes = [B * P * 2 + B * (P // 2048) * 8,  # norm: read the leaves, fp64 tile partials
+              B * 8 + B * 8,                     # clip: tiny
+              B * P * 2 + P * 2,                 # apply: read the leaves, write the bf16 sum
+              P * 2 + P * 2]                     # noise: read and write the bf16 sum
+    names = ["norm pass (dpc_leaves_sqnorm)", "clip factors (dpc_row_sum_f64 + dpc_clip_factors)",
+             "scale-store-sum pass (dpc_leaves_apply)", "noise pass (dpc_add_noise, Philox)"]
+    passes = []
+    for name, t, nb in zip(names, ms, nbytes):
+        gbs = nb / (t * 1e-3) / 1e9
+        passes.append({"pass": name, "ms": t, "bytes": nb, "GB_per_s": gbs,
+                       "frac_of_hbm_peak": gbs / HBM_PEAK_GBS})
+    ms_per_step = 1e3 * elapsed / args.steps
+    dom = max(range(4), key=lambda i: ms[i])
+    return {
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "value": B * args.steps / elapsed,
+        "config": {
+            "workload": "materialised-leaf clip + sum + device-stream noise of the config-2 "
+                        "layer's per-example gradients [32, 4096, 4096] bf16 (the reference's "
+                        "streaming clip-and-sum, as the fused-backend seam runs it; the "
+                        "gradients are synthetic, resident in HBM)",
+            "global_batch": B,
+            "clipping_norm": C,
+            "noise_multiplier": NM,
+            "clipped_fraction": clipped_frac,
+            "passes": passes,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": names[dom],
+            "achieved": passes[dom]["GB_per_s"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": passes[dom]["frac_of_hbm_peak"],
+            "avg_launch_ms": ms[dom],
+            "traffic": None,
+        },
+        "cpu_baseline": None,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--config", type=int, choices=(1, 2, 3, 4, 5), default=2,
                     help="BASELINE configuration: 2 (default line), 1 (MLP), 3 (transformer "
                          "block), 4 (LoRA) or 5 (MoE)")
+    ap.add_argument("--path", choices=("ghost", "leaves"), default="ghost",
+                    help="config 2 only: the ghost-norm step (default line) or the materialised-"
+                         "leaf passes over the layer's per-example gradients, each pass timed")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=200,
@@ -855,8 +967,10 @@ def main() -> int:
         print(json.dumps({"copy_calibration_bytes": n * 4, "copies": 5}), flush=True)
         return 0
 
-    if args.config in (1, 3, 4, 5):
-        out = {1: run_mlp, 3: run_block, 4: run_lora, 5: run_moe}[args.config](args)
+    if args.config in (1, 3, 4, 5) or args.path == "leaves":
+        runner = run_leaves if args.path == "leaves" else \
+            {1: run_mlp, 3: run_block, 4: run_lora, 5: run_moe}[args.config]
+        out = runner(args)
         line = {"metric": METRIC, "value": out["value"], "unit": "examples/s", "n_gpus": 1,
                 "steps": out["steps"], "warmup": out["warmup"], "ms_per_step": out["ms_per_step"],
                 "higher_is_better": True, "scaling": "weak", "vs_baseline": None,

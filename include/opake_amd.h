@@ -173,9 +173,10 @@ int dpc_philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32
  *   leaf_scale_row[l] (device int32 [L]; NULL: every leaf uses row 0 -- the
  *   per-group clipping of _streaming.py:63-104 gives each group its row);
  *   out_sq (nullable, same layout and dtype as out) = sum_b to_dtype(stored^2),
- *   the second moment of _streaming.py:167-172; post_sq[b, t] (nullable) =
- *   sum over the tile of stored^2 (fp32).  out_dtype is the storage dtype or
- *   float32.
+ *   the second moment of _streaming.py:167-172; post_sq (nullable, float32
+ *   [B, 4 * n_tiles]): post_sq[b, 4 t + q] = sum of stored^2 over quarter q
+ *   (elements 512 q .. 512 q + 511) of tile t, so a row sums to ||stored_b||^2.
+ *   out_dtype is the storage dtype or float32.
  * -------------------------------------------------------------------------*/
 int dpc_leaves_sqnorm(const int64_t* ptrs, const int64_t* sizes, const int32_t* tile_leaf,
                       const int32_t* tile_local, const int64_t* tile_start,

@@ -233,7 +233,8 @@ class LeafBatch:
             out_dtype = (out_dtypes or {}).get(dtype, dtype)
             flat = torch.empty(g["total"], dtype=out_dtype, device=self.device)
             flat_sq = torch.empty_like(flat) if second_moment else None
-            tile_sq = (torch.empty((B, g["n_tiles"]), dtype=torch.float32, device=self.device)
+            # Four partials per tile (one per wave of the apply kernel).
+            tile_sq = (torch.empty((B, 4 * g["n_tiles"]), dtype=torch.float32, device=self.device)
                        if with_postsq else None)
             rows = scale_rows[dtype]
             leaf_row = None

@@ -10,13 +10,14 @@
 //               rounded up into the subnormal range zeroed; summed over the
 //               batch in fp32 in order b = 0..B-1; optionally the second
 //               moment, to_dtype(stored^2) summed the same way.
+#include <tuple>
+
 #include "common.h"
 
 namespace {
 
 constexpr int kTile = 2048;
 constexpr int kThreads = 256;
-constexpr int kPerThread = kTile / kThreads;  // 8
 
 template <bool kBf16>
 __device__ __forceinline__ float load_elem(int64_t base, int64_t idx) {
@@ -36,119 +37,280 @@ __device__ __forceinline__ double block_sum_f64(double v, double* red) {
   return total;
 }
 
-__device__ __forceinline__ float block_sum_f32(float v, float* red) {
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) red[w] = v;
-  __syncthreads();
-  float total = 0.f;
-  if (threadIdx.x == 0)
-    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) total += red[i];
-  return total;
+
+// Element e of example b of leaf `base` (n elements per example).
+template <bool kBf16>
+__device__ __forceinline__ float elem_f32(int64_t base, int64_t idx) {
+  return finite_or_zero(load_elem<kBf16>(base, idx));
 }
 
+// The 8 (bf16) or 4 (fp32) values of a 16-byte chunk, widened to fp32.
+// (Each word goes through a scalar: clang's __builtin_bit_cast of a vector
+// element lvalue, c[k], reads element 0 for every k.)
+template <bool kBf16>
+__device__ __forceinline__ void chunk_f32(u32x4_t c, float* v) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t w = c[k];
+    if constexpr (kBf16) {
+      v[2 * k] = __builtin_bit_cast(float, w << 16);
+      v[2 * k + 1] = __builtin_bit_cast(float, w & 0xffff0000u);
+    } else {
+      v[k] = __builtin_bit_cast(float, w);
+    }
+  }
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
+  return v;  // lane 0
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
+  return v;  // lane 0
+}
+
+// A tile can be read with 16-byte loads when it is whole and every row of
+// its leaf starts 16-byte aligned.
+__device__ __forceinline__ bool tile_vectorizable(int64_t base, int64_t n, int64_t off0,
+                                                  int elem_bytes) {
+  return (base & 15) == 0 && ((n * elem_bytes) & 15) == 0 && off0 + kTile <= n;
+}
+
+// Norm pass: one wave per (example b, tile t) unit, unit u = b * n_tiles + t
+// (consecutive waves read consecutive tiles of one example).  A whole,
+// aligned tile is read as 16-byte chunks, chunk j * 64 + lane for lane
+// `lane` (each load instruction of the wave covers 1 KiB contiguous); each
+// value is sanitised, squared in fp32 (rounded), widened and added in fp64,
+// and the wave's fp64 partials are folded by a fixed shuffle tree.  The
+// order of the fp64 additions inside a tile is fixed, so results are
+// deterministic.
 #pragma clang fp contract(off)
 template <bool kBf16>
 __global__ void __launch_bounds__(kThreads)
 tile_sq_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ sizes,
                const int32_t* __restrict__ tile_leaf, const int32_t* __restrict__ tile_local,
-               int n_tiles, double* __restrict__ partial) {
-  __shared__ double red[kThreads / 64];
-  const int t = blockIdx.x, b = blockIdx.y;
+               int n_tiles, long long units, double* __restrict__ partial) {
+  constexpr int kElemBytes = kBf16 ? 2 : 4;
+  constexpr int kPerChunk = 16 / kElemBytes;
+  constexpr int kChunks = kTile / kPerChunk / 64;  // per lane: 4 (bf16) or 8 (fp32)
+  const long long u = (long long)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (u >= units) return;  // whole waves exit; the kernel has no barrier
+  const int lane = threadIdx.x & 63;
+  const int b = (int)(u / n_tiles), t = (int)(u % n_tiles);
   const int leaf = tile_leaf[t];
   const int64_t n = sizes[leaf];
   const int64_t base = ptrs[leaf];
   const int64_t off0 = (int64_t)tile_local[t] * kTile;
   double s = 0.0;
+  if (tile_vectorizable(base, n, off0, kElemBytes)) {
+    const u32x4_t* row =
+        reinterpret_cast<const u32x4_t*>(base + ((int64_t)b * n + off0) * kElemBytes);
+    u32x4_t c[kChunks];
 #pragma unroll
-  for (int j = 0; j < kPerThread; ++j) {
-    const int64_t off = off0 + threadIdx.x + (int64_t)j * kThreads;
-    if (off < n) {
-      float x = finite_or_zero(load_elem<kBf16>(base, (int64_t)b * n + off));
-      float sq = x * x;
-      s += (double)sq;
+    for (int j = 0; j < kChunks; ++j) c[j] = __builtin_nontemporal_load(row + j * 64 + lane);
+#pragma unroll
+    for (int j = 0; j < kChunks; ++j) {
+      float v[kPerChunk];
+      chunk_f32<kBf16>(c[j], v);
+#pragma unroll
+      for (int k = 0; k < kPerChunk; ++k) {
+        const float x = finite_or_zero(v[k]);
+        const float sq = x * x;
+        s += (double)sq;
+      }
+    }
+  } else {
+    for (int e = lane; e < kTile; e += 64) {
+      const int64_t off = off0 + e;
+      if (off < n) {
+        const float x = elem_f32<kBf16>(base, (int64_t)b * n + off);
+        const float sq = x * x;
+        s += (double)sq;
+      }
     }
   }
-  double total = block_sum_f64(s, red);
-  if (threadIdx.x == 0) partial[(size_t)b * n_tiles + t] = total;
+  s = wave_sum_f64(s);
+  if (lane == 0) partial[(size_t)b * n_tiles + t] = s;
 }
 #pragma clang fp contract(on)
 
-// leaf_sq[b, leaf_col[l]] = sum of leaf l's tile partials (fixed order).
-__global__ void __launch_bounds__(kThreads)
+// leaf_sq[b, leaf_col[l]] = sum of leaf l's tile partials.  1024 threads;
+// thread i keeps eight running sums, of the tiles t0 + i + 8192 j + 1024 r
+// (r = 0..7), so eight loads are in flight (one round trip covers a leaf of
+// up to 8192 tiles, 16.8M elements); the sums are then folded in a fixed
+// order (pairwise over r, then the block tree): deterministic.
+constexpr int kLeafSumThreads = 1024;
+
+__global__ void __launch_bounds__(kLeafSumThreads)
 leaf_sum_kernel(const double* __restrict__ partial, const int64_t* __restrict__ tile_start,
                 const int32_t* __restrict__ leaf_col, int n_tiles, double* __restrict__ leaf_sq,
                 int stride) {
-  __shared__ double red[kThreads / 64];
+  __shared__ double red[kLeafSumThreads / 64];
   const int l = blockIdx.x, b = blockIdx.y;
   const int64_t t0 = tile_start[l], t1 = tile_start[l + 1];
-  double s = 0.0;
-  for (int64_t t = t0 + threadIdx.x; t < t1; t += blockDim.x) s += partial[(size_t)b * n_tiles + t];
-  double total = block_sum_f64(s, red);
+  const double* row = partial + (size_t)b * n_tiles;
+  double s[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) s[r] = 0.0;
+  for (int64_t t = t0 + threadIdx.x; t < t1; t += 8 * kLeafSumThreads) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int64_t tt = t + r * kLeafSumThreads;
+      if (tt < t1) s[r] += row[tt];
+    }
+  }
+  const double v = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+  double total = block_sum_f64(v, red);
   if (threadIdx.x == 0) leaf_sq[(size_t)b * stride + leaf_col[l]] = total;
 }
 
+// stored = to_dtype(x * s), bf16 results that rounded up into the subnormal
+// range zeroed (bf16 shares float32's exponent range).
+template <bool kBf16>
+__device__ __forceinline__ float store_round(float x, float s) {
+  const float prod = x * s;
+  if (!kBf16) return prod;
+  const float stored = round_to_bf16(prod);
+  const float sa = fabsf(stored);
+  return (sa <= 1.17549435e-38f && sa > fabsf(prod)) ? 0.f : stored;
+}
+
+// Apply pass: one workgroup per tile; thread i owns the 8 consecutive
+// elements 8 i .. 8 i + 7 of the tile and walks the batch in order b = 0 ..
+// B - 1, loading kApplyUnroll examples ahead (one 16-byte chunk per example for
+// bf16, two for fp32), so each element's fp32 sum runs in example order.
+// With post_sq, each wave's sum of stored^2 over its 512 elements of example
+// b goes to post_sq[b, 4 t + wave] (a fixed shuffle tree over the thread
+// sums, each in element order).
+constexpr int kApplyUnroll = 4;
+
 #pragma clang fp contract(off)
-template <bool kBf16, bool kOutBf16>
+template <bool kBf16, bool kOutBf16, bool kSecond, bool kPostSq>
 __global__ void __launch_bounds__(kThreads)
 apply_sum_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ sizes,
                  const int32_t* __restrict__ tile_leaf, const int32_t* __restrict__ tile_local,
                  const int64_t* __restrict__ out_offs, int n_tiles, int B,
                  const float* __restrict__ scale, const int32_t* __restrict__ leaf_scale_row,
                  void* __restrict__ out, void* __restrict__ out_sq, float* __restrict__ post_sq) {
-  __shared__ float red[kThreads / 64];
+  constexpr int kElemBytes = kBf16 ? 2 : 4;
+  constexpr int kLoads = kBf16 ? 1 : 2;  // 16-byte chunks per thread per example
   const int t = blockIdx.x;
   const int leaf = tile_leaf[t];
   const int64_t n = sizes[leaf];
   const int64_t base = ptrs[leaf];
   const int64_t off0 = (int64_t)tile_local[t] * kTile;
-  const float smallest_normal = 1.17549435e-38f;  // bf16 shares float32's exponent range
-  float acc[kPerThread], acc2[kPerThread];
+  const int e0 = 8 * threadIdx.x;  // first element of this thread in the tile
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float acc[8], acc2[8];
 #pragma unroll
-  for (int j = 0; j < kPerThread; ++j) acc[j] = acc2[j] = 0.f;
+  for (int k = 0; k < 8; ++k) acc[k] = acc2[k] = 0.f;
   const float* srow = scale + (size_t)(leaf_scale_row ? leaf_scale_row[leaf] : 0) * B;
-  for (int b = 0; b < B; ++b) {
-    const float s = srow[b];
+  auto add_example = [&](int b, const float* x) __attribute__((always_inline)) {
+    const float sc = srow[b];
     float sq = 0.f;
 #pragma unroll
-    for (int j = 0; j < kPerThread; ++j) {
-      const int64_t off = off0 + threadIdx.x + (int64_t)j * kThreads;
-      if (off < n) {
-        float x = finite_or_zero(load_elem<kBf16>(base, (int64_t)b * n + off));
-        float prod = x * s;
-        float stored = prod;
+    for (int k = 0; k < 8; ++k) {
+      const float stored = store_round<kBf16>(finite_or_zero(x[k]), sc);
+      acc[k] = acc[k] + stored;
+      if (kSecond) {
+        float s2 = stored * stored;
+        if (kBf16) s2 = round_to_bf16(s2);
+        acc2[k] = acc2[k] + s2;
+      }
+      if (kPostSq) sq = sq + stored * stored;
+    }
+    if (kPostSq) {
+      sq = wave_sum_f32(sq);
+      if (lane == 0) post_sq[(size_t)b * (4 * n_tiles) + 4 * t + w] = sq;
+    }
+  };
+  if (tile_vectorizable(base, n, off0, kElemBytes)) {
+    const int64_t stride = n * kElemBytes;  // bytes between examples
+    const char* p = reinterpret_cast<const char*>(base) + (off0 + e0) * kElemBytes;
+    int b = 0;
+    for (; b + kApplyUnroll <= B; b += kApplyUnroll) {
+      u32x4_t c[kApplyUnroll][kLoads];
+#pragma unroll
+      for (int r = 0; r < kApplyUnroll; ++r)
+#pragma unroll
+        for (int h = 0; h < kLoads; ++h)
+          c[r][h] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4_t*>(p + (int64_t)(b + r) * stride) + h);
+#pragma unroll
+      for (int r = 0; r < kApplyUnroll; ++r) {
+        float x[8];
         if (kBf16) {
-          stored = round_to_bf16(prod);
-          float sa = fabsf(stored);
-          if (sa <= smallest_normal && sa > fabsf(prod)) stored = 0.f;
+          chunk_f32<true>(c[r][0], x);
+        } else {
+          chunk_f32<false>(c[r][0], x);
+          chunk_f32<false>(c[r][1], x + 4);
         }
-        acc[j] = acc[j] + stored;
-        if (out_sq) {
-          // Second moment: the stored value squared in its dtype, then summed.
-          float s2 = stored * stored;
-          if (kBf16) s2 = round_to_bf16(s2);
-          acc2[j] = acc2[j] + s2;
-        }
-        if (post_sq) sq = sq + stored * stored;
+        add_example(b + r, x);
       }
     }
-    if (post_sq) {
-      float total = block_sum_f32(sq, red);
-      if (threadIdx.x == 0) post_sq[(size_t)b * n_tiles + t] = total;
+    for (; b < B; ++b) {
+      float x[8];
+      const u32x4_t* q = reinterpret_cast<const u32x4_t*>(p + (int64_t)b * stride);
+      if (kBf16) {
+        chunk_f32<true>(q[0], x);
+      } else {
+        chunk_f32<false>(q[0], x);
+        chunk_f32<false>(q[1], x + 4);
+      }
+      add_example(b, x);
+    }
+  } else {
+    for (int b = 0; b < B; ++b) {
+      float x[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int64_t off = off0 + e0 + k;
+        x[k] = off < n ? load_elem<kBf16>(base, (int64_t)b * n + off) : 0.f;
+      }
+      add_example(b, x);
     }
   }
   const int64_t obase = out_offs[leaf];
+  constexpr int kOutBytes = kOutBf16 ? 2 : 4;
+  const int64_t o = obase + off0 + e0;
+  if (off0 + e0 + 8 <= n && ((o * kOutBytes) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
+      (!kSecond || (reinterpret_cast<uintptr_t>(out_sq) & 15) == 0)) {
+    if (kOutBf16) {
+      u32x4_t v, v2;
 #pragma unroll
-  for (int j = 0; j < kPerThread; ++j) {
-    const int64_t off = off0 + threadIdx.x + (int64_t)j * kThreads;
+      for (int k = 0; k < 4; ++k) {
+        v[k] = (uint32_t)f32_to_bf16_bits(acc[2 * k]) |
+               ((uint32_t)f32_to_bf16_bits(acc[2 * k + 1]) << 16);
+        v2[k] = (uint32_t)f32_to_bf16_bits(acc2[2 * k]) |
+                ((uint32_t)f32_to_bf16_bits(acc2[2 * k + 1]) << 16);
+      }
+      *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(out) + o) = v;
+      if (kSecond) *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(out_sq) + o) = v2;
+    } else {
+      float4* q = reinterpret_cast<float4*>(reinterpret_cast<float*>(out) + o);
+      q[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      q[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+      if (kSecond) {
+        float4* q2 = reinterpret_cast<float4*>(reinterpret_cast<float*>(out_sq) + o);
+        q2[0] = make_float4(acc2[0], acc2[1], acc2[2], acc2[3]);
+        q2[1] = make_float4(acc2[4], acc2[5], acc2[6], acc2[7]);
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int64_t off = off0 + e0 + k;
     if (off < n) {
       if (kOutBf16) {
-        reinterpret_cast<uint16_t*>(out)[obase + off] = f32_to_bf16_bits(acc[j]);
-        if (out_sq) reinterpret_cast<uint16_t*>(out_sq)[obase + off] = f32_to_bf16_bits(acc2[j]);
+        reinterpret_cast<uint16_t*>(out)[obase + off] = f32_to_bf16_bits(acc[k]);
+        if (kSecond) reinterpret_cast<uint16_t*>(out_sq)[obase + off] = f32_to_bf16_bits(acc2[k]);
       } else {
-        reinterpret_cast<float*>(out)[obase + off] = acc[j];
-        if (out_sq) reinterpret_cast<float*>(out_sq)[obase + off] = acc2[j];
+        reinterpret_cast<float*>(out)[obase + off] = acc[k];
+        if (kSecond) reinterpret_cast<float*>(out_sq)[obase + off] = acc2[k];
       }
     }
   }
@@ -168,6 +330,19 @@ group_sum_kernel(const double* __restrict__ x, int B, int n, int stride,
     if (col_group[j] == g) s += x[(size_t)b * stride + j];
   }
   out[(size_t)g * B + b] = s;
+}
+
+template <bool kBf16, bool kOutBf16, typename... Args>
+void launch_apply(hipStream_t s, bool second, bool postsq, Args... args) {
+  const dim3 grid((unsigned)std::get<5>(std::make_tuple(args...))), block(kThreads);
+  if (second && postsq)
+    hipLaunchKernelGGL((apply_sum_kernel<kBf16, kOutBf16, true, true>), grid, block, 0, s, args...);
+  else if (second)
+    hipLaunchKernelGGL((apply_sum_kernel<kBf16, kOutBf16, true, false>), grid, block, 0, s, args...);
+  else if (postsq)
+    hipLaunchKernelGGL((apply_sum_kernel<kBf16, kOutBf16, false, true>), grid, block, 0, s, args...);
+  else
+    hipLaunchKernelGGL((apply_sum_kernel<kBf16, kOutBf16, false, false>), grid, block, 0, s, args...);
 }
 
 }  // namespace
@@ -199,16 +374,19 @@ extern "C" int dpc_leaves_sqnorm(const int64_t* ptrs, const int64_t* sizes,
   if (B > 65535) return DPC_ENOTSUP;
   hipStream_t s = (hipStream_t)stream;
   if (n_tiles > 0) {
+    const long long units = (long long)n_tiles * B;
+    const long long blocks = (units + kThreads / 64 - 1) / (kThreads / 64);
+    if (blocks > 0x7fffffffLL) return DPC_ENOTSUP;
     if (dtype == DPC_BF16) {
-      hipLaunchKernelGGL(tile_sq_kernel<true>, dim3(n_tiles, B), dim3(kThreads), 0, s, ptrs,
-                         sizes, tile_leaf, tile_local, n_tiles, partial);
+      hipLaunchKernelGGL(tile_sq_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), 0, s,
+                         ptrs, sizes, tile_leaf, tile_local, n_tiles, units, partial);
     } else {
-      hipLaunchKernelGGL(tile_sq_kernel<false>, dim3(n_tiles, B), dim3(kThreads), 0, s, ptrs,
-                         sizes, tile_leaf, tile_local, n_tiles, partial);
+      hipLaunchKernelGGL(tile_sq_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, s,
+                         ptrs, sizes, tile_leaf, tile_local, n_tiles, units, partial);
     }
     DPC_HIP_CHECK(hipGetLastError());
   }
-  hipLaunchKernelGGL(leaf_sum_kernel, dim3(n_leaves, B), dim3(kThreads), 0, s,
+  hipLaunchKernelGGL(leaf_sum_kernel, dim3(n_leaves, B), dim3(kLeafSumThreads), 0, s,
                      (const double*)partial, tile_start, leaf_col, n_tiles, leaf_sq,
                      leaf_sq_stride);
   DPC_HIP_CHECK(hipGetLastError());
@@ -228,17 +406,17 @@ extern "C" int dpc_leaves_apply(const int64_t* ptrs, const int64_t* sizes,
     return DPC_EINVAL;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == DPC_BF16 && out_dtype == DPC_BF16) {
-    hipLaunchKernelGGL((apply_sum_kernel<true, true>), dim3(n_tiles), dim3(kThreads), 0, s, ptrs,
-                       sizes, tile_leaf, tile_local, out_offs, n_tiles, B, scale, leaf_scale_row, out, out_sq,
-                       post_sq);
+    launch_apply<true, true>(s, out_sq != nullptr, post_sq != nullptr, ptrs, sizes, tile_leaf,
+                             tile_local, out_offs, n_tiles, B, scale, leaf_scale_row, out, out_sq,
+                             post_sq);
   } else if (dtype == DPC_BF16) {
-    hipLaunchKernelGGL((apply_sum_kernel<true, false>), dim3(n_tiles), dim3(kThreads), 0, s,
-                       ptrs, sizes, tile_leaf, tile_local, out_offs, n_tiles, B, scale,
-                       leaf_scale_row, out, out_sq, post_sq);
+    launch_apply<true, false>(s, out_sq != nullptr, post_sq != nullptr, ptrs, sizes, tile_leaf,
+                              tile_local, out_offs, n_tiles, B, scale, leaf_scale_row, out, out_sq,
+                              post_sq);
   } else {
-    hipLaunchKernelGGL((apply_sum_kernel<false, false>), dim3(n_tiles), dim3(kThreads), 0, s,
-                       ptrs, sizes, tile_leaf, tile_local, out_offs, n_tiles, B, scale,
-                       leaf_scale_row, out, out_sq, post_sq);
+    launch_apply<false, false>(s, out_sq != nullptr, post_sq != nullptr, ptrs, sizes, tile_leaf,
+                               tile_local, out_offs, n_tiles, B, scale, leaf_scale_row, out,
+                               out_sq, post_sq);
   }
   DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;

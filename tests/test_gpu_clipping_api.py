@@ -82,6 +82,41 @@ def test_leaf_backend_matches_streaming_oracle(dev, dtypes, kind):
                                res.clipped_norms.double(), rtol=1e-5, atol=1e-7)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("second_moment", [False, True])
+def test_leaf_kernels_whole_ragged_and_unaligned_tiles(dev, dtype, second_moment):
+    """Leaves that exercise every path of the leaf kernels: whole 2048-element
+    tiles read with 16-byte loads, a ragged last tile, rows that do not start
+    16-byte aligned (n * elem_size % 16 != 0), output offsets that are not
+    16-byte aligned, and a batch that is not a multiple of the apply kernel's
+    4-example unroll."""
+    gen = torch.Generator().manual_seed(11 + second_moment)
+    B = 19
+    shapes = [(4096,), (2049,), (8, 1031), (3,), (16392,), (2, 2048)]
+    tree = {}
+    for i, shape in enumerate(shapes):
+        scale = torch.exp(torch.randn(B, *([1] * len(shape)), generator=gen))
+        tree[f"p{i}"] = (torch.randn(B, *shape, generator=gen) * scale * 0.02).to(dtype)
+    tree["p4"][7, 5000] = math.nan
+    tree["p0"][18, 3] = -math.inf
+    names = sorted(tree)
+    C = clip_oracle.conservative_bound(1.0)
+    res = clip_oracle.stream_clip_and_sum([tree[n] for n in names], C, return_aux=True,
+                                          second_moment=second_moment)
+    dev_tree = {k: v.to(dev) for k, v in tree.items()}
+    reduced, _, sq, _, diag = cl.fused_stream_clip_and_sum(
+        dev_tree, torch.tensor(C, device=dev), scale=_Scale("fixed"), batch_size=B,
+        reduce_leaf=_reduce, compute_dtype=None, second_moment=second_moment, return_aux=True,
+        return_stats=False)
+    for i, n in enumerate(names):
+        torch.testing.assert_close(reduced[n].cpu(), res.reduced[i])
+        if second_moment:
+            torch.testing.assert_close(sq[n].cpu(), res.squared[i])
+    torch.testing.assert_close(diag["norms"].cpu().double(), res.norms, rtol=1e-6, atol=0)
+    torch.testing.assert_close(diag["clipped_norms"].cpu().double(),
+                               res.clipped_norms.double(), rtol=1e-5, atol=1e-7)
+
+
 def test_leaf_backend_boundary_pin(dev):
     # [[3,4],[0.6,0.8]], C = 1 -> [1.2, 1.6] (test_clip_sum.py:156-161).
     batch = {"w": torch.tensor([[3.0, 4.0], [0.6, 0.8]], device=dev)}
