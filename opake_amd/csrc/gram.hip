@@ -20,7 +20,8 @@
 // are read, the barrier sits before a step's last group (which overlaps the
 // next step's first reads), and the loop body has no branch around the
 // accumulators (operands ordered so that din <= dout: the loop is the
-// "both Gram matrices" body for A's K range, then a "G G^T only" body).
+// "both Gram matrices" body for A's K range, then a "G G^T only" body that
+// stages G's tiles alone).
 #include "common.h"
 
 namespace {
@@ -271,30 +272,38 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
   // Registers hold the next K step of the four operands (the q operands are
   // not loaded on diagonal pairs).  Past an operand's K range the loads read
   // zeros, so every path issues the same loads.
-  u32x4_t rap[2], raq[2], rgp[2], rgq[2];
-  auto load_a = [&](int step) {
-    load_operand(ap, step, rap);
-    if (!diag) load_operand(aq, step, raq);
+  // Two register sets alternate by step parity: step s stores set
+  // (s + 1) & 1, which holds step s + 1, into the other stage and reloads it
+  // with step s + 3, so every load has two steps to land.
+  struct Regs {
+    u32x4_t ap[2], aq[2], gp[2], gq[2];
   };
-  auto load_g = [&](int step) {
-    load_operand(gp, step, rgp);
-    if (!diag) load_operand(gq, step, rgq);
+  Regs R[2];
+  auto load_a = [&](int step, Regs& r) __attribute__((always_inline)) {
+    load_operand(ap, step, r.ap);
+    if (!diag) load_operand(aq, step, r.aq);
   };
-  auto store_a = [&](uint8_t* stage) {
-    store_operand(stage, rap);
-    if (!diag) store_operand(stage + kGTileBytes, raq);
+  auto load_g = [&](int step, Regs& r) __attribute__((always_inline)) {
+    load_operand(gp, step, r.gp);
+    if (!diag) load_operand(gq, step, r.gq);
   };
-  auto store_g = [&](uint8_t* stage) {
-    store_operand(stage + 2 * kGTileBytes, rgp);
-    if (!diag) store_operand(stage + 3 * kGTileBytes, rgq);
+  auto store_a = [&](uint8_t* stage, const Regs& r) __attribute__((always_inline)) {
+    store_operand(stage, r.ap);
+    if (!diag) store_operand(stage + kGTileBytes, r.aq);
+  };
+  auto store_g = [&](uint8_t* stage, const Regs& r) __attribute__((always_inline)) {
+    store_operand(stage + 2 * kGTileBytes, r.gp);
+    if (!diag) store_operand(stage + 3 * kGTileBytes, r.gq);
   };
 
-  load_a(0);
-  load_g(0);
-  store_a(lds);
-  store_g(lds);
-  load_a(1);
-  load_g(1);
+  load_a(0, R[0]);
+  load_g(0, R[0]);
+  store_a(lds, R[0]);
+  store_g(lds, R[0]);
+  load_a(1, R[1]);
+  load_g(1, R[1]);
+  load_a(2, R[0]);
+  load_g(2, R[0]);
   __syncthreads();
   // A K step is four groups of MFMAs on the current stage -- A sub-steps 0
   // and 1, then G sub-steps 0 and 1 -- and each group's fragments are read
@@ -322,7 +331,7 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
   }
   // Steps inside A's K range (nka <= nkg): on entry fx holds (in flight) A's
   // sub-step 0 fragments of the current stage.
-  auto step_ag = [&](int s) __attribute__((always_inline)) {
+  auto step_ag = [&](int s, Regs& rn) __attribute__((always_inline)) {
     const uint8_t* cur = lds + (s & 1) * kGStageBytes;
     uint8_t* nxt = lds + ((s + 1) & 1) * kGStageBytes;
     const uint8_t *cap, *caq, *cgp, *cgq, *nap, *naq, *ngp, *ngq;
@@ -330,15 +339,15 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
     stage_ptrs(nxt, &nap, &naq, &ngp, &ngq);
     gram_read(cap, caq, 1, fy);
     gram_mma(fx, pa);
-    store_a(nxt);
-    load_a(s + 2);
+    store_a(nxt, rn);
+    load_a(s + 3, rn);
     __builtin_amdgcn_sched_barrier(0);
     gram_read(cgp, cgq, 0, fx);
     gram_mma(fy, pa);
     gram_read(cgp, cgq, 1, fy);
     gram_mma(fx, pg);
-    store_g(nxt);
-    load_g(s + 2);
+    store_g(nxt, rn);
+    load_g(s + 3, rn);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     // The next step's first fragments: A's sub-step 0, or G's past A's range.
@@ -347,9 +356,9 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
     gram_mma(fy, pg);
     __builtin_amdgcn_sched_barrier(0);
   };
-  // Steps past A's K range: on entry fx holds G's sub-step 0 fragments.  (A's
-  // loads, past its range, read zeros: every step issues the same loads.)
-  auto step_g = [&](int s) __attribute__((always_inline)) {
+  // Steps past A's K range: on entry fx holds G's sub-step 0 fragments.  A's
+  // tiles are neither loaded nor staged any more (only G's are read).
+  auto step_g = [&](int s, Regs& rn) __attribute__((always_inline)) {
     const uint8_t* cur = lds + (s & 1) * kGStageBytes;
     uint8_t* nxt = lds + ((s + 1) & 1) * kGStageBytes;
     const uint8_t *cap, *caq, *cgp, *cgq, *nap, *naq, *ngp, *ngq;
@@ -357,20 +366,35 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
     stage_ptrs(nxt, &nap, &naq, &ngp, &ngq);
     gram_read(cgp, cgq, 1, fy);
     gram_mma(fx, pg);
-    store_a(nxt);
-    load_a(s + 2);
     __builtin_amdgcn_sched_barrier(0);
-    store_g(nxt);
-    load_g(s + 2);
+    store_g(nxt, rn);
+    load_g(s + 3, rn);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     gram_read(ngp, ngq, 0, fx);
     gram_mma(fy, pg);
     __builtin_amdgcn_sched_barrier(0);
   };
+  // Step s uses register set (s + 1) & 1; the loops are unrolled by two so
+  // that the set is a compile-time choice.
   int s = 0;
-  for (; s < nka; ++s) step_ag(s);
-  for (; s < nkg; ++s) step_g(s);
+  for (; s + 1 < nka; s += 2) {
+    step_ag(s, R[1]);
+    step_ag(s + 1, R[0]);
+  }
+  if (s < nka) {
+    step_ag(s, R[1]);
+    ++s;
+    if (s < nkg) {
+      step_g(s, R[0]);
+      ++s;
+    }
+  }
+  for (; s + 1 < nkg; s += 2) {
+    step_g(s, R[1]);
+    step_g(s + 1, R[0]);
+  }
+  if (s < nkg) step_g(s, R[1]);
 
   // Both tiles share the MFMA output layout, so the element-wise product
   // needs no knowledge of which (s, t) a register holds.
