@@ -812,7 +812,7 @@ def run_lora(args) -> dict:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "narrow_partial_bf16_kernel + narrow_finish_kernel (dpc_per_example_grads, 14 "
+            "kernel": "narrow_wide_bf16_kernel (+ narrow_finish_kernel for split tokens; dpc_per_example_grads, 14 "
                       "launches per step)",
             "achieved": gbs,
             "peak": HBM_PEAK_GBS,

@@ -31,13 +31,16 @@ def _rel(got, want):
 # Widths % 4 != 0 take the general kernels; the others (bf16) the pipelined
 # 8-wave kernel: split chunks (2, 2048, 4096, 16), (3, 1000, 16, 1024), an odd
 # token count past one LDS chunk with a tail column block (1, 4097, 8, 520),
-# one chunk written directly (8, 64, 14336, 16) and 17..32 narrow columns
-# (1, 300, 1200, 17).
+# one chunk written directly (8, 64, 14336, 16), 17..32 narrow columns with
+# the narrow side the output (1, 300, 1200, 17), (3, 96, 4096, 32) or the
+# input (2, 512, 24, 2048), and a partial column block (2, 1056, 520, 8).
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("B,T,din,dout", [(3, 77, 513, 16), (2, 64, 16, 1030), (4, 5, 32, 33),
                                           (2, 130, 1, 700), (1, 300, 1200, 17),
                                           (2, 2048, 4096, 16), (3, 1000, 16, 1024),
-                                          (1, 4097, 8, 520), (8, 64, 14336, 16)])
+                                          (1, 4097, 8, 520), (8, 64, 14336, 16),
+                                          (2, 512, 24, 2048), (3, 96, 4096, 32),
+                                          (2, 1056, 520, 8)])
 def test_per_example_grads_match_oracle(dev, dtype, B, T, din, dout):
     g = torch.Generator().manual_seed(B * 1000 + din + dout)
     A = torch.randn(B, T, din, generator=g).to(dtype)
