@@ -95,8 +95,10 @@ int dpc_flat_sqnorms(const void* a, const void* g, int B, int din, int dout, int
  * guard_rel / guard_abs are HOST arrays of n_guards (1..4) values, one
  * pair per storage dtype.  sqnorm and all outputs are device pointers.
  * Any output pointer may be NULL.  `plan` (nullable, device memory of
- * dpc_clip_plan_bytes(B) bytes) receives the ordered list of examples whose
- * guard-0 scale is positive; the clipped-sum GEMM walks only those.
+ * dpc_clip_plan_bytes(B) bytes) receives the examples whose guard-0 scale is
+ * positive, those the bf16 GEMM may apply to its accumulators first (scale
+ * >= 2^-64 and B * C <= 2^55), then the others, each list in increasing
+ * order; the clipped-sum GEMM walks only these.
  * -------------------------------------------------------------------------*/
 size_t dpc_clip_plan_bytes(int B);
 int dpc_clip_factors(const double* sqnorm, int B, double C, int kind, double gamma,
@@ -119,8 +121,11 @@ int dpc_clip_factors(const double* sqnorm, int B, double C, int kind, double gam
  * host-drawn tensor) or from the Philox stream (mode PHILOX) keyed by
  * (seed, leaf_id).  `plan` is the dpc_clip_factors plan built from the same
  * `scale` (nullable: the generic kernel then scans every example).  On the
- * bf16 MFMA path (T % 64 == 0, din and dout multiples of 8) each G element
- * is scaled in fp32 and rounded to bf16 once before the product.  With
+ * bf16 MFMA path (T % 64 == 0, din and dout multiples of 8) the products of
+ * the given bf16 values are summed in fp32 and each example's scale is
+ * applied to the fp32 accumulators (the plan's first list); examples of the
+ * plan's second list have each G element scaled in fp32 and rounded to bf16
+ * once before the product.  With
  * with_bias, bias_out[m] = same recipe over
  * sum_i scale[i] * sum_t G[i, t, m], its noise keyed by (seed, bias_leaf_id)
  * under the [dout, 1] view.  ws (dpc_clipped_sum_workspace_bytes) holds the

@@ -7,24 +7,27 @@
 //   * 256 x 256 output tile per workgroup, 8 waves (2 per SIMD) of 128 x 64,
 //     bf16 MFMA 32x32x16 with fp32 accumulators (8 blocks per wave);
 //   * both operands are m- (n-) contiguous in HBM and are staged into LDS in
-//     that natural [k][m] layout (64-byte blocks XOR-swizzled by the k row):
-//     A straight from HBM (buffer_load ... lds), G through registers, where
-//     it is scaled.  The MFMA fragments, which need 8 consecutive k per lane,
-//     come out of LDS through the gfx950 transposing read ds_read_b64_tr_b16
-//     (two per fragment), so no data is transposed in registers; all LDS
-//     accesses are free of bank conflicts;
+//     that natural [k][m] layout (64-byte blocks XOR-swizzled by the k row),
+//     straight from HBM (buffer_load ... lds).  The MFMA fragments, which
+//     need 8 consecutive k per lane, come out of LDS through the gfx950
+//     transposing read ds_read_b64_tr_b16 (two per fragment), so no data is
+//     transposed in registers; all LDS accesses are free of bank conflicts;
 //   * a K step is 64 deep and never straddles two examples, so the
-//     per-example scale is one scalar per step: the G chunks are multiplied
-//     by it in fp32 between the global load and the LDS store and rounded to
-//     bf16 once (v_cvt_pk_bf16_f32, round-to-nearest-even) -- the same single
-//     rounding of a scaled value that the reference applies when it stores a
-//     scaled bf16 per-example gradient.  The accumulators never leave the
-//     AGPRs.  Examples with scale 0 are skipped through the clip plan, so
-//     their data (including any NaN/Inf) is never read;
-//   * two LDS stages (128 KiB), one barrier per K step; the scale + store of
-//     step s + 1 is interleaved, chunk by chunk, with the MFMAs of step s, and
-//     each chunk's registers are refilled with step s + 2 right after its
-//     store, so every global load is in flight for a whole step;
+//     per-example scale is one scalar per step.  Dense mode applies it to the
+//     fp32 accumulators: they hold the partial sum divided by the current
+//     example's scale and are multiplied by scale_prev / scale_next where the
+//     example changes (the clip plan lists first the examples for which this
+//     stays far inside fp32, see plan.h; the others are summed after the
+//     loop with G scaled in fp32 and rounded to bf16 once before the
+//     product).  Grouped mode stages G through registers, multiplied by its
+//     segment's scale in fp32 and rounded to bf16 once (v_cvt_pk_bf16_f32,
+//     round-to-nearest-even).  Examples with scale 0 are skipped through the
+//     clip plan, so their data (including any NaN/Inf) is never read;
+//   * two LDS stages (128 KiB), one barrier per K step; the DMAs of step
+//     s + 1 are issued at the start of step s (grouped mode: the scale +
+//     store of G's step s + 1 is interleaved, chunk by chunk, with the MFMAs
+//     of step s, and each chunk's registers are refilled with step s + 2
+//     right after its store);
 //   * workgroup ids are remapped so that each of the 8 XCDs owns a compact
 //     block of output tiles and re-reads operand tiles from its own L2.
 #include "common.h"
@@ -243,17 +246,15 @@ __device__ __forceinline__ int frag_off(int c0, int h, int lane) {
   return tile_off(k, c0 + 16 * (q & 1) + 4 * (L & 3));
 }
 
-// LDS of the fast kernel: the G tiles of both stages (and, after the K loop,
-// a quarter of the output tile) in one array, each stage's A tile in an array
-// of its own.  A is filled by DMA (buffer_load ... lds); keeping its stages in
-// distinct objects lets the compiler see that a DMA into one stage does not
-// alias the reads of the other, so it inserts no memory-counter wait before
-// them.
-constexpr int kQuarterRows = 64;
+// LDS of the fast kernel: each stage's G tile and A tile in an array of its
+// own (the first G array, after the K loop, also holds a 32-row slice of the
+// output tile).  Operands filled by DMA (buffer_load ... lds) sit in distinct
+// objects so that the compiler sees that a DMA into one stage does not alias
+// the reads of the other, and inserts no memory-counter wait before them.
+constexpr int kEpiPassRows = 32;
 constexpr int kEpiLd = kBN + 4;
-constexpr int kGLdsBytes = (2 * kOperandBytes > kQuarterRows * kEpiLd * 4)
-                               ? 2 * kOperandBytes
-                               : kQuarterRows * kEpiLd * 4;
+constexpr int kG0Bytes = (kOperandBytes > kEpiPassRows * kEpiLd * 4) ? kOperandBytes
+                                                                      : kEpiPassRows * kEpiLd * 4;
 
 // vmcnt(N) with the other counters left alone (gfx9 s_waitcnt encoding).
 #define DPC_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
@@ -273,7 +274,8 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
   constexpr int kGC = kBK / kRowsPerPass;   // G chunks per thread per K step
   constexpr int kGCSub = kGC / 4;           // ... stored per 16-deep sub-step
   constexpr int kDma = 32 / kWaves;         // 1 KiB A transfers per wave per K step
-  __shared__ __attribute__((aligned(16))) uint8_t lds_g[kGLdsBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_g0[kG0Bytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_g1[kOperandBytes];
   __shared__ __attribute__((aligned(16))) uint8_t lds_a0[kOperandBytes];
   __shared__ __attribute__((aligned(16))) uint8_t lds_a1[kOperandBytes];
   const int M = args.ep.M, N = args.ep.N, T = args.T;
@@ -296,7 +298,7 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
   Epilogue ep = args.ep;
   const uint16_t* Abase = args.A;
   const uint16_t* Gbase = args.G;
-  int total_rows, nsteps, step0 = 0, nactive = 0, step_base = 0;
+  int total_rows, nsteps, step0 = 0, nactive = 0, nfast = 0, step_base = 0;
   const int spe = T / kBK;
   ClipPlanView plan = clip_plan_view(const_cast<void*>(args.plan), args.B);
   if (kGrouped) {
@@ -320,7 +322,8 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     __syncthreads();
   } else {
     nactive = *plan.nactive;
-    const long long all = (long long)nactive * spe;
+    nfast = *plan.nfast;
+    const long long all = (long long)nfast * spe;
     step_base = (int)(all * split / args.splits);
     nsteps = (int)(all * (split + 1) / args.splits) - step_base;
     total_rows = args.B * T;
@@ -332,7 +335,9 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
 #pragma unroll
     for (int j = 0; j < kNB; ++j) acc[i][j] = f32x16_t{};
 
-  if (nsteps > 0) {
+  // Dense mode: split 0 also runs the plan's slow slots (see below).
+  const bool any_slow = !kGrouped && split == 0 && nactive > nfast;
+  if (nsteps > 0 || any_slow) {
     __amdgpu_buffer_rsrc_t g_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(Gbase), (short)0, total_rows * M * 2, 0x00020000);
     __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -422,6 +427,26 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
             16, (row0 * N * 2 + dma_voff[j]) | bad, 0, 0, 0);
       }
     };
+    // Dense mode: G goes into LDS by DMA too, in the same layout as A (its
+    // scale is applied to the accumulators).
+    int gdma_voff[kDma], gdma_bad[kDma];
+#pragma unroll
+    for (int j = 0; j < kDma; ++j) {
+      const int row = (w * kDma + j) * 2 + (lane >> 5);
+      const int slot = lane & 31;
+      const int gc = (((slot >> 2) ^ (row & 7)) << 5) + (slot & 3) * 8;
+      gdma_voff[j] = row * M * 2 + (m0 + gc) * 2;
+      gdma_bad[j] = (m0 + gc < M) ? 0 : kOutOfRange;
+    }
+    auto dma_g = [&](uint8_t* gstage, int row0) __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = 0; j < kDma; ++j) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            g_rsrc,
+            (__attribute__((address_space(3))) void*)((lds_u8_t*)gstage + (w * kDma + j) * 1024),
+            16, (row0 * M * 2 + gdma_voff[j]) | gdma_bad[j], 0, 0, 0);
+      }
+    };
 
     int goff[4][2], aoff[kNB][2];
 #pragma unroll
@@ -501,9 +526,21 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       }
     };
     Frags fa, fb;
+    // Dense mode: the accumulators hold the partial sum divided by the scale
+    // of the step whose MFMAs run (sc_cur); when the next step belongs to an
+    // example with another scale they are multiplied by sc_cur / sc_next.
+    float sc_cur = 0.0f;
+    auto rescale = [&](float r) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < kNB; ++j) acc[i][j] *= r;
+    };
     auto k_step = [&](int s, const uint8_t* gcur, const uint8_t* acur, uint8_t* gnxt,
                       uint8_t* anxt) __attribute__((always_inline)) {
+      const float sc_s1 = sc_next;  // scale of step s + 1
       dma_a(anxt, row_next, valid_next);
+      if constexpr (!kGrouped) dma_g(gnxt, row_next);
       float sc_after;
       int valid2;
       const int row2 = step_row0(min(s + 2, nsteps - 1), &sc_after, &valid2);
@@ -511,10 +548,12 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       // MFMAs of 16-row sub-steps past them (all zeros) are skipped.
       const int vcur = kGrouped ? valid_cur : kBK;
       auto stage_g = [&](int kk) __attribute__((always_inline)) {
+        if constexpr (kGrouped) {
 #pragma unroll
-        for (int c = 0; c < kGCSub; ++c) store_chunk(gnxt, kk * kGCSub + c, sc_next);
+          for (int c = 0; c < kGCSub; ++c) store_chunk(gnxt, kk * kGCSub + c, sc_next);
 #pragma unroll
-        for (int c = 0; c < kGCSub; ++c) load_chunk(row2, valid2, kk * kGCSub + c);
+          for (int c = 0; c < kGCSub; ++c) load_chunk(row2, valid2, kk * kGCSub + c);
+        }
       };
       __builtin_amdgcn_sched_barrier(0);
       read_frags(gcur, acur, 1, fb);
@@ -540,67 +579,104 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       row_next = row2;
       valid_cur = valid_next;
       valid_next = valid2;
-      DPC_WAIT_VMCNT(kGC);
+      DPC_WAIT_VMCNT(kGrouped ? kGC : 0);
       __syncthreads();
       read_frags(gnxt, anxt, 0, fa);
       if (vcur > 48) mma(fb);
       interleave();
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (!kGrouped) {
+        if (s + 1 < nsteps && sc_s1 != sc_cur) {
+          rescale(sc_cur / sc_s1);
+          sc_cur = sc_s1;
+        }
+      }
     };
 
-    uint8_t* g0 = lds_g;
-    uint8_t* g1 = lds_g + kOperandBytes;
-    // Prologue: step 0 into stage 0 (A by DMA, G through registers), step 1
-    // of G into the registers, the fragments of step 0's first sub-step.
-    int valid0;
-    int row0 = step_row0(0, &sc_next, &valid0);
-    valid_cur = valid0;
-    dma_a(lds_a0, row0, valid0);
+    uint8_t* g0 = lds_g0;
+    uint8_t* g1 = lds_g1;
+    if (nsteps > 0) {
+      // Prologue: step 0 into stage 0 (A by DMA; G by DMA in dense mode, else
+      // through registers, scaled), in grouped mode step 1 of G into the
+      // registers; the fragments of step 0's first sub-step.
+      int valid0;
+      int row0 = step_row0(0, &sc_next, &valid0);
+      valid_cur = valid0;
+      sc_cur = sc_next;
+      dma_a(lds_a0, row0, valid0);
+      if constexpr (kGrouped) {
 #pragma unroll
-    for (int j = 0; j < kGC; ++j) load_chunk(row0, valid0, j);
+        for (int j = 0; j < kGC; ++j) load_chunk(row0, valid0, j);
 #pragma unroll
-    for (int j = 0; j < kGC; ++j) store_chunk(g0, j, sc_next);
-    row_next = step_row0(min(1, nsteps - 1), &sc_next, &valid_next);
+        for (int j = 0; j < kGC; ++j) store_chunk(g0, j, sc_next);
+      } else {
+        dma_g(g0, row0);
+      }
+      row_next = step_row0(min(1, nsteps - 1), &sc_next, &valid_next);
+      if constexpr (kGrouped) {
 #pragma unroll
-    for (int j = 0; j < kGC; ++j) load_chunk(row_next, valid_next, j);
-    DPC_WAIT_VMCNT(kGC);  // the A DMA of step 0 has landed (kGC G loads may be in flight)
-    __syncthreads();
-    read_frags(g0, lds_a0, 0, fa);
-    int s = 0;
-    for (; s + 1 < nsteps; s += 2) {
-      k_step(s, g0, lds_a0, g1, lds_a1);
-      k_step(s + 1, g1, lds_a1, g0, lds_a0);
+        for (int j = 0; j < kGC; ++j) load_chunk(row_next, valid_next, j);
+      }
+      DPC_WAIT_VMCNT(kGrouped ? kGC : 0);  // step 0's DMAs have landed
+      __syncthreads();
+      read_frags(g0, lds_a0, 0, fa);
+      int s = 0;
+      for (; s + 1 < nsteps; s += 2) {
+        k_step(s, g0, lds_a0, g1, lds_a1);
+        k_step(s + 1, g1, lds_a1, g0, lds_a0);
+      }
+      if (s < nsteps) k_step(s, g0, lds_a0, g1, lds_a1);
+      if constexpr (!kGrouped) rescale(sc_cur);
+      DPC_WAIT_VMCNT(0);
+      __syncthreads();
     }
-    if (s < nsteps) k_step(s, g0, lds_a0, g1, lds_a1);
-    DPC_WAIT_VMCNT(0);
-    // The last step's reads of the unused stage are done before the
-    // epilogue reuses the G stages.
-    __syncthreads();
+    // Dense mode, examples whose scale is too small to divide the
+    // accumulators by (the plan's slots nfast .. nactive - 1; split 0 takes
+    // them): G is scaled in fp32 and rounded to bf16 before the product, one
+    // unpipelined K step at a time.
+    if constexpr (!kGrouped) {
+      const int nslow = split == 0 ? (nactive - nfast) * spe : 0;
+      for (int t = 0; t < nslow; ++t) {
+        const int ex = plan.active[nfast + t / spe];
+        const float sc = args.scale[ex];
+        const int rs = ex * T + (t % spe) * kBK;
+        dma_a(lds_a0, rs, kBK);
+#pragma unroll
+        for (int j = 0; j < kGC; ++j) load_chunk(rs, kBK, j);
+#pragma unroll
+        for (int j = 0; j < kGC; ++j) store_chunk(g0, j, sc);
+        DPC_WAIT_VMCNT(0);
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          read_frags(g0, lds_a0, kk, fa);
+          mma(fa);
+        }
+        __syncthreads();
+      }
+    }
   }
 
-  // Epilogue: the 256 x 256 fp32 tile goes through LDS in four quarters of 64
-  // rows; each thread owns a pair of adjacent columns and 64 / (kT / 128) of
-  // the quarter's rows, walked in even/odd row pairs: coalesced 4- or 8-byte
+  // Epilogue: the 256 x 256 fp32 tile goes through LDS in eight slices of 32
+  // rows; each thread owns a pair of adjacent columns and 32 / (kT / 128) of
+  // the slice's rows, walked in even/odd row pairs: coalesced 4- or 8-byte
   // stores, and one Philox block per (row pair, column) in a rolled loop.
-  float* tile = reinterpret_cast<float*>(lds_g);
-  constexpr int kEpiRows = kQuarterRows / (kT / 128);
+  float* tile = reinterpret_cast<float*>(lds_g0);
+  constexpr int kEpiRows = kEpiPassRows / (kT / 128);
   // Unrolled: the accumulator blocks are selected by compile-time indices
   // (a runtime index would move them to scratch memory).
 #pragma unroll
-  for (int quarter = 0; quarter < 4; ++quarter) {
-    if (wm == (quarter >> 1)) {
+  for (int e = 0; e < kBM / kEpiPassRows; ++e) {
+    if (wm == (e >> 2)) {
+      const int i = e & 3;
 #pragma unroll
-      for (int ii = 0; ii < 2; ++ii) {
-        const int i = 2 * (quarter & 1) + ii;
+      for (int j = 0; j < kNB; ++j)
 #pragma unroll
-        for (int j = 0; j < kNB; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int ml = ii * 32 + (r >> 2) * 8 + 4 * (lane >> 5) + (r & 3);
-            const int nl = wn * kWC + j * 32 + (lane & 31);
-            tile[ml * kEpiLd + nl] = acc[i][j][r];
-          }
-      }
+        for (int r = 0; r < 16; ++r) {
+          const int ml = (r >> 2) * 8 + 4 * (lane >> 5) + (r & 3);
+          const int nl = wn * kWC + j * 32 + (lane & 31);
+          tile[ml * kEpiLd + nl] = acc[i][j][r];
+        }
     }
     __syncthreads();
     const int cl = 2 * (tid & 127);
@@ -610,7 +686,7 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       float* part = args.partial + (size_t)split * M * N;
 #pragma unroll 2
       for (int ml = rr; ml < rr + kEpiRows; ++ml) {
-        const int m = m0 + quarter * kQuarterRows + ml, n = n0 + cl;
+        const int m = m0 + e * kEpiPassRows + ml, n = n0 + cl;
         if (m < M && n < N)
           *reinterpret_cast<float2*>(part + (size_t)m * N + n) =
               *reinterpret_cast<const float2*>(tile + ml * kEpiLd + cl);
@@ -621,7 +697,7 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
         const float2 t0 = *reinterpret_cast<const float2*>(tile + ml * kEpiLd + cl);
         const float2 t1 = *reinterpret_cast<const float2*>(tile + (ml + 1) * kEpiLd + cl);
         const float v[2][2] = {{t0.x, t0.y}, {t1.x, t1.y}};
-        emit_quad(ep, m0 + quarter * kQuarterRows + ml, n0 + cl, v);
+        emit_quad(ep, m0 + e * kEpiPassRows + ml, n0 + cl, v);
       }
     }
     __syncthreads();

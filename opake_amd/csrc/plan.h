@@ -1,11 +1,16 @@
 // Device-side plan passed from the clip-factor kernel to the clipped-sum
-// kernels: the examples with a positive scale, in increasing order.  The GEMM
-// walks only these, so examples with scale 0 (clipped to zero, or non-finite
-// data) are never read.
+// kernels: the examples with a positive scale.  The GEMM walks only these, so
+// examples with scale 0 (clipped to zero, or non-finite data) are never read.
+// Slots 0 .. nfast - 1 hold, in increasing order, the examples whose scale
+// the bf16 GEMM may apply to its fp32 accumulators (scale >= 2^-64, and
+// B * C <= 2^55, which bounds the unscaled partial sums); slots nfast ..
+// nactive - 1 the others (gradient norms beyond ~1.8e19 C), in increasing
+// order, whose G rows the GEMM scales before the product.
 //
 // Byte layout for a batch of B examples:
 //   [0, 4)    int   nactive       number of examples with scale > 0
-//   [4, 16)   reserved
+//   [4, 8)    int   nfast         the first nfast slots are the fast ones
+//   [8, 16)   reserved
 //   [16, ..)  int   active[B]     example index of slot j (j < nactive)
 #pragma once
 
@@ -13,8 +18,14 @@
 
 struct ClipPlanView {
   int* nactive;
+  int* nfast;
   int* active;
 };
+
+// Smallest scale the GEMM applies to its accumulators, and the largest
+// B * C for which it does (see above).
+#define DPC_FAST_SCALE_MIN 5.421010862427522e-20f /* 2^-64 */
+#define DPC_FAST_BC_MAX 3.602879701896397e16 /* 2^55 */
 
 __host__ __device__ inline size_t clip_plan_bytes(int B) {
   size_t b = B > 0 ? (size_t)B : 1;
@@ -26,6 +37,7 @@ __host__ __device__ inline ClipPlanView clip_plan_view(void* base, int B) {
   char* p = (char*)base;
   ClipPlanView v;
   v.nactive = (int*)p;
+  v.nfast = (int*)(p + 4);
   v.active = (int*)(p + 16);
   return v;
 }

@@ -207,6 +207,48 @@ def test_clipped_sum_bf16_mfma(dev, B, T, din, dout):
     torch.testing.assert_close(cf.norms.cpu().double(), res.norms, rtol=2e-2, atol=0)
 
 
+def test_clipped_sum_accumulator_scaling_is_near_exact(dev):
+    """The bf16 GEMM applies each example's scale to its fp32 accumulators
+    (no bf16 rounding of the scaled operand): against the exact clipped sum in
+    float64 the error is far below the bf16-rounding level (2^-9)."""
+    B, T, din, dout = 6, 128, 256, 256
+    g = _gen(77)
+    A = torch.randn(B, T, din, generator=g).to(torch.bfloat16)
+    G = (torch.randn(B, T, dout, generator=g) * 0.01 *
+         torch.exp(torch.randn(B, 1, 1, generator=g))).to(torch.bfloat16)
+    w, _, cf = _run_clipped_sum(dev, A, G, 1.0, out_dtype=torch.float32)
+    scale = cf.scale[0].cpu().double()
+    exact = torch.einsum("b,btm,btn->mn", scale, G.double(), A.double())
+    assert _rel_err(w.cpu(), exact) < 1e-5
+
+
+@pytest.mark.parametrize("case", ["tiny_scale", "large_bc"])
+def test_clipped_sum_slow_plan_slots(dev, case):
+    """Examples the GEMM cannot divide its accumulators by -- a scale below
+    2^-64 (gradient norm ~3e20 here, Gram entries still finite in fp32), or
+    every example when B * C > 2^55 --
+    take the slow slots of the clip plan (G scaled before the product); the
+    result matches the oracle, and the fast examples around them are intact."""
+    B, T, din, dout = 5, 128, 256, 264
+    g = _gen(91)
+    A = torch.randn(B, T, din, generator=g).to(torch.bfloat16)
+    G = torch.randn(B, T, dout, generator=g) * 0.01
+    C = 1.0
+    if case == "tiny_scale":
+        G[2] *= 1e19  # norm ~3e20: scale ~3e-21 < 2^-64
+    else:
+        C = 1e17  # B * C > 2^55: no example is clipped, all take the slow slots
+    G = G.to(torch.bfloat16)
+    w, _, cf = _run_clipped_sum(dev, A, G, C, out_dtype=torch.float32)
+    plan = cf.plan.cpu().view(torch.int32)
+    nactive, nfast = int(plan[0]), int(plan[1])
+    assert nactive == B
+    assert nfast == (B - 1 if case == "tiny_scale" else 0)
+    (want,), res = _oracle_clipped_sum(A, G, C, out_dtype=torch.float32)
+    assert _rel_err(w.cpu(), want) < 2e-2
+    torch.testing.assert_close(cf.norms.cpu().double(), res.norms, rtol=2e-2, atol=0)
+
+
 @pytest.mark.parametrize("B,T,din,dout", [(8, 256, 512, 264), (16, 128, 256, 256)])
 def test_clipped_sum_split_k(dev, B, T, din, dout):
     """Launches of few output tiles split their K steps (2-8 slices through the
