@@ -44,54 +44,58 @@ clip_factors_kernel(const double* __restrict__ sqnorm, int B, double C, int kind
   ClipPlanView plan = clip_plan_view(plan_base, B);
   __shared__ int wave_counts[kClipThreads / 64];
   __shared__ int clipped_counts[kClipThreads / 64];
-  __shared__ int base;
+  __shared__ int slow_counts[kClipThreads / 64];
+  __shared__ int base, base_slow;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int nw = blockDim.x >> 6;
   if (tid == 0) base = 0;
   int clipped_local = 0;
-  // Pass 0 computes the scales and lists the fast examples (see plan.h);
-  // pass 1 lists the other active ones after them.  Each listing is an
-  // ordered compaction: a ballot within a wave, wave offsets through LDS.
+  // One pass computes the scales and lists the active examples (see
+  // plan.h): the fast ones from the front of `active` in increasing order,
+  // the others from its back, in increasing order read backwards.  Each list
+  // is an ordered compaction: a ballot within a wave, wave offsets through
+  // LDS.
   const bool fast_ok = (double)B * C <= (double)DPC_FAST_BC_MAX;
-  int nfast = 0;
-  for (int pass = 0; pass < (have_plan ? 2 : 1); ++pass) {
-    for (int start = 0; start < B; start += blockDim.x) {
-      const int i = start + tid;
-      bool take = false;
-      if (i < B) {
-        float s0;
-        if (pass == 0) {
-          double norm;
-          for (int g = 0; g < n_guards; ++g) {
-            double s = guarded_scale(sqnorm[i], C, kind, gamma, guards.rel[g], guards.abs_[g], &norm);
-            float sf = (float)s;
-            if (scale) scale[(size_t)g * B + i] = sf;
-            if (g == 0) s0 = sf;
-          }
-          if (norms_out) norms_out[i] = (float)norm;
-          if ((float)norm > count_threshold) ++clipped_local;
-        } else {
-          s0 = scale[i];
-        }
-        const bool fast = fast_ok && s0 >= DPC_FAST_SCALE_MIN;
-        take = s0 > 0.0f && (pass == 0 ? fast : !fast);
+  if (tid == 0) base_slow = 0;
+  for (int start = 0; start < B; start += blockDim.x) {
+    const int i = start + tid;
+    bool fast = false, slow = false;
+    if (i < B) {
+      double norm;
+      float s0 = 0.0f;
+      for (int g = 0; g < n_guards; ++g) {
+        double s = guarded_scale(sqnorm[i], C, kind, gamma, guards.rel[g], guards.abs_[g], &norm);
+        float sf = (float)s;
+        if (scale) scale[(size_t)g * B + i] = sf;
+        if (g == 0) s0 = sf;
       }
-      unsigned long long mask = __ballot(take);
-      int before = __popcll(mask & ((1ull << lane) - 1ull));
-      if (lane == 0) wave_counts[w] = __popcll(mask);
-      __syncthreads();
-      int offset = base;
-      for (int v = 0; v < w; ++v) offset += wave_counts[v];
-      if (have_plan && take) plan.active[offset + before] = i;
-      __syncthreads();
-      if (tid == 0) {
-        int total = 0;
-        for (int v = 0; v < nw; ++v) total += wave_counts[v];
-        base += total;
-      }
-      __syncthreads();
+      if (norms_out) norms_out[i] = (float)norm;
+      if ((float)norm > count_threshold) ++clipped_local;
+      fast = s0 > 0.0f && fast_ok && s0 >= DPC_FAST_SCALE_MIN;
+      slow = s0 > 0.0f && !fast;
     }
-    if (pass == 0) nfast = base;  // every thread reads base after the barrier above
+    const unsigned long long mf = __ballot(fast), ms = __ballot(slow);
+    const unsigned long long below = (1ull << lane) - 1ull;
+    if (lane == 0) {
+      wave_counts[w] = __popcll(mf);
+      slow_counts[w] = __popcll(ms);
+    }
+    __syncthreads();
+    int of = base, os = base_slow;
+    for (int v = 0; v < w; ++v) {
+      of += wave_counts[v];
+      os += slow_counts[v];
+    }
+    if (have_plan && fast) plan.active[of + __popcll(mf & below)] = i;
+    if (have_plan && slow) plan.active[B - 1 - (os + __popcll(ms & below))] = i;
+    __syncthreads();
+    if (tid == 0) {
+      for (int v = 0; v < nw; ++v) {
+        base += wave_counts[v];
+        base_slow += slow_counts[v];
+      }
+    }
+    __syncthreads();
   }
   for (int off = 32; off > 0; off >>= 1) clipped_local += __shfl_down(clipped_local, off, 64);
   if (lane == 0) clipped_counts[w] = clipped_local;
@@ -101,8 +105,8 @@ clip_factors_kernel(const double* __restrict__ sqnorm, int B, double C, int kind
     for (int v = 0; v < nw; ++v) total += clipped_counts[v];
     if (nclipped) *nclipped = total;
     if (have_plan) {
-      *plan.nactive = base;
-      *plan.nfast = nfast;
+      *plan.nactive = base + base_slow;
+      *plan.nfast = base;
     }
   }
 }

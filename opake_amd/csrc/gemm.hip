@@ -631,13 +631,12 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       __syncthreads();
     }
     // Dense mode, examples whose scale is too small to divide the
-    // accumulators by (the plan's slots nfast .. nactive - 1; split 0 takes
-    // them): G is scaled in fp32 and rounded to bf16 before the product, one
+    // accumulators by (the plan's back list; split 0 takes them): G is scaled in fp32 and rounded to bf16 before the product, one
     // unpipelined K step at a time.
     if constexpr (!kGrouped) {
       const int nslow = split == 0 ? (nactive - nfast) * spe : 0;
       for (int t = 0; t < nslow; ++t) {
-        const int ex = plan.active[nfast + t / spe];
+        const int ex = plan.active[args.B - 1 - t / spe];
         const float sc = args.scale[ex];
         const int rs = ex * T + (t % spe) * kBK;
         dma_a(lds_a0, rs, kBK);
@@ -764,27 +763,34 @@ __device__ __forceinline__ float to_f32<float>(float v) { return v; }
 template <>
 __device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) { return bf16_bits_to_f32(v); }
 
+// Split-K (splits > 1, M and N even): workgroup z sums the K range
+// [z * per, (z + 1) * per) and writes its raw fp32 tile to partial[z]
+// ([M][N]); split_reduce_kernel adds the splits in order and applies the
+// epilogue.
 template <typename In>
 __global__ void __launch_bounds__(kThreads)
 clipped_sum_generic_kernel(const In* __restrict__ A, const In* __restrict__ G,
-                           const float* __restrict__ scale, int B, int T, Epilogue ep) {
+                           const float* __restrict__ scale, int B, int T, Epilogue ep,
+                           int splits, long long per, float* __restrict__ partial) {
   __shared__ float sg[kGK][kGT + 1];
   __shared__ float sa[kGK][kGT + 1];
   const int M = ep.M, N = ep.N;
   const int m0 = blockIdx.y * kGT, n0 = blockIdx.x * kGT;
   const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
   const long long K = (long long)B * T;
+  const long long kb = (long long)blockIdx.z * per;
+  const long long ke = kb + per < K ? kb + per : K;
   float acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
-  for (long long k0 = 0; k0 < K; k0 += kGK) {
+  for (long long k0 = kb; k0 < ke; k0 += kGK) {
     for (int e = tid; e < kGK * kGT; e += kThreads) {
       const int k = e / kGT, col = e % kGT;
       const long long kk = k0 + k;
       float gv = 0.f, av = 0.f;
-      if (kk < K) {
+      if (kk < ke) {
         const float s = scale[kk / T];
         if (s > 0.0f) {
           if (m0 + col < M) gv = s * to_f32<In>(G[kk * M + m0 + col]);
@@ -810,6 +816,17 @@ clipped_sum_generic_kernel(const In* __restrict__ A, const In* __restrict__ G,
     }
     __syncthreads();
   }
+  if (splits > 1) {
+    float* part = partial + (size_t)blockIdx.z * M * N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = m0 + tr * 4 + i, n = n0 + tc * 4 + j;
+        if (m < M && n < N) part[(size_t)m * N + n] = acc[i][j];
+      }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int n = n0 + tc * 4 + j;
@@ -818,6 +835,18 @@ clipped_sum_generic_kernel(const In* __restrict__ A, const In* __restrict__ G,
       emit_pair(ep, m0 + tr * 4 + i, n, acc[i][j], acc[i + 1][j]);
     }
   }
+}
+
+// Split-K factor of the generic kernel: enough workgroups for the CUs
+// (512), K slices of at least 64 rows, M and N even (split_reduce_kernel
+// works on 2 x 2 blocks).
+int generic_splits(int B, int T, int din, int dout) {
+  if (din % 2 != 0 || dout % 2 != 0) return 1;
+  const long long tiles = (long long)ceil_div(din, kGT) * ceil_div(dout, kGT);
+  const long long K = (long long)B * T;
+  long long splits = (512 + tiles - 1) / tiles;
+  splits = splits < K / 64 ? splits : K / 64;
+  return (int)(splits < 1 ? 1 : (splits > 32 ? 32 : splits));
 }
 
 // Bias: partial[split][m] = sum over examples e of the split of
@@ -1088,10 +1117,9 @@ bool fast_shape(int B, int T, int din, int dout, int dtype) {
 extern "C" size_t dpc_clipped_sum_workspace_bytes(int B, int T, int din, int dout, int dtype) {
   if (dout <= 0 || din <= 0 || T <= 0 || B < 0) return 0;
   size_t bytes = bias_ws_bytes(dout);
-  if (fast_shape(B, T, din, dout, dtype)) {
-    const int splits = fast_splits(B, T, din, dout);
-    if (splits > 1) bytes += (size_t)splits * (size_t)dout * (size_t)din * sizeof(float);
-  }
+  const int splits = fast_shape(B, T, din, dout, dtype) ? fast_splits(B, T, din, dout)
+                                                       : generic_splits(B, T, din, dout);
+  if (splits > 1) bytes += (size_t)splits * (size_t)dout * (size_t)din * sizeof(float);
   return bytes;
 }
 
@@ -1156,13 +1184,26 @@ extern "C" int dpc_clipped_sum(const void* A, const void* G, const float* scale,
                          dim3(kThreads), 0, s, (const float*)args.partial, splits, ep);
     }
   } else {
-    dim3 grid(ceil_div(din, kGT), ceil_div(dout, kGT));
+    int splits = generic_splits(B, T, din, dout);
+    const size_t need = bias_ws_bytes(dout) + (size_t)splits * dout * (size_t)din * sizeof(float);
+    if (splits > 1 && (!ws || ws_bytes < need)) splits = 1;
+    const long long K = (long long)B * T;
+    const long long per = ((K + splits - 1) / splits + kGK - 1) / kGK * kGK;
+    float* partial = splits > 1 ? (float*)((uint8_t*)ws + bias_ws_bytes(dout)) : nullptr;
+    dim3 grid(ceil_div(din, kGT), ceil_div(dout, kGT), splits);
     if (dtype == DPC_BF16) {
       hipLaunchKernelGGL(clipped_sum_generic_kernel<uint16_t>, grid, dim3(kThreads), 0, s,
-                         (const uint16_t*)A, (const uint16_t*)G, scale, B, T, ep);
+                         (const uint16_t*)A, (const uint16_t*)G, scale, B, T, ep, splits, per,
+                         partial);
     } else {
       hipLaunchKernelGGL(clipped_sum_generic_kernel<float>, grid, dim3(kThreads), 0, s,
-                         (const float*)A, (const float*)G, scale, B, T, ep);
+                         (const float*)A, (const float*)G, scale, B, T, ep, splits, per, partial);
+    }
+    if (splits > 1) {
+      DPC_HIP_CHECK(hipGetLastError());
+      const long long pairs = (long long)(dout / 2) * (din / 2);
+      hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((pairs + kThreads - 1) / kThreads)),
+                         dim3(kThreads), 0, s, (const float*)partial, splits, ep);
     }
   }
   DPC_HIP_CHECK(hipGetLastError());

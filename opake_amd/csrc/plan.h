@@ -1,17 +1,18 @@
 // Device-side plan passed from the clip-factor kernel to the clipped-sum
 // kernels: the examples with a positive scale.  The GEMM walks only these, so
 // examples with scale 0 (clipped to zero, or non-finite data) are never read.
-// Slots 0 .. nfast - 1 hold, in increasing order, the examples whose scale
+// active[0 .. nfast - 1] holds, in increasing order, the examples whose scale
 // the bf16 GEMM may apply to its fp32 accumulators (scale >= 2^-64, and
-// B * C <= 2^55, which bounds the unscaled partial sums); slots nfast ..
-// nactive - 1 the others (gradient norms beyond ~1.8e19 C), in increasing
-// order, whose G rows the GEMM scales before the product.
+// B * C <= 2^55, which bounds the unscaled partial sums); active[B - 1],
+// active[B - 2], ... down to active[B - (nactive - nfast)] the others
+// (gradient norms beyond ~1.8e19 C), in increasing order, whose G rows the
+// GEMM scales before the product.
 //
 // Byte layout for a batch of B examples:
 //   [0, 4)    int   nactive       number of examples with scale > 0
-//   [4, 8)    int   nfast         the first nfast slots are the fast ones
+//   [4, 8)    int   nfast         number of them in the front list
 //   [8, 16)   reserved
-//   [16, ..)  int   active[B]     example index of slot j (j < nactive)
+//   [16, ..)  int   active[B]
 #pragma once
 
 #include <stddef.h>
