@@ -123,8 +123,13 @@ def _oracle_scales(sq, C, rel_abs_storage, kind="fixed", gamma=0.0):
 @pytest.mark.parametrize("kind", ["fixed", "auto_s"])
 def test_clip_factors_bit_exact(dev, kind):
     g = _gen(11)
-    sq = torch.exp(torch.randn(3000, generator=g, dtype=torch.float64) * 3)
+    B = 3000
+    sq = torch.exp(torch.randn(B, generator=g, dtype=torch.float64) * 3)
     sq[:6] = torch.tensor([0.0, math.inf, math.nan, 1.0, 0.25, 1e300], dtype=torch.float64)
+    # Scales 2^-65 .. 2^-75 (positive in float32, below the plan's 2^-64
+    # fast-list bound) in each of the kernel's 1024-example passes.
+    for i, e in ((7, 130), (1500, 140), (2047, 150), (2999, 134)):
+        sq[i] = 2.0 ** e
     C = clip_oracle.conservative_bound(1.0)
     gamma = 0.01 if kind == "auto_s" else 0.0
     guards = []
@@ -141,11 +146,19 @@ def test_clip_factors_bit_exact(dev, kind):
     norms = torch.sqrt(sq).to(torch.float32)
     torch.testing.assert_close(cf.norms.cpu(), norms, rtol=0, atol=0, equal_nan=True)
     assert int(cf.nclipped.item()) == int((norms > 1.0).sum().item())
-    # Plan: examples with a positive guard-0 scale, in order.
-    active = [i for i in range(sq.numel()) if expect[0][i] > 0]
+    # Plan: examples with a positive guard-0 scale; those at or above 2^-64
+    # from the front in increasing order, the others from the back (B * C is
+    # far below the 2^55 bound here).
+    s0 = expect[0]
+    fast = [i for i in range(B) if s0[i] >= 2.0 ** -64]
+    slow = [i for i in range(B) if 0 < s0[i] < 2.0 ** -64]
+    assert slow == [7, 1500, 2047, 2999]
     plan = cf.plan.cpu().numpy().view(np.int32)
-    assert plan[0] == len(active)
-    assert list(plan[4:4 + len(active)]) == active
+    assert plan[0] == len(fast) + len(slow)
+    assert plan[1] == len(fast)
+    active = plan[4:4 + B]
+    assert list(active[:len(fast)]) == fast
+    assert list(active[B - len(slow):][::-1]) == slow
 
 
 def test_clip_factors_boundary_example(dev):
