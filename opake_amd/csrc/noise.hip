@@ -3,7 +3,11 @@
 // with z injected (float32, same shape) or drawn from the Philox stream of
 // (seed, leaf) under the [rows, cols] view described in common.h.  Each thread
 // produces one even/odd row pair of one column, so consecutive threads touch
-// consecutive columns.
+// consecutive columns.  Wide leaves (kRowBlocks) give each workgroup 256
+// columns of one row pair, so the row pair comes from one workgroup-uniform
+// division; other leaves split a flat thread index per lane (in 32 bits when
+// the leaf's pair count allows, a 64-bit division costing about as much as
+// the rest of the thread's work).
 #include "common.h"
 
 namespace {
@@ -19,15 +23,33 @@ __device__ __forceinline__ float add_scaled(float x, float sigma, float z) {
 }
 #pragma clang fp contract(on)
 
-template <bool kBf16>
+template <bool kBf16, bool kRowBlocks>
 __global__ void __launch_bounds__(kNoiseThreads)
 add_noise_kernel(const void* __restrict__ x, void* __restrict__ y, int64_t rows, int64_t cols,
                  float sigma, int mode, const float* __restrict__ noise, uint64_t seed,
-                 uint32_t leaf) {
+                 uint32_t leaf, uint32_t col_blocks) {
   const int64_t pairs = (rows + 1) >> 1;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= pairs * cols) return;
-  const int64_t pr = t / cols, c = t - pr * cols;
+  int64_t pr, c;
+  if (kRowBlocks) {
+    const uint32_t b = blockIdx.x;
+    const uint32_t p = b / col_blocks;
+    pr = p;
+    c = (int64_t)(b - p * col_blocks) * kNoiseThreads + threadIdx.x;
+    if (c >= cols) return;
+  } else {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t work = pairs * cols;
+    if (t >= work) return;
+    if (work <= 0xffffffffLL) {
+      const uint32_t q = (uint32_t)t / (uint32_t)cols;
+      pr = q;
+      c = (uint32_t)t - q * (uint32_t)cols;
+    } else {
+      pr = t / cols;
+      c = t - pr * cols;
+    }
+  }
+  const int64_t t = pr * cols + c;  // Philox block of (row pair, column)
   const int64_t r0 = pr * 2;
   float z0, z1;
   if (mode == DPC_NOISE_PHILOX) {
@@ -80,15 +102,32 @@ extern "C" int dpc_add_noise(const void* x, void* y, int64_t rows, int64_t cols,
   }
   if (noise_mode != DPC_NOISE_INJECTED && noise_mode != DPC_NOISE_PHILOX) return DPC_EINVAL;
   if (noise_mode == DPC_NOISE_INJECTED && !noise) return DPC_EINVAL;
-  const int64_t work = ((rows + 1) >> 1) * cols;
-  const int64_t blocks = (work + kNoiseThreads - 1) / kNoiseThreads;
+  const int64_t pairs = (rows + 1) >> 1;
+  const int64_t col_blocks = (cols + kNoiseThreads - 1) / kNoiseThreads;
+  // Row blocks when at most 1/8 of their lanes idle (or none do).
+  const bool row_blocks = cols % kNoiseThreads == 0 || cols >= 8 * kNoiseThreads;
+  const int64_t blocks = row_blocks ? pairs * col_blocks
+                                    : (pairs * cols + kNoiseThreads - 1) / kNoiseThreads;
   if (blocks > 0x7fffffffLL) return DPC_ENOTSUP;
+  const dim3 grid((unsigned)blocks), block(kNoiseThreads);
+  const float sg = (float)sigma;
+  const uint32_t cb = (uint32_t)col_blocks;
   if (dtype == DPC_BF16) {
-    hipLaunchKernelGGL(add_noise_kernel<true>, dim3((unsigned)blocks), dim3(kNoiseThreads), 0, s,
-                       x, y, rows, cols, (float)sigma, noise_mode, noise, seed, leaf_id);
+    if (row_blocks) {
+      hipLaunchKernelGGL((add_noise_kernel<true, true>), grid, block, 0, s, x, y, rows, cols, sg,
+                         noise_mode, noise, seed, leaf_id, cb);
+    } else {
+      hipLaunchKernelGGL((add_noise_kernel<true, false>), grid, block, 0, s, x, y, rows, cols, sg,
+                         noise_mode, noise, seed, leaf_id, cb);
+    }
   } else {
-    hipLaunchKernelGGL(add_noise_kernel<false>, dim3((unsigned)blocks), dim3(kNoiseThreads), 0, s,
-                       x, y, rows, cols, (float)sigma, noise_mode, noise, seed, leaf_id);
+    if (row_blocks) {
+      hipLaunchKernelGGL((add_noise_kernel<false, true>), grid, block, 0, s, x, y, rows, cols, sg,
+                         noise_mode, noise, seed, leaf_id, cb);
+    } else {
+      hipLaunchKernelGGL((add_noise_kernel<false, false>), grid, block, 0, s, x, y, rows, cols,
+                         sg, noise_mode, noise, seed, leaf_id, cb);
+    }
   }
   DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;

@@ -342,18 +342,21 @@ def test_clipped_sum_fast_and_generic_agree(dev):
 # --- noise ---------------------------------------------------------------------
 
 
+# Shapes on both launch layouts: a flat thread index (narrow leaves) and one
+# row pair per workgroup row (columns a multiple of 256, or at least 2048).
+@pytest.mark.parametrize("shape", [(37, 19), (5, 512), (3, 2100)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_add_noise_injected_bit_exact(dev, dtype):
+def test_add_noise_injected_bit_exact(dev, dtype, shape):
     from oracle import noise_oracle
 
     g = _gen(61)
-    x = torch.randn(37, 19, generator=g).to(dtype)
-    z = torch.randn(37, 19, generator=g)
+    x = torch.randn(*shape, generator=g).to(dtype)
+    z = torch.randn(*shape, generator=g)
     y = ops.add_noise(x.to(dev), 0.7, mode=nat.NOISE_INJECTED, noise=z.to(dev)).cpu()
     assert torch.equal(y, noise_oracle.sample(x, 0.7, z))
 
 
-@pytest.mark.parametrize("shape", [(64, 33), (7,), (5, 3, 4)])
+@pytest.mark.parametrize("shape", [(64, 33), (7,), (5, 3, 4), (7, 768), (3, 2100), (2, 4, 1024)])
 def test_add_noise_device_stream_matches_c_oracle(dev, shape):
     x = torch.zeros(shape)
     seed = 0x0123456789ABCDEF
