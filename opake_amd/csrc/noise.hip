@@ -74,6 +74,56 @@ add_noise_kernel(const void* __restrict__ x, void* __restrict__ y, int64_t rows,
   }
 }
 
+// Wide leaves with an even column count and 8-byte aligned operands: each
+// thread takes columns c, c + 1 (c even) of one row pair -- 4- or 8-byte
+// loads and stores, two independent Philox blocks -- and each workgroup 512
+// columns of one row pair.  Same Philox blocks as add_noise_kernel.
+template <bool kBf16>
+__global__ void __launch_bounds__(kNoiseThreads)
+add_noise_pairs_kernel(const void* __restrict__ x, void* __restrict__ y, int64_t rows,
+                       int64_t cols, float sigma, int mode, const float* __restrict__ noise,
+                       uint64_t seed, uint32_t leaf, uint32_t col_blocks) {
+  const uint32_t b = blockIdx.x;
+  const uint32_t p = b / col_blocks;
+  const int64_t c = (int64_t)(b - p * col_blocks) * (2 * kNoiseThreads) + 2 * threadIdx.x;
+  if (c >= cols) return;
+  const int64_t r0 = 2 * (int64_t)p;
+  float z[2][2];  // z[row h][column k]
+  if (mode == DPC_NOISE_PHILOX) {
+    const uint64_t blk = (uint64_t)p * (uint64_t)cols + (uint64_t)c;
+    philox_normal_pair(seed, leaf, blk, &z[0][0], &z[1][0]);
+    philox_normal_pair(seed, leaf, blk + 1, &z[0][1], &z[1][1]);
+  } else {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float2 v = {0.0f, 0.0f};
+      if (r0 + h < rows) v = *reinterpret_cast<const float2*>(noise + (r0 + h) * cols + c);
+      z[h][0] = v.x;
+      z[h][1] = v.y;
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t r = r0 + h;
+    if (r >= rows) break;
+    const int64_t idx = r * cols + c;
+    if (kBf16) {
+      const uint32_t xv = *reinterpret_cast<const uint32_t*>(
+          reinterpret_cast<const uint16_t*>(x) + idx);
+      const float a = add_scaled<true>(bf16_bits_to_f32((uint16_t)(xv & 0xffffu)), sigma, z[h][0]);
+      const float d = add_scaled<true>(bf16_bits_to_f32((uint16_t)(xv >> 16)), sigma, z[h][1]);
+      *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(y) + idx) =
+          (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(d) << 16);
+    } else {
+      const float2 xv = *reinterpret_cast<const float2*>(reinterpret_cast<const float*>(x) + idx);
+      float2 out;
+      out.x = add_scaled<false>(xv.x, sigma, z[h][0]);
+      out.y = add_scaled<false>(xv.y, sigma, z[h][1]);
+      *reinterpret_cast<float2*>(reinterpret_cast<float*>(y) + idx) = out;
+    }
+  }
+}
+
 __global__ void philox_kat_kernel(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
                                   uint32_t k1, int n, uint32_t* __restrict__ out) {
   const int j = blockIdx.x * blockDim.x + threadIdx.x;
@@ -112,7 +162,20 @@ extern "C" int dpc_add_noise(const void* x, void* y, int64_t rows, int64_t cols,
   const dim3 grid((unsigned)blocks), block(kNoiseThreads);
   const float sg = (float)sigma;
   const uint32_t cb = (uint32_t)col_blocks;
-  if (dtype == DPC_BF16) {
+  const uintptr_t align = (uintptr_t)x | (uintptr_t)y |
+                          (uintptr_t)(noise_mode == DPC_NOISE_INJECTED ? noise : nullptr);
+  if (row_blocks && cols % 2 == 0 && align % 8 == 0) {
+    const int64_t pair_blocks = pairs * ((cols + 2 * kNoiseThreads - 1) / (2 * kNoiseThreads));
+    const uint32_t pcb = (uint32_t)((cols + 2 * kNoiseThreads - 1) / (2 * kNoiseThreads));
+    const dim3 pgrid((unsigned)pair_blocks);
+    if (dtype == DPC_BF16) {
+      hipLaunchKernelGGL(add_noise_pairs_kernel<true>, pgrid, block, 0, s, x, y, rows, cols, sg,
+                         noise_mode, noise, seed, leaf_id, pcb);
+    } else {
+      hipLaunchKernelGGL(add_noise_pairs_kernel<false>, pgrid, block, 0, s, x, y, rows, cols, sg,
+                         noise_mode, noise, seed, leaf_id, pcb);
+    }
+  } else if (dtype == DPC_BF16) {
     if (row_blocks) {
       hipLaunchKernelGGL((add_noise_kernel<true, true>), grid, block, 0, s, x, y, rows, cols, sg,
                          noise_mode, noise, seed, leaf_id, cb);

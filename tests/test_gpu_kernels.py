@@ -356,7 +356,8 @@ def test_add_noise_injected_bit_exact(dev, dtype, shape):
     assert torch.equal(y, noise_oracle.sample(x, 0.7, z))
 
 
-@pytest.mark.parametrize("shape", [(64, 33), (7,), (5, 3, 4), (7, 768), (3, 2100), (2, 4, 1024)])
+@pytest.mark.parametrize("shape", [(64, 33), (7,), (5, 3, 4), (7, 768), (3, 2100), (2, 4, 1024),
+                                   (3, 2049)])
 def test_add_noise_device_stream_matches_c_oracle(dev, shape):
     x = torch.zeros(shape)
     seed = 0x0123456789ABCDEF
@@ -366,6 +367,27 @@ def test_add_noise_device_stream_matches_c_oracle(dev, shape):
     # The device evaluates the transform in float (normals within 1e-6 of the
     # double-precision formulas).
     torch.testing.assert_close(y.double(), want, rtol=0, atol=5e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_add_noise_misaligned_leaf_matches_aligned(dev, dtype):
+    # A leaf starting one element into its storage is not 8-byte aligned and
+    # takes the one-column kernel; the aligned copy takes the two-column one.
+    g = _gen(67)
+    flat = torch.randn(1 + 5 * 1024, generator=g).to(dtype).to(dev)
+    x = flat[1:].view(5, 1024)
+    assert x.data_ptr() % 8 != 0
+    seed = 0x5EED
+    y = ops.add_noise(x, 0.5, mode=nat.NOISE_PHILOX, seed=seed, leaf_id=2)
+    y_aligned = ops.add_noise(x.clone(), 0.5, mode=nat.NOISE_PHILOX, seed=seed, leaf_id=2)
+    assert torch.equal(y.cpu(), y_aligned.cpu())
+    z = torch.randn(5, 1024, generator=g)
+    zf = torch.zeros(1 + z.numel())
+    zf[1:] = z.flatten()
+    zv = zf.to(dev)[1:].view(5, 1024)
+    yi = ops.add_noise(x, 0.5, mode=nat.NOISE_INJECTED, noise=zv)
+    yi_aligned = ops.add_noise(x.clone(), 0.5, mode=nat.NOISE_INJECTED, noise=z.to(dev))
+    assert torch.equal(yi.cpu(), yi_aligned.cpu())
 
 
 def test_clipped_sum_epilogue_noise_injected_bit_exact(dev):
