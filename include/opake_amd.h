@@ -62,30 +62,40 @@ int dpc_write_words(void* dst, const uint32_t* host_words, int n, void* stream);
  *     ||G_i^T A_i||_F^2 = <A_i A_i^T, G_i G_i^T>.
  *
  * dpc_gram_sqnorms: A [B, T, din], G [B, T, dout] in `dtype`.  Adds (or, if
- * accumulate == 0, writes) ||G_i^T A_i||^2 to sqnorm[i] (float64, [B]).  A
- * layer bias adds ||sum_t G_i[t]||^2 when with_bias != 0.  Examples whose
- * A_i or G_i hold NaN/Inf produce a non-finite value (their clip factor
- * becomes 0).
+ * accumulate == 0, writes) ||G_i^T A_i||^2 to sqnorm[i] (float64, [B]), and
+ * an upper bound of its rounding error to sqerr[i] (float64, [B]; nullable),
+ * so that sqnorm[i] + sqerr[i] >= ||G_i^T A_i||^2 exactly for the given
+ * values -- the `abs_out` guard term: <A A^T, G G^T> cancels, so its error
+ * scales with the magnitudes of the Gram entries, not with the result.  The
+ * bound covers the Gram matrices' accumulation chains (fp32 MFMA: any
+ * rounding or truncation of at most one fp32 ulp per addend of an MFMA
+ * instruction, and flushed subnormals; generic path: fp64) and the fp64
+ * inner product.  A layer bias adds ||sum_t G_i[t]||^2 (and its bound) when
+ * with_bias != 0.  Examples whose A_i or G_i hold NaN/Inf produce a
+ * non-finite value (their clip factor becomes 0).
  * -------------------------------------------------------------------------*/
 size_t dpc_gram_workspace_bytes(int B, int T);
 int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int din, int dout, int dtype,
-                     int with_bias, int accumulate, double* sqnorm, void* ws, size_t ws_bytes,
-                     void* stream);
+                     int with_bias, int accumulate, double* sqnorm, double* sqerr, void* ws,
+                     size_t ws_bytes, void* stream);
 
 /* Flat inputs (T == 1): a [B, din], g [B, dout];
- * sqnorm[i] (+)= ||a_i||^2 ||g_i||^2 (+ ||g_i||^2 with a bias). */
+ * sqnorm[i] (+)= ||a_i||^2 ||g_i||^2 (+ ||g_i||^2 with a bias), sqerr[i] (+)=
+ * its error bound (nullable). */
 int dpc_flat_sqnorms(const void* a, const void* g, int B, int din, int dout, int dtype,
-                     int with_bias, int accumulate, double* sqnorm, void* stream);
+                     int with_bias, int accumulate, double* sqnorm, double* sqerr, void* stream);
 
 /* ------------------------------------------------------------------------
  * Clip factors from squared norms.
  *
  * Replaces the ratio and scale computation of _streaming.py:84-108 and
  * _pytree.py:111-157 (`_guard_scale` / `_finalize_scale`), evaluated in
- * float64:
- *   norm   = sqrt(sqnorm[i])
- *   ratio  = max(C, 0) / norm                      (kind FIXED)
- *          = max(C, 0) / (norm + gamma)            (kind AUTO_S)
+ * float64, from an upper bound of the norm when sqerr (nullable, the bound of
+ * dpc_gram_sqnorms) is given:
+ *   norm   = sqrt(max(sqnorm[i], 0))               (the estimate, reported)
+ *   up     = sqrt(max(sqnorm[i] + sqerr[i], 0))    (sqerr NULL: up = norm)
+ *   ratio  = max(C, 0) / up                        (kind FIXED)
+ *          = max(C, 0) / (up + gamma)              (kind AUTO_S)
  *   s      = ratio * guard_rel[g] - guard_abs[g]
  *   s      = min(1, s)                             (FIXED only)
  *   s      = isfinite(s) ? max(s, 0) : 0
@@ -95,16 +105,17 @@ int dpc_flat_sqnorms(const void* a, const void* g, int B, int din, int dout, int
  * guard_rel / guard_abs are HOST arrays of n_guards (1..4) values, one
  * pair per storage dtype.  sqnorm and all outputs are device pointers.
  * Any output pointer may be NULL.  `plan` (nullable, device memory of
- * dpc_clip_plan_bytes(B) bytes) receives the examples whose guard-0 scale is
- * positive, those the bf16 GEMM may apply to its accumulators first (scale
- * >= 2^-64 and B * C <= 2^55), then the others, each list in increasing
- * order; the clipped-sum GEMM walks only these.
+ * n_guards * dpc_clip_plan_bytes(B) bytes) receives one plan per guard: the
+ * examples whose guard-g scale is positive, those the bf16 GEMM may apply to
+ * its accumulators first (2^-64 <= scale <= 2^32 and B * C <= 2^55), then the
+ * others, each list in increasing order; the clipped-sum GEMM walks only
+ * these.
  * -------------------------------------------------------------------------*/
 size_t dpc_clip_plan_bytes(int B);
-int dpc_clip_factors(const double* sqnorm, int B, double C, int kind, double gamma,
-                     const double* guard_rel, const double* guard_abs, int n_guards,
-                     float count_threshold, float* scale, float* norms_out, int* nclipped,
-                     void* plan, void* stream);
+int dpc_clip_factors(const double* sqnorm, const double* sqerr, int B, double C, int kind,
+                     double gamma, const double* guard_rel, const double* guard_abs,
+                     int n_guards, float count_threshold, float* scale, float* norms_out,
+                     int* nclipped, void* plan, void* stream);
 
 /* ------------------------------------------------------------------------
  * Clipped batch sum of a linear layer with the noise epilogue fused.
@@ -124,8 +135,8 @@ int dpc_clip_factors(const double* sqnorm, int B, double C, int kind, double gam
  * bf16 MFMA path (T % 64 == 0, din and dout multiples of 8) the products of
  * the given bf16 values are summed in fp32 and each example's scale is
  * applied to the fp32 accumulators (the plan's first list); examples of the
- * plan's second list have each G element scaled in fp32 and rounded to bf16
- * once before the product.  With
+ * plan's second list have G multiplied by the power of two of their scale
+ * (exact) and the mantissa applied to the accumulators.  With
  * with_bias, bias_out[m] = same recipe over
  * sum_i scale[i] * sum_t G[i, t, m], its noise keyed by (seed, bias_leaf_id)
  * under the [dout, 1] view.  ws (dpc_clipped_sum_workspace_bytes) holds the
@@ -212,7 +223,8 @@ int dpc_group_sum_f64(const double* x, int B, int n, int stride, const int32_t* 
  *
  * dpc_grouped_gram_sqnorms: seg_sq[v] = ||G_v^T A_v||^2 for every segment v
  *   (float64, written), the per-sample norms of the virtual experts that
- *   _streaming.py:70-82 would take of the materialised gradients.  Problems
+ *   _streaming.py:70-82 would take of the materialised gradients, and
+ *   seg_err[v] (nullable) its error bound as in dpc_gram_sqnorms.  Problems
  *   may differ in shape: `dims` is a HOST int32 array [n_problems][2] of
  *   (din, dout), n_problems <= 64.  `items` (device int32 [n_items][4])
  *   lists (problem << 16 | pair, first row, rows, slot) for every 128-row
@@ -221,7 +233,7 @@ int dpc_group_sum_f64(const double* x, int B, int n, int stride, const int32_t* 
  *   n_items a multiple of 8, item l runs on XCD l / (n_items / 8).  slot is
  *   the item's index in segment-major order, and seg_item_start (device int32
  *   [S + 1]) gives each segment's slot range.  max_rows bounds every
- *   segment's rows.  ws: n_items float64.
+ *   segment's rows.  ws: n_items * 12 float64 (one record per item).
  * dpc_segment_plan: the step table of dpc_grouped_clipped_sum.  Segment v
  *   (rows seg_row0[v] .. + seg_len[v] of problem seg_group[v]; segments sorted
  *   by problem) contributes ceil(seg_len / 64) steps (row0, v << 7 | rows)
@@ -232,13 +244,16 @@ int dpc_group_sum_f64(const double* x, int B, int n, int stride, const int32_t* 
  *     acc[m, n] = sum_v seg_scale[v] * sum_{t in v} G_e[t, m] * A_e[t, n]
  *   written to out_ptrs[e] ([dout, din], out_dtype) with / normalize_by and
  *   noise sigmas[e] * z (z from noise_ptrs[e] or Philox (seed, leaf_ids[e])).
+ *   On the bf16 MFMA path G is multiplied by the power of two of its
+ *   segment's scale (exact) and the mantissa is applied to the fp32
+ *   accumulators.
  *   rows (device int32 [E]) bounds each problem's operand rows; max_rows
  *   bounds rows.  Segments with scale 0 are never read.
  * -------------------------------------------------------------------------*/
 int dpc_grouped_gram_sqnorms(const int64_t* a_ptrs, const int64_t* g_ptrs, const int32_t* dims,
                              int n_problems, int dtype, const int32_t* items, int n_items,
                              int max_rows, const int32_t* seg_item_start, int S, double* seg_sq,
-                             void* ws, size_t ws_bytes, void* stream);
+                             double* seg_err, void* ws, size_t ws_bytes, void* stream);
 int dpc_segment_plan(const int32_t* seg_row0, const int32_t* seg_len, const int32_t* seg_group,
                      const float* seg_scale, int S, int E, int max_steps, int32_t* steps,
                      int32_t* step_start, void* stream);

@@ -42,6 +42,8 @@ _c_u32 = ctypes.c_uint32
 _c_u64 = ctypes.c_uint64
 _c_i64 = ctypes.c_int64
 
+ABI_VERSION = 200  # dpc_version() of the library these signatures describe
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "dpc_version": (_c_int, []),
@@ -52,17 +54,17 @@ SIGNATURES = {
     "dpc_gram_sqnorms": (
         _c_int,
         [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
-         _c_void_p, _c_void_p, _c_size_t, _c_void_p],
+         _c_void_p, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
     ),
     "dpc_flat_sqnorms": (
         _c_int,
         [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,
-         _c_void_p],
+         _c_void_p, _c_void_p],
     ),
     "dpc_clip_plan_bytes": (_c_size_t, [_c_int]),
     "dpc_clip_factors": (
         _c_int,
-        [_c_void_p, _c_int, _c_double, _c_int, _c_double, ctypes.POINTER(_c_double),
+        [_c_void_p, _c_void_p, _c_int, _c_double, _c_int, _c_double, ctypes.POINTER(_c_double),
          ctypes.POINTER(_c_double), _c_int, _c_float, _c_void_p, _c_void_p, _c_void_p,
          _c_void_p, _c_void_p],
     ),
@@ -105,7 +107,7 @@ SIGNATURES = {
     "dpc_grouped_gram_sqnorms": (
         _c_int,
         [_c_void_p, _c_void_p, ctypes.POINTER(_c_int), _c_int, _c_int, _c_void_p, _c_int, _c_int,
-         _c_void_p, _c_int, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
+         _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
     ),
     "dpc_segment_plan": (
         _c_int,
@@ -145,6 +147,11 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = restype
             fn.argtypes = argtypes
+        version = lib.dpc_version()
+        if version != ABI_VERSION:
+            raise OperationError(
+                f"{LIB_PATH} has ABI version {version}, these bindings need {ABI_VERSION}; "
+                "rebuild it")
         _lib = lib
         return lib
 

@@ -9,11 +9,14 @@ output gradients ``G`` [B, T, dout] the per-example weight gradient is
 
 1. per-example squared norms through the Gram identity
    ``||G_i^T A_i||^2 = <A_i A_i^T, G_i G_i^T>`` (``dpc_gram_sqnorms``; flat
-   inputs use ``||a_i||^2 ||g_i||^2``);
+   inputs use ``||a_i||^2 ||g_i||^2``), each with an upper bound ``err_i`` of
+   its rounding error (the Gram inner product cancels, so its error scales
+   with the Gram entries, not with the result);
 2. guarded clip factors, the reference's ``_finalize_scale`` in float64
    (``dpc_clip_factors``) with the guard constants the reference would use for
    the materialised leaves (storage = leaf dtype, multiply = float32,
-   roundoff from the leaf sizes);
+   roundoff from the leaf sizes), taken from ``sqrt(sq_i + err_i)``, so that
+   ``c_i ||G_i^T A_i|| <= C`` holds exactly;
 3. one GEMM ``sum_i c_i G_i^T A_i`` with ``/ normalize_by`` and, optionally,
    the Gaussian noise fused into its epilogue (``dpc_clipped_sum``).
 
@@ -23,9 +26,16 @@ over ``{"weight": [dout, din]}`` (plus ``"bias": [dout]``) with
 
 Differences from the materialised reference, all documented in tests:
 * the norm is that of the exact product ``G_i^T A_i`` of the given values,
-  not of its bf16-rounded copy (they agree to the bf16 rounding of the entries);
-* on the bf16 MFMA path each ``c_i G_i`` entry is rounded to bf16 once
-  before the product instead of each ``c_i (G_i^T A_i)`` entry;
+  not of its bf16-rounded copy (they agree to the bf16 rounding of the
+  entries); the reported norms are the estimate ``sqrt(sq_i)``, the scales
+  come from the bound (a clipped example is scaled by up to ~0.5% less at
+  the bf16 benchmark shapes);
+* the clipped sum never rounds an operand: on the bf16 MFMA path the
+  products of the given values are summed in fp32 and each example's scale
+  multiplies the fp32 accumulators (examples with extreme scales: G times the
+  power of two of the scale, which is exact, and the mantissa on the
+  accumulators); the reference instead rounds each ``c_i (G_i^T A_i)`` entry
+  to the leaf dtype before its fp32 batch sum;
 * an example whose ``A_i`` or ``G_i`` holds NaN/Inf gets a non-finite norm
   and clip factor 0 (the whole example is dropped); the reference instead
   zeroes the non-finite gradient entries and keeps the rest.
@@ -96,12 +106,16 @@ def guard_for_linear(dtype: torch.dtype, din: int, dout: int, bias: bool):
 
 
 def ghost_sqnorms(A: torch.Tensor, G: torch.Tensor, *, bias: bool = False,
-                  out: torch.Tensor | None = None) -> torch.Tensor:
-    """Per-example squared gradient norms of one linear layer (float64 [B])."""
+                  out: torch.Tensor | None = None, err: torch.Tensor | None = None):
+    """Per-example squared gradient norms of one linear layer and the bounds of
+    their rounding errors: ``(sq, err)``, float64 [B] each, with
+    ``sq + err >= ||G_i^T A_i||^2``.  With ``out`` / ``err`` the layer's values
+    are added to them."""
     A, G = _check_inputs(A, G, bias)
     if A.shape[1] == 1:
-        return ops.flat_sqnorms(A[:, 0], G[:, 0], with_bias=bias, out=out)
-    return ops.gram_sqnorms(A, G, with_bias=bias, out=out)
+        return ops.flat_sqnorms(A[:, 0], G[:, 0], with_bias=bias, out=out, err=err,
+                                return_error=True)
+    return ops.gram_sqnorms(A, G, with_bias=bias, out=out, err=err, return_error=True)
 
 
 def _scale_kind(auto_s_gamma):
@@ -151,11 +165,12 @@ def ghost_clip_sum(
     max_norm = clipping_norm / normalize_by
 
     with record_function("opake::ghost_clip_sum"):
-        sq = ghost_sqnorms(A, G, bias=bias)
+        sq, err = ghost_sqnorms(A, G, bias=bias)
         cf = ops.clip_factors(
             sq,
             num.conservative_bound(clipping_norm),
             [guard_for_linear(A.dtype, din, dout, bias)],
+            err=err,
             kind=kind,
             gamma=gamma,
             count_threshold=num.float32_of(clipping_norm),
@@ -193,7 +208,7 @@ def ghost_clip_sum(
         if gemm_events is not None:
             gemm_events[0].record()
         w, b = ops.clipped_sum(
-            A, G, cf.scale[0], plan=cf.plan, normalize_by=normalize_by, noise=spec,
+            A, G, cf.scale[0], plan=cf.plan[0], normalize_by=normalize_by, noise=spec,
             out_dtype=out_dtype, with_bias=bias,
         )
         if gemm_events is not None:

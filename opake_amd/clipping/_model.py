@@ -398,13 +398,18 @@ def ghost_clip_captured(
     device = (dense + segmented)[0].A.device if (dense or segmented) else \
         direct[direct_names[0]].device
 
-    # Per-group, per-example squared norms.
+    # Per-group, per-example squared norms and the bounds of their rounding
+    # errors (the ghost norms' sq + err bounds ||g||^2; the materialised
+    # leaves' norms follow the reference's own roundoff, in the guard).
     sq = torch.zeros((n_groups, B), dtype=torch.float64, device=device)
+    err = torch.zeros((n_groups, B), dtype=torch.float64, device=device)
     for L in dense:
         if L.A.shape[1] == 1:
-            ops.flat_sqnorms(L.A[:, 0], L.G[:, 0], with_bias=L.cap.has_bias, out=sq[L.group])
+            ops.flat_sqnorms(L.A[:, 0], L.G[:, 0], with_bias=L.cap.has_bias, out=sq[L.group],
+                             err=err[L.group])
         else:
-            ops.gram_sqnorms(L.A, L.G, with_bias=L.cap.has_bias, out=sq[L.group])
+            ops.gram_sqnorms(L.A, L.G, with_bias=L.cap.has_bias, out=sq[L.group],
+                             err=err[L.group])
     # The norms of all segmented layers of one dtype in one grouped launch
     # (up to 64 layers each; mixed shapes, most expensive tile pairs first).
     by_dtype = {}
@@ -416,16 +421,18 @@ def ghost_clip_captured(
             members = members_all[c0:c0 + cap]
             layout = ops.SegmentLayout([L.cap.segments for L in members], device,
                                        gram_weights=[L.A.shape[1] + L.G.shape[1] for L in members])
-            seg_sq = ops.grouped_gram_sqnorms([L.A for L in members], [L.G for L in members],
-                                              layout)
+            seg_sq, seg_err = ops.grouped_gram_sqnorms(
+                [L.A for L in members], [L.G for L in members], layout, return_error=True)
             # Per-group sums over the layers, in layer order: [B, E] columns
             # folded by group.
             cols = device_table([L.group for L in members], np.int32, device)
-            by_example = seg_sq.t().contiguous()
-            gsq = torch.empty((n_groups, B), dtype=torch.float64, device=device)
-            nat.call("dpc_group_sum_f64", nat.ptr(by_example), B, len(members), len(members),
-                     nat.ptr(cols), n_groups, nat.ptr(gsq), nat.stream_handle(device))
-            sq += gsq
+            for acc, per_seg in ((sq, seg_sq), (err, seg_err)):
+                by_example = per_seg.t().contiguous()
+                gsum = torch.empty((n_groups, B), dtype=torch.float64, device=device)
+                nat.call("dpc_group_sum_f64", nat.ptr(by_example), B, len(members),
+                         len(members), nat.ptr(cols), n_groups, nat.ptr(gsum),
+                         nat.stream_handle(device))
+                acc += gsum
     # The clipped sums: one grouped launch per layer shape.
     buckets = {}
     for L in segmented:
@@ -454,7 +461,7 @@ def ghost_clip_captured(
                      key=str)
     guards = [num.guard_constants(dt, torch.promote_types(dt, torch.float32), roundoff)
               for dt in storage]
-    cfs = [ops.clip_factors(sq[g], num.conservative_bound(bounds[g]), guards,
+    cfs = [ops.clip_factors(sq[g], num.conservative_bound(bounds[g]), guards, err=err[g],
                             count_threshold=num.float32_of(bounds[g]))
            for g in range(n_groups)]
 
@@ -514,7 +521,7 @@ def ghost_clip_captured(
                 spec = ops.NoiseSpec(sigma=s_w, mode=nat.NOISE_PHILOX, seed=step_key.seed,
                                      leaf_id=leaf_index[wn], bias_leaf_id=leaf_index.get(bn, 0))
         ev = _event_pair(gemm_events)
-        w, b = ops.clipped_sum(L.A, L.G, cf.scale[si], plan=cf.plan if len(storage) == 1 else None,
+        w, b = ops.clipped_sum(L.A, L.G, cf.scale[si], plan=cf.plan[si],
                                normalize_by=normalize_by, noise=spec,
                                out_dtype=dtype or L.cap.param_dtype or L.A.dtype,
                                with_bias=L.cap.has_bias)

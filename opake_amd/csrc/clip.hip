@@ -1,13 +1,17 @@
 // Clip factors from per-example squared norms, in float64, plus the active
-// example plan consumed by the clipped-sum GEMM.
+// example plans consumed by the clipped-sum GEMM.
 //
 // The scale is the reference's guarded ratio (packages/opake-engine/src/opake/
-// api/engine/clipping/_pytree.py:111-157, _streaming.py:84-108):
-//   ratio = max(C,0)/norm  or  max(R,0)/(norm + gamma)           (AUTO-S)
+// api/engine/clipping/_pytree.py:111-157, _streaming.py:84-108), taken from
+// an upper bound of the norm when the squared norm comes with an error bound
+// (ghost norms: sqnorm + sqerr >= ||g||^2):
+//   up = sqrt(max(sq + err, 0));  norm = sqrt(max(sq, 0))
+//   ratio = max(C,0)/up  or  max(R,0)/(up + gamma)               (AUTO-S)
 //   s = ratio * rel - abs;  s = min(1, s) (fixed only; NaN stays NaN)
 //   s = isfinite(s) ? max(s, 0) : 0;  stored as float32.
-// Every step is one IEEE operation in the order written (contraction off), so
-// the result matches a host float64 evaluation bit for bit.
+// `norm` (the estimate) is what the statistics report and count.  Every step
+// is one IEEE operation in the order written (contraction off), so the result
+// matches a host float64 evaluation bit for bit.
 #include "common.h"
 #include "plan.h"
 
@@ -22,10 +26,13 @@ struct Guards {
 };
 
 #pragma clang fp contract(off)
-__device__ double guarded_scale(double sq, double C, int kind, double gamma, double rel,
-                                double abs_, double* norm_out) {
-  double norm = sqrt(sq);
-  *norm_out = norm;
+__device__ double guarded_scale(double sq, double err, double C, int kind, double gamma,
+                                double rel, double abs_, double* norm_out) {
+  const double est = sq < 0.0 ? 0.0 : sq;  // NaN stays NaN
+  *norm_out = sqrt(est);
+  double up = sq + err;
+  up = up < 0.0 ? 0.0 : up;
+  const double norm = sqrt(up);
   double bound = C > 0.0 ? C : 0.0;
   double ratio = (kind == DPC_SCALE_AUTO_S) ? bound / (norm + gamma) : bound / norm;
   double s = ratio * rel;
@@ -36,64 +43,73 @@ __device__ double guarded_scale(double sq, double C, int kind, double gamma, dou
 }
 
 __global__ void __launch_bounds__(kClipThreads)
-clip_factors_kernel(const double* __restrict__ sqnorm, int B, double C, int kind, double gamma,
-                    Guards guards, int n_guards, float count_threshold, float* __restrict__ scale,
+clip_factors_kernel(const double* __restrict__ sqnorm, const double* __restrict__ sqerr, int B,
+                    double C, int kind, double gamma, Guards guards, int n_guards,
+                    float count_threshold, float* __restrict__ scale,
                     float* __restrict__ norms_out, int* __restrict__ nclipped,
-                    void* __restrict__ plan_base) {
-  const bool have_plan = plan_base != nullptr;
-  ClipPlanView plan = clip_plan_view(plan_base, B);
+                    void* __restrict__ plans) {
   __shared__ int wave_counts[kClipThreads / 64];
   __shared__ int clipped_counts[kClipThreads / 64];
   __shared__ int slow_counts[kClipThreads / 64];
   __shared__ int base, base_slow;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int nw = blockDim.x >> 6;
-  if (tid == 0) base = 0;
   int clipped_local = 0;
-  // One pass computes the scales and lists the active examples (see
-  // plan.h): the fast ones from the front of `active` in increasing order,
-  // the others from its back, in increasing order read backwards.  Each list
-  // is an ordered compaction: a ballot within a wave, wave offsets through
-  // LDS.
+  // Guard g's pass computes its scales and lists its active examples in plan
+  // g (see plan.h): the fast ones from the front of `active` in increasing
+  // order, the others from its back, in increasing order read backwards.
+  // Each list is an ordered compaction: a ballot within a wave, wave offsets
+  // through LDS.  The norms and the clipped count come from guard 0's pass.
   const bool fast_ok = (double)B * C <= (double)DPC_FAST_BC_MAX;
-  if (tid == 0) base_slow = 0;
-  for (int start = 0; start < B; start += blockDim.x) {
-    const int i = start + tid;
-    bool fast = false, slow = false;
-    if (i < B) {
-      double norm;
-      float s0 = 0.0f;
-      for (int g = 0; g < n_guards; ++g) {
-        double s = guarded_scale(sqnorm[i], C, kind, gamma, guards.rel[g], guards.abs_[g], &norm);
-        float sf = (float)s;
-        if (scale) scale[(size_t)g * B + i] = sf;
-        if (g == 0) s0 = sf;
-      }
-      if (norms_out) norms_out[i] = (float)norm;
-      if ((float)norm > count_threshold) ++clipped_local;
-      fast = s0 > 0.0f && fast_ok && s0 >= DPC_FAST_SCALE_MIN;
-      slow = s0 > 0.0f && !fast;
-    }
-    const unsigned long long mf = __ballot(fast), ms = __ballot(slow);
-    const unsigned long long below = (1ull << lane) - 1ull;
-    if (lane == 0) {
-      wave_counts[w] = __popcll(mf);
-      slow_counts[w] = __popcll(ms);
-    }
-    __syncthreads();
-    int of = base, os = base_slow;
-    for (int v = 0; v < w; ++v) {
-      of += wave_counts[v];
-      os += slow_counts[v];
-    }
-    if (have_plan && fast) plan.active[of + __popcll(mf & below)] = i;
-    if (have_plan && slow) plan.active[B - 1 - (os + __popcll(ms & below))] = i;
-    __syncthreads();
+  for (int g = 0; g < n_guards; ++g) {
+    const bool have_plan = plans != nullptr;
+    ClipPlanView plan = clip_plan_view((char*)plans + (size_t)g * clip_plan_bytes(B), B);
     if (tid == 0) {
-      for (int v = 0; v < nw; ++v) {
-        base += wave_counts[v];
-        base_slow += slow_counts[v];
+      base = 0;
+      base_slow = 0;
+    }
+    for (int start = 0; start < B; start += blockDim.x) {
+      const int i = start + tid;
+      bool fast = false, slow = false;
+      if (i < B) {
+        double norm;
+        const double s = guarded_scale(sqnorm[i], sqerr ? sqerr[i] : 0.0, C, kind, gamma,
+                                       guards.rel[g], guards.abs_[g], &norm);
+        const float sf = (float)s;
+        if (scale) scale[(size_t)g * B + i] = sf;
+        if (g == 0) {
+          if (norms_out) norms_out[i] = (float)norm;
+          if ((float)norm > count_threshold) ++clipped_local;
+        }
+        fast = sf > 0.0f && fast_ok && sf >= DPC_FAST_SCALE_MIN && sf <= DPC_FAST_SCALE_MAX;
+        slow = sf > 0.0f && !fast;
       }
+      const unsigned long long mf = __ballot(fast), ms = __ballot(slow);
+      const unsigned long long below = (1ull << lane) - 1ull;
+      if (lane == 0) {
+        wave_counts[w] = __popcll(mf);
+        slow_counts[w] = __popcll(ms);
+      }
+      __syncthreads();
+      int of = base, os = base_slow;
+      for (int v = 0; v < w; ++v) {
+        of += wave_counts[v];
+        os += slow_counts[v];
+      }
+      if (have_plan && fast) plan.active[of + __popcll(mf & below)] = i;
+      if (have_plan && slow) plan.active[B - 1 - (os + __popcll(ms & below))] = i;
+      __syncthreads();
+      if (tid == 0) {
+        for (int v = 0; v < nw; ++v) {
+          base += wave_counts[v];
+          base_slow += slow_counts[v];
+        }
+      }
+      __syncthreads();
+    }
+    if (tid == 0 && have_plan) {
+      *plan.nactive = base + base_slow;
+      *plan.nfast = base;
     }
     __syncthreads();
   }
@@ -104,10 +120,6 @@ clip_factors_kernel(const double* __restrict__ sqnorm, int B, double C, int kind
     int total = 0;
     for (int v = 0; v < nw; ++v) total += clipped_counts[v];
     if (nclipped) *nclipped = total;
-    if (have_plan) {
-      *plan.nactive = base + base_slow;
-      *plan.nfast = base;
-    }
   }
 }
 
@@ -115,7 +127,8 @@ clip_factors_kernel(const double* __restrict__ sqnorm, int B, double C, int kind
 
 extern "C" size_t dpc_clip_plan_bytes(int B) { return clip_plan_bytes(B); }
 
-extern "C" int dpc_clip_factors(const double* sqnorm, int B, double C, int kind, double gamma,
+extern "C" int dpc_clip_factors(const double* sqnorm, const double* sqerr, int B, double C,
+                                int kind, double gamma,
                                 const double* guard_rel, const double* guard_abs, int n_guards,
                                 float count_threshold, float* scale, float* norms_out,
                                 int* nclipped, void* plan, void* stream) {
@@ -131,7 +144,7 @@ extern "C" int dpc_clip_factors(const double* sqnorm, int B, double C, int kind,
     guards.abs_[g] = guard_abs[g];
   }
   hipLaunchKernelGGL(clip_factors_kernel, dim3(1), dim3(kClipThreads), 0, (hipStream_t)stream,
-                     sqnorm, B, C, kind, gamma, guards, n_guards, count_threshold,
+                     sqnorm, sqerr, B, C, kind, gamma, guards, n_guards, count_threshold,
                      scale, norms_out, nclipped, plan);
   DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;

@@ -135,6 +135,91 @@ DPC_HOST_DEVICE float finite_or_zero(float x) {
 
 DPC_HOST_DEVICE int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// ---------------------------------------------------------------------------
+// Error model of the Gram-norm kernels (the bound that makes the ghost clip
+// sound: the clip factor is taken from sqnorm + sqerr >= ||G_i^T A_i||^2).
+//
+// A Gram entry P_st = sum_k a_sk a_tk (n products, zero-padded to the K step)
+// is accumulated in a chain of fp32 MFMA instructions, each adding 16 exact
+// bf16 products to the accumulator.  Model: one instruction returns its 17
+// addends' sum with an error of at most 17 * 2^-23 * (sum of their
+// magnitudes) -- this covers round-to-nearest, truncation, and an aligned
+// fused addition that drops bits below the largest addend's ulp -- and each
+// product or partial below the fp32 normal range may be flushed (an absolute
+// error of at most 2^-126 each).  Then
+//   |P^_st - P_st| <= gamma(n) sum_k |a_sk a_tk| + eta(n)
+//                  <= gamma(n) ||a_s|| ||a_t|| + eta(n)       (Cauchy-Schwarz)
+// with gamma(n) = g / (1 - g), g = (18/16) n u (u = 2^-23, one extra addend
+// of slack), eta(n) = n 2^-125.  Since eta(n) <= gamma(n) 2^-102,
+//   gamma ||a_s|| ||a_t|| + eta <= gamma (||a_s|| + c)(||a_t|| + c),  c = 2^-51,
+// so the row weights w_s = ||a_s|| + c carry the absolute term.  The generic
+// (FMA) Gram kernels accumulate in fp64: products of fp32 values are exact
+// there and never underflow, so the same form holds with u = 2^-52, eta = c = 0.
+// Row norms come from the computed diagonal: P^_ss >= (1 - gamma) P_ss - eta.
+// ---------------------------------------------------------------------------
+#define DPC_GRAM_U_MFMA 0x1.0p-23
+#define DPC_GRAM_U_FP64 0x1.0p-52
+#define DPC_GRAM_ROW_SLACK_MFMA 0x1.0p-51
+
+DPC_HOST_DEVICE double dpc_chain_gamma(double n, double u) {
+  const double g = 1.125 * n * u;
+  if (!(g < 0.5)) return __builtin_inf();  // no useful bound: the clip factor becomes 0
+  return g / (1.0 - g) * (1.0 + 0x1.0p-40);
+}
+
+// Upper bound of ||a_s|| + slack from a computed diagonal Gram entry.
+DPC_HOST_DEVICE double dpc_row_bound(double diag, double gamma, double eta, double slack) {
+  const double inv = (1.0 + 0x1.0p-50) / (1.0 - gamma);
+  return sqrt((fabs(diag) + eta) * inv) * (1.0 + 0x1.0p-50) + slack;
+}
+
+// Per-tile record of a Gram work item (float64, kGramRecWords words):
+//   [0] inner  <P^, Q^> over the tile (x2 for an off-diagonal pair)
+//   [1] FP     sum of P^_st^2 over the tile's entries with s != t
+//   [2] FQ     sum of Q^_st^2 over the same entries
+//   [3] XD     sum_s w_s^2 |Q^_ss|   } diagonal pairs only (0 otherwise);
+//   [4] YD     sum_s v_s^2 |P^_ss|   } w_s / v_s: row weights of the P / Q
+//   [5] W2     sum_s w_s^2           } operands over the block's rows
+//   [6] V2     sum_s v_s^2           }
+//   [7] gamma of P's chain, [8] gamma of Q's chain, [9] rows of the example
+//       or segment (T), [10..11] zero.
+// P is the Gram matrix of the narrower operand (d_lo), Q of the wider one.
+#define DPC_GRAM_REC_WORDS 12
+
+// Per-example bound from the records of one example / segment (nt row
+// blocks, pair index q (q + 1) / 2 + p for p <= q, records rec[pair]).
+// Returns the inner product folded in pair order through *sum and the error
+// bound; see the model above:
+//   |S - ||g||^2| <= gA X + gQ Y + (gA gQ + g64 (1 + gA)(1 + gQ)) W2 V2
+//   X = sum_p XD_p + sum_p W2_p ||Q^_pp,off||_F + 2 sum_{p<q} ||w_p|| ||w_q|| ||Q^_pq||_F
+//   Y likewise with V2 and P^,  g64 = (T^2 + 256) 2^-52 for the fp64 sums.
+DPC_HOST_DEVICE double dpc_gram_bound(const double* rec, int nt, double* sum) {
+  double s = 0.0, X = 0.0, Y = 0.0, W2 = 0.0, V2 = 0.0;
+  const int np = nt * (nt + 1) / 2;
+  for (int j = 0; j < np; ++j) s += rec[(size_t)j * DPC_GRAM_REC_WORDS];
+  *sum = s;
+  for (int q = 0; q < nt; ++q) {
+    const double* dq = rec + (size_t)(q * (q + 3) / 2) * DPC_GRAM_REC_WORDS;
+    W2 += dq[5];
+    V2 += dq[6];
+    for (int p = 0; p <= q; ++p) {
+      const double* r = rec + (size_t)(q * (q + 1) / 2 + p) * DPC_GRAM_REC_WORDS;
+      if (p == q) {
+        X += r[3] + r[5] * sqrt(r[2]);
+        Y += r[4] + r[6] * sqrt(r[1]);
+      } else {
+        const double* dp = rec + (size_t)(p * (p + 3) / 2) * DPC_GRAM_REC_WORDS;
+        X += 2.0 * sqrt(dp[5] * dq[5] * r[2]);
+        Y += 2.0 * sqrt(dp[6] * dq[6] * r[1]);
+      }
+    }
+  }
+  const double gA = rec[7], gQ = rec[8], T = rec[9];
+  const double g64 = (T * T + 256.0) * 0x1.0p-52;
+  const double err = gA * X + gQ * Y + (gA * gQ + g64 * (1.0 + gA) * (1.0 + gQ)) * W2 * V2;
+  return err * (1.0 + 0x1.0p-40);
+}
+
 // Remembers the last failing HIP status of the calling thread (abi.hip).
 void dpc_record_error(hipError_t e);
 

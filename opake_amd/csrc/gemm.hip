@@ -18,11 +18,15 @@
 //     example's scale and are multiplied by scale_prev / scale_next where the
 //     example changes (the clip plan lists first the examples for which this
 //     stays far inside fp32, see plan.h; the others are summed after the
-//     loop with G scaled in fp32 and rounded to bf16 once before the
-//     product).  Grouped mode stages G through registers, multiplied by its
-//     segment's scale in fp32 and rounded to bf16 once (v_cvt_pk_bf16_f32,
-//     round-to-nearest-even).  Examples with scale 0 are skipped through the
-//     clip plan, so their data (including any NaN/Inf) is never read;
+//     loop).  Grouped mode, and the plan's other examples, stage G through
+//     registers, multiplied by the power of two of the step's scale
+//     s = m 2^e (m in [1, 2)), which is exact, and apply the mantissa m to
+//     the accumulators in the same way (they hold the partial sum divided by
+//     the current m, rescaled by m_prev / m_next where it changes).  So no
+//     operand is ever rounded: each example's contribution is the fp32 sum of
+//     the exact products of the given bf16 values, times its scale.
+//     Examples with scale 0 are skipped through the clip plan, so their data
+//     (including any NaN/Inf) is never read;
 //   * two LDS stages (128 KiB), one barrier per K step; the DMAs of step
 //     s + 1 are issued at the start of step s (grouped mode: the scale +
 //     store of G's step s + 1 is interleaved, chunk by chunk, with the MFMAs
@@ -155,7 +159,20 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 
-// 8 bf16 multiplied by `s` in fp32, rounded to bf16 (RNE) once.
+// A positive finite scale s = m 2^e with m in [1, 2): the mantissa m and the
+// power of two 2^e (both exact; 2^e is subnormal below 2^-126).
+__device__ __forceinline__ float scale_mantissa(float s) {
+  int e;
+  return 2.0f * frexpf(s, &e);
+}
+__device__ __forceinline__ float scale_pow2(float s) {
+  int e;
+  (void)frexpf(s, &e);
+  return ldexpf(1.0f, e - 1);
+}
+
+// 8 bf16 multiplied by `s` in fp32, rounded to bf16 (RNE) once; exact when s
+// is a power of two (barring results below the normal range).
 __device__ __forceinline__ u32x4_t scale_chunk(u32x4_t x, float s) {
   u32x4_t o;
 #pragma unroll
@@ -526,10 +543,15 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       }
     };
     Frags fa, fb;
-    // Dense mode: the accumulators hold the partial sum divided by the scale
-    // of the step whose MFMAs run (sc_cur); when the next step belongs to an
-    // example with another scale they are multiplied by sc_cur / sc_next.
+    // The accumulators hold the partial sum divided by the accumulator factor
+    // of the step whose MFMAs run (sc_cur): dense mode, the example's scale;
+    // grouped mode, the mantissa of the segment's scale (its power of two
+    // multiplies G).  When the next step's factor differs they are multiplied
+    // by sc_cur / sc_next.
     float sc_cur = 0.0f;
+    auto acc_factor = [&](float sc) __attribute__((always_inline)) {
+      return kGrouped ? scale_mantissa(sc) : sc;
+    };
     auto rescale = [&](float r) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -538,7 +560,8 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     };
     auto k_step = [&](int s, const uint8_t* gcur, const uint8_t* acur, uint8_t* gnxt,
                       uint8_t* anxt) __attribute__((always_inline)) {
-      const float sc_s1 = sc_next;  // scale of step s + 1
+      const float sc_s1 = acc_factor(sc_next);  // accumulator factor of step s + 1
+      const float g_next = kGrouped ? scale_pow2(sc_next) : 1.0f;  // G factor of step s + 1
       dma_a(anxt, row_next, valid_next);
       if constexpr (!kGrouped) dma_g(gnxt, row_next);
       float sc_after;
@@ -550,7 +573,7 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       auto stage_g = [&](int kk) __attribute__((always_inline)) {
         if constexpr (kGrouped) {
 #pragma unroll
-          for (int c = 0; c < kGCSub; ++c) store_chunk(gnxt, kk * kGCSub + c, sc_next);
+          for (int c = 0; c < kGCSub; ++c) store_chunk(gnxt, kk * kGCSub + c, g_next);
 #pragma unroll
           for (int c = 0; c < kGCSub; ++c) load_chunk(row2, valid2, kk * kGCSub + c);
         }
@@ -585,11 +608,9 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       if (vcur > 48) mma(fb);
       interleave();
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (!kGrouped) {
-        if (s + 1 < nsteps && sc_s1 != sc_cur) {
-          rescale(sc_cur / sc_s1);
-          sc_cur = sc_s1;
-        }
+      if (s + 1 < nsteps && sc_s1 != sc_cur) {
+        rescale(sc_cur / sc_s1);
+        sc_cur = sc_s1;
       }
     };
 
@@ -602,13 +623,14 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       int valid0;
       int row0 = step_row0(0, &sc_next, &valid0);
       valid_cur = valid0;
-      sc_cur = sc_next;
+      sc_cur = acc_factor(sc_next);
       dma_a(lds_a0, row0, valid0);
       if constexpr (kGrouped) {
+        const float g0f = scale_pow2(sc_next);
 #pragma unroll
         for (int j = 0; j < kGC; ++j) load_chunk(row0, valid0, j);
 #pragma unroll
-        for (int j = 0; j < kGC; ++j) store_chunk(g0, j, sc_next);
+        for (int j = 0; j < kGC; ++j) store_chunk(g0, j, g0f);
       } else {
         dma_g(g0, row0);
       }
@@ -626,24 +648,33 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
         k_step(s + 1, g1, lds_a1, g0, lds_a0);
       }
       if (s < nsteps) k_step(s, g0, lds_a0, g1, lds_a1);
-      if constexpr (!kGrouped) rescale(sc_cur);
+      rescale(sc_cur);
       DPC_WAIT_VMCNT(0);
       __syncthreads();
     }
-    // Dense mode, examples whose scale is too small to divide the
-    // accumulators by (the plan's back list; split 0 takes them): G is scaled in fp32 and rounded to bf16 before the product, one
-    // unpipelined K step at a time.
+    // Dense mode, examples whose scale the accumulators cannot be divided by
+    // (the plan's back list; split 0 takes them), one unpipelined K step at a
+    // time: G is multiplied by the power of two of the scale (exact) and the
+    // accumulators carry the mantissa, as in grouped mode (after the loop
+    // above they hold the finished sum, factor 1).
     if constexpr (!kGrouped) {
       const int nslow = split == 0 ? (nactive - nfast) * spe : 0;
+      float m_cur = 1.0f;
       for (int t = 0; t < nslow; ++t) {
         const int ex = plan.active[args.B - 1 - t / spe];
         const float sc = args.scale[ex];
+        const float m = scale_mantissa(sc);
+        if (m != m_cur) {
+          rescale(m_cur / m);
+          m_cur = m;
+        }
         const int rs = ex * T + (t % spe) * kBK;
         dma_a(lds_a0, rs, kBK);
 #pragma unroll
         for (int j = 0; j < kGC; ++j) load_chunk(rs, kBK, j);
+        const float p2 = scale_pow2(sc);
 #pragma unroll
-        for (int j = 0; j < kGC; ++j) store_chunk(g0, j, sc);
+        for (int j = 0; j < kGC; ++j) store_chunk(g0, j, p2);
         DPC_WAIT_VMCNT(0);
         __syncthreads();
 #pragma unroll
@@ -653,6 +684,7 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
         }
         __syncthreads();
       }
+      if (m_cur != 1.0f) rescale(m_cur);
     }
   }
 
@@ -752,8 +784,12 @@ int fast_splits(int B, int T, int din, int dout) {
 
 #undef DPC_WAIT_VMCNT
 
-// Generic path: any T, float32 or bf16 operands, scale applied to the G
-// operand in fp32; 64 x 64 tiles with a 4 x 4 FMA block per thread.
+// Generic path: any T, float32 or bf16 operands; 64 x 64 tiles with a 4 x 4
+// FMA block per thread.  K is walked in chunks of at most 16 rows that never
+// straddle two examples: G is staged multiplied by the power of two of its
+// example's scale (exact) and the accumulators carry the mantissa (they hold
+// the partial sum divided by the current mantissa, rescaled where it
+// changes), so no operand is rounded; examples with scale 0 are skipped.
 constexpr int kGT = 64, kGK = 16;
 
 template <typename In>
@@ -762,6 +798,49 @@ template <>
 __device__ __forceinline__ float to_f32<float>(float v) { return v; }
 template <>
 __device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) { return bf16_bits_to_f32(v); }
+
+// Stages rows [k0, k0 + rows) (rows <= kGK; the rest zero) of G (times p2)
+// and A for the 64 x 64 tile (m0, n0), then adds their products to acc.
+template <typename In>
+__device__ __forceinline__ void generic_chunk(const In* __restrict__ A, const In* __restrict__ G,
+                                              long long k0, int rows, float p2, int M, int N,
+                                              int m0, int n0, float (*sg)[kGT + 1],
+                                              float (*sa)[kGT + 1], float acc[4][4]) {
+  const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
+  for (int e = tid; e < kGK * kGT; e += kThreads) {
+    const int k = e / kGT, col = e % kGT;
+    float gv = 0.f, av = 0.f;
+    if (k < rows) {
+      const long long kk = k0 + k;
+      if (m0 + col < M) gv = p2 * to_f32<In>(G[kk * M + m0 + col]);
+      if (n0 + col < N) av = to_f32<In>(A[kk * N + n0 + col]);
+    }
+    sg[k][col] = gv;
+    sa[k][col] = av;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kGK; ++k) {
+    float a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[i] = sg[k][tr * 4 + i];
+      b[i] = sa[k][tc * 4 + i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ void generic_rescale(float acc[4][4], float r) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] *= r;
+}
 
 // Split-K (splits > 1, M and N even): workgroup z sums the K range
 // [z * per, (z + 1) * per) and writes its raw fp32 tile to partial[z]
@@ -785,37 +864,26 @@ clipped_sum_generic_kernel(const In* __restrict__ A, const In* __restrict__ G,
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
-  for (long long k0 = kb; k0 < ke; k0 += kGK) {
-    for (int e = tid; e < kGK * kGT; e += kThreads) {
-      const int k = e / kGT, col = e % kGT;
-      const long long kk = k0 + k;
-      float gv = 0.f, av = 0.f;
-      if (kk < ke) {
-        const float s = scale[kk / T];
-        if (s > 0.0f) {
-          if (m0 + col < M) gv = s * to_f32<In>(G[kk * M + m0 + col]);
-          if (n0 + col < N) av = to_f32<In>(A[kk * N + n0 + col]);
-        }
-      }
-      sg[k][col] = gv;
-      sa[k][col] = av;
+  float m_cur = 1.0f;
+  for (long long k0 = kb; k0 < ke;) {
+    const long long ex = k0 / T, ex_end = (ex + 1) * T;
+    const float s = scale[ex];  // uniform over the workgroup
+    if (!(s > 0.0f)) {
+      k0 = ex_end < ke ? ex_end : ke;
+      continue;
     }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < kGK; ++k) {
-      float a[4], b[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a[i] = sg[k][tr * 4 + i];
-        b[i] = sa[k][tc * 4 + i];
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    long long k1 = k0 + kGK;
+    k1 = k1 < ke ? k1 : ke;
+    k1 = k1 < ex_end ? k1 : ex_end;
+    const float m = scale_mantissa(s);
+    if (m != m_cur) {
+      generic_rescale(acc, m_cur / m);
+      m_cur = m;
     }
-    __syncthreads();
+    generic_chunk<In>(A, G, k0, (int)(k1 - k0), scale_pow2(s), M, N, m0, n0, sg, sa, acc);
+    k0 = k1;
   }
+  generic_rescale(acc, m_cur);
   if (splits > 1) {
     float* part = partial + (size_t)blockIdx.z * M * N;
 #pragma unroll
@@ -888,7 +956,9 @@ bias_finish_kernel(const float* __restrict__ partial, int nsplit, Epilogue ep) {
 }
 
 // Grouped generic path (float32, or bf16 of any shape): problem blockIdx.z,
-// 64 x 64 output tiles, the steps of the problem walked row by row.
+// 64 x 64 output tiles, the steps of the problem walked in chunks of 16
+// rows, G times the power of two of the step's segment scale and the
+// mantissa on the accumulators (as in clipped_sum_generic_kernel).
 template <typename In>
 __global__ void __launch_bounds__(kThreads)
 grouped_generic_kernel(GroupedTables grp, Epilogue ep0) {
@@ -910,41 +980,24 @@ grouped_generic_kernel(GroupedTables grp, Epilogue ep0) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+  float m_cur = 1.0f;
   const int s0 = grp.step_start[e], s1 = grp.step_start[e + 1];
   for (int st = s0; st < s1; ++st) {
     const int row0 = grp.steps[2 * st];
     const int pack = grp.steps[2 * st + 1];
     const int valid = pack & 127;
-    const float sc = grp.seg_scale[pack >> 7];
-    for (int k0 = 0; k0 < valid; k0 += kGK) {
-      for (int x = tid; x < kGK * kGT; x += kThreads) {
-        const int k = x / kGT, col = x % kGT;
-        float gv = 0.f, av = 0.f;
-        if (k0 + k < valid) {
-          const size_t row = (size_t)(row0 + k0 + k);
-          if (m0 + col < M) gv = sc * to_f32<In>(G[row * M + m0 + col]);
-          if (n0 + col < N) av = to_f32<In>(A[row * N + n0 + col]);
-        }
-        sg[k][col] = gv;
-        sa[k][col] = av;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int k = 0; k < kGK; ++k) {
-        float a[4], b[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          a[i] = sg[k][tr * 4 + i];
-          b[i] = sa[k][tc * 4 + i];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
-      }
-      __syncthreads();
+    const float sc = grp.seg_scale[pack >> 7];  // > 0: the plan lists no other segment
+    const float m = scale_mantissa(sc);
+    if (m != m_cur) {
+      generic_rescale(acc, m_cur / m);
+      m_cur = m;
     }
+    const float p2 = scale_pow2(sc);
+    for (int k0 = 0; k0 < valid; k0 += kGK)
+      generic_chunk<In>(A, G, (long long)row0 + k0, min(kGK, valid - k0), p2, M, N, m0, n0, sg,
+                        sa, acc);
   }
+  generic_rescale(acc, m_cur);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int n = n0 + tc * 4 + j;

@@ -1,13 +1,18 @@
 // Per-example squared gradient norms of linear layers via the Gram identity
 //   ||G_i^T A_i||_F^2 = <A_i A_i^T, G_i G_i^T>
-// (no per-example gradient is ever formed).  The T x T Gram matrices are
-// split into 128 x 128 tiles; a workgroup of 4 waves owns one (example, tile
-// pair p <= q) and computes the (p, q) tile of both A A^T and G G^T with bf16
-// MFMA and fp32 accumulators.  Each wave holds the same 64 x 64 block of both
-// tiles, so the element-wise inner product (fp64) needs no data exchange.
-// Pairs with p < q count twice (both Gram matrices are symmetric).  One fp64
-// partial per (example, pair) lands in the workspace; dpc_row_sum_f64 folds
-// them into sqnorm in a fixed order, so results are deterministic.
+// (no per-example gradient is ever formed), with an upper bound on the
+// rounding error of the result, so that the clip factor can be taken from
+// sqnorm + sqerr >= ||G_i^T A_i||^2 (the error model is in common.h).  The
+// T x T Gram matrices are split into 128 x 128 tiles; a workgroup of 4 waves
+// owns one (example, tile pair p <= q) and computes the (p, q) tile of both
+// A A^T and G G^T with bf16 MFMA and fp32 accumulators.  Each wave holds the
+// same 64 x 64 block of both tiles, so the element-wise inner product (fp64)
+// needs no data exchange.  Pairs with p < q count twice (both Gram matrices
+// are symmetric).  Each (example, pair) writes a record to the workspace --
+// the inner product, the squared off-diagonal entries of both tiles and, on
+// diagonal pairs, row weights from the diagonal entries -- and
+// gram_finish_kernel folds an example's records in a fixed order into sqnorm
+// and sqerr, so results are deterministic.
 //
 // Two workgroups fit on a CU (64 KiB of LDS, <= 256 registers per lane at 2
 // waves per SIMD), so the 10 pairs x B examples of a typical call are all
@@ -63,6 +68,53 @@ __device__ __forceinline__ double block_sum_f64(double v, double* red) {
     for (int i = 0; i < (int)(blockDim.x >> 6); ++i) total += red[i];
   }
   return total;
+}
+
+// Record words 0..6 of a Gram work item, summed over the workgroup in a fixed
+// order (lanes by shuffle tree, then waves), written with the gammas and the
+// row count: see DPC_GRAM_REC_WORDS.  red: kRecStat * waves doubles of LDS.
+constexpr int kRecStat = 7;
+__device__ __forceinline__ void write_gram_record(double (&v)[kRecStat], double* red,
+                                                  double* rec, double gA, double gQ, int T) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int nw = (int)(blockDim.x >> 6);
+#pragma unroll
+  for (int k = 0; k < kRecStat; ++k)
+    for (int off = 32; off > 0; off >>= 1) v[k] += __shfl_down(v[k], off, 64);
+  __syncthreads();
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < kRecStat; ++k) red[w * kRecStat + k] = v[k];
+  }
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < kRecStat) {
+    double total = 0.0;
+    for (int i = 0; i < nw; ++i) total += red[i * kRecStat + t];
+    rec[t] = total;
+  } else if (t < DPC_GRAM_REC_WORDS) {
+    rec[t] = t == 7 ? gA : t == 8 ? gQ : t == 9 ? (double)T : 0.0;
+  }
+}
+
+// Adds a computed Gram entry pair (a of P, g of Q) to the record statistics;
+// `on_diag` marks an entry with s == t, whose row weights (ws, vs) enter
+// words 3..6 instead of the off-diagonal sums.
+__device__ __forceinline__ void gram_entry_stats(double a, double g, bool on_diag, double gA,
+                                                 double etaA, double gQ, double etaQ,
+                                                 double slack, double (&v)[kRecStat]) {
+  v[0] += a * g;
+  if (on_diag) {
+    const double ws = dpc_row_bound(a, gA, etaA, slack);
+    const double vs = dpc_row_bound(g, gQ, etaQ, slack);
+    v[3] += ws * ws * fabs(g);
+    v[4] += vs * vs * fabs(a);
+    v[5] += ws * ws;
+    v[6] += vs * vs;
+  } else {
+    v[1] += a * a;
+    v[2] += g * g;
+  }
 }
 
 // Linear workgroup id -> logical (example, pair) index so that each XCD
@@ -211,10 +263,10 @@ __device__ __forceinline__ int dense_item(int pos, int L0, int n, int npairs, in
 template <bool kGrouped>
 __global__ void __launch_bounds__(kGramMfmaThreads, 2)
 gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ G, int T,
-                      int din, int dout, int npairs, int nblocks, double* __restrict__ partial,
+                      int din, int dout, int npairs, int nblocks, double* __restrict__ records,
                       GramItems work, int xcd_cus) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kGStageBytes];
-  __shared__ double red[kGramMfmaThreads / 64];
+  __shared__ double red[kRecStat * (kGramMfmaThreads / 64)];
   int l = xcd_logical_block(gridDim.x, nblocks);
   if (l < 0) return;  // padding workgroup: exits before any barrier
   if (!kGrouped) {
@@ -396,21 +448,57 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
   }
   if (s < nkg) step_g(s, R[1]);
 
-  // Both tiles share the MFMA output layout, so the element-wise product
-  // needs no knowledge of which (s, t) a register holds.
-  double sum = 0.0;
+  // The tile record.  Both tiles share the MFMA output layout, so the
+  // element-wise product needs no knowledge of which (s, t) a register holds;
+  // a diagonal entry (s == t) sits in a wave on the tile's diagonal
+  // (diagonal pair, wr == wc), block i == j, at the accumulator r with
+  // (r >> 2) * 8 + 4 (lane >> 5) + (r & 3) == lane & 31 -- one per block and
+  // lane.  After the swap above, pa is the Gram matrix of the narrower
+  // operand.
+  {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const bool diag_wave = diag && (w >> 1) == (w & 1);
+    double st[kRecStat] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+    float da[2] = {0.0f, 0.0f}, dg[2] = {0.0f, 0.0f};
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sum += (double)pa[i][j][r] * (double)pg[i][j][r];
-  double total = block_sum_f64(sum, red);
-  if (threadIdx.x == 0) partial[slot] = diag ? total : 2.0 * total;  // dense: slot = ex * npairs + pair
+        for (int r = 0; r < 16; ++r) {
+          const double a = pa[i][j][r], g = pg[i][j][r];
+          st[0] += a * g;
+          const bool on_diag = i == j && diag_wave &&
+                               ((r >> 2) * 8 + 4 * (lane >> 5) + (r & 3)) == (lane & 31);
+          st[1] += on_diag ? 0.0 : a * a;
+          st[2] += on_diag ? 0.0 : g * g;
+          if (i == j) {
+            da[i] = on_diag ? pa[i][j][r] : da[i];
+            dg[i] = on_diag ? pg[i][j][r] : dg[i];
+          }
+        }
+    if (!diag) st[0] *= 2.0;  // exact: the off-diagonal pair counts twice
+    const double gA = dpc_chain_gamma((double)nka * kGK, DPC_GRAM_U_MFMA);
+    const double gQ = dpc_chain_gamma((double)nkg * kGK, DPC_GRAM_U_MFMA);
+    if (diag_wave) {
+      const double etaA = (double)nka * kGK * 0x1.0p-125, etaQ = (double)nkg * kGK * 0x1.0p-125;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const double ws = dpc_row_bound(da[i], gA, etaA, DPC_GRAM_ROW_SLACK_MFMA);
+        const double vs = dpc_row_bound(dg[i], gQ, etaQ, DPC_GRAM_ROW_SLACK_MFMA);
+        st[3] += ws * ws * fabs((double)dg[i]);
+        st[4] += vs * vs * fabs((double)da[i]);
+        st[5] += ws * ws;
+        st[6] += vs * vs;
+      }
+    }
+    write_gram_record(st, red, records + (size_t)slot * DPC_GRAM_REC_WORDS, gA, gQ, T);
+  }
 }
 
 // Generic path (float32 inputs, or bf16 with d % 8 != 0): 64 x 64 tiles,
-// FMA on fp32 with a 4 x 4 register block per thread.
+// fp64 FMA with a 4 x 4 register block per thread (products of fp32 values
+// are exact in fp64, so the Gram entries carry only fp64 summation error).
 constexpr int kGenTile = 64;
 constexpr int kGenK = 16;
 
@@ -426,12 +514,12 @@ __device__ __forceinline__ float load_as_f32<uint16_t>(const uint16_t* p) {
 template <typename In>
 __device__ void gram_tile_generic(const In* __restrict__ X, int T, int d, int p, int q,
                                   float (*sp)[kGenTile + 1], float (*sq)[kGenTile + 1],
-                                  float acc[4][4]) {
+                                  double acc[4][4]) {
   const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
   for (int k0 = 0; k0 < d; k0 += kGenK) {
     for (int e = tid; e < kGenTile * kGenK; e += kGramThreads) {
       int r = e / kGenK, k = e % kGenK;
@@ -442,7 +530,7 @@ __device__ void gram_tile_generic(const In* __restrict__ X, int T, int d, int p,
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < kGenK; ++k) {
-      float a[4], b[4];
+      double a[4], b[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         a[i] = sp[k][tr * 4 + i];
@@ -451,42 +539,57 @@ __device__ void gram_tile_generic(const In* __restrict__ X, int T, int d, int p,
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < 4; ++j) acc[i][j] = fma(a[i], b[j], acc[i][j]);
     }
     __syncthreads();
   }
 }
 
-template <typename In>
-__global__ void __launch_bounds__(kGramThreads)
-gram_generic_kernel(const In* __restrict__ A, const In* __restrict__ G, int T, int din, int dout,
-                    int npairs, double* __restrict__ partial) {
-  __shared__ float sp[kGenK][kGenTile + 1];
-  __shared__ float sq[kGenK][kGenTile + 1];
-  __shared__ double red[kGramThreads / 64];
-  const int pair = blockIdx.x, ex = blockIdx.y;
-  int p, q;
-  pair_from_index(pair, &p, &q);
-  float pa[4][4], pg[4][4];
-  gram_tile_generic<In>(A + (size_t)ex * T * din, T, din, p, q, sp, sq, pa);
-  gram_tile_generic<In>(G + (size_t)ex * T * dout, T, dout, p, q, sp, sq, pg);
-  double s = 0.0;
+// Record statistics of one 64 x 64 generic sub-tile (p, q): thread (tr, tc)
+// holds rows tr * 4 + i, columns tc * 4 + j, so the diagonal entries of a
+// diagonal sub-tile are those with tr == tc and i == j.
+__device__ __forceinline__ void generic_tile_stats(const double pa[4][4], const double pg[4][4],
+                                                   bool diag_tile, double gA, double gQ,
+                                                   double (&st)[kRecStat]) {
+  const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) s += (double)pa[i][j] * (double)pg[i][j];
-  double total = block_sum_f64(s, red);
-  if (threadIdx.x == 0) partial[(size_t)ex * npairs + pair] = (p == q) ? total : 2.0 * total;
+    for (int j = 0; j < 4; ++j)
+      gram_entry_stats(pa[i][j], pg[i][j], diag_tile && tr == tc && i == j, gA, 0.0, gQ, 0.0,
+                       0.0, st);
+}
+
+template <typename In>
+__global__ void __launch_bounds__(kGramThreads)
+gram_generic_kernel(const In* __restrict__ A, const In* __restrict__ G, int T, int din, int dout,
+                    int npairs, double* __restrict__ records) {
+  __shared__ float sp[kGenK][kGenTile + 1];
+  __shared__ float sq[kGenK][kGenTile + 1];
+  __shared__ double red[kRecStat * (kGramThreads / 64)];
+  const int pair = blockIdx.x, ex = blockIdx.y;
+  int p, q;
+  pair_from_index(pair, &p, &q);
+  double pa[4][4], pg[4][4];
+  gram_tile_generic<In>(A + (size_t)ex * T * din, T, din, p, q, sp, sq, pa);
+  gram_tile_generic<In>(G + (size_t)ex * T * dout, T, dout, p, q, sp, sq, pg);
+  const double gA = dpc_chain_gamma((double)ceil_div(din, kGenK) * kGenK, DPC_GRAM_U_FP64);
+  const double gQ = dpc_chain_gamma((double)ceil_div(dout, kGenK) * kGenK, DPC_GRAM_U_FP64);
+  double st[kRecStat] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+  generic_tile_stats(pa, pg, p == q, gA, gQ, st);
+  if (p != q) st[0] *= 2.0;
+  write_gram_record(st, red, records + ((size_t)ex * npairs + pair) * DPC_GRAM_REC_WORDS, gA, gQ,
+                    T);
 }
 
 // Grouped generic path: one 128-row tile pair (P, Q) as its four 64-row
-// sub-tile pairs; the inner products of the sub-tiles add up to the pair's.
+// sub-tile pairs; the record statistics of the sub-tiles add up to the pair's.
 template <typename In>
 __global__ void __launch_bounds__(kGramThreads)
-gram_grouped_generic_kernel(GramItems work, double* __restrict__ partial) {
+gram_grouped_generic_kernel(GramItems work, double* __restrict__ records) {
   __shared__ float sp[kGenK][kGenTile + 1];
   __shared__ float sq[kGenK][kGenTile + 1];
-  __shared__ double red[kGramThreads / 64];
+  __shared__ double red[kRecStat * (kGramThreads / 64)];
   const int l = blockIdx.x;
   const int32_t* it = work.items + 4 * (size_t)l;
   if (it[0] < 0) return;  // empty item
@@ -496,38 +599,69 @@ gram_grouped_generic_kernel(GramItems work, double* __restrict__ partial) {
   const int din = work.din[problem], dout = work.dout[problem];
   const In* Xa = reinterpret_cast<const In*>(work.a_ptrs[problem]) + (size_t)row0 * din;
   const In* Xg = reinterpret_cast<const In*>(work.g_ptrs[problem]) + (size_t)row0 * dout;
-  double s = 0.0;
+  const double gA = dpc_chain_gamma((double)ceil_div(din, kGenK) * kGenK, DPC_GRAM_U_FP64);
+  const double gQ = dpc_chain_gamma((double)ceil_div(dout, kGenK) * kGenK, DPC_GRAM_U_FP64);
+  double st[kRecStat] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
   for (int sub = 0; sub < 4; ++sub) {
     const int p = 2 * P + (sub >> 1), q = 2 * Q + (sub & 1);
-    float pa[4][4], pg[4][4];
+    double pa[4][4], pg[4][4];
     gram_tile_generic<In>(Xa, rows, din, p, q, sp, sq, pa);
     gram_tile_generic<In>(Xg, rows, dout, p, q, sp, sq, pg);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) s += (double)pa[i][j] * (double)pg[i][j];
+    generic_tile_stats(pa, pg, p == q, gA, gQ, st);
   }
-  double total = block_sum_f64(s, red);
-  if (threadIdx.x == 0) partial[slot] = (P == Q) ? total : 2.0 * total;
+  if (P != Q) st[0] *= 2.0;
+  write_gram_record(st, red, records + (size_t)slot * DPC_GRAM_REC_WORDS, gA, gQ, rows);
 }
 
-// seg_sq[v] = sum of the partials of segment v's items (fixed order).
+// Dense finish: sqnorm[b] (+)= the fold of example b's record inner products
+// in pair order (+ the bias term), sqerr[b] (+)= its error bound (+ the bias
+// term's).  bias (nullable): [B] squared norms then [B] error bounds.
 __global__ void __launch_bounds__(kGramThreads)
-segment_fold_kernel(const double* __restrict__ partial, const int32_t* __restrict__ item_start,
-                    int S, double* __restrict__ seg_sq) {
+gram_finish_kernel(const double* __restrict__ records, int B, int nt, int accumulate,
+                   const double* __restrict__ bias, double* __restrict__ sqnorm,
+                   double* __restrict__ sqerr) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const size_t np = (size_t)nt * (nt + 1) / 2;
+  double s;
+  const double e = dpc_gram_bound(records + (size_t)b * np * DPC_GRAM_REC_WORDS, nt, &s);
+  double v = accumulate ? sqnorm[b] + s : s;
+  if (bias) v = v + bias[b];
+  sqnorm[b] = v;
+  if (sqerr) {
+    double ev = accumulate ? sqerr[b] + e : e;
+    if (bias) ev = ev + bias[B + b];
+    sqerr[b] = ev;
+  }
+}
+
+// Grouped finish: seg_sq[v] / seg_err[v] (nullable) from segment v's records
+// (slots item_start[v] .. item_start[v + 1] - 1, in pair order).
+__global__ void __launch_bounds__(kGramThreads)
+segment_finish_kernel(const double* __restrict__ records, const int32_t* __restrict__ item_start,
+                      int S, double* __restrict__ seg_sq, double* __restrict__ seg_err) {
   const int v = blockIdx.x * blockDim.x + threadIdx.x;
   if (v >= S) return;
-  double s = 0.0;
-  for (int i = item_start[v]; i < item_start[v + 1]; ++i) s += partial[i];
+  const int first = item_start[v], np = item_start[v + 1] - first;
+  double s = 0.0, e = 0.0;
+  if (np > 0) {
+    int nt = 0;
+    while ((nt + 1) * (nt + 2) / 2 <= np) ++nt;
+    e = dpc_gram_bound(records + (size_t)first * DPC_GRAM_REC_WORDS, nt, &s);
+  }
   seg_sq[v] = s;
+  if (seg_err) seg_err[v] = e;
 }
 
 // ||sum_t G_i[t]||^2 for a bias: one workgroup per example, columns strided
 // over threads, column sums in fp32 (as the reference's per-example bias
-// gradient), squares summed in fp64.
+// gradient, and in the order bias_partial_kernel sums them, so the value
+// measured is the value summed), squares summed in fp64.  out[ex] = the
+// squared norm, out[B + ex] = its error bound: the fp64 sum of exact squares
+// and the fp32 product scale * column of the clipped sum, 2^-21 relative.
 template <typename In>
 __global__ void __launch_bounds__(kGramThreads)
-bias_sqnorm_kernel(const In* __restrict__ G, int T, int dout, double* __restrict__ out) {
+bias_sqnorm_kernel(const In* __restrict__ G, int B, int T, int dout, double* __restrict__ out) {
   __shared__ double red[kGramThreads / 64];
   const int ex = blockIdx.x;
   const In* g = G + (size_t)ex * T * dout;
@@ -538,13 +672,20 @@ bias_sqnorm_kernel(const In* __restrict__ G, int T, int dout, double* __restrict
     s += (double)col * (double)col;
   }
   double total = block_sum_f64(s, red);
-  if (threadIdx.x == 0) out[ex] = total;
+  if (threadIdx.x == 0) {
+    out[ex] = total;
+    out[B + ex] = total * 0x1.0p-21;
+  }
 }
 
+// Flat inputs: ||a||^2 ||g||^2 (+ ||g||^2 with a bias), each a fp64 sum of
+// exact squares; the error bound is (din + dout + 512) 2^-50 relative (the
+// fp64 sums, the product and the bias addition).
 template <typename In>
 __global__ void __launch_bounds__(kGramThreads)
 flat_sqnorm_kernel(const In* __restrict__ a, const In* __restrict__ g, int din, int dout,
-                   int with_bias, int accumulate, double* __restrict__ sqnorm) {
+                   int with_bias, int accumulate, double* __restrict__ sqnorm,
+                   double* __restrict__ sqerr) {
   __shared__ double red[kGramThreads / 64];
   const int ex = blockIdx.x;
   double sa = 0.0, sg = 0.0;
@@ -561,6 +702,10 @@ flat_sqnorm_kernel(const In* __restrict__ a, const In* __restrict__ g, int din, 
   if (threadIdx.x == 0) {
     double v = ta * tg + (with_bias ? tg : 0.0);
     sqnorm[ex] = accumulate ? sqnorm[ex] + v : v;
+    if (sqerr) {
+      const double e = fabs(v) * ((double)din + (double)dout + 512.0) * 0x1.0p-50;
+      sqerr[ex] = accumulate ? sqerr[ex] + e : e;
+    }
   }
 }
 
@@ -596,12 +741,12 @@ extern "C" size_t dpc_gram_workspace_bytes(int B, int T) {
   // Tile counts for the generic path (64-row tiles) bound the MFMA path's.
   int nt = ceil_div(T, kGenTile);
   size_t npairs = (size_t)nt * (nt + 1) / 2;
-  return (npairs * (size_t)B + (size_t)B) * sizeof(double);
+  return (npairs * (size_t)B * DPC_GRAM_REC_WORDS + 2 * (size_t)B) * sizeof(double);
 }
 
 extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int din, int dout,
                                 int dtype, int with_bias, int accumulate, double* sqnorm,
-                                void* ws, size_t ws_bytes, void* stream) {
+                                double* sqerr, void* ws, size_t ws_bytes, void* stream) {
   if (B < 0 || T <= 0 || din <= 0 || dout <= 0) return DPC_EINVAL;
   if (B == 0) return DPC_OK;
   if (!A || !G || !sqnorm || !ws) return DPC_EINVAL;
@@ -609,52 +754,52 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
   if (B > 65535) return DPC_ENOTSUP;
   if (ws_bytes < dpc_gram_workspace_bytes(B, T)) return DPC_ENOSPC;
   hipStream_t s = (hipStream_t)stream;
-  double* partial = (double*)ws;
-  int npairs;
+  double* records = (double*)ws;
+  int nt;
   // Buffer offsets are 32-bit: one example's rows (plus a tile of padding)
   // must stay below 2 GiB for the MFMA path.
   const size_t dmax = (size_t)(din > dout ? din : dout);
   const bool fits = ((size_t)T + kGramTile) * dmax * 2 < ((size_t)1 << 31);
   const bool mfma = dtype == DPC_BF16 && din % 8 == 0 && dout % 8 == 0 && fits;
   if (mfma) {
-    int nt = ceil_div(T, kGramTile);
-    npairs = nt * (nt + 1) / 2;
+    nt = ceil_div(T, kGramTile);
+    const int npairs = nt * (nt + 1) / 2;
     const int nblocks = npairs * B;
     const int padded = ceil_div(nblocks, kXcds) * kXcds;
     GramItems none = {};
     hipLaunchKernelGGL(gram_mfma_bf16_kernel<false>, dim3(padded), dim3(kGramMfmaThreads), 0, s,
                        (const uint16_t*)A, (const uint16_t*)G, T, din, dout, npairs, nblocks,
-                       partial, none, xcd_cus());
+                       records, none, xcd_cus());
   } else {
-    int nt = ceil_div(T, kGenTile);
-    npairs = nt * (nt + 1) / 2;
+    nt = ceil_div(T, kGenTile);
+    const int npairs = nt * (nt + 1) / 2;
     if (dtype == DPC_BF16) {
       hipLaunchKernelGGL(gram_generic_kernel<uint16_t>, dim3(npairs, B), dim3(kGramThreads), 0,
                          s, (const uint16_t*)A, (const uint16_t*)G, T, din, dout, npairs,
-                         partial);
+                         records);
     } else {
       hipLaunchKernelGGL(gram_generic_kernel<float>, dim3(npairs, B), dim3(kGramThreads), 0, s,
-                         (const float*)A, (const float*)G, T, din, dout, npairs, partial);
+                         (const float*)A, (const float*)G, T, din, dout, npairs, records);
     }
   }
   DPC_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(row_sum_f64_kernel, dim3(ceil_div(B, kGramThreads)), dim3(kGramThreads), 0,
-                     s, partial, B, npairs, accumulate, sqnorm);
-  DPC_HIP_CHECK(hipGetLastError());
+  double* bias = nullptr;
   if (with_bias) {
-    double* bias_sq = partial + (size_t)npairs * B;
+    const size_t np = (size_t)nt * (nt + 1) / 2;
+    bias = records + np * (size_t)B * DPC_GRAM_REC_WORDS;
     if (dtype == DPC_BF16) {
       hipLaunchKernelGGL(bias_sqnorm_kernel<uint16_t>, dim3(B), dim3(kGramThreads), 0, s,
-                         (const uint16_t*)G, T, dout, bias_sq);
+                         (const uint16_t*)G, B, T, dout, bias);
     } else {
       hipLaunchKernelGGL(bias_sqnorm_kernel<float>, dim3(B), dim3(kGramThreads), 0, s,
-                         (const float*)G, T, dout, bias_sq);
+                         (const float*)G, B, T, dout, bias);
     }
     DPC_HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(row_sum_f64_kernel, dim3(ceil_div(B, kGramThreads)), dim3(kGramThreads),
-                       0, s, bias_sq, B, 1, 1, sqnorm);
-    DPC_HIP_CHECK(hipGetLastError());
   }
+  hipLaunchKernelGGL(gram_finish_kernel, dim3(ceil_div(B, kGramThreads)), dim3(kGramThreads), 0,
+                     s, (const double*)records, B, nt, accumulate, (const double*)bias, sqnorm,
+                     sqerr);
+  DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;
 }
 
@@ -662,14 +807,15 @@ extern "C" int dpc_grouped_gram_sqnorms(const int64_t* a_ptrs, const int64_t* g_
                                         const int32_t* dims, int n_problems, int dtype,
                                         const int32_t* items, int n_items, int max_rows,
                                         const int32_t* seg_item_start, int S, double* seg_sq,
-                                        void* ws, size_t ws_bytes, void* stream) {
+                                        double* seg_err, void* ws, size_t ws_bytes,
+                                        void* stream) {
   if (n_problems < 1 || !dims || n_items < 0 || S < 0 || max_rows < 0) return DPC_EINVAL;
   if (dtype != DPC_F32 && dtype != DPC_BF16) return DPC_EINVAL;
   if (n_problems > kMaxGramProblems) return DPC_ENOTSUP;
   if (S == 0) return DPC_OK;
   if (!seg_item_start || !seg_sq || (n_items > 0 && (!a_ptrs || !g_ptrs || !items || !ws)))
     return DPC_EINVAL;
-  if (ws_bytes < (size_t)n_items * sizeof(double)) return DPC_ENOSPC;
+  if (ws_bytes < (size_t)n_items * DPC_GRAM_REC_WORDS * sizeof(double)) return DPC_ENOSPC;
   GramItems work;
   work.items = items;
   work.a_ptrs = a_ptrs;
@@ -685,31 +831,31 @@ extern "C" int dpc_grouped_gram_sqnorms(const int64_t* a_ptrs, const int64_t* g_
     dmax = max(dmax, max(work.din[p], work.dout[p]));
   }
   hipStream_t s = (hipStream_t)stream;
-  double* partial = (double*)ws;
+  double* records = (double*)ws;
   if (n_items > 0) {
     const bool fits = ((size_t)max_rows + kGramTile) * (size_t)dmax * 2 < ((size_t)1 << 31);
     if (dtype == DPC_BF16 && aligned && fits) {
       const int padded = ceil_div(n_items, kXcds) * kXcds;
       hipLaunchKernelGGL(gram_mfma_bf16_kernel<true>, dim3(padded), dim3(kGramMfmaThreads), 0, s,
-                         nullptr, nullptr, 0, 0, 0, 0, n_items, partial, work, 0);
+                         nullptr, nullptr, 0, 0, 0, 0, n_items, records, work, 0);
     } else if (dtype == DPC_BF16) {
       hipLaunchKernelGGL(gram_grouped_generic_kernel<uint16_t>, dim3(n_items), dim3(kGramThreads),
-                         0, s, work, partial);
+                         0, s, work, records);
     } else {
       hipLaunchKernelGGL(gram_grouped_generic_kernel<float>, dim3(n_items), dim3(kGramThreads), 0,
-                         s, work, partial);
+                         s, work, records);
     }
     DPC_HIP_CHECK(hipGetLastError());
   }
-  hipLaunchKernelGGL(segment_fold_kernel, dim3(ceil_div(S, kGramThreads)), dim3(kGramThreads), 0,
-                     s, (const double*)partial, seg_item_start, S, seg_sq);
+  hipLaunchKernelGGL(segment_finish_kernel, dim3(ceil_div(S, kGramThreads)), dim3(kGramThreads), 0,
+                     s, (const double*)records, seg_item_start, S, seg_sq, seg_err);
   DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;
 }
 
 extern "C" int dpc_flat_sqnorms(const void* a, const void* g, int B, int din, int dout,
                                 int dtype, int with_bias, int accumulate, double* sqnorm,
-                                void* stream) {
+                                double* sqerr, void* stream) {
   if (B < 0 || din <= 0 || dout <= 0) return DPC_EINVAL;
   if (B == 0) return DPC_OK;
   if (!a || !g || !sqnorm) return DPC_EINVAL;
@@ -718,11 +864,11 @@ extern "C" int dpc_flat_sqnorms(const void* a, const void* g, int B, int din, in
   if (dtype == DPC_BF16) {
     hipLaunchKernelGGL(flat_sqnorm_kernel<uint16_t>, dim3(B), dim3(kGramThreads), 0, s,
                        (const uint16_t*)a, (const uint16_t*)g, din, dout, with_bias, accumulate,
-                       sqnorm);
+                       sqnorm, sqerr);
   } else if (dtype == DPC_F32) {
     hipLaunchKernelGGL(flat_sqnorm_kernel<float>, dim3(B), dim3(kGramThreads), 0, s,
                        (const float*)a, (const float*)g, din, dout, with_bias, accumulate,
-                       sqnorm);
+                       sqnorm, sqerr);
   } else {
     return DPC_EINVAL;
   }

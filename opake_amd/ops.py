@@ -23,19 +23,35 @@ def _contig(t: torch.Tensor) -> torch.Tensor:
     return t if t.is_contiguous() else t.contiguous()
 
 
+def _error_out(err, B, dev, accumulate):
+    """The error-bound vector of a norm call: ``err`` itself, or a new one."""
+    if err is None:
+        if accumulate:
+            raise ConfigurationError("accumulating with an error bound needs its `err` vector")
+        return torch.empty(B, dtype=torch.float64, device=dev)
+    if err.dtype != torch.float64 or tuple(err.shape) != (B,) or not err.is_contiguous():
+        raise ConfigurationError("err must be a contiguous float64 [B] vector")
+    return err
+
+
 def gram_sqnorms(
     A: torch.Tensor,
     G: torch.Tensor,
     *,
     with_bias: bool = False,
     out: torch.Tensor | None = None,
-) -> torch.Tensor:
+    err: torch.Tensor | None = None,
+    return_error: bool = False,
+):
     """``out[i] (+)= ||G_i^T A_i||_F^2 (+ ||sum_t G_i[t]||^2)`` in float64.
 
     ``A``: [B, T, din], ``G``: [B, T, dout], same dtype (bf16 or fp32).  When
-    ``out`` is given the layer's contribution is added to it.
+    ``out`` is given the layer's contribution is added to it.  With ``err`` (or
+    ``return_error``) the kernel also writes -- or, with ``out``, adds -- an
+    upper bound of the rounding error, so that ``out + err >= ||G_i^T A_i||^2``
+    exactly; the call then returns ``(out, err)``.
     """
-    dev = nat.require_device(A, G, out)
+    dev = nat.require_device(A, G, out, err)
     if A.dim() != 3 or G.dim() != 3 or A.shape[:2] != G.shape[:2]:
         raise ConfigurationError(
             f"expected A [B, T, din] and G [B, T, dout], got {tuple(A.shape)}, {tuple(G.shape)}"
@@ -46,20 +62,22 @@ def gram_sqnorms(
     dout = G.shape[2]
     A, G = _contig(A), _contig(G)
     accumulate = out is not None
+    with_err = err is not None or return_error
     if out is None:
         out = torch.empty(B, dtype=torch.float64, device=dev)
     elif out.dtype != torch.float64 or out.shape != (B,):
         raise ConfigurationError("out must be float64 [B]")
-    if B == 0:
-        return out
-    ws_bytes = nat.load().dpc_gram_workspace_bytes(B, T)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    nat.call(
-        "dpc_gram_sqnorms", nat.ptr(A), nat.ptr(G), B, T, din, dout, nat.dtype_code(A.dtype),
-        int(with_bias), int(accumulate), nat.ptr(out), nat.ptr(ws), ws_bytes,
-        nat.stream_handle(dev),
-    )
-    return out
+    if with_err:
+        err = _error_out(err, B, dev, accumulate)
+    if B > 0:
+        ws_bytes = nat.load().dpc_gram_workspace_bytes(B, T)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        nat.call(
+            "dpc_gram_sqnorms", nat.ptr(A), nat.ptr(G), B, T, din, dout,
+            nat.dtype_code(A.dtype), int(with_bias), int(accumulate), nat.ptr(out),
+            nat.ptr(err if with_err else None), nat.ptr(ws), ws_bytes, nat.stream_handle(dev),
+        )
+    return (out, err) if with_err else out
 
 
 def flat_sqnorms(
@@ -68,24 +86,30 @@ def flat_sqnorms(
     *,
     with_bias: bool = False,
     out: torch.Tensor | None = None,
-) -> torch.Tensor:
-    """``out[i] (+)= ||a_i||^2 ||g_i||^2 (+ ||g_i||^2)`` for flat inputs [B, d]."""
-    dev = nat.require_device(a, g, out)
+    err: torch.Tensor | None = None,
+    return_error: bool = False,
+):
+    """``out[i] (+)= ||a_i||^2 ||g_i||^2 (+ ||g_i||^2)`` for flat inputs [B, d];
+    ``err`` / ``return_error`` as in :func:`gram_sqnorms`."""
+    dev = nat.require_device(a, g, out, err)
     if a.dim() != 2 or g.dim() != 2 or a.shape[0] != g.shape[0] or a.dtype != g.dtype:
         raise ConfigurationError("expected a [B, din] and g [B, dout] of one dtype")
     B, din = a.shape
     dout = g.shape[1]
     accumulate = out is not None
+    with_err = err is not None or return_error
     if out is None:
         out = torch.empty(B, dtype=torch.float64, device=dev)
-    if B == 0:
-        return out
-    a, g = _contig(a), _contig(g)
-    nat.call(
-        "dpc_flat_sqnorms", nat.ptr(a), nat.ptr(g), B, din, dout, nat.dtype_code(a.dtype),
-        int(with_bias), int(accumulate), nat.ptr(out), nat.stream_handle(dev),
-    )
-    return out
+    if with_err:
+        err = _error_out(err, B, dev, accumulate)
+    if B > 0:
+        a, g = _contig(a), _contig(g)
+        nat.call(
+            "dpc_flat_sqnorms", nat.ptr(a), nat.ptr(g), B, din, dout, nat.dtype_code(a.dtype),
+            int(with_bias), int(accumulate), nat.ptr(out), nat.ptr(err if with_err else None),
+            nat.stream_handle(dev),
+        )
+    return (out, err) if with_err else out
 
 
 @dataclass
@@ -95,7 +119,7 @@ class ClipFactors:
     scale: torch.Tensor  # float32 [n_guards, B]
     norms: torch.Tensor  # float32 [B]
     nclipped: torch.Tensor  # int32 [1]
-    plan: torch.Tensor  # uint8 plan bytes (active example list of guard 0)
+    plan: torch.Tensor  # uint8 [n_guards, plan bytes]: guard g's active example lists
 
 
 def clip_factors(
@@ -103,28 +127,35 @@ def clip_factors(
     clipping_norm: float,
     guards: list[tuple[float, float]],
     *,
+    err: torch.Tensor | None = None,
     kind: int = nat.SCALE_FIXED,
     gamma: float = 0.0,
     count_threshold: float,
 ) -> ClipFactors:
-    """Guarded clip factors for each ``(rel, abs)`` guard, per example."""
-    dev = nat.require_device(sqnorm)
+    """Guarded clip factors for each ``(rel, abs)`` guard, per example.
+
+    ``err`` (float64 [B], optional): the error bound of ``sqnorm``; the scale
+    is then taken from ``sqrt(sqnorm + err)``, the reported norms and the
+    clipped count from ``sqrt(sqnorm)``."""
+    dev = nat.require_device(sqnorm, err)
     if sqnorm.dtype != torch.float64 or sqnorm.dim() != 1:
         raise ConfigurationError("sqnorm must be a float64 vector")
     if not 1 <= len(guards) <= 4:
         raise ConfigurationError("between 1 and 4 guards are supported")
     B = sqnorm.shape[0]
+    if err is not None and (err.dtype != torch.float64 or tuple(err.shape) != (B,)):
+        raise ConfigurationError("err must be a float64 vector like sqnorm")
     n = len(guards)
     rel = (ctypes.c_double * n)(*[g[0] for g in guards])
     abs_ = (ctypes.c_double * n)(*[g[1] for g in guards])
     scale = torch.empty((n, B), dtype=torch.float32, device=dev)
     norms = torch.empty(B, dtype=torch.float32, device=dev)
     nclipped = torch.empty(1, dtype=torch.int32, device=dev)
-    plan = torch.empty(nat.load().dpc_clip_plan_bytes(B), dtype=torch.uint8, device=dev)
+    plan = torch.empty((n, nat.load().dpc_clip_plan_bytes(B)), dtype=torch.uint8, device=dev)
     nat.call(
-        "dpc_clip_factors", nat.ptr(_contig(sqnorm)), B, float(clipping_norm), kind, float(gamma),
-        rel, abs_, n, float(count_threshold), nat.ptr(scale), nat.ptr(norms), nat.ptr(nclipped),
-        nat.ptr(plan), nat.stream_handle(dev),
+        "dpc_clip_factors", nat.ptr(_contig(sqnorm)), nat.ptr(None if err is None else _contig(err)),
+        B, float(clipping_norm), kind, float(gamma), rel, abs_, n, float(count_threshold),
+        nat.ptr(scale), nat.ptr(norms), nat.ptr(nclipped), nat.ptr(plan), nat.stream_handle(dev),
     )
     return ClipFactors(scale=scale, norms=norms, nclipped=nclipped, plan=plan)
 
@@ -197,6 +228,7 @@ def clipped_sum(
 
 
 _GRAM_TILE = 128  # rows of a Gram tile of the grouped norm kernel
+_GRAM_REC_WORDS = 12  # float64 words of a Gram work item's record
 _STEP_ROWS = 64  # rows of a K step of the grouped clipped sum
 
 
@@ -347,8 +379,10 @@ def _check_grouped(A_list, G_list, layout: SegmentLayout, *, same_shape: bool):
     return din, dout, dtype
 
 
-def grouped_gram_sqnorms(A_list, G_list, layout: SegmentLayout) -> torch.Tensor:
-    """``||G_v^T A_v||^2`` for every segment v of the layout: float64 [E, K].
+def grouped_gram_sqnorms(A_list, G_list, layout: SegmentLayout, *, return_error: bool = False):
+    """``||G_v^T A_v||^2`` for every segment v of the layout: float64 [E, K]
+    (with ``return_error``, ``(seg_sq, seg_err)``: ``seg_err`` bounds the
+    rounding error as in :func:`gram_sqnorms`).
 
     Problems may differ in din / dout (at most 64 problems per call)."""
     dev = nat.require_device(*A_list, *G_list)
@@ -358,15 +392,18 @@ def grouped_gram_sqnorms(A_list, G_list, layout: SegmentLayout) -> torch.Tensor:
     dims = (ctypes.c_int * (2 * layout.E))(
         *[v for A, G in zip(A_list, G_list) for v in (A.shape[1], G.shape[1])])
     seg_sq = torch.empty((layout.E, layout.K), dtype=torch.float64, device=dev)
-    ws = torch.empty(max(layout.n_launch_items, 1), dtype=torch.float64, device=dev)
+    seg_err = (torch.empty((layout.E, layout.K), dtype=torch.float64, device=dev)
+               if return_error else None)
+    ws = torch.empty(max(layout.n_launch_items, 1) * _GRAM_REC_WORDS, dtype=torch.float64,
+                     device=dev)
     a_ptrs, g_ptrs = _ptr_table(A_list, dev), _ptr_table(G_list, dev)
     nat.call(
         "dpc_grouped_gram_sqnorms", nat.ptr(a_ptrs), nat.ptr(g_ptrs), dims, layout.E,
         nat.dtype_code(dtype), nat.ptr(layout.items), layout.n_launch_items, layout.max_rows,
-        nat.ptr(layout.item_start), layout.S, nat.ptr(seg_sq), nat.ptr(ws),
+        nat.ptr(layout.item_start), layout.S, nat.ptr(seg_sq), nat.ptr(seg_err), nat.ptr(ws),
         ws.numel() * 8, nat.stream_handle(dev),
     )
-    return seg_sq
+    return (seg_sq, seg_err) if return_error else seg_sq
 
 
 @dataclass

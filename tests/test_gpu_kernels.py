@@ -112,20 +112,30 @@ def test_gram_nonfinite_example_is_nonfinite(dev):
 # --- clip factors ---------------------------------------------------------------
 
 
-def _oracle_scales(sq, C, rel_abs_storage, kind="fixed", gamma=0.0):
+def _oracle_scales(sq, C, rel_abs_storage, kind="fixed", gamma=0.0, err=None):
     storage, mult, roundoff = rel_abs_storage
-    norm = torch.sqrt(sq)
+    up = sq if err is None else sq + err
+    up = torch.where(up < 0, torch.zeros_like(up), up)  # NaN stays NaN
+    norm = torch.sqrt(up)
     bound = torch.clamp(torch.as_tensor(C, dtype=torch.float64), min=0.0)
     ratio = bound / (norm + gamma) if kind == "auto_s" else bound / norm
     return clip_oracle.finalize_scale(ratio, storage, mult, roundoff, clamp_to_one=kind != "auto_s")
 
 
 @pytest.mark.parametrize("kind", ["fixed", "auto_s"])
-def test_clip_factors_bit_exact(dev, kind):
+@pytest.mark.parametrize("with_err", [False, True])
+def test_clip_factors_bit_exact(dev, kind, with_err):
     g = _gen(11)
     B = 3000
     sq = torch.exp(torch.randn(B, generator=g, dtype=torch.float64) * 3)
     sq[:6] = torch.tensor([0.0, math.inf, math.nan, 1.0, 0.25, 1e300], dtype=torch.float64)
+    err = None
+    if with_err:
+        # An error bound per example (a cancelled estimate may even be
+        # negative: the scale then comes from the bound alone).
+        err = sq * torch.rand(B, generator=g, dtype=torch.float64) * 0.01
+        err[3] = 0.5
+        sq[8], err[8] = -0.125, 1.0
     # Scales 2^-65 .. 2^-75 (positive in float32, below the plan's 2^-64
     # fast-list bound) in each of the kernel's 1024-example passes.
     for i, e in ((7, 130), (1500, 140), (2047, 150), (2999, 134)):
@@ -138,27 +148,33 @@ def test_clip_factors_bit_exact(dev, kind):
         mult = torch.promote_types(storage, torch.float32)
         roundoff = clip_oracle.norm_roundoff(torch.float32, torch.float64, 1, 10240)
         guards.append(num.guard_constants(storage, mult, roundoff))
-        expect.append(_oracle_scales(sq, C, (storage, mult, roundoff), kind, gamma).to(torch.float32))
-    cf = ops.clip_factors(sq.to(dev), C, guards, kind=nat.SCALE_AUTO_S if kind == "auto_s"
-                          else nat.SCALE_FIXED, gamma=gamma, count_threshold=1.0)
+        expect.append(_oracle_scales(sq, C, (storage, mult, roundoff), kind, gamma,
+                                     err).to(torch.float32))
+    cf = ops.clip_factors(sq.to(dev), C, guards, err=None if err is None else err.to(dev),
+                          kind=nat.SCALE_AUTO_S if kind == "auto_s" else nat.SCALE_FIXED,
+                          gamma=gamma, count_threshold=1.0)
     for gi in range(2):
         assert torch.equal(cf.scale[gi].cpu(), expect[gi]), gi
-    norms = torch.sqrt(sq).to(torch.float32)
+    norms = torch.sqrt(torch.where(sq < 0, torch.zeros_like(sq), sq)).to(torch.float32)
     torch.testing.assert_close(cf.norms.cpu(), norms, rtol=0, atol=0, equal_nan=True)
     assert int(cf.nclipped.item()) == int((norms > 1.0).sum().item())
     # Plan: examples with a positive guard-0 scale; those at or above 2^-64
     # from the front in increasing order, the others from the back (B * C is
     # far below the 2^55 bound here).
-    s0 = expect[0]
-    fast = [i for i in range(B) if s0[i] >= 2.0 ** -64]
-    slow = [i for i in range(B) if 0 < s0[i] < 2.0 ** -64]
-    assert slow == [7, 1500, 2047, 2999]
-    plan = cf.plan.cpu().numpy().view(np.int32)
-    assert plan[0] == len(fast) + len(slow)
-    assert plan[1] == len(fast)
-    active = plan[4:4 + B]
-    assert list(active[:len(fast)]) == fast
-    assert list(active[B - len(slow):][::-1]) == slow
+    # One plan per guard: the examples with a positive scale; those in
+    # [2^-64, 2^32] from the front in increasing order, the others from the
+    # back (B * C is far below the 2^55 bound here).
+    for gi in range(2):
+        s0 = expect[gi]
+        fast = [i for i in range(B) if 2.0 ** -64 <= s0[i] <= 2.0 ** 32]
+        slow = [i for i in range(B) if 0 < s0[i] and not 2.0 ** -64 <= s0[i] <= 2.0 ** 32]
+        assert slow == [7, 1500, 2047, 2999]
+        plan = cf.plan[gi].cpu().numpy().view(np.int32)
+        assert plan[0] == len(fast) + len(slow)
+        assert plan[1] == len(fast)
+        active = plan[4:4 + B]
+        assert list(active[:len(fast)]) == fast
+        assert list(active[B - len(slow):][::-1]) == slow
 
 
 def test_clip_factors_boundary_example(dev):
@@ -190,12 +206,13 @@ def _oracle_clipped_sum(A, G, C, nb=1.0, bias=False, out_dtype=None, kind="fixed
 def _run_clipped_sum(dev, A, G, C, nb=1.0, bias=False, out_dtype=None, use_plan=True):
     B, T, din = A.shape
     dout = G.shape[2]
-    sq = ops.gram_sqnorms(A.to(dev), G.to(dev), with_bias=bias) if T > 1 else ops.flat_sqnorms(
-        A[:, 0].to(dev), G[:, 0].to(dev), with_bias=bias)
+    sq, err = ops.gram_sqnorms(A.to(dev), G.to(dev), with_bias=bias, return_error=True) \
+        if T > 1 else ops.flat_sqnorms(A[:, 0].to(dev), G[:, 0].to(dev), with_bias=bias,
+                                       return_error=True)
     from opake_amd.clipping import guard_for_linear
     cf = ops.clip_factors(sq, num.conservative_bound(C), [guard_for_linear(A.dtype, din, dout, bias)],
-                          count_threshold=num.float32_of(C))
-    w, b = ops.clipped_sum(A.to(dev), G.to(dev), cf.scale[0], plan=cf.plan if use_plan else None,
+                          err=err, count_threshold=num.float32_of(C))
+    w, b = ops.clipped_sum(A.to(dev), G.to(dev), cf.scale[0], plan=cf.plan[0] if use_plan else None,
                            normalize_by=nb, out_dtype=out_dtype, with_bias=bias)
     return w, b, cf
 
@@ -253,7 +270,7 @@ def test_clipped_sum_slow_plan_slots(dev, case):
         C = 1e17  # B * C > 2^55: no example is clipped, all take the slow slots
     G = G.to(torch.bfloat16)
     w, _, cf = _run_clipped_sum(dev, A, G, C, out_dtype=torch.float32)
-    plan = cf.plan.cpu().view(torch.int32)
+    plan = cf.plan[0].cpu().view(torch.int32)
     nactive, nfast = int(plan[0]), int(plan[1])
     assert nactive == B
     assert nfast == (B - 1 if case == "tiny_scale" else 0)
@@ -280,7 +297,7 @@ def test_clipped_sum_split_k(dev, B, T, din, dout):
     assert _rel_err(b.cpu(), wb) < 2e-2
     w2, _, _ = _run_clipped_sum(dev, A, G, 1.0, nb=2.0, bias=True, out_dtype=torch.float32)
     assert torch.equal(w, w2)
-    kw = dict(plan=cf.plan, normalize_by=2.0, out_dtype=torch.bfloat16)
+    kw = dict(plan=cf.plan[0], normalize_by=2.0, out_dtype=torch.bfloat16)
     center, _ = ops.clipped_sum(A.to(dev), G.to(dev), cf.scale[0], **kw)
     spec = ops.NoiseSpec(sigma=0.5, mode=nat.NOISE_PHILOX, seed=7, leaf_id=3)
     noisy, _ = ops.clipped_sum(A.to(dev), G.to(dev), cf.scale[0], noise=spec, **kw)
@@ -401,11 +418,11 @@ def test_clipped_sum_epilogue_noise_injected_bit_exact(dev):
     cf = ops.clip_factors(sq, 1.0, [guard_for_linear(torch.bfloat16, 256, 256, False)],
                           count_threshold=1.0)
     for out_dtype in (torch.float32, torch.bfloat16):
-        center, _ = ops.clipped_sum(A.to(dev), G.to(dev), cf.scale[0], plan=cf.plan,
+        center, _ = ops.clipped_sum(A.to(dev), G.to(dev), cf.scale[0], plan=cf.plan[0],
                                     normalize_by=4.0, out_dtype=out_dtype)
         z = torch.randn(256, 256, generator=g)
         noisy, _ = ops.clipped_sum(
-            A.to(dev), G.to(dev), cf.scale[0], plan=cf.plan, normalize_by=4.0, out_dtype=out_dtype,
+            A.to(dev), G.to(dev), cf.scale[0], plan=cf.plan[0], normalize_by=4.0, out_dtype=out_dtype,
             noise=ops.NoiseSpec(sigma=0.25, mode=nat.NOISE_INJECTED, noise=z.to(dev)))
         assert torch.equal(noisy.cpu(), noise_oracle.sample(center.cpu(), 0.25, z))
 
@@ -418,7 +435,7 @@ def test_clipped_sum_epilogue_noise_philox_matches_add_noise(dev):
     from opake_amd.clipping import guard_for_linear
     cf = ops.clip_factors(sq, 1.0, [guard_for_linear(torch.bfloat16, 264, 136, True)],
                           count_threshold=1.0)
-    kw = dict(plan=cf.plan, normalize_by=2.0, out_dtype=torch.float32, with_bias=True)
+    kw = dict(plan=cf.plan[0], normalize_by=2.0, out_dtype=torch.float32, with_bias=True)
     cw, cb = ops.clipped_sum(A.to(dev), G.to(dev), cf.scale[0], **kw)
     spec = ops.NoiseSpec(sigma=0.5, mode=nat.NOISE_PHILOX, seed=99, leaf_id=1, bias_leaf_id=0)
     nw, nbias = ops.clipped_sum(A.to(dev), G.to(dev), cf.scale[0], noise=spec, **kw)
