@@ -79,6 +79,20 @@ int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int din, int do
                      int with_bias, int accumulate, double* sqnorm, double* sqerr, void* ws,
                      size_t ws_bytes, void* stream);
 
+/* dpc_gram_sqnorms_noalloc: no counterpart in the reference.  The same
+ * computation as dpc_gram_sqnorms with no workspace argument and no
+ * allocation, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * workspace is a static device array of DPC_NOALLOC_SCRATCH_BYTES per device,
+ * held until the process ends.  Calls needing more
+ * (dpc_gram_workspace_bytes(B, T) > DPC_NOALLOC_SCRATCH_BYTES) return
+ * DPC_ENOSPC.  Every call on a device shares that device's array, so calls
+ * that overlap on one device (other streams, other threads) race. */
+#define DPC_NOALLOC_SCRATCH_BYTES (4u << 20)
+int dpc_gram_sqnorms_noalloc(const void* A, const void* G, int B, int T, int din, int dout,
+                             int dtype, int with_bias, int accumulate, double* sqnorm,
+                             double* sqerr, void* stream);
+
 /* Flat inputs (T == 1): a [B, din], g [B, dout];
  * sqnorm[i] (+)= ||a_i||^2 ||g_i||^2 (+ ||g_i||^2 with a bias), sqerr[i] (+)=
  * its error bound (nullable). */

@@ -56,6 +56,11 @@ SIGNATURES = {
         [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
          _c_void_p, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
     ),
+    "dpc_gram_sqnorms_noalloc": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_void_p, _c_void_p, _c_void_p],
+    ),
     "dpc_flat_sqnorms": (
         _c_int,
         [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,

@@ -27,7 +27,15 @@
 // accumulators (operands ordered so that din <= dout: the loop is the
 // "both Gram matrices" body for A's K range, then a "G G^T only" body that
 // stages G's tiles alone).
+#include <mutex>
+
 #include "common.h"
+
+// Workspace of dpc_gram_sqnorms_noalloc: one copy per device, resolved to a
+// device address once per device (hipGetSymbolAddress) and used through that
+// address only; the records of a call are written in full before they are
+// read, so nothing in it needs clearing between calls.
+static __device__ __align__(256) uint8_t scratch[DPC_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -884,4 +892,45 @@ extern "C" int dpc_row_sum_f64(const double* x, int B, int n, int accumulate, do
                      (hipStream_t)stream, x, B, n, accumulate, out);
   DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;
+}
+
+namespace {
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Address of this device's `scratch`, looked up on the device's first call.
+void* scratch_on_current_device() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    dpc_record_error(e);
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) {
+      dpc_record_error(e);
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" int dpc_gram_sqnorms_noalloc(const void* A, const void* G, int B, int T, int din,
+                                        int dout, int dtype, int with_bias, int accumulate,
+                                        double* sqnorm, double* sqerr, void* stream) {
+  if (B < 0 || T <= 0 || din <= 0 || dout <= 0) return DPC_EINVAL;
+  if (B == 0) return DPC_OK;
+  const size_t need = dpc_gram_workspace_bytes(B, T);
+  if (need > (size_t)DPC_NOALLOC_SCRATCH_BYTES) return DPC_ENOSPC;
+  void* ws = scratch_on_current_device();
+  if (!ws) return DPC_EHIP;
+  return dpc_gram_sqnorms(A, G, B, T, din, dout, dtype, with_bias, accumulate, sqnorm, sqerr, ws,
+                          (size_t)DPC_NOALLOC_SCRATCH_BYTES, stream);
 }
