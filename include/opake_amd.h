@@ -114,10 +114,13 @@ int dpc_flat_sqnorms(const void* a, const void* g, int B, int din, int dout, int
  *   s      = min(1, s)                             (FIXED only)
  *   s      = isfinite(s) ? max(s, 0) : 0
  *   scale[g * B + i] = (float)s                    for each guard g < n_guards
+ *                    (guard_bf16[g] != 0: s rounded to the nearest bf16 --
+ *                    the reference's scale.to(multiply dtype) for an explicit
+ *                    compute_dtype=bfloat16, _pytree.py:160-187)
  * norms_out[i] = (float)norm; *nclipped = #{i : (float)norm > count_threshold}
  * (the reference's strict `norms > clipping_norm`, _clipped_fun.py:348-396).
- * guard_rel / guard_abs are HOST arrays of n_guards (1..4) values, one
- * pair per storage dtype.  sqnorm and all outputs are device pointers.
+ * guard_rel / guard_abs / guard_bf16 (nullable: all 0) are HOST arrays of
+ * n_guards (1..4) values, one per storage dtype.  sqnorm and all outputs are device pointers.
  * Any output pointer may be NULL.  `plan` (nullable, device memory of
  * n_guards * dpc_clip_plan_bytes(B) bytes) receives one plan per guard: the
  * examples whose guard-g scale is positive, those the bf16 GEMM may apply to
@@ -128,8 +131,8 @@ int dpc_flat_sqnorms(const void* a, const void* g, int B, int din, int dout, int
 size_t dpc_clip_plan_bytes(int B);
 int dpc_clip_factors(const double* sqnorm, const double* sqerr, int B, double C, int kind,
                      double gamma, const double* guard_rel, const double* guard_abs,
-                     int n_guards, float count_threshold, float* scale, float* norms_out,
-                     int* nclipped, void* plan, void* stream);
+                     const int* guard_bf16, int n_guards, float count_threshold, float* scale,
+                     float* norms_out, int* nclipped, void* plan, void* stream);
 
 /* ------------------------------------------------------------------------
  * Clipped batch sum of a linear layer with the noise epilogue fused.
@@ -195,7 +198,9 @@ int dpc_philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32
  * leaf into 2048-element tiles.
  *
  * dpc_leaves_sqnorm: partial[b, t] = float64 sum over tile t of example b of
- *   (float)sanitise(x)^2 (fp32 square, fp64 sum), then
+ *   (float)sanitise(x)^2 (fp32 square, fp64 sum; square_dtype DPC_BF16, bf16
+ *   leaves only: each square rounded to bf16, the reference's reduction in an
+ *   explicit compute_dtype=bfloat16, _pytree.py:286-314), then
  *   leaf_sq[b, leaf_col[l]] = sum of leaf l's tiles (tile_start [L + 1]).
  * dpc_leaves_apply: out[off_l + j] = sum_b stored(b, l, j) in fp32, where
  *   stored = to_dtype(float(sanitise(x)) * scale[row_l * B + b]) with bf16
@@ -211,7 +216,8 @@ int dpc_philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32
 int dpc_leaves_sqnorm(const int64_t* ptrs, const int64_t* sizes, const int32_t* tile_leaf,
                       const int32_t* tile_local, const int64_t* tile_start,
                       const int32_t* leaf_col, int n_leaves, int n_tiles, int B, int dtype,
-                      double* partial, double* leaf_sq, int leaf_sq_stride, void* stream);
+                      int square_dtype, double* partial, double* leaf_sq, int leaf_sq_stride,
+                      void* stream);
 int dpc_leaves_apply(const int64_t* ptrs, const int64_t* sizes, const int32_t* tile_leaf,
                      const int32_t* tile_local, const int64_t* out_offs, int n_tiles, int B,
                      int dtype, const float* scale, const int32_t* leaf_scale_row, void* out,

@@ -70,8 +70,8 @@ SIGNATURES = {
     "dpc_clip_factors": (
         _c_int,
         [_c_void_p, _c_void_p, _c_int, _c_double, _c_int, _c_double, ctypes.POINTER(_c_double),
-         ctypes.POINTER(_c_double), _c_int, _c_float, _c_void_p, _c_void_p, _c_void_p,
-         _c_void_p, _c_void_p],
+         ctypes.POINTER(_c_double), ctypes.POINTER(_c_int), _c_int, _c_float, _c_void_p,
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     ),
     "dpc_clipped_sum_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "dpc_clipped_sum": (
@@ -92,7 +92,7 @@ SIGNATURES = {
     "dpc_leaves_sqnorm": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
-         _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p],
+         _c_int, _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p],
     ),
     "dpc_leaves_apply": (
         _c_int,

@@ -7,11 +7,13 @@ it was copied from: repeated calls with the same operands issue no host to
 device copy, and a HIP graph that recorded the copy can replay it (its source
 buffer stays alive and unchanged).  A table first needed while a graph is being
 captured is written by a kernel that carries its words as arguments
-(``dpc_write_words``).  Entries are never written after creation.
+(``dpc_write_words``).  Entries are never written after creation.  A graph
+owner collects the tables its capture used with :func:`keep_alive`.
 """
 
 from __future__ import annotations
 
+import contextlib
 import threading
 from collections import OrderedDict
 
@@ -21,6 +23,30 @@ import torch
 _MAX_ENTRIES = 1024
 _cache: OrderedDict = OrderedDict()
 _lock = threading.Lock()
+_recording = threading.local()
+
+
+@contextlib.contextmanager
+def keep_alive():
+    """Collects every table (and its host source) handed out on this thread
+    inside the block into the yielded list.  A HIP graph captured inside the
+    block reads those tables on every replay: its owner keeps the list for the
+    graph's lifetime, so an entry evicted from the cache later is not freed
+    while the graph can still read it."""
+    kept: list = []
+    stack = getattr(_recording, "stack", None)
+    if stack is None:
+        stack = _recording.stack = []
+    stack.append(kept)
+    try:
+        yield kept
+    finally:
+        stack.pop()
+
+
+def _record(*objs) -> None:
+    for kept in getattr(_recording, "stack", ()):
+        kept.extend(objs)
 
 
 def device_table(values, np_dtype, device) -> torch.Tensor:
@@ -32,12 +58,15 @@ def device_table(values, np_dtype, device) -> torch.Tensor:
         hit = _cache.get(key)
         if hit is not None:
             _cache.move_to_end(key)
+            _record(*hit)
             return hit[1]
     if dev.type == "cuda" and torch.cuda.is_current_stream_capturing():
         # Under graph capture: the words travel as kernel arguments (no host
-        # buffer to keep alive); the table is not cached (it lives in the
-        # graph's memory pool).
-        return _write_table(arr, dev)
+        # buffer to keep alive; every replay rewrites the table); the table is
+        # not cached.
+        table = _write_table(arr, dev)
+        _record(table)
+        return table
     host = torch.from_numpy(arr.copy())
     if dev.type == "cuda":
         host = host.pin_memory()
@@ -48,6 +77,7 @@ def device_table(values, np_dtype, device) -> torch.Tensor:
         _cache[key] = (host, table)
         while len(_cache) > _MAX_ENTRIES:
             _cache.popitem(last=False)
+    _record(host, table)
     return table
 
 
@@ -68,4 +98,4 @@ def pointer_table(tensors, device) -> torch.Tensor:
     return device_table([t.data_ptr() for t in tensors], np.int64, device)
 
 
-__all__ = ["device_table", "pointer_table"]
+__all__ = ["device_table", "keep_alive", "pointer_table"]

@@ -26,7 +26,17 @@ _clipped_grad.py:86-362, _auto.py:211-367):
   ``max_norm = C^2 / normalize_by`` for the squared stream
   (``_clipped_fun.py:414-423``).
 
-Not covered (``OperationError``): an explicit ``compute_dtype``, custom scale
+* ``compute_dtype`` (``_clipped_fun.py:91-170``, ``_pytree.py:84-108``):
+  float32, or bfloat16 with bfloat16 leaves -- squares, guard roundoff and
+  scale multiply in it (``promote(leaf, compute_dtype)``), batch sums in it and
+  cast to the output dtype after, microbatch running sums in the wider of it
+  and the output dtype.
+
+* ``pre_clipping_transform`` (``_clipped_grad.py:97,285``, ``_auto.py:222``):
+  applied to each example's gradient pytree inside the vmapped gradient
+  function, and to the zero gradients of an empty batch.
+
+Not covered (``OperationError``): other compute dtypes, custom scale
 functions.
 """
 
@@ -171,9 +181,28 @@ class _ChunkResult:
     squared: Any = None  # second moment: batch sums of the squared stored values
 
 
+def _check_compute_dtype(compute_dtype):
+    if compute_dtype is not None and not compute_dtype.is_floating_point:
+        raise InputTypeError(
+            f"compute_dtype must be a real floating-point dtype, got {compute_dtype!r}.  "
+            "Integer/bool/complex compute dtypes can silently corrupt the L2-norm reduction "
+            "(the squared sum is non-negative real and the final sqrt assumes a real "
+            "accumulator).")
+
+
+_ACCUMULATE = object()  # chunk sums of a microbatched call: the accumulation dtype
+
+
 def _clip_sum_values(values, clipping_norm, scale, *, dtype, with_postsq,
-                     second_moment=False) -> _ChunkResult:
-    """HIP clip-and-sum of a stacked pytree (``_streaming.py:39-185``)."""
+                     second_moment=False, compute_dtype=None, output_dtype=None) -> _ChunkResult:
+    """HIP clip-and-sum of a stacked pytree (``_streaming.py:39-185``).
+
+    ``dtype``: the dtype of the batch sums (default: the leaf dtype); with
+    ``compute_dtype`` bfloat16 the sums are taken in bfloat16 and cast to it
+    (``_sum_clipped_tensor``, ``_clipped_fun.py:114-132``).  ``dtype`` may be
+    ``_ACCUMULATE``: each leaf's sum is then taken in the microbatch
+    accumulation dtype for the requested ``output_dtype``."""
+    _check_compute_dtype(compute_dtype)
     grouped = isinstance(clipping_norm, PerGroup)
     if grouped:
         paths, leaves, treedef = tree_flatten_with_paths(values)
@@ -182,12 +211,21 @@ def _clip_sum_values(values, clipping_norm, scale, *, dtype, with_postsq,
     if not leaves:
         raise ConfigurationError("the clipped function returned no tensor leaves")
     B = leaves[0].shape[0]
-    reason = unsupported_reason(leaves, clipping_norm, scale, compute_dtype=None,
+    reason = unsupported_reason(leaves, clipping_norm, scale, compute_dtype=compute_dtype,
                                 second_moment=False, batch_size=B)
     if reason is not None:
         raise OperationError(f"HIP clip-and-sum cannot serve this call: {reason}")
     out_dtypes = None
-    if dtype is not None:
+    cast_to = None
+    if dtype is _ACCUMULATE:
+        out_dtypes = {l.dtype: _accumulation_dtype(l.dtype, output_dtype, compute_dtype)
+                      for l in leaves}
+        if any(v not in (k, torch.float32) for k, v in out_dtypes.items()):
+            raise OperationError(f"microbatch accumulation dtypes {out_dtypes} are not supported "
+                                 "(float32 or the leaf dtype)")
+    elif compute_dtype == torch.bfloat16:
+        cast_to = dtype
+    elif dtype is not None:
         if dtype != torch.float32:
             raise OperationError(f"output dtype {dtype} is not supported (float32 or the leaf dtype)")
         out_dtypes = {torch.bfloat16: torch.float32, torch.float32: torch.float32}
@@ -197,11 +235,16 @@ def _clip_sum_values(values, clipping_norm, scale, *, dtype, with_postsq,
         names, leaf_groups, bounds = _group_layout(paths, clipping_norm)
         res = leaves_clip_sum(detached, bounds, kind=scale.kind, gamma=scale.gamma,
                               with_postsq=with_postsq, out_dtypes=out_dtypes,
-                              leaf_groups=leaf_groups, second_moment=second_moment)
+                              leaf_groups=leaf_groups, second_moment=second_moment,
+                              compute_dtype=compute_dtype)
     else:
         res = leaves_clip_sum(detached, float(clipping_norm), kind=scale.kind,
                               gamma=scale.gamma, with_postsq=with_postsq, out_dtypes=out_dtypes,
-                              second_moment=second_moment)
+                              second_moment=second_moment, compute_dtype=compute_dtype)
+    if cast_to is not None:
+        res.reduced = [x.to(cast_to) for x in res.reduced]
+        if second_moment:
+            res.squared = [x.to(cast_to) for x in res.squared]
     group_norms = None
     if grouped:
         group_norms = {n: res.group_norms[k] for k, n in enumerate(names)}
@@ -224,8 +267,19 @@ def _stats(nclipped: torch.Tensor, clipping_norm, batch_size: int):
     return num, num / max(1.0, float(batch_size))
 
 
+def _accumulation_dtype(leaf_dtype, output_dtype, compute_dtype):
+    """Microbatch sum dtype (``_accumulation_dtype``, ``_clipped_fun.py:135-148``)."""
+    resolved = compute_dtype
+    if resolved is None and leaf_dtype in (torch.float16, torch.bfloat16):
+        resolved = torch.float32
+    if output_dtype is None:
+        return resolved if resolved is not None else leaf_dtype
+    return torch.promote_types(resolved if resolved is not None else leaf_dtype, output_dtype)
+
+
 def _make_clipped_fun(fun, has_aux, *, batch_argnums, clipping_norm, normalize_by, return_aux,
-                      return_stats, microbatch_size, dtype, scale, state, second_moment=False):
+                      return_stats, microbatch_size, dtype, scale, state, second_moment=False,
+                      compute_dtype=None):
     batch_argnums = _to_tuple(batch_argnums)
     if microbatch_size is not None and microbatch_size <= 0:
         raise ConfigurationError(f"microbatch_size must be positive, got {microbatch_size}")
@@ -241,7 +295,8 @@ def _make_clipped_fun(fun, has_aux, *, batch_argnums, clipping_norm, normalize_b
             values = vmap(fun, in_dims=in_dims, out_dims=0, randomness="same")(*args, **kwargs)
             aux = None
         res = _clip_sum_values(values, clipping_norm, scale, dtype=out_dtype,
-                               with_postsq=return_aux, second_moment=second_moment)
+                               with_postsq=return_aux, second_moment=second_moment,
+                               compute_dtype=compute_dtype, output_dtype=dtype)
         res.aux = aux
         return res
 
@@ -258,12 +313,14 @@ def _make_clipped_fun(fun, has_aux, *, batch_argnums, clipping_norm, normalize_b
                 res = run_chunk(args, kwargs, dtype)
                 reduced, squared = res.reduced, res.squared
             else:
-                # Chunk sums are accumulated in float32 and cast once at the end
-                # (_microbatch_accumulate_reduced, _clipped_fun.py:252-345).
+                # Chunk sums are accumulated in the wider of the compute and
+                # output dtypes (float32 for bfloat16 leaves by default) and
+                # cast once at the end (_microbatch_accumulate_reduced,
+                # _clipped_fun.py:252-345).
                 acc, acc_sq, parts = None, None, []
                 for start in range(0, B, microbatch_size):
                     chunk = _slice_args(args, batch_argnums, start, min(B, start + microbatch_size))
-                    r = run_chunk(chunk, kwargs, torch.float32)
+                    r = run_chunk(chunk, kwargs, _ACCUMULATE)
                     acc = r.reduced if acc is None else tree_map(torch.add, acc, r.reduced)
                     if second_moment:
                         acc_sq = (r.squared if acc_sq is None
@@ -334,24 +391,29 @@ def clipped_fun(
         raise ConfigurationError(f"normalize_by must be > 0, got {normalize_by}.")
     if return_aux and return_stats:
         raise ConfigurationError("return_stats cannot be combined with return_aux=True")
-    if compute_dtype is not None:
-        raise OperationError("an explicit compute_dtype is not implemented by the HIP clip-and-sum")
     _validate_clipping_norm(clipping_norm)
     state = FixedClipState()
     fn = _make_clipped_fun(fun, has_aux, batch_argnums=batch_argnums, clipping_norm=clipping_norm,
                            normalize_by=normalize_by, return_aux=return_aux,
                            return_stats=return_stats, microbatch_size=microbatch_size,
                            dtype=dtype, scale=_Scale("fixed"), state=state,
-                           second_moment=second_moment)
+                           second_moment=second_moment, compute_dtype=compute_dtype)
     return fn, state
 
 
-def _grad_wrapper(loss_fn, argnums, has_aux, return_aux):
-    """Per-example ``grad_and_value`` returning ``g`` or ``(g, {"values", "value_aux"})``."""
+def _identity(x):
+    return x
+
+
+def _grad_wrapper(loss_fn, argnums, has_aux, return_aux, pre_clipping_transform=_identity):
+    """Per-example ``grad_and_value`` returning ``g`` or ``(g, {"values", "value_aux"})``;
+    ``g`` is the per-example gradient after ``pre_clipping_transform``
+    (``_clipped_grad.py:278-296``)."""
     gv = grad_and_value(loss_fn, argnums=argnums, has_aux=has_aux)
 
     def grad_fn(*args, **kwargs):
         g, out = gv(*args, **kwargs)
+        g = pre_clipping_transform(g)
         if not return_aux:
             return g
         if has_aux:
@@ -364,24 +426,31 @@ def _grad_wrapper(loss_fn, argnums, has_aux, return_aux):
 
 def _make_grad(loss_fn, argnums, has_aux, *, clipping_norm, normalize_by, batch_argnums,
                return_aux, return_stats, microbatch_size, dtype, scale, state,
-               second_moment=False):
+               second_moment=False, compute_dtype=None, pre_clipping_transform=_identity):
     _validate_static_args(argnums, batch_argnums, normalize_by)
     if return_aux and return_stats:
         raise ConfigurationError("return_stats cannot be combined with return_aux=True")
     argnums_t = argnums if isinstance(argnums, int) else tuple(argnums)
-    grad_fn = _grad_wrapper(loss_fn, argnums_t, has_aux, return_aux)
+    grad_fn = _grad_wrapper(loss_fn, argnums_t, has_aux, return_aux, pre_clipping_transform)
     inner = _make_clipped_fun(grad_fn, return_aux, batch_argnums=batch_argnums,
                               clipping_norm=clipping_norm, normalize_by=normalize_by,
                               return_aux=return_aux, return_stats=return_stats,
                               microbatch_size=microbatch_size, dtype=dtype, scale=scale,
-                              state=state, second_moment=second_moment)
+                              state=state, second_moment=second_moment,
+                              compute_dtype=compute_dtype)
     batch_t = _to_tuple(batch_argnums)
     max_norm = clipping_norm / normalize_by
 
     def wrapper(*args, state, **kwargs):
         if _batch_size(args, batch_t) == 0:
-            zeros = tree_map(torch.zeros_like, args[argnums_t] if isinstance(argnums_t, int)
-                             else tuple(args[i] for i in argnums_t))
+            # Zeros in the transformed gradient schema (empty_clipped_grads_like,
+            # _helpers.py:95-122): the transform fixes structure, shape, device
+            # and default dtype.
+            template = pre_clipping_transform(tree_map(
+                torch.zeros_like, args[argnums_t] if isinstance(argnums_t, int)
+                else tuple(args[i] for i in argnums_t)))
+            zeros = tree_map(lambda x: torch.zeros_like(x, dtype=dtype)
+                             if isinstance(x, torch.Tensor) else x, template)
             grads = clipped(zeros, max_norm=max_norm)
             if second_moment:
                 grads = SecondMomentClippingOutput(
@@ -430,6 +499,7 @@ def clipped_grad(
     return_aux: bool = False,
     return_stats: bool = False,
     second_moment: bool = False,
+    pre_clipping_transform: Callable = _identity,
     microbatch_size: int | None = None,
     dtype: torch.dtype | None = None,
     compute_dtype: torch.dtype | None = None,
@@ -439,16 +509,18 @@ def clipped_grad(
     With ``second_moment`` the result is a ``SecondMomentClippingOutput``: the
     clipped sum and the sum of the squared clipped per-example gradients, with
     ``max_norm`` ``C / normalize_by`` and ``C^2 / normalize_by``.
+    ``pre_clipping_transform`` maps each example's gradient pytree to the
+    pytree that is clipped (e.g. a preconditioner scaling); ``compute_dtype``
+    is the reduction dtype (float32, or bfloat16 with bfloat16 gradients).
     """
-    if compute_dtype is not None:
-        raise OperationError("an explicit compute_dtype is not implemented by the HIP clip-and-sum")
     _validate_clipping_norm(clipping_norm)
     state = FixedClipState()
     fn = _make_grad(loss_fn, argnums, has_aux, clipping_norm=clipping_norm,
                     normalize_by=normalize_by, batch_argnums=batch_argnums,
                     return_aux=return_aux, return_stats=return_stats,
                     microbatch_size=microbatch_size, dtype=dtype, scale=_Scale("fixed"),
-                    state=state, second_moment=second_moment)
+                    state=state, second_moment=second_moment, compute_dtype=compute_dtype,
+                    pre_clipping_transform=pre_clipping_transform)
     return fn, state
 
 
@@ -463,11 +535,13 @@ def auto_clipped_grad(
     batch_argnums: int | tuple[int, ...] = 1,
     return_aux: bool = False,
     return_stats: bool = False,
+    pre_clipping_transform: Callable = _identity,
     microbatch_size: int | None = None,
     dtype: Any = None,
     second_moment: bool = False,
 ):
-    """AUTO-S: ``R * g_i / (||g_i|| + gamma)`` per example, summed (``_auto.py:211-367``)."""
+    """AUTO-S: ``R * g_i / (||g_i|| + gamma)`` per example, summed (``_auto.py:211-367``);
+    ``pre_clipping_transform`` as in :func:`clipped_grad`."""
     if isinstance(gamma, bool) or not isinstance(gamma, (int, float)) or not gamma > 0:
         raise ConfigurationError(f"gamma must be a positive float, got {gamma!r}")
     _validate_clipping_norm(R, "R")
@@ -476,7 +550,7 @@ def auto_clipped_grad(
                     batch_argnums=batch_argnums, return_aux=return_aux,
                     return_stats=return_stats, microbatch_size=microbatch_size, dtype=dtype,
                     scale=_Scale("auto_s", float(gamma)), state=state,
-                    second_moment=second_moment)
+                    second_moment=second_moment, pre_clipping_transform=pre_clipping_transform)
     return fn, state
 
 

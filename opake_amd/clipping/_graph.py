@@ -23,14 +23,17 @@ Rules, as in the reference:
   noise key changes every step, a replayed graph would repeat it).
 
 Every device table a kernel reads comes from a content-keyed cache that keeps
-its pinned host source alive, so the recorded copies stay valid; the leaf,
-norm, clip-factor and clipped-sum kernels record no memset.
+its pinned host source alive, so the recorded copies stay valid; each graph
+entry also holds every table its capture used, so none is freed while the
+graph can replay; the leaf, norm, clip-factor and clipped-sum kernels record
+no memset.
 """
 
 from __future__ import annotations
 
 import torch
 
+from opake_amd import _tables
 from opake_amd.clipping._model import DirectCapture, LinearCapture, ghost_clip_captured
 from opake_amd.exceptions import ConfigurationError
 from opake_amd.types import clipped
@@ -119,11 +122,14 @@ class GraphedGhostClip:
             if self._pool is None:
                 self._pool = torch.cuda.graph_pool_handle()
             graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, pool=self._pool):
+            # The device tables the captured kernels read (cache hits made
+            # during warm-up included) stay referenced by the entry, so a
+            # later eviction from the table cache cannot free them.
+            with _tables.keep_alive() as tables, torch.cuda.graph(graph, pool=self._pool):
                 out = self._eager(static)
             torch.cuda.synchronize()
         self.captures += 1
-        return graph, static, out
+        return graph, static, out, tables
 
     def __call__(self, captures):
         key = _signature(captures)
@@ -132,7 +138,7 @@ class GraphedGhostClip:
             if self.captures >= self.max_graphs:
                 return self._eager(captures)
             entry = self._graphs[key] = self._capture(captures)
-        graph, static, out = entry
+        graph, static, out, _ = entry
         torch._foreach_copy_(_tensors(static), [t.detach() for t in _tensors(captures)])
         graph.replay()
         self.replays += 1

@@ -17,9 +17,11 @@ number of HIP launches per storage dtype, whatever the number of leaves:
 
 Per-group clipping norms (``PerGroup``) clip each group to its own bound by
 its own norm, with one scale row per group; ``second_moment`` adds the batch
-sums of the squared stored values.  A call the kernels do not cover (an
-explicit ``compute_dtype``, dtypes other than float32 / bfloat16, leaves that
-need grad) goes to the ``fallback`` the caller registered with
+sums of the squared stored values.  An explicit ``compute_dtype`` of float32,
+or of bfloat16 with bfloat16 leaves, follows the reference's reduction and
+multiply dtypes.  A call the kernels do not cover (another ``compute_dtype``,
+dtypes other than float32 / bfloat16, leaves that need grad) goes to the
+``fallback`` the caller registered with
 :func:`make_fused_backend` -- in the reference that is its own PyTorch
 streaming path -- and raises ``OperationError`` when there is none.
 """
@@ -71,8 +73,12 @@ def unsupported_reason(leaves, clipping_norm, scale, *, compute_dtype, second_mo
     """Why the kernels cannot serve this call, or ``None``."""
     if getattr(scale, "kind", "fixed") not in ("fixed", "auto_s"):
         return f"unknown scale kind {scale.kind!r}"
-    if compute_dtype is not None:
-        return "an explicit compute_dtype is not supported"
+    if compute_dtype is not None and compute_dtype != torch.float32:
+        if compute_dtype != torch.bfloat16:
+            return f"compute_dtype {compute_dtype} (supported: float32, or bfloat16 with " \
+                   "bfloat16 leaves)"
+        if any(isinstance(l, torch.Tensor) and l.dtype != torch.bfloat16 for l in leaves):
+            return "compute_dtype bfloat16 needs bfloat16 leaves"
     if batch_size > _MAX_BATCH:
         return f"batch size {batch_size} exceeds {_MAX_BATCH}"
     grad_mode = torch.is_grad_enabled()
@@ -202,9 +208,10 @@ class LeafBatch:
     def dtypes(self):
         return [g["dtype"] for g in self.plan["groups"]]
 
-    def sqnorms(self) -> torch.Tensor:
+    def sqnorms(self, acc_dtype: torch.dtype = torch.float32) -> torch.Tensor:
         """Per-leaf squared norms float64 [B, L] (``_leaf_sq_sum``: sanitised,
-        squared in float32, summed in float64 per 2048-element tile)."""
+        squared in ``acc_dtype`` -- float32, or bfloat16 for bfloat16 leaves --
+        summed in float64 per 2048-element tile)."""
         B, L = self.B, self.L
         stream = nat.stream_handle(self.device)
         leaf_sq = torch.empty((B, L), dtype=torch.float64, device=self.device)
@@ -213,7 +220,8 @@ class LeafBatch:
             nat.call("dpc_leaves_sqnorm", nat.ptr(ptrs), nat.ptr(g["sizes"]),
                      nat.ptr(g["tile_leaf"]), nat.ptr(g["tile_local"]), nat.ptr(g["tile_start"]),
                      nat.ptr(g["leaf_col"]), len(g["idx"]), g["n_tiles"], B,
-                     nat.dtype_code(g["dtype"]), nat.ptr(partial), nat.ptr(leaf_sq), L, stream)
+                     nat.dtype_code(g["dtype"]), nat.dtype_code(acc_dtype), nat.ptr(partial),
+                     nat.ptr(leaf_sq), L, stream)
         return leaf_sq
 
     def apply(self, scale_rows: dict, leaf_rows=None, out_dtypes=None, with_postsq=False,
@@ -261,7 +269,8 @@ class LeafBatch:
 
 def leaves_clip_sum(leaves, clipping_norm, *, kind: str = "fixed", gamma: float = 0.0,
                     with_postsq: bool = False, out_dtypes=None, leaf_groups=None,
-                    conservative: bool = True, second_moment: bool = False):
+                    conservative: bool = True, second_moment: bool = False,
+                    compute_dtype: torch.dtype | None = None):
     """Clip-and-sum of stacked leaves ``[B, *P]`` with the HIP kernels.
 
     ``clipping_norm`` is one bound, or -- with ``leaf_groups`` (group index of
@@ -270,7 +279,11 @@ def leaves_clip_sum(leaves, clipping_norm, *, kind: str = "fixed", gamma: float 
     ``out_dtypes[dtype]`` (default: the leaf dtype).  ``conservative`` rounds
     each bound down to float32 first, as the reference's batch path does
     (``_clipped_fun.py:211-216``); the single-pytree functions use the exact
-    bound (``_pytree.py:624-628``).  See :class:`LeafClipResult`.
+    bound (``_pytree.py:624-628``).  ``compute_dtype`` (float32, or bfloat16
+    with bfloat16 leaves) is the reference's explicit reduction dtype
+    (``_pytree.py:84-108``): squares in it, the guard's roundoff from it, and
+    the scale multiply in ``promote(leaf dtype, compute_dtype)`` (``_pytree.py:
+    160-187``).  See :class:`LeafClipResult`.
     """
     batch = LeafBatch(leaves)
     device, B, L = batch.device, batch.B, batch.L
@@ -278,14 +291,16 @@ def leaves_clip_sum(leaves, clipping_norm, *, kind: str = "fixed", gamma: float 
     bounds = list(clipping_norm) if grouped else [clipping_norm]
     n_groups = len(bounds)
     stream = nat.stream_handle(device)
-    acc = torch.float32
+    acc = num.compute_dtype_for_reduction(batch.dtypes, compute_dtype)
     roundoff = num.norm_roundoff(acc, torch.float64, L,
                                  num.reduction_terms([math.prod(l.shape[1:]) for l in leaves]))
-    leaf_sq = batch.sqnorms()
+    leaf_sq = batch.sqnorms(acc)
     sq = torch.empty(B, dtype=torch.float64, device=device)
     nat.call("dpc_row_sum_f64", nat.ptr(leaf_sq), B, L, 0, nat.ptr(sq), stream)
-    guards = [num.guard_constants(dt, torch.promote_types(dt, acc), roundoff)
-              for dt in batch.dtypes]
+    guards = []
+    for dt in batch.dtypes:
+        mult = torch.promote_types(dt, acc)
+        guards.append((*num.guard_constants(dt, mult, roundoff), mult == torch.bfloat16))
     scale_kind = nat.SCALE_AUTO_S if kind == "auto_s" else nat.SCALE_FIXED
     bound_of = num.conservative_bound if conservative else float
     if grouped:
@@ -360,10 +375,17 @@ def make_fused_backend(fallback=None):
         reason = unsupported_reason(leaves, clipping_norm, scale, compute_dtype=compute_dtype,
                                     second_moment=second_moment, batch_size=batch_size)
         out_dtypes = None
+        cast_to = None
         if reason is None and leaves and batch_size > 0:
-            out_dtypes = _output_dtypes(leaves, reduce_leaf)
-            if out_dtypes is None:
-                reason = "the requested output dtype is not supported"
+            if compute_dtype == torch.bfloat16:
+                # The reference sums in the compute dtype and casts after
+                # (_sum_clipped_tensor, _clipped_fun.py:114-132).
+                cast_to = {torch.bfloat16: reduce_leaf(
+                    torch.zeros((1,), dtype=torch.bfloat16, device=leaves[0].device)).dtype}
+            else:
+                out_dtypes = _output_dtypes(leaves, reduce_leaf)
+                if out_dtypes is None:
+                    reason = "the requested output dtype is not supported"
         if reason is not None:
             if fallback is None:
                 raise OperationError(f"HIP clip-and-sum cannot serve this call: {reason}")
@@ -388,13 +410,18 @@ def make_fused_backend(fallback=None):
                 names, leaf_groups, bounds = _group_layout(paths, clipping_norm)
                 res = leaves_clip_sum(leaves, bounds, kind=kind, gamma=gamma,
                                       with_postsq=return_aux, out_dtypes=out_dtypes,
-                                      leaf_groups=leaf_groups, second_moment=second_moment)
+                                      leaf_groups=leaf_groups, second_moment=second_moment,
+                                      compute_dtype=compute_dtype)
             else:
                 res = leaves_clip_sum(leaves, float(clipping_norm), kind=kind, gamma=gamma,
                                       with_postsq=return_aux, out_dtypes=out_dtypes,
-                                      second_moment=second_moment)
+                                      second_moment=second_moment, compute_dtype=compute_dtype)
             reduced, norms, post, group_norms = res.reduced, res.norms, res.post_sq, res.group_norms
             squared = res.squared
+            if cast_to is not None:
+                reduced = [x.to(cast_to[l.dtype]) for x, l in zip(reduced, leaves)]
+                if second_moment:
+                    squared = [x.to(cast_to[l.dtype]) for x, l in zip(squared, leaves)]
         diagnostics = {}
         if return_aux or return_stats:
             diagnostics["norms"] = norms.detach()

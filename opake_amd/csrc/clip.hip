@@ -8,7 +8,8 @@
 //   up = sqrt(max(sq + err, 0));  norm = sqrt(max(sq, 0))
 //   ratio = max(C,0)/up  or  max(R,0)/(up + gamma)               (AUTO-S)
 //   s = ratio * rel - abs;  s = min(1, s) (fixed only; NaN stays NaN)
-//   s = isfinite(s) ? max(s, 0) : 0;  stored as float32.
+//   s = isfinite(s) ? max(s, 0) : 0;  stored as float32 (or, for a guard whose
+//   multiply dtype is bf16, rounded to the nearest bf16 first).
 // `norm` (the estimate) is what the statistics report and count.  Every step
 // is one IEEE operation in the order written (contraction off), so the result
 // matches a host float64 evaluation bit for bit.
@@ -23,7 +24,21 @@ constexpr int kMaxGuards = 4;
 struct Guards {
   double rel[kMaxGuards];
   double abs_[kMaxGuards];
+  int bf16[kMaxGuards];  // scale stored as a bf16 value (multiply in bf16)
 };
+
+// A non-negative double rounded to the nearest bf16 (ties to even), returned
+// as the float of that value: rounded to float32 with round-to-odd first
+// (float32 keeps 16 more bits than bf16, so the second rounding is exact).
+__device__ float round_scale_to_bf16(double s) {
+  float f = (float)s;
+  if ((double)f != s && f != 0.0f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 1u) == 0u) u = ((double)f > s) ? u - 1u : u + 1u;
+    f = __builtin_bit_cast(float, u);
+  }
+  return round_to_bf16(f);
+}
 
 #pragma clang fp contract(off)
 __device__ double guarded_scale(double sq, double err, double C, int kind, double gamma,
@@ -75,7 +90,7 @@ clip_factors_kernel(const double* __restrict__ sqnorm, const double* __restrict_
         double norm;
         const double s = guarded_scale(sqnorm[i], sqerr ? sqerr[i] : 0.0, C, kind, gamma,
                                        guards.rel[g], guards.abs_[g], &norm);
-        const float sf = (float)s;
+        const float sf = guards.bf16[g] ? round_scale_to_bf16(s) : (float)s;
         if (scale) scale[(size_t)g * B + i] = sf;
         if (g == 0) {
           if (norms_out) norms_out[i] = (float)norm;
@@ -129,9 +144,10 @@ extern "C" size_t dpc_clip_plan_bytes(int B) { return clip_plan_bytes(B); }
 
 extern "C" int dpc_clip_factors(const double* sqnorm, const double* sqerr, int B, double C,
                                 int kind, double gamma,
-                                const double* guard_rel, const double* guard_abs, int n_guards,
-                                float count_threshold, float* scale, float* norms_out,
-                                int* nclipped, void* plan, void* stream) {
+                                const double* guard_rel, const double* guard_abs,
+                                const int* guard_bf16, int n_guards, float count_threshold,
+                                float* scale, float* norms_out, int* nclipped, void* plan,
+                                void* stream) {
   if (B < 0 || n_guards < 1 || n_guards > kMaxGuards || !guard_rel || !guard_abs) {
     return DPC_EINVAL;
   }
@@ -142,6 +158,7 @@ extern "C" int dpc_clip_factors(const double* sqnorm, const double* sqerr, int B
   for (int g = 0; g < n_guards; ++g) {
     guards.rel[g] = guard_rel[g];
     guards.abs_[g] = guard_abs[g];
+    guards.bf16[g] = guard_bf16 ? guard_bf16[g] != 0 : 0;
   }
   hipLaunchKernelGGL(clip_factors_kernel, dim3(1), dim3(kClipThreads), 0, (hipStream_t)stream,
                      sqnorm, sqerr, B, C, kind, gamma, guards, n_guards, count_threshold,

@@ -85,9 +85,17 @@ __device__ __forceinline__ bool tile_vectorizable(int64_t base, int64_t n, int64
 // value is sanitised, squared in fp32 (rounded), widened and added in fp64,
 // and the wave's fp64 partials are folded by a fixed shuffle tree.  The
 // order of the fp64 additions inside a tile is fixed, so results are
-// deterministic.
+// deterministic.  kSqBf16 (bf16 leaves, the reference's explicit
+// compute_dtype=bfloat16): each square is rounded to bf16, as x * x in bf16
+// is, before the fp64 sum.
 #pragma clang fp contract(off)
-template <bool kBf16>
+template <bool kSqBf16>
+__device__ __forceinline__ float square_in(float x) {
+  const float sq = x * x;
+  return kSqBf16 ? round_to_bf16(sq) : sq;
+}
+
+template <bool kBf16, bool kSqBf16 = false>
 __global__ void __launch_bounds__(kThreads)
 tile_sq_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ sizes,
                const int32_t* __restrict__ tile_leaf, const int32_t* __restrict__ tile_local,
@@ -117,7 +125,7 @@ tile_sq_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ siz
 #pragma unroll
       for (int k = 0; k < kPerChunk; ++k) {
         const float x = finite_or_zero(v[k]);
-        const float sq = x * x;
+        const float sq = square_in<kSqBf16>(x);
         s += (double)sq;
       }
     }
@@ -126,7 +134,7 @@ tile_sq_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ siz
       const int64_t off = off0 + e;
       if (off < n) {
         const float x = elem_f32<kBf16>(base, (int64_t)b * n + off);
-        const float sq = x * x;
+        const float sq = square_in<kSqBf16>(x);
         s += (double)sq;
       }
     }
@@ -363,10 +371,13 @@ extern "C" int dpc_group_sum_f64(const double* x, int B, int n, int stride,
 extern "C" int dpc_leaves_sqnorm(const int64_t* ptrs, const int64_t* sizes,
                                  const int32_t* tile_leaf, const int32_t* tile_local,
                                  const int64_t* tile_start, const int32_t* leaf_col,
-                                 int n_leaves, int n_tiles, int B, int dtype, double* partial,
-                                 double* leaf_sq, int leaf_sq_stride, void* stream) {
+                                 int n_leaves, int n_tiles, int B, int dtype,
+                                 int square_dtype, double* partial, double* leaf_sq,
+                                 int leaf_sq_stride, void* stream) {
   if (n_leaves < 0 || n_tiles < 0 || B < 0 || leaf_sq_stride < n_leaves) return DPC_EINVAL;
   if (dtype != DPC_F32 && dtype != DPC_BF16) return DPC_EINVAL;
+  if (square_dtype != DPC_F32 && !(square_dtype == DPC_BF16 && dtype == DPC_BF16))
+    return DPC_EINVAL;
   if (B == 0 || n_leaves == 0) return DPC_OK;
   if (!ptrs || !sizes || !tile_leaf || !tile_local || !tile_start || !leaf_col || !partial ||
       !leaf_sq)
@@ -377,7 +388,10 @@ extern "C" int dpc_leaves_sqnorm(const int64_t* ptrs, const int64_t* sizes,
     const long long units = (long long)n_tiles * B;
     const long long blocks = (units + kThreads / 64 - 1) / (kThreads / 64);
     if (blocks > 0x7fffffffLL) return DPC_ENOTSUP;
-    if (dtype == DPC_BF16) {
+    if (dtype == DPC_BF16 && square_dtype == DPC_BF16) {
+      hipLaunchKernelGGL((tile_sq_kernel<true, true>), dim3((unsigned)blocks), dim3(kThreads), 0,
+                         s, ptrs, sizes, tile_leaf, tile_local, n_tiles, units, partial);
+    } else if (dtype == DPC_BF16) {
       hipLaunchKernelGGL(tile_sq_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), 0, s,
                          ptrs, sizes, tile_leaf, tile_local, n_tiles, units, partial);
     } else {

@@ -134,9 +134,11 @@ def clip_factors(
 ) -> ClipFactors:
     """Guarded clip factors for each ``(rel, abs)`` guard, per example.
 
-    ``err`` (float64 [B], optional): the error bound of ``sqnorm``; the scale
-    is then taken from ``sqrt(sqnorm + err)``, the reported norms and the
-    clipped count from ``sqrt(sqnorm)``."""
+    A guard may carry a third element: true when its multiply dtype is
+    bfloat16, so that the scale is rounded to the nearest bfloat16.  ``err``
+    (float64 [B], optional): the error bound of ``sqnorm``; the scale is then
+    taken from ``sqrt(sqnorm + err)``, the reported norms and the clipped count
+    from ``sqrt(sqnorm)``."""
     dev = nat.require_device(sqnorm, err)
     if sqnorm.dtype != torch.float64 or sqnorm.dim() != 1:
         raise ConfigurationError("sqnorm must be a float64 vector")
@@ -148,13 +150,14 @@ def clip_factors(
     n = len(guards)
     rel = (ctypes.c_double * n)(*[g[0] for g in guards])
     abs_ = (ctypes.c_double * n)(*[g[1] for g in guards])
+    bf16 = (ctypes.c_int * n)(*[int(bool(g[2])) if len(g) > 2 else 0 for g in guards])
     scale = torch.empty((n, B), dtype=torch.float32, device=dev)
     norms = torch.empty(B, dtype=torch.float32, device=dev)
     nclipped = torch.empty(1, dtype=torch.int32, device=dev)
     plan = torch.empty((n, nat.load().dpc_clip_plan_bytes(B)), dtype=torch.uint8, device=dev)
     nat.call(
         "dpc_clip_factors", nat.ptr(_contig(sqnorm)), nat.ptr(None if err is None else _contig(err)),
-        B, float(clipping_norm), kind, float(gamma), rel, abs_, n, float(count_threshold),
+        B, float(clipping_norm), kind, float(gamma), rel, abs_, bf16, n, float(count_threshold),
         nat.ptr(scale), nat.ptr(norms), nat.ptr(nclipped), nat.ptr(plan), nat.stream_handle(dev),
     )
     return ClipFactors(scale=scale, norms=norms, nclipped=nclipped, plan=plan)

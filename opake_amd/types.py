@@ -180,12 +180,14 @@ class ClippedPytree:
     def __add__(self, o):
         raise InputTypeError(_unsupported("addition"))
 
-    __radd__ = __add__
+    def __radd__(self, o):
+        raise InputTypeError(_unsupported("addition"))
 
     def __sub__(self, o):
         raise InputTypeError(_unsupported("subtraction"))
 
-    __rsub__ = __sub__
+    def __rsub__(self, o):
+        raise InputTypeError(_unsupported("subtraction"))
 
     def __pow__(self, o):
         raise InputTypeError(_unsupported("power"))

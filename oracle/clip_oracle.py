@@ -210,7 +210,10 @@ def stream_clip_and_sum(leaves, clipping_norm, *, kind="fixed", gamma=0.0, group
             x = stored.to(acc)
             post_sq = post_sq + (x * x).reshape(B, -1).sum(dim=1, dtype=acc)
         out_dtype = (reduce_dtype or {}).get(leaf.dtype, leaf.dtype)
-        accum = torch.float32 if leaf.dtype in (torch.float16, torch.bfloat16) else None
+        # _resolve_compute_dtype (_clipped_fun.py:91-111): an explicit
+        # compute dtype, else float32 for float16 / bfloat16.
+        accum = compute_dtype if compute_dtype is not None else (
+            torch.float32 if leaf.dtype in (torch.float16, torch.bfloat16) else None)
         summed = torch.sum(stored, dim=0, dtype=accum)
         reduced.append(summed.to(out_dtype))
         if second_moment:

@@ -38,3 +38,27 @@ def test_version_and_size_queries():
     assert lib.dpc_clip_plan_bytes(32) == 16 + 32 * 4
     assert lib.dpc_gram_workspace_bytes(0, 5) == 0
     assert lib.dpc_gram_workspace_bytes(2, 128) > 0
+
+
+def test_tables_used_under_keep_alive_survive_eviction():
+    # A graph owner holds the tables its capture used: filling the content
+    # cache past its bound afterwards evicts the cache's entries but not the
+    # owner's references (CPU tables: the cache logic is device-independent).
+    import gc
+    import weakref
+
+    from opake_amd import _tables
+
+    with _tables.keep_alive() as kept:
+        t1 = _tables.device_table([1, 2, 3], "int32", "cpu")
+        t2 = _tables.device_table([1, 2, 3], "int32", "cpu")  # a cache hit
+    assert t1 is t2 and any(x is t1 for x in kept)
+    ref = weakref.ref(t1)
+    del t1, t2
+    for i in range(_tables._MAX_ENTRIES + 10):
+        _tables.device_table([i, i + 1, 7777], "int32", "cpu")
+    gc.collect()
+    assert ref() is not None  # evicted from the cache, alive through `kept`
+    del kept
+    gc.collect()
+    assert ref() is None
