@@ -93,6 +93,39 @@ def make_inputs(device, b=B, t=T, din=DIN, dout=DOUT, seed=0):
     return A, G
 
 
+CPU_REPEATS = 5  # timed CPU-baseline steps (median) after one warm-up
+
+
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: every CPU this process may run on,
+    capped by OMP_NUM_THREADS when the environment sets it (the GPU box sets
+    it to the host share of one GPU)."""
+    visible = len(os.sched_getaffinity(0))
+    try:
+        share = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        share = 0
+    return min(visible, share) if share > 0 else visible
+
+
+def cpu_host() -> str:
+    """CPU model and the CPUs visible to the process, for the baseline line."""
+    return f"{cpu_model()}; {len(os.sched_getaffinity(0))} CPUs visible"
+
+
+def median_rate(step, examples: int, repeats: int = CPU_REPEATS) -> float:
+    """Examples/s of ``step`` (``examples`` per call): one warm-up call, then
+    the median of ``repeats`` timed calls."""
+    step()
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return examples / times[len(times) // 2]
+
+
 def cpu_baseline(sample_b: int, threads: int):
     """Reference restatement on the CPU (oracle package), examples/s."""
     import torch
@@ -110,14 +143,7 @@ def cpu_baseline(sample_b: int, threads: int):
         draw = noise_oracle.draws_for([center], seed)[0]
         return noise_oracle.sample(center, NM * C, draw)
 
-    step()  # warm-up
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    return sample_b / times[len(times) // 2]
+    return median_rate(step, sample_b)
 
 
 def measured_traffic(kernel: str):
@@ -163,16 +189,59 @@ def sustained_mfma_tflops(device, iters: int = 16384) -> float:
     return flops / min(times) / 1e12
 
 
-def add_sustained(roofline: dict, device) -> dict:
-    """Adds the measured sustained bf16 MFMA ceiling to a bf16 MFMA roofline."""
+SUSTAINED_METHOD = ("dpc_calib_mfma_bf16 in this run: random N(0,1) bf16 operands, 2 "
+                    "workgroups of 8 waves per CU, back-to-back 32x32x16 MFMAs (best of 3 "
+                    "launches); context only, the roofline fraction is against `peak`")
+
+
+def add_sustained(roofline: dict, device, sustained: float | None = None) -> dict:
+    """Adds the measured sustained bf16 MFMA rate to a bf16 MFMA roofline as
+    context (``frac`` stays against the published peak)."""
     if roofline.get("bound") == "mfma" and roofline.get("peak") == MFMA_BF16_PEAK_TFLOPS:
-        sus = sustained_mfma_tflops(device)
-        roofline["sustained_peak"] = sus
-        roofline["frac_of_sustained"] = roofline["achieved"] / sus
-        roofline["sustained_method"] = (
-            "dpc_calib_mfma_bf16 in this run: random N(0,1) bf16 operands, 2 workgroups of "
-            "8 waves per CU, back-to-back 32x32x16 MFMAs (best of 3 launches)")
+        roofline["sustained_mfma_tflops"] = (sustained if sustained is not None
+                                             else sustained_mfma_tflops(device))
+        roofline["sustained_method"] = SUSTAINED_METHOD
     return roofline
+
+
+def library_reference(A, G, reps: int = 10) -> dict:
+    """Same-box library time of the identical GEMM: sum over the B*T rows of
+    G^T A (bf16 in, bf16 out, fp32 accumulation, no scales, no epilogue) by
+    ``torch.mm`` (hipBLASLt / rocBLAS on ROCm), median of ``reps`` launches
+    after 3 warm-ups -- in the operands' own layout (m- and n-contiguous rows,
+    the reduction dimension slow) and with K-contiguous copies of both."""
+    import torch
+
+    rows = A.shape[0] * A.shape[1]
+    din, dout = A.shape[2], G.shape[2]
+    G2, A2 = G.reshape(rows, dout), A.reshape(rows, din)
+
+    def median_ms(fn):
+        for _ in range(3):
+            fn()
+        times = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            b.synchronize()
+            times.append(a.elapsed_time(b))
+        times.sort()
+        return times[len(times) // 2]
+
+    natural = median_ms(lambda: torch.mm(G2.t(), A2))
+    Gt, At = G2.t().contiguous(), A2.t().contiguous()
+    kcontig = median_ms(lambda: torch.mm(Gt, At.t()))
+    del Gt, At
+    flops = 2.0 * rows * din * dout
+    return {
+        "op": "torch.mm (hipBLASLt): G^T A over B*T rows, bf16 -> bf16, fp32 accumulation",
+        "natural_layout_ms": natural,
+        "natural_layout_tflops": flops / (natural * 1e-3) / 1e12,
+        "k_contiguous_copies_ms": kcontig,
+        "k_contiguous_copies_tflops": flops / (kcontig * 1e-3) / 1e12,
+    }
 
 
 def cpu_model() -> str:
@@ -273,9 +342,7 @@ def moe_cpu_baseline(threads: int):
         sig = NM * math.sqrt(C / math.sqrt(MOE_E) * C * math.sqrt(MOE_E))
         return [noise_oracle.sample(x, sig, z) for x, z in zip(res.reduced, draws)]
 
-    t0 = time.perf_counter()
-    step()
-    return 1.0 / (time.perf_counter() - t0)
+    return median_rate(step, 1)
 
 
 def run_moe(args) -> dict:
@@ -319,7 +386,7 @@ def run_moe(args) -> dict:
     gemm_tflops = gemm_f / (gemm_ms * 1e-3) / 1e12
     cpu = None
     if not args.no_cpu_baseline:
-        threads = min(len(os.sched_getaffinity(0)), 16)
+        threads = cpu_threads()
         print(f"[bench] cpu baseline: 1 example on {threads} threads", file=sys.stderr, flush=True)
         cpu = {
             "value": moe_cpu_baseline(threads),
@@ -328,7 +395,8 @@ def run_moe(args) -> dict:
             "kind": "port",
             "sample": ("config 5 at B=1: the example's per-expert gradients materialised from "
                        "its captured segments (16 leaves, 276.8M parameters), per-group "
-                       f"streaming clip-and-sum, CPU randn noise; one step; {cpu_model()}"),
+                       f"streaming clip-and-sum, CPU randn noise; median of {CPU_REPEATS} steps after 1 "
+                       f"warm-up; {cpu_host()}"),
         }
     return {
         "steps": steps,
@@ -403,14 +471,16 @@ def block_cpu_baseline(threads: int):
     g = torch.Generator().manual_seed(2)
     ids = torch.randint(0, BLK_V, (1, BLK_T), generator=g)
     tgt = torch.randint(0, BLK_V, (1, BLK_T), generator=g)
-    t0 = time.perf_counter()
-    per = ghost_oracle.per_example_grads_loop(model, per_example_lm_loss, (ids,), tgt)
-    names = sorted(per)
-    res = clip_oracle.stream_clip_and_sum([per[n] for n in names],
-                                          clip_oracle.conservative_bound(C))
-    draws = noise_oracle.draws_for(res.reduced, noise_oracle.step_seed(0, 0))
-    [noise_oracle.sample(x, NM * C, z) for x, z in zip(res.reduced, draws)]
-    return 1.0 / (time.perf_counter() - t0)
+
+    def step():
+        per = ghost_oracle.per_example_grads_loop(model, per_example_lm_loss, (ids,), tgt)
+        names = sorted(per)
+        res = clip_oracle.stream_clip_and_sum([per[n] for n in names],
+                                              clip_oracle.conservative_bound(C))
+        draws = noise_oracle.draws_for(res.reduced, noise_oracle.step_seed(0, 0))
+        return [noise_oracle.sample(x, NM * C, z) for x, z in zip(res.reduced, draws)]
+
+    return median_rate(step, 1)
 
 
 def run_block(args) -> dict:
@@ -470,7 +540,7 @@ def run_block(args) -> dict:
     gemm_tflops = gemm_f / (gemm_ms * 1e-3) / 1e12
     cpu = None
     if not args.no_cpu_baseline:
-        threads = min(len(os.sched_getaffinity(0)), 16)
+        threads = cpu_threads()
         print(f"[bench] cpu baseline: 1 example on {threads} threads", file=sys.stderr, flush=True)
         cpu = {
             "value": block_cpu_baseline(threads),
@@ -479,7 +549,8 @@ def run_block(args) -> dict:
             "kind": "port",
             "sample": ("config 3 at B=1 (float32): the example's per-parameter gradients by its "
                        "own forward and backward (67.1M block parameters), streaming "
-                       f"clip-and-sum, CPU randn noise; one step; {cpu_model()}"),
+                       f"clip-and-sum, CPU randn noise; median of {CPU_REPEATS} steps after 1 warm-up; "
+                       f"{cpu_host()}"),
         }
     return {
         "steps": steps,
@@ -527,7 +598,7 @@ def _mlp_ce(out, target):
     return torch.nn.functional.cross_entropy(out, target, reduction="none")
 
 
-def mlp_cpu_baseline(threads: int, repeats: int = 3):
+def mlp_cpu_baseline(threads: int, repeats: int = CPU_REPEATS):
     """The config-1 step as the reference runs it on the CPU: vmap(grad) of the
     per-example cross-entropy, the streaming clip-and-sum and the CPU-generator
     noise, at the full batch of 256.  Examples/s (median of ``repeats``)."""
@@ -551,14 +622,7 @@ def mlp_cpu_baseline(threads: int, repeats: int = 3):
         draws = noise_oracle.draws_for(res.reduced, noise_oracle.step_seed(0, 0))
         return [noise_oracle.sample(v, NM * C, z) for v, z in zip(res.reduced, draws)]
 
-    step()
-    times = []
-    for _ in range(repeats):
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    return MLP_B / times[len(times) // 2]
+    return median_rate(step, MLP_B, repeats)
 
 
 def run_mlp(args) -> dict:
@@ -618,15 +682,15 @@ def run_mlp(args) -> dict:
     flops = 2 * MLP_B * (784 * 512 + 512 * 10)  # clipped sums (flat layers)
     cpu = None
     if not args.no_cpu_baseline:
-        threads = min(len(os.sched_getaffinity(0)), 16)
+        threads = cpu_threads()
         cpu = {
             "value": mlp_cpu_baseline(threads),
             "unit": "examples/s",
             "cores": threads,
             "kind": "port",
             "sample": ("config 1 in full (B=256, float32): vmap(grad) of the per-example "
-                       "cross-entropy, streaming clip-and-sum, CPU randn noise; median of 3 "
-                       f"steps after 1 warm-up; {cpu_model()}"),
+                       "cross-entropy, streaming clip-and-sum, CPU randn noise; median of "
+                       f"{CPU_REPEATS} steps after 1 warm-up; {cpu_host()}"),
         }
     return {
         "steps": args.steps,
@@ -711,14 +775,16 @@ def lora_cpu_baseline(threads: int):
     g = torch.Generator().manual_seed(2)
     x = torch.randn(1, LORA_T, LORA_D, generator=g)
     tgt = torch.randn(1, LORA_T, LORA_D, generator=g)
-    t0 = time.perf_counter()
-    per = ghost_oracle.per_example_grads_loop(model, _mse_loss, (x,), tgt)
-    names = sorted(per)
-    res = clip_oracle.stream_clip_and_sum([per[n] for n in names],
-                                          clip_oracle.conservative_bound(C))
-    draws = noise_oracle.draws_for(res.reduced, noise_oracle.step_seed(0, 0))
-    [noise_oracle.sample(v, NM * C, z) for v, z in zip(res.reduced, draws)]
-    return 1.0 / (time.perf_counter() - t0)
+
+    def step():
+        per = ghost_oracle.per_example_grads_loop(model, _mse_loss, (x,), tgt)
+        names = sorted(per)
+        res = clip_oracle.stream_clip_and_sum([per[n] for n in names],
+                                              clip_oracle.conservative_bound(C))
+        draws = noise_oracle.draws_for(res.reduced, noise_oracle.step_seed(0, 0))
+        return [noise_oracle.sample(v, NM * C, z) for v, z in zip(res.reduced, draws)]
+
+    return median_rate(step, 1)
 
 
 def run_lora(args) -> dict:
@@ -774,7 +840,7 @@ def run_lora(args) -> dict:
     gbs = nbytes / (kern_ms * 1e-3) / 1e9
     cpu = None
     if not args.no_cpu_baseline:
-        threads = min(len(os.sched_getaffinity(0)), 16)
+        threads = cpu_threads()
         print(f"[bench] cpu baseline: 1 example on {threads} threads", file=sys.stderr, flush=True)
         cpu = {
             "value": lora_cpu_baseline(threads),
@@ -782,8 +848,8 @@ def run_lora(args) -> dict:
             "cores": threads,
             "kind": "port",
             "sample": ("config 4 at B=1 (float32): the 14 adapters' gradients by the example's "
-                       "own forward and backward, streaming clip-and-sum, CPU randn noise; one "
-                       f"step; {cpu_model()}"),
+                       "own forward and backward, streaming clip-and-sum, CPU randn noise; "
+                       f"median of {CPU_REPEATS} steps after 1 warm-up; {cpu_host()}"),
         }
     return {
         "steps": steps,
@@ -991,6 +1057,14 @@ def main() -> int:
     A, G = make_inputs(dev)
     noise_fn, state = gaussian_noise(noise_multiplier=NM, key=key(0), stream="device")
 
+    # Measurement preparation, before the warm-up steps: the sustained MFMA
+    # rate and the library reference of the same GEMM (~0.2 s of MFMA work,
+    # which also brings the GPU clocks to their loaded state).
+    sustained = sustained_mfma_tflops(dev)
+    lib_ref = library_reference(A, G)
+    print(f"[bench] preparation done: sustained {sustained:.0f} TFLOP/s, library GEMM "
+          f"{lib_ref['natural_layout_ms']:.3f} ms", file=sys.stderr, flush=True)
+
     gemm_events = []
 
     def step(st, record):
@@ -1024,7 +1098,7 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        threads = min(len(os.sched_getaffinity(0)), 16)
+        threads = cpu_threads()
         print(f"[bench] cpu baseline: {args.cpu_sample} examples on {threads} threads",
               file=sys.stderr, flush=True)
         rate = cpu_baseline(args.cpu_sample, threads)
@@ -1035,7 +1109,7 @@ def main() -> int:
             "kind": "port",
             "sample": (f"config 2 layer (4096x4096, T=512, bf16) at B={args.cpu_sample}: "
                        "vmap(grad) of the linear surrogate loss + streaming clip-and-sum + "
-                       f"CPU randn noise; median of 3 steps after 1 warm-up; {cpu_model()}"),
+                       f"CPU randn noise; median of {CPU_REPEATS} steps after 1 warm-up; {cpu_host()}"),
         }
 
     line = {
@@ -1075,10 +1149,13 @@ def main() -> int:
             "traffic": measured_traffic("clipped_sum_bf16_kernel"),
             "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1, "
                             "copy-calibrated; profiles/clipped_sum_cfg2_traffic.md)",
+            "library_reference": lib_ref,
         },
         "cpu_baseline": cpu,
+        "preparation": "sustained-MFMA measurement and library reference GEMM run before the "
+                       "warm-up steps",
     }
-    add_sustained(line["roofline"], dev)
+    add_sustained(line["roofline"], dev, sustained)
     print(json.dumps(line), flush=True)
     return 0
 
