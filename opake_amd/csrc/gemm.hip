@@ -5,7 +5,7 @@
 //
 // Fast path (bf16, T % 64 == 0, din % 8 == 0, dout % 8 == 0):
 //   * 256 x 256 output tile per workgroup, 8 waves (2 per SIMD) of 128 x 64,
-//     bf16 MFMA 32x32x16 with fp32 accumulators (8 blocks per wave);
+//     bf16 MFMA 16x16x32 with fp32 accumulators (32 blocks per wave);
 //   * both operands are m- (n-) contiguous in HBM and are staged into LDS in
 //     that natural [k][m] layout (64-byte blocks XOR-swizzled by the k row),
 //     straight from HBM (buffer_load ... lds).  The MFMA fragments, which
@@ -28,10 +28,13 @@
 //     Examples with scale 0 are skipped through the clip plan, so their data
 //     (including any NaN/Inf) is never read;
 //   * two LDS stages (128 KiB), one barrier per K step; the DMAs of step
-//     s + 1 are issued at the start of step s (grouped mode: the scale +
-//     store of G's step s + 1 is interleaved, chunk by chunk, with the MFMAs
-//     of step s, and each chunk's registers are refilled with step s + 2
-//     right after its store);
+//     s + 2 are issued right after the barrier of step s, the moment the
+//     stage is free (grouped mode: the scale + store of G's step s + 1 is
+//     interleaved, chunk by chunk, with the MFMAs of step s, and each
+//     chunk's registers are refilled with step s + 2 right after its store).
+//     In dense mode a chunk whose columns lie past the matrix reads the
+//     row's last 8 columns (they feed only outputs that are not stored), so
+//     every transfer is in range and a lane's DMA offsets are fixed;
 //   * workgroup ids are remapped so that each of the 8 XCDs owns a compact
 //     block of output tiles and re-reads operand tiles from its own L2.
 #include "common.h"
@@ -44,17 +47,27 @@ constexpr int kFastWaves = 8;
 
 // LDS layout of one operand tile for a 64-deep K step: 64 rows (k) of 256
 // bf16 (512 bytes), the row's eight 64-byte blocks permuted by XOR with
-// (k & 7).  A 16-lane group of a 16-byte store covers 4 consecutive blocks
-// of one row, and a 32-lane half of a transposing read covers one block in 4
-// consecutive rows: both land on 64 distinct banks.
+// (k & 7), and the two 32-byte halves of every block swapped in rows with
+// bit 2 of k set.  The 64 four-byte banks span 256 bytes, so blocks b and
+// b ^ 4 of a row share banks.  A 16-lane group of a 16-byte store covers 4
+// consecutive blocks of one row, and a 32-lane half of a fragment read covers
+// one 32-byte half block in 8 rows (k & 7 = 0 .. 7, the rows with bit 2 set
+// in the other half): both land on 64 distinct banks.
 constexpr int kRowBytes = 512;
 constexpr int kOperandBytes = kBK * kRowBytes;   // 32 KiB
 constexpr int kStageBytes = 2 * kOperandBytes;   // G tile + A tile
 
-// Byte offset of bf16 element (k, col) (col < 256, byte offset within the
-// 64-byte block preserved).
+// Byte offset of bf16 element (k, col) (col < 256; 16-byte chunks of 8
+// columns stay contiguous).
 __device__ __forceinline__ int tile_off(int k, int col) {
-  return k * kRowBytes + ((((col >> 5) ^ (k & 7)) << 6) | ((col & 31) << 1));
+  return k * kRowBytes +
+         ((((col >> 5) ^ (k & 7)) << 6) | (((col & 31) << 1) ^ (((k >> 2) & 1) << 5)));
+}
+
+// Logical first column of the 16-byte chunk at physical 16-byte slot `slot`
+// (0..31) of row k: the inverse of tile_off.
+__device__ __forceinline__ int tile_slot_col(int k, int slot) {
+  return (((slot >> 2) ^ (k & 7)) << 5) + (((slot & 3) ^ (((k >> 2) & 1) << 1)) << 3);
 }
 
 
@@ -251,17 +264,24 @@ struct FastArgs {
   float* partial;
 };
 
-// Per-lane LDS offsets of the transposing fragment reads.  For a 32 x 16
-// (rows x k) fragment at tile column c0 and K sub-step 0, half h (k 4h..4h+3
-// of the lane's 8): lane l of 16-lane group q = l / 16, L = l % 16 reads the 8
-// bytes at k = 8 (q >> 1) + 4 h + (L >> 2), col = c0 + 16 (q & 1) + 4 (L & 3);
-// after the transpose it holds k = 8 (l / 32) + 4 h + 0..3 of col c0 + l % 32,
-// which is the MFMA operand layout.  K sub-step kk adds kk * 16 rows.
-__device__ __forceinline__ int frag_off(int c0, int h, int lane) {
+// Per-lane LDS offset of the transposing fragment read (ds_read_b64_tr_b16)
+// for a 16 x 32 fragment of the 16x16x32 MFMA at tile column c0, K sub-step
+// 0, half h (k-slots 4h..4h+3 of the lane's 8).  The MFMA operand lane l
+// holds k-slots 8 (l / 16) .. + 7 of row (column) l % 16.  The k-slots are a
+// permutation of the sub-step's 32 rows, the same for both operands, so the
+// MFMA still sums over all of them: slot 8 q + 4 h + e (q = l / 16, e < 4)
+// is row 16 h + 4 q + e.  Lane L of group q reads the 8 bytes at k = 16 h + 4
+// q + (L >> 2), col = c0 + 4 (L & 3), and after the transpose holds 4
+// consecutive rows of col c0 + L.  With this order the two 16-lane groups of
+// a 32-lane half read rows 4 q' .. 4 q' + 3 and 4 q' + 4 .. 4 q' + 7: 8
+// distinct (k & 7), the second four with swapped block halves, which is what
+// keeps the read on 64 distinct banks (tile_off).  Sub-step kk adds kk * 32
+// rows.
+__device__ __forceinline__ int frag16_off(int c0, int h, int lane) {
   const int q = lane >> 4, L = lane & 15;
-  const int k = 8 * (q >> 1) + 4 * h + (L >> 2);
-  return tile_off(k, c0 + 16 * (q & 1) + 4 * (L & 3));
+  return tile_off(16 * h + 4 * q + (L >> 2), c0 + 4 * (L & 3));
 }
+
 
 // LDS of the fast kernel: each stage's G tile and A tile in an array of its
 // own (the first G array, after the K loop, also holds a 32-row slice of the
@@ -278,18 +298,23 @@ constexpr int kG0Bytes = (kOperandBytes > kEpiPassRows * kEpiLd * 4) ? kOperandB
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 
-// The body of the fast kernel for one 256 x 256 output tile.  kWaves = 8:
-// waves of 128 x 64 (2 per SIMD); kWaves = 4: waves of 128 x 128 (1 per SIMD,
-// accumulators in AGPRs; half the LDS fragment traffic per MFMA).
+// The body of the fast kernel for one 256 x 256 output tile: kWaves = 8
+// waves (2 per SIMD) of 128 x 64, each made of 8 x 4 blocks of 16 x 16
+// (16x16x32 MFMA, fp32 accumulators).  (The 16x16x32 instruction sustains a
+// higher clock than 32x32x16 on the same data, and 8 waves measure faster
+// than 4 waves of 128 x 128 whose 256 accumulators per lane leave too few
+// registers for the pipeline.)
 template <bool kGrouped, int kWaves>
 __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
   constexpr int kT = kWaves * 64;           // threads
   constexpr int kWavesN = kWaves / 2;       // waves along the tile columns
   constexpr int kWC = kBN / kWavesN;        // columns of a wave tile
-  constexpr int kNB = kWC / 32;             // 32-column MFMA blocks of a wave tile
+  constexpr int kRB = 8;                    // 16-row accumulator blocks of a wave tile
+  constexpr int kCB = kWC / 16;             // 16-column accumulator blocks
+  typedef f32x4_t Acc;
   constexpr int kRowsPerPass = kT / 32;     // G rows staged per pass of all threads
   constexpr int kGC = kBK / kRowsPerPass;   // G chunks per thread per K step
-  constexpr int kGCSub = kGC / 4;           // ... stored per 16-deep sub-step
+  constexpr int kGCSub = kGC / 4;           // ... stored per phase
   constexpr int kDma = 32 / kWaves;         // 1 KiB A transfers per wave per K step
   __shared__ __attribute__((aligned(16))) uint8_t lds_g0[kG0Bytes];
   __shared__ __attribute__((aligned(16))) uint8_t lds_g1[kOperandBytes];
@@ -309,7 +334,9 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
   int tm, tn;
   tile_coords(lin, tiles_m, tiles_n, &tm, &tn);
   const int m0 = tm * kBM, n0 = tn * kBN;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // The wave index is uniform: read it into a scalar register, so that the
+  // LDS destinations of the DMAs (which go through M0) are scalar too.
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = w / kWavesN, wn = w % kWavesN;  // wave tile: rows wm * 128, columns wn * kWC
 
   Epilogue ep = args.ep;
@@ -346,11 +373,11 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     total_rows = args.B * T;
   }
 
-  f32x16_t acc[4][kNB];
+  Acc acc[kRB][kCB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kRB; ++i)
 #pragma unroll
-    for (int j = 0; j < kNB; ++j) acc[i][j] = f32x16_t{};
+    for (int j = 0; j < kCB; ++j) acc[i][j] = Acc{};
 
   // Dense mode: split 0 also runs the plan's slow slots (see below).
   const bool any_slow = !kGrouped && split == 0 && nactive > nfast;
@@ -420,115 +447,140 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
           scale_chunk(g[j], sc);
     };
     // A goes straight from memory into LDS (buffer_load ... lds): wave w's
-    // instruction j fills the 1 KiB at (w * kDma + j) * 1024 of the A tile,
-    // lane i the 16 bytes at i * 16 -- row (w * kDma + j) * 2 + i / 32,
-    // physical 16-byte slot i % 32, which holds logical columns
-    // (((i % 32) / 4) ^ (row & 7)) * 32 + (i % 4) * 8.
-    int dma_voff[kDma], dma_bad[kDma], dma_row[kDma];
-#pragma unroll
-    for (int j = 0; j < kDma; ++j) {
-      const int row = (w * kDma + j) * 2 + (lane >> 5);
-      const int slot = lane & 31;
-      const int acol = (((slot >> 2) ^ (row & 7)) << 5) + (slot & 3) * 8;
-      dma_row[j] = row;
-      dma_voff[j] = row * N * 2 + (n0 + acol) * 2;
-      dma_bad[j] = (n0 + acol < N) ? 0 : kOutOfRange;
-    }
+    // instruction j fills the 1 KiB of tile rows 2 w + 2 kWaves j and the
+    // next, lane i the 16 bytes at i * 16 -- row 2 w + 2 kWaves j + i / 32,
+    // physical 16-byte slot i % 32, which holds the 8 logical columns from
+    // tile_slot_col(row, i % 32).  The swizzle depends on row & 7, which is
+    // the same for every j, so a lane has one column offset per operand and
+    // instruction j only adds the uniform 2 kWaves j rows.
+    // Grouped mode: rows past the step's `valid` and chunks whose columns lie
+    // past the matrix are given an out-of-range offset (read as zero).  Dense
+    // mode: every row is valid, and a chunk past the matrix reads the row's
+    // last 8 columns instead -- they feed only output rows (columns) that are
+    // never stored -- so every transfer is in range, the per-lane offset is
+    // fixed, and the row offset of the step and instruction is the uniform
+    // soffset.
+    const int dma_row = 2 * w + (lane >> 5);  // + 2 kWaves j
+    const int dma_col = tile_slot_col(dma_row, lane & 31);
+    const int dma_voff = dma_row * N * 2 + (kGrouped ? n0 + dma_col : min(n0 + dma_col, N - 8)) * 2;
+    const int dma_bad = (kGrouped && n0 + dma_col >= N) ? kOutOfRange : 0;
     auto dma_a = [&](uint8_t* astage, int row0, int valid) __attribute__((always_inline)) {
 #pragma unroll
       for (int j = 0; j < kDma; ++j) {
-        const int bad = (kGrouped && dma_row[j] >= valid) ? kOutOfRange : dma_bad[j];
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            a_rsrc,
-            (__attribute__((address_space(3))) void*)((lds_u8_t*)astage + (w * kDma + j) * 1024),
-            16, (row0 * N * 2 + dma_voff[j]) | bad, 0, 0, 0);
+        auto* dst = (__attribute__((address_space(3))) void*)((lds_u8_t*)astage +
+                                                               (w + kWaves * j) * 1024);
+        const int rows = row0 + 2 * kWaves * j;
+        if constexpr (kGrouped) {
+          const int bad = dma_row >= valid - 2 * kWaves * j ? kOutOfRange : dma_bad;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, dst, 16, (rows * N * 2 + dma_voff) | bad,
+                                                   0, 0, 0);
+        } else {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, dst, 16, dma_voff, rows * N * 2, 0, 0);
+        }
       }
     };
     // Dense mode: G goes into LDS by DMA too, in the same layout as A (its
     // scale is applied to the accumulators).
-    int gdma_voff[kDma], gdma_bad[kDma];
-#pragma unroll
-    for (int j = 0; j < kDma; ++j) {
-      const int row = (w * kDma + j) * 2 + (lane >> 5);
-      const int slot = lane & 31;
-      const int gc = (((slot >> 2) ^ (row & 7)) << 5) + (slot & 3) * 8;
-      gdma_voff[j] = row * M * 2 + (m0 + gc) * 2;
-      gdma_bad[j] = (m0 + gc < M) ? 0 : kOutOfRange;
-    }
+    const int gdma_voff = dma_row * M * 2 + min(m0 + dma_col, M - 8) * 2;
     auto dma_g = [&](uint8_t* gstage, int row0) __attribute__((always_inline)) {
 #pragma unroll
       for (int j = 0; j < kDma; ++j) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             g_rsrc,
-            (__attribute__((address_space(3))) void*)((lds_u8_t*)gstage + (w * kDma + j) * 1024),
-            16, (row0 * M * 2 + gdma_voff[j]) | gdma_bad[j], 0, 0, 0);
+            (__attribute__((address_space(3))) void*)((lds_u8_t*)gstage + (w + kWaves * j) * 1024),
+            16, gdma_voff, (row0 + 2 * kWaves * j) * M * 2, 0, 0);
       }
     };
 
-    int goff[4][2], aoff[kNB][2];
+    // 16x16x32 blocks: a K step is two 32-deep sub-steps kk, each run as two
+    // phases ih of 16 MFMAs -- G block rows 4 ih .. 4 ih + 3 of the wave tile
+    // against its kCB A block columns.  G fragments are read per phase, A
+    // fragments per sub-step.  Block rows 2 r and 2 r + 1 are the two halves
+    // of a 64-byte LDS block, so the per-lane offsets are kept for even block
+    // rows (columns) only; the odd one's is that offset XOR 32 (whether a
+    // lane's halves are swapped depends on its row).
+    // The second half of a fragment (h = 1) is 16 rows further, with the
+    // same (k & 7): 16 * kRowBytes bytes.
+    int g16off[4], a16off[kCB / 2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int r = 0; r < 4; ++r) g16off[r] = frag16_off(wm * 128 + r * 32, 0, lane);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) goff[i][h] = frag_off(wm * 128 + i * 32, h, lane);
-#pragma unroll
-      for (int j = 0; j < kNB; ++j) aoff[j][h] = frag_off(wn * kWC + j * 32, h, lane);
-    }
-    // Fragments of K sub-step kk: 4 of G^T (rows) and kNB of A (columns).
-    struct Frags {
-      bf16x8_t a[4], b[kNB];
+    for (int r = 0; r < kCB / 2; ++r) a16off[r] = frag16_off(wn * kWC + r * 32, 0, lane);
+    struct G16 {
+      bf16x8_t f[4];
     };
-    auto read_frags = [&](const uint8_t* gstage, const uint8_t* astage, int kk, Frags& f) __attribute__((always_inline)) {
-      const int kofs = kk * 16 * kRowBytes;
+    struct A16 {
+      bf16x8_t f[kCB];
+    };
+    auto read_g16 = [&](const uint8_t* gstage, int kk, int ih, G16& f) __attribute__((always_inline)) {
+      const int kofs = kk * 32 * kRowBytes;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int bi = 4 * ih + i, o = (g16off[bi >> 1] ^ (32 * (bi & 1))) + kofs;
+        f.f[i] = join_frag(read_tr(gstage, o), read_tr(gstage, o + 16 * kRowBytes));
+      }
+    };
+    auto read_a16 = [&](const uint8_t* astage, int kk, A16& f) __attribute__((always_inline)) {
+      const int kofs = kk * 32 * kRowBytes;
+#pragma unroll
+      for (int j = 0; j < kCB; ++j) {
+        const int o = (a16off[j >> 1] ^ (32 * (j & 1))) + kofs;
+        f.f[j] = join_frag(read_tr(astage, o), read_tr(astage, o + 16 * kRowBytes));
+      }
+    };
+    auto mma16 = [&](const G16& g, const A16& a, int ih) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        f.a[i] = join_frag(read_tr(gstage, goff[i][0] + kofs), read_tr(gstage, goff[i][1] + kofs));
 #pragma unroll
-      for (int j = 0; j < kNB; ++j)
-        f.b[j] = join_frag(read_tr(astage, aoff[j][0] + kofs), read_tr(astage, aoff[j][1] + kofs));
-    };
-    auto mma = [&](const Frags& f) __attribute__((always_inline)) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < kNB; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < kCB; ++j)
+          acc[4 * ih + i][j] =
+              __builtin_amdgcn_mfma_f32_16x16x32_bf16(g.f[i], a.f[j], acc[4 * ih + i][j], 0, 0, 0);
     };
 
-    // One K step on stage (gcur, acur), staging step s + 1 into (gnxt, anxt).
-    // On entry the fragments of sub-step 0 are in flight into `fa`.
-    //   * The DMA of A's step s + 1 is issued first.
-    //   * Sub-steps 0..2: the MFMAs of sub-step kk run while the fragments of
-    //     sub-step kk + 1 are read (fragments alternate between fa and fb); G
-    //     chunks of step s + 1 go from the registers (scaled) into the other
-    //     stage, and their registers are refilled with step s + 2, so each
-    //     load is in flight for a whole step.
-    //   * Barrier: the other stage is complete (the DMA has landed, every G
+    // One K step on stage (gcur, acur); the DMAs of step s + 1 into (gnxt,
+    // anxt) were issued during step s - 1.  A step is four phases (two
+    // 32-deep sub-steps of two phases each).  On entry the fragments of phase
+    // 0 are in flight.
+    //   * Phases 0..2: the MFMAs of phase p run while the fragments of phase
+    //     p + 1 are read; grouped mode: G chunks of step s + 1 go from the
+    //     registers (scaled) into the other stage, and their registers are
+    //     refilled with step s + 2, so each load is in flight for a whole
+    //     step.
+    //   * Barrier: the other stage is complete (its DMAs have landed, every G
     //     store is done), and this stage's last fragments are in registers.
-    //   * Sub-step 3: its MFMAs run while the fragments of sub-step 0 of step
-    //     s + 1 are read from the other stage.
-    // So the MFMAs of every sub-step, across step boundaries too, overlap the
-    // reads of the next, and the barrier is the only place a wave waits for
-    // the others.  With 8 waves the sched_group_barriers interleave each
-    // sub-step's 8 MFMAs with the 12 reads of the next (the scheduler would
-    // otherwise bunch them); with the sched_barriers they also keep each G
-    // chunk's store and reload inside its sub-step.  Before the barrier only
-    // the kGC G loads may still be outstanding.  Past the last step the stores
-    // and loads repeat the last step's (in-range) rows into the unused stage:
-    // every path issues the same memory operations, which keeps the counter
-    // waits exact.
+    //   * Phase 3: the DMAs of step s + 2 go into this stage (no wave reads it
+    //     any more), and the phase's MFMAs run while the fragments of phase 0
+    //     of step s + 1 are read from the other stage.
+    // So the MFMAs of every phase, across step boundaries too, overlap the
+    // reads of the next, each DMA has a step and a quarter to land, and the
+    // barrier is the only place a wave waits for the others.  With 8 waves
+    // the sched_group_barriers interleave each phase's MFMAs with the reads
+    // of the next (the scheduler would otherwise bunch them); with the
+    // sched_barriers they also keep each G chunk's store and reload inside
+    // its phase.  Before the barrier only the kGC G loads may still be
+    // outstanding.  Past the last step the DMAs, stores and loads repeat the
+    // last step's (in-range) rows into a stage no one reads: every path
+    // issues the same memory operations, which keeps the counter waits exact.
     float sc_next = 0.0f;
     int row_next = 0, valid_next = kBK, valid_cur = kBK;
-    auto interleave = [&]() __attribute__((always_inline)) {
+    // Phases 0 and 2 read 8 fragment halves (4 G fragments), phases 1 and 3
+    // 16 (4 G and 4 A fragments), under 16 MFMAs each.
+    auto interleave = [&](int phase) __attribute__((always_inline)) {
       if constexpr (kWaves == 8) {
 #define DPC_SG(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
-#define DPC_SG_PAIR(reads) \
-  DPC_SG(0x008, 1);        \
-  DPC_SG(0x100, reads);    \
-  DPC_SG(0x002, 3)
         // 0x008 MFMA, 0x100 LDS read, 0x002 VALU.
-        DPC_SG_PAIR(2); DPC_SG_PAIR(1); DPC_SG_PAIR(2); DPC_SG_PAIR(1);
-        DPC_SG_PAIR(2); DPC_SG_PAIR(1); DPC_SG_PAIR(2); DPC_SG_PAIR(1);
-#undef DPC_SG_PAIR
+        if (phase & 1) {
+#pragma unroll
+          for (int g = 0; g < 16; ++g) {
+            DPC_SG(0x008, 1); DPC_SG(0x100, 1); DPC_SG(0x002, 2);
+          }
+        } else {
+#pragma unroll
+          for (int g = 0; g < 8; ++g) {
+            DPC_SG(0x008, 1); DPC_SG(0x100, 1); DPC_SG(0x002, 2);
+            DPC_SG(0x008, 1); DPC_SG(0x002, 1);
+          }
+        }
       }
     };
     // LDS writes and global loads of the G chunks staged in a sub-step.
@@ -542,7 +594,8 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
 #undef DPC_SG
       }
     };
-    Frags fa, fb;
+    G16 gf0, gf1;
+    A16 af0, af1;
     // The accumulators hold the partial sum divided by the accumulator factor
     // of the step whose MFMAs run (sc_cur): dense mode, the example's scale;
     // grouped mode, the mantissa of the segment's scale (its power of two
@@ -554,21 +607,19 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     };
     auto rescale = [&](float r) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < kRB; ++i)
 #pragma unroll
-        for (int j = 0; j < kNB; ++j) acc[i][j] *= r;
+        for (int j = 0; j < kCB; ++j) acc[i][j] *= r;
     };
-    auto k_step = [&](int s, const uint8_t* gcur, const uint8_t* acur, uint8_t* gnxt,
+    auto k_step = [&](int s, uint8_t* gcur, uint8_t* acur, uint8_t* gnxt,
                       uint8_t* anxt) __attribute__((always_inline)) {
       const float sc_s1 = acc_factor(sc_next);  // accumulator factor of step s + 1
       const float g_next = kGrouped ? scale_pow2(sc_next) : 1.0f;  // G factor of step s + 1
-      dma_a(anxt, row_next, valid_next);
-      if constexpr (!kGrouped) dma_g(gnxt, row_next);
       float sc_after;
       int valid2;
       const int row2 = step_row0(min(s + 2, nsteps - 1), &sc_after, &valid2);
       // Grouped mode: a segment's last step may hold fewer than 64 rows; the
-      // MFMAs of 16-row sub-steps past them (all zeros) are skipped.
+      // MFMAs of a 32-row sub-step past them (all zeros) are skipped.
       const int vcur = kGrouped ? valid_cur : kBK;
       auto stage_g = [&](int kk) __attribute__((always_inline)) {
         if constexpr (kGrouped) {
@@ -579,23 +630,24 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
         }
       };
       __builtin_amdgcn_sched_barrier(0);
-      read_frags(gcur, acur, 1, fb);
-      mma(fa);
+      read_g16(gcur, 0, 1, gf1);
+      mma16(gf0, af0, 0);
       stage_g(0);
-      interleave();
+      interleave(0);
       order_stores(1);
       __builtin_amdgcn_sched_barrier(0);
-      read_frags(gcur, acur, 2, fa);
-      if (vcur > 16) mma(fb);
+      read_g16(gcur, 1, 0, gf0);
+      read_a16(acur, 1, af1);
+      mma16(gf1, af0, 1);
       stage_g(1);
-      interleave();
+      interleave(1);
       order_stores(1);
       __builtin_amdgcn_sched_barrier(0);
-      read_frags(gcur, acur, 3, fb);
-      if (vcur > 32) mma(fa);
+      read_g16(gcur, 1, 1, gf1);
+      if (vcur > 32) mma16(gf0, af1, 0);
       stage_g(2);
       stage_g(3);
-      interleave();
+      interleave(2);
       order_stores(2);
       __builtin_amdgcn_sched_barrier(0);
       sc_next = sc_after;
@@ -604,9 +656,14 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       valid_next = valid2;
       DPC_WAIT_VMCNT(kGrouped ? kGC : 0);
       __syncthreads();
-      read_frags(gnxt, anxt, 0, fa);
-      if (vcur > 48) mma(fb);
-      interleave();
+      // Every wave has read this stage for the last time: the DMAs of step
+      // s + 2 go into it now, a quarter step before the next step starts.
+      dma_a(acur, row_next, valid_next);
+      if constexpr (!kGrouped) dma_g(gcur, row_next);
+      read_g16(gnxt, 0, 0, gf0);
+      read_a16(anxt, 0, af0);
+      if (vcur > 32) mma16(gf1, af1, 1);
+      interleave(3);
       __builtin_amdgcn_sched_barrier(0);
       if (s + 1 < nsteps && sc_s1 != sc_cur) {
         rescale(sc_cur / sc_s1);
@@ -635,13 +692,18 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
         dma_g(g0, row0);
       }
       row_next = step_row0(min(1, nsteps - 1), &sc_next, &valid_next);
+      dma_a(lds_a1, row_next, valid_next);
       if constexpr (kGrouped) {
 #pragma unroll
         for (int j = 0; j < kGC; ++j) load_chunk(row_next, valid_next, j);
+      } else {
+        dma_g(g1, row_next);
       }
-      DPC_WAIT_VMCNT(kGrouped ? kGC : 0);  // step 0's DMAs have landed
+      // Step 0's transfers have landed (step 1's DMAs and G loads may not).
+      DPC_WAIT_VMCNT(kGrouped ? kDma + kGC : 2 * kDma);
       __syncthreads();
-      read_frags(g0, lds_a0, 0, fa);
+      read_g16(g0, 0, 0, gf0);
+      read_a16(lds_a0, 0, af0);
       int s = 0;
       for (; s + 1 < nsteps; s += 2) {
         k_step(s, g0, lds_a0, g1, lds_a1);
@@ -678,9 +740,12 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
         DPC_WAIT_VMCNT(0);
         __syncthreads();
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          read_frags(g0, lds_a0, kk, fa);
-          mma(fa);
+        for (int kk = 0; kk < 2; ++kk) {
+          read_a16(lds_a0, kk, af0);
+          read_g16(g0, kk, 0, gf0);
+          mma16(gf0, af0, 0);
+          read_g16(g0, kk, 1, gf0);
+          mma16(gf0, af0, 1);
         }
         __syncthreads();
       }
@@ -699,15 +764,17 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
 #pragma unroll
   for (int e = 0; e < kBM / kEpiPassRows; ++e) {
     if (wm == (e >> 2)) {
-      const int i = e & 3;
+      // 16x16 block (i, j): lane l holds rows 4 (l / 16) + r of column l % 16.
 #pragma unroll
-      for (int j = 0; j < kNB; ++j)
+      for (int i2 = 0; i2 < 2; ++i2)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int ml = (r >> 2) * 8 + 4 * (lane >> 5) + (r & 3);
-          const int nl = wn * kWC + j * 32 + (lane & 31);
-          tile[ml * kEpiLd + nl] = acc[i][j][r];
-        }
+        for (int j = 0; j < kCB; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int ml = 16 * i2 + 4 * (lane >> 4) + r;
+            const int nl = wn * kWC + j * 16 + (lane & 15);
+            tile[ml * kEpiLd + nl] = acc[2 * (e & 3) + i2][j][r];
+          }
     }
     __syncthreads();
     const int cl = 2 * (tid & 127);
