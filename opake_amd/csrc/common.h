@@ -14,6 +14,11 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
+// vmcnt(N) with the other counters left alone (gfx9 s_waitcnt encoding):
+// the wait for a wave's direct-to-LDS transfers (buffer_load ... lds), which
+// the compiler does not track.
+#define DPC_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
+
 // ---------------------------------------------------------------------------
 // bfloat16 <-> float.  bf16 is the upper half of an IEEE binary32; the
 // narrowing conversion rounds to nearest-even and keeps NaN a NaN.

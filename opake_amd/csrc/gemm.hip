@@ -293,8 +293,6 @@ constexpr int kEpiLd = kBN + 4;
 constexpr int kG0Bytes = (kOperandBytes > kEpiPassRows * kEpiLd * 4) ? kOperandBytes
                                                                       : kEpiPassRows * kEpiLd * 4;
 
-// vmcnt(N) with the other counters left alone (gfx9 s_waitcnt encoding).
-#define DPC_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 

@@ -41,7 +41,6 @@ namespace {
 
 constexpr int kGramTile = 128;  // rows of a T-tile
 constexpr int kGramThreads = 256;
-constexpr int kGramMfmaThreads = 256;
 constexpr int kGK = 32;                              // reduction depth per K step
 constexpr int kGTileBytes = kGramTile * kGK * 2;     // 8 KiB per staged tile
 constexpr int kGStageBytes = 4 * kGTileBytes;        // A_p, A_q, G_p, G_q
@@ -78,14 +77,15 @@ __device__ __forceinline__ double block_sum_f64(double v, double* red) {
   return total;
 }
 
-// Record words 0..6 of a Gram work item, summed over the workgroup in a fixed
-// order (lanes by shuffle tree, then waves), written with the gammas and the
-// row count: see DPC_GRAM_REC_WORDS.  red: kRecStat * waves doubles of LDS.
+// Record words 0..6 of a Gram tile, summed over the waves that computed it
+// -- waves 4 h .. 4 h + 3 of the workgroup for h = w / 4 -- in a fixed order
+// (lanes by shuffle tree, then waves), written to `rec` (if not null) with the
+// gammas and the row count: see DPC_GRAM_REC_WORDS.  red: kRecStat doubles of
+// LDS per wave.
 constexpr int kRecStat = 7;
 __device__ __forceinline__ void write_gram_record(double (&v)[kRecStat], double* red,
                                                   double* rec, double gA, double gQ, int T) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int nw = (int)(blockDim.x >> 6);
 #pragma unroll
   for (int k = 0; k < kRecStat; ++k)
     for (int off = 32; off > 0; off >>= 1) v[k] += __shfl_down(v[k], off, 64);
@@ -95,10 +95,11 @@ __device__ __forceinline__ void write_gram_record(double (&v)[kRecStat], double*
     for (int k = 0; k < kRecStat; ++k) red[w * kRecStat + k] = v[k];
   }
   __syncthreads();
-  const int t = threadIdx.x;
+  const int t = threadIdx.x & 255, w0 = (w >> 2) * 4;
+  if (rec == nullptr) return;
   if (t < kRecStat) {
     double total = 0.0;
-    for (int i = 0; i < nw; ++i) total += red[i * kRecStat + t];
+    for (int i = 0; i < 4; ++i) total += red[(w0 + i) * kRecStat + t];
     rec[t] = total;
   } else if (t < DPC_GRAM_REC_WORDS) {
     rec[t] = t == 7 ? gA : t == 8 ? gQ : t == 9 ? (double)T : 0.0;
@@ -135,44 +136,50 @@ __device__ __forceinline__ int xcd_logical_block(int padded, int nblocks) {
   return l < nblocks ? l : -1;
 }
 
-// One staged operand (rows row0.. of X [T, d], a 32-deep K step): per thread
-// two 16-byte chunks, chunk id q = tid + 256 j -> row q >> 2, chunk q & 3.
+// One staged operand tile (rows row0 .. row0 + 127 of X [T, d], a 32-deep K
+// step: 512 16-byte chunks): the workgroup's threads each move kC chunks,
+// chunk id q = tid + (512 / kC) j -> row q >> 2, chunk q & 3.
+template <int kC>
 struct GramOperand {
   __amdgpu_buffer_rsrc_t rsrc;
   int row_bytes;   // d * 2
-  int voff[2];     // byte offset of the thread's chunks at K step 0
-  int col[2];      // first column of the chunks
+  int voff[kC];    // byte offset of the thread's chunks at K step 0
+  int col[kC];     // first column of the chunks
   int d;
 };
 
-__device__ __forceinline__ GramOperand make_operand(const uint16_t* X, int T, int d, int row0) {
-  GramOperand o;
+template <int kC>
+__device__ __forceinline__ GramOperand<kC> make_operand(const uint16_t* X, int T, int d,
+                                                        int row0) {
+  GramOperand<kC> o;
   o.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(X), (short)0, T * d * 2,
                                              0x00020000);
   o.row_bytes = d * 2;
   o.d = d;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int q = threadIdx.x + kGramMfmaThreads * j;
+  for (int j = 0; j < kC; ++j) {
+    const int q = threadIdx.x + (512 / kC) * j;
     o.col[j] = (q & 3) * 8;
     o.voff[j] = (row0 + (q >> 2)) * o.row_bytes + o.col[j] * 2;
   }
   return o;
 }
 
-__device__ __forceinline__ void load_operand(const GramOperand& o, int step, u32x4_t r[2]) {
+template <int kC>
+__device__ __forceinline__ void load_operand(const GramOperand<kC>& o, int step, u32x4_t r[kC]) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < kC; ++j) {
     const int k = step * kGK + o.col[j];
     const int bad = k < o.d ? 0 : kGramOutOfRange;
     r[j] = __builtin_amdgcn_raw_buffer_load_b128(o.rsrc, (o.voff[j] + step * kGK * 2) | bad, 0, 0);
   }
 }
 
-__device__ __forceinline__ void store_operand(uint8_t* tile, const u32x4_t r[2]) {
+template <int kC>
+__device__ __forceinline__ void store_operand(uint8_t* tile, const u32x4_t r[kC]) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int q = threadIdx.x + kGramMfmaThreads * j;
+  for (int j = 0; j < kC; ++j) {
+    const int q = threadIdx.x + (512 / kC) * j;
     *reinterpret_cast<u32x4_t*>(tile + gtile_off(q >> 2, q & 3)) = r[j];
   }
 }
@@ -185,7 +192,7 @@ struct GramFrags {
 
 __device__ __forceinline__ void gram_read(const uint8_t* tp, const uint8_t* tq, int kk,
                                           GramFrags& f) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = (threadIdx.x >> 6) & 3;
   const int wr = w >> 1, wc = w & 1;
   const int c = kk * 2 + (lane >> 5);
 #pragma unroll
@@ -206,11 +213,8 @@ __device__ __forceinline__ void gram_mma(const GramFrags& f, f32x16_t acc[2][2])
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
 }
 
-// Grouped mode: work item l is (problem << 16 | pair, first row, rows, slot)
-// -- the tile pair `pair` of the rows-long segment starting at `first row` of
-// problem `problem`'s operands (a_ptrs / g_ptrs, widths din[problem] /
-// dout[problem]); rows past the segment read as zero; the result goes to
-// partial[slot].
+// Grouped mode: the work-item table (see gram_grouped_mfma_bf16_kernel) and
+// the operands and widths of up to kMaxGramProblems problems.
 constexpr int kMaxGramProblems = 64;
 
 struct GramItems {
@@ -221,24 +225,16 @@ struct GramItems {
   int dout[kMaxGramProblems];
 };
 
-// Dense mode: the order in which an XCD's work items are dispatched.
-// Hardware hands an XCD's workgroups to its CUs in turn, so when an XCD has
-// n items and C CUs (C < n <= 2 C), the items at positions k and C + k share
-// CU k.  Diagonal pairs (p == q: two operand tiles instead of four) are the
-// light items, so they go first and last -- the CUs that run two items run
-// two light ones -- and the off-diagonal pairs fill the middle.  All items of
-// the XCD's range stay on it (its L2 holds their examples).
-
-// Diagonal pairs (pair index q (q + 3) / 2) of an example below pair index r.
-__device__ __forceinline__ int diag_below(int r, int nt) {
-  int c = 0;
-  while (c < nt && c * (c + 3) / 2 < r) ++c;
-  return c;
-}
-
-// Diagonal items among items 0 .. L - 1 (example-major order).
-__device__ __forceinline__ int diag_before(int L, int npairs, int nt) {
-  return (L / npairs) * nt + diag_below(L % npairs, nt);
+// Dense mode: the work items of an example.  An off-diagonal item (p, q)
+// stages the rows of blocks p and q of both operands, which is all that the
+// diagonal tiles (p, p) and (q, q) need as well, so an item also computes one
+// diagonal tile from the same staged data: (b, b + 1) carries (b, b), and
+// (0, nt - 1) carries (nt - 1, nt - 1) -- every diagonal tile once when nt >=
+// 3.  So an example is nt (nt - 1) / 2 items of equal staging (nt = 2: (0, 1)
+// carrying (0, 0), and (1, 1); nt = 1: (0, 0)), and the memory traffic of the
+// diagonal tiles disappears.
+DPC_HOST_DEVICE int dense_items_per_example(int nt) {
+  return nt >= 3 ? nt * (nt - 1) / 2 : nt;
 }
 
 // Pair index of the j-th off-diagonal pair (p < q) of an example.
@@ -251,59 +247,33 @@ __device__ __forceinline__ int offdiag_pair(int j) {
   return q * (q + 1) / 2 + j;
 }
 
-// Item (example-major index) at dispatch position pos of the range
-// L0 .. L0 + n - 1 of an XCD with `cus` CUs.
-__device__ __forceinline__ int dense_item(int pos, int L0, int n, int npairs, int nt, int cus) {
-  const int f0 = diag_before(L0, npairs, nt);
-  const int nd = diag_before(L0 + n, npairs, nt) - f0;
-  const int no = n - nd;
-  const int a = min(nd, max(0, n - cus));
-  if (pos < a || pos >= a + no) {
-    const int r = f0 + (pos < a ? pos : pos - no);
-    const int qd = r % nt;
-    return (r / nt) * npairs + qd * (qd + 3) / 2;
+// Item i of an example: its pair (p, q) and carried diagonal block c (-1:
+// none).
+__device__ __forceinline__ void dense_item(int i, int nt, int* p, int* q, int* c) {
+  if (nt == 1) {
+    *p = *q = 0;
+    *c = -1;
+    return;
   }
-  const int noff = npairs - nt;
-  const int r = (L0 - f0) + (pos - a);
-  return (r / noff) * npairs + offdiag_pair(r % noff);
+  if (nt == 2) {
+    *p = i;
+    *q = 1;
+    *c = i == 0 ? 0 : -1;
+    return;
+  }
+  pair_from_index(offdiag_pair(i), p, q);
+  *c = (*q == *p + 1) ? *p : ((*p == 0 && *q == nt - 1) ? *q : -1);
 }
 
-template <bool kGrouped>
-__global__ void __launch_bounds__(kGramMfmaThreads, 2)
-gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ G, int T,
-                      int din, int dout, int npairs, int nblocks, double* __restrict__ records,
-                      GramItems work, int xcd_cus) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kGStageBytes];
-  __shared__ double red[kRecStat * (kGramMfmaThreads / 64)];
-  int l = xcd_logical_block(gridDim.x, nblocks);
-  if (l < 0) return;  // padding workgroup: exits before any barrier
-  if (!kGrouped) {
-    const int per = gridDim.x / kXcds, x = blockIdx.x % kXcds, L0 = x * per;
-    const int nt = ceil_div(T, kGramTile);
-    l = dense_item(blockIdx.x / kXcds, L0, min(per, nblocks - L0), npairs, nt, xcd_cus);
-  }
-  const uint16_t* Xa;
-  const uint16_t* Xg;
-  int pair, slot = l;
-  if (kGrouped) {
-    const int32_t* it = work.items + 4 * (size_t)l;
-    if (it[0] < 0) return;  // empty item: exits before any barrier
-    const int problem = it[0] >> 16, row0 = it[1];
-    pair = it[0] & 0xffff;
-    T = it[2];
-    slot = it[3];
-    din = work.din[problem];
-    dout = work.dout[problem];
-    Xa = reinterpret_cast<const uint16_t*>(work.a_ptrs[problem]) + (size_t)row0 * din;
-    Xg = reinterpret_cast<const uint16_t*>(work.g_ptrs[problem]) + (size_t)row0 * dout;
-  } else {
-    const int ex = l / npairs;
-    pair = l % npairs;
-    Xa = A + (size_t)ex * T * din;
-    Xg = G + (size_t)ex * T * dout;
-  }
-  int p, q;
-  pair_from_index(pair, &p, &q);
+// One work item: tiles (p, q) of A A^T and G G^T (waves 0..3, a 64 x 64 block
+// each), and with kWaves = 8 the diagonal tiles (c, c) (waves 4..7; c = p
+// when the item carries none, whose results are not recorded).  rec_pq /
+// rec_c: the records to write (rec_c null: none).
+template <int kWaves>
+__device__ __forceinline__ void gram_body(const uint16_t* Xa, const uint16_t* Xg, int T, int din,
+                                          int dout, int p, int q, int c, double* rec_pq,
+                                          double* rec_c, uint8_t* lds, double* red) {
+  constexpr int kC = 512 / (kWaves * 64);  // staged chunks per thread and tile
   const bool diag = (p == q);
   // <A A^T, G G^T> is symmetric in A and G: order them so that din <= dout;
   // the K loop then has one shape (both Gram matrices, then G G^T alone).
@@ -316,12 +286,11 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
     dout = d;
   }
 
-  const GramOperand ap = make_operand(Xa, T, din, p * kGramTile);
-  const GramOperand aq = make_operand(Xa, T, din, q * kGramTile);
-  const GramOperand gp = make_operand(Xg, T, dout, p * kGramTile);
-  const GramOperand gq = make_operand(Xg, T, dout, q * kGramTile);
+  const GramOperand<kC> ap = make_operand<kC>(Xa, T, din, p * kGramTile);
+  const GramOperand<kC> aq = make_operand<kC>(Xa, T, din, q * kGramTile);
+  const GramOperand<kC> gp = make_operand<kC>(Xg, T, dout, p * kGramTile);
+  const GramOperand<kC> gq = make_operand<kC>(Xg, T, dout, q * kGramTile);
   const int nka = ceil_div(din, kGK), nkg = ceil_div(dout, kGK);
-  const int nk = max(nka, nkg);
 
   f32x16_t pa[2][2], pg[2][2];
 #pragma unroll
@@ -332,28 +301,28 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
   // Registers hold the next K step of the four operands (the q operands are
   // not loaded on diagonal pairs).  Past an operand's K range the loads read
   // zeros, so every path issues the same loads.
-  // Two register sets alternate by step parity: step s stores set
-  // (s + 1) & 1, which holds step s + 1, into the other stage and reloads it
-  // with step s + 3, so every load has two steps to land.
+  // Two register sets alternate by step parity: step s stores set (s + 1) & 1,
+  // which holds step s + 1, into the other stage and reloads it with step
+  // s + 3, so every load has two steps to land.
   struct Regs {
-    u32x4_t ap[2], aq[2], gp[2], gq[2];
+    u32x4_t ap[kC], aq[kC], gp[kC], gq[kC];
   };
   Regs R[2];
   auto load_a = [&](int step, Regs& r) __attribute__((always_inline)) {
-    load_operand(ap, step, r.ap);
-    if (!diag) load_operand(aq, step, r.aq);
+    load_operand<kC>(ap, step, r.ap);
+    if (!diag) load_operand<kC>(aq, step, r.aq);
   };
   auto load_g = [&](int step, Regs& r) __attribute__((always_inline)) {
-    load_operand(gp, step, r.gp);
-    if (!diag) load_operand(gq, step, r.gq);
+    load_operand<kC>(gp, step, r.gp);
+    if (!diag) load_operand<kC>(gq, step, r.gq);
   };
   auto store_a = [&](uint8_t* stage, const Regs& r) __attribute__((always_inline)) {
-    store_operand(stage, r.ap);
-    if (!diag) store_operand(stage + kGTileBytes, r.aq);
+    store_operand<kC>(stage, r.ap);
+    if (!diag) store_operand<kC>(stage + kGTileBytes, r.aq);
   };
   auto store_g = [&](uint8_t* stage, const Regs& r) __attribute__((always_inline)) {
-    store_operand(stage + 2 * kGTileBytes, r.gp);
-    if (!diag) store_operand(stage + 3 * kGTileBytes, r.gq);
+    store_operand<kC>(stage + 2 * kGTileBytes, r.gp);
+    if (!diag) store_operand<kC>(stage + 3 * kGTileBytes, r.gq);
   };
 
   load_a(0, R[0]);
@@ -368,20 +337,25 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
   // A K step is four groups of MFMAs on the current stage -- A sub-steps 0
   // and 1, then G sub-steps 0 and 1 -- and each group's fragments are read
   // before the previous group's MFMAs (two fragment sets, fx and fy), so the
-  // LDS latency overlaps MFMA work even with one wave per SIMD.  A's step
-  // s + 1 is stored into the other stage (and its registers reloaded with
-  // step s + 2) after A's MFMAs, G's after G's; each load is in flight for a
-  // whole step.  The barrier before the last group completes the other
-  // stage, so the next step's first fragments are read from it while that
-  // group's MFMAs run.  (Every wave's reads of the current stage are done at
-  // the barrier -- it waits for the wave's LDS operations -- so the next step
-  // may overwrite it.)
+  // LDS latency overlaps MFMA work.  A's step s + 1 is stored into the other
+  // stage (and its registers reloaded with step s + 2) after A's MFMAs, G's
+  // after G's; each load is in flight for a whole step.  The barrier before
+  // the last group completes the other stage, so the next step's first
+  // fragments are read from it while that group's MFMAs run.  (Every wave's
+  // reads of the current stage are done at the barrier -- it waits for the
+  // wave's LDS operations -- so the next step may overwrite it.)
+  // Waves 0..3 read the tiles of blocks p and q, waves 4..7 those of block c
+  // for both operands of the product (the offsets are wave-uniform).
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool second = w >= 4;
+  const int off_p = (second && c == q && !diag) ? kGTileBytes : 0;
+  const int off_q = second ? off_p : (diag ? 0 : kGTileBytes);
   auto stage_ptrs = [&](const uint8_t* st, const uint8_t** tap, const uint8_t** taq,
                         const uint8_t** tgp, const uint8_t** tgq) __attribute__((always_inline)) {
-    *tap = st;
-    *taq = diag ? st : st + kGTileBytes;
-    *tgp = st + 2 * kGTileBytes;
-    *tgq = diag ? *tgp : st + 3 * kGTileBytes;
+    *tap = st + off_p;
+    *taq = st + off_q;
+    *tgp = st + 2 * kGTileBytes + off_p;
+    *tgq = st + 2 * kGTileBytes + off_q;
   };
   GramFrags fx, fy;
   {
@@ -456,16 +430,17 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
   }
   if (s < nkg) step_g(s, R[1]);
 
-  // The tile record.  Both tiles share the MFMA output layout, so the
-  // element-wise product needs no knowledge of which (s, t) a register holds;
-  // a diagonal entry (s == t) sits in a wave on the tile's diagonal
-  // (diagonal pair, wr == wc), block i == j, at the accumulator r with
-  // (r >> 2) * 8 + 4 (lane >> 5) + (r & 3) == lane & 31 -- one per block and
-  // lane.  After the swap above, pa is the Gram matrix of the narrower
-  // operand.
+  // The tile records.  Both tiles of a wave share the MFMA output layout, so
+  // the element-wise product needs no knowledge of which (s, t) a register
+  // holds; a diagonal entry (s == t) sits in a wave on its tile's diagonal
+  // (diagonal tile, block row == block column), block i == j, at the
+  // accumulator r with (r >> 2) * 8 + 4 (lane >> 5) + (r & 3) == lane & 31 --
+  // one per block and lane.  After the swap above, pa is the Gram matrix of
+  // the narrower operand.
   {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const bool diag_wave = diag && (w >> 1) == (w & 1);
+    const int lane = threadIdx.x & 63, wl = w & 3;
+    const bool tile_diag = second || diag;
+    const bool diag_wave = tile_diag && (wl >> 1) == (wl & 1);
     double st[kRecStat] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
     float da[2] = {0.0f, 0.0f}, dg[2] = {0.0f, 0.0f};
 #pragma unroll
@@ -485,7 +460,7 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
             dg[i] = on_diag ? pg[i][j][r] : dg[i];
           }
         }
-    if (!diag) st[0] *= 2.0;  // exact: the off-diagonal pair counts twice
+    if (!tile_diag) st[0] *= 2.0;  // exact: the off-diagonal pair counts twice
     const double gA = dpc_chain_gamma((double)nka * kGK, DPC_GRAM_U_MFMA);
     const double gQ = dpc_chain_gamma((double)nkg * kGK, DPC_GRAM_U_MFMA);
     if (diag_wave) {
@@ -500,8 +475,52 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
         st[6] += vs * vs;
       }
     }
-    write_gram_record(st, red, records + (size_t)slot * DPC_GRAM_REC_WORDS, gA, gQ, T);
+    write_gram_record(st, red, second ? rec_c : rec_pq, gA, gQ, T);
   }
+}
+
+// Dense mode: item l (after the XCD remap: each XCD takes a contiguous range
+// of items, so an example's items share its L2) is item l % items of example
+// l / items; 8 waves, the second four on the carried diagonal tile.
+__global__ void __launch_bounds__(512, 1)
+gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ G, int T,
+                      int din, int dout, int npairs, int items, int nblocks,
+                      double* __restrict__ records) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kGStageBytes];
+  __shared__ double red[kRecStat * 8];
+  const int l = xcd_logical_block(gridDim.x, nblocks);
+  if (l < 0) return;  // padding workgroup: exits before any barrier
+  const int ex = l / items;
+  int p, q, c;
+  dense_item(l % items, ceil_div(T, kGramTile), &p, &q, &c);
+  double* rec = records + (size_t)ex * npairs * DPC_GRAM_REC_WORDS;
+  gram_body<8>(A + (size_t)ex * T * din, G + (size_t)ex * T * dout, T, din, dout, p, q,
+               c < 0 ? p : c, rec + (size_t)(q * (q + 1) / 2 + p) * DPC_GRAM_REC_WORDS,
+               c < 0 ? nullptr : rec + (size_t)(c * (c + 3) / 2) * DPC_GRAM_REC_WORDS, lds, red);
+}
+
+// Grouped mode: work item l is (problem << 16 | pair, first row, rows, slot)
+// -- the tile pair `pair` of the rows-long segment starting at `first row` of
+// problem `problem`'s operands (a_ptrs / g_ptrs, widths din[problem] /
+// dout[problem]); rows past the segment read as zero; the result goes to
+// partial[slot].  4 waves; two workgroups fit on a CU (64 KiB of LDS, <= 256
+// registers per lane at 2 waves per SIMD).
+__global__ void __launch_bounds__(256, 2)
+gram_grouped_mfma_bf16_kernel(GramItems work, int nblocks, double* __restrict__ records) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kGStageBytes];
+  __shared__ double red[kRecStat * 4];
+  const int l = xcd_logical_block(gridDim.x, nblocks);
+  if (l < 0) return;  // padding workgroup: exits before any barrier
+  const int32_t* it = work.items + 4 * (size_t)l;
+  if (it[0] < 0) return;  // empty item: exits before any barrier
+  const int problem = it[0] >> 16, row0 = it[1];
+  const int din = work.din[problem], dout = work.dout[problem];
+  int p, q;
+  pair_from_index(it[0] & 0xffff, &p, &q);
+  gram_body<4>(reinterpret_cast<const uint16_t*>(work.a_ptrs[problem]) + (size_t)row0 * din,
+               reinterpret_cast<const uint16_t*>(work.g_ptrs[problem]) + (size_t)row0 * dout,
+               it[2], din, dout, p, q, p, records + (size_t)it[3] * DPC_GRAM_REC_WORDS, nullptr,
+               lds, red);
 }
 
 // Generic path (float32 inputs, or bf16 with d % 8 != 0): 64 x 64 tiles,
@@ -727,21 +746,6 @@ row_sum_f64_kernel(const double* __restrict__ x, int B, int n, int accumulate,
   out[b] = accumulate ? out[b] + s : s;
 }
 
-// CUs per XCD of the current device (cached per device; 32 on MI355X).
-int xcd_cus() {
-  static int cached[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 32;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        n < kXcds)
-      n = 256;
-    cached[dev] = n / kXcds;
-  }
-  return cached[dev];
-}
-
 }  // namespace
 
 extern "C" size_t dpc_gram_workspace_bytes(int B, int T) {
@@ -772,12 +776,11 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
   if (mfma) {
     nt = ceil_div(T, kGramTile);
     const int npairs = nt * (nt + 1) / 2;
-    const int nblocks = npairs * B;
+    const int items = dense_items_per_example(nt);
+    const int nblocks = items * B;
     const int padded = ceil_div(nblocks, kXcds) * kXcds;
-    GramItems none = {};
-    hipLaunchKernelGGL(gram_mfma_bf16_kernel<false>, dim3(padded), dim3(kGramMfmaThreads), 0, s,
-                       (const uint16_t*)A, (const uint16_t*)G, T, din, dout, npairs, nblocks,
-                       records, none, xcd_cus());
+    hipLaunchKernelGGL(gram_mfma_bf16_kernel, dim3(padded), dim3(512), 0, s, (const uint16_t*)A,
+                       (const uint16_t*)G, T, din, dout, npairs, items, nblocks, records);
   } else {
     nt = ceil_div(T, kGenTile);
     const int npairs = nt * (nt + 1) / 2;
@@ -844,8 +847,8 @@ extern "C" int dpc_grouped_gram_sqnorms(const int64_t* a_ptrs, const int64_t* g_
     const bool fits = ((size_t)max_rows + kGramTile) * (size_t)dmax * 2 < ((size_t)1 << 31);
     if (dtype == DPC_BF16 && aligned && fits) {
       const int padded = ceil_div(n_items, kXcds) * kXcds;
-      hipLaunchKernelGGL(gram_mfma_bf16_kernel<true>, dim3(padded), dim3(kGramMfmaThreads), 0, s,
-                         nullptr, nullptr, 0, 0, 0, 0, n_items, records, work, 0);
+      hipLaunchKernelGGL(gram_grouped_mfma_bf16_kernel, dim3(padded), dim3(256), 0, s, work,
+                         n_items, records);
     } else if (dtype == DPC_BF16) {
       hipLaunchKernelGGL(gram_grouped_generic_kernel<uint16_t>, dim3(n_items), dim3(kGramThreads),
                          0, s, work, records);

@@ -22,6 +22,11 @@ class OpakeError(Exception):
         cause: BaseException | None = None,
         suppress_context: bool = False,
     ) -> NoReturn:
+        """Raise ``cls(message)``, chained to ``cause`` or with the context
+        suppressed.  Nothing in this package calls it: it is kept for API
+        compatibility, because code written against the reference raises its
+        errors as ``ConfigurationError.raise_(...)``
+        (packages/opake-base/src/opake/api/base/exceptions/__init__.py)."""
         if suppress_context:
             raise cls(message) from None
         if cause is not None:
