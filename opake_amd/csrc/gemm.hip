@@ -864,20 +864,24 @@ __device__ __forceinline__ float to_f32<float>(float v) { return v; }
 template <>
 __device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) { return bf16_bits_to_f32(v); }
 
-// Stages rows [k0, k0 + rows) (rows <= kGK; the rest zero) of G (times p2)
-// and A for the 64 x 64 tile (m0, n0), then adds their products to acc.
-template <typename In>
+// Stages rows [k0, k0 + rows) (rows <= kGK; the rest zero) of G and A for
+// the 64 x 64 tile (m0, n0), then adds their products to acc.  G is
+// multiplied by p2 -- or, with kRowScale (one token per example: row k is
+// example k), by row k's own scale, and rows with scale 0 are not read.
+template <typename In, bool kRowScale>
 __device__ __forceinline__ void generic_chunk(const In* __restrict__ A, const In* __restrict__ G,
-                                              long long k0, int rows, float p2, int M, int N,
+                                              long long k0, int rows, float p2,
+                                              const float* __restrict__ scale, int M, int N,
                                               int m0, int n0, float (*sg)[kGT + 1],
                                               float (*sa)[kGT + 1], float acc[4][4]) {
   const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
   for (int e = tid; e < kGK * kGT; e += kThreads) {
     const int k = e / kGT, col = e % kGT;
     float gv = 0.f, av = 0.f;
-    if (k < rows) {
+    const float sk = kRowScale ? (k < rows ? scale[k0 + k] : 0.0f) : p2;
+    if (k < rows && (!kRowScale || sk > 0.0f)) {
       const long long kk = k0 + k;
-      if (m0 + col < M) gv = p2 * to_f32<In>(G[kk * M + m0 + col]);
+      if (m0 + col < M) gv = sk * to_f32<In>(G[kk * M + m0 + col]);
       if (n0 + col < N) av = to_f32<In>(A[kk * N + n0 + col]);
     }
     sg[k][col] = gv;
@@ -930,7 +934,17 @@ clipped_sum_generic_kernel(const In* __restrict__ A, const In* __restrict__ G,
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
   float m_cur = 1.0f;
-  for (long long k0 = kb; k0 < ke;) {
+  if (T == 1) {
+    // One token per example: the example's gradient is the outer product
+    // g a^T, so rounding s g in fp32 changes its norm by at most the
+    // relative rounding of the scaled multiply that the guard already
+    // covers (as for a materialised gradient); kGK examples per chunk.
+    for (long long k0 = kb; k0 < ke; k0 += kGK) {
+      const long long k1 = k0 + kGK < ke ? k0 + kGK : ke;
+      generic_chunk<In, true>(A, G, k0, (int)(k1 - k0), 1.0f, scale, M, N, m0, n0, sg, sa, acc);
+    }
+  }
+  for (long long k0 = T == 1 ? ke : kb; k0 < ke;) {
     const long long ex = k0 / T, ex_end = (ex + 1) * T;
     const float s = scale[ex];  // uniform over the workgroup
     if (!(s > 0.0f)) {
@@ -945,7 +959,8 @@ clipped_sum_generic_kernel(const In* __restrict__ A, const In* __restrict__ G,
       generic_rescale(acc, m_cur / m);
       m_cur = m;
     }
-    generic_chunk<In>(A, G, k0, (int)(k1 - k0), scale_pow2(s), M, N, m0, n0, sg, sa, acc);
+    generic_chunk<In, false>(A, G, k0, (int)(k1 - k0), scale_pow2(s), nullptr, M, N, m0, n0, sg, sa,
+                             acc);
     k0 = k1;
   }
   generic_rescale(acc, m_cur);
@@ -1059,8 +1074,8 @@ grouped_generic_kernel(GroupedTables grp, Epilogue ep0) {
     }
     const float p2 = scale_pow2(sc);
     for (int k0 = 0; k0 < valid; k0 += kGK)
-      generic_chunk<In>(A, G, (long long)row0 + k0, min(kGK, valid - k0), p2, M, N, m0, n0, sg,
-                        sa, acc);
+      generic_chunk<In, false>(A, G, (long long)row0 + k0, min(kGK, valid - k0), p2, nullptr, M, N,
+                               m0, n0, sg, sa, acc);
   }
   generic_rescale(acc, m_cur);
 #pragma unroll

@@ -334,17 +334,25 @@ def test_clipped_sum_fp32_generic(dev, B, T, din, dout):
     assert torch.equal(w, w2)
 
 
-def test_clipped_sum_plan_skips_nonfinite_examples(dev):
+# bf16 at T = 64: the MFMA kernel's clip plan; fp32 at T = 1: the generic
+# kernel's one-token path (16 examples per chunk, each row scaled by its own
+# example's scale), whose zero-scale rows must not be read either.
+@pytest.mark.parametrize("dtype,B,T,tol", [(torch.bfloat16, 3, 64, 2e-2),
+                                           (torch.float32, 40, 1, 1e-5)])
+def test_clipped_sum_plan_skips_nonfinite_examples(dev, dtype, B, T, tol):
     g = _gen(41)
-    A = torch.randn(3, 64, 64, generator=g).to(torch.bfloat16)
-    G = (torch.randn(3, 64, 64, generator=g) * 0.01).to(torch.bfloat16)
+    A = torch.randn(B, T, 64, generator=g).to(dtype)
+    G = (torch.randn(B, T, 64, generator=g) * 0.01).to(dtype)
     A[1, 0, 0] = float("nan")
+    if B > 3:
+        G[17, 0, 3] = float("inf")
     w, _, cf = _run_clipped_sum(dev, A, G, 1.0, out_dtype=torch.float32)
     assert torch.isfinite(w).all()
     assert cf.scale[0, 1].item() == 0.0
-    keep = torch.tensor([0, 2])
+    keep = torch.tensor([i for i in range(B) if i not in (1, 17)])
+    assert all(cf.scale[0, i].item() > 0.0 for i in keep.tolist())
     (want,), _ = _oracle_clipped_sum(A[keep], G[keep], 1.0, out_dtype=torch.float32)
-    assert _rel_err(w.cpu(), want) < 2e-2
+    assert _rel_err(w.cpu(), want) < tol
 
 
 def test_clipped_sum_fast_and_generic_agree(dev):
