@@ -192,38 +192,12 @@ DPC_HOST_DEVICE double dpc_row_bound(double diag, double gamma, double eta, doub
 #define DPC_GRAM_REC_WORDS 12
 
 // Per-example bound from the records of one example / segment (nt row
-// blocks, pair index q (q + 1) / 2 + p for p <= q, records rec[pair]).
-// Returns the inner product folded in pair order through *sum and the error
-// bound; see the model above:
+// blocks, pair index q (q + 1) / 2 + p for p <= q, records rec[pair]), folded
+// by the finish kernels (gram.hip: gram_bound_wave); see the model above:
 //   |S - ||g||^2| <= gA X + gQ Y + (gA gQ + g64 (1 + gA)(1 + gQ)) W2 V2
 //   X = sum_p XD_p + sum_p W2_p ||Q^_pp,off||_F + 2 sum_{p<q} ||w_p|| ||w_q|| ||Q^_pq||_F
-//   Y likewise with V2 and P^,  g64 = (T^2 + 256) 2^-52 for the fp64 sums.
-DPC_HOST_DEVICE double dpc_gram_bound(const double* rec, int nt, double* sum) {
-  double s = 0.0, X = 0.0, Y = 0.0, W2 = 0.0, V2 = 0.0;
-  const int np = nt * (nt + 1) / 2;
-  for (int j = 0; j < np; ++j) s += rec[(size_t)j * DPC_GRAM_REC_WORDS];
-  *sum = s;
-  for (int q = 0; q < nt; ++q) {
-    const double* dq = rec + (size_t)(q * (q + 3) / 2) * DPC_GRAM_REC_WORDS;
-    W2 += dq[5];
-    V2 += dq[6];
-    for (int p = 0; p <= q; ++p) {
-      const double* r = rec + (size_t)(q * (q + 1) / 2 + p) * DPC_GRAM_REC_WORDS;
-      if (p == q) {
-        X += r[3] + r[5] * sqrt(r[2]);
-        Y += r[4] + r[6] * sqrt(r[1]);
-      } else {
-        const double* dp = rec + (size_t)(p * (p + 3) / 2) * DPC_GRAM_REC_WORDS;
-        X += 2.0 * sqrt(dp[5] * dq[5] * r[2]);
-        Y += 2.0 * sqrt(dp[6] * dq[6] * r[1]);
-      }
-    }
-  }
-  const double gA = rec[7], gQ = rec[8], T = rec[9];
-  const double g64 = (T * T + 256.0) * 0x1.0p-52;
-  const double err = gA * X + gQ * Y + (gA * gQ + g64 * (1.0 + gA) * (1.0 + gQ)) * W2 * V2;
-  return err * (1.0 + 0x1.0p-40);
-}
+//   Y likewise with V2 and P^,  g64 = (T^2 + 256) 2^-52 for the fp64 sums,
+// inflated by 1 + 2^-40 for the fold's own rounding.
 
 // Remembers the last failing HIP status of the calling thread (abi.hip).
 void dpc_record_error(hipError_t e);

@@ -3,30 +3,28 @@
 // (no per-example gradient is ever formed), with an upper bound on the
 // rounding error of the result, so that the clip factor can be taken from
 // sqnorm + sqerr >= ||G_i^T A_i||^2 (the error model is in common.h).  The
-// T x T Gram matrices are split into 128 x 128 tiles; a workgroup of 4 waves
-// owns one (example, tile pair p <= q) and computes the (p, q) tile of both
-// A A^T and G G^T with bf16 MFMA and fp32 accumulators.  Each wave holds the
-// same 64 x 64 block of both tiles, so the element-wise inner product (fp64)
-// needs no data exchange.  Pairs with p < q count twice (both Gram matrices
-// are symmetric).  Each (example, pair) writes a record to the workspace --
-// the inner product, the squared off-diagonal entries of both tiles and, on
-// diagonal pairs, row weights from the diagonal entries -- and
+// T x T Gram matrices are split into 128 x 128 tiles.  A dense work item
+// stages, per 32-deep K step, the rows of two 128-row blocks p and q of both
+// operands and computes from them the (p, q) tile of both A A^T and G G^T
+// (waves 0..3, the same 64 x 64 block of both tiles each, so the element-wise
+// inner product in fp64 needs no data exchange) and one diagonal tile that
+// needs no other rows (waves 4..7; see dense_item).  Pairs with p < q count
+// twice (both Gram matrices are symmetric).  Each tile writes a record to the
+// workspace -- the inner product, the squared off-diagonal entries of both
+// tiles and, on diagonal tiles, row weights from the diagonal entries -- and
 // gram_finish_kernel folds an example's records in a fixed order into sqnorm
 // and sqerr, so results are deterministic.
 //
-// Two workgroups fit on a CU (64 KiB of LDS, <= 256 registers per lane at 2
-// waves per SIMD), so the 10 pairs x B examples of a typical call are all
-// resident at once.  Workgroups are placed so that all pairs of one example
-// run on one XCD (hardware dispatch is round-robin over the 8 XCDs): the pairs
-// re-read the example's rows from that XCD's L2 instead of from HBM.
-//
-// A lone workgroup has one wave per SIMD, so the K loop hides LDS latency
-// itself: every group of four MFMAs runs while the next group's fragments
-// are read, the barrier sits before a step's last group (which overlaps the
-// next step's first reads), and the loop body has no branch around the
-// accumulators (operands ordered so that din <= dout: the loop is the
-// "both Gram matrices" body for A's K range, then a "G G^T only" body that
-// stages G's tiles alone).
+// Items are placed so that all items of one example run on one XCD (hardware
+// dispatch is round-robin over the 8 XCDs): they re-read the example's rows
+// from that XCD's L2 instead of from HBM.  The K loop hides LDS latency with
+// two fragment sets: every group of four MFMAs runs while the next group's
+// fragments are read, the barrier sits before a step's last group (which
+// overlaps the next step's first reads), and the loop body has no branch
+// around the accumulators (operands ordered so that din <= dout: the loop is
+// the "both Gram matrices" body for A's K range, then a "G G^T only" body
+// that stages G's tiles alone).  The grouped (MoE) kernel runs items of one
+// tile pair on 4 waves.
 #include <mutex>
 
 #include "common.h"
@@ -640,18 +638,58 @@ gram_grouped_generic_kernel(GramItems work, double* __restrict__ records) {
   write_gram_record(st, red, records + (size_t)slot * DPC_GRAM_REC_WORDS, gA, gQ, rows);
 }
 
-// Dense finish: sqnorm[b] (+)= the fold of example b's record inner products
-// in pair order (+ the bias term), sqerr[b] (+)= its error bound (+ the bias
-// term's).  bias (nullable): [B] squared norms then [B] error bounds.
+// dpc_gram_bound's fold of an example's nt (nt + 1) / 2 records by one wave:
+// lane j takes pairs j, j + 64, ..., and the five partial sums are added by
+// a fixed butterfly (every lane ends with the same totals), so the result
+// does not depend on timing; it differs from the serial fold only in the
+// order of its fp64 additions of non-negative terms, which the bound's final
+// 1 + 2^-40 covers.  Returns the bound; *sum = the inner products' sum.
+__device__ __forceinline__ double gram_bound_wave(const double* rec, int nt, double* sum) {
+  const int lane = threadIdx.x & 63;
+  const int np = nt * (nt + 1) / 2;
+  double v[5] = {0.0, 0.0, 0.0, 0.0, 0.0};  // sum, X, Y, W2, V2
+  for (int j = lane; j < np; j += 64) {
+    int p, q;
+    pair_from_index(j, &p, &q);
+    const double* r = rec + (size_t)j * DPC_GRAM_REC_WORDS;
+    v[0] += r[0];
+    if (p == q) {
+      v[1] += r[3] + r[5] * sqrt(r[2]);
+      v[2] += r[4] + r[6] * sqrt(r[1]);
+      v[3] += r[5];
+      v[4] += r[6];
+    } else {
+      const double* dp = rec + (size_t)(p * (p + 3) / 2) * DPC_GRAM_REC_WORDS;
+      const double* dq = rec + (size_t)(q * (q + 3) / 2) * DPC_GRAM_REC_WORDS;
+      v[1] += 2.0 * sqrt(dp[5] * dq[5] * r[2]);
+      v[2] += 2.0 * sqrt(dp[6] * dq[6] * r[1]);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 5; ++k)
+    for (int off = 32; off > 0; off >>= 1) v[k] += __shfl_xor(v[k], off, 64);
+  *sum = v[0];
+  const double gA = rec[7], gQ = rec[8], T = rec[9];
+  const double g64 = (T * T + 256.0) * 0x1.0p-52;
+  const double err =
+      gA * v[1] + gQ * v[2] + (gA * gQ + g64 * (1.0 + gA) * (1.0 + gQ)) * v[3] * v[4];
+  return err * (1.0 + 0x1.0p-40);
+}
+
+// Dense finish, one wave per example: sqnorm[b] (+)= the fold of example b's
+// record inner products (+ the bias term), sqerr[b] (+)= its error bound (+
+// the bias term's).  bias (nullable): [B] squared norms then [B] error
+// bounds.
 __global__ void __launch_bounds__(kGramThreads)
 gram_finish_kernel(const double* __restrict__ records, int B, int nt, int accumulate,
                    const double* __restrict__ bias, double* __restrict__ sqnorm,
                    double* __restrict__ sqerr) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.x * (kGramThreads / 64) + (int)(threadIdx.x >> 6);
   if (b >= B) return;
   const size_t np = (size_t)nt * (nt + 1) / 2;
   double s;
-  const double e = dpc_gram_bound(records + (size_t)b * np * DPC_GRAM_REC_WORDS, nt, &s);
+  const double e = gram_bound_wave(records + (size_t)b * np * DPC_GRAM_REC_WORDS, nt, &s);
+  if ((threadIdx.x & 63) != 0) return;
   double v = accumulate ? sqnorm[b] + s : s;
   if (bias) v = v + bias[b];
   sqnorm[b] = v;
@@ -662,20 +700,22 @@ gram_finish_kernel(const double* __restrict__ records, int B, int nt, int accumu
   }
 }
 
-// Grouped finish: seg_sq[v] / seg_err[v] (nullable) from segment v's records
-// (slots item_start[v] .. item_start[v + 1] - 1, in pair order).
+// Grouped finish, one wave per segment: seg_sq[v] / seg_err[v] (nullable)
+// from segment v's records (slots item_start[v] .. item_start[v + 1] - 1, in
+// pair order).
 __global__ void __launch_bounds__(kGramThreads)
 segment_finish_kernel(const double* __restrict__ records, const int32_t* __restrict__ item_start,
                       int S, double* __restrict__ seg_sq, double* __restrict__ seg_err) {
-  const int v = blockIdx.x * blockDim.x + threadIdx.x;
+  const int v = blockIdx.x * (kGramThreads / 64) + (int)(threadIdx.x >> 6);
   if (v >= S) return;
   const int first = item_start[v], np = item_start[v + 1] - first;
   double s = 0.0, e = 0.0;
   if (np > 0) {
     int nt = 0;
     while ((nt + 1) * (nt + 2) / 2 <= np) ++nt;
-    e = dpc_gram_bound(records + (size_t)first * DPC_GRAM_REC_WORDS, nt, &s);
+    e = gram_bound_wave(records + (size_t)first * DPC_GRAM_REC_WORDS, nt, &s);
   }
+  if ((threadIdx.x & 63) != 0) return;
   seg_sq[v] = s;
   if (seg_err) seg_err[v] = e;
 }
@@ -807,7 +847,7 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
     }
     DPC_HIP_CHECK(hipGetLastError());
   }
-  hipLaunchKernelGGL(gram_finish_kernel, dim3(ceil_div(B, kGramThreads)), dim3(kGramThreads), 0,
+  hipLaunchKernelGGL(gram_finish_kernel, dim3(ceil_div(B, kGramThreads / 64)), dim3(kGramThreads), 0,
                      s, (const double*)records, B, nt, accumulate, (const double*)bias, sqnorm,
                      sqerr);
   DPC_HIP_CHECK(hipGetLastError());
@@ -858,7 +898,8 @@ extern "C" int dpc_grouped_gram_sqnorms(const int64_t* a_ptrs, const int64_t* g_
     }
     DPC_HIP_CHECK(hipGetLastError());
   }
-  hipLaunchKernelGGL(segment_finish_kernel, dim3(ceil_div(S, kGramThreads)), dim3(kGramThreads), 0,
+  hipLaunchKernelGGL(segment_finish_kernel, dim3(ceil_div(S, kGramThreads / 64)), dim3(kGramThreads),
+                     0,
                      s, (const double*)records, seg_item_start, S, seg_sq, seg_err);
   DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;

@@ -117,8 +117,9 @@ def per_example_grads_loop(model: torch.nn.Module, loss_fn, args: tuple, targets
 # `err` of its rounding error with every squared norm (the clip factor is taken
 # from sq + err).  The bound is new work of this build -- the reference
 # materialises gradients and has no Gram norm -- so the functions below restate
-# the device formula (opake_amd/csrc/common.h: dpc_chain_gamma, dpc_row_bound,
-# dpc_gram_bound) for the CPU tests, which pin it by its defining property
+# the device formula (opake_amd/csrc/common.h: dpc_chain_gamma, dpc_row_bound;
+# opake_amd/csrc/gram.hip: the tile records and gram_bound_wave) for the CPU
+# tests, which pin it by its defining property
 # |S - ||g||^2| <= err on emulated accumulation chains of the two rounding
 # behaviours the model covers (round-to-nearest, truncation) and on crafted
 # cancellation inputs, with exact float64 gradients as the truth.
