@@ -27,9 +27,10 @@
 //     the exact products of the given bf16 values, times its scale.
 //     Examples with scale 0 are skipped through the clip plan, so their data
 //     (including any NaN/Inf) is never read;
-//   * two LDS stages (128 KiB), one barrier per K step; the DMAs of step
+//   * two LDS stages (128 KiB), one barrier per K step; the A DMAs of step
 //     s + 2 are issued right after the barrier of step s, the moment the
-//     stage is free (grouped mode: the scale + store of G's step s + 1 is
+//     stage is free, dense mode's G DMAs of step s + 2 at the start of step
+//     s + 1 (grouped mode: the scale + store of G's step s + 1 is
 //     interleaved, chunk by chunk, with the MFMAs of step s, and each
 //     chunk's registers are refilled with step s + 2 right after its store).
 //     In dense mode a chunk whose columns lie past the matrix reads the
@@ -535,10 +536,11 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
               __builtin_amdgcn_mfma_f32_16x16x32_bf16(g.f[i], a.f[j], acc[4 * ih + i][j], 0, 0, 0);
     };
 
-    // One K step on stage (gcur, acur); the DMAs of step s + 1 into (gnxt,
-    // anxt) were issued during step s - 1.  A step is four phases (two
-    // 32-deep sub-steps of two phases each).  On entry the fragments of phase
-    // 0 are in flight.
+    // One K step on stage (gcur, acur); the A DMAs of step s + 1 into anxt
+    // were issued during step s - 1.  A step is four phases (two 32-deep
+    // sub-steps of two phases each).  On entry the fragments of phase 0 are
+    // in flight.
+    //   * Phase 0: dense mode issues the G DMAs of step s + 1 into gnxt.
     //   * Phases 0..2: the MFMAs of phase p run while the fragments of phase
     //     p + 1 are read; grouped mode: G chunks of step s + 1 go from the
     //     registers (scaled) into the other stage, and their registers are
@@ -546,17 +548,18 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     //     step.
     //   * Barrier: the other stage is complete (its DMAs have landed, every G
     //     store is done), and this stage's last fragments are in registers.
-    //   * Phase 3: the DMAs of step s + 2 go into this stage (no wave reads it
-    //     any more), and the phase's MFMAs run while the fragments of phase 0
-    //     of step s + 1 are read from the other stage.
+    //   * Phase 3: the A DMAs of step s + 2 go into this stage (no wave reads
+    //     it any more), and the phase's MFMAs run while the fragments of phase
+    //     0 of step s + 1 are read from the other stage.
     // So the MFMAs of every phase, across step boundaries too, overlap the
-    // reads of the next, each DMA has a step and a quarter to land, and the
-    // barrier is the only place a wave waits for the others.  With 8 waves
-    // the sched_group_barriers interleave each phase's MFMAs with the reads
-    // of the next (the scheduler would otherwise bunch them); with the
-    // sched_barriers they also keep each G chunk's store and reload inside
-    // its phase.  Before the barrier only the kGC G loads may still be
-    // outstanding.  Past the last step the DMAs, stores and loads repeat the
+    // reads of the next, an A DMA has a step and a quarter to land and a G
+    // DMA three quarters, and the barrier is the only place a wave waits for
+    // the others.  (Issuing both operands' DMAs together after the barrier
+    // measured 4% slower.)  With 8 waves the sched_group_barriers interleave
+    // each phase's MFMAs with the reads of the next (the scheduler would
+    // otherwise bunch them); with the sched_barriers they also keep each G
+    // chunk's store and reload inside its phase.  Before the barrier only
+    // the kGC G loads may still be outstanding.  Past the last step the DMAs, stores and loads repeat the
     // last step's (in-range) rows into a stage no one reads: every path
     // issues the same memory operations, which keeps the counter waits exact.
     float sc_next = 0.0f;
@@ -628,6 +631,7 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
         }
       };
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (!kGrouped) dma_g(gnxt, row_next);
       read_g16(gcur, 0, 1, gf1);
       mma16(gf0, af0, 0);
       stage_g(0);
@@ -654,10 +658,9 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       valid_next = valid2;
       DPC_WAIT_VMCNT(kGrouped ? kGC : 0);
       __syncthreads();
-      // Every wave has read this stage for the last time: the DMAs of step
+      // Every wave has read this stage for the last time: the A DMAs of step
       // s + 2 go into it now, a quarter step before the next step starts.
       dma_a(acur, row_next, valid_next);
-      if constexpr (!kGrouped) dma_g(gcur, row_next);
       read_g16(gnxt, 0, 0, gf0);
       read_a16(anxt, 0, af0);
       if (vcur > 32) mma16(gf1, af1, 1);
@@ -673,8 +676,9 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     uint8_t* g1 = lds_g1;
     if (nsteps > 0) {
       // Prologue: step 0 into stage 0 (A by DMA; G by DMA in dense mode, else
-      // through registers, scaled), in grouped mode step 1 of G into the
-      // registers; the fragments of step 0's first sub-step.
+      // through registers, scaled), step 1's A DMAs, in grouped mode step 1 of
+      // G into the registers (dense mode: step 0's phase 0 issues step 1's G
+      // DMAs); the fragments of step 0's first sub-step.
       int valid0;
       int row0 = step_row0(0, &sc_next, &valid0);
       valid_cur = valid0;
@@ -694,11 +698,9 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       if constexpr (kGrouped) {
 #pragma unroll
         for (int j = 0; j < kGC; ++j) load_chunk(row_next, valid_next, j);
-      } else {
-        dma_g(g1, row_next);
       }
       // Step 0's transfers have landed (step 1's DMAs and G loads may not).
-      DPC_WAIT_VMCNT(kGrouped ? kDma + kGC : 2 * kDma);
+      DPC_WAIT_VMCNT(kGrouped ? kDma + kGC : kDma);
       __syncthreads();
       read_g16(g0, 0, 0, gf0);
       read_a16(lds_a0, 0, af0);
