@@ -88,7 +88,7 @@ int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int din, int do
  * (dpc_gram_workspace_bytes(B, T) > DPC_NOALLOC_SCRATCH_BYTES) return
  * DPC_ENOSPC.  Every call on a device shares that device's array, so calls
  * that overlap on one device (other streams, other threads) race. */
-#define DPC_NOALLOC_SCRATCH_BYTES (4u << 20)
+#define DPC_NOALLOC_SCRATCH_BYTES (24u << 20)
 int dpc_gram_sqnorms_noalloc(const void* A, const void* G, int B, int T, int din, int dout,
                              int dtype, int with_bias, int accumulate, double* sqnorm,
                              double* sqerr, void* stream);

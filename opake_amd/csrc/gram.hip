@@ -497,6 +497,393 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
                c < 0 ? nullptr : rec + (size_t)(c * (c + 3) / 2) * DPC_GRAM_REC_WORDS, lds, red);
 }
 
+// ---------------------------------------------------------------------------
+// Dense split mode (bf16, din == dout, an even number nt of 128-row blocks):
+// a work item computes Gram tiles of ONE operand.  The upper triangle of an
+// example's T x T Gram matrix is cut into (nt / 2)^2 tile sets:
+//   * nt / 2 diagonal sets: tiles (t, t), (t, t + 1), (t + 1, t + 1), t even
+//     -- the rows of blocks t and t + 1 (8 row blocks of 32), and of the
+//     diagonal tiles only the 32 x 32 blocks on or above the diagonal: 36
+//     blocks;
+//   * off-diagonal sets: tiles (t, q) and (t + 1, q), t even, q >= t + 2 --
+//     the rows of blocks t, t + 1 and q: 32 blocks;
+// and each set is computed twice, for A and for G, by two workgroups (items
+// 2 j and 2 j + 1 of the example).  A workgroup stages one operand's rows (16
+// or 24 KiB per 32-deep K step instead of 32) and holds at most 5 blocks per
+// wave, the 8 waves' blocks balanced over the 4 SIMDs (9 or 8 per SIMD), so
+// B (nt / 2)^2 x 2 items of nearly equal cost cover the chip (256 at B = 32,
+// T = 512).  The two workgroups of a set meet through the workspace: each
+// publishes its accumulators, then takes an atomic ticket; the one with the
+// second ticket reads its partner's accumulators and writes the set's tile
+// records -- the paired kernel's records, from the same fp32 Gram entries (a
+// block above a diagonal tile's diagonal stands for itself and its mirror,
+// which the MFMA computes to the same bits).  No workgroup waits for
+// another.  (Against the paired kernel at B = 32, T = 512, d = 4096: 10%
+// less time, 29% fewer MFMA cycles; the exchange costs 8-13 us of it.)
+// ---------------------------------------------------------------------------
+constexpr int kSplitWaves = 8;
+constexpr int kSplitMaxBlocks = 5;
+constexpr int kSplitWaveBytes = kSplitMaxBlocks * 16 * 64 * 4;  // 20 KiB of accumulators
+constexpr int kSplitSetBytes = kSplitWaves * kSplitWaveBytes;   // 160 KiB per set
+
+DPC_HOST_DEVICE int split_sets_per_example(int nt) { return (nt / 2) * (nt / 2); }
+
+// Tile set j of an example: *t, and *q = -1 for a diagonal set.
+__device__ __forceinline__ void split_set(int j, int nt, int* t, int* q) {
+  if (j < nt / 2) {
+    *t = 2 * j;
+    *q = -1;
+    return;
+  }
+  j -= nt / 2;
+  int tt = 0;
+  while (j >= nt - tt - 2) {
+    j -= nt - tt - 2;
+    tt += 2;
+  }
+  *t = tt;
+  *q = tt + 2 + j;
+}
+
+// The blocks of wave w, as row-block indices f[0..3] of the set's staged rows
+// (0..7: blocks t, t + 1; 8..11: block q) and a kind:
+//   kMacro      blocks (f0, f2), (f0, f3), (f1, f2), (f1, f3)
+//   kExtraRows  those and (f0, f1)
+//   kExtraCols  those and (f2, f3)
+//   kDiag4      blocks (fk, fk), k = 0..3
+// Diagonal set: the six 2 x 2 blocks above the diagonal of the 8 x 8 block
+// grid go to waves 0..5, its four (2 i, 2 i + 1) blocks to waves 0..3 and its
+// diagonal blocks to waves 6, 7 -- so SIMD s (waves s and s + 4) holds 9
+// blocks.  Off-diagonal set: wave w holds rows 2 (w / 2), + 1 by columns 8 + 2
+// (w % 2), + 1.
+enum SplitKind { kMacro = 0, kExtraRows = 1, kExtraCols = 2, kDiag4 = 3 };
+
+__device__ __forceinline__ int split_role(bool diag_set, int w, int f[4]) {
+  if (!diag_set) {
+    f[0] = 2 * (w >> 1);
+    f[1] = f[0] + 1;
+    f[2] = 8 + 2 * (w & 1);
+    f[3] = f[2] + 1;
+    return kMacro;
+  }
+  static constexpr int kF[8][4] = {{0, 1, 2, 3}, {2, 3, 4, 5}, {4, 5, 6, 7}, {2, 3, 6, 7},
+                                   {0, 1, 4, 5}, {0, 1, 6, 7}, {0, 1, 2, 3}, {4, 5, 6, 7}};
+  static constexpr int kKind[8] = {kExtraRows, kExtraRows, kExtraRows, kExtraCols,
+                                   kMacro,     kMacro,     kDiag4,     kDiag4};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) f[k] = kF[w][k];
+  return kKind[w];
+}
+
+template <int kKind>
+struct SplitShape {
+  static constexpr int kBlocks = (kKind == kExtraRows || kKind == kExtraCols) ? 5 : 4;
+  // Operand slots of block b: rows from slot row(b), columns from col(b).
+  static __device__ __forceinline__ int row(int b) {
+    if (kKind == kDiag4) return b;
+    if (b == 4) return kKind == kExtraRows ? 0 : 2;
+    return b >> 1;
+  }
+  static __device__ __forceinline__ int col(int b) {
+    if (kKind == kDiag4) return b;
+    if (b == 4) return kKind == kExtraRows ? 1 : 3;
+    return 2 + (b & 1);
+  }
+};
+
+// Tile-set record statistics of one block: its tile (0: (t, t) or (t, q);
+// 1: (t, t + 1) or (t + 1, q); 2: (t + 1, t + 1)), its weight (2 for a block
+// above a diagonal tile's diagonal: it stands for its mirror too) and whether
+// it holds diagonal entries.
+__device__ __forceinline__ void split_block_tile(bool diag_set, int rb, int cb, int* tile,
+                                                 double* weight, bool* diag_block) {
+  if (diag_set) {
+    *tile = rb < 4 ? (cb < 4 ? 0 : 1) : 2;
+    *weight = (*tile != 1 && rb < cb) ? 2.0 : 1.0;
+    *diag_block = rb == cb;
+  } else {
+    *tile = rb < 4 ? 0 : 1;
+    *weight = 1.0;
+    *diag_block = false;
+  }
+}
+
+template <int kKind, bool diag_set>
+__device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int t,
+                                           int q, const int f[4], int op, int slot,
+                                           double* rec_ex, int32_t* tickets,
+                                           float* __restrict__ xbuf, uint8_t* lds, double* red,
+                                           int* ticket_lds) {
+  typedef SplitShape<kKind> S;
+  constexpr int kB = S::kBlocks;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  constexpr int ntr = diag_set ? 2 : 3;  // staged 128-row blocks
+  const int tr_row0[3] = {t * kGramTile, (t + 1) * kGramTile, (diag_set ? t : q) * kGramTile};
+  constexpr int kStage = 3 * kGTileBytes;
+
+  // Staging: thread tid moves chunk tid (row tid / 4, 16-byte chunk tid % 4)
+  // of each staged block, two K steps ahead through two register sets.
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(X), (short)0, T * d * 2, 0x00020000);
+  const int crow = tid >> 2, cchunk = tid & 3;
+  int voff[3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) voff[j] = (tr_row0[j] + crow) * d * 2 + cchunk * 16;
+  const int st_off = gtile_off(crow, cchunk);
+  struct Regs {
+    u32x4_t x[3];
+  };
+  auto load = [&](int step, Regs& r) __attribute__((always_inline)) {
+    const int bad = step * kGK + cchunk * 8 < d ? 0 : kGramOutOfRange;
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      if (j < ntr)
+        r.x[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (voff[j] + step * kGK * 2) | bad, 0, 0);
+  };
+  auto store = [&](uint8_t* stage, const Regs& r) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      if (j < ntr) *reinterpret_cast<u32x4_t*>(stage + j * kGTileBytes + st_off) = r.x[j];
+  };
+
+  // Fragment of row block f[k] at 16-deep sub-step kk: lane l reads row l % 32
+  // of the block, k chunk 2 kk + l / 32 (the 32x32x16 operand layout); sub-step
+  // 1's chunk is sub-step 0's with bit 1 set, i.e. its offset XOR 32.
+  int foff[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    foff[k] = (f[k] >> 2) * kGTileBytes + gtile_off((f[k] & 3) * 32 + (lane & 31), lane >> 5);
+  struct Frags {
+    bf16x8_t v[4];
+  };
+  auto read = [&](const uint8_t* stage, int kk, Frags& fr) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      fr.v[k] = *reinterpret_cast<const bf16x8_t*>(stage + (foff[k] ^ (32 * kk)));
+  };
+  f32x16_t acc[kB];
+#pragma unroll
+  for (int b = 0; b < kB; ++b) acc[b] = f32x16_t{};
+  auto mma = [&](const Frags& fr) __attribute__((always_inline)) {
+#pragma unroll
+    for (int b = 0; b < kB; ++b)
+      acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr.v[S::row(b)], fr.v[S::col(b)], acc[b],
+                                                       0, 0, 0);
+  };
+
+  // The K loop of the paired kernel's G-only steps: sub-step 1's fragments
+  // are read before sub-step 0's MFMAs, the next step's rows (loaded two
+  // steps earlier) go into the other stage before the barrier and the
+  // registers are reloaded, and sub-step 0 of the next step is read (from
+  // the other stage) before this step's second MFMA group.  (Storing at the
+  // start of the step measured slower.)
+  const int nk = ceil_div(d, kGK);
+  Regs R[2];
+  load(0, R[0]);
+  store(lds, R[0]);
+  load(1, R[1]);
+  load(2, R[0]);
+  __syncthreads();
+  Frags fx, fy;
+  read(lds, 0, fx);
+  auto step = [&](int s, Regs& rn) __attribute__((always_inline)) {
+    const uint8_t* cur = lds + (s & 1) * kStage;
+    uint8_t* nxt = lds + ((s + 1) & 1) * kStage;
+    read(cur, 1, fy);
+    mma(fx);
+    __builtin_amdgcn_sched_barrier(0);
+    store(nxt, rn);
+    load(s + 3, rn);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    read(nxt, 0, fx);
+    mma(fy);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int s = 0;
+  for (; s + 1 < nk; s += 2) {
+    step(s, R[1]);
+    step(s + 1, R[0]);
+  }
+  if (s < nk) step(s, R[1]);
+
+  // Meet the set's other workgroup.  Both publish their accumulators (1 KiB
+  // per store instruction), wait for their stores to complete, and take an
+  // atomic ticket with device-scope acquire-release semantics (the release
+  // makes every wave's completed stores visible device-wide -- the two
+  // workgroups may sit on different XCDs, whose L2 caches are not coherent
+  // -- and the acquire makes the partner's visible to this workgroup); the
+  // one that takes the second ticket reads its partner's accumulators and
+  // writes the records.  Nobody waits for anybody.  (The waves of a
+  // diagonal set run different instantiations of this function: the ticket
+  // goes through the kernel's LDS word.)
+  float4* base = reinterpret_cast<float4*>(xbuf) + (size_t)slot * (2 * kSplitSetBytes / 16);
+  float4* mine = base + (size_t)op * (kSplitSetBytes / 16) + (size_t)w * (kSplitWaveBytes / 16);
+  const float4* theirs =
+      base + (size_t)(op ^ 1) * (kSplitSetBytes / 16) + (size_t)w * (kSplitWaveBytes / 16);
+#pragma unroll
+  for (int b = 0; b < kB; ++b)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4)
+      mine[(b * 4 + r4) * 64 + lane] =
+          make_float4(acc[b][4 * r4], acc[b][4 * r4 + 1], acc[b][4 * r4 + 2], acc[b][4 * r4 + 3]);
+  DPC_WAIT_VMCNT(0);
+  __syncthreads();
+  if (tid == 0)
+    *ticket_lds = __hip_atomic_fetch_add(&tickets[slot], 1, __ATOMIC_ACQ_REL,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (*ticket_lds == 0) return;
+  if (tid == 0) tickets[slot] = 0;  // the partner has taken its ticket: reset for the next call
+
+  // Statistics per tile of the set (the paired kernel's record words; A's
+  // Gram is P, G's is Q), block by block: the partner's block is read, the
+  // block's words are summed over the lanes (shuffle tree) and added into
+  // this wave's LDS slot of its tile; then the slots are summed over the
+  // waves in order.
+  const double gam = dpc_chain_gamma((double)nk * kGK, DPC_GRAM_U_MFMA);
+  const double eta = (double)nk * kGK * 0x1.0p-125;
+  if (lane < 3 * kRecStat) red[((lane / kRecStat) * kSplitWaves + w) * kRecStat + lane % kRecStat] = 0.0;
+  // All of the partner's blocks are requested before any is used.
+  f32x16_t others[kB];
+#pragma unroll
+  for (int b = 0; b < kB; ++b)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const float4 x = theirs[(b * 4 + r4) * 64 + lane];
+      others[b][4 * r4] = x.x;
+      others[b][4 * r4 + 1] = x.y;
+      others[b][4 * r4 + 2] = x.z;
+      others[b][4 * r4 + 3] = x.w;
+    }
+#pragma unroll
+  for (int b = 0; b < kB; ++b) {
+    const f32x16_t& other = others[b];
+    int tile;
+    double wgt;
+    bool dblk;
+    split_block_tile(diag_set, f[S::row(b)], f[S::col(b)], &tile, &wgt, &dblk);
+    double v[kRecStat] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+    float da = 0.0f, dg = 0.0f;
+    bool has_diag = false;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const double a = op == 0 ? acc[b][r] : other[r];
+      const double g = op == 0 ? other[r] : acc[b][r];
+      v[0] += a * g;
+      const bool on_diag = dblk && ((r >> 2) * 8 + 4 * (lane >> 5) + (r & 3)) == (lane & 31);
+      v[1] += on_diag ? 0.0 : a * a;
+      v[2] += on_diag ? 0.0 : g * g;
+      da = on_diag ? (float)a : da;
+      dg = on_diag ? (float)g : dg;
+      has_diag = has_diag || on_diag;
+    }
+    if (has_diag) {
+      const double ws = dpc_row_bound(da, gam, eta, DPC_GRAM_ROW_SLACK_MFMA);
+      const double vs = dpc_row_bound(dg, gam, eta, DPC_GRAM_ROW_SLACK_MFMA);
+      v[3] = ws * ws * fabs((double)dg);
+      v[4] = vs * vs * fabs((double)da);
+      v[5] = ws * ws;
+      v[6] = vs * vs;
+    }
+    // Weight 2 (exact) for a block that stands for its mirror as well.
+    v[0] *= wgt;
+    v[1] *= wgt;
+    v[2] *= wgt;
+#pragma unroll
+    for (int k = 0; k < kRecStat; ++k)
+      for (int off = 32; off > 0; off >>= 1) v[k] += __shfl_down(v[k], off, 64);
+    if (lane == 0) {
+#pragma unroll
+      for (int k = 0; k < kRecStat; ++k) red[(tile * kSplitWaves + w) * kRecStat + k] += v[k];
+    }
+  }
+  __syncthreads();
+
+  // Records.
+  const int ntiles = diag_set ? 3 : 2;
+  int pair[3];
+  if (diag_set) {
+    pair[0] = t * (t + 3) / 2;
+    pair[1] = (t + 1) * (t + 2) / 2 + t;
+    pair[2] = (t + 1) * (t + 4) / 2;
+  } else {
+    pair[0] = q * (q + 1) / 2 + t;
+    pair[1] = q * (q + 1) / 2 + t + 1;
+    pair[2] = 0;
+  }
+  if (tid < 3 * DPC_GRAM_REC_WORDS) {
+    const int u = tid / DPC_GRAM_REC_WORDS, k = tid % DPC_GRAM_REC_WORDS;
+    if (u < ntiles) {
+      double val;
+      if (k < kRecStat) {
+        val = 0.0;
+        for (int i = 0; i < kSplitWaves; ++i) val += red[(u * kSplitWaves + i) * kRecStat + k];
+        // The off-diagonal tile of the pair counts twice (exact).
+        const bool offdiag = !diag_set || u == 1;
+        if (k == 0 && offdiag) val *= 2.0;
+      } else {
+        val = k == 7 ? gam : k == 8 ? gam : k == 9 ? (double)T : 0.0;
+      }
+      rec_ex[(size_t)pair[u] * DPC_GRAM_REC_WORDS + k] = val;
+    }
+  }
+}
+
+// Dense split mode: item l (after the XCD remap: an example's items, and
+// the two items of each set, share an XCD) is operand l % 2 of set (l / 2) %
+// nsets of example l / (2 nsets).
+__global__ void __launch_bounds__(512, 1)
+gram_split_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ G, int T,
+                       int d, int npairs, int nsets, int nblocks, double* __restrict__ records,
+                       int32_t* __restrict__ tickets, float* __restrict__ xbuf) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * 3 * kGTileBytes];
+  __shared__ double red[3 * kSplitWaves * kRecStat];
+  __shared__ int ticket_lds;
+  const int l = xcd_logical_block(gridDim.x, nblocks);
+  if (l < 0) return;  // padding workgroup: exits before any barrier
+  const int op = l & 1, set = (l >> 1) % nsets, ex = (l >> 1) / nsets;
+  const int nt = ceil_div(T, kGramTile);
+  int t, q;
+  split_set(set, nt, &t, &q);
+  const bool diag_set = q < 0;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int f[4];
+  const int kind = split_role(diag_set, w, f);
+  const uint16_t* X = (op == 0 ? A : G) + (size_t)ex * T * d;
+  double* rec_ex = records + (size_t)ex * npairs * DPC_GRAM_REC_WORDS;
+  const int slot = (l >> 1);
+  if (!diag_set) {
+    split_item<kMacro, false>(X, T, d, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
+                              &ticket_lds);
+    return;
+  }
+  switch (kind) {
+    case kMacro:
+      split_item<kMacro, true>(X, T, d, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
+                               &ticket_lds);
+      break;
+    case kExtraRows:
+      split_item<kExtraRows, true>(X, T, d, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
+                                   &ticket_lds);
+      break;
+    case kExtraCols:
+      split_item<kExtraCols, true>(X, T, d, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
+                                   &ticket_lds);
+      break;
+    default:
+      split_item<kDiag4, true>(X, T, d, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
+                               &ticket_lds);
+      break;
+  }
+}
+
+__global__ void __launch_bounds__(kGramThreads) fill_zero_i32_kernel(int32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
 // Grouped mode: work item l is (problem << 16 | pair, first row, rows, slot)
 // -- the tile pair `pair` of the rows-long segment starting at `first row` of
 // problem `problem`'s operands (a_ptrs / g_ptrs, widths din[problem] /
@@ -788,12 +1175,31 @@ row_sum_f64_kernel(const double* __restrict__ x, int B, int n, int accumulate,
 
 }  // namespace
 
+namespace {
+// Workspace of dpc_gram_sqnorms: the tile records (sized for the generic
+// path's 64-row tiles, which bound the MFMA paths' counts) and the bias
+// terms; when T spans an even number of 128-row blocks, then the split
+// mode's tickets (one per tile set) and accumulator exchange area (both
+// operands' accumulators of every set), each 256-byte aligned.
+size_t gram_records_bytes(int B, int T) {
+  const int nt = ceil_div(T, kGenTile);
+  const size_t npairs = (size_t)nt * (nt + 1) / 2;
+  return (npairs * (size_t)B * DPC_GRAM_REC_WORDS + 2 * (size_t)B) * sizeof(double);
+}
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+bool split_shape(int T) { return ceil_div(T, kGramTile) % 2 == 0; }
+size_t split_tickets_bytes(int B, int T) {
+  return align256((size_t)B * split_sets_per_example(ceil_div(T, kGramTile)) * sizeof(int32_t));
+}
+}  // namespace
+
 extern "C" size_t dpc_gram_workspace_bytes(int B, int T) {
   if (B <= 0 || T <= 0) return 0;
-  // Tile counts for the generic path (64-row tiles) bound the MFMA path's.
-  int nt = ceil_div(T, kGenTile);
-  size_t npairs = (size_t)nt * (nt + 1) / 2;
-  return (npairs * (size_t)B * DPC_GRAM_REC_WORDS + 2 * (size_t)B) * sizeof(double);
+  size_t n = align256(gram_records_bytes(B, T));
+  if (split_shape(T))
+    n += split_tickets_bytes(B, T) +
+         (size_t)B * split_sets_per_example(ceil_div(T, kGramTile)) * 2 * kSplitSetBytes;
+  return n;
 }
 
 extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int din, int dout,
@@ -813,7 +1219,21 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
   const size_t dmax = (size_t)(din > dout ? din : dout);
   const bool fits = ((size_t)T + kGramTile) * dmax * 2 < ((size_t)1 << 31);
   const bool mfma = dtype == DPC_BF16 && din % 8 == 0 && dout % 8 == 0 && fits;
-  if (mfma) {
+  if (mfma && din == dout && split_shape(T)) {
+    // One operand per work item; the tickets start at zero.
+    nt = ceil_div(T, kGramTile);
+    const int npairs = nt * (nt + 1) / 2;
+    const int nsets = split_sets_per_example(nt);
+    const int nblocks = 2 * nsets * B;
+    const int padded = ceil_div(nblocks, kXcds) * kXcds;
+    uint8_t* base = (uint8_t*)ws + align256(gram_records_bytes(B, T));
+    int32_t* tickets = (int32_t*)base;
+    float* xbuf = (float*)(base + split_tickets_bytes(B, T));
+    hipLaunchKernelGGL(fill_zero_i32_kernel, dim3(ceil_div(nsets * B, kGramThreads)),
+                       dim3(kGramThreads), 0, s, tickets, nsets * B);
+    hipLaunchKernelGGL(gram_split_bf16_kernel, dim3(padded), dim3(512), 0, s, (const uint16_t*)A,
+                       (const uint16_t*)G, T, din, npairs, nsets, nblocks, records, tickets, xbuf);
+  } else if (mfma) {
     nt = ceil_div(T, kGramTile);
     const int npairs = nt * (nt + 1) / 2;
     const int items = dense_items_per_example(nt);

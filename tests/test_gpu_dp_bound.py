@@ -60,6 +60,8 @@ def _exact_sq(A, G):
     (torch.bfloat16, 128, 256, 512),   # MFMA kernel, one tile
     (torch.bfloat16, 300, 64, 1024),   # MFMA kernel, 3 tiles, ragged, d_in < d_out
     (torch.bfloat16, 256, 1024, 64),   # MFMA kernel, operands swapped
+    (torch.bfloat16, 512, 256, 256),   # MFMA, one operand per item (diagonal + off-diagonal sets)
+    (torch.bfloat16, 200, 96, 96),     # MFMA, one operand per item, ragged second block
     (torch.float32, 130, 72, 40),      # generic kernel (fp64 accumulation)
     (torch.bfloat16, 70, 36, 20),      # generic kernel, misaligned widths
 ])
@@ -92,6 +94,22 @@ def test_gram_error_bound_matches_oracle_formula(dev):
     for b in range(B):
         Ad, Gd = A[b].double().numpy(), G[b].double().numpy()
         _, want = ghost_oracle.gram_error_bound(Ad @ Ad.T, Gd @ Gd.T, d_p=din, d_q=dout)
+        assert err[b].item() == pytest.approx(want, rel=1e-3)
+
+
+def test_gram_error_bound_matches_oracle_formula_split_items(dev):
+    # As above for the kernel that computes one operand per work item (din ==
+    # dout, an even number of 128-row blocks), whose diagonal tiles come from
+    # their upper-triangular 32 x 32 blocks.
+    gen = _gen(4)
+    B, T, d = 2, 512, 192
+    A = torch.randn(B, T, d, generator=gen).to(torch.bfloat16)
+    G = (torch.randn(B, T, d, generator=gen) * 0.1).to(torch.bfloat16)
+    sq, err = ops.gram_sqnorms(A.to(dev), G.to(dev), return_error=True)
+    torch.testing.assert_close(sq.cpu(), _exact_sq(A, G), rtol=1e-4, atol=0)
+    for b in range(B):
+        Ad, Gd = A[b].double().numpy(), G[b].double().numpy()
+        _, want = ghost_oracle.gram_error_bound(Ad @ Ad.T, Gd @ Gd.T, d_p=d, d_q=d)
         assert err[b].item() == pytest.approx(want, rel=1e-3)
 
 

@@ -55,7 +55,12 @@ def _exact_sqnorms(A, G, bias=False):
 
 @pytest.mark.parametrize(
     "B,T,din,dout",
-    [(3, 128, 64, 64), (2, 200, 136, 72), (2, 512, 256, 128), (1, 1, 8, 8), (4, 130, 64, 40)],
+    [(3, 128, 64, 64), (2, 200, 136, 72), (2, 512, 256, 128), (1, 1, 8, 8), (4, 130, 64, 40),
+     # din == dout and an even number of 128-row blocks: one operand per work
+     # item (diagonal and off-diagonal tile sets, a ragged last block, 16 sets)
+     (2, 256, 64, 64), (3, 512, 128, 128), (2, 200, 72, 72), (2, 1024, 64, 64),
+     # din == dout with an odd number of blocks: the paired kernel
+     (2, 384, 96, 96)],
 )
 @pytest.mark.parametrize("bias", [False, True])
 def test_gram_sqnorms_bf16(dev, B, T, din, dout, bias):

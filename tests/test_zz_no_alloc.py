@@ -21,7 +21,7 @@ from opake_amd.exceptions import OperationError
 
 pytestmark = pytest.mark.gpu
 
-SCRATCH_BYTES = 4 << 20
+SCRATCH_BYTES = 24 << 20
 
 
 def _noalloc(A, G, *, with_bias, out=None, err=None):
