@@ -498,8 +498,10 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
 }
 
 // ---------------------------------------------------------------------------
-// Dense split mode (bf16, din == dout, an even number nt of 128-row blocks):
-// a work item computes Gram tiles of ONE operand.  The upper triangle of an
+// Dense split mode (bf16, an even number nt of 128-row blocks): a work item
+// computes Gram tiles of ONE operand (A's K loop runs over din, G's over
+// dout; with din != dout the two items of a set differ in length, and the
+// dispatcher packs the short ones between the long ones).  The upper triangle of an
 // example's T x T Gram matrix is cut into (nt / 2)^2 tile sets:
 //   * nt / 2 diagonal sets: tiles (t, t), (t, t + 1), (t + 1, t + 1), t even
 //     -- the rows of blocks t and t + 1 (8 row blocks of 32), and of the
@@ -609,8 +611,8 @@ __device__ __forceinline__ void split_block_tile(bool diag_set, int rb, int cb, 
 }
 
 template <int kKind, bool diag_set>
-__device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int t,
-                                           int q, const int f[4], int op, int slot,
+__device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int din, int dout,
+                                           int t, int q, const int f[4], int op, int slot,
                                            double* rec_ex, int32_t* tickets,
                                            float* __restrict__ xbuf, uint8_t* lds, double* red,
                                            int* ticket_lds) {
@@ -738,12 +740,15 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
   if (tid == 0) tickets[slot] = 0;  // the partner has taken its ticket: reset for the next call
 
   // Statistics per tile of the set (the paired kernel's record words; A's
-  // Gram is P, G's is Q), block by block: the partner's block is read, the
+  // Gram is P, G's is Q, each with the gamma of its own chain -- the bound is
+  // symmetric in the two), block by block: the partner's block is read, the
   // block's words are summed over the lanes (shuffle tree) and added into
   // this wave's LDS slot of its tile; then the slots are summed over the
   // waves in order.
-  const double gam = dpc_chain_gamma((double)nk * kGK, DPC_GRAM_U_MFMA);
-  const double eta = (double)nk * kGK * 0x1.0p-125;
+  const int nka = ceil_div(din, kGK), nkg = ceil_div(dout, kGK);
+  const double gA = dpc_chain_gamma((double)nka * kGK, DPC_GRAM_U_MFMA);
+  const double gQ = dpc_chain_gamma((double)nkg * kGK, DPC_GRAM_U_MFMA);
+  const double etaA = (double)nka * kGK * 0x1.0p-125, etaQ = (double)nkg * kGK * 0x1.0p-125;
   if (lane < 3 * kRecStat) red[((lane / kRecStat) * kSplitWaves + w) * kRecStat + lane % kRecStat] = 0.0;
   // All of the partner's blocks are requested before any is used.
   f32x16_t others[kB];
@@ -780,8 +785,8 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
       has_diag = has_diag || on_diag;
     }
     if (has_diag) {
-      const double ws = dpc_row_bound(da, gam, eta, DPC_GRAM_ROW_SLACK_MFMA);
-      const double vs = dpc_row_bound(dg, gam, eta, DPC_GRAM_ROW_SLACK_MFMA);
+      const double ws = dpc_row_bound(da, gA, etaA, DPC_GRAM_ROW_SLACK_MFMA);
+      const double vs = dpc_row_bound(dg, gQ, etaQ, DPC_GRAM_ROW_SLACK_MFMA);
       v[3] = ws * ws * fabs((double)dg);
       v[4] = vs * vs * fabs((double)da);
       v[5] = ws * ws;
@@ -824,7 +829,7 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
         const bool offdiag = !diag_set || u == 1;
         if (k == 0 && offdiag) val *= 2.0;
       } else {
-        val = k == 7 ? gam : k == 8 ? gam : k == 9 ? (double)T : 0.0;
+        val = k == 7 ? gA : k == 8 ? gQ : k == 9 ? (double)T : 0.0;
       }
       rec_ex[(size_t)pair[u] * DPC_GRAM_REC_WORDS + k] = val;
     }
@@ -836,8 +841,9 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
 // nsets of example l / (2 nsets).
 __global__ void __launch_bounds__(512, 1)
 gram_split_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ G, int T,
-                       int d, int npairs, int nsets, int nblocks, double* __restrict__ records,
-                       int32_t* __restrict__ tickets, float* __restrict__ xbuf) {
+                       int din, int dout, int npairs, int nsets, int nblocks,
+                       double* __restrict__ records, int32_t* __restrict__ tickets,
+                       float* __restrict__ xbuf) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * 3 * kGTileBytes];
   __shared__ double red[3 * kSplitWaves * kRecStat];
   __shared__ int ticket_lds;
@@ -851,29 +857,30 @@ gram_split_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int f[4];
   const int kind = split_role(diag_set, w, f);
-  const uint16_t* X = (op == 0 ? A : G) + (size_t)ex * T * d;
+  const int d = op == 0 ? din : dout;
+  const uint16_t* X = (op == 0 ? A + (size_t)ex * T * din : G + (size_t)ex * T * dout);
   double* rec_ex = records + (size_t)ex * npairs * DPC_GRAM_REC_WORDS;
   const int slot = (l >> 1);
   if (!diag_set) {
-    split_item<kMacro, false>(X, T, d, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
+    split_item<kMacro, false>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
                               &ticket_lds);
     return;
   }
   switch (kind) {
     case kMacro:
-      split_item<kMacro, true>(X, T, d, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
+      split_item<kMacro, true>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
                                &ticket_lds);
       break;
     case kExtraRows:
-      split_item<kExtraRows, true>(X, T, d, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
+      split_item<kExtraRows, true>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
                                    &ticket_lds);
       break;
     case kExtraCols:
-      split_item<kExtraCols, true>(X, T, d, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
+      split_item<kExtraCols, true>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
                                    &ticket_lds);
       break;
     default:
-      split_item<kDiag4, true>(X, T, d, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
+      split_item<kDiag4, true>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
                                &ticket_lds);
       break;
   }
@@ -1219,7 +1226,7 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
   const size_t dmax = (size_t)(din > dout ? din : dout);
   const bool fits = ((size_t)T + kGramTile) * dmax * 2 < ((size_t)1 << 31);
   const bool mfma = dtype == DPC_BF16 && din % 8 == 0 && dout % 8 == 0 && fits;
-  if (mfma && din == dout && split_shape(T)) {
+  if (mfma && split_shape(T)) {
     // One operand per work item; the tickets start at zero.
     nt = ceil_div(T, kGramTile);
     const int npairs = nt * (nt + 1) / 2;
@@ -1232,7 +1239,8 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
     hipLaunchKernelGGL(fill_zero_i32_kernel, dim3(ceil_div(nsets * B, kGramThreads)),
                        dim3(kGramThreads), 0, s, tickets, nsets * B);
     hipLaunchKernelGGL(gram_split_bf16_kernel, dim3(padded), dim3(512), 0, s, (const uint16_t*)A,
-                       (const uint16_t*)G, T, din, npairs, nsets, nblocks, records, tickets, xbuf);
+                       (const uint16_t*)G, T, din, dout, npairs, nsets, nblocks, records, tickets,
+                       xbuf);
   } else if (mfma) {
     nt = ceil_div(T, kGramTile);
     const int npairs = nt * (nt + 1) / 2;
