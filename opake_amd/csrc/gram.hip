@@ -615,7 +615,7 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
                                            int t, int q, const int f[4], int op, int slot,
                                            double* rec_ex, int32_t* tickets,
                                            float* __restrict__ xbuf, uint8_t* lds, double* red,
-                                           int* ticket_lds) {
+                                           int* ticket_lds, int my_xcc) {
   typedef SplitShape<kKind> S;
   constexpr int kB = S::kBlocks;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -712,14 +712,16 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
 
   // Meet the set's other workgroup.  Both publish their accumulators (1 KiB
   // per store instruction), wait for their stores to complete, and take an
-  // atomic ticket with device-scope acquire-release semantics (the release
-  // makes every wave's completed stores visible device-wide -- the two
-  // workgroups may sit on different XCDs, whose L2 caches are not coherent
-  // -- and the acquire makes the partner's visible to this workgroup); the
-  // one that takes the second ticket reads its partner's accumulators and
-  // writes the records.  Nobody waits for anybody.  (The waves of a
-  // diagonal set run different instantiations of this function: the ticket
-  // goes through the kernel's LDS word.)
+  // atomic ticket; the one that takes the second ticket reads its partner's
+  // accumulators and writes the records.  Nobody waits for anybody.  Where
+  // the data meets depends on the XCDs of the two workgroups (published at
+  // their start, see below): on one XCD its L2 cache holds the stores and
+  // the reader only drops stale lines from its CU's L1; otherwise (or when
+  // the partner's XCD is not known yet) the writer's ticket carries a
+  // device-scope release and the reader's a device-scope acquire, which
+  // write the stores back past the writer's L2 and drop the reader's stale
+  // L2 lines.  (The waves of a diagonal set run different instantiations of
+  // this function: the ticket goes through the kernel's LDS words.)
   float4* base = reinterpret_cast<float4*>(xbuf) + (size_t)slot * (2 * kSplitSetBytes / 16);
   float4* mine = base + (size_t)op * (kSplitSetBytes / 16) + (size_t)w * (kSplitWaveBytes / 16);
   const float4* theirs =
@@ -732,12 +734,21 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
           make_float4(acc[b][4 * r4], acc[b][4 * r4 + 1], acc[b][4 * r4 + 2], acc[b][4 * r4 + 3]);
   DPC_WAIT_VMCNT(0);
   __syncthreads();
-  if (tid == 0)
-    *ticket_lds = __hip_atomic_fetch_add(&tickets[slot], 1, __ATOMIC_ACQ_REL,
-                                         __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) {
+    const int partner =
+        __hip_atomic_load(&tickets[3 * slot + 1 + (op ^ 1)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool same = partner == my_xcc + 1;
+    if (!same) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    ticket_lds[0] = __hip_atomic_fetch_add(&tickets[3 * slot], 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    ticket_lds[1] = same;
+  }
   __syncthreads();
-  if (*ticket_lds == 0) return;
-  if (tid == 0) tickets[slot] = 0;  // the partner has taken its ticket: reset for the next call
+  if (ticket_lds[0] == 0) return;
+  if (ticket_lds[1])
+    asm volatile("buffer_inv sc0" ::: "memory");  // drop stale lines from this CU's L1
+  else
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 
   // Statistics per tile of the set (the paired kernel's record words; A's
   // Gram is P, G's is Q, each with the gamma of its own chain -- the bound is
@@ -846,7 +857,7 @@ gram_split_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
                        float* __restrict__ xbuf) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * 3 * kGTileBytes];
   __shared__ double red[3 * kSplitWaves * kRecStat];
-  __shared__ int ticket_lds;
+  __shared__ int ticket_lds[2];
   const int l = xcd_logical_block(gridDim.x, nblocks);
   if (l < 0) return;  // padding workgroup: exits before any barrier
   const int op = l & 1, set = (l >> 1) % nsets, ex = (l >> 1) / nsets;
@@ -861,27 +872,35 @@ gram_split_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
   const uint16_t* X = (op == 0 ? A + (size_t)ex * T * din : G + (size_t)ex * T * dout);
   double* rec_ex = records + (size_t)ex * npairs * DPC_GRAM_REC_WORDS;
   const int slot = (l >> 1);
+  // This workgroup's XCD, published for the partner (tickets[3 slot + 1 +
+  // op] = xcc + 1; 0 until published).
+  int xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  xcc &= 0xf;
+  if (threadIdx.x == 0)
+    __hip_atomic_store(&tickets[3 * slot + 1 + op], xcc + 1, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   if (!diag_set) {
     split_item<kMacro, false>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
-                              &ticket_lds);
+                              ticket_lds, xcc);
     return;
   }
   switch (kind) {
     case kMacro:
       split_item<kMacro, true>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
-                               &ticket_lds);
+                               ticket_lds, xcc);
       break;
     case kExtraRows:
       split_item<kExtraRows, true>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
-                                   &ticket_lds);
+                                   ticket_lds, xcc);
       break;
     case kExtraCols:
       split_item<kExtraCols, true>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
-                                   &ticket_lds);
+                                   ticket_lds, xcc);
       break;
     default:
       split_item<kDiag4, true>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
-                               &ticket_lds);
+                               ticket_lds, xcc);
       break;
   }
 }
@@ -1186,8 +1205,9 @@ namespace {
 // Workspace of dpc_gram_sqnorms: the tile records (sized for the generic
 // path's 64-row tiles, which bound the MFMA paths' counts) and the bias
 // terms; when T spans an even number of 128-row blocks, then the split
-// mode's tickets (one per tile set) and accumulator exchange area (both
-// operands' accumulators of every set), each 256-byte aligned.
+// mode's tickets (a counter and the two items' XCDs per tile set) and
+// accumulator exchange area (both operands' accumulators of every set), each
+// 256-byte aligned.
 size_t gram_records_bytes(int B, int T) {
   const int nt = ceil_div(T, kGenTile);
   const size_t npairs = (size_t)nt * (nt + 1) / 2;
@@ -1196,7 +1216,7 @@ size_t gram_records_bytes(int B, int T) {
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 bool split_shape(int T) { return ceil_div(T, kGramTile) % 2 == 0; }
 size_t split_tickets_bytes(int B, int T) {
-  return align256((size_t)B * split_sets_per_example(ceil_div(T, kGramTile)) * sizeof(int32_t));
+  return align256((size_t)3 * B * split_sets_per_example(ceil_div(T, kGramTile)) * sizeof(int32_t));
 }
 }  // namespace
 
@@ -1236,8 +1256,8 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
     uint8_t* base = (uint8_t*)ws + align256(gram_records_bytes(B, T));
     int32_t* tickets = (int32_t*)base;
     float* xbuf = (float*)(base + split_tickets_bytes(B, T));
-    hipLaunchKernelGGL(fill_zero_i32_kernel, dim3(ceil_div(nsets * B, kGramThreads)),
-                       dim3(kGramThreads), 0, s, tickets, nsets * B);
+    hipLaunchKernelGGL(fill_zero_i32_kernel, dim3(ceil_div(3 * nsets * B, kGramThreads)),
+                       dim3(kGramThreads), 0, s, tickets, 3 * nsets * B);
     hipLaunchKernelGGL(gram_split_bf16_kernel, dim3(padded), dim3(512), 0, s, (const uint16_t*)A,
                        (const uint16_t*)G, T, din, dout, npairs, nsets, nblocks, records, tickets,
                        xbuf);
