@@ -511,7 +511,8 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
 //     the rows of blocks t, t + 1 and q: 32 blocks;
 // and each set is computed twice, for A and for G, by two workgroups (items
 // 2 j and 2 j + 1 of the example).  A workgroup stages one operand's rows (16
-// or 24 KiB per 32-deep K step instead of 32) and holds at most 5 blocks per
+// or 24 KiB per 32-deep K step instead of 32, by DMA into three LDS stages)
+// and holds at most 5 blocks per
 // wave, the 8 waves' blocks balanced over the 4 SIMDs (9 or 8 per SIMD), so
 // B (nt / 2)^2 x 2 items of nearly equal cost cover the chip (256 at B = 32,
 // T = 512).  The two workgroups of a set meet through the workspace: each
@@ -524,6 +525,36 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
 // less time, 29% fewer MFMA cycles; the exchange costs 8-13 us of it.)
 // ---------------------------------------------------------------------------
 constexpr int kSplitWaves = 8;
+typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
+
+// A buffer resource as four scalar words (base, stride 0, size in bytes,
+// flags), the layout __builtin_amdgcn_make_buffer_rsrc builds, for inline
+// assembly.
+__device__ __forceinline__ u32x4_t rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return u32x4_t{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+// buffer_load_dwordx4 ... lds: lane i's 16 bytes at buffer offset voff + soff
+// go to LDS address lds + 16 i.  Inline assembly, so that the compiler does
+// not see an LDS write: it would otherwise make the fragment reads of the
+// other stages wait for every transfer in flight.  The caller orders the
+// transfers with explicit memory-counter waits and barriers.
+__device__ __forceinline__ void dma16(u32x4_t rsrc, uint32_t lds, int voff, int soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+               : "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+  return (uint32_t)reinterpret_cast<uintptr_t>((const lds_u8_t*)p);
+}
+
+template <int P>
+struct StageIdx {
+  static constexpr int value = P;
+};
 constexpr int kSplitMaxBlocks = 5;
 constexpr int kSplitWaveBytes = kSplitMaxBlocks * 16 * 64 * 4;  // 20 KiB of accumulators
 constexpr int kSplitSetBytes = kSplitWaves * kSplitWaveBytes;   // 160 KiB per set
@@ -624,31 +655,22 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
   const int tr_row0[3] = {t * kGramTile, (t + 1) * kGramTile, (diag_set ? t : q) * kGramTile};
   constexpr int kStage = 3 * kGTileBytes;
 
-  // Staging: thread tid moves chunk tid (row tid / 4, 16-byte chunk tid % 4)
-  // of each staged block, two K steps ahead through two register sets.
-  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(X), (short)0, T * d * 2, 0x00020000);
-  const int crow = tid >> 2, cchunk = tid & 3;
-  int voff[3];
+  // Staging by DMA: wave w moves rows 16 w .. 16 w + 15 of each staged
+  // block per K step (one 1 KiB buffer_load ... lds each); lane i the 16
+  // bytes of row 16 w + i / 4 that belong at physical chunk i % 4.
+  const u32x4_t words = rsrc_words(X, (uint32_t)(T * d * 2));
+  const int lrow = 16 * w + (lane >> 2);
+  const int lchunk = (lane & 3) ^ ((lane >> 4) & 3);
+  int dvoff[3];
 #pragma unroll
-  for (int j = 0; j < 3; ++j) voff[j] = (tr_row0[j] + crow) * d * 2 + cchunk * 16;
-  const int st_off = gtile_off(crow, cchunk);
-  struct Regs {
-    u32x4_t x[3];
-  };
-  auto load = [&](int step, Regs& r) __attribute__((always_inline)) {
-    const int bad = step * kGK + cchunk * 8 < d ? 0 : kGramOutOfRange;
+  for (int j = 0; j < 3; ++j) dvoff[j] = (tr_row0[j] + lrow) * d * 2 + lchunk * 16;
+  auto dma = [&](uint8_t* stage, int step) __attribute__((always_inline)) {
+    const int bad = step * kGK + lchunk * 8 < d ? 0 : kGramOutOfRange;
+    const uint32_t base = lds_addr(stage) + w * 1024;
 #pragma unroll
-    for (int j = 0; j < 3; ++j)
-      if (j < ntr)
-        r.x[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (voff[j] + step * kGK * 2) | bad, 0, 0);
+    for (int j = 0; j < ntr; ++j)
+      dma16(words, base + j * kGTileBytes, dvoff[j] | bad, step * kGK * 2);
   };
-  auto store = [&](uint8_t* stage, const Regs& r) __attribute__((always_inline)) {
-#pragma unroll
-    for (int j = 0; j < 3; ++j)
-      if (j < ntr) *reinterpret_cast<u32x4_t*>(stage + j * kGTileBytes + st_off) = r.x[j];
-  };
-
   // Fragment of row block f[k] at 16-deep sub-step kk: lane l reads row l % 32
   // of the block, k chunk 2 kk + l / 32 (the 32x32x16 operand layout); sub-step
   // 1's chunk is sub-step 0's with bit 1 set, i.e. its offset XOR 32.
@@ -680,35 +702,46 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
   // registers are reloaded, and sub-step 0 of the next step is read (from
   // the other stage) before this step's second MFMA group.  (Storing at the
   // start of the step measured slower.)
+  // The K loop: three LDS stages; the DMAs of step s + 3 go into step s's
+  // stage right after the barrier of step s (two steps to land), and the
+  // barrier of step s waits for step s + 1's.  Sub-step 1's fragments are
+  // read before sub-step 0's MFMAs, and sub-step 0 of the next step (from
+  // the next stage, after the barrier) before this step's second MFMA
+  // group.  (Register staging two steps ahead -- 16-byte loads and LDS
+  // stores -- measured 10% slower at B = 8, 3-7% at B = 32: a wave's load of
+  // 16 rows x 64 bytes moves at half the rate of a DMA of the same rows.)
   const int nk = ceil_div(d, kGK);
-  Regs R[2];
-  load(0, R[0]);
-  store(lds, R[0]);
-  load(1, R[1]);
-  load(2, R[0]);
+  uint8_t* const ring[3] = {lds, lds + kStage, lds + 2 * kStage};
+  dma(ring[0], 0);
+  dma(ring[1], 1);
+  dma(ring[2], 2);
+  DPC_WAIT_VMCNT(2 * ntr);
   __syncthreads();
   Frags fx, fy;
-  read(lds, 0, fx);
-  auto step = [&](int s, Regs& rn) __attribute__((always_inline)) {
-    const uint8_t* cur = lds + (s & 1) * kStage;
-    uint8_t* nxt = lds + ((s + 1) & 1) * kStage;
+  read(ring[0], 0, fx);
+  auto step = [&](auto P, int s) __attribute__((always_inline)) {
+    constexpr int p = decltype(P)::value;
+    uint8_t* cur = ring[p];
+    const uint8_t* nxt = ring[(p + 1) % 3];
     read(cur, 1, fy);
     mma(fx);
     __builtin_amdgcn_sched_barrier(0);
-    store(nxt, rn);
-    load(s + 3, rn);
-    __builtin_amdgcn_sched_barrier(0);
+    DPC_WAIT_VMCNT(ntr);  // step s + 1 has landed
     __syncthreads();
+    dma(cur, s + 3);
     read(nxt, 0, fx);
     mma(fy);
     __builtin_amdgcn_sched_barrier(0);
   };
   int s = 0;
-  for (; s + 1 < nk; s += 2) {
-    step(s, R[1]);
-    step(s + 1, R[0]);
+  for (; s + 3 <= nk; s += 3) {
+    step(StageIdx<0>(), s);
+    step(StageIdx<1>(), s + 1);
+    step(StageIdx<2>(), s + 2);
   }
-  if (s < nk) step(s, R[1]);
+  if (s < nk) step(StageIdx<0>(), s);
+  if (s + 1 < nk) step(StageIdx<1>(), s + 1);
+  DPC_WAIT_VMCNT(0);
 
   // Meet the set's other workgroup.  Both publish their accumulators (1 KiB
   // per store instruction), wait for their stores to complete, and take an
@@ -855,7 +888,7 @@ gram_split_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
                        int din, int dout, int npairs, int nsets, int nblocks,
                        double* __restrict__ records, int32_t* __restrict__ tickets,
                        float* __restrict__ xbuf) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * 3 * kGTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * 3 * kGTileBytes];
   __shared__ double red[3 * kSplitWaves * kRecStat];
   __shared__ int ticket_lds[2];
   const int l = xcd_logical_block(gridDim.x, nblocks);
