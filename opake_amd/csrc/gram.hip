@@ -511,7 +511,7 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
 //     the rows of blocks t, t + 1 and q: 32 blocks;
 // and each set is computed twice, for A and for G, by two workgroups (items
 // 2 j and 2 j + 1 of the example).  A workgroup stages one operand's rows (16
-// or 24 KiB per 32-deep K step instead of 32, by DMA into three LDS stages)
+// or 24 KiB per 32-deep K step instead of 32, by DMA into four LDS stages)
 // and holds at most 5 blocks per
 // wave, the 8 waves' blocks balanced over the 4 SIMDs (9 or 8 per SIMD), so
 // B (nt / 2)^2 x 2 items of nearly equal cost cover the chip (256 at B = 32,
@@ -521,8 +521,8 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
 // records -- the paired kernel's records, from the same fp32 Gram entries (a
 // block above a diagonal tile's diagonal stands for itself and its mirror,
 // which the MFMA computes to the same bits).  No workgroup waits for
-// another.  (Against the paired kernel at B = 32, T = 512, d = 4096: 10%
-// less time, 29% fewer MFMA cycles; the exchange costs 8-13 us of it.)
+// another.  (Letting only the first publish and the second wait for it
+// measured the same.)
 // ---------------------------------------------------------------------------
 constexpr int kSplitWaves = 8;
 typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
@@ -702,45 +702,49 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
   // registers are reloaded, and sub-step 0 of the next step is read (from
   // the other stage) before this step's second MFMA group.  (Storing at the
   // start of the step measured slower.)
-  // The K loop: three LDS stages; the DMAs of step s + 3 go into step s's
-  // stage right after the barrier of step s (two steps to land), and the
-  // barrier of step s waits for step s + 1's.  Sub-step 1's fragments are
+  // The K loop: four LDS stages; the DMAs of step s + 4 go into step s's
+  // stage right after the barrier of step s (three steps to land; three
+  // stages measured 1-2% slower), and the barrier of step s waits for step
+  // s + 1's.  Sub-step 1's fragments are
   // read before sub-step 0's MFMAs, and sub-step 0 of the next step (from
   // the next stage, after the barrier) before this step's second MFMA
   // group.  (Register staging two steps ahead -- 16-byte loads and LDS
   // stores -- measured 10% slower at B = 8, 3-7% at B = 32: a wave's load of
   // 16 rows x 64 bytes moves at half the rate of a DMA of the same rows.)
   const int nk = ceil_div(d, kGK);
-  uint8_t* const ring[3] = {lds, lds + kStage, lds + 2 * kStage};
+  uint8_t* const ring[4] = {lds, lds + kStage, lds + 2 * kStage, lds + 3 * kStage};
   dma(ring[0], 0);
   dma(ring[1], 1);
   dma(ring[2], 2);
-  DPC_WAIT_VMCNT(2 * ntr);
+  dma(ring[3], 3);
+  DPC_WAIT_VMCNT(3 * ntr);
   __syncthreads();
   Frags fx, fy;
   read(ring[0], 0, fx);
   auto step = [&](auto P, int s) __attribute__((always_inline)) {
     constexpr int p = decltype(P)::value;
     uint8_t* cur = ring[p];
-    const uint8_t* nxt = ring[(p + 1) % 3];
+    const uint8_t* nxt = ring[(p + 1) % 4];
     read(cur, 1, fy);
     mma(fx);
     __builtin_amdgcn_sched_barrier(0);
-    DPC_WAIT_VMCNT(ntr);  // step s + 1 has landed
+    DPC_WAIT_VMCNT(2 * ntr);  // step s + 1 has landed
     __syncthreads();
-    dma(cur, s + 3);
+    dma(cur, s + 4);
     read(nxt, 0, fx);
     mma(fy);
     __builtin_amdgcn_sched_barrier(0);
   };
   int s = 0;
-  for (; s + 3 <= nk; s += 3) {
+  for (; s + 4 <= nk; s += 4) {
     step(StageIdx<0>(), s);
     step(StageIdx<1>(), s + 1);
     step(StageIdx<2>(), s + 2);
+    step(StageIdx<3>(), s + 3);
   }
   if (s < nk) step(StageIdx<0>(), s);
   if (s + 1 < nk) step(StageIdx<1>(), s + 1);
+  if (s + 2 < nk) step(StageIdx<2>(), s + 2);
   DPC_WAIT_VMCNT(0);
 
   // Meet the set's other workgroup.  Both publish their accumulators (1 KiB
@@ -888,7 +892,7 @@ gram_split_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restric
                        int din, int dout, int npairs, int nsets, int nblocks,
                        double* __restrict__ records, int32_t* __restrict__ tickets,
                        float* __restrict__ xbuf) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * 3 * kGTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[4 * 3 * kGTileBytes];
   __shared__ double red[3 * kSplitWaves * kRecStat];
   __shared__ int ticket_lds[2];
   const int l = xcd_logical_block(gridDim.x, nblocks);
