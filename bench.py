@@ -878,13 +878,13 @@ def run_lora(args) -> dict:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "narrow_wide_bf16_kernel (+ narrow_finish_kernel for split tokens; dpc_per_example_grads, 14 "
-                      "launches per step)",
+            "kernel": "narrow_wide_mfma_kernel<16> (dpc_per_example_grads_grouped: the 14 "
+                      "adapter gradients in one launch per step)",
             "achieved": gbs,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": gbs / HBM_PEAK_GBS,
-            "avg_launch_ms": kern_ms / 14,
+            "avg_launch_ms": kern_ms,
             "traffic": None,
         },
         "cpu_baseline": cpu,

@@ -180,6 +180,17 @@ int dpc_add_noise(const void* x, void* y, int64_t rows, int64_t cols, int dtype,
                   int noise_mode, const float* noise, uint64_t seed, uint32_t leaf_id,
                   void* stream);
 
+/* The Philox-stream noise of n leaves of one dtype in as few launches as
+ * possible (one per 32 leaves), for the many small leaves of a step (LoRA
+ * adapters): leaf i gets exactly dpc_add_noise(x[i], y[i], rows[i], cols[i],
+ * dtype, sigma[i], DPC_NOISE_PHILOX, NULL, seed, leaf_ids[i]).  The arrays
+ * are host memory; y[i] may equal x[i] (in place).  Same reference
+ * interface as dpc_add_noise (_gaussian.py:188-204, one call per leaf of
+ * the pytree). */
+int dpc_add_noise_leaves(int n, const void* const* x, void* const* y, const int64_t* rows,
+                         const int64_t* cols, const double* sigma, const uint32_t* leaf_ids,
+                         int dtype, uint64_t seed, void* stream);
+
 /* Known-answer hook: n Philox4x32-10 blocks for counters (c0 + j, c1, c2, c3),
  * key (k0, k1), written as out[4 j + w]. */
 int dpc_philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
@@ -303,6 +314,21 @@ size_t dpc_per_example_grads_workspace_bytes(int B, int T, int din, int dout);
 int dpc_per_example_grads(const void* A, const void* G, int B, int T, int din, int dout,
                           int dtype, void* out, int out_dtype, void* ws, size_t ws_bytes,
                           void* stream);
+
+/* The per-example gradients of n such layers that share B and T (the
+ * adapters of a block, lora.py:687-701 once per adapter) in as few launches
+ * as possible: problem i is dpc_per_example_grads(A[i], G[i], B, T, din[i],
+ * dout[i], dtype, out[i], out_dtype, ...), its result the same up to the
+ * order of the fp32 token sums (bf16 layers whose wide side is a multiple of
+ * 8 and narrow side even share MFMA launches of up to 32 problems; the
+ * others run one by one).  The arrays are host memory.  ws:
+ * dpc_per_example_grads_grouped_workspace_bytes. */
+size_t dpc_per_example_grads_grouped_workspace_bytes(int n, const int* din, const int* dout,
+                                                     int B, int T, int dtype);
+int dpc_per_example_grads_grouped(int n, const void* const* A, const void* const* G,
+                                  void* const* out, const int* din, const int* dout, int B, int T,
+                                  int dtype, int out_dtype, void* ws, size_t ws_bytes,
+                                  void* stream);
 
 /* Row sums: out[b] (+)= sum_j x[b, j] (float64), used to fold per-leaf
  * squared norms into per-example totals in a fixed order. */

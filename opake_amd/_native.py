@@ -42,7 +42,7 @@ _c_u32 = ctypes.c_uint32
 _c_u64 = ctypes.c_uint64
 _c_i64 = ctypes.c_int64
 
-ABI_VERSION = 200  # dpc_version() of the library these signatures describe
+ABI_VERSION = 201  # dpc_version() of the library these signatures describe
 
 # name -> (restype, argtypes)
 SIGNATURES = {
@@ -108,6 +108,18 @@ SIGNATURES = {
         _c_int,
         [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_int,
          _c_void_p, _c_size_t, _c_void_p],
+    ),
+    "dpc_per_example_grads_grouped_workspace_bytes": (
+        _c_size_t, [_c_int, _c_void_p, _c_void_p, _c_int, _c_int, _c_int]),
+    "dpc_per_example_grads_grouped": (
+        _c_int,
+        [_c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+         _c_int, _c_void_p, _c_size_t, _c_void_p],
+    ),
+    "dpc_add_noise_leaves": (
+        _c_int,
+        [_c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_u64,
+         _c_void_p],
     ),
     "dpc_grouped_gram_sqnorms": (
         _c_int,

@@ -344,6 +344,7 @@ def ghost_clip_captured(
 
     B = None
     dense, segmented = [], []
+    direct_jobs = {}
     for c in captures:
         g = leaf_group[f"{c.name}.weight"]
         if c.has_bias and leaf_group[f"{c.name}.bias"] != g:
@@ -366,11 +367,10 @@ def ghost_clip_captured(
                     f"layer {c.name!r}: the direct method needs din or dout <= {ops.NARROW_MAX}")
             if direct_ok and (c.norm_method == "direct" or (
                     c.norm_method == "auto" and _direct_is_cheaper(T_, din_, dout_))):
-                # Materialised per-example gradients, clipped as leaves.
+                # Materialised per-example gradients, clipped as leaves (formed
+                # below, the layers of one dtype and shape class together).
                 pdt = c.param_dtype or A3.dtype
-                ev = _event_pair(gemm_events)
-                direct[f"{c.name}.weight"] = ops.per_example_grads(A3, G3, out_dtype=pdt)
-                _close_pair(ev)
+                direct_jobs.setdefault((A3.dtype, pdt, T_), []).append((c.name, A3, G3))
                 if c.has_bias:
                     direct[f"{c.name}.bias"] = G3.float().sum(dim=1).to(pdt)
                 continue
@@ -388,6 +388,13 @@ def ghost_clip_captured(
                     f"layer {c.name!r}: the row segments must give B row counts that add up "
                     "to the layer's input rows")
             segmented.append(_Layer(c, g, A2, G2))
+    for (_, pdt, _), jobs in direct_jobs.items():
+        ev = _event_pair(gemm_events)
+        grads = ops.per_example_grads_grouped([A3 for _, A3, _ in jobs], [G3 for _, _, G3 in jobs],
+                                              out_dtype=pdt)
+        _close_pair(ev)
+        for (name, _, _), g in zip(jobs, grads):
+            direct[f"{name}.weight"] = g
     direct_names = sorted(direct)
     if direct_names:
         nb = direct[direct_names[0]].shape[0]
@@ -564,6 +571,7 @@ def ghost_clip_captured(
         out_dtypes = {dt: dtype for dt in direct_batch.dtypes} if dtype is not None else None
         reduced, _ = direct_batch.apply(scale_rows, [leaf_group[n] for n in direct_names],
                                         out_dtypes)
+        philox = {}
         for n, x in zip(direct_names, reduced):
             if normalize_by != 1.0:
                 x = x / normalize_by
@@ -572,9 +580,14 @@ def ghost_clip_captured(
                 if gen is not None:
                     x = ops.add_noise(x, s_n, mode=nat.NOISE_INJECTED, noise=to_dev(draws[n]))
                 else:
-                    x = ops.add_noise(x, s_n, mode=nat.NOISE_PHILOX, seed=step_key.seed,
-                                      leaf_id=leaf_index[n])
+                    # Added below, in place (x is this step's own buffer), the
+                    # leaves of one dtype in one launch.
+                    philox.setdefault(x.dtype, []).append((n, x, s_n))
             tree[n] = x
+        for items in philox.values():
+            ops.add_noise_leaves([x for _, x, _ in items], [s for _, _, s in items],
+                                 seed=step_key.seed, leaf_ids=[leaf_index[n] for n, _, _ in items],
+                                 inplace=True)
     tree = {k: tree[k] for k in leaf_names}
     if noise_fn is None:
         result = clipped(tree, max_norm=max_norm)

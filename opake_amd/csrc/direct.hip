@@ -25,7 +25,11 @@
 //
 // Token chunks write fp32 partial sums, added in chunk order by a second
 // kernel that also lays out (and rounds) the result.
+#include <algorithm>
+#include <vector>
+
 #include "common.h"
+#include "lds_stage.h"
 
 namespace {
 
@@ -373,6 +377,324 @@ narrow_wide_bf16_kernel(const uint16_t* __restrict__ wide, const uint16_t* __res
   }
 }
 
+// ---------------------------------------------------------------------------
+// MFMA kernel (bf16, nw % 8 == 0, ns even): out[s, w] = sum_t N[t, s] W[t, w]
+// is a GEMM of M = ns (<= 32), N = nw, K = the chunk's tokens, run on the
+// 16x16x32 bf16 MFMA with fp32 accumulators.  A workgroup of 8 waves owns 256
+// wide columns of one example; each 64-token step stages the wide tile (64
+// rows of 512 bytes in the swizzled layout of tile_off, by 16-byte DMA) and
+// the narrow rows (64 rows of NS bf16, by 4-byte DMA; columns past ns and
+// rows past T read zeros) into one of four LDS stages, three steps ahead.
+// Wave w owns wide columns 32 w .. 32 w + 31: per step it reads 2 x 2 wide
+// and 2 x NS / 16 narrow fragments through ds_read_b64_tr_b16 and runs
+// 4 NS / 16 MFMAs.  Each product of two bf16 is exact in fp32, as in the
+// other kernels; only the summation order differs.
+// ---------------------------------------------------------------------------
+constexpr int kNmWaves = 8;
+constexpr int kNmThreads = kNmWaves * 64;
+constexpr int kNmCols = 256;                                   // wide columns per workgroup
+constexpr int kNmK = 64;                                       // tokens per step
+constexpr int kNmStages = 4;
+constexpr int kNmWideBytes = kNmK * kTileRowBytes;             // 32 KiB
+constexpr int kNmWideDma = kNmWideBytes / (kNmWaves * 1024);   // 16-byte DMAs per lane and step
+
+// One problem of a grouped launch: out[b, s, w] (narrow side G) or out[b, w,
+// s] (narrow side A) over the tokens [split * chunk, min(T, (split + 1) *
+// chunk)), written to `out` when splits == 1, else as the fp32 partial
+// partial[split][b][s][w].  Workgroups wg_start .. wg_start + col_tiles * B *
+// splits - 1 of the launch take it, column tile fastest.  Requires chunk % 64
+// == 0, nw % 8 == 0, ns even, ns <= NS and (T + 64) * nw * 2 < kNwOutOfRange.
+constexpr int kNmMaxProblems = 32;
+struct NmProblem {
+  const uint16_t* wide;
+  const uint16_t* narrow;
+  void* out;
+  float* partial;
+  int nw, ns, narrow_is_g;
+  int col_tiles, splits, chunk;
+  int wg_start;
+};
+// Passed by value (kernel arguments): no table upload per launch.
+struct NmTable {
+  NmProblem p[kNmMaxProblems];
+  int n, B, T, out_bf16;
+};
+
+template <int NS>
+__global__ void __launch_bounds__(kNmThreads, 1)
+narrow_wide_mfma_kernel(const NmTable tab) {
+  constexpr int kRowN = NS * 2;                                 // bytes of a narrow row in LDS
+  constexpr int kNarrowBytes = kNmK * kRowN;                    // 2 or 4 KiB
+  constexpr int kNarrowDma = kNarrowBytes / (kNmWaves * 256);   // 4-byte DMAs per lane and step
+  constexpr int kDma = kNmWideDma + kNarrowDma;
+  constexpr int kStage = kNmWideBytes + kNarrowBytes;
+  constexpr int kMB = NS / 16;                                  // 16-row blocks of narrow columns
+  static_assert(kNarrowDma * kNmWaves * 256 == kNarrowBytes, "narrow tile split");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kNmStages * kStage];
+  const int lin = blockIdx.x;
+  int pi = 0;
+  for (int i = 1; i < tab.n; ++i)
+    if (lin >= tab.p[i].wg_start) pi = i;
+  const NmProblem& P = tab.p[pi];
+  const int B = tab.B, T = tab.T;
+  const int nw = P.nw, ns = P.ns, chunk = P.chunk, splits = P.splits;
+  const int local = lin - P.wg_start;
+  const int ct = local % P.col_tiles, rest = local / P.col_tiles;
+  const int b = rest % B, split = rest / B;
+  const uint16_t* wide = P.wide;
+  const uint16_t* narrow = P.narrow;
+  const int col0 = ct * kNmCols;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t0 = split * chunk;
+  const int n = max(min(T, t0 + chunk) - t0, 0);
+  const int nsteps = (n + kNmK - 1) / kNmK;
+
+  // Example b's operands; a transfer at or past the example's end (rows >= T)
+  // reads zeros.
+  const u32x4_t wrsrc = rsrc_words(wide + (size_t)b * T * nw, (uint32_t)T * nw * 2);
+  const u32x4_t nrsrc = rsrc_words(narrow + (size_t)b * T * ns, (uint32_t)T * ns * 2);
+  // Wide: wave w's transfer j fills the 1 KiB of tile rows 2 w + 16 j and the
+  // next, lane i the 16 bytes at i * 16 -- row 2 w + 16 j + i / 32, physical
+  // slot i % 32, which holds the 8 columns from tile_slot_col(row, i % 32).
+  // A chunk past nw reads the row's last 8 columns instead: they feed only
+  // output columns that are never stored.
+  const int drow = 2 * w + (lane >> 5);
+  const int dcol = min(col0 + tile_slot_col(drow, lane & 31), nw - 8);
+  const uint32_t wvoff = (uint32_t)((t0 + drow) * nw + dcol) * 2u;
+  const uint32_t wstep = (uint32_t)kNmK * nw * 2u, wrow16 = 16u * nw * 2u;
+  // Narrow: wave w's transfer i fills the 256 bytes at (w * kNarrowDma + i) *
+  // 256 of the narrow tile, lane l the dword at + 4 l: row r, physical dword
+  // p.  With 64-byte rows (NS = 32) the two 32-byte halves are swapped in rows
+  // with bit 2 set, so that a fragment read is free of bank conflicts.
+  uint32_t nvoff[kNarrowDma];
+#pragma unroll
+  for (int i = 0; i < kNarrowDma; ++i) {
+    const int byte = (w * kNarrowDma + i) * 256 + 4 * lane;
+    const int r = byte / kRowN, p = (byte % kRowN) / 4;
+    const int d = (NS == 32) ? p ^ (((r >> 2) & 1) << 3) : p;
+    nvoff[i] = (2 * d < ns) ? (uint32_t)((t0 + r) * ns + 2 * d) * 2u : (uint32_t)kNwOutOfRange;
+  }
+  const uint32_t nstep = (uint32_t)kNmK * ns * 2u;
+  const uint32_t lds0 = lds_addr(lds);
+  auto dma_step = [&](int stage, int step) __attribute__((always_inline)) {
+    const uint32_t base = lds0 + stage * kStage;
+    const uint32_t wv = wvoff + (uint32_t)step * wstep;
+#pragma unroll
+    for (int j = 0; j < kNmWideDma; ++j)
+      dma16(wrsrc, base + (w + kNmWaves * j) * 1024, (int)(wv + j * wrow16), 0);
+#pragma unroll
+    for (int i = 0; i < kNarrowDma; ++i) {
+      const uint32_t v = nvoff[i] + (uint32_t)step * nstep;
+      dma4(nrsrc, base + kNmWideBytes + (w * kNarrowDma + i) * 256, (int)v, 0);
+    }
+  };
+
+  // Fragment offsets (sub-step 0, half 0): wide column blocks 32 w and
+  // 32 w + 16 (the latter is the former XOR 32, tile_off), narrow row blocks
+  // 16 mb; half 1 is 16 rows further, sub-step 1 32 rows.
+  const int boff = frag16_off(32 * w, 0, lane);
+  int aoff[kMB];
+  {
+    const int q = lane >> 4, L = lane & 15;
+    const int k = 4 * q + (L >> 2);
+#pragma unroll
+    for (int mb = 0; mb < kMB; ++mb) {
+      const int dw = 8 * mb + 2 * (L & 3);
+      aoff[mb] = kNmWideBytes + k * kRowN + 4 * ((NS == 32) ? dw ^ ((q & 1) << 3) : dw);
+    }
+  }
+  f32x4_t acc[kMB][2];
+#pragma unroll
+  for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int stage) __attribute__((always_inline)) {
+    const uint8_t* st = lds + stage * kStage;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      bf16x8_t bf[2], af[kMB];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const int o = (boff ^ (32 * nb)) + kk * 32 * kTileRowBytes;
+        bf[nb] = join_frag(read_tr(st, o), read_tr(st, o + 16 * kTileRowBytes));
+      }
+#pragma unroll
+      for (int mb = 0; mb < kMB; ++mb) {
+        const int o = aoff[mb] + kk * 32 * kRowN;
+        af[mb] = join_frag(read_tr(st, o), read_tr(st, o + 16 * kRowN));
+      }
+#pragma unroll
+      for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mb], bf[nb], acc[mb][nb], 0, 0, 0);
+    }
+  };
+
+  // Step s waits for its own transfers (those of the next two steps may be in
+  // flight); after the barrier every wave is done with stage (s + 3) % 4,
+  // which takes the transfers of step s + 3.
+#pragma unroll
+  for (int p = 0; p < kNmStages - 1; ++p)
+    if (p < nsteps) dma_step(p, p);
+  auto iteration = [&](int s, int stage) __attribute__((always_inline)) {
+    const int ahead = nsteps - 1 - s;
+    if (ahead >= 2) {
+      DPC_WAIT_VMCNT(2 * kDma);
+    } else if (ahead == 1) {
+      DPC_WAIT_VMCNT(kDma);
+    } else {
+      DPC_WAIT_VMCNT(0);
+    }
+    __syncthreads();
+    if (s + kNmStages - 1 < nsteps) dma_step((stage + kNmStages - 1) % kNmStages, s + kNmStages - 1);
+    compute(stage);
+  };
+  for (int s = 0; s < nsteps; s += kNmStages) {
+    iteration(s, 0);
+    if (s + 1 < nsteps) iteration(s + 1, 1);
+    if (s + 2 < nsteps) iteration(s + 2, 2);
+    if (s + 3 < nsteps) iteration(s + 3, 3);
+  }
+
+  // Lane l holds out[16 mb + 4 (l / 16) + e][32 w + 16 nb + l % 16].
+#pragma unroll
+  for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int col = col0 + 32 * w + 16 * nb + (lane & 15);
+      if (col >= nw) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int s = 16 * mb + 4 * (lane >> 4) + e;
+        if (s >= ns) continue;
+        const float v = acc[mb][nb][e];
+        if (splits > 1) {
+          P.partial[(((size_t)split * B + b) * ns + s) * nw + col] = v;
+        } else {
+          const size_t o =
+              P.narrow_is_g ? ((size_t)b * ns + s) * nw + col : ((size_t)b * nw + col) * ns + s;
+          if (tab.out_bf16) {
+            reinterpret_cast<uint16_t*>(P.out)[o] = f32_to_bf16_bits(v);
+          } else {
+            reinterpret_cast<float*>(P.out)[o] = v;
+          }
+        }
+      }
+    }
+}
+
+bool narrow_mfma_ok(int T, int nw, int ns) {
+  return nw % 8 == 0 && ns % 2 == 0 && ns > 0 && ns <= kMaxNarrow &&
+         (long long)(T + kNmK) * nw * 2 < kNwOutOfRange;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// One problem of dpc_per_example_grads(_grouped): out [B, dout, din].
+struct NmDesc {
+  const void* A;
+  const void* G;
+  void* out;
+  int din, dout;
+};
+
+// The table of one MFMA launch over problems d[idx[0 .. m)) (m <=
+// kNmMaxProblems, all with narrow widths in one NS class): token chunks of a
+// multiple of 64 tokens, as many splits of every problem as it takes for the
+// launch to have a workgroup for every CU; a split problem's partials at ws +
+// its offset (ws may be null to size them).  Returns the launch's workgroups;
+// *ws_bytes receives the partials' bytes.
+int nm_table(NmTable& tab, const NmDesc* d, const int* idx, int m, int B, int T, int out_bf16,
+             char* ws, size_t* ws_bytes) {
+  long long base = 0;
+  for (int i = 0; i < m; ++i) {
+    const NmDesc& q = d[idx[i]];
+    base += (long long)ceil_div(q.dout <= q.din ? q.din : q.dout, kNmCols) * B;
+  }
+  const int want = (int)std::max<long long>(1, (256 + base - 1) / base);
+  const int chunk = ceil_div(ceil_div(T, want), kNmK) * kNmK;
+  const int splits = ceil_div(T, chunk);
+  size_t off = 0;
+  long long wg = 0;
+  for (int i = 0; i < m; ++i) {
+    const NmDesc& q = d[idx[i]];
+    NmProblem& P = tab.p[i];
+    P.narrow_is_g = q.dout <= q.din;
+    P.ns = P.narrow_is_g ? q.dout : q.din;
+    P.nw = P.narrow_is_g ? q.din : q.dout;
+    P.wide = (const uint16_t*)(P.narrow_is_g ? q.A : q.G);
+    P.narrow = (const uint16_t*)(P.narrow_is_g ? q.G : q.A);
+    P.out = q.out;
+    P.col_tiles = ceil_div(P.nw, kNmCols);
+    P.splits = splits;
+    P.chunk = chunk;
+    P.wg_start = (int)wg;
+    wg += (long long)P.col_tiles * B * splits;
+    P.partial = nullptr;
+    if (splits > 1) {
+      P.partial = ws ? (float*)(ws + off) : nullptr;
+      off = align256(off + (size_t)splits * B * P.ns * P.nw * sizeof(float));
+    }
+  }
+  tab.n = m;
+  tab.B = B;
+  tab.T = T;
+  tab.out_bf16 = out_bf16;
+  *ws_bytes = off;
+  return wg > 0x7fffffffLL ? -1 : (int)wg;
+}
+
+// The MFMA launches of the eligible problems d[idx[0 .. m)): one per NS
+// class and run of up to kNmMaxProblems problems, each followed by the
+// finish kernels of its split problems (so launches reuse the workspace).
+// With launch false only sizes the workspace (the largest launch's partials).
+int nm_run(const NmDesc* d, const int* idx, int m, int B, int T, int out_bf16, void* ws,
+           size_t ws_bytes, hipStream_t s, bool launch, size_t* ws_need) {
+  size_t need = 0;
+  for (int cls = 0; cls < 2; ++cls) {
+    int sel[kNmMaxProblems];
+    int k = 0;
+    for (int i = 0; i <= m; ++i) {
+      if (i < m) {
+        const NmDesc& q = d[idx[i]];
+        const int ns = q.dout <= q.din ? q.dout : q.din;
+        if ((ns > 16) != (cls == 1)) continue;
+        sel[k++] = idx[i];
+      }
+      if (k == 0 || (k < kNmMaxProblems && i < m)) continue;
+      NmTable tab;
+      size_t part = 0;
+      const int wgs = nm_table(tab, d, sel, k, B, T, out_bf16, (char*)ws, &part);
+      if (wgs < 0) return DPC_ENOTSUP;
+      need = std::max(need, part);
+      if (launch && wgs > 0) {
+        if (part > ws_bytes || (part > 0 && !ws)) return DPC_ENOSPC;
+        if (cls == 0) {
+          hipLaunchKernelGGL(narrow_wide_mfma_kernel<16>, dim3(wgs), dim3(kNmThreads), 0, s, tab);
+        } else {
+          hipLaunchKernelGGL(narrow_wide_mfma_kernel<32>, dim3(wgs), dim3(kNmThreads), 0, s, tab);
+        }
+        DPC_HIP_CHECK(hipGetLastError());
+        for (int j = 0; j < k; ++j) {
+          const NmProblem& P = tab.p[j];
+          if (P.splits <= 1) continue;
+          const size_t total = (size_t)B * P.ns * P.nw;
+          hipLaunchKernelGGL(narrow_finish_kernel,
+                             dim3((unsigned)((total + kDirThreads - 1) / kDirThreads)),
+                             dim3(kDirThreads), 0, s, (const float*)P.partial, P.splits, B, P.nw,
+                             P.ns, P.narrow_is_g, out_bf16, P.out);
+          DPC_HIP_CHECK(hipGetLastError());
+        }
+      }
+      k = 0;
+    }
+  }
+  *ws_need = need;
+  return DPC_OK;
+}
+
 bool narrow_wide_ok(int T, int nw, int ns) {
   return nw % 4 == 0 && ns <= kMaxNarrow && (long long)T * nw * 2 < kNwOutOfRange;
 }
@@ -402,12 +724,19 @@ extern "C" size_t dpc_per_example_grads_workspace_bytes(int B, int T, int din, i
   if (B <= 0 || T <= 0 || din <= 0 || dout <= 0) return 0;
   const int ns = din < dout ? din : dout, nw = din < dout ? dout : din;
   if (ns > kMaxNarrow) return 0;
-  // The larger of the two paths' needs (the query does not know the dtype).
+  // The largest of the paths' needs (the query does not know the dtype).
   size_t bytes = (size_t)narrow_splits(B, T, nw) * B * ns * nw * sizeof(float);
   if (narrow_wide_ok(T, nw, ns)) {
     int chunk;
     const int splits = narrow_wide_splits(B, T, nw, ns, &chunk);
     if (splits > 1) bytes = max(bytes, (size_t)splits * B * ns * nw * sizeof(float));
+  }
+  if (narrow_mfma_ok(T, nw, ns)) {
+    const NmDesc d{nullptr, nullptr, nullptr, din, dout};
+    const int idx = 0;
+    size_t need = 0;
+    if (nm_run(&d, &idx, 1, B, T, 0, nullptr, 0, nullptr, false, &need) == DPC_OK)
+      bytes = max(bytes, need);
   }
   return bytes;
 }
@@ -427,6 +756,12 @@ extern "C" int dpc_per_example_grads(const void* A, const void* G, int B, int T,
   hipStream_t s = (hipStream_t)stream;
   const void* wide = narrow_is_g ? A : G;
   const void* narrow = narrow_is_g ? G : A;
+  if (dtype == DPC_BF16 && narrow_mfma_ok(T, nw, ns)) {
+    const NmDesc d{A, G, out, din, dout};
+    const int idx = 0;
+    size_t need = 0;
+    return nm_run(&d, &idx, 1, B, T, (int)(out_dtype == DPC_BF16), ws, ws_bytes, s, true, &need);
+  }
   if (dtype == DPC_BF16 && narrow_wide_ok(T, nw, ns)) {
     int chunk;
     const int splits = narrow_wide_splits(B, T, nw, ns, &chunk);
@@ -486,5 +821,77 @@ extern "C" int dpc_per_example_grads(const void* A, const void* G, int B, int T,
                      dim3(kDirThreads), 0, s, (const float*)partial, splits, B, nw, ns,
                      (int)narrow_is_g, (int)(out_dtype == DPC_BF16), out);
   DPC_HIP_CHECK(hipGetLastError());
+  return DPC_OK;
+}
+
+// Problems for the MFMA kernel (bf16 operands, eligible widths) and the others.
+static int grouped_split(int n, const int* din, const int* dout, int T, int dtype, int* mfma,
+                         int* other, int* n_mfma, int* n_other) {
+  *n_mfma = *n_other = 0;
+  for (int i = 0; i < n; ++i) {
+    if (din[i] <= 0 || dout[i] <= 0) return DPC_EINVAL;
+    const int ns = std::min(din[i], dout[i]), nw = std::max(din[i], dout[i]);
+    if (ns > kMaxNarrow) return DPC_ENOTSUP;
+    if (dtype == DPC_BF16 && narrow_mfma_ok(T, nw, ns)) {
+      mfma[(*n_mfma)++] = i;
+    } else {
+      other[(*n_other)++] = i;
+    }
+  }
+  return DPC_OK;
+}
+
+extern "C" size_t dpc_per_example_grads_grouped_workspace_bytes(int n, const int* din,
+                                                                const int* dout, int B, int T,
+                                                                int dtype) {
+  if (n <= 0 || B <= 0 || T <= 0 || !din || !dout) return 0;
+  std::vector<int> mfma(n), other(n);
+  int nm = 0, no = 0;
+  if (grouped_split(n, din, dout, T, dtype, mfma.data(), other.data(), &nm, &no) != DPC_OK) return 0;
+  size_t bytes = 0;
+  for (int i = 0; i < no; ++i)
+    bytes = std::max(bytes, dpc_per_example_grads_workspace_bytes(B, T, din[other[i]], dout[other[i]]));
+  if (nm > 0) {
+    std::vector<NmDesc> d(n);
+    for (int i = 0; i < n; ++i) d[i] = NmDesc{nullptr, nullptr, nullptr, din[i], dout[i]};
+    size_t need = 0;
+    if (nm_run(d.data(), mfma.data(), nm, B, T, 0, nullptr, 0, nullptr, false, &need) == DPC_OK)
+      bytes = std::max(bytes, need);
+  }
+  return bytes;
+}
+
+extern "C" int dpc_per_example_grads_grouped(int n, const void* const* A, const void* const* G,
+                                             void* const* out, const int* din, const int* dout,
+                                             int B, int T, int dtype, int out_dtype, void* ws,
+                                             size_t ws_bytes, void* stream) {
+  if (n < 0 || B < 0 || T <= 0) return DPC_EINVAL;
+  if (dtype != DPC_F32 && dtype != DPC_BF16) return DPC_EINVAL;
+  if (out_dtype != DPC_F32 && out_dtype != DPC_BF16) return DPC_EINVAL;
+  if (n == 0 || B == 0) return DPC_OK;
+  if (!A || !G || !out || !din || !dout) return DPC_EINVAL;
+  for (int i = 0; i < n; ++i)
+    if (!A[i] || !G[i] || !out[i]) return DPC_EINVAL;
+  if (B > 65535) return DPC_ENOTSUP;
+  std::vector<int> mfma(n), other(n);
+  int nm = 0, no = 0;
+  const int rc = grouped_split(n, din, dout, T, dtype, mfma.data(), other.data(), &nm, &no);
+  if (rc != DPC_OK) return rc;
+  if (!ws || ws_bytes < dpc_per_example_grads_grouped_workspace_bytes(n, din, dout, B, T, dtype))
+    return DPC_ENOSPC;
+  if (nm > 0) {
+    std::vector<NmDesc> d(n);
+    for (int i = 0; i < n; ++i) d[i] = NmDesc{A[i], G[i], out[i], din[i], dout[i]};
+    size_t need = 0;
+    const int r = nm_run(d.data(), mfma.data(), nm, B, T, (int)(out_dtype == DPC_BF16), ws,
+                         ws_bytes, (hipStream_t)stream, true, &need);
+    if (r != DPC_OK) return r;
+  }
+  for (int i = 0; i < no; ++i) {
+    const int j = other[i];
+    const int r = dpc_per_example_grads(A[j], G[j], B, T, din[j], dout[j], dtype, out[j],
+                                        out_dtype, ws, ws_bytes, stream);
+    if (r != DPC_OK) return r;
+  }
   return DPC_OK;
 }

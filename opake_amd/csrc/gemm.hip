@@ -39,6 +39,7 @@
 //   * workgroup ids are remapped so that each of the 8 XCDs owns a compact
 //     block of output tiles and re-reads operand tiles from its own L2.
 #include "common.h"
+#include "lds_stage.h"
 #include "plan.h"
 
 namespace {
@@ -47,29 +48,10 @@ constexpr int kBM = 256, kBN = 256, kBK = 64, kThreads = 256;
 constexpr int kFastWaves = 8;
 
 // LDS layout of one operand tile for a 64-deep K step: 64 rows (k) of 256
-// bf16 (512 bytes), the row's eight 64-byte blocks permuted by XOR with
-// (k & 7), and the two 32-byte halves of every block swapped in rows with
-// bit 2 of k set.  The 64 four-byte banks span 256 bytes, so blocks b and
-// b ^ 4 of a row share banks.  A 16-lane group of a 16-byte store covers 4
-// consecutive blocks of one row, and a 32-lane half of a fragment read covers
-// one 32-byte half block in 8 rows (k & 7 = 0 .. 7, the rows with bit 2 set
-// in the other half): both land on 64 distinct banks.
-constexpr int kRowBytes = 512;
+// bf16 in the swizzled layout of tile_off.
+constexpr int kRowBytes = kTileRowBytes;
 constexpr int kOperandBytes = kBK * kRowBytes;   // 32 KiB
 constexpr int kStageBytes = 2 * kOperandBytes;   // G tile + A tile
-
-// Byte offset of bf16 element (k, col) (col < 256; 16-byte chunks of 8
-// columns stay contiguous).
-__device__ __forceinline__ int tile_off(int k, int col) {
-  return k * kRowBytes +
-         ((((col >> 5) ^ (k & 7)) << 6) | (((col & 31) << 1) ^ (((k >> 2) & 1) << 5)));
-}
-
-// Logical first column of the 16-byte chunk at physical 16-byte slot `slot`
-// (0..31) of row k: the inverse of tile_off.
-__device__ __forceinline__ int tile_slot_col(int k, int slot) {
-  return (((slot >> 2) ^ (k & 7)) << 5) + (((slot & 3) ^ (((k >> 2) & 1) << 1)) << 3);
-}
 
 
 struct Epilogue {
@@ -170,8 +152,6 @@ constexpr int kOutOfRange = 0x7ff00000;
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef short i16x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 
 // A positive finite scale s = m 2^e with m in [1, 2): the mantissa m and the
 // power of two 2^e (both exact; 2^e is subnormal below 2^-126).
@@ -198,16 +178,6 @@ __device__ __forceinline__ u32x4_t scale_chunk(u32x4_t x, float s) {
   return o;
 }
 
-// Transposing read of 4 k-consecutive bf16 per lane (see the fragment
-// addressing in the kernel).
-__device__ __forceinline__ i16x4_t read_tr(const uint8_t* lds_base, int off) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_i16x4_t*)((__attribute__((address_space(3))) uint8_t*)lds_base + off));
-}
-
-__device__ __forceinline__ bf16x8_t join_frag(i16x4_t lo, i16x4_t hi) {
-  return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-}
 
 // Linear workgroup id -> (tile_m, tile_n) in GROUP_M order, so a group of
 // tile rows shares the activation tiles.
@@ -265,25 +235,6 @@ struct FastArgs {
   float* partial;
 };
 
-// Per-lane LDS offset of the transposing fragment read (ds_read_b64_tr_b16)
-// for a 16 x 32 fragment of the 16x16x32 MFMA at tile column c0, K sub-step
-// 0, half h (k-slots 4h..4h+3 of the lane's 8).  The MFMA operand lane l
-// holds k-slots 8 (l / 16) .. + 7 of row (column) l % 16.  The k-slots are a
-// permutation of the sub-step's 32 rows, the same for both operands, so the
-// MFMA still sums over all of them: slot 8 q + 4 h + e (q = l / 16, e < 4)
-// is row 16 h + 4 q + e.  Lane L of group q reads the 8 bytes at k = 16 h + 4
-// q + (L >> 2), col = c0 + 4 (L & 3), and after the transpose holds 4
-// consecutive rows of col c0 + L.  With this order the two 16-lane groups of
-// a 32-lane half read rows 4 q' .. 4 q' + 3 and 4 q' + 4 .. 4 q' + 7: 8
-// distinct (k & 7), the second four with swapped block halves, which is what
-// keeps the read on 64 distinct banks (tile_off).  Sub-step kk adds kk * 32
-// rows.
-__device__ __forceinline__ int frag16_off(int c0, int h, int lane) {
-  const int q = lane >> 4, L = lane & 15;
-  return tile_off(16 * h + 4 * q + (L >> 2), c0 + 4 * (L & 3));
-}
-
-
 // LDS of the fast kernel: each stage's G tile and A tile in an array of its
 // own (the first G array, after the K loop, also holds a 32-row slice of the
 // output tile).  Operands filled by DMA (buffer_load ... lds) sit in distinct
@@ -295,7 +246,6 @@ constexpr int kG0Bytes = (kOperandBytes > kEpiPassRows * kEpiLd * 4) ? kOperandB
                                                                       : kEpiPassRows * kEpiLd * 4;
 
 
-typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 
 // The body of the fast kernel for one 256 x 256 output tile: kWaves = 8
 // waves (2 per SIMD) of 128 x 64, each made of 8 x 4 blocks of 16 x 16

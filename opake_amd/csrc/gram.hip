@@ -28,6 +28,7 @@
 #include <mutex>
 
 #include "common.h"
+#include "lds_stage.h"
 
 // Workspace of dpc_gram_sqnorms_noalloc: one copy per device, resolved to a
 // device address once per device (hipGetSymbolAddress) and used through that
@@ -525,32 +526,6 @@ gram_mfma_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
 // measured the same.)
 // ---------------------------------------------------------------------------
 constexpr int kSplitWaves = 8;
-typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
-
-// A buffer resource as four scalar words (base, stride 0, size in bytes,
-// flags), the layout __builtin_amdgcn_make_buffer_rsrc builds, for inline
-// assembly.
-__device__ __forceinline__ u32x4_t rsrc_words(const void* base, uint32_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  return u32x4_t{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};
-}
-
-// buffer_load_dwordx4 ... lds: lane i's 16 bytes at buffer offset voff + soff
-// go to LDS address lds + 16 i.  Inline assembly, so that the compiler does
-// not see an LDS write: it would otherwise make the fragment reads of the
-// other stages wait for every transfer in flight.  The caller orders the
-// transfers with explicit memory-counter waits and barriers.
-__device__ __forceinline__ void dma16(u32x4_t rsrc, uint32_t lds, int voff, int soff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
-               : "m0");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
-  return (uint32_t)reinterpret_cast<uintptr_t>((const lds_u8_t*)p);
-}
-
 template <int P>
 struct StageIdx {
   static constexpr int value = P;

@@ -124,6 +124,68 @@ add_noise_pairs_kernel(const void* __restrict__ x, void* __restrict__ y, int64_t
   }
 }
 
+// Philox noise on up to kLeafMax leaves in one launch, by value (no table
+// upload): leaf i takes workgroups block_start[i] .. block_start[i + 1] - 1,
+// one (row pair, column) per thread as in add_noise_kernel (the same Philox
+// blocks, so each leaf gets exactly dpc_add_noise's values); a leaf with sigma
+// 0 is copied.  y may equal x (each element is read, then written, by one
+// thread).
+constexpr int kLeafMax = 32;
+struct NoiseLeaf {
+  const void* x;
+  void* y;
+  int64_t rows, cols;
+  float sigma;
+  uint32_t leaf;
+  uint32_t block_start;
+};
+struct NoiseLeafTable {
+  NoiseLeaf l[kLeafMax];
+  int n;
+  uint64_t seed;
+};
+
+template <bool kBf16>
+__global__ void __launch_bounds__(kNoiseThreads) add_noise_leaves_kernel(const NoiseLeafTable tab) {
+  const uint32_t blk = blockIdx.x;
+  int li = 0;
+  for (int i = 1; i < tab.n; ++i)
+    if (blk >= tab.l[i].block_start) li = i;
+  const NoiseLeaf& L = tab.l[li];
+  const int64_t rows = L.rows, cols = L.cols;
+  const int64_t work = ((rows + 1) >> 1) * cols;
+  const int64_t t = (int64_t)(blk - L.block_start) * kNoiseThreads + threadIdx.x;
+  if (t >= work) return;
+  int64_t pr, c;
+  if (work <= 0xffffffffLL) {
+    const uint32_t q = (uint32_t)t / (uint32_t)cols;
+    pr = q;
+    c = (uint32_t)t - q * (uint32_t)cols;
+  } else {
+    pr = t / cols;
+    c = t - pr * cols;
+  }
+  float z0 = 0.0f, z1 = 0.0f;
+  if (L.sigma != 0.0f) philox_normal_pair(tab.seed, L.leaf, (uint64_t)t, &z0, &z1);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t r = 2 * pr + h;
+    if (r >= rows) break;
+    const int64_t idx = r * cols + c;
+    const float z = h ? z1 : z0;
+    if (kBf16) {
+      const uint16_t xv = reinterpret_cast<const uint16_t*>(L.x)[idx];
+      reinterpret_cast<uint16_t*>(L.y)[idx] =
+          L.sigma != 0.0f ? f32_to_bf16_bits(add_scaled<true>(bf16_bits_to_f32(xv), L.sigma, z))
+                          : xv;
+    } else {
+      const float xv = reinterpret_cast<const float*>(L.x)[idx];
+      reinterpret_cast<float*>(L.y)[idx] =
+          L.sigma != 0.0f ? add_scaled<false>(xv, L.sigma, z) : xv;
+    }
+  }
+}
+
 __global__ void philox_kat_kernel(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
                                   uint32_t k1, int n, uint32_t* __restrict__ out) {
   const int j = blockIdx.x * blockDim.x + threadIdx.x;
@@ -203,5 +265,60 @@ extern "C" int dpc_philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t
   hipLaunchKernelGGL(philox_kat_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, (hipStream_t)stream,
                      c0, c1, c2, c3, k0, k1, n, out);
   DPC_HIP_CHECK(hipGetLastError());
+  return DPC_OK;
+}
+
+extern "C" int dpc_add_noise_leaves(int n, const void* const* x, void* const* y,
+                                    const int64_t* rows, const int64_t* cols, const double* sigma,
+                                    const uint32_t* leaf_ids, int dtype, uint64_t seed,
+                                    void* stream) {
+  if (n < 0) return DPC_EINVAL;
+  if (dtype != DPC_F32 && dtype != DPC_BF16) return DPC_EINVAL;
+  if (n == 0) return DPC_OK;
+  if (!x || !y || !rows || !cols || !sigma || !leaf_ids) return DPC_EINVAL;
+  for (int i = 0; i < n; ++i) {
+    if (rows[i] < 0 || cols[i] < 0 || !(sigma[i] >= 0.0)) return DPC_EINVAL;
+    if (rows[i] > 0 && cols[i] > 0 && (!x[i] || !y[i])) return DPC_EINVAL;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  NoiseLeafTable tab;
+  tab.seed = seed;
+  int k = 0;
+  uint64_t blocks = 0;
+  for (int i = 0; i <= n; ++i) {
+    if (i < n && rows[i] > 0 && cols[i] > 0) {
+      const uint64_t b = (uint64_t)((((rows[i] + 1) >> 1) * cols[i] + kNoiseThreads - 1) /
+                                    kNoiseThreads);
+      if (b > 0x7fffffffULL) return DPC_ENOTSUP;
+      if (k == kLeafMax || blocks + b > 0x7fffffffULL) {
+        tab.n = k;
+        if (dtype == DPC_BF16) {
+          hipLaunchKernelGGL(add_noise_leaves_kernel<true>, dim3((unsigned)blocks),
+                             dim3(kNoiseThreads), 0, s, tab);
+        } else {
+          hipLaunchKernelGGL(add_noise_leaves_kernel<false>, dim3((unsigned)blocks),
+                             dim3(kNoiseThreads), 0, s, tab);
+        }
+        DPC_HIP_CHECK(hipGetLastError());
+        k = 0;
+        blocks = 0;
+      }
+      tab.l[k] = NoiseLeaf{x[i], y[i], rows[i], cols[i], (float)sigma[i], leaf_ids[i],
+                           (uint32_t)blocks};
+      blocks += b;
+      ++k;
+    }
+    if (i == n && k > 0) {
+      tab.n = k;
+      if (dtype == DPC_BF16) {
+        hipLaunchKernelGGL(add_noise_leaves_kernel<true>, dim3((unsigned)blocks),
+                           dim3(kNoiseThreads), 0, s, tab);
+      } else {
+        hipLaunchKernelGGL(add_noise_leaves_kernel<false>, dim3((unsigned)blocks),
+                           dim3(kNoiseThreads), 0, s, tab);
+      }
+      DPC_HIP_CHECK(hipGetLastError());
+    }
+  }
   return DPC_OK;
 }

@@ -517,6 +517,53 @@ def per_example_grads(A: torch.Tensor, G: torch.Tensor, *,
     return out
 
 
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous and 16-byte aligned (the kernels read rows with aligned
+    vector loads)."""
+    if t.is_contiguous() and t.data_ptr() % 16 == 0:
+        return t
+    return t.clone(memory_format=torch.contiguous_format)
+
+
+def per_example_grads_grouped(A_list, G_list, *,
+                              out_dtype: torch.dtype | None = None) -> list[torch.Tensor]:
+    """``per_example_grads`` of several layers that share the batch and token
+    count (``dpc_per_example_grads_grouped``: the eligible bfloat16 layers
+    share MFMA launches).  Returns one [B, dout, din] tensor per layer."""
+    if len(A_list) != len(G_list) or not A_list:
+        raise ConfigurationError("expected matching, non-empty lists of A and G")
+    dev = nat.require_device(*A_list, *G_list)
+    dtype = A_list[0].dtype
+    B, T = A_list[0].shape[:2]
+    for A, G in zip(A_list, G_list):
+        if A.dim() != 3 or G.dim() != 3 or A.shape[:2] != (B, T) or G.shape[:2] != (B, T):
+            raise ConfigurationError("expected A [B, T, din], G [B, T, dout] with one B and T")
+        if A.dtype != dtype or G.dtype != dtype:
+            raise ConfigurationError("the layers' operands must share one dtype")
+        if min(A.shape[2], G.shape[2]) > NARROW_MAX:
+            raise ConfigurationError(f"per_example_grads needs din or dout <= {NARROW_MAX}")
+    out_dtype = out_dtype or dtype
+    n = len(A_list)
+    dins = [A.shape[2] for A in A_list]
+    douts = [G.shape[2] for G in G_list]
+    outs = [torch.empty((B, o, i), dtype=out_dtype, device=dev) for i, o in zip(dins, douts)]
+    if B == 0:
+        return outs
+    As = [_aligned(A) for A in A_list]
+    Gs = [_aligned(G) for G in G_list]
+    c_din = (ctypes.c_int * n)(*dins)
+    c_dout = (ctypes.c_int * n)(*douts)
+    ws_bytes = nat.load().dpc_per_example_grads_grouped_workspace_bytes(
+        n, c_din, c_dout, B, T, nat.dtype_code(dtype))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    nat.call("dpc_per_example_grads_grouped", n, (ctypes.c_void_p * n)(*[t.data_ptr() for t in As]),
+             (ctypes.c_void_p * n)(*[t.data_ptr() for t in Gs]),
+             (ctypes.c_void_p * n)(*[t.data_ptr() for t in outs]), c_din, c_dout, B, T,
+             nat.dtype_code(dtype), nat.dtype_code(out_dtype), nat.ptr(ws), ws_bytes,
+             nat.stream_handle(dev))
+    return outs
+
+
 def leaf_view(t: torch.Tensor) -> tuple[int, int]:
     """The [rows, cols] view of a leaf for the device noise stream."""
     if t.dim() == 0:
@@ -549,6 +596,34 @@ def add_noise(
         nat.stream_handle(dev),
     )
     return y
+
+
+def add_noise_leaves(xs, sigmas, *, seed: int, leaf_ids, inplace: bool = False
+                     ) -> list[torch.Tensor]:
+    """``add_noise`` (Philox stream) of several leaves of one dtype in as few
+    launches as possible (``dpc_add_noise_leaves``); each result equals
+    ``add_noise(x, sigma, seed=seed, leaf_id=leaf_id)``.  With ``inplace``
+    the (contiguous) leaves themselves receive the noise."""
+    if not (len(xs) == len(sigmas) == len(leaf_ids)) or not xs:
+        raise ConfigurationError("expected matching, non-empty lists of leaves, sigmas and ids")
+    dev = nat.require_device(*xs)
+    dtype = xs[0].dtype
+    if any(x.dtype != dtype for x in xs):
+        raise ConfigurationError("the leaves must share one dtype")
+    if inplace and not all(x.is_contiguous() for x in xs):
+        raise ConfigurationError("in-place noise needs contiguous leaves")
+    xs = [_contig(x) for x in xs]
+    ys = xs if inplace else [torch.empty_like(x) for x in xs]
+    n = len(xs)
+    views = [leaf_view(x) for x in xs]
+    nat.call("dpc_add_noise_leaves", n, (ctypes.c_void_p * n)(*[x.data_ptr() for x in xs]),
+             (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys]),
+             (ctypes.c_int64 * n)(*[r for r, _ in views]),
+             (ctypes.c_int64 * n)(*[c for _, c in views]),
+             (ctypes.c_double * n)(*[float(v) for v in sigmas]),
+             (ctypes.c_uint32 * n)(*[i & 0xFFFFFFFF for i in leaf_ids]),
+             nat.dtype_code(dtype), seed & ((1 << 64) - 1), nat.stream_handle(dev))
+    return ys
 
 
 def philox4x32_10(counter: tuple[int, int, int, int], key: tuple[int, int], n: int,

@@ -386,6 +386,33 @@ def test_add_noise_injected_bit_exact(dev, dtype, shape):
     assert torch.equal(y, noise_oracle.sample(x, 0.7, z))
 
 
+# The grouped noise gives every leaf exactly add_noise's values: 37 leaves
+# (two launches of up to 32), flat and row-block shapes, a 1-D leaf, an empty
+# one, a scalar, sigma 0 (copied, -0.0 kept), out of place and in place.
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("inplace", [False, True])
+def test_add_noise_leaves_matches_per_leaf(dev, dtype, inplace):
+    g = _gen(71)
+    shapes = [(64, 33), (7,), (5, 3, 4), (7, 768), (3, 2100), (0, 5), (), (16, 4096)]
+    shapes = (shapes * 5)[:37]
+    xs = [torch.randn(sh, generator=g).to(dtype).to(dev) for sh in shapes]
+    xs[2].view(-1)[0] = -0.0
+    sigmas = [0.0 if i % 7 == 2 else 0.25 + 0.1 * i for i in range(len(xs))]
+    ids = [3 * i + 1 for i in range(len(xs))]
+    seed = 0x0F1E2D3C4B5A6978
+    want = [ops.add_noise(x, s, mode=nat.NOISE_PHILOX, seed=seed, leaf_id=i)
+            for x, s, i in zip(xs, sigmas, ids)]
+    ins = [x.clone() for x in xs]
+    got = ops.add_noise_leaves(ins, sigmas, seed=seed, leaf_ids=ids, inplace=inplace)
+    bits = torch.int16 if dtype == torch.bfloat16 else torch.int32
+    for k, (a, b) in enumerate(zip(got, want)):
+        assert a.shape == b.shape, k
+        assert torch.equal(a.view(bits), b.view(bits)), k
+        if a.numel():
+            assert (a.data_ptr() == ins[k].data_ptr()) == inplace, k
+    assert torch.equal(got[2].reshape(-1)[:1].view(bits), xs[2].reshape(-1)[:1].view(bits))
+
+
 @pytest.mark.parametrize("shape", [(64, 33), (7,), (5, 3, 4), (7, 768), (3, 2100), (2, 4, 1024),
                                    (3, 2049)])
 def test_add_noise_device_stream_matches_c_oracle(dev, shape):

@@ -28,19 +28,24 @@ def _rel(got, want):
     return ((got - want).norm() / want.norm().clamp_min(1e-300)).item()
 
 
-# Widths % 4 != 0 take the general kernels; the others (bf16) the pipelined
-# 8-wave kernel: split chunks (2, 2048, 4096, 16), (3, 1000, 16, 1024), an odd
-# token count past one LDS chunk with a tail column block (1, 4097, 8, 520),
-# one chunk written directly (8, 64, 14336, 16), 17..32 narrow columns with
-# the narrow side the output (1, 300, 1200, 17), (3, 96, 4096, 32) or the
-# input (2, 512, 24, 2048), and a partial column block (2, 1056, 520, 8).
+# Widths % 4 != 0 take the general kernels.  In bfloat16, wide widths % 8 ==
+# 0 with an even narrow width take the MFMA kernel: split chunks (2, 2048,
+# 4096, 16), (3, 1000, 16, 1024) (a partial last step), an odd token count
+# with a tail column block of 8 (1, 4097, 8, 520), one step written directly
+# (8, 64, 14336, 16), 17..32 narrow columns with the narrow side the output
+# (3, 96, 4096, 32) or the input (2, 512, 24, 2048), narrow widths 2 and 6
+# (2, 333, 2, 1024), (1, 2100, 4104, 6) and a partial column block (2, 1056,
+# 520, 8); the other widths % 4 == 0 the 8-wave v_dot2 kernel: (2, 130, 1,
+# 700), an odd narrow width (1, 300, 1200, 17) and split chunks past one LDS
+# chunk (2, 2500, 2044, 16).
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("B,T,din,dout", [(3, 77, 513, 16), (2, 64, 16, 1030), (4, 5, 32, 33),
                                           (2, 130, 1, 700), (1, 300, 1200, 17),
                                           (2, 2048, 4096, 16), (3, 1000, 16, 1024),
                                           (1, 4097, 8, 520), (8, 64, 14336, 16),
                                           (2, 512, 24, 2048), (3, 96, 4096, 32),
-                                          (2, 1056, 520, 8)])
+                                          (2, 1056, 520, 8), (2, 333, 2, 1024),
+                                          (1, 2100, 4104, 6), (2, 2500, 2044, 16)])
 def test_per_example_grads_match_oracle(dev, dtype, B, T, din, dout):
     g = torch.Generator().manual_seed(B * 1000 + din + dout)
     A = torch.randn(B, T, din, generator=g).to(dtype)
@@ -55,6 +60,32 @@ def test_per_example_grads_match_oracle(dev, dtype, B, T, din, dout):
     assert torch.equal(got_bf.cpu(), got.cpu().to(torch.bfloat16))
     # Deterministic: a second call gives the same bits.
     assert torch.equal(ops.per_example_grads(A.to(dev), G.to(dev), out_dtype=torch.float32), got)
+
+
+# The grouped call: every problem as the oracle has it, whatever launch it
+# lands in -- 37 bfloat16 problems (two MFMA launches of up to 32 in the
+# 16-column class, one in the 32-column class; narrow side the input or the
+# output), problems the MFMA kernel does not take (wide side % 8 != 0, an odd
+# narrow side) run one by one, and the same set in float32 (none in MFMA
+# launches).  Few workgroups (T = 300) make the launches split the tokens.
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T", [300, 64])
+def test_per_example_grads_grouped_match_oracle(dev, dtype, T):
+    B = 2
+    g = torch.Generator().manual_seed(T)
+    dims = [(96, 16), (16, 520), (24, 2048), (4096, 32), (1028, 12), (17, 600), (8, 8)]
+    dims += [(64 + 8 * i, 2 + 2 * (i % 8)) for i in range(30)]
+    A = [torch.randn(B, T, din, generator=g).to(dtype) for din, _ in dims]
+    G = [torch.randn(B, T, dout, generator=g).to(dtype) for _, dout in dims]
+    got = ops.per_example_grads_grouped([a.to(dev) for a in A], [x.to(dev) for x in G],
+                                        out_dtype=torch.float32)
+    got_bf = ops.per_example_grads_grouped([a.to(dev) for a in A], [x.to(dev) for x in G],
+                                           out_dtype=torch.bfloat16)
+    for k, (a, x) in enumerate(zip(A, G)):
+        want = ghost_oracle.linear_per_example_grads(a, x, dtype=torch.float64)[0]
+        assert got[k].shape == want.shape, k
+        assert _rel(got[k], want) < 1e-5, k
+        assert torch.equal(got_bf[k].cpu(), got[k].cpu().to(torch.bfloat16)), k
 
 
 def _case(dtype, seed=0):
@@ -91,9 +122,9 @@ def test_ghost_lora_block_matches_per_example_oracle(dev, dtype, monkeypatch):
     names = sorted(n for n, p in model.named_parameters() if p.requires_grad)
     assert len(names) == 14
     calls = []
-    real = ops.per_example_grads
-    monkeypatch.setattr(ops, "per_example_grads",
-                        lambda *a, **k: calls.append(1) or real(*a, **k))
+    real = ops.per_example_grads_grouped
+    monkeypatch.setattr(ops, "per_example_grads_grouped",
+                        lambda A_list, G_list, **k: calls.extend(A_list) or real(A_list, G_list, **k))
     C = 0.5
     res = _oracle(ref, x, t, C, names)
     fn, st = ghost_clipped_grad(model, _sq, clipping_norm=C, normalize_by=2.0, return_aux=True,
