@@ -12,7 +12,17 @@
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// A pointer to global memory as such: a pointer loaded from a device table
+// has the generic address space, and accesses through it become flat
+// instructions, which also count as LDS operations (so a later barrier waits
+// for them to complete).
+template <typename T>
+DPC_DEVICE __attribute__((address_space(1))) T* global_ptr(const void* p) {
+  return (__attribute__((address_space(1))) T*)(const_cast<void*>(p));
+}
 
 // vmcnt(N) with the other counters left alone (gfx9 s_waitcnt encoding):
 // the wait for a wave's direct-to-LDS transfers (buffer_load ... lds), which
@@ -29,15 +39,14 @@ DPC_HOST_DEVICE float bf16_bits_to_f32(uint16_t b) {
   return v.f;
 }
 
+// Branch-free (a select, not a divergent branch around the NaN case).
 DPC_HOST_DEVICE uint16_t f32_to_bf16_bits(float f) {
   union { uint32_t u; float f; } v;
   v.f = f;
-  uint32_t u = v.u;
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
-    return (uint16_t)((u >> 16) | 0x0040u);  // quiet NaN
-  }
-  uint32_t rounding = 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)((u + rounding) >> 16);
+  const uint32_t u = v.u;
+  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t quiet_nan = (u >> 16) | 0x0040u;
+  return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? quiet_nan : rounded);
 }
 
 // Round a float to the nearest bf16 and widen it back (one rounding).

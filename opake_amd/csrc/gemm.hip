@@ -18,13 +18,17 @@
 //     example's scale and are multiplied by scale_prev / scale_next where the
 //     example changes (the clip plan lists first the examples for which this
 //     stays far inside fp32, see plan.h; the others are summed after the
-//     loop).  Grouped mode, and the plan's other examples, stage G through
-//     registers, multiplied by the power of two of the step's scale
-//     s = m 2^e (m in [1, 2)), which is exact, and apply the mantissa m to
-//     the accumulators in the same way (they hold the partial sum divided by
-//     the current m, rescaled by m_prev / m_next where it changes).  So no
-//     operand is ever rounded: each example's contribution is the fp32 sum of
-//     the exact products of the given bf16 values, times its scale.
+//     loop).  Grouped mode does the same for a problem whose scales all lie
+//     in [2^-16, 2^16] (checked per workgroup: the grouped launch is two
+//     launches, one per case, and a workgroup returns at once from the one
+//     that does not match its problem).  Other grouped problems, and the
+//     plan's other examples, stage G through registers, multiplied by the
+//     power of two of the step's scale s = m 2^e (m in [1, 2)), which is
+//     exact, and apply the mantissa m to the accumulators in the same way
+//     (they hold the partial sum divided by the current m, rescaled by
+//     m_prev / m_next where it changes).  So no operand is ever rounded:
+//     each example's contribution is the fp32 sum of the exact products of
+//     the given bf16 values, times its scale.
 //     Examples with scale 0 are skipped through the clip plan, so their data
 //     (including any NaN/Inf) is never read;
 //   * two LDS stages (128 KiB), one barrier per K step; the A DMAs of step
@@ -87,9 +91,9 @@ __device__ __forceinline__ float finish_value(float v, const Epilogue& ep, float
 
 __device__ __forceinline__ void store_value(const Epilogue& ep, size_t idx, float v) {
   if (ep.out_bf16) {
-    reinterpret_cast<uint16_t*>(ep.out)[idx] = f32_to_bf16_bits(v);
+    global_ptr<uint16_t>(ep.out)[idx] = f32_to_bf16_bits(v);
   } else {
-    reinterpret_cast<float*>(ep.out)[idx] = v;
+    global_ptr<float>(ep.out)[idx] = v;
   }
 }
 
@@ -102,8 +106,8 @@ __device__ __forceinline__ void emit_pair(const Epilogue& ep, int m, int n, floa
       philox_normal_pair(ep.seed, ep.leaf, (uint64_t)(m >> 1) * (uint64_t)ep.N + (uint64_t)n,
                          &z0, &z1);
     } else {
-      z0 = ep.noise[(size_t)m * ep.N + n];
-      if (m + 1 < ep.M) z1 = ep.noise[(size_t)(m + 1) * ep.N + n];
+      z0 = global_ptr<const float>(ep.noise)[(size_t)m * ep.N + n];
+      if (m + 1 < ep.M) z1 = global_ptr<const float>(ep.noise)[(size_t)(m + 1) * ep.N + n];
     }
   }
   store_value(ep, (size_t)m * ep.N + n, finish_value(v0, ep, z0));
@@ -124,7 +128,7 @@ __device__ __forceinline__ void emit_quad(const Epilogue& ep, int m, int n, cons
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
         if (m + r < ep.M) {
-          const float2 zz = *reinterpret_cast<const float2*>(ep.noise + (size_t)(m + r) * ep.N + n);
+          const f32x2_t zz = *global_ptr<const f32x2_t>(ep.noise + (size_t)(m + r) * ep.N + n);
           z[r][0] = zz.x;
           z[r][1] = zz.y;
         }
@@ -139,9 +143,9 @@ __device__ __forceinline__ void emit_quad(const Epilogue& ep, int m, int n, cons
     const size_t idx = (size_t)(m + r) * ep.N + n;
     if (ep.out_bf16) {
       const uint32_t packed = (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
-      *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(ep.out) + idx) = packed;
+      *global_ptr<uint32_t>(reinterpret_cast<uint16_t*>(ep.out) + idx) = packed;
     } else {
-      *reinterpret_cast<float2*>(reinterpret_cast<float*>(ep.out) + idx) = make_float2(a, b);
+      *global_ptr<f32x2_t>(reinterpret_cast<float*>(ep.out) + idx) = f32x2_t{a, b};
     }
   }
 }
@@ -151,7 +155,6 @@ __device__ __forceinline__ void emit_quad(const Epilogue& ep, int m, int n, cons
 constexpr int kOutOfRange = 0x7ff00000;
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 // A positive finite scale s = m 2^e with m in [1, 2): the mantissa m and the
 // power of two 2^e (both exact; 2^e is subnormal below 2^-126).
@@ -253,7 +256,7 @@ constexpr int kG0Bytes = (kOperandBytes > kEpiPassRows * kEpiLd * 4) ? kOperandB
 // higher clock than 32x32x16 on the same data, and 8 waves measure faster
 // than 4 waves of 128 x 128 whose 256 accumulators per lane leave too few
 // registers for the pipeline.)
-template <bool kGrouped, int kWaves>
+template <bool kGrouped, bool kGdma, int kWaves>
 __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
   constexpr int kT = kWaves * 64;           // threads
   constexpr int kWavesN = kWaves / 2;       // waves along the tile columns
@@ -273,11 +276,13 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
   const int tiles_m = ceil_div(M, kBM), tiles_n = ceil_div(N, kBN);
   int lin = xcd_linear_id(gridDim.x);
   int grp = 0, split = 0;
+  // The quotients are workgroup-uniform, but the compiler's integer division
+  // leaves them in vector registers: read them into scalar ones.
   if (kGrouped) {
-    grp = lin / (tiles_m * tiles_n);
+    grp = __builtin_amdgcn_readfirstlane(lin / (tiles_m * tiles_n));
     lin -= grp * tiles_m * tiles_n;
   } else if (args.splits > 1) {
-    split = lin / (tiles_m * tiles_n);
+    split = __builtin_amdgcn_readfirstlane(lin / (tiles_m * tiles_n));
     lin -= split * tiles_m * tiles_n;
   }
   int tm, tn;
@@ -295,9 +300,17 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
   const int spe = T / kBK;
   ClipPlanView plan = clip_plan_view(const_cast<void*>(args.plan), args.B);
   if (kGrouped) {
-    Abase = reinterpret_cast<const uint16_t*>(args.grp.a_ptrs[grp]);
-    Gbase = reinterpret_cast<const uint16_t*>(args.grp.g_ptrs[grp]);
-    total_rows = args.grp.rows[grp];
+    // Table entries of the (uniform) problem, read into scalar registers: the
+    // compiler loads them into vector registers, and a buffer resource built
+    // from those would make every DMA a loop over the distinct values.
+    auto uniform64 = [](int64_t v) __attribute__((always_inline)) {
+      const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+      const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+      return (int64_t)(((uint64_t)hi << 32) | lo);
+    };
+    Abase = reinterpret_cast<const uint16_t*>(uniform64(args.grp.a_ptrs[grp]));
+    Gbase = reinterpret_cast<const uint16_t*>(uniform64(args.grp.g_ptrs[grp]));
+    total_rows = __builtin_amdgcn_readfirstlane(args.grp.rows[grp]);
     step0 = args.grp.step_start[grp];
     nsteps = args.grp.step_start[grp + 1] - step0;
     ep.out = reinterpret_cast<void*>(args.grp.out_ptrs[grp]);
@@ -311,6 +324,10 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     for (int i = tid * 16; i < kOperandBytes; i += kT * 16) {
       *reinterpret_cast<u32x4_t*>(lds_a0 + i) = zero;
       *reinterpret_cast<u32x4_t*>(lds_a1 + i) = zero;
+      if constexpr (kGdma) {
+        *reinterpret_cast<u32x4_t*>(lds_g0 + i) = zero;
+        *reinterpret_cast<u32x4_t*>(lds_g1 + i) = zero;
+      }
     }
     __syncthreads();
   } else {
@@ -428,16 +445,26 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
         }
       }
     };
-    // Dense mode: G goes into LDS by DMA too, in the same layout as A (its
-    // scale is applied to the accumulators).
-    const int gdma_voff = dma_row * M * 2 + min(m0 + dma_col, M - 8) * 2;
-    auto dma_g = [&](uint8_t* gstage, int row0) __attribute__((always_inline)) {
+    // kGdma (dense mode, and grouped problems whose scales the accumulators
+    // can carry): G goes into LDS by DMA too, in the same layout as A (its
+    // scale is applied to the accumulators); grouped rows past `valid` and
+    // columns past M read as zero, as for A.
+    const int gdma_voff =
+        dma_row * M * 2 + (kGrouped ? m0 + dma_col : min(m0 + dma_col, M - 8)) * 2;
+    const int gdma_bad = (kGrouped && m0 + dma_col >= M) ? kOutOfRange : 0;
+    auto dma_g = [&](uint8_t* gstage, int row0, int valid) __attribute__((always_inline)) {
 #pragma unroll
       for (int j = 0; j < kDma; ++j) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            g_rsrc,
-            (__attribute__((address_space(3))) void*)((lds_u8_t*)gstage + (w + kWaves * j) * 1024),
-            16, gdma_voff, (row0 + 2 * kWaves * j) * M * 2, 0, 0);
+        auto* dst = (__attribute__((address_space(3))) void*)((lds_u8_t*)gstage +
+                                                               (w + kWaves * j) * 1024);
+        const int rows = row0 + 2 * kWaves * j;
+        if constexpr (kGrouped) {
+          const int bad = dma_row >= valid - 2 * kWaves * j ? kOutOfRange : gdma_bad;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(g_rsrc, dst, 16,
+                                                   (rows * M * 2 + gdma_voff) | bad, 0, 0, 0);
+        } else {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(g_rsrc, dst, 16, gdma_voff, rows * M * 2, 0, 0);
+        }
       }
     };
 
@@ -554,7 +581,7 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     // by sc_cur / sc_next.
     float sc_cur = 0.0f;
     auto acc_factor = [&](float sc) __attribute__((always_inline)) {
-      return kGrouped ? scale_mantissa(sc) : sc;
+      return kGdma ? sc : scale_mantissa(sc);
     };
     auto rescale = [&](float r) __attribute__((always_inline)) {
 #pragma unroll
@@ -565,7 +592,7 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     auto k_step = [&](int s, uint8_t* gcur, uint8_t* acur, uint8_t* gnxt,
                       uint8_t* anxt) __attribute__((always_inline)) {
       const float sc_s1 = acc_factor(sc_next);  // accumulator factor of step s + 1
-      const float g_next = kGrouped ? scale_pow2(sc_next) : 1.0f;  // G factor of step s + 1
+      const float g_next = kGdma ? 1.0f : scale_pow2(sc_next);  // G factor of step s + 1
       float sc_after;
       int valid2;
       const int row2 = step_row0(min(s + 2, nsteps - 1), &sc_after, &valid2);
@@ -573,7 +600,7 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       // MFMAs of a 32-row sub-step past them (all zeros) are skipped.
       const int vcur = kGrouped ? valid_cur : kBK;
       auto stage_g = [&](int kk) __attribute__((always_inline)) {
-        if constexpr (kGrouped) {
+        if constexpr (!kGdma) {
 #pragma unroll
           for (int c = 0; c < kGCSub; ++c) store_chunk(gnxt, kk * kGCSub + c, g_next);
 #pragma unroll
@@ -581,7 +608,7 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
         }
       };
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (!kGrouped) dma_g(gnxt, row_next);
+      if constexpr (kGdma) dma_g(gnxt, row_next, valid_next);
       read_g16(gcur, 0, 1, gf1);
       mma16(gf0, af0, 0);
       stage_g(0);
@@ -606,7 +633,7 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       row_next = row2;
       valid_cur = valid_next;
       valid_next = valid2;
-      DPC_WAIT_VMCNT(kGrouped ? kGC : 0);
+      DPC_WAIT_VMCNT(kGdma ? 0 : kGC);
       __syncthreads();
       // Every wave has read this stage for the last time: the A DMAs of step
       // s + 2 go into it now, a quarter step before the next step starts.
@@ -634,23 +661,23 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
       valid_cur = valid0;
       sc_cur = acc_factor(sc_next);
       dma_a(lds_a0, row0, valid0);
-      if constexpr (kGrouped) {
+      if constexpr (!kGdma) {
         const float g0f = scale_pow2(sc_next);
 #pragma unroll
         for (int j = 0; j < kGC; ++j) load_chunk(row0, valid0, j);
 #pragma unroll
         for (int j = 0; j < kGC; ++j) store_chunk(g0, j, g0f);
       } else {
-        dma_g(g0, row0);
+        dma_g(g0, row0, valid0);
       }
       row_next = step_row0(min(1, nsteps - 1), &sc_next, &valid_next);
       dma_a(lds_a1, row_next, valid_next);
-      if constexpr (kGrouped) {
+      if constexpr (!kGdma) {
 #pragma unroll
         for (int j = 0; j < kGC; ++j) load_chunk(row_next, valid_next, j);
       }
       // Step 0's transfers have landed (step 1's DMAs and G loads may not).
-      DPC_WAIT_VMCNT(kGrouped ? kDma + kGC : kDma);
+      DPC_WAIT_VMCNT(kGdma ? kDma : kDma + kGC);
       __syncthreads();
       read_g16(g0, 0, 0, gf0);
       read_a16(lds_a0, 0, af0);
@@ -707,6 +734,8 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
   // rows; each thread owns a pair of adjacent columns and 32 / (kT / 128) of
   // the slice's rows, walked in even/odd row pairs: coalesced 4- or 8-byte
   // stores, and one Philox block per (row pair, column) in a rolled loop.
+  // (Writing each lane's accumulators straight out, without the LDS slices,
+  // measured slower: it needs more registers at the end of the K loop.)
   float* tile = reinterpret_cast<float*>(lds_g0);
   constexpr int kEpiRows = kEpiPassRows / (kT / 128);
   // Unrolled: the accumulator blocks are selected by compile-time indices
@@ -731,13 +760,13 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     const int rr = (tid >> 7) * kEpiRows;
     if (!kGrouped && args.splits > 1) {
       // Split-K: the raw fp32 tile; the reduce kernel finishes it.
-      float* part = args.partial + (size_t)split * M * N;
+      auto* part = global_ptr<float>(args.partial + (size_t)split * M * N);
 #pragma unroll 2
       for (int ml = rr; ml < rr + kEpiRows; ++ml) {
         const int m = m0 + e * kEpiPassRows + ml, n = n0 + cl;
         if (m < M && n < N)
-          *reinterpret_cast<float2*>(part + (size_t)m * N + n) =
-              *reinterpret_cast<const float2*>(tile + ml * kEpiLd + cl);
+          *reinterpret_cast<__attribute__((address_space(1))) f32x2_t*>(part + (size_t)m * N + n) =
+              *reinterpret_cast<const f32x2_t*>(tile + ml * kEpiLd + cl);
       }
     } else {
 #pragma unroll 2
@@ -755,14 +784,45 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
 // 8 waves (2 per SIMD) measure faster than the 4-wave 128 x 128 layout on
 // both the dense and the grouped workloads.  (Launch bounds must not depend on
 // a template parameter: the host stub of such a kernel is not emitted.)
-template <bool kGrouped>
+// Grouped mode: whether the scales of this workgroup's problem let the
+// accumulators carry them (every step's scale in [2^-16, 2^16], so the
+// accumulators never hold more than 2^16 times the sum computed so far):
+// then G goes in by DMA (kGdma), else through registers.  Called by every
+// thread; the result is workgroup-uniform.
+__device__ __forceinline__ bool grouped_scales_fit(const FastArgs& args) {
+  const int tiles = ceil_div(args.ep.M, kBM) * ceil_div(args.ep.N, kBN);
+  const int grp = xcd_linear_id(gridDim.x) / tiles;
+  const int s0 = args.grp.step_start[grp], s1 = args.grp.step_start[grp + 1];
+  int fit = 1;
+  for (int i = s0 + (int)threadIdx.x; i < s1; i += (int)blockDim.x) {
+    const float sc = args.grp.seg_scale[args.grp.steps[2 * i + 1] >> 7];
+    fit &= (sc >= 0x1.0p-16f && sc <= 0x1.0p16f) ? 1 : 0;
+  }
+  return __syncthreads_and(fit) != 0;
+}
+
+// A grouped launch is a pair of launches over the same grid, kGdma first:
+// each workgroup runs in the launch that matches its problem's scales and
+// returns at once from the other.
+template <bool kGrouped, bool kGdma>
 __global__ void __launch_bounds__(kFastWaves * 64, 1) clipped_sum_bf16_kernel(FastArgs args) {
-  clipped_sum_tile<kGrouped, kFastWaves>(args);
+  if constexpr (kGrouped) {
+    if (grouped_scales_fit(args) != kGdma) return;
+  }
+  clipped_sum_tile<kGrouped, kGdma, kFastWaves>(args);
 }
 
 template <bool kGrouped>
 void launch_fast(dim3 grid, hipStream_t s, const FastArgs& args) {
-  hipLaunchKernelGGL(clipped_sum_bf16_kernel<kGrouped>, grid, dim3(kFastWaves * 64), 0, s, args);
+  if constexpr (kGrouped) {
+    hipLaunchKernelGGL((clipped_sum_bf16_kernel<true, true>), grid, dim3(kFastWaves * 64), 0, s,
+                       args);
+    hipLaunchKernelGGL((clipped_sum_bf16_kernel<true, false>), grid, dim3(kFastWaves * 64), 0, s,
+                       args);
+  } else {
+    hipLaunchKernelGGL((clipped_sum_bf16_kernel<false, true>), grid, dim3(kFastWaves * 64), 0, s,
+                       args);
+  }
 }
 
 // Split-K finish: out = epilogue(sum over splits of partial[split], in

@@ -21,8 +21,9 @@ constexpr int kThreads = 256;
 
 template <bool kBf16>
 __device__ __forceinline__ float load_elem(int64_t base, int64_t idx) {
-  if (kBf16) return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(base)[idx]);
-  return reinterpret_cast<const float*>(base)[idx];
+  const void* p = reinterpret_cast<const void*>(base);
+  if (kBf16) return bf16_bits_to_f32(global_ptr<const uint16_t>(p)[idx]);
+  return global_ptr<const float>(p)[idx];
 }
 
 __device__ __forceinline__ double block_sum_f64(double v, double* red) {
@@ -113,8 +114,8 @@ tile_sq_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ siz
   const int64_t off0 = (int64_t)tile_local[t] * kTile;
   double s = 0.0;
   if (tile_vectorizable(base, n, off0, kElemBytes)) {
-    const u32x4_t* row =
-        reinterpret_cast<const u32x4_t*>(base + ((int64_t)b * n + off0) * kElemBytes);
+    const auto* row = global_ptr<const u32x4_t>(
+        reinterpret_cast<const void*>(base + ((int64_t)b * n + off0) * kElemBytes));
     u32x4_t c[kChunks];
 #pragma unroll
     for (int j = 0; j < kChunks; ++j) c[j] = __builtin_nontemporal_load(row + j * 64 + lane);
@@ -245,7 +246,7 @@ apply_sum_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ s
 #pragma unroll
         for (int h = 0; h < kLoads; ++h)
           c[r][h] = __builtin_nontemporal_load(
-              reinterpret_cast<const u32x4_t*>(p + (int64_t)(b + r) * stride) + h);
+              global_ptr<const u32x4_t>(p + (int64_t)(b + r) * stride) + h);
 #pragma unroll
       for (int r = 0; r < kApplyUnroll; ++r) {
         float x[8];
@@ -260,7 +261,7 @@ apply_sum_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ s
     }
     for (; b < B; ++b) {
       float x[8];
-      const u32x4_t* q = reinterpret_cast<const u32x4_t*>(p + (int64_t)b * stride);
+      const auto* q = global_ptr<const u32x4_t>(p + (int64_t)b * stride);
       if (kBf16) {
         chunk_f32<true>(q[0], x);
       } else {
