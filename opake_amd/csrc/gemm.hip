@@ -42,6 +42,8 @@
 //     every transfer is in range and a lane's DMA offsets are fixed;
 //   * workgroup ids are remapped so that each of the 8 XCDs owns a compact
 //     block of output tiles and re-reads operand tiles from its own L2.
+#include <type_traits>
+
 #include "common.h"
 #include "lds_stage.h"
 #include "plan.h"
@@ -150,6 +152,84 @@ __device__ __forceinline__ void emit_quad(const Epilogue& ep, int m, int n, cons
   }
 }
 
+#pragma clang fp contract(off)
+// finish_value with the epilogue's workgroup-uniform choices fixed at compile
+// time (bf16 output, / normalize_by, noise added): the tile epilogues pick
+// one variant per slice, so that their loops run no branch per value.
+template <bool kBf, bool kNb, bool kNoise>
+__device__ __forceinline__ float finish_value_t(float v, const Epilogue& ep, float z) {
+  if (kBf) v = round_to_bf16(v);
+  if (kNb) {
+    v = v / ep.nb;
+    if (kBf) v = round_to_bf16(v);
+  }
+  if (kNoise) {
+    float t = ep.sigma * z;
+    v = v + t;
+    if (kBf) v = round_to_bf16(v);
+  }
+  return v;
+}
+#pragma clang fp contract(on)
+
+// emit_quad with the choices of finish_value_t (kNoise: sigma != 0).
+template <bool kBf, bool kNb, bool kNoise>
+__device__ __forceinline__ void emit_quad_t(const Epilogue& ep, int m, int n, const float v[2][2]) {
+  if (n >= ep.N || m >= ep.M) return;
+  float z[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+  if (kNoise) {
+    if (ep.noise_mode == DPC_NOISE_PHILOX) {
+      const uint64_t blk = (uint64_t)(m >> 1) * (uint64_t)ep.N + (uint64_t)n;
+      philox_normal_pair(ep.seed, ep.leaf, blk, &z[0][0], &z[1][0]);
+      philox_normal_pair(ep.seed, ep.leaf, blk + 1, &z[0][1], &z[1][1]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        if (m + r < ep.M) {
+          const f32x2_t zz = *global_ptr<const f32x2_t>(ep.noise + (size_t)(m + r) * ep.N + n);
+          z[r][0] = zz.x;
+          z[r][1] = zz.y;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    if (m + r >= ep.M) break;
+    const float a = finish_value_t<kBf, kNb, kNoise>(v[r][0], ep, z[r][0]);
+    const float b = finish_value_t<kBf, kNb, kNoise>(v[r][1], ep, z[r][1]);
+    const size_t idx = (size_t)(m + r) * ep.N + n;
+    if (kBf) {
+      const uint32_t packed = (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+      *global_ptr<uint32_t>(reinterpret_cast<uint16_t*>(ep.out) + idx) = packed;
+    } else {
+      *global_ptr<f32x2_t>(reinterpret_cast<float*>(ep.out) + idx) = f32x2_t{a, b};
+    }
+  }
+}
+
+// Calls f(bf16 out, / normalize_by, noise) with the epilogue's choices as
+// compile-time constants.
+template <typename F>
+__device__ __forceinline__ void with_epilogue_choices(const Epilogue& ep, F&& f) {
+  using T = std::true_type;
+  using Fa = std::false_type;
+  const bool bf = ep.out_bf16 != 0, nb = ep.apply_nb != 0, nz = ep.sigma != 0.0f;
+  if (bf) {
+    if (nb) {
+      if (nz) f(T(), T(), T()); else f(T(), T(), Fa());
+    } else {
+      if (nz) f(T(), Fa(), T()); else f(T(), Fa(), Fa());
+    }
+  } else {
+    if (nb) {
+      if (nz) f(Fa(), T(), T()); else f(Fa(), T(), Fa());
+    } else {
+      if (nz) f(Fa(), Fa(), T()); else f(Fa(), Fa(), Fa());
+    }
+  }
+}
+
 // A 16-byte chunk outside the matrix columns is given an offset past the
 // buffer's range, which the hardware reads as zero.
 constexpr int kOutOfRange = 0x7ff00000;
@@ -239,10 +319,10 @@ struct FastArgs {
 };
 
 // LDS of the fast kernel: each stage's G tile and A tile in an array of its
-// own (the first G array, after the K loop, also holds a 32-row slice of the
-// output tile).  Operands filled by DMA (buffer_load ... lds) sit in distinct
-// objects so that the compiler sees that a DMA into one stage does not alias
-// the reads of the other, and inserts no memory-counter wait before them.
+// own (after the K loop they hold slices of the output tile).  Operands
+// filled by DMA (buffer_load ... lds) sit in distinct objects so that the
+// compiler sees that a DMA into one stage does not alias the reads of the
+// other, and inserts no memory-counter wait before them.
 constexpr int kEpiPassRows = 32;
 constexpr int kEpiLd = kBN + 4;
 constexpr int kG0Bytes = (kOperandBytes > kEpiPassRows * kEpiLd * 4) ? kOperandBytes
@@ -730,54 +810,126 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     }
   }
 
-  // Epilogue: the 256 x 256 fp32 tile goes through LDS in eight slices of 32
-  // rows; each thread owns a pair of adjacent columns and 32 / (kT / 128) of
-  // the slice's rows, walked in even/odd row pairs: coalesced 4- or 8-byte
-  // stores, and one Philox block per (row pair, column) in a rolled loop.
-  // (Writing each lane's accumulators straight out, without the LDS slices,
-  // measured slower: it needs more registers at the end of the K loop.)
-  float* tile = reinterpret_cast<float*>(lds_g0);
-  constexpr int kEpiRows = kEpiPassRows / (kT / 128);
-  // Unrolled: the accumulator blocks are selected by compile-time indices
-  // (a runtime index would move them to scratch memory).
+  // Two epilogues: the grouped kernels write the tile in two 128-row halves,
+  // which frees half the accumulators before any store; the dense kernel,
+  // whose back list leaves no registers to spare, keeps eight 32-row slices
+  // (the halves would spill in its K loop).
+  if constexpr (kGrouped) {
+    // Epilogue: the 256 x 256 fp32 tile goes through LDS in two halves of 128
+    // rows -- half h holds block rows 4h .. 4h + 3 of both wave rows (tile
+    // rows 64 h .. 64 h + 63 and 128 + 64 h ..), one 32-row quarter in each of
+    // the four LDS arrays, columns XOR-swizzled by 16-float groups so that the
+    // four row groups of a 16x16 block's write land on distinct banks.  After
+    // half 0 those accumulators are dead in every wave, and half 1 has more
+    // registers.  Each thread owns a pair of adjacent columns and 32 rows of a
+    // half, walked in even/odd row pairs: coalesced 4- or 8-byte stores, one
+    // Philox block per (row pair, column).  (Staging 32-row slices, and
+    // writing each lane's accumulators straight out without LDS, measured
+    // slower.)
+    static_assert(kT == 512 && kRB == 8, "two 128-row halves of 512 threads");
+    auto quarter = [&](int qi) __attribute__((always_inline)) {
+      return qi == 0 ? lds_g0 : qi == 1 ? lds_g1 : qi == 2 ? lds_a0 : lds_a1;
+    };
+    auto tile_off_epi = [](int row, int col) __attribute__((always_inline)) {
+      return row * kBN + (col ^ (((row >> 2) & 3) << 4));
+    };
+    const int eq = tid >> 7;  // emission quarter
+    const int cl = 2 * (tid & 127);
+    auto half = [&](auto H) __attribute__((always_inline)) {
+      constexpr int h = decltype(H)::value;
+      // Block row 4 h + ib (ib < 4) of wave row wm goes to quarter 2 wm + ib / 2,
+      // rows 16 (ib % 2) + 4 (lane / 16) + r.
 #pragma unroll
-  for (int e = 0; e < kBM / kEpiPassRows; ++e) {
-    if (wm == (e >> 2)) {
-      // 16x16 block (i, j): lane l holds rows 4 (l / 16) + r of column l % 16.
-#pragma unroll
-      for (int i2 = 0; i2 < 2; ++i2)
+      for (int ib = 0; ib < 4; ++ib) {
+        float* q = reinterpret_cast<float*>(quarter(2 * wm + (ib >> 1)));
 #pragma unroll
         for (int j = 0; j < kCB; ++j)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int ml = 16 * i2 + 4 * (lane >> 4) + r;
+            const int ml = 16 * (ib & 1) + 4 * (lane >> 4) + r;
             const int nl = wn * kWC + j * 16 + (lane & 15);
-            tile[ml * kEpiLd + nl] = acc[2 * (e & 3) + i2][j][r];
+            q[tile_off_epi(ml, nl)] = acc[4 * h + ib][j][r];
           }
-    }
-    __syncthreads();
-    const int cl = 2 * (tid & 127);
-    const int rr = (tid >> 7) * kEpiRows;
-    if (!kGrouped && args.splits > 1) {
-      // Split-K: the raw fp32 tile; the reduce kernel finishes it.
-      auto* part = global_ptr<float>(args.partial + (size_t)split * M * N);
-#pragma unroll 2
-      for (int ml = rr; ml < rr + kEpiRows; ++ml) {
-        const int m = m0 + e * kEpiPassRows + ml, n = n0 + cl;
-        if (m < M && n < N)
-          *reinterpret_cast<__attribute__((address_space(1))) f32x2_t*>(part + (size_t)m * N + n) =
-              *reinterpret_cast<const f32x2_t*>(tile + ml * kEpiLd + cl);
       }
-    } else {
+      __syncthreads();
+      // Quarter eq: tile rows (eq < 2 ? 0 : 128) + 64 h + 32 (eq & 1) + 0 .. 31.
+      const float* qr = reinterpret_cast<const float*>(quarter(eq));
+      const int mbase = m0 + (eq < 2 ? 0 : 128) + 64 * h + 32 * (eq & 1);
+      const int n = n0 + cl;
+      if (!kGrouped && args.splits > 1) {
+        // Split-K: the raw fp32 tile; the reduce kernel finishes it.
+        auto* part = global_ptr<float>(args.partial + (size_t)split * M * N);
+#pragma unroll 4
+        for (int ml = 0; ml < 32; ++ml) {
+          const int m = mbase + ml;
+          if (m < M && n < N)
+            *reinterpret_cast<__attribute__((address_space(1))) f32x2_t*>(part + (size_t)m * N + n) =
+                *reinterpret_cast<const f32x2_t*>(qr + tile_off_epi(ml, cl));
+        }
+      } else {
+          with_epilogue_choices(ep, [&](auto BF, auto NB, auto NZ) __attribute__((always_inline)) {
 #pragma unroll 2
-      for (int ml = rr; ml < rr + kEpiRows; ml += 2) {
-        const float2 t0 = *reinterpret_cast<const float2*>(tile + ml * kEpiLd + cl);
-        const float2 t1 = *reinterpret_cast<const float2*>(tile + (ml + 1) * kEpiLd + cl);
-        const float v[2][2] = {{t0.x, t0.y}, {t1.x, t1.y}};
-        emit_quad(ep, m0 + e * kEpiPassRows + ml, n0 + cl, v);
+          for (int ml = 0; ml < 32; ml += 2) {
+            const float2 t0 = *reinterpret_cast<const float2*>(qr + tile_off_epi(ml, cl));
+            const float2 t1 = *reinterpret_cast<const float2*>(qr + tile_off_epi(ml + 1, cl));
+            const float v[2][2] = {{t0.x, t0.y}, {t1.x, t1.y}};
+            emit_quad_t<decltype(BF)::value, decltype(NB)::value, decltype(NZ)::value>(
+                ep, mbase + ml, n, v);
+          }
+        });
       }
+      __syncthreads();
+    };
+    half(std::integral_constant<int, 0>());
+    half(std::integral_constant<int, 1>());
+  } else {
+    // Epilogue: the 256 x 256 fp32 tile goes through LDS in eight slices of 32
+    // rows; each thread owns a pair of adjacent columns and 32 / (kT / 128) of
+    // the slice's rows, walked in even/odd row pairs: coalesced 4- or 8-byte
+    // stores, and one Philox block per (row pair, column) in a rolled loop.
+    float* tile = reinterpret_cast<float*>(lds_g0);
+    constexpr int kEpiRows = kEpiPassRows / (kT / 128);
+    // Unrolled: the accumulator blocks are selected by compile-time indices
+    // (a runtime index would move them to scratch memory).
+#pragma unroll
+    for (int e = 0; e < kBM / kEpiPassRows; ++e) {
+      if (wm == (e >> 2)) {
+        // 16x16 block (i, j): lane l holds rows 4 (l / 16) + r of column l % 16.
+#pragma unroll
+        for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+          for (int j = 0; j < kCB; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int ml = 16 * i2 + 4 * (lane >> 4) + r;
+              const int nl = wn * kWC + j * 16 + (lane & 15);
+              tile[ml * kEpiLd + nl] = acc[2 * (e & 3) + i2][j][r];
+            }
+      }
+      __syncthreads();
+      const int cl = 2 * (tid & 127);
+      const int rr = (tid >> 7) * kEpiRows;
+      if (!kGrouped && args.splits > 1) {
+        // Split-K: the raw fp32 tile; the reduce kernel finishes it.
+        auto* part = global_ptr<float>(args.partial + (size_t)split * M * N);
+#pragma unroll 2
+        for (int ml = rr; ml < rr + kEpiRows; ++ml) {
+          const int m = m0 + e * kEpiPassRows + ml, n = n0 + cl;
+          if (m < M && n < N)
+            *reinterpret_cast<__attribute__((address_space(1))) f32x2_t*>(part + (size_t)m * N + n) =
+                *reinterpret_cast<const f32x2_t*>(tile + ml * kEpiLd + cl);
+        }
+      } else {
+#pragma unroll 2
+        for (int ml = rr; ml < rr + kEpiRows; ml += 2) {
+          const float2 t0 = *reinterpret_cast<const float2*>(tile + ml * kEpiLd + cl);
+          const float2 t1 = *reinterpret_cast<const float2*>(tile + (ml + 1) * kEpiLd + cl);
+          const float v[2][2] = {{t0.x, t0.y}, {t1.x, t1.y}};
+          emit_quad(ep, m0 + e * kEpiPassRows + ml, n0 + cl, v);
+        }
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
