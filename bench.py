@@ -420,7 +420,8 @@ def run_moe(args) -> dict:
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "clipped_sum_bf16_kernel<true> (grouped; 2 launches per step)",
+            "kernel": "clipped_sum_bf16_kernel<true, true> (grouped, G by DMA; 2 grouped "
+                      "GEMMs per step, each with its empty <true, false> companion launch)",
             "achieved": gemm_tflops,
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
