@@ -746,8 +746,10 @@ def lora_model(device, dtype, seed=0):
 
 def lora_work(b=LORA_B, t=LORA_T):
     """Per-example adapter gradients: FLOPs (2 T din r per adapter side) and the
-    algorithmic HBM bytes of their kernel (read A and G, write the [B, dout,
-    din] gradients in bf16), summed over the 14 adapters."""
+    algorithmic HBM bytes of their kernel -- every operand read once (q / k / v
+    share their input, and so do gate / up: 3 of the 7 lora_A inputs are
+    repeats) and the [B, dout, din] gradients written in bf16 -- summed over
+    the 14 adapters."""
     kv = LORA_D // LORA_H * LORA_KV
     projs = [(LORA_D, LORA_D), (LORA_D, kv), (LORA_D, kv), (LORA_D, LORA_D),
              (LORA_D, LORA_F), (LORA_D, LORA_F), (LORA_F, LORA_D)]
@@ -756,6 +758,7 @@ def lora_work(b=LORA_B, t=LORA_T):
         for a, g in ((din, LORA_R), (LORA_R, dout)):
             flops += b * 2 * t * a * g
             nbytes += b * (t * (a + g) * 2 + a * g * 2)
+    nbytes -= 3 * b * t * LORA_D * 2
     return flops, nbytes
 
 
@@ -879,8 +882,9 @@ def run_lora(args) -> dict:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "narrow_wide_mfma_kernel<16> (dpc_per_example_grads_grouped: the 14 "
-                      "adapter gradients in one launch per step)",
+            "kernel": "narrow_wide_mfma_kernel<16, 3> (dpc_per_example_grads_grouped: the 14 "
+                      "adapter gradients in one launch per step, as 11 groups -- q / k / v and "
+                      "gate / up each share one pass over their input)",
             "achieved": gbs,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -398,19 +398,24 @@ constexpr int kNmStages = 4;
 constexpr int kNmWideBytes = kNmK * kTileRowBytes;             // 32 KiB
 constexpr int kNmWideDma = kNmWideBytes / (kNmWaves * 1024);   // 16-byte DMAs per lane and step
 
-// One problem of a grouped launch: out[b, s, w] (narrow side G) or out[b, w,
-// s] (narrow side A) over the tokens [split * chunk, min(T, (split + 1) *
-// chunk)), written to `out` when splits == 1, else as the fp32 partial
-// partial[split][b][s][w].  Workgroups wg_start .. wg_start + col_tiles * B *
-// splits - 1 of the launch take it, column tile fastest.  Requires chunk % 64
-// == 0, nw % 8 == 0, ns even, ns <= NS and (T + 64) * nw * 2 < kNwOutOfRange.
-constexpr int kNmMaxProblems = 32;
+// One problem of a grouped launch: up to kNmMaxSlots layers that share the
+// wide operand (the LoRA A factors of the projections fed by one activation),
+// each with its own narrow operand (narrow[k], ns[k] columns), written as
+// out_k[b, s, w] (narrow side G) or out_k[b, w, s] (narrow side A) over the
+// tokens [split * chunk, min(T, (split + 1) * chunk)) -- to out[k] when
+// splits == 1, else as the fp32 partial partial[k][split][b][s][w].
+// Workgroups wg_start .. wg_start + col_tiles * B * splits - 1 of the launch
+// take it, column tile fastest.  Requires chunk % 64 == 0, nw % 8 == 0, every
+// ns[k] even and <= NS, and (T + 64) * nw * 2 < kNwOutOfRange.
+constexpr int kNmMaxProblems = 24;
+constexpr int kNmMaxSlots = 3;
 struct NmProblem {
   const uint16_t* wide;
-  const uint16_t* narrow;
-  void* out;
-  float* partial;
-  int nw, ns, narrow_is_g;
+  const uint16_t* narrow[kNmMaxSlots];
+  void* out[kNmMaxSlots];
+  float* partial[kNmMaxSlots];
+  int ns[kNmMaxSlots];
+  int nslots, nw, narrow_is_g;
   int col_tiles, splits, chunk;
   int wg_start;
 };
@@ -420,16 +425,22 @@ struct NmTable {
   int n, B, T, out_bf16;
 };
 
-template <int NS>
+// kSlots narrow operands per problem (NS = 16: 3, NS = 32: 1); the LDS stage
+// holds the wide tile and kSlots narrow tiles.  Every wave issues the DMAs of
+// all kSlots tiles (an absent one reads zeros, from an empty range, without
+// memory traffic), so the memory-counter waits are compile-time constants;
+// the MFMAs and stores of absent slots are skipped.
+template <int NS, int kSlots>
 __global__ void __launch_bounds__(kNmThreads, 1)
 narrow_wide_mfma_kernel(const NmTable tab) {
   constexpr int kRowN = NS * 2;                                 // bytes of a narrow row in LDS
-  constexpr int kNarrowBytes = kNmK * kRowN;                    // 2 or 4 KiB
-  constexpr int kNarrowDma = kNarrowBytes / (kNmWaves * 256);   // 4-byte DMAs per lane and step
-  constexpr int kDma = kNmWideDma + kNarrowDma;
-  constexpr int kStage = kNmWideBytes + kNarrowBytes;
+  constexpr int kNarrowBytes = kNmK * kRowN;                    // 2 or 4 KiB per slot
+  constexpr int kNarrowDma = kNarrowBytes / (kNmWaves * 256);   // 4-byte DMAs per lane, slot, step
+  constexpr int kDma = kNmWideDma + kSlots * kNarrowDma;
+  constexpr int kStage = kNmWideBytes + kSlots * kNarrowBytes;
   constexpr int kMB = NS / 16;                                  // 16-row blocks of narrow columns
   static_assert(kNarrowDma * kNmWaves * 256 == kNarrowBytes, "narrow tile split");
+  static_assert(kSlots <= kNmMaxSlots && kNmStages * kStage <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(16))) uint8_t lds[kNmStages * kStage];
   const int lin = blockIdx.x;
   int pi = 0;
@@ -437,12 +448,11 @@ narrow_wide_mfma_kernel(const NmTable tab) {
     if (lin >= tab.p[i].wg_start) pi = i;
   const NmProblem& P = tab.p[pi];
   const int B = tab.B, T = tab.T;
-  const int nw = P.nw, ns = P.ns, chunk = P.chunk, splits = P.splits;
+  const int nw = P.nw, chunk = P.chunk, splits = P.splits, nslots = P.nslots;
   const int local = lin - P.wg_start;
   const int ct = local % P.col_tiles, rest = local / P.col_tiles;
   const int b = rest % B, split = rest / B;
   const uint16_t* wide = P.wide;
-  const uint16_t* narrow = P.narrow;
   const int col0 = ct * kNmCols;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -451,9 +461,15 @@ narrow_wide_mfma_kernel(const NmTable tab) {
   const int nsteps = (n + kNmK - 1) / kNmK;
 
   // Example b's operands; a transfer at or past the example's end (rows >= T)
-  // reads zeros.
+  // reads zeros, and so does every transfer of an absent slot (size 0).
   const u32x4_t wrsrc = rsrc_words(wide + (size_t)b * T * nw, (uint32_t)T * nw * 2);
-  const u32x4_t nrsrc = rsrc_words(narrow + (size_t)b * T * ns, (uint32_t)T * ns * 2);
+  u32x4_t nrsrc[kSlots];
+#pragma unroll
+  for (int k = 0; k < kSlots; ++k) {
+    const int kk = k < nslots ? k : 0;
+    nrsrc[k] = rsrc_words(P.narrow[kk] + (size_t)b * T * P.ns[kk],
+                          k < nslots ? (uint32_t)T * P.ns[kk] * 2 : 0u);
+  }
   // Wide: wave w's transfer j fills the 1 KiB of tile rows 2 w + 16 j and the
   // next, lane i the 16 bytes at i * 16 -- row 2 w + 16 j + i / 32, physical
   // slot i % 32, which holds the 8 columns from tile_slot_col(row, i % 32).
@@ -463,19 +479,23 @@ narrow_wide_mfma_kernel(const NmTable tab) {
   const int dcol = min(col0 + tile_slot_col(drow, lane & 31), nw - 8);
   const uint32_t wvoff = (uint32_t)((t0 + drow) * nw + dcol) * 2u;
   const uint32_t wstep = (uint32_t)kNmK * nw * 2u, wrow16 = 16u * nw * 2u;
-  // Narrow: wave w's transfer i fills the 256 bytes at (w * kNarrowDma + i) *
-  // 256 of the narrow tile, lane l the dword at + 4 l: row r, physical dword
-  // p.  With 64-byte rows (NS = 32) the two 32-byte halves are swapped in rows
-  // with bit 2 set, so that a fragment read is free of bank conflicts.
-  uint32_t nvoff[kNarrowDma];
+  // Narrow slot k: wave w's transfer i fills the 256 bytes at (w * kNarrowDma
+  // + i) * 256 of the slot's tile, lane l the dword at + 4 l: row r, physical
+  // dword p.  With 64-byte rows (NS = 32) the two 32-byte halves are swapped
+  // in rows with bit 2 set, so that a fragment read is free of bank conflicts.
+  uint32_t nvoff[kSlots][kNarrowDma], nstep[kSlots];
 #pragma unroll
-  for (int i = 0; i < kNarrowDma; ++i) {
-    const int byte = (w * kNarrowDma + i) * 256 + 4 * lane;
-    const int r = byte / kRowN, p = (byte % kRowN) / 4;
-    const int d = (NS == 32) ? p ^ (((r >> 2) & 1) << 3) : p;
-    nvoff[i] = (2 * d < ns) ? (uint32_t)((t0 + r) * ns + 2 * d) * 2u : (uint32_t)kNwOutOfRange;
+  for (int k = 0; k < kSlots; ++k) {
+    const int ns = k < nslots ? P.ns[k] : 0;
+    nstep[k] = (uint32_t)kNmK * ns * 2u;
+#pragma unroll
+    for (int i = 0; i < kNarrowDma; ++i) {
+      const int byte = (w * kNarrowDma + i) * 256 + 4 * lane;
+      const int r = byte / kRowN, p = (byte % kRowN) / 4;
+      const int d = (NS == 32) ? p ^ (((r >> 2) & 1) << 3) : p;
+      nvoff[k][i] = (2 * d < ns) ? (uint32_t)((t0 + r) * ns + 2 * d) * 2u : (uint32_t)kNwOutOfRange;
+    }
   }
-  const uint32_t nstep = (uint32_t)kNmK * ns * 2u;
   const uint32_t lds0 = lds_addr(lds);
   auto dma_step = [&](int stage, int step) __attribute__((always_inline)) {
     const uint32_t base = lds0 + stage * kStage;
@@ -484,15 +504,19 @@ narrow_wide_mfma_kernel(const NmTable tab) {
     for (int j = 0; j < kNmWideDma; ++j)
       dma16(wrsrc, base + (w + kNmWaves * j) * 1024, (int)(wv + j * wrow16), 0);
 #pragma unroll
-    for (int i = 0; i < kNarrowDma; ++i) {
-      const uint32_t v = nvoff[i] + (uint32_t)step * nstep;
-      dma4(nrsrc, base + kNmWideBytes + (w * kNarrowDma + i) * 256, (int)v, 0);
-    }
+    for (int k = 0; k < kSlots; ++k)
+#pragma unroll
+      for (int i = 0; i < kNarrowDma; ++i) {
+        const uint32_t v = nvoff[k][i] + (uint32_t)step * nstep[k];
+        dma4(nrsrc[k], base + kNmWideBytes + k * kNarrowBytes + (w * kNarrowDma + i) * 256, (int)v,
+             0);
+      }
   };
 
   // Fragment offsets (sub-step 0, half 0): wide column blocks 32 w and
   // 32 w + 16 (the latter is the former XOR 32, tile_off), narrow row blocks
-  // 16 mb; half 1 is 16 rows further, sub-step 1 32 rows.
+  // 16 mb of slot k at + k * kNarrowBytes; half 1 is 16 rows further,
+  // sub-step 1 32 rows.
   const int boff = frag16_off(32 * w, 0, lane);
   int aoff[kMB];
   {
@@ -504,31 +528,39 @@ narrow_wide_mfma_kernel(const NmTable tab) {
       aoff[mb] = kNmWideBytes + k * kRowN + 4 * ((NS == 32) ? dw ^ ((q & 1) << 3) : dw);
     }
   }
-  f32x4_t acc[kMB][2];
+  f32x4_t acc[kSlots][kMB][2];
 #pragma unroll
-  for (int mb = 0; mb < kMB; ++mb)
+  for (int k = 0; k < kSlots; ++k)
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) acc[k][mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   auto compute = [&](int stage) __attribute__((always_inline)) {
     const uint8_t* st = lds + stage * kStage;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      bf16x8_t bf[2], af[kMB];
+      bf16x8_t bf[2];
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
         const int o = (boff ^ (32 * nb)) + kk * 32 * kTileRowBytes;
         bf[nb] = join_frag(read_tr(st, o), read_tr(st, o + 16 * kTileRowBytes));
       }
 #pragma unroll
-      for (int mb = 0; mb < kMB; ++mb) {
-        const int o = aoff[mb] + kk * 32 * kRowN;
-        af[mb] = join_frag(read_tr(st, o), read_tr(st, o + 16 * kRowN));
+      for (int k = 0; k < kSlots; ++k) {
+        if (k > 0 && k >= nslots) break;
+        bf16x8_t af[kMB];
+#pragma unroll
+        for (int mb = 0; mb < kMB; ++mb) {
+          const int o = aoff[mb] + k * kNarrowBytes + kk * 32 * kRowN;
+          af[mb] = join_frag(read_tr(st, o), read_tr(st, o + 16 * kRowN));
+        }
+#pragma unroll
+        for (int mb = 0; mb < kMB; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb)
+            acc[k][mb][nb] =
+                __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mb], bf[nb], acc[k][mb][nb], 0, 0, 0);
       }
-#pragma unroll
-      for (int mb = 0; mb < kMB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
-          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mb], bf[nb], acc[mb][nb], 0, 0, 0);
     }
   };
 
@@ -558,31 +590,36 @@ narrow_wide_mfma_kernel(const NmTable tab) {
     if (s + 3 < nsteps) iteration(s + 3, 3);
   }
 
-  // Lane l holds out[16 mb + 4 (l / 16) + e][32 w + 16 nb + l % 16].
+  // Lane l holds out_k[16 mb + 4 (l / 16) + e][32 w + 16 nb + l % 16].
 #pragma unroll
-  for (int mb = 0; mb < kMB; ++mb)
+  for (int k = 0; k < kSlots; ++k) {
+    if (k > 0 && k >= nslots) break;
+    const int ns = P.ns[k];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int col = col0 + 32 * w + 16 * nb + (lane & 15);
-      if (col >= nw) continue;
+    for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int s = 16 * mb + 4 * (lane >> 4) + e;
-        if (s >= ns) continue;
-        const float v = acc[mb][nb][e];
-        if (splits > 1) {
-          P.partial[(((size_t)split * B + b) * ns + s) * nw + col] = v;
-        } else {
-          const size_t o =
-              P.narrow_is_g ? ((size_t)b * ns + s) * nw + col : ((size_t)b * nw + col) * ns + s;
-          if (tab.out_bf16) {
-            reinterpret_cast<uint16_t*>(P.out)[o] = f32_to_bf16_bits(v);
+      for (int nb = 0; nb < 2; ++nb) {
+        const int col = col0 + 32 * w + 16 * nb + (lane & 15);
+        if (col >= nw) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int s = 16 * mb + 4 * (lane >> 4) + e;
+          if (s >= ns) continue;
+          const float v = acc[k][mb][nb][e];
+          if (splits > 1) {
+            P.partial[k][(((size_t)split * B + b) * ns + s) * nw + col] = v;
           } else {
-            reinterpret_cast<float*>(P.out)[o] = v;
+            const size_t o =
+                P.narrow_is_g ? ((size_t)b * ns + s) * nw + col : ((size_t)b * nw + col) * ns + s;
+            if (tab.out_bf16) {
+              reinterpret_cast<uint16_t*>(P.out[k])[o] = f32_to_bf16_bits(v);
+            } else {
+              reinterpret_cast<float*>(P.out[k])[o] = v;
+            }
           }
         }
       }
-    }
+  }
 }
 
 bool narrow_mfma_ok(int T, int nw, int ns) {
@@ -600,43 +637,56 @@ struct NmDesc {
   int din, dout;
 };
 
-// The table of one MFMA launch over problems d[idx[0 .. m)) (m <=
+// Problems of one MFMA launch entry: d[slot[0 .. n)) share the wide operand
+// (same pointer, width and side), so one pass over it serves all of them.
+struct NmGroup {
+  int slot[kNmMaxSlots];
+  int n;
+};
+
+inline bool nm_narrow_is_g(const NmDesc& q) { return q.dout <= q.din; }
+inline const void* nm_wide(const NmDesc& q) { return nm_narrow_is_g(q) ? q.A : q.G; }
+inline int nm_nw(const NmDesc& q) { return nm_narrow_is_g(q) ? q.din : q.dout; }
+inline int nm_ns(const NmDesc& q) { return nm_narrow_is_g(q) ? q.dout : q.din; }
+
+// The table of one MFMA launch over the groups g[0 .. m) (m <=
 // kNmMaxProblems, all with narrow widths in one NS class): token chunks of a
-// multiple of 64 tokens, as many splits of every problem as it takes for the
+// multiple of 64 tokens, as many splits of every group as it takes for the
 // launch to have a workgroup for every CU; a split problem's partials at ws +
 // its offset (ws may be null to size them).  Returns the launch's workgroups;
 // *ws_bytes receives the partials' bytes.
-int nm_table(NmTable& tab, const NmDesc* d, const int* idx, int m, int B, int T, int out_bf16,
+int nm_table(NmTable& tab, const NmDesc* d, const NmGroup* g, int m, int B, int T, int out_bf16,
              char* ws, size_t* ws_bytes) {
   long long base = 0;
-  for (int i = 0; i < m; ++i) {
-    const NmDesc& q = d[idx[i]];
-    base += (long long)ceil_div(q.dout <= q.din ? q.din : q.dout, kNmCols) * B;
-  }
+  for (int i = 0; i < m; ++i) base += (long long)ceil_div(nm_nw(d[g[i].slot[0]]), kNmCols) * B;
   const int want = (int)std::max<long long>(1, (256 + base - 1) / base);
   const int chunk = ceil_div(ceil_div(T, want), kNmK) * kNmK;
   const int splits = ceil_div(T, chunk);
   size_t off = 0;
   long long wg = 0;
   for (int i = 0; i < m; ++i) {
-    const NmDesc& q = d[idx[i]];
+    const NmDesc& q0 = d[g[i].slot[0]];
     NmProblem& P = tab.p[i];
-    P.narrow_is_g = q.dout <= q.din;
-    P.ns = P.narrow_is_g ? q.dout : q.din;
-    P.nw = P.narrow_is_g ? q.din : q.dout;
-    P.wide = (const uint16_t*)(P.narrow_is_g ? q.A : q.G);
-    P.narrow = (const uint16_t*)(P.narrow_is_g ? q.G : q.A);
-    P.out = q.out;
+    P.narrow_is_g = nm_narrow_is_g(q0);
+    P.nw = nm_nw(q0);
+    P.wide = (const uint16_t*)nm_wide(q0);
+    P.nslots = g[i].n;
+    for (int k = 0; k < kNmMaxSlots; ++k) {
+      const NmDesc& q = d[g[i].slot[k < g[i].n ? k : 0]];
+      P.ns[k] = nm_ns(q);
+      P.narrow[k] = (const uint16_t*)(P.narrow_is_g ? q.G : q.A);
+      P.out[k] = q.out;
+      P.partial[k] = nullptr;
+      if (k < g[i].n && splits > 1) {
+        P.partial[k] = ws ? (float*)(ws + off) : nullptr;
+        off = align256(off + (size_t)splits * B * P.ns[k] * P.nw * sizeof(float));
+      }
+    }
     P.col_tiles = ceil_div(P.nw, kNmCols);
     P.splits = splits;
     P.chunk = chunk;
     P.wg_start = (int)wg;
     wg += (long long)P.col_tiles * B * splits;
-    P.partial = nullptr;
-    if (splits > 1) {
-      P.partial = ws ? (float*)(ws + off) : nullptr;
-      off = align256(off + (size_t)splits * B * P.ns * P.nw * sizeof(float));
-    }
   }
   tab.n = m;
   tab.B = B;
@@ -646,49 +696,77 @@ int nm_table(NmTable& tab, const NmDesc* d, const int* idx, int m, int B, int T,
   return wg > 0x7fffffffLL ? -1 : (int)wg;
 }
 
-// The MFMA launches of the eligible problems d[idx[0 .. m)): one per NS
-// class and run of up to kNmMaxProblems problems, each followed by the
-// finish kernels of its split problems (so launches reuse the workspace).
-// With launch false only sizes the workspace (the largest launch's partials).
+// The MFMA launches of the eligible problems d[idx[0 .. m)): problems of
+// narrow width <= 16 that share a wide operand are merged, up to kNmMaxSlots
+// to a group; one launch per NS class and run of up to kNmMaxProblems groups,
+// each followed by the finish kernels of its split problems (so launches
+// reuse the workspace).  With launch false only sizes the workspace, without
+// the operand pointers (so without the grouping): a bound on every launch's
+// partials -- a problem's token splits grow as its launch's workgroup count
+// shrinks, and that count is at least the problem's own column tiles times
+// B, so the sum of the problems' partials at that many splits covers any
+// launch (for a single problem it is exact).
 int nm_run(const NmDesc* d, const int* idx, int m, int B, int T, int out_bf16, void* ws,
            size_t ws_bytes, hipStream_t s, bool launch, size_t* ws_need) {
   size_t need = 0;
+  if (!launch) {
+    for (int i = 0; i < m; ++i) {
+      const NmDesc& q = d[idx[i]];
+      const int own = ceil_div(nm_nw(q), kNmCols) * B;
+      const int want = std::max(1, ceil_div(256, own));
+      const int splits = ceil_div(T, ceil_div(ceil_div(T, want), kNmK) * kNmK);
+      if (splits > 1) need = align256(need + (size_t)splits * B * nm_ns(q) * nm_nw(q) * sizeof(float));
+    }
+    *ws_need = need;
+    return DPC_OK;
+  }
   for (int cls = 0; cls < 2; ++cls) {
-    int sel[kNmMaxProblems];
-    int k = 0;
-    for (int i = 0; i <= m; ++i) {
-      if (i < m) {
-        const NmDesc& q = d[idx[i]];
-        const int ns = q.dout <= q.din ? q.dout : q.din;
-        if ((ns > 16) != (cls == 1)) continue;
-        sel[k++] = idx[i];
+    const int max_slots = cls == 0 ? kNmMaxSlots : 1;
+    std::vector<NmGroup> groups;
+    for (int i = 0; i < m; ++i) {
+      const NmDesc& q = d[idx[i]];
+      if ((nm_ns(q) > 16) != (cls == 1)) continue;
+      bool merged = false;
+      for (NmGroup& grp : groups) {
+        const NmDesc& q0 = d[grp.slot[0]];
+        if (grp.n < max_slots && nm_wide(q0) == nm_wide(q) && nm_nw(q0) == nm_nw(q) &&
+            nm_narrow_is_g(q0) == nm_narrow_is_g(q)) {
+          grp.slot[grp.n++] = idx[i];
+          merged = true;
+          break;
+        }
       }
-      if (k == 0 || (k < kNmMaxProblems && i < m)) continue;
+      if (!merged) groups.push_back(NmGroup{{idx[i], idx[i], idx[i]}, 1});
+    }
+    for (size_t g0 = 0; g0 < groups.size(); g0 += kNmMaxProblems) {
+      const int k = (int)std::min<size_t>(kNmMaxProblems, groups.size() - g0);
       NmTable tab;
       size_t part = 0;
-      const int wgs = nm_table(tab, d, sel, k, B, T, out_bf16, (char*)ws, &part);
+      const int wgs = nm_table(tab, d, groups.data() + g0, k, B, T, out_bf16, (char*)ws, &part);
       if (wgs < 0) return DPC_ENOTSUP;
       need = std::max(need, part);
-      if (launch && wgs > 0) {
-        if (part > ws_bytes || (part > 0 && !ws)) return DPC_ENOSPC;
-        if (cls == 0) {
-          hipLaunchKernelGGL(narrow_wide_mfma_kernel<16>, dim3(wgs), dim3(kNmThreads), 0, s, tab);
-        } else {
-          hipLaunchKernelGGL(narrow_wide_mfma_kernel<32>, dim3(wgs), dim3(kNmThreads), 0, s, tab);
-        }
-        DPC_HIP_CHECK(hipGetLastError());
-        for (int j = 0; j < k; ++j) {
-          const NmProblem& P = tab.p[j];
-          if (P.splits <= 1) continue;
-          const size_t total = (size_t)B * P.ns * P.nw;
+      if (!launch || wgs == 0) continue;
+      if (part > ws_bytes || (part > 0 && !ws)) return DPC_ENOSPC;
+      if (cls == 0) {
+        hipLaunchKernelGGL((narrow_wide_mfma_kernel<16, kNmMaxSlots>), dim3(wgs), dim3(kNmThreads),
+                           0, s, tab);
+      } else {
+        hipLaunchKernelGGL((narrow_wide_mfma_kernel<32, 1>), dim3(wgs), dim3(kNmThreads), 0, s,
+                           tab);
+      }
+      DPC_HIP_CHECK(hipGetLastError());
+      for (int j = 0; j < k; ++j) {
+        const NmProblem& P = tab.p[j];
+        if (P.splits <= 1) continue;
+        for (int sl = 0; sl < P.nslots; ++sl) {
+          const size_t total = (size_t)B * P.ns[sl] * P.nw;
           hipLaunchKernelGGL(narrow_finish_kernel,
                              dim3((unsigned)((total + kDirThreads - 1) / kDirThreads)),
-                             dim3(kDirThreads), 0, s, (const float*)P.partial, P.splits, B, P.nw,
-                             P.ns, P.narrow_is_g, out_bf16, P.out);
+                             dim3(kDirThreads), 0, s, (const float*)P.partial[sl], P.splits, B,
+                             P.nw, P.ns[sl], P.narrow_is_g, out_bf16, P.out[sl]);
           DPC_HIP_CHECK(hipGetLastError());
         }
       }
-      k = 0;
     }
   }
   *ws_need = need;

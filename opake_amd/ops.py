@@ -549,8 +549,17 @@ def per_example_grads_grouped(A_list, G_list, *,
     outs = [torch.empty((B, o, i), dtype=out_dtype, device=dev) for i, o in zip(dins, douts)]
     if B == 0:
         return outs
-    As = [_aligned(A) for A in A_list]
-    Gs = [_aligned(G) for G in G_list]
+    # A tensor passed for several layers stays one buffer (layers that share
+    # their wide operand share the kernel's pass over it).
+    seen = {}
+
+    def once(t):
+        if id(t) not in seen:
+            seen[id(t)] = _aligned(t)
+        return seen[id(t)]
+
+    As = [once(A) for A in A_list]
+    Gs = [once(G) for G in G_list]
     c_din = (ctypes.c_int * n)(*dins)
     c_dout = (ctypes.c_int * n)(*douts)
     ws_bytes = nat.load().dpc_per_example_grads_grouped_workspace_bytes(

@@ -63,7 +63,7 @@ def test_per_example_grads_match_oracle(dev, dtype, B, T, din, dout):
 
 
 # The grouped call: every problem as the oracle has it, whatever launch it
-# lands in -- 37 bfloat16 problems (two MFMA launches of up to 32 in the
+# lands in -- 37 bfloat16 problems (two MFMA launches of up to 24 in the
 # 16-column class, one in the 32-column class; narrow side the input or the
 # output), problems the MFMA kernel does not take (wide side % 8 != 0, an odd
 # narrow side) run one by one, and the same set in float32 (none in MFMA
@@ -86,6 +86,40 @@ def test_per_example_grads_grouped_match_oracle(dev, dtype, T):
         assert got[k].shape == want.shape, k
         assert _rel(got[k], want) < 1e-5, k
         assert torch.equal(got_bf[k].cpu(), got[k].cpu().to(torch.bfloat16)), k
+
+
+# Problems that share their wide operand (the same tensor) run as one group of
+# the MFMA launch, up to three to a group: five narrow-output problems on one
+# input x (widths 16, 2, 8, 14, 6: a group of three, then one of two), two
+# narrow-input problems on one output gradient y, a problem whose wide side
+# is x but as its output gradient (another output layout: not merged with
+# x's), and one of narrow width 24 on x (the 32-column class: a launch of its
+# own).  T = 300 splits the tokens, T = 2048 (B = 4) writes directly.
+@pytest.mark.parametrize("B,T", [(2, 300), (4, 2048)])
+def test_per_example_grads_grouped_shared_wide(dev, B, T):
+    g = torch.Generator().manual_seed(T + B)
+    bf = torch.bfloat16
+    x = torch.randn(B, T, 1032, generator=g).to(bf)
+    y = torch.randn(B, T, 520, generator=g).to(bf)
+    narrow = {w: torch.randn(B, T, w, generator=g).to(bf) for w in (16, 2, 8, 14, 6, 12, 4, 24)}
+    pairs = [(x, narrow[16]), (x, narrow[2]), (narrow[12], y), (x, narrow[8]),
+             (narrow[4], x), (x, narrow[14]), (narrow[6], y), (x, narrow[6]), (x, narrow[24])]
+    xd, yd = x.to(dev), y.to(dev)
+    nd = {w: t.to(dev) for w, t in narrow.items()}
+
+    def on_dev(t):
+        return xd if t is x else yd if t is y else nd[t.shape[-1]]
+
+    for out_dtype in (torch.float32, torch.bfloat16):
+        got = ops.per_example_grads_grouped([on_dev(a) for a, _ in pairs],
+                                            [on_dev(o) for _, o in pairs], out_dtype=out_dtype)
+        for k, (a, o) in enumerate(pairs):
+            want = ghost_oracle.linear_per_example_grads(a, o, dtype=torch.float64)[0]
+            assert got[k].shape == want.shape, k
+            if out_dtype == torch.float32:
+                assert _rel(got[k], want) < 1e-5, k
+            else:
+                assert _rel(got[k], want) < 1e-2, k
 
 
 def _case(dtype, seed=0):
