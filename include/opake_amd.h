@@ -169,6 +169,25 @@ int dpc_clipped_sum(const void* A, const void* G, const float* scale, const void
                     void* bias_out, void* ws, size_t ws_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * dpc_clipped_sum over several bias-free linear layers of one clipping group
+ * (the same examples, scale and plan): the reference's apply pass visits the
+ * leaves one by one (_streaming.py:137-167, with the per-leaf noise of
+ * _gaussian.py:188-229); here layer i gets exactly
+ *   dpc_clipped_sum(A[i], G[i], scale, plan, B, T, din[i], dout[i], dtype,
+ *                   normalize_by, noise_mode, noise ? noise[i] : NULL, NULL,
+ *                   seed, leaf_ids ? leaf_ids[i] : 0, 0, sigmas[i], out_dtype,
+ *                   out[i], 0, NULL, NULL, 0, stream)
+ * (one pass, no split-K), and when every layer takes the bf16 MFMA path the
+ * layers share launches (up to 8 layers each): the output tiles of all of
+ * them fill the chip together instead of one layer at a time.
+ * -------------------------------------------------------------------------*/
+int dpc_clipped_sum_multi(int n, const void* const* A, const void* const* G, const int* din,
+                          const int* dout, const float* scale, const void* plan, int B, int T,
+                          int dtype, double normalize_by, int noise_mode,
+                          const float* const* noise, uint64_t seed, const uint32_t* leaf_ids,
+                          const double* sigmas, int out_dtype, void* const* out, void* stream);
+
+/* ------------------------------------------------------------------------
  * Gaussian noise on an arbitrary leaf (out-of-place).
  *
  * Replaces `_sample` of _gaussian.py:188-204:

@@ -509,6 +509,7 @@ def ghost_clip_captured(
         return t.pin_memory().to(device, non_blocking=True)
 
     tree = {}
+    multi = {}
     for L in dense:
         si = storage.index(L.A.dtype)
         cf = cfs[L.group]
@@ -527,15 +528,37 @@ def ghost_clip_captured(
             else:
                 spec = ops.NoiseSpec(sigma=s_w, mode=nat.NOISE_PHILOX, seed=step_key.seed,
                                      leaf_id=leaf_index[wn], bias_leaf_id=leaf_index.get(bn, 0))
-        ev = _event_pair(gemm_events)
-        w, b = ops.clipped_sum(L.A, L.G, cf.scale[si], plan=cf.plan[si],
-                               normalize_by=normalize_by, noise=spec,
-                               out_dtype=dtype or L.cap.param_dtype or L.A.dtype,
-                               with_bias=L.cap.has_bias)
-        _close_pair(ev)
-        tree[wn] = w
+        out_dtype = dtype or L.cap.param_dtype or L.A.dtype
         if L.cap.has_bias:
+            ev = _event_pair(gemm_events)
+            w, b = ops.clipped_sum(L.A, L.G, cf.scale[si], plan=cf.plan[si],
+                                   normalize_by=normalize_by, noise=spec, out_dtype=out_dtype,
+                                   with_bias=True)
+            _close_pair(ev)
+            tree[wn] = w
             tree[bn] = b
+            continue
+        # Bias-free layers of one clipping group, operand dtype, output dtype
+        # and noise kind go out together (their output tiles share launches).
+        kind = (spec.mode, spec.seed) if spec is not None else None
+        multi.setdefault((L.group, si, L.A.dtype, out_dtype, kind), []).append((L, wn, spec))
+    for (g, si, _, out_dtype, _), members in multi.items():
+        cf = cfs[g]
+        ev = _event_pair(gemm_events)
+        if len(members) == 1:
+            L, wn, spec = members[0]
+            outs = [ops.clipped_sum(L.A, L.G, cf.scale[si], plan=cf.plan[si],
+                                    normalize_by=normalize_by, noise=spec,
+                                    out_dtype=out_dtype)[0]]
+        else:
+            outs = ops.clipped_sum_multi([L.A for L, _, _ in members],
+                                         [L.G for L, _, _ in members], cf.scale[si],
+                                         plan=cf.plan[si], normalize_by=normalize_by,
+                                         noises=[sp for _, _, sp in members],
+                                         out_dtype=out_dtype)
+        _close_pair(ev)
+        for (_, wn, _), w in zip(members, outs):
+            tree[wn] = w
     for members, layout in bucket_layouts:
         si = storage.index(members[0].A.dtype)
         seg_scale = torch.stack([cfs[L.group].scale[si] for L in members])

@@ -302,6 +302,22 @@ struct GroupedTables {
   int E;
 };
 
+// Dense multi-layer mode: layers that share the examples, the clip plan and
+// the scales (one clipping group) in one launch -- layer p takes workgroups
+// tile_start .. tile_start + its tiles - 1, with its own operands, shape,
+// output and noise leaf.
+constexpr int kMaxDense = 8;
+struct DenseProblem {
+  const uint16_t* A;  // [B * T, N]
+  const uint16_t* G;  // [B * T, M]
+  void* out;
+  const float* noise;  // injected noise [M, N] (or null)
+  int M, N, tile_start;
+  uint32_t leaf;
+  float sigma;
+  int pad;
+};
+
 struct FastArgs {
   const uint16_t* A;  // [B * T, N] (dense mode)
   const uint16_t* G;  // [B * T, M]
@@ -316,6 +332,10 @@ struct FastArgs {
   // reduce kernel adds the splits in order and applies the epilogue.
   int splits;
   float* partial;
+  // Dense multi-layer mode when nprob > 0 (splits is then 1; A, G and the
+  // per-layer fields of ep are taken from dp).
+  int nprob;
+  DenseProblem dp[kMaxDense];
 };
 
 // LDS of the fast kernel: each stage's G tile and A tile in an array of its
@@ -352,9 +372,34 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_g1[kOperandBytes];
   __shared__ __attribute__((aligned(16))) uint8_t lds_a0[kOperandBytes];
   __shared__ __attribute__((aligned(16))) uint8_t lds_a1[kOperandBytes];
-  const int M = args.ep.M, N = args.ep.N, T = args.T;
-  const int tiles_m = ceil_div(M, kBM), tiles_n = ceil_div(N, kBN);
+  int M = args.ep.M, N = args.ep.N;
+  const int T = args.T;
   int lin = xcd_linear_id(gridDim.x);
+  Epilogue ep = args.ep;
+  const uint16_t* Abase = args.A;
+  const uint16_t* Gbase = args.G;
+  if constexpr (!kGrouped) {
+    if (args.nprob > 0) {
+      // The layer of this workgroup (uniform, in scalar registers).
+      int p = 0;
+      for (int i = 1; i < args.nprob; ++i)
+        if (lin >= args.dp[i].tile_start) p = i;
+      p = __builtin_amdgcn_readfirstlane(p);
+      const DenseProblem& P = args.dp[p];
+      lin -= P.tile_start;
+      M = P.M;
+      N = P.N;
+      Abase = P.A;
+      Gbase = P.G;
+      ep.M = M;
+      ep.N = N;
+      ep.out = P.out;
+      ep.noise = P.noise;
+      ep.leaf = P.leaf;
+      ep.sigma = P.sigma;
+    }
+  }
+  const int tiles_m = ceil_div(M, kBM), tiles_n = ceil_div(N, kBN);
   int grp = 0, split = 0;
   // The quotients are workgroup-uniform, but the compiler's integer division
   // leaves them in vector registers: read them into scalar ones.
@@ -373,9 +418,6 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = w / kWavesN, wn = w % kWavesN;  // wave tile: rows wm * 128, columns wn * kWC
 
-  Epilogue ep = args.ep;
-  const uint16_t* Abase = args.A;
-  const uint16_t* Gbase = args.G;
   int total_rows, nsteps, step0 = 0, nactive = 0, nfast = 0, step_base = 0;
   const int spe = T / kBK;
   ClipPlanView plan = clip_plan_view(const_cast<void*>(args.plan), args.B);
@@ -1375,6 +1417,7 @@ extern "C" int dpc_grouped_clipped_sum(const int64_t* a_ptrs, const int64_t* g_p
     FastArgs args;
     args.A = nullptr;
     args.G = nullptr;
+    args.nprob = 0;
     args.T = 0;
     args.B = 0;
     args.plan = nullptr;
@@ -1461,6 +1504,7 @@ extern "C" int dpc_clipped_sum(const void* A, const void* G, const float* scale,
     FastArgs args;
     args.A = (const uint16_t*)A;
     args.G = (const uint16_t*)G;
+    args.nprob = 0;
     args.T = T;
     args.B = B;
     args.plan = plan;
@@ -1527,6 +1571,90 @@ extern "C" int dpc_clipped_sum(const void* A, const void* G, const float* scale,
     eb.out = bias_out;
     hipLaunchKernelGGL(bias_finish_kernel, dim3(ceil_div(ceil_div(dout, 2), kThreads)),
                        dim3(kThreads), 0, s, (const float*)partial, B > 0 ? nsplit : 0, eb);
+    DPC_HIP_CHECK(hipGetLastError());
+  }
+  return DPC_OK;
+}
+
+extern "C" int dpc_clipped_sum_multi(int n, const void* const* A, const void* const* G,
+                                     const int* din, const int* dout, const float* scale,
+                                     const void* plan, int B, int T, int dtype,
+                                     double normalize_by, int noise_mode,
+                                     const float* const* noise, uint64_t seed,
+                                     const uint32_t* leaf_ids, const double* sigmas,
+                                     int out_dtype, void* const* out, void* stream) {
+  if (n < 0 || B < 0 || T <= 0) return DPC_EINVAL;
+  if (n == 0) return DPC_OK;
+  if (!A || !G || !din || !dout || !out || !sigmas) return DPC_EINVAL;
+  if (dtype != DPC_F32 && dtype != DPC_BF16) return DPC_EINVAL;
+  if (out_dtype != DPC_F32 && out_dtype != DPC_BF16) return DPC_EINVAL;
+  if (!(normalize_by > 0.0)) return DPC_EINVAL;
+  if (noise_mode < DPC_NOISE_NONE || noise_mode > DPC_NOISE_PHILOX) return DPC_EINVAL;
+  if (B > 65535) return DPC_ENOTSUP;
+  bool fast = plan != nullptr && B > 0;
+  for (int i = 0; i < n; ++i) {
+    if (din[i] <= 0 || dout[i] <= 0 || !out[i]) return DPC_EINVAL;
+    if (B > 0 && (!A[i] || !G[i] || !scale)) return DPC_EINVAL;
+    if (!(sigmas[i] >= 0.0)) return DPC_EINVAL;
+    if (sigmas[i] != 0.0 && noise_mode == DPC_NOISE_NONE) return DPC_EINVAL;
+    if (sigmas[i] != 0.0 && noise_mode == DPC_NOISE_INJECTED && (!noise || !noise[i]))
+      return DPC_EINVAL;
+    fast = fast && fast_shape(B, T, din[i], dout[i], dtype);
+  }
+  hipStream_t s = (hipStream_t)stream;
+  if (!fast) {
+    // Layer by layer, each exactly as its own call without a workspace.
+    for (int i = 0; i < n; ++i) {
+      const int r = dpc_clipped_sum(A[i], G[i], scale, plan, B, T, din[i], dout[i], dtype,
+                                    normalize_by, noise_mode, noise ? noise[i] : nullptr, nullptr,
+                                    seed, leaf_ids ? leaf_ids[i] : 0u, 0u, sigmas[i], out_dtype,
+                                    out[i], 0, nullptr, nullptr, 0, stream);
+      if (r != DPC_OK) return r;
+    }
+    return DPC_OK;
+  }
+  for (int i0 = 0; i0 < n; i0 += kMaxDense) {
+    const int m = n - i0 < kMaxDense ? n - i0 : kMaxDense;
+    FastArgs args;
+    args.A = nullptr;
+    args.G = nullptr;
+    args.T = T;
+    args.B = B;
+    args.plan = plan;
+    args.scale = scale;
+    args.splits = 1;
+    args.partial = nullptr;
+    args.nprob = m;
+    Epilogue& ep = args.ep;
+    ep.M = 0;
+    ep.N = 0;
+    ep.nb = (float)normalize_by;
+    ep.apply_nb = normalize_by != 1.0;
+    ep.noise_mode = noise_mode;
+    ep.noise = nullptr;
+    ep.seed = seed;
+    ep.leaf = 0;
+    ep.sigma = 0.0f;
+    ep.out_bf16 = out_dtype == DPC_BF16;
+    ep.out = nullptr;
+    long long tiles = 0;
+    for (int k = 0; k < m; ++k) {
+      const int i = i0 + k;
+      DenseProblem& P = args.dp[k];
+      P.A = (const uint16_t*)A[i];
+      P.G = (const uint16_t*)G[i];
+      P.out = out[i];
+      P.noise = sigmas[i] != 0.0 && noise_mode == DPC_NOISE_INJECTED ? noise[i] : nullptr;
+      P.M = dout[i];
+      P.N = din[i];
+      P.tile_start = (int)tiles;
+      P.leaf = leaf_ids ? leaf_ids[i] : 0u;
+      P.sigma = noise_mode == DPC_NOISE_NONE ? 0.0f : (float)sigmas[i];
+      P.pad = 0;
+      tiles += (long long)ceil_div(dout[i], kBM) * ceil_div(din[i], kBN);
+    }
+    if (tiles > 0x7fffffffLL) return DPC_ENOTSUP;
+    launch_fast<false>(dim3((unsigned)tiles), s, args);
     DPC_HIP_CHECK(hipGetLastError());
   }
   return DPC_OK;

@@ -230,6 +230,81 @@ def clipped_sum(
     return out, bias_out
 
 
+def clipped_sum_multi(
+    A_list,
+    G_list,
+    scale: torch.Tensor,
+    *,
+    plan: torch.Tensor | None = None,
+    normalize_by: float = 1.0,
+    noises: list[NoiseSpec | None] | None = None,
+    out_dtype: torch.dtype | None = None,
+) -> list[torch.Tensor]:
+    """``clipped_sum`` of several bias-free layers of one clipping group (the
+    same examples, ``scale`` and ``plan``) -- ``dpc_clipped_sum_multi``: on the
+    bf16 MFMA path the layers' output tiles share launches.  ``noises[i]``:
+    layer i's noise (None: none); the specs must share one mode and seed.
+    Returns one [dout, din] tensor per layer.  When every layer takes the
+    MFMA path (bf16, T % 64 == 0, widths % 8 == 0, a plan) each result equals
+    its own ``clipped_sum`` call without a split-K workspace; otherwise the
+    layers run as their own ``clipped_sum`` calls."""
+    n = len(A_list)
+    if n == 0 or len(G_list) != n:
+        raise ConfigurationError("expected matching, non-empty lists of A and G")
+    dev = nat.require_device(*A_list, *G_list, scale, plan)
+    dtype = A_list[0].dtype
+    B, T = A_list[0].shape[:2]
+    for A, G in zip(A_list, G_list):
+        if A.dim() != 3 or G.dim() != 3 or A.shape[:2] != (B, T) or G.shape[:2] != (B, T):
+            raise ConfigurationError("expected A [B, T, din], G [B, T, dout] with one B and T")
+        if A.dtype != dtype or G.dtype != dtype:
+            raise ConfigurationError("the layers' operands must share one dtype")
+    if scale.dtype != torch.float32 or scale.numel() < B:
+        raise ConfigurationError("scale must be float32 with B entries")
+    noises = list(noises) if noises is not None else [None] * n
+    if len(noises) != n:
+        raise ConfigurationError("expected one noise spec (or None) per layer")
+    live = [sp for sp in noises if sp is not None and sp.sigma != 0.0]
+    mode = live[0].mode if live else nat.NOISE_NONE
+    seed = live[0].seed if live else 0
+    if any(sp.mode != mode or sp.seed != seed or sp.bias_noise is not None for sp in live):
+        raise ConfigurationError("the layers' noise specs must share one mode and seed, no bias")
+    out_dtype = out_dtype or dtype
+    mfma = plan is not None and B > 0 and dtype == torch.bfloat16 and T % 64 == 0 and all(
+        A.shape[2] % 8 == 0 and G.shape[2] % 8 == 0
+        and B * T * max(A.shape[2], G.shape[2]) * 2 < 2 ** 31 for A, G in zip(A_list, G_list))
+    if not mfma:
+        return [clipped_sum(A, G, scale, plan=plan, normalize_by=normalize_by, noise=sp,
+                            out_dtype=out_dtype)[0] for A, G, sp in zip(A_list, G_list, noises)]
+    As = [_contig(A) for A in A_list]
+    Gs = [_contig(G) for G in G_list]
+    dins = [A.shape[2] for A in As]
+    douts = [G.shape[2] for G in Gs]
+    outs = [torch.empty((o, i), dtype=out_dtype, device=dev) for i, o in zip(dins, douts)]
+    sig = [sp.sigma if sp is not None else 0.0 for sp in noises]
+    zs = []
+    for sp, o, i in zip(noises, douts, dins):
+        z = None
+        if sp is not None and sp.sigma != 0.0 and mode == nat.NOISE_INJECTED:
+            z = sp.noise
+            if z is None or z.dtype != torch.float32 or tuple(z.shape) != (o, i) or not z.is_cuda:
+                raise ConfigurationError(f"injected noise must be float32 {(o, i)} on the device")
+            z = _contig(z)
+        zs.append(z)
+    vp = ctypes.c_void_p * n
+    nat.call(
+        "dpc_clipped_sum_multi", n, vp(*[t.data_ptr() for t in As]), vp(*[t.data_ptr() for t in Gs]),
+        (ctypes.c_int * n)(*dins), (ctypes.c_int * n)(*douts), nat.ptr(_contig(scale)),
+        nat.ptr(plan), B, T, nat.dtype_code(dtype), float(normalize_by), mode,
+        vp(*[z.data_ptr() if z is not None else None for z in zs]), seed & ((1 << 64) - 1),
+        (ctypes.c_uint32 * n)(*[(sp.leaf_id if sp is not None else 0) & 0xFFFFFFFF
+                                for sp in noises]),
+        (ctypes.c_double * n)(*sig), nat.dtype_code(out_dtype),
+        vp(*[t.data_ptr() for t in outs]), nat.stream_handle(dev),
+    )
+    return outs
+
+
 _GRAM_TILE = 128  # rows of a Gram tile of the grouped norm kernel
 _GRAM_REC_WORDS = 12  # float64 words of a Gram work item's record
 _STEP_ROWS = 64  # rows of a K step of the grouped clipped sum
@@ -655,6 +730,7 @@ __all__ = [
     "add_noise",
     "clip_factors",
     "clipped_sum",
+    "clipped_sum_multi",
     "flat_sqnorms",
     "gram_sqnorms",
     "grouped_clipped_sum",

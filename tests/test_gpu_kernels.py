@@ -257,6 +257,74 @@ def test_clipped_sum_accumulator_scaling_is_near_exact(dev):
     assert _rel_err(w.cpu(), exact) < 1e-5
 
 
+def _multi_case(dev, dims, B, T, seed, slow=False):
+    g = _gen(seed)
+    As = [torch.randn(B, T, din, generator=g).to(torch.bfloat16) for din, _ in dims]
+    Gs = []
+    for _, dout in dims:
+        G = torch.randn(B, T, dout, generator=g) * 0.01 * torch.exp(torch.randn(B, 1, 1, generator=g))
+        if slow:
+            # Example 1's norm ~6e20 (scale below 2^-64: the plan's slow
+            # slots) with its Gram entries (~5e36) still finite in fp32.
+            G[1] = torch.randn(T, dout, generator=g) * 1e17
+        Gs.append(G.to(torch.bfloat16))
+    As_d, Gs_d = [a.to(dev) for a in As], [x.to(dev) for x in Gs]
+    sq = torch.zeros(B, dtype=torch.float64, device=dev)
+    err = torch.zeros(B, dtype=torch.float64, device=dev)
+    for a, x in zip(As_d, Gs_d):
+        ops.gram_sqnorms(a, x, out=sq, err=err)
+    from opake_amd.clipping import guard_for_linear
+    guard = guard_for_linear(torch.bfloat16, max(d for d, _ in dims), max(o for _, o in dims), False)
+    cf = ops.clip_factors(sq, num.conservative_bound(1.0), [guard], err=err,
+                          count_threshold=num.float32_of(1.0))
+    return As, Gs, As_d, Gs_d, cf
+
+
+# Layers of one clipping group in shared launches (dpc_clipped_sum_multi):
+# mixed shapes -- one output tile (8 x 8), partial tiles (264, 136, 520
+# rows), several tiles -- and 11 layers (two launches of up to 8).  Each
+# layer equals its own one-layer launch bit for bit (float32 output; bfloat16
+# with / normalize_by and Philox noise, whose values depend only on the
+# layer's leaf id), and the exact float64 clipped sum with the device's
+# scales to 1e-5; with an example on the plan's slow slots the oracle's
+# clipped sum to 2e-2 (its G is scaled and rounded to bf16 first).
+@pytest.mark.parametrize("case", ["mixed", "eleven", "noise_bf16", "slow"])
+def test_clipped_sum_multi_matches_single_layers(dev, case):
+    B, T = 3, 128
+    if case == "eleven":
+        dims = [(64 + 32 * i, 8 + 64 * (i % 4)) for i in range(11)]
+    else:
+        dims = [(256, 264), (320, 136), (64, 520), (512, 256), (8, 8)]
+    As, Gs, As_d, Gs_d, cf = _multi_case(dev, dims, B, T, 100 + len(case), slow=case == "slow")
+    nplan = cf.plan[0].cpu().view(torch.int32)
+    assert int(nplan[1]) == (B - 1 if case == "slow" else B)  # fast examples
+    kw = dict(plan=cf.plan[0], out_dtype=torch.float32)
+    noises = None
+    if case == "noise_bf16":
+        kw = dict(plan=cf.plan[0], out_dtype=torch.bfloat16, normalize_by=2.0)
+        noises = [ops.NoiseSpec(sigma=0.5 + 0.1 * i, mode=nat.NOISE_PHILOX, seed=77, leaf_id=3 * i)
+                  for i in range(len(dims))]
+        noises[1] = None  # a layer without noise among noisy ones
+    got = ops.clipped_sum_multi(As_d, Gs_d, cf.scale[0], noises=noises, **kw)
+    for i in range(len(dims)):
+        one = ops.clipped_sum_multi([As_d[i]], [Gs_d[i]], cf.scale[0],
+                                    noises=None if noises is None else [noises[i]], **kw)[0]
+        assert got[i].shape == (dims[i][1], dims[i][0])
+        assert torch.equal(got[i], one), i
+    scale = cf.scale[0].cpu().double()
+    for i in range(len(dims)):
+        if case == "noise_bf16":
+            break
+        if case == "slow":
+            leaves = [ghost_oracle.linear_per_example_grads(a, x)[0] for a, x in zip(As, Gs)]
+            res = clip_oracle.stream_clip_and_sum(leaves, clip_oracle.conservative_bound(1.0),
+                                                  reduce_dtype={torch.bfloat16: torch.float32})
+            assert _rel_err(got[i].cpu(), res.reduced[i]) < 2e-2, i
+        else:
+            exact = torch.einsum("b,btm,btn->mn", scale, Gs[i].double(), As[i].double())
+            assert _rel_err(got[i].cpu(), exact) < 1e-5, i
+
+
 @pytest.mark.parametrize("case", ["tiny_scale", "large_bc"])
 def test_clipped_sum_slow_plan_slots(dev, case):
     """Examples the GEMM cannot divide its accumulators by -- a scale below
