@@ -68,6 +68,19 @@ DPC_HOST_DEVICE void philox_mulhilo(uint32_t a, uint32_t b, uint32_t* hi, uint32
   *lo = (uint32_t)p;
 }
 
+// a ^ b ^ c; on the device one v_bitop3_b32 (gfx950's three-input bitwise
+// operation, truth table 0x96 = odd parity), where the compiler emits two
+// XORs.
+DPC_HOST_DEVICE uint32_t xor3_u32(uint32_t a, uint32_t b, uint32_t c) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  uint32_t r;
+  asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x96" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+#else
+  return a ^ b ^ c;
+#endif
+}
+
 DPC_HOST_DEVICE Philox4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
                                       uint32_t k0, uint32_t k1) {
   const uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
@@ -77,9 +90,9 @@ DPC_HOST_DEVICE Philox4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uin
     uint32_t hi0, lo0, hi1, lo1;
     philox_mulhilo(M0, c0, &hi0, &lo0);
     philox_mulhilo(M1, c2, &hi1, &lo1);
-    uint32_t n0 = hi1 ^ c1 ^ k0;
+    uint32_t n0 = xor3_u32(hi1, c1, k0);
     uint32_t n1 = lo1;
-    uint32_t n2 = hi0 ^ c3 ^ k1;
+    uint32_t n2 = xor3_u32(hi0, c3, k1);
     uint32_t n3 = lo0;
     c0 = n0; c1 = n1; c2 = n2; c3 = n3;
     k0 += W0;
@@ -104,7 +117,8 @@ DPC_HOST_DEVICE Philox4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uin
 // ln u1 = e ln 2 + log1p(f), f = m - 1, with log1p(f) = 2 atanh(f / (2 + f))
 // from its odd Taylor series to the s^11 term (|s| <= 0.1716, truncation
 // below 2e-9 relative), so ln u1 keeps its relative accuracy as u1 -> 1; the
-// angle uses the hardware sine and cosine, whose argument is in revolutions.
+// angle uses the hardware sine and cosine, whose argument is in revolutions
+// (the reciprocal of 2 + f and the square root are the 1-ulp hardware ones).
 // Against the same formulas in double precision the normals differ by less
 // than 1e-6.  The function of (seed, leaf, r, c) does not depend on how a
 // kernel tiles the leaf, so every kernel that writes a leaf draws the same
@@ -117,7 +131,7 @@ DPC_DEVICE float ln_unit_interval(double u) {
     e -= 1;
   }
   const float f = (float)(m - 1.0);
-  const float s = f / (2.0f + f);
+  const float s = f * __builtin_amdgcn_rcpf(2.0f + f);  // 1-ulp reciprocal, 2 + f in [1.7, 2.5]
   const float s2 = s * s;
   float p = 1.0f / 11.0f;
   p = fmaf(p, s2, 1.0f / 9.0f);
@@ -135,7 +149,9 @@ DPC_DEVICE void philox_normal_pair(uint64_t seed, uint32_t leaf, uint64_t block,
   uint64_t bits = ((uint64_t)w.v[0] << 32) | (uint64_t)w.v[1];
   double u1 = ((double)(bits >> 11) + 0.5) * 0x1.0p-53;
   float u2 = (float)(((double)w.v[2] + 0.5) * 0x1.0p-32);
-  float radius = sqrtf(-2.0f * ln_unit_interval(u1));
+  // -2 ln u1 >= 2.2e-16 (u1 <= 1 - 2^-54): a normal float, so the 1-ulp
+  // hardware square root needs no scaling.
+  float radius = __builtin_amdgcn_sqrtf(-2.0f * ln_unit_interval(u1));
   *z0 = radius * __builtin_amdgcn_cosf(u2);
   *z1 = radius * __builtin_amdgcn_sinf(u2);
 }
