@@ -79,6 +79,21 @@ int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int din, int do
                      int with_bias, int accumulate, double* sqnorm, double* sqerr, void* ws,
                      size_t ws_bytes, void* stream);
 
+/* dpc_gram_sqnorms over several bias-free layers of one example batch (the
+ * per-layer norm loop of _streaming.py:70-82 over the layers of a model):
+ * layer i adds exactly what dpc_gram_sqnorms(A[i], G[i], B, T, din[i],
+ * dout[i], dtype, 0, i == 0 ? accumulate : 1, ...) would, in layer order.
+ * With bf16 operands, T an even number of 128-row blocks, B a multiple of 8
+ * and up to 8 layers, all layers share one launch (the work items of every
+ * layer spread over all XCDs); otherwise the layers run one by one.  ws:
+ * dpc_gram_sqnorms_multi_workspace_bytes. */
+size_t dpc_gram_sqnorms_multi_workspace_bytes(int n, const int* din, const int* dout, int B,
+                                              int T, int dtype);
+int dpc_gram_sqnorms_multi(int n, const void* const* A, const void* const* G, const int* din,
+                           const int* dout, int B, int T, int dtype, int accumulate,
+                           double* sqnorm, double* sqerr, void* ws, size_t ws_bytes,
+                           void* stream);
+
 /* dpc_gram_sqnorms_noalloc: no counterpart in the reference.  The same
  * computation as dpc_gram_sqnorms with no workspace argument and no
  * allocation, for callers that cannot allocate device memory (code under HIP

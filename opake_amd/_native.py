@@ -42,7 +42,7 @@ _c_u32 = ctypes.c_uint32
 _c_u64 = ctypes.c_uint64
 _c_i64 = ctypes.c_int64
 
-ABI_VERSION = 202  # dpc_version() of the library these signatures describe
+ABI_VERSION = 203  # dpc_version() of the library these signatures describe
 
 # name -> (restype, argtypes)
 SIGNATURES = {
@@ -79,6 +79,14 @@ SIGNATURES = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int,
          _c_double, _c_int, _c_void_p, _c_void_p, _c_u64, _c_u32, _c_u32, _c_double, _c_int,
          _c_void_p, _c_int, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
+    ),
+    "dpc_gram_sqnorms_multi_workspace_bytes": (
+        _c_size_t, [_c_int, _c_void_p, _c_void_p, _c_int, _c_int, _c_int],
+    ),
+    "dpc_gram_sqnorms_multi": (
+        _c_int,
+        [_c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
+         _c_void_p, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
     ),
     "dpc_clipped_sum_multi": (
         _c_int,

@@ -410,13 +410,25 @@ def ghost_clip_captured(
     # leaves' norms follow the reference's own roundoff, in the guard).
     sq = torch.zeros((n_groups, B), dtype=torch.float64, device=device)
     err = torch.zeros((n_groups, B), dtype=torch.float64, device=device)
+    gram_batches = {}
     for L in dense:
         if L.A.shape[1] == 1:
             ops.flat_sqnorms(L.A[:, 0], L.G[:, 0], with_bias=L.cap.has_bias, out=sq[L.group],
                              err=err[L.group])
+        elif L.cap.has_bias:
+            ops.gram_sqnorms(L.A, L.G, with_bias=True, out=sq[L.group], err=err[L.group])
         else:
-            ops.gram_sqnorms(L.A, L.G, with_bias=L.cap.has_bias, out=sq[L.group],
-                             err=err[L.group])
+            gram_batches.setdefault((L.group, L.A.dtype, L.A.shape[1]), []).append(L)
+    # Bias-free layers of one clipping group, dtype and token count: one Gram
+    # launch for all of them (up to 8 layers each).
+    for (g, _, _), members in gram_batches.items():
+        for k in range(0, len(members), 8):
+            part = members[k:k + 8]
+            if len(part) == 1:
+                ops.gram_sqnorms(part[0].A, part[0].G, out=sq[g], err=err[g])
+            else:
+                ops.gram_sqnorms_multi([L.A for L in part], [L.G for L in part], out=sq[g],
+                                       err=err[g])
     # The norms of all segmented layers of one dtype in one grouped launch
     # (up to 64 layers each; mixed shapes, most expensive tile pairs first).
     by_dtype = {}

@@ -27,6 +27,8 @@
 // tile pair on 4 waves.
 #include <mutex>
 
+#include <algorithm>
+
 #include "common.h"
 #include "lds_stage.h"
 
@@ -862,16 +864,47 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
 // Dense split mode: item l (after the XCD remap: an example's items, and
 // the two items of each set, share an XCD) is operand l % 2 of set (l / 2) %
 // nsets of example l / (2 nsets).
+// The layers of a split launch (up to kSplitMaxLayers, one T and B): layer
+// L's operands and widths, and `region`, the index of its share of the
+// records, tickets and exchange area.
+constexpr int kSplitMaxLayers = 8;
+struct SplitLayers {
+  const uint16_t* A[kSplitMaxLayers];
+  const uint16_t* G[kSplitMaxLayers];
+  int din[kSplitMaxLayers], dout[kSplitMaxLayers], region[kSplitMaxLayers];
+  int n;
+};
+
 __global__ void __launch_bounds__(512, 1)
-gram_split_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ G, int T,
-                       int din, int dout, int npairs, int nsets, int nblocks,
+gram_split_bf16_kernel(const SplitLayers lay, int B, int T, int npairs, int nsets, int nblocks,
                        double* __restrict__ records, int32_t* __restrict__ tickets,
                        float* __restrict__ xbuf) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[4 * 3 * kGTileBytes];
   __shared__ double red[3 * kSplitWaves * kRecStat];
   __shared__ int ticket_lds[2];
-  const int l = xcd_logical_block(gridDim.x, nblocks);
-  if (l < 0) return;  // padding workgroup: exits before any barrier
+  const int l0 = xcd_logical_block(gridDim.x, nblocks);
+  if (l0 < 0) return;  // padding workgroup: exits before any barrier
+  // Several layers (B % 8 == 0): every XCD's range holds, layer after layer,
+  // the items of B / 8 examples of each layer, so the XCDs get equal work.
+  int L = 0, l = l0;
+  if (lay.n > 1) {
+    const int per_xcd = nblocks / kXcds, bpx = B / kXcds, per_lx = bpx * 2 * nsets;
+    const int x = l0 / per_xcd, lx = l0 - x * per_xcd;
+    L = lx / per_lx;
+    const int r = lx - L * per_lx;
+    l = (x * bpx + r / (2 * nsets)) * 2 * nsets + r % (2 * nsets);
+  }
+  L = __builtin_amdgcn_readfirstlane(L);
+  l = __builtin_amdgcn_readfirstlane(l);
+  const uint16_t* A = lay.A[L];
+  const uint16_t* G = lay.G[L];
+  const int din = lay.din[L], dout = lay.dout[L];
+  {
+    const size_t reg = (size_t)lay.region[L];
+    records += reg * B * npairs * DPC_GRAM_REC_WORDS;
+    tickets += reg * 3 * nsets * B;
+    xbuf += reg * B * nsets * (2 * kSplitSetBytes / 4);
+  }
   const int op = l & 1, set = (l >> 1) % nsets, ex = (l >> 1) / nsets;
   const int nt = ceil_div(T, kGramTile);
   int t, q;
@@ -1106,20 +1139,27 @@ __device__ __forceinline__ double gram_bound_wave(const double* rec, int nt, dou
 // the bias term's).  bias (nullable): [B] squared norms then [B] error
 // bounds.
 __global__ void __launch_bounds__(kGramThreads)
-gram_finish_kernel(const double* __restrict__ records, int B, int nt, int accumulate,
-                   const double* __restrict__ bias, double* __restrict__ sqnorm,
+gram_finish_kernel(const double* __restrict__ records, int B, int nt, int nlayers,
+                   int accumulate, const double* __restrict__ bias, double* __restrict__ sqnorm,
                    double* __restrict__ sqerr) {
   const int b = blockIdx.x * (kGramThreads / 64) + (int)(threadIdx.x >> 6);
   if (b >= B) return;
   const size_t np = (size_t)nt * (nt + 1) / 2;
-  double s;
-  const double e = gram_bound_wave(records + (size_t)b * np * DPC_GRAM_REC_WORDS, nt, &s);
+  // Layers' records one after the other (B examples each), added in layer
+  // order as consecutive accumulating calls would.
+  double v = 0.0, ev = 0.0;
+  for (int L = 0; L < nlayers; ++L) {
+    double s;
+    const double e = gram_bound_wave(
+        records + ((size_t)L * B + (size_t)b) * np * DPC_GRAM_REC_WORDS, nt, &s);
+    const bool first = L == 0 && !accumulate;
+    v = first ? s : (L == 0 ? sqnorm[b] : v) + s;
+    ev = first ? e : (L == 0 && sqerr ? sqerr[b] : ev) + e;
+  }
   if ((threadIdx.x & 63) != 0) return;
-  double v = accumulate ? sqnorm[b] + s : s;
   if (bias) v = v + bias[b];
   sqnorm[b] = v;
   if (sqerr) {
-    double ev = accumulate ? sqerr[b] + e : e;
     if (bias) ev = ev + bias[B + b];
     sqerr[b] = ev;
   }
@@ -1270,9 +1310,17 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
     float* xbuf = (float*)(base + split_tickets_bytes(B, T));
     hipLaunchKernelGGL(fill_zero_i32_kernel, dim3(ceil_div(3 * nsets * B, kGramThreads)),
                        dim3(kGramThreads), 0, s, tickets, 3 * nsets * B);
-    hipLaunchKernelGGL(gram_split_bf16_kernel, dim3(padded), dim3(512), 0, s, (const uint16_t*)A,
-                       (const uint16_t*)G, T, din, dout, npairs, nsets, nblocks, records, tickets,
-                       xbuf);
+    SplitLayers lay;
+    lay.n = 1;
+    for (int i = 0; i < kSplitMaxLayers; ++i) {
+      lay.A[i] = (const uint16_t*)A;
+      lay.G[i] = (const uint16_t*)G;
+      lay.din[i] = din;
+      lay.dout[i] = dout;
+      lay.region[i] = 0;
+    }
+    hipLaunchKernelGGL(gram_split_bf16_kernel, dim3(padded), dim3(512), 0, s, lay, B, T, npairs,
+                       nsets, nblocks, records, tickets, xbuf);
   } else if (mfma) {
     nt = ceil_div(T, kGramTile);
     const int npairs = nt * (nt + 1) / 2;
@@ -1308,7 +1356,7 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
     DPC_HIP_CHECK(hipGetLastError());
   }
   hipLaunchKernelGGL(gram_finish_kernel, dim3(ceil_div(B, kGramThreads / 64)), dim3(kGramThreads), 0,
-                     s, (const double*)records, B, nt, accumulate, (const double*)bias, sqnorm,
+                     s, (const double*)records, B, nt, 1, accumulate, (const double*)bias, sqnorm,
                      sqerr);
   DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;
@@ -1437,4 +1485,99 @@ extern "C" int dpc_gram_sqnorms_noalloc(const void* A, const void* G, int B, int
   if (!ws) return DPC_EHIP;
   return dpc_gram_sqnorms(A, G, B, T, din, dout, dtype, with_bias, accumulate, sqnorm, sqerr, ws,
                           (size_t)DPC_NOALLOC_SCRATCH_BYTES, stream);
+}
+
+namespace {
+// The split-mode shape of dpc_gram_sqnorms_multi: bf16, T an even number of
+// 128-row blocks, B a multiple of 8, every layer on the MFMA path.
+bool split_multi_shape(int n, const int* din, const int* dout, int B, int T, int dtype) {
+  if (n < 2 || n > kSplitMaxLayers || dtype != DPC_BF16 || B % kXcds != 0 || !split_shape(T))
+    return false;
+  for (int i = 0; i < n; ++i) {
+    const size_t dmax = (size_t)(din[i] > dout[i] ? din[i] : dout[i]);
+    if (din[i] % 8 != 0 || dout[i] % 8 != 0 || ((size_t)T + kGramTile) * dmax * 2 >= ((size_t)1 << 31))
+      return false;
+  }
+  return true;
+}
+size_t split_multi_bytes(int n, int B, int T) {
+  const int nt = ceil_div(T, kGramTile);
+  const size_t npairs = (size_t)nt * (nt + 1) / 2, nsets = split_sets_per_example(nt);
+  return align256((size_t)n * B * npairs * DPC_GRAM_REC_WORDS * sizeof(double)) +
+         align256((size_t)n * 3 * nsets * B * sizeof(int32_t)) +
+         (size_t)n * B * nsets * 2 * kSplitSetBytes;
+}
+}  // namespace
+
+extern "C" size_t dpc_gram_sqnorms_multi_workspace_bytes(int n, const int* din, const int* dout,
+                                                        int B, int T, int dtype) {
+  if (n <= 0 || B <= 0 || T <= 0 || !din || !dout) return 0;
+  const size_t one = dpc_gram_workspace_bytes(B, T);
+  if (!split_multi_shape(n, din, dout, B, T, dtype)) return one;
+  const size_t multi = split_multi_bytes(n, B, T);
+  return multi > one ? multi : one;
+}
+
+extern "C" int dpc_gram_sqnorms_multi(int n, const void* const* A, const void* const* G,
+                                      const int* din, const int* dout, int B, int T, int dtype,
+                                      int accumulate, double* sqnorm, double* sqerr, void* ws,
+                                      size_t ws_bytes, void* stream) {
+  if (n < 0 || B < 0 || T <= 0) return DPC_EINVAL;
+  if (n == 0 || B == 0) return DPC_OK;
+  if (!A || !G || !din || !dout || !sqnorm || !ws) return DPC_EINVAL;
+  if (dtype != DPC_F32 && dtype != DPC_BF16) return DPC_EINVAL;
+  for (int i = 0; i < n; ++i)
+    if (!A[i] || !G[i] || din[i] <= 0 || dout[i] <= 0) return DPC_EINVAL;
+  if (B > 65535) return DPC_ENOTSUP;
+  if (ws_bytes < dpc_gram_sqnorms_multi_workspace_bytes(n, din, dout, B, T, dtype))
+    return DPC_ENOSPC;
+  if (!split_multi_shape(n, din, dout, B, T, dtype)) {
+    // Layer by layer, each accumulating into the previous layers' sums.
+    for (int i = 0; i < n; ++i) {
+      const int r = dpc_gram_sqnorms(A[i], G[i], B, T, din[i], dout[i], dtype, 0,
+                                     i == 0 ? accumulate : 1, sqnorm, sqerr, ws, ws_bytes, stream);
+      if (r != DPC_OK) return r;
+    }
+    return DPC_OK;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  const int nt = ceil_div(T, kGramTile);
+  const int npairs = nt * (nt + 1) / 2;
+  const int nsets = split_sets_per_example(nt);
+  const int nblocks = n * 2 * nsets * B;  // a multiple of 8: B is
+  uint8_t* base = (uint8_t*)ws;
+  double* records = (double*)base;
+  base += align256((size_t)n * B * npairs * DPC_GRAM_REC_WORDS * sizeof(double));
+  int32_t* tickets = (int32_t*)base;
+  base += align256((size_t)n * 3 * nsets * B * sizeof(int32_t));
+  float* xbuf = (float*)base;
+  // Table order: the layers with the longest K loops first (within each
+  // XCD's range they run first, the short ones fill the end); region = the
+  // caller's index, so the finish adds the layers in the caller's order.
+  int order[kSplitMaxLayers];
+  for (int i = 0; i < n; ++i) order[i] = i;
+  std::stable_sort(order, order + n, [&](int a, int b) {
+    return (long long)din[a] + dout[a] > (long long)din[b] + dout[b];
+  });
+  SplitLayers lay;
+  lay.n = n;
+  for (int k = 0; k < kSplitMaxLayers; ++k) {
+    const int i = order[k < n ? k : 0];
+    lay.A[k] = (const uint16_t*)A[i];
+    lay.G[k] = (const uint16_t*)G[i];
+    lay.din[k] = din[i];
+    lay.dout[k] = dout[i];
+    lay.region[k] = i;
+  }
+  const int nticket = n * 3 * nsets * B;
+  hipLaunchKernelGGL(fill_zero_i32_kernel, dim3(ceil_div(nticket, kGramThreads)),
+                     dim3(kGramThreads), 0, s, tickets, nticket);
+  hipLaunchKernelGGL(gram_split_bf16_kernel, dim3(nblocks), dim3(512), 0, s, lay, B, T, npairs,
+                     nsets, nblocks, records, tickets, xbuf);
+  DPC_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(gram_finish_kernel, dim3(ceil_div(B, kGramThreads / 64)), dim3(kGramThreads), 0,
+                     s, (const double*)records, B, nt, n, accumulate, (const double*)nullptr,
+                     sqnorm, sqerr);
+  DPC_HIP_CHECK(hipGetLastError());
+  return DPC_OK;
 }

@@ -80,6 +80,56 @@ def gram_sqnorms(
     return (out, err) if with_err else out
 
 
+def gram_sqnorms_multi(
+    A_list,
+    G_list,
+    *,
+    out: torch.Tensor | None = None,
+    err: torch.Tensor | None = None,
+    return_error: bool = False,
+):
+    """``gram_sqnorms`` of several bias-free layers of one batch, summed over
+    the layers in list order (``dpc_gram_sqnorms_multi``: one launch for all
+    of them when they take the bf16 split path).  ``out`` / ``err`` as in
+    :func:`gram_sqnorms`; the result equals consecutive ``gram_sqnorms``
+    calls accumulating into the same ``out`` / ``err``."""
+    n = len(A_list)
+    if n == 0 or len(G_list) != n:
+        raise ConfigurationError("expected matching, non-empty lists of A and G")
+    dev = nat.require_device(*A_list, *G_list, out, err)
+    dtype = A_list[0].dtype
+    B, T = A_list[0].shape[:2]
+    for A, G in zip(A_list, G_list):
+        if A.dim() != 3 or G.dim() != 3 or A.shape[:2] != (B, T) or G.shape[:2] != (B, T):
+            raise ConfigurationError("expected A [B, T, din], G [B, T, dout] with one B and T")
+        if A.dtype != dtype or G.dtype != dtype:
+            raise ConfigurationError("the layers' operands must share one dtype")
+    accumulate = out is not None
+    with_err = err is not None or return_error
+    if out is None:
+        out = torch.empty(B, dtype=torch.float64, device=dev)
+    elif out.dtype != torch.float64 or out.shape != (B,):
+        raise ConfigurationError("out must be float64 [B]")
+    if with_err:
+        err = _error_out(err, B, dev, accumulate)
+    if B > 0:
+        As = [_contig(A) for A in A_list]
+        Gs = [_contig(G) for G in G_list]
+        c_din = (ctypes.c_int * n)(*[A.shape[2] for A in As])
+        c_dout = (ctypes.c_int * n)(*[G.shape[2] for G in Gs])
+        ws_bytes = nat.load().dpc_gram_sqnorms_multi_workspace_bytes(
+            n, c_din, c_dout, B, T, nat.dtype_code(dtype))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        vp = ctypes.c_void_p * n
+        nat.call(
+            "dpc_gram_sqnorms_multi", n, vp(*[t.data_ptr() for t in As]),
+            vp(*[t.data_ptr() for t in Gs]), c_din, c_dout, B, T, nat.dtype_code(dtype),
+            int(accumulate), nat.ptr(out), nat.ptr(err if with_err else None), nat.ptr(ws),
+            ws_bytes, nat.stream_handle(dev),
+        )
+    return (out, err) if with_err else out
+
+
 def flat_sqnorms(
     a: torch.Tensor,
     g: torch.Tensor,
@@ -731,6 +781,7 @@ __all__ = [
     "clip_factors",
     "clipped_sum",
     "clipped_sum_multi",
+    "gram_sqnorms_multi",
     "flat_sqnorms",
     "gram_sqnorms",
     "grouped_clipped_sum",

@@ -257,6 +257,44 @@ def test_clipped_sum_accumulator_scaling_is_near_exact(dev):
     assert _rel_err(w.cpu(), exact) < 1e-5
 
 
+# Several layers' Gram norms in one call (dpc_gram_sqnorms_multi): the sums
+# (and error bounds) equal consecutive accumulating gram_sqnorms calls bit
+# for bit -- one shared split launch (bf16, an even number of 128-row
+# blocks, B % 8 == 0; layers of different widths, run longest first and
+# summed in the caller's order) and the layer-by-layer fallbacks (B = 6,
+# T = 300, 9 layers); with and without sums already in out / err.
+@pytest.mark.parametrize("B,T,n,acc", [(8, 256, 3, False), (16, 512, 5, True), (6, 256, 3, False),
+                                       (8, 300, 2, True), (8, 256, 9, False)])
+def test_gram_sqnorms_multi_matches_consecutive_calls(dev, B, T, n, acc):
+    g = _gen(B * 100 + T + n)
+    dims = [(256, 264), (512, 128), (64, 1024), (1024, 64), (136, 8), (8, 520), (320, 320),
+            (96, 200), (48, 56)][:n]
+    As = [torch.randn(B, T, din, generator=g).to(torch.bfloat16).to(dev) for din, _ in dims]
+    Gs = [(torch.randn(B, T, dout, generator=g) * torch.exp(torch.randn(B, 1, 1, generator=g)))
+          .to(torch.bfloat16).to(dev) for _, dout in dims]
+    start = torch.rand(B, generator=g, dtype=torch.float64).to(dev) if acc else None
+    want = start.clone() if acc else None
+    want_err = start.clone() * 1e-6 if acc else None
+    for i, (a, x) in enumerate(zip(As, Gs)):
+        if i == 0 and not acc:
+            want, want_err = ops.gram_sqnorms(a, x, return_error=True)
+        else:
+            ops.gram_sqnorms(a, x, out=want, err=want_err)
+    out = start.clone() if acc else None
+    err = start.clone() * 1e-6 if acc else None
+    if acc:
+        got, got_err = ops.gram_sqnorms_multi(As, Gs, out=out, err=err)
+    else:
+        got, got_err = ops.gram_sqnorms_multi(As, Gs, return_error=True)
+    assert torch.equal(got, want)
+    assert torch.equal(got_err, want_err)
+    # And the sums are the layers' norms: against float64 on the host.
+    if not acc:
+        ref = sum(ghost_oracle.linear_per_example_grads(a.cpu(), x.cpu(), dtype=torch.float64)[0]
+                  .pow(2).sum(dim=(1, 2)) for a, x in zip(As, Gs))
+        torch.testing.assert_close(got.cpu(), ref, rtol=1e-4, atol=0)
+
+
 def _multi_case(dev, dims, B, T, seed, slow=False):
     g = _gen(seed)
     As = [torch.randn(B, T, din, generator=g).to(torch.bfloat16) for din, _ in dims]
