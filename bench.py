@@ -1154,10 +1154,9 @@ def main() -> int:
     elapsed = time.perf_counter() - t0
     print(f"[bench] {args.steps} timed steps in {elapsed:.4f} s", file=sys.stderr, flush=True)
 
-    # Context measurements, after the timed steps: the sustained MFMA rate
-    # (back-to-back MFMAs at full power for ~40 ms) and the library reference
-    # of the same GEMM.  Run before the steps they slowed a short timed run
-    # (5 warm-up steps) up to 4-fold while the clocks recovered.
+    # Context measurements, after the timed steps (not part of the step):
+    # the sustained MFMA rate (back-to-back MFMAs at full power for ~40 ms)
+    # and the library reference of the same GEMM.
     sustained = sustained_mfma_tflops(dev)
     lib_ref = library_reference(A, G)
     print(f"[bench] context done: sustained {sustained:.0f} TFLOP/s, library GEMM "
