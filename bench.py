@@ -77,54 +77,6 @@ HBM_PEAK_GBS = 8000.0
 CLOCK_SETTLE_S = 0.2  # untimed steps before the warm-up of the default line
 
 
-class FenceFreeEvent:
-    """A HIP timing event created with hipEventDisableSystemFence (the HIP
-    runtime's flag for events that only measure time: recording it performs
-    no system-scope cache writeback and invalidation), with the two methods
-    of torch.cuda.Event that the timing hooks use.  torch's events cost the
-    default line ~5-9 us per step through those fences."""
-
-    _lib = None
-
-    @classmethod
-    def _hip(cls):
-        if cls._lib is None:
-            import ctypes
-
-            # The HIP runtime torch has loaded (one copy per process).
-            with open("/proc/self/maps") as f:
-                path = next(line.split()[-1] for line in f if "libamdhip64.so" in line)
-            cls._lib = ctypes.CDLL(path)
-        return cls._lib
-
-    def __init__(self):
-        import ctypes
-
-        self._ct = ctypes
-        self.handle = ctypes.c_void_p()
-        rc = self._hip().hipEventCreateWithFlags(ctypes.byref(self.handle),
-                                                 ctypes.c_uint(0x20000000))
-        if rc != 0:
-            raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
-
-    def record(self):
-        stream = torch.cuda.current_stream().cuda_stream
-        rc = self._hip().hipEventRecord(self.handle, self._ct.c_void_p(stream))
-        if rc != 0:
-            raise RuntimeError(f"hipEventRecord failed ({rc})")
-
-    def elapsed_time(self, end) -> float:
-        ms = self._ct.c_float()
-        rc = self._hip().hipEventElapsedTime(self._ct.byref(ms), self.handle, end.handle)
-        if rc != 0:
-            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
-        return ms.value
-
-    def __del__(self):
-        if self._lib is not None and self.handle:
-            self._lib.hipEventDestroy(self.handle)
-
-
 def algorithmic_flops(b=B, t=T, din=DIN, dout=DOUT):
     """Gram norms (SYRK convention T(T+1)(din+dout)), inner products 2T^2, GEMM 2BTdin dout."""
     gram = b * (t * (t + 1) * (din + dout) + 2 * t * t)
@@ -1144,7 +1096,10 @@ def main() -> int:
           f"clipped fraction {clipped_frac:.3f}", file=sys.stderr, flush=True)
 
     torch.cuda.synchronize()
-    pairs = [(FenceFreeEvent(), FenceFreeEvent()) for _ in range(args.steps)]
+    # Timing events without the system-scope fence (dpc_timing_event_*):
+    # torch's events cost this line 5-9 us per step and inflate the GEMM's
+    # measured duration with the cache writeback and invalidation they do.
+    pairs = [(_native.TimingEvent(), _native.TimingEvent()) for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for pair in pairs:

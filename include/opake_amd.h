@@ -43,6 +43,18 @@ int dpc_version(void);
 /* Last HIP error string recorded by a failing call on this thread. */
 const char* dpc_last_error(void);
 
+/* Timing events recorded without the system-scope fence (HIP's
+ * hipEventDisableSystemFence): the timing hooks of the clipping entry points
+ * and of bench.py use them to time launches without adding cache writeback
+ * and invalidation around them (no reference counterpart: measurement
+ * plumbing of this build).  create -> record on a stream (any number of
+ * times) -> elapsed_ms between two recorded events once both completed ->
+ * destroy. */
+int dpc_timing_event_create(void** event);
+int dpc_timing_event_record(void* event, void* stream);
+int dpc_timing_event_elapsed_ms(void* start, void* end, float* ms);
+int dpc_timing_event_destroy(void* event);
+
 /* Writes n 32-bit words from HOST memory `host_words` to device memory `dst`
  * with kernels that carry the words as arguments: no host buffer has to
  * outlive the call, so it may be recorded into a HIP graph.  Used for the

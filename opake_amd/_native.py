@@ -42,7 +42,7 @@ _c_u32 = ctypes.c_uint32
 _c_u64 = ctypes.c_uint64
 _c_i64 = ctypes.c_int64
 
-ABI_VERSION = 203  # dpc_version() of the library these signatures describe
+ABI_VERSION = 204  # dpc_version() of the library these signatures describe
 
 # name -> (restype, argtypes)
 SIGNATURES = {
@@ -80,6 +80,10 @@ SIGNATURES = {
          _c_double, _c_int, _c_void_p, _c_void_p, _c_u64, _c_u32, _c_u32, _c_double, _c_int,
          _c_void_p, _c_int, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
     ),
+    "dpc_timing_event_create": (_c_int, [_c_void_p]),
+    "dpc_timing_event_record": (_c_int, [_c_void_p, _c_void_p]),
+    "dpc_timing_event_elapsed_ms": (_c_int, [_c_void_p, _c_void_p, _c_void_p]),
+    "dpc_timing_event_destroy": (_c_int, [_c_void_p]),
     "dpc_gram_sqnorms_multi_workspace_bytes": (
         _c_size_t, [_c_int, _c_void_p, _c_void_p, _c_int, _c_int, _c_int],
     ),
@@ -209,6 +213,33 @@ def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
 
 def stream_handle(device: torch.device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+class TimingEvent:
+    """A timing event recorded without the system-scope fence
+    (``dpc_timing_event_*``), with the ``record`` / ``elapsed_time`` methods
+    of ``torch.cuda.Event`` that the timing hooks use: recording one adds no
+    cache writeback or invalidation around the launch it brackets."""
+
+    def __init__(self):
+        self._h = ctypes.c_void_p()
+        call("dpc_timing_event_create", ctypes.addressof(self._h))
+
+    def record(self) -> None:
+        call("dpc_timing_event_record", self._h,
+             stream_handle(torch.device("cuda", torch.cuda.current_device())))
+
+    def elapsed_time(self, end: "TimingEvent") -> float:
+        ms = ctypes.c_float()
+        call("dpc_timing_event_elapsed_ms", self._h, end._h, ctypes.addressof(ms))
+        return ms.value
+
+    def __del__(self):
+        try:
+            if self._h:
+                load().dpc_timing_event_destroy(self._h)
+        except Exception:  # interpreter shutdown
+            pass
 
 
 def dtype_code(dtype: torch.dtype) -> int:

@@ -148,7 +148,8 @@ def ghost_clip_sum(
     ``(NoisedPytree, next_state)`` (or ``((NoisedPytree, aux), next_state)``),
     bit-identical to ``noise_fn(ghost_clip_sum(...), noise_state)``.
     ``auto_s_gamma`` selects AUTO-S scaling ``C / (||g|| + gamma)``.
-    ``gemm_events``: optional ``(start, end)`` pair of ``torch.cuda.Event``
+    ``gemm_events``: optional ``(start, end)`` pair of events (``torch.cuda.Event``
+    or the fence-free ``opake_amd._native.TimingEvent``)
     recorded on the current stream around the clipped-sum launch (timing hook).
     """
     if isinstance(clipping_norm, PerGroup):

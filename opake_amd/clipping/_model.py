@@ -276,7 +276,7 @@ def _event_pair(sink):
     """Record a start event on the current stream (the one the kernels use)."""
     if sink is None:
         return None
-    pair = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+    pair = (nat.TimingEvent(), nat.TimingEvent())
     pair[0].record()
     sink.append(pair)
     return pair
@@ -306,7 +306,8 @@ def ghost_clip_captured(
     with ``noise_fn``), and with ``return_aux`` the first element is
     ``(result, GhostGradAux)`` whose ``loss_values`` is ``None``.
     ``gemm_events`` (timing hook): a list that receives one pair of recorded
-    ``torch.cuda.Event`` around each clipped-sum launch (and each per-example
+    timing events (``TimingEvent``: fence-free, ``elapsed_time`` like
+    ``torch.cuda.Event``) around each clipped-sum launch (and each per-example
     gradient launch of a layer that takes the direct method).
     """
     _validate_bound(clipping_norm)

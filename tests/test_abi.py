@@ -34,7 +34,7 @@ def test_version_and_size_queries():
     if not _native.LIB_PATH.exists():
         pytest.skip("native library not built")
     lib = _native.load()
-    assert lib.dpc_version() == _native.ABI_VERSION == 203
+    assert lib.dpc_version() == _native.ABI_VERSION == 204
     assert lib.dpc_clip_plan_bytes(32) == 16 + 32 * 4
     assert lib.dpc_gram_workspace_bytes(0, 5) == 0
     assert lib.dpc_gram_workspace_bytes(2, 128) > 0
