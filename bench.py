@@ -603,6 +603,22 @@ def _mlp_ce(out, target):
     return torch.nn.functional.cross_entropy(out, target, reduction="none")
 
 
+def make_mlp():
+    """The config-1 model, 784-512-10 with ReLU (torch's default Linear init)."""
+    import torch
+
+    class MLP(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.fc1 = torch.nn.Linear(784, 512)
+            self.fc2 = torch.nn.Linear(512, 10)
+
+        def forward(self, x):
+            return self.fc2(torch.relu(self.fc1(x)))
+
+    return MLP()
+
+
 def mlp_cpu_baseline(threads: int, repeats: int = CPU_REPEATS):
     """The config-1 step as the reference runs it on the CPU: vmap(grad) of the
     per-example cross-entropy, the streaming clip-and-sum and the CPU-generator
@@ -613,7 +629,7 @@ def mlp_cpu_baseline(threads: int, repeats: int = CPU_REPEATS):
 
     torch.set_num_threads(threads)
     torch.manual_seed(0)
-    model = ghost_oracle.MLP()
+    model = make_mlp()
     params = {k: v.detach() for k, v in model.named_parameters()}
     g = torch.Generator().manual_seed(1)
     x = torch.randn(MLP_B, 784, generator=g)
@@ -642,12 +658,11 @@ def run_mlp(args) -> dict:
     )
     from opake_amd.noise import gaussian_noise
     from opake_amd.random import key
-    from oracle import ghost_oracle
 
     _native.load()
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
-    model = ghost_oracle.MLP().to(dev)
+    model = make_mlp().to(dev)
     g = torch.Generator(device=dev).manual_seed(1)
     x = torch.randn(MLP_B, 784, generator=g, device=dev)
     y = torch.randint(0, 10, (MLP_B,), generator=g, device=dev)
@@ -1147,7 +1162,7 @@ def main() -> int:
         "unit": "examples/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": n_settle + args.warmup,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
@@ -1157,8 +1172,9 @@ def main() -> int:
         "config": {
             "workload": "linear 4096x4096, B=32, T=512, bf16; ghost-norm clip + sum + fused "
                         "device-stream noise (BASELINE configs[1])",
-            "clock_settle": f"{n_settle} untimed steps ({CLOCK_SETTLE_S} s) before the "
-                            f"{args.warmup} warm-up steps",
+            "untimed_steps": f"{n_settle + args.warmup}: {n_settle} clock-settling steps "
+                             f"({CLOCK_SETTLE_S} s of wall time) then the {args.warmup} "
+                             "requested warm-up steps",
             "global_batch": B,
             "seq_len": T,
             "clipping_norm": C,
@@ -1183,8 +1199,8 @@ def main() -> int:
             "library_reference": lib_ref,
         },
         "cpu_baseline": cpu,
-        "preparation": "sustained-MFMA measurement and library reference GEMM run before the "
-                       "warm-up steps",
+        "preparation": "sustained-MFMA measurement and library reference GEMM run after the "
+                       "timed steps",
     }
     add_sustained(line["roofline"], dev, sustained)
     print(json.dumps(line), flush=True)

@@ -33,7 +33,10 @@ extern "C" {
 #define DPC_ENOSPC (-28)
 #define DPC_EHIP (-1000)
 
-enum dpc_dtype { DPC_F32 = 0, DPC_BF16 = 1 };
+/* Element types.  Most entry points take DPC_F32 / DPC_BF16 operands; the
+ * materialised-leaf passes, the clip-factor guards and dpc_add_noise_ex also
+ * take DPC_F16 and DPC_F64. */
+enum dpc_dtype { DPC_F32 = 0, DPC_BF16 = 1, DPC_F16 = 2, DPC_F64 = 3 };
 enum dpc_scale_kind { DPC_SCALE_FIXED = 0, DPC_SCALE_AUTO_S = 1 };
 enum dpc_noise_mode { DPC_NOISE_NONE = 0, DPC_NOISE_INJECTED = 1, DPC_NOISE_PHILOX = 2 };
 
@@ -115,7 +118,7 @@ int dpc_gram_sqnorms_multi(int n, const void* const* A, const void* const* G, co
  * (dpc_gram_workspace_bytes(B, T) > DPC_NOALLOC_SCRATCH_BYTES) return
  * DPC_ENOSPC.  Every call on a device shares that device's array, so calls
  * that overlap on one device (other streams, other threads) race. */
-#define DPC_NOALLOC_SCRATCH_BYTES (24u << 20)
+#define DPC_NOALLOC_SCRATCH_BYTES (48u << 20)
 int dpc_gram_sqnorms_noalloc(const void* A, const void* G, int B, int T, int din, int dout,
                              int dtype, int with_bias, int accumulate, double* sqnorm,
                              double* sqerr, void* stream);
@@ -140,13 +143,18 @@ int dpc_flat_sqnorms(const void* a, const void* g, int B, int din, int dout, int
  *   s      = ratio * guard_rel[g] - guard_abs[g]
  *   s      = min(1, s)                             (FIXED only)
  *   s      = isfinite(s) ? max(s, 0) : 0
- *   scale[g * B + i] = (float)s                    for each guard g < n_guards
- *                    (guard_bf16[g] != 0: s rounded to the nearest bf16 --
- *                    the reference's scale.to(multiply dtype) for an explicit
- *                    compute_dtype=bfloat16, _pytree.py:160-187)
+ *   scale[g * B + i] = s.to(guard_mult[g]) as float, for each guard g
+ *                    (the reference's scale.to(multiply dtype),
+ *                    _pytree.py:160-187: DPC_F32 / DPC_F64 (float)s,
+ *                    DPC_BF16 / DPC_F16 (float)s rounded to nearest even
+ *                    in that type, as torch converts a float64 through
+ *                    float32)
+ *   scale64[g * B + i] = s for DPC_F64 guards, (double)scale[g * B + i]
+ *                    otherwise (nullable; the float64 multiply of float64
+ *                    leaves)
  * norms_out[i] = (float)norm; *nclipped = #{i : (float)norm > count_threshold}
  * (the reference's strict `norms > clipping_norm`, _clipped_fun.py:348-396).
- * guard_rel / guard_abs / guard_bf16 (nullable: all 0) are HOST arrays of
+ * guard_rel / guard_abs / guard_mult (nullable: all DPC_F32) are HOST arrays of
  * n_guards (1..4) values, one per storage dtype.  sqnorm and all outputs are device pointers.
  * Any output pointer may be NULL.  `plan` (nullable, device memory of
  * n_guards * dpc_clip_plan_bytes(B) bytes) receives one plan per guard: the
@@ -158,8 +166,9 @@ int dpc_flat_sqnorms(const void* a, const void* g, int B, int din, int dout, int
 size_t dpc_clip_plan_bytes(int B);
 int dpc_clip_factors(const double* sqnorm, const double* sqerr, int B, double C, int kind,
                      double gamma, const double* guard_rel, const double* guard_abs,
-                     const int* guard_bf16, int n_guards, float count_threshold, float* scale,
-                     float* norms_out, int* nclipped, void* plan, void* stream);
+                     const int* guard_mult, int n_guards, float count_threshold, float* scale,
+                     double* scale64, float* norms_out, int* nclipped, void* plan,
+                     void* stream);
 
 /* ------------------------------------------------------------------------
  * Clipped batch sum of a linear layer with the noise epilogue fused.
@@ -226,6 +235,19 @@ int dpc_add_noise(const void* x, void* y, int64_t rows, int64_t cols, int dtype,
                   int noise_mode, const float* noise, uint64_t seed, uint32_t leaf_id,
                   void* stream);
 
+/* dpc_add_noise_ex: `_sample` of _gaussian.py:188-204 for any leaf dtype
+ * and any compute_dtype cd (each of DPC_F16 / DPC_BF16 / DPC_F32 / DPC_F64):
+ *   y = to_dtype(to_cd(to_cd(x) + to_cd(sigma_op * z)))
+ * with sigma_op = (float)sigma for cd of 16 or 32 bits (torch's Python-scalar
+ * multiply of such a tensor) and sigma itself for DPC_F64, and to_cd of a
+ * 16-bit cd through float32 (torch's float arithmetic for 16-bit tensors).
+ * z: injected (`noise`, cd values shaped like x: the reference's
+ * torch.randn(shape, dtype=compute_dtype) on its CPU generator) or the
+ * Philox stream of dpc_add_noise rounded to cd.  sigma == 0 copies x. */
+int dpc_add_noise_ex(const void* x, void* y, int64_t rows, int64_t cols, int dtype,
+                     int compute_dtype, double sigma, int noise_mode, const void* noise,
+                     uint64_t seed, uint32_t leaf_id, void* stream);
+
 /* The Philox-stream noise of n leaves of one dtype in as few launches as
  * possible (one per 32 leaves), for the many small leaves of a step (LoRA
  * adapters): leaf i gets exactly dpc_add_noise(x[i], y[i], rows[i], cols[i],
@@ -255,10 +277,11 @@ int dpc_philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32
  * leaf into 2048-element tiles.
  *
  * dpc_leaves_sqnorm: partial[b, t] = float64 sum over tile t of example b of
- *   (float)sanitise(x)^2 (fp32 square, fp64 sum; square_dtype DPC_BF16, bf16
- *   leaves only: each square rounded to bf16, the reference's reduction in an
- *   explicit compute_dtype=bfloat16, _pytree.py:286-314), then
- *   leaf_sq[b, leaf_col[l]] = sum of leaf l's tiles (tile_start [L + 1]).
+ *   to_sq(v * v), v = to_sq(sanitise(x)), sq = square_dtype (the reference's
+ *   reduction dtype, _pytree.py:84-108,286-314: float32 by default, float64
+ *   for float64 leaves, or an explicit compute_dtype; any of the four
+ *   dtypes, leaves of any of them), then leaf_sq[b, leaf_col[l]] = sum of
+ *   leaf l's tiles (tile_start [L + 1]).
  * dpc_leaves_apply: out[off_l + j] = sum_b stored(b, l, j) in fp32, where
  *   stored = to_dtype(float(sanitise(x)) * scale[row_l * B + b]) with bf16
  *   subnormals that rounded up zeroed (_pytree.py:160-204); row_l =
@@ -279,6 +302,23 @@ int dpc_leaves_apply(const int64_t* ptrs, const int64_t* sizes, const int32_t* t
                      const int32_t* tile_local, const int64_t* out_offs, int n_tiles, int B,
                      int dtype, const float* scale, const int32_t* leaf_scale_row, void* out,
                      void* out_sq, int out_dtype, float* post_sq, void* stream);
+/* dpc_leaves_apply_ex: the apply pass for every dtype combination of
+ * _pytree.py:160-204 with _clipped_fun.py:112-132 -- storage dtype S
+ * (`dtype`), multiply dtype M = promote(S, compute dtype) (`mult_dtype`),
+ * batch-sum dtype A (`acc_dtype`: the compute dtype, float32 for 16-bit
+ * storage, else S) and output dtype O (`out_dtype`), each any of the four:
+ *   prod = to_M(sanitise(x) * scale_M[b]), stored = to_S(prod) (zeroed if it
+ *   rounded up into S's subnormal range), out = to_O(to_A(sum_b to_A(stored)))
+ *   with the sum in float32 (A of 16 or 32 bits) or float64 (A = float64), in
+ *   example order.  scale_M is row leaf_scale_row[l] of `scale` (float32,
+ *   already converted to M) or, for M = float64, of `scale64` (float64).
+ *   out_sq (nullable): the same sum of to_S(stored^2); post_sq (nullable,
+ *   float64 [B, 4 * n_tiles]) as in dpc_leaves_apply. */
+int dpc_leaves_apply_ex(const int64_t* ptrs, const int64_t* sizes, const int32_t* tile_leaf,
+                        const int32_t* tile_local, const int64_t* out_offs, int n_tiles, int B,
+                        int dtype, int mult_dtype, int acc_dtype, const float* scale,
+                        const double* scale64, const int32_t* leaf_scale_row, void* out,
+                        void* out_sq, int out_dtype, double* post_sq, void* stream);
 
 /* Per-group sums of per-leaf squared norms: out[g * B + b] (float64) = sum of
  * x[b * stride + j] over the columns j with col_group[j] == g, in column

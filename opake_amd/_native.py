@@ -27,6 +27,8 @@ DPC_EHIP = -1000
 
 DPC_F32 = 0
 DPC_BF16 = 1
+DPC_F16 = 2
+DPC_F64 = 3
 SCALE_FIXED = 0
 SCALE_AUTO_S = 1
 NOISE_NONE = 0
@@ -42,7 +44,7 @@ _c_u32 = ctypes.c_uint32
 _c_u64 = ctypes.c_uint64
 _c_i64 = ctypes.c_int64
 
-ABI_VERSION = 204  # dpc_version() of the library these signatures describe
+ABI_VERSION = 205  # dpc_version() of the library these signatures describe
 
 # name -> (restype, argtypes)
 SIGNATURES = {
@@ -71,7 +73,7 @@ SIGNATURES = {
         _c_int,
         [_c_void_p, _c_void_p, _c_int, _c_double, _c_int, _c_double, ctypes.POINTER(_c_double),
          ctypes.POINTER(_c_double), ctypes.POINTER(_c_int), _c_int, _c_float, _c_void_p,
-         _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     ),
     "dpc_clipped_sum_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "dpc_clipped_sum": (
@@ -116,6 +118,17 @@ SIGNATURES = {
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_void_p,
          _c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p],
+    ),
+    "dpc_leaves_apply_ex": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
+         _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p,
+         _c_void_p],
+    ),
+    "dpc_add_noise_ex": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_int, _c_int, _c_double, _c_int, _c_void_p,
+         _c_u64, _c_u32, _c_void_p],
     ),
     "dpc_group_sum_f64": (
         _c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_void_p],
@@ -242,12 +255,19 @@ class TimingEvent:
             pass
 
 
-def dtype_code(dtype: torch.dtype) -> int:
-    if dtype == torch.float32:
-        return DPC_F32
-    if dtype == torch.bfloat16:
-        return DPC_BF16
-    raise ConfigurationError(f"unsupported dtype {dtype} (supported: float32, bfloat16)")
+_CODES = {torch.float32: DPC_F32, torch.bfloat16: DPC_BF16, torch.float16: DPC_F16,
+          torch.float64: DPC_F64}
+
+
+def dtype_code(dtype: torch.dtype, *, wide: bool = False) -> int:
+    """The library's code of ``dtype``: float32 or bfloat16 for the linear-layer
+    kernels; with ``wide`` (the materialised-leaf, clip-guard and noise entry
+    points) also float16 and float64."""
+    code = _CODES.get(dtype)
+    if code is None or (not wide and code not in (DPC_F32, DPC_BF16)):
+        supported = "float16, bfloat16, float32, float64" if wide else "float32, bfloat16"
+        raise ConfigurationError(f"unsupported dtype {dtype} (supported: {supported})")
+    return code
 
 
 def require_device(*tensors: torch.Tensor) -> torch.device:

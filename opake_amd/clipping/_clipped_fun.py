@@ -26,18 +26,20 @@ _clipped_grad.py:86-362, _auto.py:211-367):
   ``max_norm = C^2 / normalize_by`` for the squared stream
   (``_clipped_fun.py:414-423``).
 
-* ``compute_dtype`` (``_clipped_fun.py:91-170``, ``_pytree.py:84-108``):
-  float32, or bfloat16 with bfloat16 leaves -- squares, guard roundoff and
-  scale multiply in it (``promote(leaf, compute_dtype)``), batch sums in it and
-  cast to the output dtype after, microbatch running sums in the wider of it
-  and the output dtype.
+* leaves of float16, bfloat16, float32 or float64 (mixed), and
+  ``compute_dtype`` (``_clipped_fun.py:91-170``, ``_pytree.py:84-108``) any of
+  those four -- squares, guard roundoff and scale multiply in it
+  (``promote(leaf, compute_dtype)``), batch sums in it and cast to the output
+  dtype after, microbatch running sums in the wider of it and the output
+  dtype; without one, the reference's defaults (float32 reductions for
+  16-bit leaves, float64 when a leaf is float64).
 
 * ``pre_clipping_transform`` (``_clipped_grad.py:97,285``, ``_auto.py:222``):
   applied to each example's gradient pytree inside the vmapped gradient
   function, and to the zero gradients of an empty batch.
 
-Not covered (``OperationError``): other compute dtypes, custom scale
-functions.
+Not covered (``OperationError``): custom scale functions, non-floating
+leaves.
 """
 
 from __future__ import annotations
@@ -49,7 +51,12 @@ import torch
 from torch.autograd.profiler import record_function
 from torch.func import grad_and_value, vmap
 
-from opake_amd.clipping._leaves import _group_layout, leaves_clip_sum, unsupported_reason
+from opake_amd.clipping._leaves import (
+    _group_layout,
+    _sum_dtype_of,
+    leaves_clip_sum,
+    unsupported_reason,
+)
 from opake_amd.exceptions import ConfigurationError, InputTypeError, OperationError
 from opake_amd.pytree import (
     tree_flatten,
@@ -197,11 +204,11 @@ def _clip_sum_values(values, clipping_norm, scale, *, dtype, with_postsq,
                      second_moment=False, compute_dtype=None, output_dtype=None) -> _ChunkResult:
     """HIP clip-and-sum of a stacked pytree (``_streaming.py:39-185``).
 
-    ``dtype``: the dtype of the batch sums (default: the leaf dtype); with
-    ``compute_dtype`` bfloat16 the sums are taken in bfloat16 and cast to it
-    (``_sum_clipped_tensor``, ``_clipped_fun.py:114-132``).  ``dtype`` may be
-    ``_ACCUMULATE``: each leaf's sum is then taken in the microbatch
-    accumulation dtype for the requested ``output_dtype``."""
+    ``dtype``: the dtype of the batch sums (default: the leaf dtype); they are
+    reduced in ``compute_dtype`` (float32 for 16-bit leaves without one) and
+    cast to it (``_sum_clipped_tensor``, ``_clipped_fun.py:112-132``).
+    ``dtype`` may be ``_ACCUMULATE``: each leaf's sum is then taken and kept in
+    the microbatch accumulation dtype for the requested ``output_dtype``."""
     _check_compute_dtype(compute_dtype)
     grouped = isinstance(clipping_norm, PerGroup)
     if grouped:
@@ -215,36 +222,25 @@ def _clip_sum_values(values, clipping_norm, scale, *, dtype, with_postsq,
                                 second_moment=False, batch_size=B)
     if reason is not None:
         raise OperationError(f"HIP clip-and-sum cannot serve this call: {reason}")
-    out_dtypes = None
-    cast_to = None
     if dtype is _ACCUMULATE:
-        out_dtypes = {l.dtype: _accumulation_dtype(l.dtype, output_dtype, compute_dtype)
+        # Microbatch chunks: summed and kept in the accumulation dtype.
+        sum_dtypes = {l.dtype: (_accumulation_dtype(l.dtype, output_dtype, compute_dtype),) * 2
                       for l in leaves}
-        if any(v not in (k, torch.float32) for k, v in out_dtypes.items()):
-            raise OperationError(f"microbatch accumulation dtypes {out_dtypes} are not supported "
-                                 "(float32 or the leaf dtype)")
-    elif compute_dtype == torch.bfloat16:
-        cast_to = dtype
-    elif dtype is not None:
-        if dtype != torch.float32:
-            raise OperationError(f"output dtype {dtype} is not supported (float32 or the leaf dtype)")
-        out_dtypes = {torch.bfloat16: torch.float32, torch.float32: torch.float32}
+    else:
+        sum_dtypes = {l.dtype: (_sum_dtype_of(l.dtype, compute_dtype), dtype or l.dtype)
+                      for l in leaves}
     detached = [l.detach() for l in leaves]
     names = None
     if grouped:
         names, leaf_groups, bounds = _group_layout(paths, clipping_norm)
         res = leaves_clip_sum(detached, bounds, kind=scale.kind, gamma=scale.gamma,
-                              with_postsq=with_postsq, out_dtypes=out_dtypes,
+                              with_postsq=with_postsq, sum_dtypes=sum_dtypes,
                               leaf_groups=leaf_groups, second_moment=second_moment,
                               compute_dtype=compute_dtype)
     else:
         res = leaves_clip_sum(detached, float(clipping_norm), kind=scale.kind,
-                              gamma=scale.gamma, with_postsq=with_postsq, out_dtypes=out_dtypes,
+                              gamma=scale.gamma, with_postsq=with_postsq, sum_dtypes=sum_dtypes,
                               second_moment=second_moment, compute_dtype=compute_dtype)
-    if cast_to is not None:
-        res.reduced = [x.to(cast_to) for x in res.reduced]
-        if second_moment:
-            res.squared = [x.to(cast_to) for x in res.squared]
     group_norms = None
     if grouped:
         group_norms = {n: res.group_norms[k] for k, n in enumerate(names)}

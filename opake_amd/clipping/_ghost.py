@@ -106,16 +106,21 @@ def guard_for_linear(dtype: torch.dtype, din: int, dout: int, bias: bool):
 
 
 def ghost_sqnorms(A: torch.Tensor, G: torch.Tensor, *, bias: bool = False,
-                  out: torch.Tensor | None = None, err: torch.Tensor | None = None):
+                  out: torch.Tensor | None = None, err: torch.Tensor | None = None,
+                  return_error: bool = True):
     """Per-example squared gradient norms of one linear layer and the bounds of
     their rounding errors: ``(sq, err)``, float64 [B] each, with
     ``sq + err >= ||G_i^T A_i||^2``.  With ``out`` / ``err`` the layer's values
-    are added to them."""
+    are added to them.  ``return_error=False`` returns ``sq`` alone (and
+    accumulates into ``out`` without a bound): such norms are not a sound
+    basis for a clip factor."""
     A, G = _check_inputs(A, G, bias)
+    if not return_error and err is not None:
+        raise ConfigurationError("err was given together with return_error=False")
     if A.shape[1] == 1:
         return ops.flat_sqnorms(A[:, 0], G[:, 0], with_bias=bias, out=out, err=err,
-                                return_error=True)
-    return ops.gram_sqnorms(A, G, with_bias=bias, out=out, err=err, return_error=True)
+                                return_error=return_error)
+    return ops.gram_sqnorms(A, G, with_bias=bias, out=out, err=err, return_error=return_error)
 
 
 def _scale_kind(auto_s_gamma):
@@ -165,6 +170,18 @@ def ghost_clip_sum(
     kind, gamma = _scale_kind(auto_s_gamma)
     max_norm = clipping_norm / normalize_by
 
+    if noise_fn is not None and noise_fn.compute_dtype != torch.float32:
+        # The GEMM epilogue adds noise in float32; another compute dtype adds
+        # it after the clipped sum, through noise_fn itself.
+        if noise_state is None:
+            raise ConfigurationError("noise_state is required with noise_fn")
+        out = ghost_clip_sum(A, G, clipping_norm=clipping_norm, normalize_by=normalize_by,
+                             bias=bias, auto_s_gamma=auto_s_gamma, dtype=dtype,
+                             return_aux=return_aux, gemm_events=gemm_events)
+        res, aux = out if return_aux else (out, None)
+        res, next_state = noise_fn(res, noise_state)
+        return ((res, aux) if return_aux else res), next_state
+
     with record_function("opake::ghost_clip_sum"):
         sq, err = ghost_sqnorms(A, G, bias=bias)
         cf = ops.clip_factors(
@@ -184,8 +201,6 @@ def ghost_clip_sum(
                 raise ConfigurationError("noise_state is required with noise_fn")
             std = noise_fn.clipped_stddev(clipped(None, max_norm=max_norm))
             if std != 0.0:
-                if noise_fn.compute_dtype != torch.float32:
-                    raise ConfigurationError("fused noise supports compute_dtype float32 only")
                 step_key = step_key_for(noise_state)
                 # Flatten order of {"bias", "weight"}: bias first when present.
                 w_leaf, b_leaf = (1, 0) if bias else (0, 0)

@@ -8,28 +8,33 @@ of the backend that ``register_fused_clip_backend`` accepts
 It takes stacked per-example values ``[B, *P]`` and does the work in a fixed
 number of HIP launches per storage dtype, whatever the number of leaves:
 
-1. ``dpc_leaves_sqnorm``: per (example, leaf) fp64 sums of fp32 squares of the
-   sanitised values, 2048-element tiles, then ``dpc_row_sum_f64`` folds the
-   leaves in flatten order (the reference's ``sq_norm = sq_0 + sq_1 + ...``);
-2. ``dpc_clip_factors``: the guarded scale per storage dtype (fixed or AUTO-S);
-3. ``dpc_leaves_apply``: scale in fp32, one cast to the storage dtype, bf16
-   subnormals that rounded up zeroed, fp32 sum over the batch in example order.
+1. ``dpc_leaves_sqnorm``: per (example, leaf) fp64 sums of the squares of the
+   sanitised values in the reduction dtype, 2048-element tiles, then
+   ``dpc_row_sum_f64`` folds the leaves in flatten order (the reference's
+   ``sq_norm = sq_0 + sq_1 + ...``);
+2. ``dpc_clip_factors``: the guarded scale per storage dtype (fixed or AUTO-S),
+   converted to that dtype's multiply dtype;
+3. ``dpc_leaves_apply`` (float32 / bfloat16 leaves, float32 arithmetic) or
+   ``dpc_leaves_apply_ex`` (every other combination): scale in the multiply
+   dtype, one cast to the storage dtype, subnormals that rounded up zeroed,
+   the batch sum in example order in the reduction dtype.
 
+Leaves may be float16, bfloat16, float32 or float64, mixed; ``compute_dtype``
+may be any of those four (the reference's reduction, multiply and sum dtypes
+follow from it, ``_pytree.py:84-204``, ``_clipped_fun.py:91-148``).
 Per-group clipping norms (``PerGroup``) clip each group to its own bound by
 its own norm, with one scale row per group; ``second_moment`` adds the batch
-sums of the squared stored values.  An explicit ``compute_dtype`` of float32,
-or of bfloat16 with bfloat16 leaves, follows the reference's reduction and
-multiply dtypes.  A call the kernels do not cover (another ``compute_dtype``,
-dtypes other than float32 / bfloat16, leaves that need grad) goes to the
-``fallback`` the caller registered with
-:func:`make_fused_backend` -- in the reference that is its own PyTorch
-streaming path -- and raises ``OperationError`` when there is none.
+sums of the squared stored values.  A call the kernels cannot take (leaves off
+the GPU, non-floating leaves, leaves that need grad) goes to the ``fallback``
+the caller registered with :func:`make_fused_backend` -- in the reference that
+is its own PyTorch streaming path -- and raises ``OperationError`` when there
+is none.
 """
-
 from __future__ import annotations
 
+import functools
+import itertools
 import math
-from collections import OrderedDict
 from dataclasses import dataclass
 
 import numpy as np
@@ -50,9 +55,8 @@ from opake_amd.pytree import (
 from opake_amd.types import PerGroup
 
 TILE = 2048  # elements per tile: the reference's blocked-reduction width
-_MAX_BATCH = 65535
-_SUPPORTED = (torch.float32, torch.bfloat16)
-_MAX_PLANS = 64
+_MAX_BATCH = 65535  # examples per launch (grid dimension of the leaf-sum pass)
+KERNEL_DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 
 _fused_clip_backend = None
 
@@ -70,115 +74,124 @@ def get_fused_clip_backend():
 
 def unsupported_reason(leaves, clipping_norm, scale, *, compute_dtype, second_moment,
                        batch_size) -> str | None:
-    """Why the kernels cannot serve this call, or ``None``."""
-    if getattr(scale, "kind", "fixed") not in ("fixed", "auto_s"):
-        return f"unknown scale kind {scale.kind!r}"
-    if compute_dtype is not None and compute_dtype != torch.float32:
-        if compute_dtype != torch.bfloat16:
-            return f"compute_dtype {compute_dtype} (supported: float32, or bfloat16 with " \
-                   "bfloat16 leaves)"
-        if any(isinstance(l, torch.Tensor) and l.dtype != torch.bfloat16 for l in leaves):
-            return "compute_dtype bfloat16 needs bfloat16 leaves"
+    """Why the leaf kernels cannot serve this call, or ``None``.
+
+    The kernels take stacked ``[B, *P]`` leaves of any of the four floating
+    dtypes on one ROCm device, any floating ``compute_dtype`` among them, the
+    fixed and AUTO-S scales, with or without the second moment."""
+    kind = getattr(scale, "kind", "fixed")
+    if kind not in ("fixed", "auto_s"):
+        return f"scale kind {kind!r} has no kernel"
+    if compute_dtype is not None and compute_dtype not in KERNEL_DTYPES:
+        return f"no kernel computes in {compute_dtype}"
     if batch_size > _MAX_BATCH:
-        return f"batch size {batch_size} exceeds {_MAX_BATCH}"
-    grad_mode = torch.is_grad_enabled()
-    for leaf in leaves:
-        if not isinstance(leaf, torch.Tensor):
-            return f"non-tensor leaf of type {type(leaf).__name__}"
-        if not leaf.is_cuda:
-            return f"leaf on device {leaf.device}, not a ROCm device"
-        if leaf.device != leaves[0].device:
-            return "the leaves span more than one device"
-        if leaf.dtype not in _SUPPORTED:
-            return f"leaf dtype {leaf.dtype} (supported: float32, bfloat16)"
-        if grad_mode and leaf.requires_grad:
-            return "a leaf requires grad"
-        if leaf.dim() == 0 or leaf.shape[0] != batch_size:
-            return "a leaf's leading dimension is not the batch"
+        return f"{batch_size} examples exceed the {_MAX_BATCH} one launch takes"
+    odd = [type(x).__name__ for x in leaves if not isinstance(x, torch.Tensor)]
+    if odd:
+        return f"the values hold non-tensor leaves ({', '.join(sorted(set(odd)))})"
+    devices = {x.device for x in leaves}
+    if len(devices) > 1:
+        return f"the leaves live on {len(devices)} devices"
+    if devices and next(iter(devices)).type != "cuda":
+        return f"the leaves live on {next(iter(devices))}, not on a ROCm device"
+    foreign = {x.dtype for x in leaves} - set(KERNEL_DTYPES)
+    if foreign:
+        return f"no kernel stores {', '.join(sorted(map(str, foreign)))} leaves"
+    if any(x.dim() == 0 or x.shape[0] != batch_size for x in leaves):
+        return f"not every leaf is stacked along the batch of {batch_size}"
+    if torch.is_grad_enabled() and any(x.requires_grad for x in leaves):
+        return "leaves that require grad (the kernels record no autograd graph)"
     return None
 
 
-def _output_dtypes(leaves, reduce_leaf):
-    """Output dtype of ``reduce_leaf`` per storage dtype (the storage dtype or float32)."""
-    out = {}
-    for dtype in {leaf.dtype for leaf in leaves}:
-        probe = reduce_leaf(torch.zeros((1,), dtype=dtype, device=leaves[0].device))
-        if probe.dtype not in (dtype, torch.float32):
-            return None
-        out[dtype] = probe.dtype
-    return out
+def _sum_dtype_of(storage: torch.dtype, compute_dtype) -> torch.dtype:
+    """Reduction dtype of a leaf's batch sum (``_resolve_compute_dtype``,
+    ``_clipped_fun.py:91-110``): the compute dtype, else float32 for 16-bit
+    storage, else the storage dtype."""
+    if compute_dtype is not None:
+        return compute_dtype
+    return torch.float32 if storage in (torch.float16, torch.bfloat16) else storage
 
 
-_PLANS: OrderedDict = OrderedDict()
+def probe_output_dtype(reduce_leaf, storage: torch.dtype, device) -> torch.dtype:
+    """The dtype ``reduce_leaf`` returns for ``storage`` values: evaluated on
+    the meta device (no data, no launch), on one element of the real device if
+    the callable cannot run there."""
+    try:
+        return reduce_leaf(torch.empty((1, 1), dtype=storage, device="meta")).dtype
+    except Exception:  # a callable that needs real data
+        return reduce_leaf(torch.zeros((1, 1), dtype=storage, device=device)).dtype
 
 
-def _plan(leaves, device):
-    """Tile tables per storage dtype, built on the host and copied once;
-    cached by device and per-example shapes (bounded LRU)."""
-    key = (device, tuple((leaf.dtype, tuple(leaf.shape[1:])) for leaf in leaves))
-    plan = _PLANS.get(key)
-    if plan is not None:
-        _PLANS.move_to_end(key)
-        return plan
-    groups = []
-    for dtype in (torch.bfloat16, torch.float32):
-        idx = [i for i, leaf in enumerate(leaves) if leaf.dtype == dtype]
-        if not idx:
+@dataclass(frozen=True)
+class _HostTiles:
+    """One storage dtype's share of a leaf list, as host tables: which leaves
+    (``members``, positions in the list), their per-example element counts,
+    where each leaf's batch sum starts in the dtype's flat output, and the
+    2048-element tiles (``tile_owner``: member index, ``tile_index``: tile
+    number inside that leaf; ``first_tile``: each member's first tile)."""
+
+    dtype: torch.dtype
+    members: tuple
+    numels: tuple
+    out_starts: tuple
+    total: int
+    n_tiles: int
+    first_tile: np.ndarray
+    tile_owner: np.ndarray
+    tile_index: np.ndarray
+
+
+@functools.lru_cache(maxsize=64)
+def _host_layout(signature: tuple) -> tuple:
+    """Tile tables of a leaf list given as ``((dtype, numel), ...)``: they
+    depend only on the element counts, not on the shapes."""
+    parts = []
+    for dtype in KERNEL_DTYPES:
+        members = tuple(i for i, (dt, _) in enumerate(signature) if dt == dtype)
+        if not members:
             continue
-        sizes = np.array([math.prod(leaves[i].shape[1:]) for i in idx], dtype=np.int64)
-        tiles = (sizes + TILE - 1) // TILE
-        tile_start = np.concatenate([[0], np.cumsum(tiles)]).astype(np.int64)
-        tile_leaf = np.repeat(np.arange(len(idx), dtype=np.int32), tiles)
-        tile_local = (np.arange(int(tile_start[-1]), dtype=np.int64) - tile_start[tile_leaf]).astype(
-            np.int32)
-        offsets = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
-
-        def dev(a):
-            return torch.from_numpy(np.ascontiguousarray(a)).to(device)
-
-        groups.append({
-            "dtype": dtype,
-            "idx": idx,
-            "sizes_host": sizes.tolist(),
-            "offsets_host": offsets.tolist(),
-            "total": int(sizes.sum()),
-            "n_tiles": int(tile_start[-1]),
-            "sizes": dev(sizes),
-            "out_offs": dev(offsets),
-            "leaf_col": dev(np.array(idx, dtype=np.int32)),
-            "tile_start": dev(tile_start),
-            "tile_leaf": dev(tile_leaf),
-            "tile_local": dev(tile_local),
-        })
-    plan = {"groups": groups, "n_leaves": len(leaves)}
-    _PLANS[key] = plan
-    if len(_PLANS) > _MAX_PLANS:
-        _PLANS.popitem(last=False)
-    return plan
+        numels = tuple(signature[i][1] for i in members)
+        per_leaf = [-(-n // TILE) for n in numels]
+        first = np.fromiter(itertools.accumulate(per_leaf, initial=0), dtype=np.int64,
+                            count=len(per_leaf) + 1)
+        owner = np.repeat(np.arange(len(numels), dtype=np.int32), per_leaf)
+        index = (np.arange(first[-1], dtype=np.int64) - first[owner]).astype(np.int32)
+        starts = tuple(itertools.accumulate(numels[:-1], initial=0))
+        parts.append(_HostTiles(dtype=dtype, members=members, numels=numels, out_starts=starts,
+                                total=sum(numels), n_tiles=int(first[-1]), first_tile=first,
+                                tile_owner=owner, tile_index=index))
+    return tuple(parts)
 
 
-_MARKERS: dict = {}
+class _DeviceTiles:
+    """A :class:`_HostTiles` with its tables on the device (content-cached
+    device tables, so a HIP graph that captures a call keeps them alive)."""
 
-
-def _dtype_marker(leaf):
-    key = (leaf.dtype, leaf.device)
-    marker = _MARKERS.get(key)
-    if marker is None:
-        marker = _MARKERS[key] = leaf.new_zeros(())
-    return marker
+    def __init__(self, host: _HostTiles, device):
+        self.host = host
+        self.dtype = host.dtype
+        self.numel_t = device_table(host.numels, np.int64, device)
+        self.out_start_t = device_table(host.out_starts, np.int64, device)
+        self.column_t = device_table(host.members, np.int32, device)
+        self.first_tile_t = device_table(host.first_tile, np.int64, device)
+        self.tile_owner_t = device_table(host.tile_owner, np.int32, device)
+        self.tile_index_t = device_table(host.tile_index, np.int32, device)
 
 
 @dataclass
 class LeafClipResult:
     """Outputs of :func:`leaves_clip_sum` (device tensors, nothing synchronised).
 
-    ``reduced``: per-leaf batch sums.  ``norms``: float32 [B] global norms.
-    ``post_sq``: float32 [B] ``||stored||^2`` or ``None``.  ``nclipped``:
-    int32 [1] examples with norm > C (global clipping) or [G] per group.
-    ``group_norms``: float32 [G, B] (per-group clipping) or ``None``.
-    ``scales``: float32 scale rows per storage dtype, [G, B] (G = 1 without groups).
-    ``squared``: per-leaf batch sums of the squared stored values (second
-    moment) or ``None``.
+    ``reduced``: per-leaf batch sums.  ``norms``: [B] global norms in the
+    reduction dtype.  ``post_sq``: float64 [B] ``||stored||^2`` or ``None``.
+    ``nclipped``: int32 [1] examples with norm > C (global clipping) or [G] per
+    group.  ``group_norms``: [G, B] (per-group clipping) or ``None``.
+    ``scales``: float32 scale rows per storage dtype, [G, B] (G = 1 without
+    groups), converted to that dtype's multiply dtype; ``scales64``: the
+    float64 rows of the dtypes whose multiply dtype is float64.  ``squared``:
+    per-leaf batch sums of the squared stored values (second moment) or
+    ``None``.
     """
 
     reduced: list
@@ -188,6 +201,7 @@ class LeafClipResult:
     group_norms: torch.Tensor | None
     scales: dict
     squared: list | None = None
+    scales64: dict | None = None
 
 
 class LeafBatch:
@@ -200,65 +214,86 @@ class LeafBatch:
         self.device = self.leaves[0].device
         self.B = self.leaves[0].shape[0]
         self.L = len(self.leaves)
-        self.plan = _plan(self.leaves, self.device)
-        self.ptr_tables = [pointer_table([self.leaves[i] for i in g["idx"]], self.device)
-                           for g in self.plan["groups"]]
+        signature = tuple((l.dtype, math.prod(l.shape[1:])) for l in self.leaves)
+        self.parts = [_DeviceTiles(h, self.device) for h in _host_layout(signature)]
+        self.ptr_tables = [pointer_table([self.leaves[i] for i in p.host.members], self.device)
+                           for p in self.parts]
 
     @property
     def dtypes(self):
-        return [g["dtype"] for g in self.plan["groups"]]
+        return [p.dtype for p in self.parts]
 
     def sqnorms(self, acc_dtype: torch.dtype = torch.float32) -> torch.Tensor:
         """Per-leaf squared norms float64 [B, L] (``_leaf_sq_sum``: sanitised,
-        squared in ``acc_dtype`` -- float32, or bfloat16 for bfloat16 leaves --
-        summed in float64 per 2048-element tile)."""
+        converted to ``acc_dtype`` and squared there -- the reference's
+        reduction dtype, any of the four floating dtypes -- summed in float64
+        per 2048-element tile)."""
         B, L = self.B, self.L
         stream = nat.stream_handle(self.device)
         leaf_sq = torch.empty((B, L), dtype=torch.float64, device=self.device)
-        for g, ptrs in zip(self.plan["groups"], self.ptr_tables):
-            partial = torch.empty((B, max(g["n_tiles"], 1)), dtype=torch.float64, device=self.device)
-            nat.call("dpc_leaves_sqnorm", nat.ptr(ptrs), nat.ptr(g["sizes"]),
-                     nat.ptr(g["tile_leaf"]), nat.ptr(g["tile_local"]), nat.ptr(g["tile_start"]),
-                     nat.ptr(g["leaf_col"]), len(g["idx"]), g["n_tiles"], B,
-                     nat.dtype_code(g["dtype"]), nat.dtype_code(acc_dtype), nat.ptr(partial),
-                     nat.ptr(leaf_sq), L, stream)
+        for p, ptrs in zip(self.parts, self.ptr_tables):
+            h = p.host
+            partial = torch.empty((B, max(h.n_tiles, 1)), dtype=torch.float64, device=self.device)
+            nat.call("dpc_leaves_sqnorm", nat.ptr(ptrs), nat.ptr(p.numel_t),
+                     nat.ptr(p.tile_owner_t), nat.ptr(p.tile_index_t), nat.ptr(p.first_tile_t),
+                     nat.ptr(p.column_t), len(h.members), h.n_tiles, B,
+                     nat.dtype_code(p.dtype, wide=True), nat.dtype_code(acc_dtype, wide=True),
+                     nat.ptr(partial), nat.ptr(leaf_sq), L, stream)
         return leaf_sq
 
-    def apply(self, scale_rows: dict, leaf_rows=None, out_dtypes=None, with_postsq=False,
-              second_moment=False):
+    def apply(self, scale_rows: dict, leaf_rows=None, sum_dtypes=None, with_postsq=False,
+              second_moment=False, mult_dtypes=None, scale64_rows=None):
         """Scale-store-sum over the batch: leaf l of storage dtype t uses row
-        ``leaf_rows[l]`` (default 0) of ``scale_rows[t]`` (float32 [R, B]).
-        Returns ``(reduced, post_sq)``; ``post_sq`` is float32 [B] or None.
-        With ``second_moment`` also the batch sums of the squared stored values:
+        ``leaf_rows[l]`` (default 0) of ``scale_rows[t]`` (float32 [R, B],
+        converted to t's multiply dtype ``mult_dtypes[t]``, default
+        ``promote(t, float32)``; float64 multiplies read ``scale64_rows[t]``).
+        ``sum_dtypes[t] = (A, O)``: the batch sum's reduction and output dtypes
+        (default: :func:`_sum_dtype_of` and the storage dtype).  Returns
+        ``(reduced, post_sq)`` (``post_sq`` float64 [B] or None), with
+        ``second_moment`` also the batch sums of the squared stored values:
         ``(reduced, post_sq, squared)``."""
         B = self.B
         stream = nat.stream_handle(self.device)
         reduced = [None] * self.L
         squared = [None] * self.L
-        post_sq = torch.zeros(B, dtype=torch.float32, device=self.device) if with_postsq else None
-        for g, ptrs in zip(self.plan["groups"], self.ptr_tables):
-            dtype = g["dtype"]
-            out_dtype = (out_dtypes or {}).get(dtype, dtype)
-            flat = torch.empty(g["total"], dtype=out_dtype, device=self.device)
+        post_sq = torch.zeros(B, dtype=torch.float64, device=self.device) if with_postsq else None
+        for p, ptrs in zip(self.parts, self.ptr_tables):
+            h, dtype = p.host, p.dtype
+            acc, out_dtype = (sum_dtypes or {}).get(dtype, (_sum_dtype_of(dtype, None), dtype))
+            mult = (mult_dtypes or {}).get(dtype, torch.promote_types(dtype, torch.float32))
+            flat = torch.empty(h.total, dtype=out_dtype, device=self.device)
             flat_sq = torch.empty_like(flat) if second_moment else None
-            # Four partials per tile (one per wave of the apply kernel).
-            tile_sq = (torch.empty((B, 4 * g["n_tiles"]), dtype=torch.float32, device=self.device)
-                       if with_postsq else None)
-            rows = scale_rows[dtype]
             leaf_row = None
             if leaf_rows is not None:
-                idx_rows = [leaf_rows[i] for i in g["idx"]]
-                leaf_row = _device_table(self.device, ("leaf_row", dtype, tuple(idx_rows)),
-                                         idx_rows, np.int32)
-            nat.call("dpc_leaves_apply", nat.ptr(ptrs), nat.ptr(g["sizes"]),
-                     nat.ptr(g["tile_leaf"]), nat.ptr(g["tile_local"]), nat.ptr(g["out_offs"]),
-                     g["n_tiles"], B, nat.dtype_code(dtype), nat.ptr(rows), nat.ptr(leaf_row),
-                     nat.ptr(flat), nat.ptr(flat_sq), nat.dtype_code(out_dtype), nat.ptr(tile_sq),
-                     stream)
+                leaf_row = device_table([leaf_rows[i] for i in h.members], np.int32, self.device)
+            # The fp32 kernel: fp32 multiply and sum, output in the storage dtype or fp32.
+            fast = (dtype in (torch.float32, torch.bfloat16) and mult == torch.float32
+                    and acc == torch.float32 and out_dtype in (dtype, torch.float32))
+            # Per (example, tile) partials of ||stored||^2, one per wave of the apply kernel.
+            tile_sq = (torch.empty((B, 4 * h.n_tiles), device=self.device,
+                                   dtype=torch.float32 if fast else torch.float64)
+                       if with_postsq else None)
+            if fast:
+                nat.call("dpc_leaves_apply", nat.ptr(ptrs), nat.ptr(p.numel_t),
+                         nat.ptr(p.tile_owner_t), nat.ptr(p.tile_index_t), nat.ptr(p.out_start_t),
+                         h.n_tiles, B, nat.dtype_code(dtype), nat.ptr(scale_rows[dtype]),
+                         nat.ptr(leaf_row), nat.ptr(flat), nat.ptr(flat_sq),
+                         nat.dtype_code(out_dtype), nat.ptr(tile_sq), stream)
+            else:
+                rows64 = (scale64_rows or {}).get(dtype) if mult == torch.float64 else None
+                if mult == torch.float64 and rows64 is None:
+                    raise ConfigurationError("a float64 multiply needs the float64 scale rows")
+                nat.call("dpc_leaves_apply_ex", nat.ptr(ptrs), nat.ptr(p.numel_t),
+                         nat.ptr(p.tile_owner_t), nat.ptr(p.tile_index_t), nat.ptr(p.out_start_t),
+                         h.n_tiles, B, nat.dtype_code(dtype, wide=True),
+                         nat.dtype_code(mult, wide=True), nat.dtype_code(acc, wide=True),
+                         nat.ptr(scale_rows[dtype]), nat.ptr(rows64), nat.ptr(leaf_row),
+                         nat.ptr(flat), nat.ptr(flat_sq), nat.dtype_code(out_dtype, wide=True),
+                         nat.ptr(tile_sq), stream)
             if with_postsq:
-                post_sq += tile_sq.sum(dim=1)
-            for j, i in enumerate(g["idx"]):
-                off, n = g["offsets_host"][j], g["sizes_host"][j]
+                post_sq += tile_sq.sum(dim=1, dtype=torch.float64)
+            for j, i in enumerate(h.members):
+                off, n = h.out_starts[j], h.numels[j]
                 reduced[i] = flat[off:off + n].view(self.leaves[i].shape[1:])
                 if second_moment:
                     squared[i] = flat_sq[off:off + n].view(self.leaves[i].shape[1:])
@@ -268,22 +303,23 @@ class LeafBatch:
 
 
 def leaves_clip_sum(leaves, clipping_norm, *, kind: str = "fixed", gamma: float = 0.0,
-                    with_postsq: bool = False, out_dtypes=None, leaf_groups=None,
+                    with_postsq: bool = False, sum_dtypes=None, leaf_groups=None,
                     conservative: bool = True, second_moment: bool = False,
                     compute_dtype: torch.dtype | None = None):
     """Clip-and-sum of stacked leaves ``[B, *P]`` with the HIP kernels.
 
     ``clipping_norm`` is one bound, or -- with ``leaf_groups`` (group index of
     each leaf) -- a list of per-group bounds: each group is clipped to its own
-    bound by its own norm (``_streaming.py:63-104``).  Batch sums come out in
-    ``out_dtypes[dtype]`` (default: the leaf dtype).  ``conservative`` rounds
-    each bound down to float32 first, as the reference's batch path does
-    (``_clipped_fun.py:211-216``); the single-pytree functions use the exact
-    bound (``_pytree.py:624-628``).  ``compute_dtype`` (float32, or bfloat16
-    with bfloat16 leaves) is the reference's explicit reduction dtype
-    (``_pytree.py:84-108``): squares in it, the guard's roundoff from it, and
-    the scale multiply in ``promote(leaf dtype, compute_dtype)`` (``_pytree.py:
-    160-187``).  See :class:`LeafClipResult`.
+    bound by its own norm (``_streaming.py:63-104``).  ``sum_dtypes[dtype] =
+    (reduction dtype, output dtype)`` of the batch sums (default: the
+    reference's reduction dtype for that storage dtype, output in the storage
+    dtype).  ``conservative`` rounds each bound down to float32 first, as the
+    reference's batch path does (``_clipped_fun.py:211-216``); the
+    single-pytree functions use the exact bound (``_pytree.py:624-628``).
+    ``compute_dtype`` (any of the four floating dtypes) is the reference's
+    explicit reduction dtype (``_pytree.py:84-108``): squares in it, the
+    guard's roundoff from it, and the scale multiply in ``promote(leaf dtype,
+    compute_dtype)`` (``_pytree.py:160-187``).  See :class:`LeafClipResult`.
     """
     batch = LeafBatch(leaves)
     device, B, L = batch.device, batch.B, batch.L
@@ -297,15 +333,12 @@ def leaves_clip_sum(leaves, clipping_norm, *, kind: str = "fixed", gamma: float 
     leaf_sq = batch.sqnorms(acc)
     sq = torch.empty(B, dtype=torch.float64, device=device)
     nat.call("dpc_row_sum_f64", nat.ptr(leaf_sq), B, L, 0, nat.ptr(sq), stream)
-    guards = []
-    for dt in batch.dtypes:
-        mult = torch.promote_types(dt, acc)
-        guards.append((*num.guard_constants(dt, mult, roundoff), mult == torch.bfloat16))
+    mults = {dt: torch.promote_types(dt, acc) for dt in batch.dtypes}
+    guards = [(*num.guard_constants(dt, mults[dt], roundoff), mults[dt]) for dt in batch.dtypes]
     scale_kind = nat.SCALE_AUTO_S if kind == "auto_s" else nat.SCALE_FIXED
     bound_of = num.conservative_bound if conservative else float
     if grouped:
-        col_group = _device_table(device, ("col_group", tuple(leaf_groups)), leaf_groups,
-                                  np.int32)
+        col_group = device_table(leaf_groups, np.int32, device)
         group_sq = torch.empty((n_groups, B), dtype=torch.float64, device=device)
         nat.call("dpc_group_sum_f64", nat.ptr(leaf_sq), B, L, L, nat.ptr(col_group), n_groups,
                  nat.ptr(group_sq), stream)
@@ -313,28 +346,36 @@ def leaves_clip_sum(leaves, clipping_norm, *, kind: str = "fixed", gamma: float 
                                 kind=scale_kind, gamma=gamma,
                                 count_threshold=num.float32_of(bounds[k]))
                for k in range(n_groups)]
-        norms = torch.sqrt(sq).to(torch.float32)
-        group_norms = torch.stack([cf.norms for cf in cfs])
+        # The clip kernel's norms are (float)sqrt(sq): the diagnostic when the
+        # reduction dtype is float32 (_streaming.py:174-180).
+        if acc == torch.float32:
+            norms = torch.sqrt(sq).to(acc)
+            group_norms = torch.stack([cf.norms for cf in cfs])
+        else:
+            norms = torch.sqrt(sq).to(acc)
+            group_norms = torch.sqrt(group_sq).to(acc)
         nclipped = torch.cat([cf.nclipped for cf in cfs])
     else:
         cfs = [ops.clip_factors(sq, bound_of(bounds[0]), guards, kind=scale_kind,
                                 gamma=gamma, count_threshold=num.float32_of(bounds[0]))]
-        norms, group_norms, nclipped = cfs[0].norms, None, cfs[0].nclipped
-    scales = {}
+        norms = cfs[0].norms if acc == torch.float32 else torch.sqrt(sq).to(acc)
+        group_norms, nclipped = None, cfs[0].nclipped
+    scales, scales64 = {}, {}
     for gi, dtype in enumerate(batch.dtypes):
-        scales[dtype] = (torch.stack([cf.scale[gi] for cf in cfs]) if grouped
-                         else cfs[0].scale[gi:gi + 1])
-    out = batch.apply(scales, leaf_groups if grouped else None, out_dtypes, with_postsq,
-                      second_moment=second_moment)
+        scales[dtype] = torch.stack([cf.scale[gi] for cf in cfs])
+        if mults[dtype] == torch.float64:
+            scales64[dtype] = torch.stack([cf.scale64[gi] for cf in cfs])
+    if sum_dtypes is None:
+        sum_dtypes = {dt: (_sum_dtype_of(dt, compute_dtype), dt) for dt in batch.dtypes}
+    out = batch.apply(scales, leaf_groups if grouped else None, sum_dtypes, with_postsq,
+                      second_moment=second_moment, mult_dtypes=mults, scale64_rows=scales64)
     reduced, post_sq = out[0], out[1]
+    if post_sq is not None:
+        post_sq = post_sq.to(acc)
     return LeafClipResult(reduced=reduced, norms=norms, post_sq=post_sq, nclipped=nclipped,
                           group_norms=group_norms, scales=scales,
-                          squared=out[2] if second_moment else None)
-
-
-def _device_table(device, key, values, np_dtype):
-    """Small immutable index tables on the device (cached by content)."""
-    return device_table(values, np_dtype, device)
+                          squared=out[2] if second_moment else None,
+                          scales64=scales64 or None)
 
 
 def _group_layout(paths, clipping_norm):
@@ -374,18 +415,6 @@ def make_fused_backend(fallback=None):
         leaves, treedef = tree_flatten(values)
         reason = unsupported_reason(leaves, clipping_norm, scale, compute_dtype=compute_dtype,
                                     second_moment=second_moment, batch_size=batch_size)
-        out_dtypes = None
-        cast_to = None
-        if reason is None and leaves and batch_size > 0:
-            if compute_dtype == torch.bfloat16:
-                # The reference sums in the compute dtype and casts after
-                # (_sum_clipped_tensor, _clipped_fun.py:114-132).
-                cast_to = {torch.bfloat16: reduce_leaf(
-                    torch.zeros((1,), dtype=torch.bfloat16, device=leaves[0].device)).dtype}
-            else:
-                out_dtypes = _output_dtypes(leaves, reduce_leaf)
-                if out_dtypes is None:
-                    reason = "the requested output dtype is not supported"
         if reason is not None:
             if fallback is None:
                 raise OperationError(f"HIP clip-and-sum cannot serve this call: {reason}")
@@ -393,35 +422,35 @@ def make_fused_backend(fallback=None):
                             reduce_leaf=reduce_leaf, compute_dtype=compute_dtype,
                             second_moment=second_moment, return_aux=return_aux,
                             return_stats=return_stats)
-        kind = getattr(scale, "kind", "fixed")
-        gamma = float(getattr(scale, "gamma", 0.0))
+        device = leaves[0].device if leaves else torch.device("cuda")
+        storage = sorted({l.dtype for l in leaves}, key=str)
+        # One shared 0-d zero per storage dtype carries the leaves' dtypes.
+        zero_of = {dt: torch.zeros((), dtype=dt, device=device) for dt in storage}
         grouped = isinstance(clipping_norm, PerGroup)
         names = None
         if not leaves or batch_size == 0:
-            device = leaves[0].device if leaves else torch.device("cuda")
             reduced = [reduce_leaf(l) for l in leaves]
             squared = [reduce_leaf(l) for l in leaves] if second_moment else None
             norms = torch.zeros(batch_size, dtype=torch.float32, device=device)
             post = norms.clone()
             group_norms = None
         else:
+            # Batch sums: reduced in the reference's reduction dtype for the
+            # storage dtype, returned in the dtype `reduce_leaf` produces.
+            sum_dtypes = {dt: (_sum_dtype_of(dt, compute_dtype),
+                               probe_output_dtype(reduce_leaf, dt, device)) for dt in storage}
+            kind = getattr(scale, "kind", "fixed")
+            gamma = float(getattr(scale, "gamma", 0.0))
+            common = dict(kind=kind, gamma=gamma, with_postsq=return_aux, sum_dtypes=sum_dtypes,
+                          second_moment=second_moment, compute_dtype=compute_dtype)
             if grouped:
                 paths, _, _ = tree_flatten_with_paths(values)
                 names, leaf_groups, bounds = _group_layout(paths, clipping_norm)
-                res = leaves_clip_sum(leaves, bounds, kind=kind, gamma=gamma,
-                                      with_postsq=return_aux, out_dtypes=out_dtypes,
-                                      leaf_groups=leaf_groups, second_moment=second_moment,
-                                      compute_dtype=compute_dtype)
+                res = leaves_clip_sum(leaves, bounds, leaf_groups=leaf_groups, **common)
             else:
-                res = leaves_clip_sum(leaves, float(clipping_norm), kind=kind, gamma=gamma,
-                                      with_postsq=return_aux, out_dtypes=out_dtypes,
-                                      second_moment=second_moment, compute_dtype=compute_dtype)
+                res = leaves_clip_sum(leaves, float(clipping_norm), **common)
             reduced, norms, post, group_norms = res.reduced, res.norms, res.post_sq, res.group_norms
             squared = res.squared
-            if cast_to is not None:
-                reduced = [x.to(cast_to[l.dtype]) for x, l in zip(reduced, leaves)]
-                if second_moment:
-                    squared = [x.to(cast_to[l.dtype]) for x, l in zip(squared, leaves)]
         diagnostics = {}
         if return_aux or return_stats:
             diagnostics["norms"] = norms.detach()
@@ -429,7 +458,7 @@ def make_fused_backend(fallback=None):
                 diagnostics["group_norms"] = {n: group_norms[k].detach() for k, n in enumerate(names)}
         if return_aux:
             diagnostics["clipped_norms"] = torch.sqrt(post).detach()
-        markers = [_dtype_marker(l) for l in leaves]
+        markers = [zero_of[l.dtype] for l in leaves]
         return (
             tree_unflatten(treedef, reduced),
             tree_unflatten(treedef, markers),
@@ -450,6 +479,7 @@ __all__ = [
     "LeafClipResult",
     "leaves_clip_sum",
     "make_fused_backend",
+    "probe_output_dtype",
     "register_fused_clip_backend",
     "unsupported_reason",
 ]

@@ -59,7 +59,7 @@ from opake_amd import ops
 from opake_amd._tables import device_table
 from opake_amd.clipping import _numerics as num
 from opake_amd.clipping._clipped_fun import FixedClipState
-from opake_amd.clipping._leaves import LeafBatch
+from opake_amd.clipping._leaves import LeafBatch, _sum_dtype_of
 from opake_amd.exceptions import ConfigurationError, InputTypeError
 from opake_amd.noise import GaussianNoiseState, step_key_for
 from opake_amd.pytree import param_path
@@ -315,6 +315,17 @@ def ghost_clip_captured(
         raise ConfigurationError(f"normalize_by must be > 0, got {normalize_by}.")
     if not captures:
         raise ConfigurationError("no layers to clip")
+    if noise_fn is not None and noise_fn.compute_dtype != torch.float32:
+        # The epilogues add noise in float32; another compute dtype adds it
+        # after the clipped sums, through noise_fn itself.
+        if noise_state is None:
+            raise ConfigurationError("noise_state is required with noise_fn")
+        out = ghost_clip_captured(captures, clipping_norm=clipping_norm,
+                                  normalize_by=normalize_by, dtype=dtype,
+                                  return_aux=return_aux, gemm_events=gemm_events)
+        res, aux = out if return_aux else (out, None)
+        res, next_state = noise_fn(res, noise_state)
+        return ((res, aux) if return_aux else res), next_state
     max_norm = clipping_norm / normalize_by
     per_group = isinstance(clipping_norm, PerGroup)
     direct = {}
@@ -495,8 +506,6 @@ def ghost_clip_captured(
         std = noise_fn.clipped_stddev(clipped(None, max_norm=max_norm))
         noisy = any((std.for_path(param_path(n)) if isinstance(std, PerGroup) else std) != 0.0
                     for n in leaf_names)
-        if noisy and noise_fn.compute_dtype != torch.float32:
-            raise ConfigurationError("fused noise supports compute_dtype float32 only")
         step_key = step_key_for(noise_state)
         if noisy and noise_fn.stream == "reference":
             gen = generator_from_key(step_key)
@@ -604,9 +613,10 @@ def ghost_clip_captured(
     if direct_batch is not None:
         scale_rows = {dt: torch.stack([cf.scale[storage.index(dt)] for cf in cfs])
                       for dt in direct_batch.dtypes}
-        out_dtypes = {dt: dtype for dt in direct_batch.dtypes} if dtype is not None else None
+        sum_dtypes = ({dt: (_sum_dtype_of(dt, None), dtype) for dt in direct_batch.dtypes}
+                      if dtype is not None else None)
         reduced, _ = direct_batch.apply(scale_rows, [leaf_group[n] for n in direct_names],
-                                        out_dtypes)
+                                        sum_dtypes)
         philox = {}
         for n, x in zip(direct_names, reduced):
             if normalize_by != 1.0:

@@ -40,8 +40,6 @@ class _Kind:
 
 def _scale_one(pytree: Any, bound, kind: _Kind, *, return_zero: bool,
                compute_dtype) -> tuple[Any, ClipPytreeAux]:
-    if compute_dtype is not None:
-        raise OperationError("an explicit compute_dtype is not implemented by the HIP kernels")
     paths, flat, treedef = tree_flatten_with_paths(pytree)
     positions = [i for i, x in enumerate(flat) if isinstance(x, torch.Tensor)]
     leaves = [flat[i] for i in positions]
@@ -54,16 +52,20 @@ def _scale_one(pytree: Any, bound, kind: _Kind, *, return_zero: bool,
     stacked = [leaf.detach().unsqueeze(0) for leaf in leaves]
     if any(leaf.requires_grad for leaf in leaves) and torch.is_grad_enabled():
         raise OperationError("HIP clip_pytree does not differentiate through the clip")
-    reason = unsupported_reason(stacked, 1.0, kind, compute_dtype=None, second_moment=False,
-                                batch_size=1)
+    reason = unsupported_reason(stacked, 1.0, kind, compute_dtype=compute_dtype,
+                                second_moment=False, batch_size=1)
     if reason is not None:
         raise OperationError(f"HIP clip_pytree cannot serve this call: {reason}")
+    # One example: its "batch sum" is the stored value itself, kept in the
+    # storage dtype.
+    keep = {leaf.dtype: (leaf.dtype, leaf.dtype) for leaf in leaves}
     if grouped:
         res = leaves_clip_sum(stacked, bounds, kind=kind.kind, gamma=kind.gamma,
-                              leaf_groups=leaf_groups, conservative=False)
+                              leaf_groups=leaf_groups, conservative=False, sum_dtypes=keep,
+                              compute_dtype=compute_dtype)
     else:
         res = leaves_clip_sum(stacked, float(bound), kind=kind.kind, gamma=kind.gamma,
-                              conservative=False)
+                              conservative=False, sum_dtypes=keep, compute_dtype=compute_dtype)
     out = list(flat)
     for j, i in enumerate(positions):
         out[i] = torch.zeros_like(leaves[j]) if return_zero else res.reduced[j]

@@ -8,8 +8,10 @@
 //   up = sqrt(max(sq + err, 0));  norm = sqrt(max(sq, 0))
 //   ratio = max(C,0)/up  or  max(R,0)/(up + gamma)               (AUTO-S)
 //   s = ratio * rel - abs;  s = min(1, s) (fixed only; NaN stays NaN)
-//   s = isfinite(s) ? max(s, 0) : 0;  stored as float32 (or, for a guard whose
-//   multiply dtype is bf16, rounded to the nearest bf16 first).
+//   s = isfinite(s) ? max(s, 0) : 0;  stored as float32, or as the value of
+//   the guard's multiply dtype (scale.to(multiply_dtype): for bfloat16 and
+//   float16 through float32, as torch converts a float64); `scale64` (when
+//   given) keeps s itself for float64 guards.
 // `norm` (the estimate) is what the statistics report and count.  Every step
 // is one IEEE operation in the order written (contraction off), so the result
 // matches a host float64 evaluation bit for bit.
@@ -24,20 +26,16 @@ constexpr int kMaxGuards = 4;
 struct Guards {
   double rel[kMaxGuards];
   double abs_[kMaxGuards];
-  int bf16[kMaxGuards];  // scale stored as a bf16 value (multiply in bf16)
+  int mult[kMaxGuards];  // the multiply dtype the scale is converted to
 };
 
-// A non-negative double rounded to the nearest bf16 (ties to even), returned
-// as the float of that value: rounded to float32 with round-to-odd first
-// (float32 keeps 16 more bits than bf16, so the second rounding is exact).
-__device__ float round_scale_to_bf16(double s) {
-  float f = (float)s;
-  if ((double)f != s && f != 0.0f) {
-    uint32_t u = __builtin_bit_cast(uint32_t, f);
-    if ((u & 1u) == 0u) u = ((double)f > s) ? u - 1u : u + 1u;
-    f = __builtin_bit_cast(float, u);
-  }
-  return round_to_bf16(f);
+// s.to(multiply dtype) as a float: torch converts a float64 to bfloat16 or
+// float16 through float32 (each step to nearest even).
+__device__ float scale_in(double s, int mult) {
+  const float f = (float)s;
+  if (mult == DPC_BF16) return round_to_bf16(f);
+  if (mult == DPC_F16) return round_to_f16(f);
+  return f;
 }
 
 #pragma clang fp contract(off)
@@ -61,8 +59,8 @@ __global__ void __launch_bounds__(kClipThreads)
 clip_factors_kernel(const double* __restrict__ sqnorm, const double* __restrict__ sqerr, int B,
                     double C, int kind, double gamma, Guards guards, int n_guards,
                     float count_threshold, float* __restrict__ scale,
-                    float* __restrict__ norms_out, int* __restrict__ nclipped,
-                    void* __restrict__ plans) {
+                    double* __restrict__ scale64, float* __restrict__ norms_out,
+                    int* __restrict__ nclipped, void* __restrict__ plans) {
   __shared__ int wave_counts[kClipThreads / 64];
   __shared__ int clipped_counts[kClipThreads / 64];
   __shared__ int slow_counts[kClipThreads / 64];
@@ -90,8 +88,9 @@ clip_factors_kernel(const double* __restrict__ sqnorm, const double* __restrict_
         double norm;
         const double s = guarded_scale(sqnorm[i], sqerr ? sqerr[i] : 0.0, C, kind, gamma,
                                        guards.rel[g], guards.abs_[g], &norm);
-        const float sf = guards.bf16[g] ? round_scale_to_bf16(s) : (float)s;
+        const float sf = scale_in(s, guards.mult[g]);
         if (scale) scale[(size_t)g * B + i] = sf;
+        if (scale64) scale64[(size_t)g * B + i] = guards.mult[g] == DPC_F64 ? s : (double)sf;
         if (g == 0) {
           if (norms_out) norms_out[i] = (float)norm;
           if ((float)norm > count_threshold) ++clipped_local;
@@ -145,9 +144,9 @@ extern "C" size_t dpc_clip_plan_bytes(int B) { return clip_plan_bytes(B); }
 extern "C" int dpc_clip_factors(const double* sqnorm, const double* sqerr, int B, double C,
                                 int kind, double gamma,
                                 const double* guard_rel, const double* guard_abs,
-                                const int* guard_bf16, int n_guards, float count_threshold,
-                                float* scale, float* norms_out, int* nclipped, void* plan,
-                                void* stream) {
+                                const int* guard_mult, int n_guards, float count_threshold,
+                                float* scale, double* scale64, float* norms_out, int* nclipped,
+                                void* plan, void* stream) {
   if (B < 0 || n_guards < 1 || n_guards > kMaxGuards || !guard_rel || !guard_abs) {
     return DPC_EINVAL;
   }
@@ -158,11 +157,12 @@ extern "C" int dpc_clip_factors(const double* sqnorm, const double* sqerr, int B
   for (int g = 0; g < n_guards; ++g) {
     guards.rel[g] = guard_rel[g];
     guards.abs_[g] = guard_abs[g];
-    guards.bf16[g] = guard_bf16 ? guard_bf16[g] != 0 : 0;
+    guards.mult[g] = guard_mult ? guard_mult[g] : DPC_F32;
+    if (!known_dtype(guards.mult[g])) return DPC_EINVAL;
   }
   hipLaunchKernelGGL(clip_factors_kernel, dim3(1), dim3(kClipThreads), 0, (hipStream_t)stream,
                      sqnorm, sqerr, B, C, kind, gamma, guards, n_guards, count_threshold,
-                     scale, norms_out, nclipped, plan);
+                     scale, scale64, norms_out, nclipped, plan);
   DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;
 }

@@ -166,6 +166,90 @@ DPC_HOST_DEVICE float finite_or_zero(float x) {
 DPC_HOST_DEVICE int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 // ---------------------------------------------------------------------------
+// The four element types of the materialised-leaf and noise passes, carried
+// as double.  Conversions follow torch's: to float16 / bfloat16 from a wider
+// type goes through float32 (c10's Half(float) / BFloat16(float)), each step
+// rounding to nearest even, overflow to infinity and subnormals kept.
+// ---------------------------------------------------------------------------
+DPC_DEVICE double load_as_f64(const void* base, int64_t idx, int dtype) {
+  switch (dtype) {
+    case DPC_BF16:
+      return (double)bf16_bits_to_f32(global_ptr<const uint16_t>(base)[idx]);
+    case DPC_F16:
+      return (double)(float)global_ptr<const _Float16>(base)[idx];
+    case DPC_F64:
+      return global_ptr<const double>(base)[idx];
+    default:
+      return (double)global_ptr<const float>(base)[idx];
+  }
+}
+
+// A float the compiler must take as given: without it, a float64 -> float32
+// -> float16 chain is folded into one float64 -> float16 conversion, which
+// rounds once where torch rounds twice.
+DPC_DEVICE float opaque_f32(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// float -> float16 -> float, rounding to nearest even (v_cvt_f16_f32).
+DPC_DEVICE float round_to_f16(float f) { return (float)(_Float16)opaque_f32(f); }
+
+// v rounded to `dtype` (and widened back).
+DPC_DEVICE double round_to_dtype(double v, int dtype) {
+  switch (dtype) {
+    case DPC_BF16:
+      return (double)round_to_bf16((float)v);
+    case DPC_F16:
+      return (double)round_to_f16((float)v);
+    case DPC_F64:
+      return v;
+    default:
+      return (double)(float)v;
+  }
+}
+
+// Stores v, which must already be a value of `dtype` (round_to_dtype).
+DPC_DEVICE void store_from_f64(void* base, int64_t idx, double v, int dtype) {
+  switch (dtype) {
+    case DPC_BF16:
+      global_ptr<uint16_t>(base)[idx] = f32_to_bf16_bits((float)v);
+      break;
+    case DPC_F16:
+      global_ptr<_Float16>(base)[idx] = (_Float16)opaque_f32((float)v);
+      break;
+    case DPC_F64:
+      global_ptr<double>(base)[idx] = v;
+      break;
+    default:
+      global_ptr<float>(base)[idx] = (float)v;
+  }
+}
+
+DPC_HOST_DEVICE int dtype_bytes(int dtype) {
+  return dtype == DPC_F64 ? 8 : (dtype == DPC_F32 ? 4 : 2);
+}
+
+DPC_HOST_DEVICE bool known_dtype(int dtype) {
+  return dtype == DPC_F32 || dtype == DPC_BF16 || dtype == DPC_F16 || dtype == DPC_F64;
+}
+
+// Smallest positive normal value of `dtype` (torch.finfo(dtype).smallest_normal).
+DPC_HOST_DEVICE double smallest_normal_of(int dtype) {
+  switch (dtype) {
+    case DPC_F16:
+      return 6.103515625e-05;  // 2^-14
+    case DPC_F64:
+      return 2.2250738585072014e-308;  // 2^-1022
+    default:
+      return 1.1754943508222875e-38;  // 2^-126
+  }
+}
+
+// torch.nan_to_num(x, nan=0, posinf=0, neginf=0) of a value held as double.
+DPC_HOST_DEVICE double finite_or_zero_f64(double x) { return isfinite(x) ? x : 0.0; }
+
+// ---------------------------------------------------------------------------
 // Error model of the Gram-norm kernels (the bound that makes the ghost clip
 // sound: the clip factor is taken from sqnorm + sqerr >= ||G_i^T A_i||^2).
 //

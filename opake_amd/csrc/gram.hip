@@ -1459,7 +1459,10 @@ void* scratch_on_current_device() {
     dpc_record_error(e);
     return nullptr;
   }
-  if (dev < 0 || dev >= kMaxDevices) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) {
+    dpc_record_error(hipErrorInvalidDevice);
+    return nullptr;
+  }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
     void* p = nullptr;

@@ -145,6 +145,39 @@ tile_sq_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ siz
 }
 #pragma clang fp contract(on)
 
+// Norm pass for any storage dtype and any square dtype (the reference's
+// reduction dtype: x.to(sq_dtype) * itself, _pytree.py:284-314), one element
+// per lane step: sanitised in the storage dtype, converted, squared and
+// rounded to sq_dtype, widened and added in fp64.  Same units, partials and
+// fixed fold as tile_sq_kernel; used for the combinations it does not take.
+#pragma clang fp contract(off)
+__global__ void __launch_bounds__(kThreads)
+tile_sq_generic_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ sizes,
+                       const int32_t* __restrict__ tile_leaf, const int32_t* __restrict__ tile_local,
+                       int n_tiles, long long units, int dtype, int sq_dtype,
+                       double* __restrict__ partial) {
+  const long long u = (long long)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (u >= units) return;
+  const int lane = threadIdx.x & 63;
+  const int b = (int)(u / n_tiles), t = (int)(u % n_tiles);
+  const int leaf = tile_leaf[t];
+  const int64_t n = sizes[leaf];
+  const void* base = reinterpret_cast<const void*>(ptrs[leaf]);
+  const int64_t off0 = (int64_t)tile_local[t] * kTile;
+  double s = 0.0;
+  for (int e = lane; e < kTile; e += 64) {
+    const int64_t off = off0 + e;
+    if (off < n) {
+      const double x = finite_or_zero_f64(load_as_f64(base, (int64_t)b * n + off, dtype));
+      const double v = round_to_dtype(x, sq_dtype);
+      s += round_to_dtype(v * v, sq_dtype);
+    }
+  }
+  s = wave_sum_f64(s);
+  if (lane == 0) partial[(size_t)b * n_tiles + t] = s;
+}
+#pragma clang fp contract(on)
+
 // leaf_sq[b, leaf_col[l]] = sum of leaf l's tile partials.  1024 threads;
 // thread i keeps eight running sums, of the tiles t0 + i + 8192 j + 1024 r
 // (r = 0..7), so eight loads are in flight (one round trip covers a leaf of
@@ -326,6 +359,82 @@ apply_sum_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ s
 }
 #pragma clang fp contract(on)
 
+// Apply pass for any storage dtype S, multiply dtype M = promote(S, compute
+// dtype), accumulation dtype A and output dtype O (_pytree.py:160-204 and
+// _clipped_fun.py:112-132): per element x of example b,
+//   prod   = to_M(to_M(sanitise(x)) * scale_M[b])
+//   stored = to_S(prod), zeroed if it rounded up into S's subnormal range
+//   sum   += to_A(stored)          (in float for A of 16 or 32 bits, in
+//                                   double for A = float64: torch's
+//                                   accumulation types)
+//   out    = to_O(to_A(sum))
+// in example order b = 0 .. B - 1.  scale_M is row r of `scale32` (already
+// rounded to M, for M of at most 32 bits) or of `scale64` (M = float64).
+// The second moment sums to_A(to_S(stored * stored)) the same way; post_sq
+// gets, per example and wave, the fp64 sum of stored^2 over the wave's
+// elements.  Layout as apply_sum_kernel: a workgroup per tile, thread i
+// owns elements 8 i .. 8 i + 7.
+#pragma clang fp contract(off)
+__global__ void __launch_bounds__(kThreads)
+apply_sum_generic_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ sizes,
+                         const int32_t* __restrict__ tile_leaf,
+                         const int32_t* __restrict__ tile_local,
+                         const int64_t* __restrict__ out_offs, int n_tiles, int B, int dtype,
+                         int mult, int acc, int out_dtype, const float* __restrict__ scale32,
+                         const double* __restrict__ scale64,
+                         const int32_t* __restrict__ leaf_scale_row, void* __restrict__ out,
+                         void* __restrict__ out_sq, double* __restrict__ post_sq) {
+  const int t = blockIdx.x;
+  const int leaf = tile_leaf[t];
+  const int64_t n = sizes[leaf];
+  const void* base = reinterpret_cast<const void*>(ptrs[leaf]);
+  const int64_t off0 = (int64_t)tile_local[t] * kTile;
+  const int e0 = 8 * threadIdx.x;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const bool wide = acc == DPC_F64;
+  const double tiny = smallest_normal_of(dtype);
+  const size_t row = (size_t)(leaf_scale_row ? leaf_scale_row[leaf] : 0) * B;
+  double sum[8], sum2[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) sum[k] = sum2[k] = 0.0;
+  for (int b = 0; b < B; ++b) {
+    const double sc = mult == DPC_F64 ? scale64[row + b] : (double)scale32[row + b];
+    double sq = 0.0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int64_t off = off0 + e0 + k;
+      if (off >= n) continue;
+      const double x = finite_or_zero_f64(load_as_f64(base, (int64_t)b * n + off, dtype));
+      const double prod = round_to_dtype(x * sc, mult);
+      double stored = round_to_dtype(prod, dtype);
+      if (fabs(stored) <= tiny && fabs(stored) > fabs(prod)) stored = 0.0;
+      const double a = round_to_dtype(stored, acc);
+      sum[k] = wide ? sum[k] + a : (double)((float)sum[k] + (float)a);
+      if (out_sq) {
+        const double a2 = round_to_dtype(round_to_dtype(stored * stored, dtype), acc);
+        sum2[k] = wide ? sum2[k] + a2 : (double)((float)sum2[k] + (float)a2);
+      }
+      sq += stored * stored;
+    }
+    if (post_sq) {
+      sq = wave_sum_f64(sq);
+      if (lane == 0) post_sq[(size_t)b * (4 * n_tiles) + 4 * t + w] = sq;
+    }
+  }
+  const int64_t obase = out_offs[leaf];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int64_t off = off0 + e0 + k;
+    if (off >= n) continue;
+    store_from_f64(out, obase + off, round_to_dtype(round_to_dtype(sum[k], acc), out_dtype),
+                   out_dtype);
+    if (out_sq)
+      store_from_f64(out_sq, obase + off,
+                     round_to_dtype(round_to_dtype(sum2[k], acc), out_dtype), out_dtype);
+  }
+}
+#pragma clang fp contract(on)
+
 // out[g * B + b] = sum over columns j with col_group[j] == g of x[b, j], in
 // column order (fp64): the reference's per-group accumulation in leaf order.
 __global__ void __launch_bounds__(kThreads)
@@ -376,9 +485,7 @@ extern "C" int dpc_leaves_sqnorm(const int64_t* ptrs, const int64_t* sizes,
                                  int square_dtype, double* partial, double* leaf_sq,
                                  int leaf_sq_stride, void* stream) {
   if (n_leaves < 0 || n_tiles < 0 || B < 0 || leaf_sq_stride < n_leaves) return DPC_EINVAL;
-  if (dtype != DPC_F32 && dtype != DPC_BF16) return DPC_EINVAL;
-  if (square_dtype != DPC_F32 && !(square_dtype == DPC_BF16 && dtype == DPC_BF16))
-    return DPC_EINVAL;
+  if (!known_dtype(dtype) || !known_dtype(square_dtype)) return DPC_EINVAL;
   if (B == 0 || n_leaves == 0) return DPC_OK;
   if (!ptrs || !sizes || !tile_leaf || !tile_local || !tile_start || !leaf_col || !partial ||
       !leaf_sq)
@@ -392,12 +499,16 @@ extern "C" int dpc_leaves_sqnorm(const int64_t* ptrs, const int64_t* sizes,
     if (dtype == DPC_BF16 && square_dtype == DPC_BF16) {
       hipLaunchKernelGGL((tile_sq_kernel<true, true>), dim3((unsigned)blocks), dim3(kThreads), 0,
                          s, ptrs, sizes, tile_leaf, tile_local, n_tiles, units, partial);
-    } else if (dtype == DPC_BF16) {
+    } else if (dtype == DPC_BF16 && square_dtype == DPC_F32) {
       hipLaunchKernelGGL(tile_sq_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), 0, s,
                          ptrs, sizes, tile_leaf, tile_local, n_tiles, units, partial);
-    } else {
+    } else if (dtype == DPC_F32 && square_dtype == DPC_F32) {
       hipLaunchKernelGGL(tile_sq_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, s,
                          ptrs, sizes, tile_leaf, tile_local, n_tiles, units, partial);
+    } else {
+      hipLaunchKernelGGL(tile_sq_generic_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s,
+                         ptrs, sizes, tile_leaf, tile_local, n_tiles, units, dtype, square_dtype,
+                         partial);
     }
     DPC_HIP_CHECK(hipGetLastError());
   }
@@ -433,6 +544,32 @@ extern "C" int dpc_leaves_apply(const int64_t* ptrs, const int64_t* sizes,
                                tile_local, out_offs, n_tiles, B, scale, leaf_scale_row, out,
                                out_sq, post_sq);
   }
+  DPC_HIP_CHECK(hipGetLastError());
+  return DPC_OK;
+}
+
+extern "C" int dpc_leaves_apply_ex(const int64_t* ptrs, const int64_t* sizes,
+                                   const int32_t* tile_leaf, const int32_t* tile_local,
+                                   const int64_t* out_offs, int n_tiles, int B, int dtype,
+                                   int mult_dtype, int acc_dtype, const float* scale,
+                                   const double* scale64, const int32_t* leaf_scale_row,
+                                   void* out, void* out_sq, int out_dtype, double* post_sq,
+                                   void* stream) {
+  if (n_tiles < 0 || B < 0) return DPC_EINVAL;
+  if (!known_dtype(dtype) || !known_dtype(mult_dtype) || !known_dtype(acc_dtype) ||
+      !known_dtype(out_dtype))
+    return DPC_EINVAL;
+  // The multiply dtype is promote(storage, compute): never narrower than storage.
+  if (dtype_bytes(mult_dtype) < dtype_bytes(dtype) ||
+      (dtype_bytes(mult_dtype) == 2 && mult_dtype != dtype))
+    return DPC_EINVAL;
+  if (n_tiles == 0) return DPC_OK;
+  if (!ptrs || !sizes || !tile_leaf || !tile_local || !out_offs || !out) return DPC_EINVAL;
+  if (B > 0 && (mult_dtype == DPC_F64 ? !scale64 : !scale)) return DPC_EINVAL;
+  hipLaunchKernelGGL(apply_sum_generic_kernel, dim3(n_tiles), dim3(kThreads), 0,
+                     (hipStream_t)stream, ptrs, sizes, tile_leaf, tile_local, out_offs, n_tiles, B,
+                     dtype, mult_dtype, acc_dtype, out_dtype, scale, scale64, leaf_scale_row, out,
+                     out_sq, post_sq);
   DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;
 }

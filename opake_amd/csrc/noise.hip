@@ -8,6 +8,8 @@
 // division; other leaves split a flat thread index per lane (in 32 bits when
 // the leaf's pair count allows, a 64-bit division costing about as much as
 // the rest of the thread's work).
+#include <algorithm>
+
 #include "common.h"
 
 namespace {
@@ -186,6 +188,43 @@ __global__ void __launch_bounds__(kNoiseThreads) add_noise_leaves_kernel(const N
   }
 }
 
+// Any leaf dtype and any compute dtype cd (_gaussian.py:188-204 with
+// compute_dtype): per element,
+//   c = to_cd(x), z = draw (injected: a cd value; device stream: the float
+//   normal rounded to cd), t = to_cd(sigma_op * z), y = to_dtype(to_cd(c + t))
+// with sigma_op = (float)sigma for cd of 16 or 32 bits (torch multiplies a
+// tensor by a Python scalar in float there) and sigma itself for float64;
+// to_cd of a 16-bit cd rounds through float32, as torch's float arithmetic
+// for 16-bit tensors does.  One (row pair, column) per thread, the same
+// Philox blocks as add_noise_kernel; a grid-stride loop covers any size.
+#pragma clang fp contract(off)
+__global__ void __launch_bounds__(kNoiseThreads)
+add_noise_generic_kernel(const void* __restrict__ x, void* __restrict__ y, int64_t rows,
+                         int64_t cols, int dtype, int cd, double sigma, int mode,
+                         const void* __restrict__ noise, uint64_t seed, uint32_t leaf) {
+  const int64_t work = ((rows + 1) >> 1) * cols;
+  const double sig = cd == DPC_F64 ? sigma : (double)(float)sigma;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < work;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t pr = t / cols, c = t - pr * cols;
+    float z32[2] = {0.0f, 0.0f};
+    if (mode == DPC_NOISE_PHILOX) philox_normal_pair(seed, leaf, (uint64_t)t, &z32[0], &z32[1]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t r = 2 * pr + h;
+      if (r >= rows) break;
+      const int64_t idx = r * cols + c;
+      const double z = mode == DPC_NOISE_PHILOX ? round_to_dtype((double)z32[h], cd)
+                                                : load_as_f64(noise, idx, cd);
+      const double cx = round_to_dtype(load_as_f64(x, idx, dtype), cd);
+      const double term = round_to_dtype(sig * z, cd);
+      const double v = round_to_dtype(cx + term, cd);
+      store_from_f64(y, idx, round_to_dtype(v, dtype), dtype);
+    }
+  }
+}
+#pragma clang fp contract(on)
+
 __global__ void philox_kat_kernel(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
                                   uint32_t k1, int n, uint32_t* __restrict__ out) {
   const int j = blockIdx.x * blockDim.x + threadIdx.x;
@@ -320,5 +359,32 @@ extern "C" int dpc_add_noise_leaves(int n, const void* const* x, void* const* y,
       DPC_HIP_CHECK(hipGetLastError());
     }
   }
+  return DPC_OK;
+}
+
+extern "C" int dpc_add_noise_ex(const void* x, void* y, int64_t rows, int64_t cols, int dtype,
+                                int compute_dtype, double sigma, int noise_mode,
+                                const void* noise, uint64_t seed, uint32_t leaf_id,
+                                void* stream) {
+  if (rows < 0 || cols < 0 || !(sigma >= 0.0)) return DPC_EINVAL;
+  if (!known_dtype(dtype) || !known_dtype(compute_dtype)) return DPC_EINVAL;
+  if (rows == 0 || cols == 0) return DPC_OK;
+  if (!x || !y) return DPC_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  if (sigma == 0.0) {
+    if (x != y) {
+      DPC_HIP_CHECK(hipMemcpyAsync(y, x, (size_t)rows * cols * dtype_bytes(dtype),
+                                   hipMemcpyDeviceToDevice, s));
+    }
+    return DPC_OK;
+  }
+  if (noise_mode != DPC_NOISE_INJECTED && noise_mode != DPC_NOISE_PHILOX) return DPC_EINVAL;
+  if (noise_mode == DPC_NOISE_INJECTED && !noise) return DPC_EINVAL;
+  const int64_t work = ((rows + 1) >> 1) * cols;
+  const int64_t blocks = std::min<int64_t>((work + kNoiseThreads - 1) / kNoiseThreads, 1 << 20);
+  hipLaunchKernelGGL(add_noise_generic_kernel, dim3((unsigned)blocks), dim3(kNoiseThreads), 0, s,
+                     x, y, rows, cols, dtype, compute_dtype, sigma, noise_mode, noise, seed,
+                     leaf_id);
+  DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;
 }

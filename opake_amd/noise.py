@@ -20,7 +20,11 @@ The addition runs in a HIP kernel (``dpc_add_noise``) on the leaf's device.
   stream with the same distribution; it does not depend on which device or
   how many devices run it.  No host work or copy, so it is the fast path.
 
-Supported: float32 / bfloat16 leaves on a ROCm device, compute_dtype float32.
+Supported: float16 / bfloat16 / float32 / float64 leaves on a ROCm device and
+each of those compute dtypes: the draw (``torch.randn(dtype=compute_dtype)``
+in the reference stream, the Philox normal rounded to it in the device
+stream), the scaling and the addition happen in ``compute_dtype`` and the
+result is cast back to the leaf dtype, as ``_gaussian.py:188-204`` does.
 """
 
 from __future__ import annotations
@@ -129,20 +133,17 @@ def add_noise_tree(tree: Any, std, step_key: RngKey, *, stream: str,
         if s == 0:
             out.append(leaf)  # the reference returns the centre itself, no draw
             continue
-        if compute_dtype != torch.float32:
+        if leaf.dtype not in _SUPPORTED_COMPUTE:
             raise OperationError(
-                f"compute_dtype {compute_dtype} is not implemented by the device kernel "
-                "(float32 only)"
-            )
-        if leaf.dtype not in (torch.float32, torch.bfloat16):
-            raise OperationError(f"leaf dtype {leaf.dtype} is not supported (float32, bfloat16)")
+                f"leaf dtype {leaf.dtype} is not supported (float16, bfloat16, float32, float64)")
         if stream == "reference":
             draw = torch.randn(tuple(leaf.shape), dtype=compute_dtype, generator=gen)
             draw = draw.pin_memory().to(leaf.device, non_blocking=True)
-            out.append(ops.add_noise(leaf, s, mode=nat.NOISE_INJECTED, noise=draw))
+            out.append(ops.add_noise(leaf, s, mode=nat.NOISE_INJECTED, noise=draw,
+                                     compute_dtype=compute_dtype))
         else:
             out.append(ops.add_noise(leaf, s, mode=nat.NOISE_PHILOX, seed=step_key.seed,
-                                     leaf_id=index))
+                                     leaf_id=index, compute_dtype=compute_dtype))
     return tree_unflatten(treedef, out)
 
 

@@ -23,6 +23,22 @@ def _contig(t: torch.Tensor) -> torch.Tensor:
     return t if t.is_contiguous() else t.contiguous()
 
 
+def _wants_error(out, err, return_error):
+    """Whether a norm call writes its error bound.  Accumulating into ``out``
+    without ``err`` drops the bound of the sum (``out + err`` would no longer
+    bound the norm), so it must be asked for with ``return_error=False``."""
+    if err is not None:
+        if return_error is False:
+            raise ConfigurationError("err was given together with return_error=False")
+        return True
+    if out is not None and return_error is None:
+        raise ConfigurationError(
+            "accumulating into `out` without `err` drops the rounding-error bound of the sum; "
+            "pass the matching `err` vector, or return_error=False to accumulate the norms alone"
+        )
+    return bool(return_error)
+
+
 def _error_out(err, B, dev, accumulate):
     """The error-bound vector of a norm call: ``err`` itself, or a new one."""
     if err is None:
@@ -41,15 +57,17 @@ def gram_sqnorms(
     with_bias: bool = False,
     out: torch.Tensor | None = None,
     err: torch.Tensor | None = None,
-    return_error: bool = False,
+    return_error: bool | None = None,
 ):
     """``out[i] (+)= ||G_i^T A_i||_F^2 (+ ||sum_t G_i[t]||^2)`` in float64.
 
     ``A``: [B, T, din], ``G``: [B, T, dout], same dtype (bf16 or fp32).  When
     ``out`` is given the layer's contribution is added to it.  With ``err`` (or
-    ``return_error``) the kernel also writes -- or, with ``out``, adds -- an
-    upper bound of the rounding error, so that ``out + err >= ||G_i^T A_i||^2``
-    exactly; the call then returns ``(out, err)``.
+    ``return_error=True``) the kernel also writes -- or, with ``out``, adds --
+    an upper bound of the rounding error, so that ``out + err >=
+    ||G_i^T A_i||^2`` exactly; the call then returns ``(out, err)``.
+    Accumulating into ``out`` without ``err`` needs ``return_error=False``:
+    the sum then carries no bound.
     """
     dev = nat.require_device(A, G, out, err)
     if A.dim() != 3 or G.dim() != 3 or A.shape[:2] != G.shape[:2]:
@@ -62,7 +80,7 @@ def gram_sqnorms(
     dout = G.shape[2]
     A, G = _contig(A), _contig(G)
     accumulate = out is not None
-    with_err = err is not None or return_error
+    with_err = _wants_error(out, err, return_error)
     if out is None:
         out = torch.empty(B, dtype=torch.float64, device=dev)
     elif out.dtype != torch.float64 or out.shape != (B,):
@@ -86,7 +104,7 @@ def gram_sqnorms_multi(
     *,
     out: torch.Tensor | None = None,
     err: torch.Tensor | None = None,
-    return_error: bool = False,
+    return_error: bool | None = None,
 ):
     """``gram_sqnorms`` of several bias-free layers of one batch, summed over
     the layers in list order (``dpc_gram_sqnorms_multi``: one launch for all
@@ -105,7 +123,7 @@ def gram_sqnorms_multi(
         if A.dtype != dtype or G.dtype != dtype:
             raise ConfigurationError("the layers' operands must share one dtype")
     accumulate = out is not None
-    with_err = err is not None or return_error
+    with_err = _wants_error(out, err, return_error)
     if out is None:
         out = torch.empty(B, dtype=torch.float64, device=dev)
     elif out.dtype != torch.float64 or out.shape != (B,):
@@ -137,7 +155,7 @@ def flat_sqnorms(
     with_bias: bool = False,
     out: torch.Tensor | None = None,
     err: torch.Tensor | None = None,
-    return_error: bool = False,
+    return_error: bool | None = None,
 ):
     """``out[i] (+)= ||a_i||^2 ||g_i||^2 (+ ||g_i||^2)`` for flat inputs [B, d];
     ``err`` / ``return_error`` as in :func:`gram_sqnorms`."""
@@ -147,7 +165,7 @@ def flat_sqnorms(
     B, din = a.shape
     dout = g.shape[1]
     accumulate = out is not None
-    with_err = err is not None or return_error
+    with_err = _wants_error(out, err, return_error)
     if out is None:
         out = torch.empty(B, dtype=torch.float64, device=dev)
     if with_err:
@@ -170,6 +188,7 @@ class ClipFactors:
     norms: torch.Tensor  # float32 [B]
     nclipped: torch.Tensor  # int32 [1]
     plan: torch.Tensor  # uint8 [n_guards, plan bytes]: guard g's active example lists
+    scale64: torch.Tensor | None = None  # float64 [n_guards, B] (guards with a float64 multiply)
 
 
 def clip_factors(
@@ -184,8 +203,10 @@ def clip_factors(
 ) -> ClipFactors:
     """Guarded clip factors for each ``(rel, abs)`` guard, per example.
 
-    A guard may carry a third element: true when its multiply dtype is
-    bfloat16, so that the scale is rounded to the nearest bfloat16.  ``err``
+    A guard may carry a third element, its multiply dtype (``True`` means
+    bfloat16): the scale is converted to it as ``scale.to(multiply_dtype)``
+    does (float16 and bfloat16 through float32); with a float64 multiply the
+    unconverted scale also comes back in ``scale64``.  ``err``
     (float64 [B], optional): the error bound of ``sqnorm``; the scale is then
     taken from ``sqrt(sqnorm + err)``, the reported norms and the clipped count
     from ``sqrt(sqnorm)``."""
@@ -200,17 +221,27 @@ def clip_factors(
     n = len(guards)
     rel = (ctypes.c_double * n)(*[g[0] for g in guards])
     abs_ = (ctypes.c_double * n)(*[g[1] for g in guards])
-    bf16 = (ctypes.c_int * n)(*[int(bool(g[2])) if len(g) > 2 else 0 for g in guards])
+    def mult_code(g):
+        m = g[2] if len(g) > 2 else torch.float32
+        if isinstance(m, bool):
+            m = torch.bfloat16 if m else torch.float32
+        return nat.dtype_code(m, wide=True)
+
+    codes = [mult_code(g) for g in guards]
+    mult = (ctypes.c_int * n)(*codes)
     scale = torch.empty((n, B), dtype=torch.float32, device=dev)
+    scale64 = (torch.empty((n, B), dtype=torch.float64, device=dev)
+               if nat.DPC_F64 in codes else None)
     norms = torch.empty(B, dtype=torch.float32, device=dev)
     nclipped = torch.empty(1, dtype=torch.int32, device=dev)
     plan = torch.empty((n, nat.load().dpc_clip_plan_bytes(B)), dtype=torch.uint8, device=dev)
     nat.call(
         "dpc_clip_factors", nat.ptr(_contig(sqnorm)), nat.ptr(None if err is None else _contig(err)),
-        B, float(clipping_norm), kind, float(gamma), rel, abs_, bf16, n, float(count_threshold),
-        nat.ptr(scale), nat.ptr(norms), nat.ptr(nclipped), nat.ptr(plan), nat.stream_handle(dev),
+        B, float(clipping_norm), kind, float(gamma), rel, abs_, mult, n, float(count_threshold),
+        nat.ptr(scale), nat.ptr(scale64), nat.ptr(norms), nat.ptr(nclipped), nat.ptr(plan),
+        nat.stream_handle(dev),
     )
-    return ClipFactors(scale=scale, norms=norms, nclipped=nclipped, plan=plan)
+    return ClipFactors(scale=scale, norms=norms, nclipped=nclipped, plan=plan, scale64=scale64)
 
 
 @dataclass
@@ -714,21 +745,36 @@ def add_noise(
     noise: torch.Tensor | None = None,
     seed: int = 0,
     leaf_id: int = 0,
+    compute_dtype: torch.dtype = torch.float32,
 ) -> torch.Tensor:
-    """Out-of-place ``to_dtype(float(x) + float32(sigma) * z)``."""
+    """Out-of-place ``to_dtype(to_cd(to_cd(x) + to_cd(sigma * z)))`` with
+    ``cd = compute_dtype`` (float32: ``to_dtype(float(x) + float32(sigma) *
+    z)``).  Injected ``noise`` is a ``compute_dtype`` tensor shaped like
+    ``x``.  float32 / bfloat16 leaves with a float32 compute dtype take
+    ``dpc_add_noise``, every other combination ``dpc_add_noise_ex``."""
     dev = nat.require_device(x, noise)
     x = _contig(x)
     y = torch.empty_like(x)
     rows, cols = leaf_view(x)
     if mode == nat.NOISE_INJECTED and sigma != 0.0:
-        if noise is None or noise.dtype != torch.float32 or noise.shape != x.shape:
-            raise ConfigurationError("injected noise must be float32 shaped like the leaf")
+        if noise is None or noise.dtype != compute_dtype or noise.shape != x.shape:
+            raise ConfigurationError(
+                f"injected noise must be {compute_dtype} shaped like the leaf")
         noise = _contig(noise)
-    nat.call(
-        "dpc_add_noise", nat.ptr(x), nat.ptr(y), rows, cols, nat.dtype_code(x.dtype),
-        float(sigma), mode, nat.ptr(noise), seed & ((1 << 64) - 1), leaf_id & 0xFFFFFFFF,
-        nat.stream_handle(dev),
-    )
+    seed &= (1 << 64) - 1
+    if compute_dtype == torch.float32 and x.dtype in (torch.float32, torch.bfloat16):
+        nat.call(
+            "dpc_add_noise", nat.ptr(x), nat.ptr(y), rows, cols, nat.dtype_code(x.dtype),
+            float(sigma), mode, nat.ptr(noise), seed, leaf_id & 0xFFFFFFFF,
+            nat.stream_handle(dev),
+        )
+    else:
+        nat.call(
+            "dpc_add_noise_ex", nat.ptr(x), nat.ptr(y), rows, cols,
+            nat.dtype_code(x.dtype, wide=True), nat.dtype_code(compute_dtype, wide=True),
+            float(sigma), mode, nat.ptr(noise), seed, leaf_id & 0xFFFFFFFF,
+            nat.stream_handle(dev),
+        )
     return y
 
 

@@ -6,7 +6,7 @@
  * philox4x32_10: Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
  *   easy as 1, 2, 3" (SC'11), Philox4x32 with 10 rounds: multipliers
  *   0xD2511F53 / 0xCD9E8D57, key schedule increments 0x9E3779B9 / 0xBB67AE85.
- *   Pinned by the Random123 known-answer vectors (tests/test_oracle_philox.py).
+ *   Pinned by the Random123 known-answer vectors (tests/test_oracle_noise.py).
  * normal_pair: the Box-Muller map of the device stream (53-bit radius
  *   uniform, 32-bit angle uniform) evaluated with the C library in double.
  */

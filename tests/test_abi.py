@@ -34,7 +34,7 @@ def test_version_and_size_queries():
     if not _native.LIB_PATH.exists():
         pytest.skip("native library not built")
     lib = _native.load()
-    assert lib.dpc_version() == _native.ABI_VERSION == 204
+    assert lib.dpc_version() == _native.ABI_VERSION == 205
     assert lib.dpc_clip_plan_bytes(32) == 16 + 32 * 4
     assert lib.dpc_gram_workspace_bytes(0, 5) == 0
     assert lib.dpc_gram_workspace_bytes(2, 128) > 0
@@ -62,3 +62,20 @@ def test_tables_used_under_keep_alive_survive_eviction():
     del kept
     gc.collect()
     assert ref() is None
+
+
+def test_err_less_accumulation_must_be_explicit():
+    # Accumulating norms into `out` without `err` drops the bound of the sum;
+    # the norm helpers refuse it unless return_error=False says so.
+    from opake_amd import ops
+    from opake_amd.exceptions import ConfigurationError
+
+    out, err = object(), object()
+    assert ops._wants_error(None, None, None) is False
+    assert ops._wants_error(None, None, True) is True
+    assert ops._wants_error(out, err, None) is True
+    assert ops._wants_error(out, None, False) is False
+    with pytest.raises(ConfigurationError, match="drops the rounding-error bound"):
+        ops._wants_error(out, None, None)
+    with pytest.raises(ConfigurationError, match="return_error=False"):
+        ops._wants_error(out, err, False)

@@ -145,10 +145,11 @@ def test_leaf_backend_many_leaves_and_stored_bound(dev):
 
 
 def test_leaf_backend_unsupported_raises_or_falls_back(dev):
-    tree = {"w": torch.randn(3, 4, device=dev, dtype=torch.float64)}
+    # Integer leaves have no kernel (the reference's torch path serves them).
+    tree = {"w": torch.arange(12, device=dev, dtype=torch.int32).reshape(3, 4)}
     kw = dict(scale=_Scale("fixed"), batch_size=3, reduce_leaf=_reduce, compute_dtype=None,
               second_moment=False, return_aux=False, return_stats=False)
-    with pytest.raises(OperationError, match="float64"):
+    with pytest.raises(OperationError, match="int32"):
         cl.fused_stream_clip_and_sum(tree, torch.tensor(1.0, device=dev), **kw)
     called = {}
 

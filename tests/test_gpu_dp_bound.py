@@ -82,6 +82,36 @@ def test_gram_error_bound_holds(dev, dtype, T, din, dout, ratio):
         assert torch.all(err / exact < 2e-2), err / exact
 
 
+def _spread(shape, lo_exp, gen):
+    """bf16 values whose magnitudes alternate between ~2^15 and ~2^lo_exp
+    along the feature (K) dimension, each with a random sign: inside every
+    16-product K block of an MFMA the addends then span 2^30 to 2^(2 lo_exp),
+    where the alignment and truncation of the hardware adder, and (for
+    lo_exp = -70) the flush of subnormal products, lose the most."""
+    mant = 1.0 + torch.rand(shape, generator=gen)
+    k = torch.arange(shape[-1])
+    exp = torch.where(k % 2 == 0, 15.0, float(lo_exp))
+    sign = torch.where(torch.rand(shape, generator=gen) < 0.5, -1.0, 1.0)
+    return (sign * mant * torch.exp2(exp)).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("lo_exp", [-15, -70])
+@pytest.mark.parametrize("T,din,dout", [
+    (512, 256, 256),   # one operand per work item (split kernel)
+    (384, 128, 256),   # paired kernel (odd number of 128-row blocks)
+    (70, 40, 24),      # generic kernel (misaligned widths)
+])
+def test_gram_error_bound_holds_on_exponent_spread(dev, lo_exp, T, din, dout):
+    gen = _gen(T + din - lo_exp)
+    A = _spread((2, T, din), lo_exp, gen)
+    G = _spread((2, T, dout), lo_exp, gen)
+    sq, err = ops.gram_sqnorms(A.to(dev), G.to(dev), return_error=True)
+    sq, err = sq.cpu(), err.cpu()
+    exact = _exact_sq(A, G)
+    assert torch.all(torch.isfinite(sq)) and torch.all(err > 0)
+    assert torch.all((sq - exact).abs() <= err), ((sq - exact).abs() / err)
+
+
 def test_gram_error_bound_matches_oracle_formula(dev):
     # The device bound from its own fp32 Gram tiles against the oracle's
     # formula evaluated on the exact Gram matrices: the same up to the tiles'

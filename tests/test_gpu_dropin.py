@@ -3,9 +3,9 @@
 * ``compute_dtype`` (packages/opake-engine/src/opake/api/engine/clipping/
   _clipped_grad.py:100, _pytree.py:84-108, _clipped_fun.py:91-170): float32
   gives the default's bits for bfloat16 and float32 leaves; bfloat16 (with
-  bfloat16 leaves) squares, guards and multiplies in bfloat16 -- against the
-  streaming oracle run with the same compute dtype; float64 is refused with
-  ``OperationError``.
+  bfloat16 leaves) squares, guards and multiplies in bfloat16, float64
+  squares and multiplies in float64 -- against the streaming oracle run with
+  the same compute dtype (every other combination: tests/test_gpu_dtypes.py).
 * ``pre_clipping_transform`` (_clipped_grad.py:97,285, _auto.py:222): applied
   to each example's gradient before clipping, against the oracle clipping the
   transformed per-example gradients, including a transform that changes the
@@ -18,7 +18,6 @@ import pytest
 import torch
 
 from opake_amd.clipping import auto_clipped_grad, clipped_fun, clipped_grad
-from opake_amd.exceptions import OperationError
 from oracle import clip_oracle
 
 pytestmark = pytest.mark.gpu
@@ -63,7 +62,10 @@ def test_compute_dtype_bfloat16_matches_oracle(dev, microbatch):
     for n, w in zip(names, want.reduced):
         assert res.pytree[n].dtype == torch.bfloat16
         assert _rel(res.pytree[n], w) < 2e-2, n
-    torch.testing.assert_close(aux.norms.cpu().double(), want.norms, rtol=1e-6, atol=0)
+    # The diagnostic norms come in the reduction dtype (_streaming.py:174-180).
+    assert aux.norms.dtype == torch.bfloat16
+    torch.testing.assert_close(aux.norms.cpu().double(), want.norms.to(torch.bfloat16).double(),
+                               rtol=2 ** -8, atol=0)
     # The bf16 guard and multiply: every stored example's norm is within C.
     fn2, st2 = clipped_fun(lambda v: v, batch_argnums=0, clipping_norm=0.3,
                            compute_dtype=torch.bfloat16, return_aux=True)
@@ -71,11 +73,20 @@ def test_compute_dtype_bfloat16_matches_oracle(dev, microbatch):
     assert torch.all(aux2.clipped_norms.double() <= 0.3 * (1 + 1e-6))
 
 
-def test_compute_dtype_float64_refused(dev):
-    fn, st = clipped_fun(lambda v: v, batch_argnums=0, clipping_norm=1.0,
-                         compute_dtype=torch.float64)
-    with pytest.raises(OperationError, match="compute_dtype"):
-        fn(_tree(dev, torch.float32), state=st)
+def test_compute_dtype_float64_matches_oracle(dev):
+    tree = _tree(dev, torch.float32, B=8, seed=4)
+    fn, st = clipped_fun(lambda v: v, batch_argnums=0, clipping_norm=0.3,
+                         compute_dtype=torch.float64, return_aux=True)
+    (res, aux), _ = fn(tree, state=st)
+    names = sorted(tree)
+    want = clip_oracle.stream_clip_and_sum([tree[n].cpu() for n in names],
+                                           clip_oracle.conservative_bound(0.3),
+                                           compute_dtype=torch.float64)
+    for n, w in zip(names, want.reduced):
+        assert res.pytree[n].dtype == torch.float32
+        torch.testing.assert_close(res.pytree[n].cpu(), w, rtol=1e-6, atol=1e-9)
+    assert aux.norms.dtype == torch.float64
+    torch.testing.assert_close(aux.norms.cpu(), want.norms, rtol=1e-12, atol=0)
 
 
 def _loss(p, x):
