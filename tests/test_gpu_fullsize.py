@@ -4,8 +4,9 @@ The smaller parity tests cover every code path on reduced shapes; these run
 the exact launches the benchmark times -- config 2 (one linear layer 4096 x
 4096, B = 32, T = 512, bf16: 256 output tiles, no split-K, the 8-way XCD
 remap, an 8192-step K loop), config 3 (the Llama-style block, d = 2048, B =
-16, T = 1024) and config 5 (the top-2 MoE, 8 experts 2048 / 5632, B = 16, T =
-1024) -- on the benchmark's own synthetic inputs, and check them against float64
+16, T = 1024), config 4 (LoRA r = 16 on an 8B-shaped block, B = 8, T = 2048)
+and config 5 (the top-2 MoE, 8 experts 2048 / 5632, B = 16, T = 1024) -- on
+the benchmark's own synthetic inputs, and check them against float64
 mathematics computed on the device:
 
 * per-example squared norms against the exact ``||G_i^T A_i||^2`` (fp64
@@ -17,6 +18,12 @@ mathematics computed on the device:
 * sampled output rows of every clipped sum (all columns) against the float64
   sum ``sum_i scale_i G_i[:, m]^T A_i`` with the device's scales, 1e-5
   relative (fp32 accumulation);
+* config 3's block norm from the multi-layer Gram launch, both sides, against
+  the exact projection norms plus the RMSNorm weights' per-example squares;
+* config 4's grouped per-example gradients (16 sampled rows of every adapter
+  and example) against float64 at 1e-5, the bf16 launch equal to the fp32
+  one rounded, the leaf clip-and-sum against float64 with the device's
+  scales, and the fused noise equal to ``noise_fn`` on the noiseless result;
 * at config 2, the fused noise: an injected float32 draw is added bit-exactly
   (``to_bf16(v + sigma z)``), and the Philox epilogue equals ``dpc_add_noise``
   on the noiseless output.
@@ -177,11 +184,78 @@ def test_cfg3_block_projections(dev):
         w = res.pytree[f"{c.name}.weight"]
         rows = _sample_rows(c.G.shape[2], 16, k)
         assert _rel(w[rows], _rows_exact(c.A, c.G, scale, rows)) < 1e-5, c.name
-    # The block's norm: the projections plus the RMSNorm weights' materialised
-    # per-example gradients (a few values each).
-    assert torch.all(aux.grad_norms.double() ** 2 >= total_exact * (1 - 2e-2))
-    lin_part = total_exact.sqrt()
-    assert torch.all(scale.double() * lin_part <= bench.C)
+    # The block's norm, from the multi-layer Gram launch the benchmark times
+    # (dpc_gram_sqnorms_multi) plus the leaf kernels: the projections' exact
+    # squared norms plus the RMSNorm weights' materialised per-example
+    # gradients, both sides.
+    direct = [c for c in caps if not isinstance(c, LinearCapture)]
+    assert len(direct) == 1
+    for g in direct[0].grads.values():
+        total_exact += g.double().reshape(g.shape[0], -1).square().sum(dim=1)
+    got = aux.grad_norms.double() ** 2
+    assert torch.all((got - total_exact).abs() / total_exact < 2e-2), got / total_exact
+    assert torch.all(scale.double() * total_exact.sqrt() <= bench.C)
+
+
+# --- config 4 ---------------------------------------------------------------------
+
+
+def test_cfg4_lora_block(dev):
+    """The launches config 4 times: all 14 adapter sides' per-example
+    gradients in one grouped launch (narrow_wide_mfma_kernel over the 11
+    shared-wide groups: wide sides 4096 and 14336, B = 8, T = 2048), then the
+    leaf clip-and-sum and the fused Philox noise."""
+    from opake_amd.noise import gaussian_noise
+    from opake_amd.random import key
+
+    model = bench.lora_model(dev, torch.bfloat16)
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(bench.LORA_B, bench.LORA_T, bench.LORA_D, generator=g,
+                    device=dev).to(torch.bfloat16)
+    tgt = torch.randn(bench.LORA_B, bench.LORA_T, bench.LORA_D, generator=g, device=dev)
+    caps, _ = ghost_capture(model, bench._mse_loss, x, tgt)
+    linears = [c for c in caps if isinstance(c, LinearCapture)]
+    assert len(linears) == 14 and all(min(c.A.shape[-1], c.G.shape[-1]) <= 16 for c in linears)
+    B = bench.LORA_B
+    # The model path's grouped launch, its operands as the model path forms them.
+    As = [c.A.reshape(B, -1, c.A.shape[-1]) for c in linears]
+    Gs = [c.G.reshape(B, -1, c.G.shape[-1]) for c in linears]
+    g32 = ops.per_example_grads_grouped(As, Gs, out_dtype=torch.float32)
+    g16 = ops.per_example_grads_grouped(As, Gs)
+    exact_sq = torch.zeros(B, dtype=torch.float64, device=dev)
+    for k, (c, A, G, w32, w16) in enumerate(zip(linears, As, Gs, g32, g16)):
+        rows = _sample_rows(G.shape[2], 16, k)
+        for b in range(B):
+            want = G[b][:, rows].double().t() @ A[b].double()
+            assert _rel(w32[b][rows], want) < 1e-5, (c.name, b)
+        # The bf16 launch stores the same fp32 sums, rounded.
+        assert torch.equal(w16, w32.to(torch.bfloat16)), c.name
+        exact_sq += w16.double().reshape(B, -1).square().sum(dim=1)
+    # Clip and sum (leaf kernels) against float64 with the device's scales.
+    res, aux = ghost_clip_captured(caps, clipping_norm=bench.C, return_aux=True,
+                                   dtype=torch.float32)
+    got = aux.grad_norms.double() ** 2
+    assert torch.all((got - exact_sq).abs() / exact_sq < 1e-5), got / exact_sq
+    scale = aux.clip_scales[0]
+    for c, w16 in zip(linears, g16):
+        stored = (w16.float() * scale.view(B, 1, 1)).to(torch.bfloat16)
+        want = stored.double().sum(dim=0)
+        assert _rel(res.pytree[f"{c.name}.weight"], want) < 1e-5, c.name
+    # Every example's stored gradient is within C (the guard covers the bf16 store).
+    stored_sq = torch.zeros(B, dtype=torch.float64, device=dev)
+    for w16 in g16:
+        st = (w16.float() * scale.view(B, 1, 1)).to(torch.bfloat16).double()
+        stored_sq += st.reshape(B, -1).square().sum(dim=1)
+    assert torch.all(stored_sq.sqrt() <= bench.C)
+    # The fused Philox noise equals noise_fn on the noiseless result, bit for bit.
+    noise_fn, state = gaussian_noise(noise_multiplier=bench.NM, key=key(0), stream="device")
+    noised, _ = ghost_clip_captured(caps, clipping_norm=bench.C, noise_fn=noise_fn,
+                                    noise_state=state)
+    plain = ghost_clip_captured(caps, clipping_norm=bench.C)
+    separate, _ = noise_fn(plain, state)
+    assert set(noised.pytree) == set(separate.pytree)
+    for n in noised.pytree:
+        assert torch.equal(noised.pytree[n], separate.pytree[n]), n
 
 
 # --- config 5 ---------------------------------------------------------------------
