@@ -170,6 +170,34 @@ int dpc_clip_factors(const double* sqnorm, const double* sqerr, int B, double C,
                      double* scale64, float* norms_out, int* nclipped, void* plan,
                      void* stream);
 
+/* dpc_gram_clip_factors: the norm pass and the clip factors of one linear
+ * layer -- _streaming.py:70-108 for a layer whose per-example gradients are
+ * never formed -- exactly
+ *   dpc_gram_sqnorms(A, G, B, T, din, dout, dtype, with_bias, 0, sqnorm,
+ *                    sqerr, ...) then
+ *   dpc_clip_factors(sqnorm, sqerr, B, C, kind, gamma, guard_rel, guard_abs,
+ *                    guard_mult, n_guards, count_threshold, scale, scale64,
+ *                    norms_out, nclipped, plan, stream)
+ * (the same bits), in ONE launch when the split Gram kernel applies (bf16,
+ * T an even number of 128-row blocks, din and dout multiples of 8, no bias,
+ * B <= 2048): its last work item folds the records and computes the clip
+ * factors.  ws: dpc_gram_clip_workspace_bytes(B, T) bytes of scratch (any
+ * content).  counters: dpc_gram_clip_counter_bytes(B, T) bytes that must be
+ * zero before the first call on them; every call leaves them zero again, so
+ * one zero-filled buffer (as large as the largest call needs) serves call
+ * after call of any shape on one stream -- calls that overlap on one
+ * counter buffer race; the separate-launch shapes do not touch it.  sqnorm
+ * is required. */
+size_t dpc_gram_clip_workspace_bytes(int B, int T);
+size_t dpc_gram_clip_counter_bytes(int B, int T);
+int dpc_gram_clip_factors(const void* A, const void* G, int B, int T, int din, int dout,
+                          int dtype, int with_bias, double C, int kind, double gamma,
+                          const double* guard_rel, const double* guard_abs, const int* guard_mult,
+                          int n_guards, float count_threshold, double* sqnorm, double* sqerr,
+                          float* scale, double* scale64, float* norms_out, int* nclipped,
+                          void* plan, void* ws, size_t ws_bytes, int32_t* counters,
+                          size_t counter_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Clipped batch sum of a linear layer with the noise epilogue fused.
  *

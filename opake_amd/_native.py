@@ -89,6 +89,15 @@ SIGNATURES = {
     "dpc_gram_sqnorms_multi_workspace_bytes": (
         _c_size_t, [_c_int, _c_void_p, _c_void_p, _c_int, _c_int, _c_int],
     ),
+    "dpc_gram_clip_workspace_bytes": (_c_size_t, [_c_int, _c_int]),
+    "dpc_gram_clip_counter_bytes": (_c_size_t, [_c_int, _c_int]),
+    "dpc_gram_clip_factors": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_double, _c_int,
+         _c_double, ctypes.POINTER(_c_double), ctypes.POINTER(_c_double), ctypes.POINTER(_c_int),
+         _c_int, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p, _c_size_t, _c_void_p, _c_size_t, _c_void_p],
+    ),
     "dpc_gram_sqnorms_multi": (
         _c_int,
         [_c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int,

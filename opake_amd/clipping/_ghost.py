@@ -183,16 +183,17 @@ def ghost_clip_sum(
         return ((res, aux) if return_aux else res), next_state
 
     with record_function("opake::ghost_clip_sum"):
-        sq, err = ghost_sqnorms(A, G, bias=bias)
-        cf = ops.clip_factors(
-            sq,
-            num.conservative_bound(clipping_norm),
-            [guard_for_linear(A.dtype, din, dout, bias)],
-            err=err,
-            kind=kind,
-            gamma=gamma,
-            count_threshold=num.float32_of(clipping_norm),
-        )
+        guards = [guard_for_linear(A.dtype, din, dout, bias)]
+        bound = num.conservative_bound(clipping_norm)
+        threshold = num.float32_of(clipping_norm)
+        if T > 1:
+            # Norms and clip factors in one launch where the split Gram kernel applies.
+            _, _, cf = ops.gram_clip_factors(A, G, bound, guards, with_bias=bias, kind=kind,
+                                             gamma=gamma, count_threshold=threshold)
+        else:
+            sq, err = ghost_sqnorms(A, G, bias=bias)
+            cf = ops.clip_factors(sq, bound, guards, err=err, kind=kind, gamma=gamma,
+                                  count_threshold=threshold)
         spec = None
         next_state = None
         std = 0.0

@@ -1,140 +1,17 @@
 // Clip factors from per-example squared norms, in float64, plus the active
-// example plans consumed by the clipped-sum GEMM.
-//
-// The scale is the reference's guarded ratio (packages/opake-engine/src/opake/
-// api/engine/clipping/_pytree.py:111-157, _streaming.py:84-108), taken from
-// an upper bound of the norm when the squared norm comes with an error bound
-// (ghost norms: sqnorm + sqerr >= ||g||^2):
-//   up = sqrt(max(sq + err, 0));  norm = sqrt(max(sq, 0))
-//   ratio = max(C,0)/up  or  max(R,0)/(up + gamma)               (AUTO-S)
-//   s = ratio * rel - abs;  s = min(1, s) (fixed only; NaN stays NaN)
-//   s = isfinite(s) ? max(s, 0) : 0;  stored as float32, or as the value of
-//   the guard's multiply dtype (scale.to(multiply_dtype): for bfloat16 and
-//   float16 through float32, as torch converts a float64); `scale64` (when
-//   given) keeps s itself for float64 guards.
-// `norm` (the estimate) is what the statistics report and count.  Every step
-// is one IEEE operation in the order written (contraction off), so the result
-// matches a host float64 evaluation bit for bit.
-#include "common.h"
-#include "plan.h"
+// example plans consumed by the clipped-sum GEMM: one workgroup running
+// clip_factors_block (clip_block.h, which states the arithmetic).
+#include "clip_block.h"
 
 namespace {
 
 constexpr int kClipThreads = 1024;
-constexpr int kMaxGuards = 4;
-
-struct Guards {
-  double rel[kMaxGuards];
-  double abs_[kMaxGuards];
-  int mult[kMaxGuards];  // the multiply dtype the scale is converted to
-};
-
-// s.to(multiply dtype) as a float: torch converts a float64 to bfloat16 or
-// float16 through float32 (each step to nearest even).
-__device__ float scale_in(double s, int mult) {
-  const float f = (float)s;
-  if (mult == DPC_BF16) return round_to_bf16(f);
-  if (mult == DPC_F16) return round_to_f16(f);
-  return f;
-}
-
-#pragma clang fp contract(off)
-__device__ double guarded_scale(double sq, double err, double C, int kind, double gamma,
-                                double rel, double abs_, double* norm_out) {
-  const double est = sq < 0.0 ? 0.0 : sq;  // NaN stays NaN
-  *norm_out = sqrt(est);
-  double up = sq + err;
-  up = up < 0.0 ? 0.0 : up;
-  const double norm = sqrt(up);
-  double bound = C > 0.0 ? C : 0.0;
-  double ratio = (kind == DPC_SCALE_AUTO_S) ? bound / (norm + gamma) : bound / norm;
-  double s = ratio * rel;
-  s = s - abs_;
-  if (kind != DPC_SCALE_AUTO_S) s = (s > 1.0) ? 1.0 : s;  // torch.minimum keeps NaN
-  if (!isfinite(s)) s = 0.0;
-  return s < 0.0 ? 0.0 : s;
-}
 
 __global__ void __launch_bounds__(kClipThreads)
 clip_factors_kernel(const double* __restrict__ sqnorm, const double* __restrict__ sqerr, int B,
-                    double C, int kind, double gamma, Guards guards, int n_guards,
-                    float count_threshold, float* __restrict__ scale,
-                    double* __restrict__ scale64, float* __restrict__ norms_out,
-                    int* __restrict__ nclipped, void* __restrict__ plans) {
-  __shared__ int wave_counts[kClipThreads / 64];
-  __shared__ int clipped_counts[kClipThreads / 64];
-  __shared__ int slow_counts[kClipThreads / 64];
-  __shared__ int base, base_slow;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int nw = blockDim.x >> 6;
-  int clipped_local = 0;
-  // Guard g's pass computes its scales and lists its active examples in plan
-  // g (see plan.h): the fast ones from the front of `active` in increasing
-  // order, the others from its back, in increasing order read backwards.
-  // Each list is an ordered compaction: a ballot within a wave, wave offsets
-  // through LDS.  The norms and the clipped count come from guard 0's pass.
-  const bool fast_ok = (double)B * C <= (double)DPC_FAST_BC_MAX;
-  for (int g = 0; g < n_guards; ++g) {
-    const bool have_plan = plans != nullptr;
-    ClipPlanView plan = clip_plan_view((char*)plans + (size_t)g * clip_plan_bytes(B), B);
-    if (tid == 0) {
-      base = 0;
-      base_slow = 0;
-    }
-    for (int start = 0; start < B; start += blockDim.x) {
-      const int i = start + tid;
-      bool fast = false, slow = false;
-      if (i < B) {
-        double norm;
-        const double s = guarded_scale(sqnorm[i], sqerr ? sqerr[i] : 0.0, C, kind, gamma,
-                                       guards.rel[g], guards.abs_[g], &norm);
-        const float sf = scale_in(s, guards.mult[g]);
-        if (scale) scale[(size_t)g * B + i] = sf;
-        if (scale64) scale64[(size_t)g * B + i] = guards.mult[g] == DPC_F64 ? s : (double)sf;
-        if (g == 0) {
-          if (norms_out) norms_out[i] = (float)norm;
-          if ((float)norm > count_threshold) ++clipped_local;
-        }
-        fast = sf > 0.0f && fast_ok && sf >= DPC_FAST_SCALE_MIN && sf <= DPC_FAST_SCALE_MAX;
-        slow = sf > 0.0f && !fast;
-      }
-      const unsigned long long mf = __ballot(fast), ms = __ballot(slow);
-      const unsigned long long below = (1ull << lane) - 1ull;
-      if (lane == 0) {
-        wave_counts[w] = __popcll(mf);
-        slow_counts[w] = __popcll(ms);
-      }
-      __syncthreads();
-      int of = base, os = base_slow;
-      for (int v = 0; v < w; ++v) {
-        of += wave_counts[v];
-        os += slow_counts[v];
-      }
-      if (have_plan && fast) plan.active[of + __popcll(mf & below)] = i;
-      if (have_plan && slow) plan.active[B - 1 - (os + __popcll(ms & below))] = i;
-      __syncthreads();
-      if (tid == 0) {
-        for (int v = 0; v < nw; ++v) {
-          base += wave_counts[v];
-          base_slow += slow_counts[v];
-        }
-      }
-      __syncthreads();
-    }
-    if (tid == 0 && have_plan) {
-      *plan.nactive = base + base_slow;
-      *plan.nfast = base;
-    }
-    __syncthreads();
-  }
-  for (int off = 32; off > 0; off >>= 1) clipped_local += __shfl_down(clipped_local, off, 64);
-  if (lane == 0) clipped_counts[w] = clipped_local;
-  __syncthreads();
-  if (tid == 0) {
-    int total = 0;
-    for (int v = 0; v < nw; ++v) total += clipped_counts[v];
-    if (nclipped) *nclipped = total;
-  }
+                    const ClipJob job) {
+  __shared__ int shm[3 * (kClipThreads / 64) + 2];
+  clip_factors_block(sqnorm, sqerr, B, job, shm);
 }
 
 }  // namespace
@@ -147,22 +24,14 @@ extern "C" int dpc_clip_factors(const double* sqnorm, const double* sqerr, int B
                                 const int* guard_mult, int n_guards, float count_threshold,
                                 float* scale, double* scale64, float* norms_out, int* nclipped,
                                 void* plan, void* stream) {
-  if (B < 0 || n_guards < 1 || n_guards > kMaxGuards || !guard_rel || !guard_abs) {
-    return DPC_EINVAL;
-  }
-  if (kind != DPC_SCALE_FIXED && kind != DPC_SCALE_AUTO_S) return DPC_EINVAL;
-  if (B > 0 && !sqnorm) return DPC_EINVAL;
-  if (plan && !scale) return DPC_EINVAL;
-  Guards guards = {};
-  for (int g = 0; g < n_guards; ++g) {
-    guards.rel[g] = guard_rel[g];
-    guards.abs_[g] = guard_abs[g];
-    guards.mult[g] = guard_mult ? guard_mult[g] : DPC_F32;
-    if (!known_dtype(guards.mult[g])) return DPC_EINVAL;
-  }
+  if (B < 0 || (B > 0 && !sqnorm)) return DPC_EINVAL;
+  ClipJob job;
+  const int r = clip_job_from_args(C, kind, gamma, guard_rel, guard_abs, guard_mult, n_guards,
+                                   count_threshold, scale, scale64, norms_out, nclipped, plan,
+                                   &job);
+  if (r != DPC_OK) return r;
   hipLaunchKernelGGL(clip_factors_kernel, dim3(1), dim3(kClipThreads), 0, (hipStream_t)stream,
-                     sqnorm, sqerr, B, C, kind, gamma, guards, n_guards, count_threshold,
-                     scale, scale64, norms_out, nclipped, plan);
+                     sqnorm, sqerr, B, job);
   DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;
 }

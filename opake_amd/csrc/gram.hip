@@ -29,6 +29,7 @@
 
 #include <algorithm>
 
+#include "clip_block.h"
 #include "common.h"
 #include "lds_stage.h"
 
@@ -856,7 +857,11 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
       } else {
         val = k == 7 ? gA : k == 8 ? gQ : k == 9 ? (double)T : 0.0;
       }
-      rec_ex[(size_t)pair[u] * DPC_GRAM_REC_WORDS + k] = val;
+      // A device-scope store: written through to memory, where another XCD's
+      // workgroup (the launch's tail) reads it without a writeback of this
+      // XCD's L2.
+      __hip_atomic_store(&rec_ex[(size_t)pair[u] * DPC_GRAM_REC_WORDS + k], val, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -875,10 +880,112 @@ struct SplitLayers {
   int n;
 };
 
+// The clip factors folded into a split launch (dpc_gram_clip_factors).  Each
+// tile set's record writer (the item with the second ticket) clears the
+// set's ticket words and counts the set into its example's counter; the
+// last set of an example folds the example's records into sqnorm / sqerr
+// (as gram_finish_kernel does: the same bits) while other items still run,
+// and counts the example into `done`; the last example's finisher computes
+// the clip factors and plans of all examples from them (clip_factors_block:
+// the same bits as clip_factors_kernel).  Every counter is back at zero when
+// the launch ends, for the next one.  done == nullptr: no tail (the caller
+// launches the finish).
+struct SplitTail {
+  int32_t* done;     // [1]
+  int32_t* ex_done;  // [B]: sets (of all layers) written per example
+  double* sqnorm;
+  double* sqerr;
+  ClipJob job;
+};
+
+__device__ __forceinline__ double gram_bound_wave(const double* rec, int nt, double* sum);
+
+// Largest batch whose squared norms and bounds the tail keeps in the
+// staging LDS (16 bytes per example, plus the clip routine's words).
+constexpr int kSplitTailMaxB = 1024;
+
+// Device-scope loads of n doubles into LDS by the whole workgroup, eight per
+// thread in flight (the data may come from other XCDs: no cache is trusted).
+__device__ __forceinline__ void load_agent_to_lds(const double* __restrict__ src, double* dst,
+                                                  int n) {
+  constexpr int kU = 8;
+  for (int i0 = 0; i0 < n; i0 += kU * (int)blockDim.x) {
+    double v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int i = i0 + u * (int)blockDim.x + (int)threadIdx.x;
+      v[u] = i < n ? __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0;
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int i = i0 + u * (int)blockDim.x + (int)threadIdx.x;
+      if (i < n) dst[i] = v[u];
+    }
+  }
+}
+
+// Called by every item after its part of the set (`writer`: this item wrote
+// the set's records; its partner has taken its ticket).  Counters advance
+// only after the data they announce has completed at the memory side
+// (device-scope stores and a wait), so no cache writeback is needed.
+__device__ void split_tail(const SplitTail& tail, const double* __restrict__ records,
+                           int32_t* set_tickets, bool writer, int ex, int B, int nt, int nsets,
+                           int nlayers, uint8_t* lds, int* flag) {
+  if (!writer) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (tid < 3) set_tickets[tid] = 0;  // both items of the set are past them
+  DPC_WAIT_VMCNT(0);                  // this wave's record stores have completed
+  __syncthreads();
+  if (tid == 0)
+    flag[0] = __hip_atomic_fetch_add(&tail.ex_done[ex], 1, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) == nsets * nlayers - 1;
+  __syncthreads();
+  if (!flag[0]) return;
+  // The example's last set: fold its records (every layer's).
+  const size_t np = (size_t)nt * (nt + 1) / 2;
+  const int ex_words = (int)(np * DPC_GRAM_REC_WORDS);
+  double* rec_lds = reinterpret_cast<double*>(lds);
+  for (int L = 0; L < nlayers; ++L)
+    load_agent_to_lds(records + ((size_t)L * B + ex) * ex_words, rec_lds + L * ex_words,
+                      ex_words);
+  __syncthreads();
+  if (tid < 64) {
+    double v = 0.0, ev = 0.0;
+    for (int L = 0; L < nlayers; ++L) {
+      double sm;
+      const double e = gram_bound_wave(rec_lds + L * ex_words, nt, &sm);
+      v = L == 0 ? sm : v + sm;
+      ev = L == 0 ? e : ev + e;
+    }
+    if (lane == 0) {
+      __hip_atomic_store(&tail.sqnorm[ex], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tail.sqerr)
+        __hip_atomic_store(&tail.sqerr[ex], ev, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      tail.ex_done[ex] = 0;
+    }
+  }
+  DPC_WAIT_VMCNT(0);
+  __syncthreads();
+  if (tid == 0)
+    flag[0] = __hip_atomic_fetch_add(tail.done, 1, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) == B - 1;
+  __syncthreads();
+  if (!flag[0]) return;
+  // The last example: the clip factors of all of them.
+  if (tid == 0) *tail.done = 0;
+  double* sq = reinterpret_cast<double*>(lds);
+  double* er = sq + B;
+  load_agent_to_lds(tail.sqnorm, sq, B);
+  if (tail.sqerr) load_agent_to_lds(tail.sqerr, er, B);
+  __syncthreads();
+  clip_factors_block(sq, tail.sqerr ? er : nullptr, B, tail.job,
+                     reinterpret_cast<int*>(er + B));
+}
+
 __global__ void __launch_bounds__(512, 1)
 gram_split_bf16_kernel(const SplitLayers lay, int B, int T, int npairs, int nsets, int nblocks,
                        double* __restrict__ records, int32_t* __restrict__ tickets,
-                       float* __restrict__ xbuf) {
+                       float* __restrict__ xbuf, const SplitTail tail) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[4 * 3 * kGTileBytes];
   __shared__ double red[3 * kSplitWaves * kRecStat];
   __shared__ int ticket_lds[2];
@@ -899,6 +1006,7 @@ gram_split_bf16_kernel(const SplitLayers lay, int B, int T, int npairs, int nset
   const uint16_t* A = lay.A[L];
   const uint16_t* G = lay.G[L];
   const int din = lay.din[L], dout = lay.dout[L];
+  const double* all_records = records;
   {
     const size_t reg = (size_t)lay.region[L];
     records += reg * B * npairs * DPC_GRAM_REC_WORDS;
@@ -928,26 +1036,29 @@ gram_split_bf16_kernel(const SplitLayers lay, int B, int T, int npairs, int nset
   if (!diag_set) {
     split_item<kMacro, false>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
                               ticket_lds, xcc);
-    return;
+  } else {
+    switch (kind) {
+      case kMacro:
+        split_item<kMacro, true>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds,
+                                 red, ticket_lds, xcc);
+        break;
+      case kExtraRows:
+        split_item<kExtraRows, true>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf,
+                                     lds, red, ticket_lds, xcc);
+        break;
+      case kExtraCols:
+        split_item<kExtraCols, true>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf,
+                                     lds, red, ticket_lds, xcc);
+        break;
+      default:
+        split_item<kDiag4, true>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds,
+                                 red, ticket_lds, xcc);
+        break;
+    }
   }
-  switch (kind) {
-    case kMacro:
-      split_item<kMacro, true>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
-                               ticket_lds, xcc);
-      break;
-    case kExtraRows:
-      split_item<kExtraRows, true>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
-                                   ticket_lds, xcc);
-      break;
-    case kExtraCols:
-      split_item<kExtraCols, true>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
-                                   ticket_lds, xcc);
-      break;
-    default:
-      split_item<kDiag4, true>(X, T, d, din, dout, t, q, f, op, slot, rec_ex, tickets, xbuf, lds, red,
-                               ticket_lds, xcc);
-      break;
-  }
+  if (tail.done)
+    split_tail(tail, all_records, tickets + 3 * slot, ticket_lds[0] != 0, ex, B, nt, nsets, lay.n,
+               lds, ticket_lds);
 }
 
 __global__ void __launch_bounds__(kGramThreads) fill_zero_i32_kernel(int32_t* p, int n) {
@@ -1320,7 +1431,7 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
       lay.region[i] = 0;
     }
     hipLaunchKernelGGL(gram_split_bf16_kernel, dim3(padded), dim3(512), 0, s, lay, B, T, npairs,
-                       nsets, nblocks, records, tickets, xbuf);
+                       nsets, nblocks, records, tickets, xbuf, SplitTail{});
   } else if (mfma) {
     nt = ceil_div(T, kGramTile);
     const int npairs = nt * (nt + 1) / 2;
@@ -1576,11 +1687,98 @@ extern "C" int dpc_gram_sqnorms_multi(int n, const void* const* A, const void* c
   hipLaunchKernelGGL(fill_zero_i32_kernel, dim3(ceil_div(nticket, kGramThreads)),
                      dim3(kGramThreads), 0, s, tickets, nticket);
   hipLaunchKernelGGL(gram_split_bf16_kernel, dim3(nblocks), dim3(512), 0, s, lay, B, T, npairs,
-                     nsets, nblocks, records, tickets, xbuf);
+                     nsets, nblocks, records, tickets, xbuf, SplitTail{});
   DPC_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(gram_finish_kernel, dim3(ceil_div(B, kGramThreads / 64)), dim3(kGramThreads), 0,
                      s, (const double*)records, B, nt, n, accumulate, (const double*)nullptr,
                      sqnorm, sqerr);
+  DPC_HIP_CHECK(hipGetLastError());
+  return DPC_OK;
+}
+
+namespace {
+bool gram_clip_one_launch(int B, int T, int din, int dout, int dtype, int with_bias) {
+  const size_t dmax = (size_t)(din > dout ? din : dout);
+  // The tail's LDS holds one example's records, then 2 B doubles and the
+  // clip routine's words.
+  const size_t nt = (size_t)ceil_div(T, kGramTile), np = nt * (nt + 1) / 2;
+  const size_t lds_doubles = (size_t)(4 * 3 * kGTileBytes) / sizeof(double);
+  return dtype == DPC_BF16 && !with_bias && din % 8 == 0 && dout % 8 == 0 && split_shape(T) &&
+         B <= kSplitTailMaxB && ((size_t)T + kGramTile) * dmax * 2 < ((size_t)1 << 31) &&
+         np * DPC_GRAM_REC_WORDS <= lds_doubles && 2 * (size_t)B + 64 <= lds_doubles;
+}
+}  // namespace
+
+extern "C" size_t dpc_gram_clip_workspace_bytes(int B, int T) {
+  return dpc_gram_workspace_bytes(B, T);
+}
+
+extern "C" size_t dpc_gram_clip_counter_bytes(int B, int T) {
+  if (B <= 0 || T <= 0) return 0;
+  const int nsets = split_shape(T) ? split_sets_per_example(ceil_div(T, kGramTile)) : 0;
+  // The split kernel's tickets, one counter per example, the example counter.
+  return (size_t)(3 * (size_t)B * nsets + (size_t)B + 1) * sizeof(int32_t);
+}
+
+extern "C" int dpc_gram_clip_factors(const void* A, const void* G, int B, int T, int din,
+                                     int dout, int dtype, int with_bias, double C, int kind,
+                                     double gamma, const double* guard_rel,
+                                     const double* guard_abs, const int* guard_mult, int n_guards,
+                                     float count_threshold, double* sqnorm, double* sqerr,
+                                     float* scale, double* scale64, float* norms_out,
+                                     int* nclipped, void* plan, void* ws, size_t ws_bytes,
+                                     int32_t* counters, size_t counter_bytes, void* stream) {
+  if (B < 0 || T <= 0 || din <= 0 || dout <= 0) return DPC_EINVAL;
+  if (B == 0) return DPC_OK;
+  if (!A || !G || !sqnorm || !ws) return DPC_EINVAL;
+  if (dtype != DPC_F32 && dtype != DPC_BF16) return DPC_EINVAL;
+  if (B > 65535) return DPC_ENOTSUP;
+  if (ws_bytes < dpc_gram_clip_workspace_bytes(B, T)) return DPC_ENOSPC;
+  ClipJob job;
+  int r = clip_job_from_args(C, kind, gamma, guard_rel, guard_abs, guard_mult, n_guards,
+                             count_threshold, scale, scale64, norms_out, nclipped, plan, &job);
+  if (r != DPC_OK) return r;
+  if (!gram_clip_one_launch(B, T, din, dout, dtype, with_bias)) {
+    // The norms and the clip factors as separate launches (the counters
+    // are not used).
+    r = dpc_gram_sqnorms(A, G, B, T, din, dout, dtype, with_bias, 0, sqnorm, sqerr, ws, ws_bytes,
+                         stream);
+    if (r != DPC_OK) return r;
+    return dpc_clip_factors(sqnorm, sqerr, B, C, kind, gamma, guard_rel, guard_abs, guard_mult,
+                            n_guards, count_threshold, scale, scale64, norms_out, nclipped, plan,
+                            stream);
+  }
+  if (!counters) return DPC_EINVAL;
+  if (counter_bytes < dpc_gram_clip_counter_bytes(B, T)) return DPC_ENOSPC;
+  hipStream_t s = (hipStream_t)stream;
+  const int nt = ceil_div(T, kGramTile);
+  const int npairs = nt * (nt + 1) / 2;
+  const int nsets = split_sets_per_example(nt);
+  const int nblocks = 2 * nsets * B;
+  const int padded = ceil_div(nblocks, kXcds) * kXcds;
+  uint8_t* base = (uint8_t*)ws;
+  double* records = (double*)base;
+  // The exchange area where dpc_gram_sqnorms keeps it (after the records
+  // and its own ticket words, unused here).
+  float* xbuf = (float*)(base + align256(gram_records_bytes(B, T)) + split_tickets_bytes(B, T));
+  const int n_tickets = 3 * nsets * B;
+  SplitLayers lay;
+  lay.n = 1;
+  for (int i = 0; i < kSplitMaxLayers; ++i) {
+    lay.A[i] = (const uint16_t*)A;
+    lay.G[i] = (const uint16_t*)G;
+    lay.din[i] = din;
+    lay.dout[i] = dout;
+    lay.region[i] = 0;
+  }
+  SplitTail tail;
+  tail.ex_done = counters + n_tickets;
+  tail.done = tail.ex_done + B;
+  tail.sqnorm = sqnorm;
+  tail.sqerr = sqerr;
+  tail.job = job;
+  hipLaunchKernelGGL(gram_split_bf16_kernel, dim3(padded), dim3(512), 0, s, lay, B, T, npairs,
+                     nsets, nblocks, records, counters, xbuf, tail);
   DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;
 }

@@ -221,27 +221,109 @@ def clip_factors(
     n = len(guards)
     rel = (ctypes.c_double * n)(*[g[0] for g in guards])
     abs_ = (ctypes.c_double * n)(*[g[1] for g in guards])
-    def mult_code(g):
+    mult, codes = _guard_mults(guards)
+    cf = _clip_outputs(B, n, codes, dev)
+    nat.call(
+        "dpc_clip_factors", nat.ptr(_contig(sqnorm)), nat.ptr(None if err is None else _contig(err)),
+        B, float(clipping_norm), kind, float(gamma), rel, abs_, mult, n, float(count_threshold),
+        nat.ptr(cf.scale), nat.ptr(cf.scale64), nat.ptr(cf.norms), nat.ptr(cf.nclipped),
+        nat.ptr(cf.plan), nat.stream_handle(dev),
+    )
+    return cf
+
+
+def _guard_mults(guards):
+    """The guards' multiply dtype codes (third element: a dtype, ``True`` for
+    bfloat16, absent for float32) as a ctypes array, and as a list."""
+
+    def code(g):
         m = g[2] if len(g) > 2 else torch.float32
         if isinstance(m, bool):
             m = torch.bfloat16 if m else torch.float32
         return nat.dtype_code(m, wide=True)
 
-    codes = [mult_code(g) for g in guards]
-    mult = (ctypes.c_int * n)(*codes)
-    scale = torch.empty((n, B), dtype=torch.float32, device=dev)
-    scale64 = (torch.empty((n, B), dtype=torch.float64, device=dev)
-               if nat.DPC_F64 in codes else None)
-    norms = torch.empty(B, dtype=torch.float32, device=dev)
-    nclipped = torch.empty(1, dtype=torch.int32, device=dev)
-    plan = torch.empty((n, nat.load().dpc_clip_plan_bytes(B)), dtype=torch.uint8, device=dev)
-    nat.call(
-        "dpc_clip_factors", nat.ptr(_contig(sqnorm)), nat.ptr(None if err is None else _contig(err)),
-        B, float(clipping_norm), kind, float(gamma), rel, abs_, mult, n, float(count_threshold),
-        nat.ptr(scale), nat.ptr(scale64), nat.ptr(norms), nat.ptr(nclipped), nat.ptr(plan),
-        nat.stream_handle(dev),
-    )
-    return ClipFactors(scale=scale, norms=norms, nclipped=nclipped, plan=plan, scale64=scale64)
+    codes = [code(g) for g in guards]
+    return (ctypes.c_int * len(codes))(*codes), codes
+
+
+def _clip_outputs(B, n, codes, dev) -> ClipFactors:
+    return ClipFactors(
+        scale=torch.empty((n, B), dtype=torch.float32, device=dev),
+        norms=torch.empty(B, dtype=torch.float32, device=dev),
+        nclipped=torch.empty(1, dtype=torch.int32, device=dev),
+        plan=torch.empty((n, nat.load().dpc_clip_plan_bytes(B)), dtype=torch.uint8, device=dev),
+        scale64=(torch.empty((n, B), dtype=torch.float64, device=dev)
+                 if nat.DPC_F64 in codes else None))
+
+
+# Counter buffers of dpc_gram_clip_factors, one per (device, stream), zero
+# filled once: every call leaves them zero.
+_GRAM_CLIP_COUNTERS: dict = {}
+
+
+def _gram_clip_counters(dev, stream, nbytes: int) -> torch.Tensor:
+    key = (str(dev), stream.value or 0)
+    buf = _GRAM_CLIP_COUNTERS.get(key)
+    if buf is None or buf.numel() * 4 < nbytes:
+        buf = torch.zeros(max(1, (nbytes + 3) // 4), dtype=torch.int32, device=dev)
+        _GRAM_CLIP_COUNTERS[key] = buf
+    return buf
+
+
+def gram_clip_factors(
+    A: torch.Tensor,
+    G: torch.Tensor,
+    clipping_norm: float,
+    guards,
+    *,
+    with_bias: bool = False,
+    kind: int = nat.SCALE_FIXED,
+    gamma: float = 0.0,
+    count_threshold: float,
+):
+    """:func:`gram_sqnorms` (with its error bound) followed by
+    :func:`clip_factors` on the result, in one launch where the split Gram
+    kernel applies (``dpc_gram_clip_factors``; the same bits as the two
+    calls).  Returns ``(sqnorm, err, ClipFactors)``.  Under HIP-graph capture
+    the two calls run instead (the one-launch path keeps counters that live
+    across calls)."""
+    dev = nat.require_device(A, G)
+    if A.dim() != 3 or G.dim() != 3 or A.shape[:2] != G.shape[:2] or A.dtype != G.dtype:
+        raise ConfigurationError(
+            f"expected A [B, T, din] and G [B, T, dout] of one dtype, got {tuple(A.shape)}, "
+            f"{tuple(G.shape)}")
+    if not 1 <= len(guards) <= 4:
+        raise ConfigurationError("between 1 and 4 guards are supported")
+    if torch.cuda.is_current_stream_capturing():
+        sq, err = gram_sqnorms(A, G, with_bias=with_bias, return_error=True)
+        cf = clip_factors(sq, clipping_norm, guards, err=err, kind=kind, gamma=gamma,
+                          count_threshold=count_threshold)
+        return sq, err, cf
+    B, T, din = A.shape
+    dout = G.shape[2]
+    A, G = _contig(A), _contig(G)
+    n = len(guards)
+    rel = (ctypes.c_double * n)(*[g[0] for g in guards])
+    abs_ = (ctypes.c_double * n)(*[g[1] for g in guards])
+    mult, codes = _guard_mults(guards)
+    cf = _clip_outputs(B, n, codes, dev)
+    sq = torch.empty(B, dtype=torch.float64, device=dev)
+    err = torch.empty(B, dtype=torch.float64, device=dev)
+    if B > 0:
+        stream = nat.stream_handle(dev)
+        lib = nat.load()
+        ws_bytes = lib.dpc_gram_clip_workspace_bytes(B, T)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        counters = _gram_clip_counters(dev, stream, lib.dpc_gram_clip_counter_bytes(B, T))
+        nat.call(
+            "dpc_gram_clip_factors", nat.ptr(A), nat.ptr(G), B, T, din, dout,
+            nat.dtype_code(A.dtype), int(with_bias), float(clipping_norm), kind, float(gamma),
+            rel, abs_, mult, n, float(count_threshold), nat.ptr(sq), nat.ptr(err),
+            nat.ptr(cf.scale), nat.ptr(cf.scale64), nat.ptr(cf.norms), nat.ptr(cf.nclipped),
+            nat.ptr(cf.plan), nat.ptr(ws), ws_bytes, nat.ptr(counters), counters.numel() * 4,
+            stream,
+        )
+    return sq, err, cf
 
 
 @dataclass
@@ -820,6 +902,7 @@ def philox4x32_10(counter: tuple[int, int, int, int], key: tuple[int, int], n: i
 
 __all__ = [
     "ClipFactors",
+    "gram_clip_factors",
     "GroupedNoise",
     "NoiseSpec",
     "SegmentLayout",
