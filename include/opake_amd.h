@@ -153,7 +153,12 @@ int dpc_flat_sqnorms(const void* a, const void* g, int B, int din, int dout, int
  *                    otherwise (nullable; the float64 multiply of float64
  *                    leaves)
  * norms_out[i] = (float)norm; *nclipped = #{i : (float)norm > count_threshold}
- * (the reference's strict `norms > clipping_norm`, _clipped_fun.py:348-396).
+ * (the reference's strict `norms > clipping_norm`, _clipped_fun.py:348-396);
+ * *nonfinite (nullable; written with system scope, so it may point to pinned
+ * host memory that the host reads once the call has completed) = #{i :
+ * sqnorm[i] or sqerr[i] not finite} -- the examples whose operands held
+ * NaN / Inf, which the ghost paths then clip from their sanitised
+ * per-example gradients (_streaming.py:73,151).
  * guard_rel / guard_abs / guard_mult (nullable: all DPC_F32) are HOST arrays of
  * n_guards (1..4) values, one per storage dtype.  sqnorm and all outputs are device pointers.
  * Any output pointer may be NULL.  `plan` (nullable, device memory of
@@ -168,7 +173,7 @@ int dpc_clip_factors(const double* sqnorm, const double* sqerr, int B, double C,
                      double gamma, const double* guard_rel, const double* guard_abs,
                      const int* guard_mult, int n_guards, float count_threshold, float* scale,
                      double* scale64, float* norms_out, int* nclipped, void* plan,
-                     void* stream);
+                     int* nonfinite, void* stream);
 
 /* dpc_gram_clip_factors: the norm pass and the clip factors of one linear
  * layer -- _streaming.py:70-108 for a layer whose per-example gradients are
@@ -195,8 +200,8 @@ int dpc_gram_clip_factors(const void* A, const void* G, int B, int T, int din, i
                           const double* guard_rel, const double* guard_abs, const int* guard_mult,
                           int n_guards, float count_threshold, double* sqnorm, double* sqerr,
                           float* scale, double* scale64, float* norms_out, int* nclipped,
-                          void* plan, void* ws, size_t ws_bytes, int32_t* counters,
-                          size_t counter_bytes, void* stream);
+                          void* plan, int* nonfinite, void* ws, size_t ws_bytes,
+                          int32_t* counters, size_t counter_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Clipped batch sum of a linear layer with the noise epilogue fused.
@@ -347,6 +352,15 @@ int dpc_leaves_apply_ex(const int64_t* ptrs, const int64_t* sizes, const int32_t
                         int dtype, int mult_dtype, int acc_dtype, const float* scale,
                         const double* scale64, const int32_t* leaf_scale_row, void* out,
                         void* out_sq, int out_dtype, double* post_sq, void* stream);
+
+/* dpc_sanitize_columns: out[e, :, k] = x[e, :, k] when column k of matrix e
+ * (n matrices [T, d], any of the four dtypes) holds only finite values, else
+ * zeros.  With A and G sanitised this way, G'^T A' is exactly the
+ * reference's sanitised per-example gradient of a linear layer
+ * (nan_to_num of G^T A, _streaming.py:73,151): a non-finite A[t, k] makes
+ * column k of G^T A non-finite, a non-finite G[t, m] row m.  The ghost
+ * paths clip the examples whose Gram norm is not finite from these. */
+int dpc_sanitize_columns(const void* x, void* out, int n, int T, int d, int dtype, void* stream);
 
 /* Per-group sums of per-leaf squared norms: out[g * B + b] (float64) = sum of
  * x[b * stride + j] over the columns j with col_group[j] == g, in column

@@ -73,7 +73,7 @@ SIGNATURES = {
         _c_int,
         [_c_void_p, _c_void_p, _c_int, _c_double, _c_int, _c_double, ctypes.POINTER(_c_double),
          ctypes.POINTER(_c_double), ctypes.POINTER(_c_int), _c_int, _c_float, _c_void_p,
-         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     ),
     "dpc_clipped_sum_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "dpc_clipped_sum": (
@@ -96,7 +96,7 @@ SIGNATURES = {
         [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_double, _c_int,
          _c_double, ctypes.POINTER(_c_double), ctypes.POINTER(_c_double), ctypes.POINTER(_c_int),
          _c_int, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-         _c_void_p, _c_void_p, _c_size_t, _c_void_p, _c_size_t, _c_void_p],
+         _c_void_p, _c_void_p, _c_void_p, _c_size_t, _c_void_p, _c_size_t, _c_void_p],
     ),
     "dpc_gram_sqnorms_multi": (
         _c_int,
@@ -127,6 +127,9 @@ SIGNATURES = {
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_void_p,
          _c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p],
+    ),
+    "dpc_sanitize_columns": (
+        _c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p],
     ),
     "dpc_leaves_apply_ex": (
         _c_int,

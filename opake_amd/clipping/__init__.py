@@ -15,6 +15,7 @@ from opake_amd.clipping._model import (
     DirectCapture,
     GhostGradAux,
     LinearCapture,
+    auto_ghost_clipped_grad,
     ghost_capture,
     ghost_clip_captured,
     ghost_clipped_grad,
@@ -44,6 +45,7 @@ __all__ = [
     "LeafClipResult",
     "LinearCapture",
     "auto_clipped_grad",
+    "auto_ghost_clipped_grad",
     "auto_scale_pytree",
     "clip_pytree",
     "clipped_fun",

@@ -36,9 +36,11 @@ Differences from the materialised reference, all documented in tests:
   power of two of the scale, which is exact, and the mantissa on the
   accumulators); the reference instead rounds each ``c_i (G_i^T A_i)`` entry
   to the leaf dtype before its fp32 batch sum;
-* an example whose ``A_i`` or ``G_i`` holds NaN/Inf gets a non-finite norm
-  and clip factor 0 (the whole example is dropped); the reference instead
-  zeroes the non-finite gradient entries and keeps the rest.
+* an example whose ``A_i`` or ``G_i`` holds NaN/Inf is clipped the
+  reference's way (its non-finite gradient entries zeroed, see
+  ``_nonfinite``), with ``nonfinite="sanitize"`` (the default) outside HIP
+  graph capture; with ``nonfinite="drop"`` (and under capture) it gets clip
+  factor 0 and is left out.
 """
 
 from __future__ import annotations
@@ -50,7 +52,9 @@ from torch.autograd.profiler import record_function
 
 from opake_amd import _native as nat
 from opake_amd import ops
+from opake_amd.clipping import _nonfinite as _nf
 from opake_amd.clipping import _numerics as num
+from opake_amd.clipping._leaves import _sum_dtype_of, leaves_clip_sum
 from opake_amd.exceptions import ConfigurationError, InputTypeError
 from opake_amd.noise import GaussianNoiseState, step_key_for
 from opake_amd.random import generator_from_key
@@ -66,12 +70,19 @@ class GhostClipAux:
     ``grad_norms``: per-example gradient norms before clipping (float32, the
     reference's accumulation dtype).  ``clip_scales``: the guarded factors that
     were applied.  ``num_clipped``: int32 [1], examples with norm > C.
+    ``clipped_grad_norms``: per-example norms after clipping, ``scale_i *
+    norm_i`` (float32, computed on access; the clipped gradient is never
+    formed).
     """
 
     grad_norms: torch.Tensor
     clip_scales: torch.Tensor
     num_clipped: torch.Tensor
     batch_size: int
+
+    @property
+    def clipped_grad_norms(self) -> torch.Tensor:
+        return self.clip_scales * self.grad_norms
 
     @property
     def clipping_rate(self) -> float:
@@ -144,6 +155,7 @@ def ghost_clip_sum(
     noise_fn=None,
     noise_state: GaussianNoiseState | None = None,
     gemm_events=None,
+    nonfinite: str = "sanitize",
 ):
     """Clipped (and optionally noised) sum of a linear layer's per-example gradients.
 
@@ -156,6 +168,9 @@ def ghost_clip_sum(
     ``gemm_events``: optional ``(start, end)`` pair of events (``torch.cuda.Event``
     or the fence-free ``opake_amd._native.TimingEvent``)
     recorded on the current stream around the clipped-sum launch (timing hook).
+    ``nonfinite``: ``"sanitize"`` clips an example whose operands hold NaN/Inf
+    from its sanitised gradient, as the reference does (the host reads a
+    count the norm pass leaves in pinned memory); ``"drop"`` leaves it out.
     """
     if isinstance(clipping_norm, PerGroup):
         raise ConfigurationError("per-group clipping is not supported by ghost_clip_sum")
@@ -177,23 +192,27 @@ def ghost_clip_sum(
             raise ConfigurationError("noise_state is required with noise_fn")
         out = ghost_clip_sum(A, G, clipping_norm=clipping_norm, normalize_by=normalize_by,
                              bias=bias, auto_s_gamma=auto_s_gamma, dtype=dtype,
-                             return_aux=return_aux, gemm_events=gemm_events)
+                             return_aux=return_aux, gemm_events=gemm_events,
+                             nonfinite=nonfinite)
         res, aux = out if return_aux else (out, None)
         res, next_state = noise_fn(res, noise_state)
         return ((res, aux) if return_aux else res), next_state
 
+    watch = _nf.watch(A.device, 1, nonfinite)
+    flag = watch.slot(0) if watch is not None else None
     with record_function("opake::ghost_clip_sum"):
         guards = [guard_for_linear(A.dtype, din, dout, bias)]
         bound = num.conservative_bound(clipping_norm)
         threshold = num.float32_of(clipping_norm)
         if T > 1:
             # Norms and clip factors in one launch where the split Gram kernel applies.
-            _, _, cf = ops.gram_clip_factors(A, G, bound, guards, with_bias=bias, kind=kind,
-                                             gamma=gamma, count_threshold=threshold)
+            sq, err, cf = ops.gram_clip_factors(A, G, bound, guards, with_bias=bias, kind=kind,
+                                                gamma=gamma, count_threshold=threshold,
+                                                nonfinite=flag)
         else:
             sq, err = ghost_sqnorms(A, G, bias=bias)
             cf = ops.clip_factors(sq, bound, guards, err=err, kind=kind, gamma=gamma,
-                                  count_threshold=threshold)
+                                  count_threshold=threshold, nonfinite=flag)
         spec = None
         next_state = None
         std = 0.0
@@ -233,6 +252,10 @@ def ghost_clip_sum(
     tree = {"weight": w}
     if bias:
         tree["bias"] = b
+    if watch is not None and watch.count() > 0:
+        _clip_nonfinite_examples(A, G, sq, err, cf, tree, bias=bias, clipping_norm=clipping_norm,
+                                 kind=kind, gamma=gamma, normalize_by=normalize_by,
+                                 threshold=threshold)
     aux = GhostClipAux(grad_norms=cf.norms, clip_scales=cf.scale[0], num_clipped=cf.nclipped,
                        batch_size=B)
     if noise_fn is None:
@@ -240,6 +263,34 @@ def ghost_clip_sum(
         return (result, aux) if return_aux else result
     result = NoisedPytree(pytree=tree, max_norm=max_norm, noise_stddev=std)
     return ((result, aux) if return_aux else result), next_state
+
+
+def _clip_nonfinite_examples(A, G, sq, err, cf, tree, *, bias, clipping_norm, kind, gamma,
+                             normalize_by, threshold):
+    """The examples whose norm is not finite (their operands hold NaN/Inf),
+    clipped from their sanitised per-example gradients by the leaf kernels and
+    added to ``tree``; their norms, scales and the clipped count in ``cf``
+    are replaced."""
+    bad = _nf.bad_examples(sq, err)
+    if bad.numel() == 0:
+        return
+    pdt = A.dtype
+    w, b = _nf.sanitized_linear_grads(A[bad], G[bad], pdt, bias)
+    leaves = [b, w] if bias else [w]  # flatten order: "bias" < "weight"
+    out_dtype = tree["weight"].dtype
+    res = leaves_clip_sum(leaves, float(clipping_norm),
+                          kind="auto_s" if kind == nat.SCALE_AUTO_S else "fixed", gamma=gamma,
+                          sum_dtypes={pdt: (_sum_dtype_of(pdt, None), out_dtype)})
+    sums = res.reduced if bias else [None, res.reduced[0]]
+    for name, x in zip(("bias", "weight"), sums):
+        if x is None:
+            continue
+        if normalize_by != 1.0:
+            x = x / normalize_by
+        tree[name] = (tree[name] + x).to(out_dtype)
+    cf.norms[bad] = res.norms
+    cf.scale[0][bad] = res.scales[pdt][0]
+    cf.nclipped.copy_((cf.norms > threshold).sum().reshape(1).to(torch.int32))
 
 
 __all__ = ["GhostClipAux", "ghost_clip_sum", "ghost_sqnorms", "guard_for_linear"]

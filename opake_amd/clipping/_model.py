@@ -57,9 +57,10 @@ from torch.autograd.profiler import record_function
 from opake_amd import _native as nat
 from opake_amd import ops
 from opake_amd._tables import device_table
+from opake_amd.clipping import _nonfinite as _nf
 from opake_amd.clipping import _numerics as num
 from opake_amd.clipping._clipped_fun import FixedClipState
-from opake_amd.clipping._leaves import LeafBatch, _sum_dtype_of
+from opake_amd.clipping._leaves import LeafBatch, _sum_dtype_of, leaves_clip_sum
 from opake_amd.exceptions import ConfigurationError, InputTypeError
 from opake_amd.noise import GaussianNoiseState, step_key_for
 from opake_amd.pytree import param_path
@@ -72,7 +73,8 @@ class GhostGradAux:
     """Per-example diagnostics (device tensors): loss values, norms before
     clipping (float32 [B]), applied clip scales (float32 [n_guards, B] per
     group), ``num_clipped`` (int32 [1], or [G] per group), and per-group norms
-    ``{group: float32 [B]}`` with ``PerGroup`` clipping."""
+    ``{group: float32 [B]}`` with ``PerGroup`` clipping; ``clipped_grad_norms``
+    from them."""
 
     loss_values: torch.Tensor | None
     grad_norms: torch.Tensor
@@ -80,6 +82,17 @@ class GhostGradAux:
     num_clipped: torch.Tensor
     batch_size: int
     group_norms: dict | None = None
+
+    @property
+    def clipped_grad_norms(self) -> torch.Tensor:
+        """Per-example norms after clipping (``ClippedGradAux.clipped_grad_norms``,
+        _clipped_grad.py:34-61): ``scale_i * norm_i``, per group then combined
+        (float32, computed on access; the clipped gradient is never formed)."""
+        if self.group_norms is None:
+            return self.clip_scales[0] * self.grad_norms
+        parts = [self.clip_scales[k][0].double() * self.group_norms[n].double()
+                 for k, n in enumerate(sorted(self.group_norms))]
+        return torch.sqrt(sum(p * p for p in parts)).to(torch.float32)
 
     @property
     def clipping_rate(self) -> float | None:
@@ -297,6 +310,8 @@ def ghost_clip_captured(
     dtype: torch.dtype | None = None,
     return_aux: bool = False,
     gemm_events: list | None = None,
+    auto_s_gamma: float | None = None,
+    nonfinite: str = "sanitize",
 ):
     """Clip -> sum (-> noise) from the captured operands of linear layers.
 
@@ -309,8 +324,14 @@ def ghost_clip_captured(
     timing events (``TimingEvent``: fence-free, ``elapsed_time`` like
     ``torch.cuda.Event``) around each clipped-sum launch (and each per-example
     gradient launch of a layer that takes the direct method).
+    ``auto_s_gamma``: AUTO-S scaling ``R / (||g|| + gamma)`` with ``R =
+    clipping_norm`` (``_auto.py:211-367``) instead of ``min(1, C / ||g||)``.
+    ``nonfinite``: ``"sanitize"`` (default) clips an example whose operands
+    hold NaN/Inf from its sanitised per-example gradients, as the reference
+    does; ``"drop"`` leaves it out (as happens under HIP-graph capture).
     """
     _validate_bound(clipping_norm)
+    kind, gamma = _scale_kind(auto_s_gamma)
     if normalize_by <= 0.0:
         raise ConfigurationError(f"normalize_by must be > 0, got {normalize_by}.")
     if not captures:
@@ -322,7 +343,8 @@ def ghost_clip_captured(
             raise ConfigurationError("noise_state is required with noise_fn")
         out = ghost_clip_captured(captures, clipping_norm=clipping_norm,
                                   normalize_by=normalize_by, dtype=dtype,
-                                  return_aux=return_aux, gemm_events=gemm_events)
+                                  return_aux=return_aux, gemm_events=gemm_events,
+                                  auto_s_gamma=auto_s_gamma, nonfinite=nonfinite)
         res, aux = out if return_aux else (out, None)
         res, next_state = noise_fn(res, noise_state)
         return ((res, aux) if return_aux else res), next_state
@@ -492,8 +514,10 @@ def ghost_clip_captured(
                      key=str)
     guards = [num.guard_constants(dt, torch.promote_types(dt, torch.float32), roundoff)
               for dt in storage]
+    watch = _nf.watch(device, n_groups, nonfinite)
     cfs = [ops.clip_factors(sq[g], num.conservative_bound(bounds[g]), guards, err=err[g],
-                            count_threshold=num.float32_of(bounds[g]))
+                            kind=kind, gamma=gamma, count_threshold=num.float32_of(bounds[g]),
+                            nonfinite=watch.slot(g) if watch is not None else None)
            for g in range(n_groups)]
 
     std = 0.0
@@ -635,6 +659,10 @@ def ghost_clip_captured(
                                  seed=step_key.seed, leaf_ids=[leaf_index[n] for n, _, _ in items],
                                  inplace=True)
     tree = {k: tree[k] for k in leaf_names}
+    if watch is not None and watch.count() > 0:
+        _clip_nonfinite_examples(
+            dense, segmented, direct, leaf_names, leaf_group, bounds, sq, err, cfs, storage, tree,
+            per_group=per_group, kind=kind, gamma=gamma, normalize_by=normalize_by, dtype=dtype)
     if noise_fn is None:
         result = clipped(tree, max_norm=max_norm)
     else:
@@ -654,6 +682,77 @@ def ghost_clip_captured(
     if noise_fn is None:
         return result
     return result, next_noise_state
+
+
+def _scale_kind(auto_s_gamma):
+    if auto_s_gamma is None:
+        return nat.SCALE_FIXED, 0.0
+    if isinstance(auto_s_gamma, bool) or not auto_s_gamma > 0:
+        raise ConfigurationError(f"gamma must be positive, got {auto_s_gamma}")
+    return nat.SCALE_AUTO_S, float(auto_s_gamma)
+
+
+def _clip_nonfinite_examples(dense, segmented, direct, leaf_names, leaf_group, bounds, sq, err,
+                             cfs, storage, tree, *, per_group, kind, gamma, normalize_by, dtype):
+    """The (example, group) pairs whose norm is not finite (a dense or
+    segmented layer of the group holds NaN/Inf for the example), clipped from
+    the example's sanitised per-example gradients of that group's leaves --
+    as the reference materialises them -- by the leaf kernels with the
+    group's bound; their sums are added to ``tree`` and their norms, scales
+    and counts replace the flagged entries in ``sq`` / ``cfs``.  A group's
+    clip factor depends on that group's leaves only, so pairs whose group
+    norm is finite were already right."""
+    scale = "auto_s" if kind == nat.SCALE_AUTO_S else "fixed"
+    for g, cf in enumerate(cfs):
+        bad = _nf.bad_examples(sq[g], err[g])
+        if bad.numel() == 0:
+            continue
+        bad_list = bad.tolist()
+        names = [n for n in leaf_names if leaf_group[n] == g]
+        leaves = {}
+        for L in dense:
+            wn, bn = f"{L.name}.weight", f"{L.name}.bias"
+            if wn not in names and bn not in names:
+                continue
+            pdt = L.cap.param_dtype or L.A.dtype
+            w, b = _nf.sanitized_linear_grads(L.A[bad], L.G[bad], pdt, L.cap.has_bias)
+            leaves[wn] = w
+            if b is not None:
+                leaves[bn] = b
+        for L in segmented:
+            wn = f"{L.name}.weight"
+            if wn not in names:
+                continue
+            pdt = L.cap.param_dtype or L.A.dtype
+            starts = np.concatenate([[0], np.cumsum(L.cap.segments)]).tolist()
+            ws = []
+            for b in bad_list:
+                r0, r1 = starts[b], starts[b + 1]
+                if r1 == r0:
+                    ws.append(torch.zeros((L.G.shape[1], L.A.shape[1]), dtype=pdt,
+                                          device=L.A.device))
+                    continue
+                w, _ = _nf.sanitized_linear_grads(L.A[r0:r1].unsqueeze(0),
+                                                  L.G[r0:r1].unsqueeze(0), pdt, False)
+                ws.append(w[0])
+            leaves[wn] = torch.stack(ws)
+        for n, t in direct.items():
+            if n in names:
+                leaves[n] = t[bad]
+        order = [leaves[n] for n in names]
+        sum_dtypes = {t.dtype: (_sum_dtype_of(t.dtype, None), dtype or t.dtype) for t in order}
+        res = leaves_clip_sum(order, bounds[g], kind=scale, gamma=gamma, sum_dtypes=sum_dtypes)
+        for n, x in zip(names, res.reduced):
+            if normalize_by != 1.0:
+                x = x / normalize_by
+            tree[n] = (tree[n] + x).to(tree[n].dtype)
+        cf.norms[bad] = res.norms.to(cf.norms.dtype)
+        for si, dt in enumerate(storage):
+            if dt in res.scales:
+                cf.scale[si][bad] = res.scales[dt][0]
+        cf.nclipped.copy_((cf.norms > num.float32_of(bounds[g])).sum().reshape(1).to(torch.int32))
+        sq[g, bad] = res.norms.double() ** 2
+        err[g, bad] = 0.0
 
 
 def _capture(model, layers, others, loss_fn, inputs, targets):
@@ -750,6 +849,8 @@ def ghost_clipped_grad(
     return_aux: bool = False,
     dtype: torch.dtype | None = None,
     microbatch_size: int | None = None,
+    auto_s_gamma: float | None = None,
+    nonfinite: str = "sanitize",
 ):
     """Create ``grad_fn(inputs, targets, *, state, noise_fn=None, noise_state=None)``.
 
@@ -764,8 +865,14 @@ def ghost_clipped_grad(
     chunk (chunk sums accumulated in float32 and cast once, as
     ``_microbatch_accumulate_reduced``, _clipped_fun.py:252-345); the noise is
     then added to the total by ``noise_fn`` (not fused).
+
+    ``auto_s_gamma``: AUTO-S scaling (``auto_clipped_grad``, _auto.py:211-367)
+    with ``R = clipping_norm``; ``nonfinite``: as in
+    :func:`ghost_clip_captured`.
     """
     _validate_bound(clipping_norm)
+    _scale_kind(auto_s_gamma)
+    _nf.check_mode(nonfinite)
     if normalize_by <= 0.0:
         raise ConfigurationError(f"normalize_by must be > 0, got {normalize_by}.")
     if microbatch_size is not None and (isinstance(microbatch_size, bool)
@@ -792,7 +899,8 @@ def ghost_clipped_grad(
                                         _slice_batch(inputs, start, stop), targets[start:stop])
             out = ghost_clip_captured(captures, clipping_norm=clipping_norm,
                                       normalize_by=normalize_by, dtype=torch.float32,
-                                      return_aux=return_aux)
+                                      return_aux=return_aux, auto_s_gamma=auto_s_gamma,
+                                      nonfinite=nonfinite)
             if return_aux:
                 out, aux = out
                 auxes.append(replace(aux, loss_values=losses.detach()))
@@ -819,7 +927,8 @@ def ghost_clipped_grad(
         captures, losses = _capture(model, layers, others, loss_fn, inputs, targets)
         out = ghost_clip_captured(captures, clipping_norm=clipping_norm,
                                   normalize_by=normalize_by, noise_fn=noise_fn,
-                                  noise_state=noise_state, dtype=dtype, return_aux=return_aux)
+                                  noise_state=noise_state, dtype=dtype, return_aux=return_aux,
+                                  auto_s_gamma=auto_s_gamma, nonfinite=nonfinite)
         if noise_fn is not None:
             out, next_state = out
         if return_aux:
@@ -832,7 +941,29 @@ def ghost_clipped_grad(
     return grad_fn, state0
 
 
+def auto_ghost_clipped_grad(
+    model: torch.nn.Module,
+    loss_fn,
+    *,
+    R=1.0,
+    gamma: float = 0.01,
+    normalize_by: float = 1.0,
+    return_aux: bool = False,
+    dtype: torch.dtype | None = None,
+    microbatch_size: int | None = None,
+    nonfinite: str = "sanitize",
+):
+    """:func:`ghost_clipped_grad` with AUTO-S scaling ``R / (||g_i|| + gamma)``
+    (``auto_clipped_grad``, _auto.py:211-367): ``max_norm = R /
+    normalize_by``; ``R`` may be a ``PerGroup``."""
+    return ghost_clipped_grad(model, loss_fn, clipping_norm=R, normalize_by=normalize_by,
+                              return_aux=return_aux, dtype=dtype,
+                              microbatch_size=microbatch_size, auto_s_gamma=gamma,
+                              nonfinite=nonfinite)
+
+
 __all__ = [
+    "auto_ghost_clipped_grad",
     "DirectCapture",
     "GhostGradAux",
     "LinearCapture",

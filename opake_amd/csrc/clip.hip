@@ -23,12 +23,12 @@ extern "C" int dpc_clip_factors(const double* sqnorm, const double* sqerr, int B
                                 const double* guard_rel, const double* guard_abs,
                                 const int* guard_mult, int n_guards, float count_threshold,
                                 float* scale, double* scale64, float* norms_out, int* nclipped,
-                                void* plan, void* stream) {
+                                void* plan, int* nonfinite, void* stream) {
   if (B < 0 || (B > 0 && !sqnorm)) return DPC_EINVAL;
   ClipJob job;
   const int r = clip_job_from_args(C, kind, gamma, guard_rel, guard_abs, guard_mult, n_guards,
                                    count_threshold, scale, scale64, norms_out, nclipped, plan,
-                                   &job);
+                                   nonfinite, &job);
   if (r != DPC_OK) return r;
   hipLaunchKernelGGL(clip_factors_kernel, dim3(1), dim3(kClipThreads), 0, (hipStream_t)stream,
                      sqnorm, sqerr, B, job);

@@ -44,6 +44,9 @@ struct ClipJob {
   float* norms_out;  // [B]
   int* nclipped;     // [1]
   void* plans;       // n_guards plans of clip_plan_bytes(B)
+  int* nonfinite;    // [1]: examples whose squared norm (or bound) is not
+                     // finite, stored with system scope (may be pinned host
+                     // memory the host reads once the pass has completed)
 };
 
 // s.to(multiply dtype) as a float: torch converts a float64 to bfloat16 or
@@ -94,7 +97,9 @@ __device__ inline void clip_factors_block(const double* sq, const double* err, i
   int* slow_counts = shm + 2 * nw;
   int* base = shm + 3 * nw;
   int* base_slow = base + 1;
-  int clipped_local = 0;
+  int clipped_local = 0, nonfinite_local = 0;
+  for (int i = tid; i < B; i += blockDim.x)
+    nonfinite_local += !(isfinite(sq[i]) && (err == nullptr || isfinite(err[i])));
   const bool fast_ok = (double)B * job.C <= (double)DPC_FAST_BC_MAX;
   for (int g = 0; g < job.n_guards; ++g) {
     const bool have_plan = job.plans != nullptr;
@@ -151,13 +156,24 @@ __device__ inline void clip_factors_block(const double* sq, const double* err, i
     }
     __syncthreads();
   }
-  for (int off = 32; off > 0; off >>= 1) clipped_local += __shfl_down(clipped_local, off, 64);
-  if (lane == 0) clipped_counts[w] = clipped_local;
+  for (int off = 32; off > 0; off >>= 1) {
+    clipped_local += __shfl_down(clipped_local, off, 64);
+    nonfinite_local += __shfl_down(nonfinite_local, off, 64);
+  }
+  if (lane == 0) {
+    clipped_counts[w] = clipped_local;
+    wave_counts[w] = nonfinite_local;
+  }
   __syncthreads();
   if (tid == 0) {
-    int total = 0;
-    for (int v = 0; v < nw; ++v) total += clipped_counts[v];
+    int total = 0, bad = 0;
+    for (int v = 0; v < nw; ++v) {
+      total += clipped_counts[v];
+      bad += wave_counts[v];
+    }
     if (job.nclipped) *job.nclipped = total;
+    if (job.nonfinite)
+      __hip_atomic_store(job.nonfinite, bad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 
@@ -165,7 +181,8 @@ __device__ inline void clip_factors_block(const double* sq, const double* err, i
 inline int clip_job_from_args(double C, int kind, double gamma, const double* guard_rel,
                               const double* guard_abs, const int* guard_mult, int n_guards,
                               float count_threshold, float* scale, double* scale64,
-                              float* norms_out, int* nclipped, void* plan, ClipJob* job) {
+                              float* norms_out, int* nclipped, void* plan, int* nonfinite,
+                              ClipJob* job) {
   if (n_guards < 1 || n_guards > kClipMaxGuards || !guard_rel || !guard_abs) return DPC_EINVAL;
   if (kind != DPC_SCALE_FIXED && kind != DPC_SCALE_AUTO_S) return DPC_EINVAL;
   if (plan && !scale) return DPC_EINVAL;
@@ -186,6 +203,7 @@ inline int clip_job_from_args(double C, int kind, double gamma, const double* gu
   j.norms_out = norms_out;
   j.nclipped = nclipped;
   j.plans = plan;
+  j.nonfinite = nonfinite;
   *job = j;
   return DPC_OK;
 }

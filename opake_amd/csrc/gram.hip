@@ -1726,8 +1726,9 @@ extern "C" int dpc_gram_clip_factors(const void* A, const void* G, int B, int T,
                                      const double* guard_abs, const int* guard_mult, int n_guards,
                                      float count_threshold, double* sqnorm, double* sqerr,
                                      float* scale, double* scale64, float* norms_out,
-                                     int* nclipped, void* plan, void* ws, size_t ws_bytes,
-                                     int32_t* counters, size_t counter_bytes, void* stream) {
+                                     int* nclipped, void* plan, int* nonfinite, void* ws,
+                                     size_t ws_bytes, int32_t* counters, size_t counter_bytes,
+                                     void* stream) {
   if (B < 0 || T <= 0 || din <= 0 || dout <= 0) return DPC_EINVAL;
   if (B == 0) return DPC_OK;
   if (!A || !G || !sqnorm || !ws) return DPC_EINVAL;
@@ -1736,7 +1737,8 @@ extern "C" int dpc_gram_clip_factors(const void* A, const void* G, int B, int T,
   if (ws_bytes < dpc_gram_clip_workspace_bytes(B, T)) return DPC_ENOSPC;
   ClipJob job;
   int r = clip_job_from_args(C, kind, gamma, guard_rel, guard_abs, guard_mult, n_guards,
-                             count_threshold, scale, scale64, norms_out, nclipped, plan, &job);
+                             count_threshold, scale, scale64, norms_out, nclipped, plan, nonfinite,
+                             &job);
   if (r != DPC_OK) return r;
   if (!gram_clip_one_launch(B, T, din, dout, dtype, with_bias)) {
     // The norms and the clip factors as separate launches (the counters
@@ -1746,7 +1748,7 @@ extern "C" int dpc_gram_clip_factors(const void* A, const void* G, int B, int T,
     if (r != DPC_OK) return r;
     return dpc_clip_factors(sqnorm, sqerr, B, C, kind, gamma, guard_rel, guard_abs, guard_mult,
                             n_guards, count_threshold, scale, scale64, norms_out, nclipped, plan,
-                            stream);
+                            nonfinite, stream);
   }
   if (!counters) return DPC_EINVAL;
   if (counter_bytes < dpc_gram_clip_counter_bytes(B, T)) return DPC_ENOSPC;

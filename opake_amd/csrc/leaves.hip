@@ -573,3 +573,36 @@ extern "C" int dpc_leaves_apply_ex(const int64_t* ptrs, const int64_t* sizes,
   DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;
 }
+
+namespace {
+// out[e, :, k] = x[e, :, k] if column k of matrix e holds only finite values,
+// else 0 (every row): the operands whose product G'^T A' is the reference's
+// sanitised per-example gradient of a linear layer (nan_to_num of G^T A,
+// _streaming.py:73,151: a non-finite A[t, k] makes column k of G^T A
+// non-finite, a non-finite G[t, m] row m).  One thread per column: a pass to
+// test it, a pass to copy it; consecutive threads read consecutive columns.
+__global__ void __launch_bounds__(kThreads)
+sanitize_columns_kernel(const void* __restrict__ x, void* __restrict__ out, int T, int d,
+                        int dtype) {
+  const int k = blockIdx.x * kThreads + threadIdx.x;
+  if (k >= d) return;
+  const int64_t base = (int64_t)blockIdx.y * T * d + k;
+  bool finite = true;
+  for (int t = 0; t < T; ++t) finite = finite && isfinite(load_as_f64(x, base + (int64_t)t * d, dtype));
+  for (int t = 0; t < T; ++t) {
+    const int64_t i = base + (int64_t)t * d;
+    store_from_f64(out, i, finite ? load_as_f64(x, i, dtype) : 0.0, dtype);
+  }
+}
+}  // namespace
+
+extern "C" int dpc_sanitize_columns(const void* x, void* out, int n, int T, int d, int dtype,
+                                    void* stream) {
+  if (n < 0 || T < 0 || d < 0 || !known_dtype(dtype)) return DPC_EINVAL;
+  if (n == 0 || T == 0 || d == 0) return DPC_OK;
+  if (!x || !out || n > 65535) return DPC_EINVAL;
+  hipLaunchKernelGGL(sanitize_columns_kernel, dim3(ceil_div(d, kThreads), n), dim3(kThreads), 0,
+                     (hipStream_t)stream, x, out, T, d, dtype);
+  DPC_HIP_CHECK(hipGetLastError());
+  return DPC_OK;
+}

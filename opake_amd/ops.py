@@ -200,6 +200,7 @@ def clip_factors(
     kind: int = nat.SCALE_FIXED,
     gamma: float = 0.0,
     count_threshold: float,
+    nonfinite: torch.Tensor | None = None,
 ) -> ClipFactors:
     """Guarded clip factors for each ``(rel, abs)`` guard, per example.
 
@@ -209,7 +210,9 @@ def clip_factors(
     unconverted scale also comes back in ``scale64``.  ``err``
     (float64 [B], optional): the error bound of ``sqnorm``; the scale is then
     taken from ``sqrt(sqnorm + err)``, the reported norms and the clipped count
-    from ``sqrt(sqnorm)``."""
+    from ``sqrt(sqnorm)``.  ``nonfinite`` (int32 [1], device or pinned host
+    memory, optional) receives the number of examples whose ``sqnorm`` or
+    ``err`` is not finite."""
     dev = nat.require_device(sqnorm, err)
     if sqnorm.dtype != torch.float64 or sqnorm.dim() != 1:
         raise ConfigurationError("sqnorm must be a float64 vector")
@@ -227,7 +230,7 @@ def clip_factors(
         "dpc_clip_factors", nat.ptr(_contig(sqnorm)), nat.ptr(None if err is None else _contig(err)),
         B, float(clipping_norm), kind, float(gamma), rel, abs_, mult, n, float(count_threshold),
         nat.ptr(cf.scale), nat.ptr(cf.scale64), nat.ptr(cf.norms), nat.ptr(cf.nclipped),
-        nat.ptr(cf.plan), nat.stream_handle(dev),
+        nat.ptr(cf.plan), nat.ptr(nonfinite), nat.stream_handle(dev),
     )
     return cf
 
@@ -280,6 +283,7 @@ def gram_clip_factors(
     kind: int = nat.SCALE_FIXED,
     gamma: float = 0.0,
     count_threshold: float,
+    nonfinite: torch.Tensor | None = None,
 ):
     """:func:`gram_sqnorms` (with its error bound) followed by
     :func:`clip_factors` on the result, in one launch where the split Gram
@@ -297,7 +301,7 @@ def gram_clip_factors(
     if torch.cuda.is_current_stream_capturing():
         sq, err = gram_sqnorms(A, G, with_bias=with_bias, return_error=True)
         cf = clip_factors(sq, clipping_norm, guards, err=err, kind=kind, gamma=gamma,
-                          count_threshold=count_threshold)
+                          count_threshold=count_threshold, nonfinite=nonfinite)
         return sq, err, cf
     B, T, din = A.shape
     dout = G.shape[2]
@@ -320,8 +324,8 @@ def gram_clip_factors(
             nat.dtype_code(A.dtype), int(with_bias), float(clipping_norm), kind, float(gamma),
             rel, abs_, mult, n, float(count_threshold), nat.ptr(sq), nat.ptr(err),
             nat.ptr(cf.scale), nat.ptr(cf.scale64), nat.ptr(cf.norms), nat.ptr(cf.nclipped),
-            nat.ptr(cf.plan), nat.ptr(ws), ws_bytes, nat.ptr(counters), counters.numel() * 4,
-            stream,
+            nat.ptr(cf.plan), nat.ptr(nonfinite), nat.ptr(ws), ws_bytes, nat.ptr(counters),
+            counters.numel() * 4, stream,
         )
     return sq, err, cf
 
@@ -860,6 +864,19 @@ def add_noise(
     return y
 
 
+def sanitize_columns(x: torch.Tensor) -> torch.Tensor:
+    """``x`` [n, T, d] with every column (over T) of each matrix that holds a
+    non-finite value set to zero (``dpc_sanitize_columns``)."""
+    dev = nat.require_device(x)
+    if x.dim() != 3:
+        raise ConfigurationError("expected x [n, T, d]")
+    x = _contig(x)
+    out = torch.empty_like(x)
+    nat.call("dpc_sanitize_columns", nat.ptr(x), nat.ptr(out), x.shape[0], x.shape[1],
+             x.shape[2], nat.dtype_code(x.dtype, wide=True), nat.stream_handle(dev))
+    return out
+
+
 def add_noise_leaves(xs, sigmas, *, seed: int, leaf_ids, inplace: bool = False
                      ) -> list[torch.Tensor]:
     """``add_noise`` (Philox stream) of several leaves of one dtype in as few
@@ -903,6 +920,7 @@ def philox4x32_10(counter: tuple[int, int, int, int], key: tuple[int, int], n: i
 __all__ = [
     "ClipFactors",
     "gram_clip_factors",
+    "sanitize_columns",
     "GroupedNoise",
     "NoiseSpec",
     "SegmentLayout",

@@ -19,7 +19,7 @@ import torch
 
 from opake_amd import _native as nat
 from opake_amd import ops
-from opake_amd.clipping import ghost_clipped_grad
+from opake_amd.clipping import auto_ghost_clipped_grad, ghost_clipped_grad
 from opake_amd.moe import TopKMoE, expert_groups
 from opake_amd.noise import gaussian_noise
 from opake_amd.random import key
@@ -174,15 +174,17 @@ def _moe_case(dtype, d, inter, E, B, T, seed=0):
     return ref_model, x, logits, target
 
 
-def _oracle(model, x, logits, target, clipping_norm, names):
+def _oracle(model, x, logits, target, clipping_norm, names, kind="fixed", gamma=0.0):
     per = ghost_oracle.per_example_grads_loop(model, _mse, (x.double(), logits.double()),
                                               target.double())
     leaves = [per[n].float() for n in names]
     if isinstance(clipping_norm, PerGroup):
         groups = [clipping_norm.groups[(n,)] for n in names]
         values = {g: clip_oracle.conservative_bound(v) for g, v in clipping_norm.values.items()}
-        return clip_oracle.stream_clip_and_sum(leaves, None, groups=groups, group_values=values)
-    return clip_oracle.stream_clip_and_sum(leaves, clip_oracle.conservative_bound(clipping_norm))
+        return clip_oracle.stream_clip_and_sum(leaves, None, groups=groups, group_values=values,
+                                               kind=kind, gamma=gamma)
+    return clip_oracle.stream_clip_and_sum(leaves, clip_oracle.conservative_bound(clipping_norm),
+                                           kind=kind, gamma=gamma)
 
 
 @pytest.mark.parametrize("per_group", [True, False])
@@ -205,6 +207,32 @@ def test_ghost_moe_float32_matches_per_example_oracle(dev, per_group):
         assert aux.clipping_rate is None
     else:
         torch.testing.assert_close(aux.grad_norms.cpu().double(), res.norms, rtol=1e-5, atol=0)
+
+
+@pytest.mark.parametrize("per_group", [True, False])
+def test_ghost_moe_auto_s_matches_per_example_oracle(dev, per_group):
+    # AUTO-S on the grouped (per-expert) path: R_k / (||g_k|| + gamma) per
+    # example and group, no min(1, .), the scaled norms below R_k.
+    ref, x, logits, target = _moe_case(torch.float32, 48, 40, 4, 4, 50, seed=9)
+    model = TopKMoE(48, 40, 4, 2).to(dev)
+    model.load_state_dict({k: v.float() for k, v in ref.state_dict().items()})
+    R = expert_groups(model, clipping_norm=0.5) if per_group else 0.5
+    names = sorted(n for n, p in model.named_parameters() if p.requires_grad)
+    res = _oracle(ref, x, logits, target, R, names, kind="auto_s", gamma=0.01)
+    fn, st = auto_ghost_clipped_grad(model, _mse, R=R, gamma=0.01, normalize_by=4.0,
+                                     return_aux=True)
+    (out, aux), _ = fn((x.to(dev), logits.to(dev)), target.to(dev), state=st)
+    for i, n in enumerate(names):
+        assert _rel(out.pytree[n], res.reduced[i] / 4.0) < 1e-5, n
+    if per_group:
+        for k, gname in enumerate(sorted(R.values)):
+            torch.testing.assert_close(aux.group_norms[gname].cpu().double(),
+                                       res.group_norms[gname], rtol=1e-5, atol=0)
+            scaled = aux.clip_scales[k][0].double() * aux.group_norms[gname].double()
+            assert torch.all(scaled <= R.values[gname])
+    else:
+        torch.testing.assert_close(aux.grad_norms.cpu().double(), res.norms, rtol=1e-5, atol=0)
+        assert torch.all(aux.clipped_grad_norms.double() <= 0.5)
 
 
 def test_ghost_moe_bf16_matches_per_example_oracle(dev):

@@ -13,7 +13,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from opake_amd.clipping import ghost_clipped_grad
+from opake_amd.clipping import auto_ghost_clipped_grad, ghost_clipped_grad
 from opake_amd.noise import gaussian_noise
 from opake_amd.random import key
 from opake_amd.transformer import BlockLM, per_example_lm_loss
@@ -47,14 +47,16 @@ def _groups(names):
                      for n in names}, {"attn": 0.3, "mlp": 0.2})
 
 
-def _oracle(ref, ids, tgt, C, names):
+def _oracle(ref, ids, tgt, C, names, kind="fixed", gamma=0.0):
     per = ghost_oracle.per_example_grads_loop(ref, per_example_lm_loss, (ids,), tgt)
     leaves = [per[n].float() for n in names]
     if isinstance(C, PerGroup):
         groups = [C.groups[(n,)] for n in names]
         values = {k: clip_oracle.conservative_bound(v) for k, v in C.values.items()}
-        return clip_oracle.stream_clip_and_sum(leaves, None, groups=groups, group_values=values)
-    return clip_oracle.stream_clip_and_sum(leaves, clip_oracle.conservative_bound(C))
+        return clip_oracle.stream_clip_and_sum(leaves, None, groups=groups, group_values=values,
+                                               kind=kind, gamma=gamma, return_aux=True)
+    return clip_oracle.stream_clip_and_sum(leaves, clip_oracle.conservative_bound(C), kind=kind,
+                                           gamma=gamma, return_aux=True)
 
 
 @pytest.mark.parametrize("per_group", [False, True])
@@ -116,3 +118,36 @@ def test_ghost_block_fused_noise_equals_separate_noise(dev, stream):
     assert isinstance(fused, NoisedPytree)
     for n in names:
         assert torch.equal(fused.pytree[n], separate.pytree[n]), n
+
+
+@pytest.mark.parametrize("per_group", [False, True])
+def test_ghost_block_auto_s_matches_per_example_oracle(dev, per_group):
+    # AUTO-S on the model path (auto_clipped_grad, _auto.py:211-367): scale
+    # R / (||g|| + gamma) per example (per group), no min(1, .); the clipped
+    # norms R ||g|| / (||g|| + gamma) stay below R (the DP bound).
+    ref, ids, tgt = _case(torch.float32, 61, 32, 4, 48, 3, 20, seed=5)
+    model = BlockLM(61, 32, 4, 48, dtype=torch.float32).to(dev)
+    model.load_state_dict({k: v.float() for k, v in ref.state_dict().items()})
+    names = sorted(n for n, p in model.named_parameters() if p.requires_grad)
+    R = _groups(names) if per_group else 0.25
+    res = _oracle(ref, ids, tgt, R, names, kind="auto_s", gamma=0.02)
+    fn, st = auto_ghost_clipped_grad(model, per_example_lm_loss, R=R, gamma=0.02,
+                                     normalize_by=3.0, return_aux=True)
+    (out, aux), _ = fn(ids.to(dev), tgt.to(dev), state=st)
+    assert out.max_norm == (R / 3.0 if not per_group else out.max_norm)
+    for i, n in enumerate(names):
+        assert _rel(out.pytree[n], res.reduced[i] / 3.0) < 1e-5, n
+    torch.testing.assert_close(aux.clipped_grad_norms.cpu().double(),
+                               res.clipped_norms.double(), rtol=1e-4, atol=1e-9)
+    if per_group:
+        for gname in ("attn", "mlp"):
+            torch.testing.assert_close(aux.group_norms[gname].cpu().double(),
+                                       res.group_norms[gname], rtol=1e-5, atol=0)
+        parts = [aux.clip_scales[k][0].double() * aux.group_norms[g].double()
+                 for k, g in enumerate(sorted(aux.group_norms))]
+        bounds = [R.values[g] for g in sorted(aux.group_norms)]
+        for part, bound in zip(parts, bounds):
+            assert torch.all(part <= bound)
+    else:
+        torch.testing.assert_close(aux.grad_norms.cpu().double(), res.norms, rtol=1e-5, atol=0)
+        assert torch.all(aux.clipped_grad_norms.double() <= R)
