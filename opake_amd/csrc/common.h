@@ -184,6 +184,31 @@ DPC_DEVICE double load_as_f64(const void* base, int64_t idx, int dtype) {
   }
 }
 
+// x as read from another lane by the DPP lane move kCtrl (both 32-bit halves
+// from the same lane); lanes of rows outside kRowMask get 0.0.
+template <int kCtrl, int kRowMask>
+DPC_DEVICE double dpp_f64(double x) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(x);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)b, kCtrl, kRowMask, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), kCtrl, kRowMask, 0xf,
+                                             false);
+  return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+
+// Sum of v over the 64 lanes of a wave, in a fixed order, by DPP lane moves
+// (no LDS round trips): pairs, quads, half rows, rows (every lane of a row
+// then holds the row's sum), then row 1 += row 0 and row 3 += row 2, then
+// rows 2, 3 += row 1.  The total is in lane 63.  Every lane must be active.
+DPC_DEVICE double wave_sum_lane63_f64(double v) {
+  v += dpp_f64<0xB1, 0xf>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_f64<0x4E, 0xf>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_f64<0x141, 0xf>(v);  // row_half_mirror
+  v += dpp_f64<0x140, 0xf>(v);  // row_mirror
+  v += dpp_f64<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_f64<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
 // A float the compiler must take as given: without it, a float64 -> float32
 // -> float16 chain is folded into one float64 -> float16 conversion, which
 // rounds once where torch rounds twice.
@@ -281,10 +306,15 @@ DPC_HOST_DEVICE double dpc_chain_gamma(double n, double u) {
   return g / (1.0 - g) * (1.0 + 0x1.0p-40);
 }
 
-// Upper bound of ||a_s|| + slack from a computed diagonal Gram entry.
-DPC_HOST_DEVICE double dpc_row_bound(double diag, double gamma, double eta, double slack) {
-  const double inv = (1.0 + 0x1.0p-50) / (1.0 - gamma);
+// Upper bound of ||a_s|| + slack from a computed diagonal Gram entry;
+// dpc_row_bound_inv takes the chain's factor dpc_row_inv(gamma) computed once
+// (the same bits).
+DPC_HOST_DEVICE double dpc_row_inv(double gamma) { return (1.0 + 0x1.0p-50) / (1.0 - gamma); }
+DPC_HOST_DEVICE double dpc_row_bound_inv(double diag, double inv, double eta, double slack) {
   return sqrt((fabs(diag) + eta) * inv) * (1.0 + 0x1.0p-50) + slack;
+}
+DPC_HOST_DEVICE double dpc_row_bound(double diag, double gamma, double eta, double slack) {
+  return dpc_row_bound_inv(diag, dpc_row_inv(gamma), eta, slack);
 }
 
 // Per-tile record of a Gram work item (float64, kGramRecWords words):

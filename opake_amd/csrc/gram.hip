@@ -775,6 +775,7 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
   const double gA = dpc_chain_gamma((double)nka * kGK, DPC_GRAM_U_MFMA);
   const double gQ = dpc_chain_gamma((double)nkg * kGK, DPC_GRAM_U_MFMA);
   const double etaA = (double)nka * kGK * 0x1.0p-125, etaQ = (double)nkg * kGK * 0x1.0p-125;
+  const double invA = dpc_row_inv(gA), invQ = dpc_row_inv(gQ);
   if (lane < 3 * kRecStat) red[((lane / kRecStat) * kSplitWaves + w) * kRecStat + lane % kRecStat] = 0.0;
   // All of the partner's blocks are requested before any is used.
   f32x16_t others[kB];
@@ -788,6 +789,18 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
       others[b][4 * r4 + 2] = x.z;
       others[b][4 * r4 + 3] = x.w;
     }
+  // Each lane sums its blocks' words per tile (blocks in order); the lanes
+  // are then summed once per tile the wave touches, and only the words its
+  // blocks can make non-zero (row weights: the diagonal blocks of kDiag4
+  // waves only), so a wave runs at most 7 cross-lane sums instead of 7 per
+  // block.
+  constexpr int kWords = kKind == kDiag4 ? kRecStat : 3;
+  double tv[3][kWords];
+  bool touched[3] = {false, false, false};
+#pragma unroll
+  for (int u = 0; u < 3; ++u)
+#pragma unroll
+    for (int k = 0; k < kWords; ++k) tv[u][k] = 0.0;
 #pragma unroll
   for (int b = 0; b < kB; ++b) {
     const f32x16_t& other = others[b];
@@ -811,8 +824,8 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
       has_diag = has_diag || on_diag;
     }
     if (has_diag) {
-      const double ws = dpc_row_bound(da, gA, etaA, DPC_GRAM_ROW_SLACK_MFMA);
-      const double vs = dpc_row_bound(dg, gQ, etaQ, DPC_GRAM_ROW_SLACK_MFMA);
+      const double ws = dpc_row_bound_inv(da, invA, etaA, DPC_GRAM_ROW_SLACK_MFMA);
+      const double vs = dpc_row_bound_inv(dg, invQ, etaQ, DPC_GRAM_ROW_SLACK_MFMA);
       v[3] = ws * ws * fabs((double)dg);
       v[4] = vs * vs * fabs((double)da);
       v[5] = ws * ws;
@@ -823,11 +836,20 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
     v[1] *= wgt;
     v[2] *= wgt;
 #pragma unroll
-    for (int k = 0; k < kRecStat; ++k)
-      for (int off = 32; off > 0; off >>= 1) v[k] += __shfl_down(v[k], off, 64);
-    if (lane == 0) {
+    for (int u = 0; u < 3; ++u) {
+      const bool mine = tile == u;
+      touched[u] = touched[u] || mine;
 #pragma unroll
-      for (int k = 0; k < kRecStat; ++k) red[(tile * kSplitWaves + w) * kRecStat + k] += v[k];
+      for (int k = 0; k < kWords; ++k) tv[u][k] = mine ? tv[u][k] + v[k] : tv[u][k];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 3; ++u) {
+    if (!touched[u]) continue;  // wave-uniform
+#pragma unroll
+    for (int k = 0; k < kWords; ++k) {
+      const double x = wave_sum_lane63_f64(tv[u][k]);
+      if (lane == 63) red[(u * kSplitWaves + w) * kRecStat + k] = x;
     }
   }
   __syncthreads();
