@@ -392,7 +392,19 @@ int dpc_group_sum_f64(const double* x, int B, int n, int stride, const int32_t* 
  *   n_items a multiple of 8, item l runs on XCD l / (n_items / 8).  slot is
  *   the item's index in segment-major order, and seg_item_start (device int32
  *   [S + 1]) gives each segment's slot range.  max_rows bounds every
- *   segment's rows.  ws: n_items * 12 float64 (one record per item).
+ *   segment's rows.
+ *   set_items (device int32 [n_set_items][4], nullable when n_set_items is 0;
+ *   bf16 operands with din and dout multiples of 8 only) lists segments of 1
+ *   to 320 rows computed by the grouped split kernel instead: two items per
+ *   segment, (problem | op << 8 | set << 9, first row, rows, first slot), op
+ *   0 for A and 1 for G, set in 0 .. n_sets - 1 naming the segment's pair of
+ *   items, first slot = seg_item_start of the segment (the kernel writes all
+ *   of its tile-pair records); the two items of a set must lie in the same
+ *   eighth of the table (one XCD), -1 items are padding.  `items` then lists
+ *   only the other segments' tile pairs.
+ *   n_records = seg_item_start[S] (one 12-float64 record per tile pair of
+ *   every segment); ws: dpc_grouped_gram_workspace_bytes(n_records, n_sets)
+ *   bytes.
  * dpc_segment_plan: the step table of dpc_grouped_clipped_sum.  Segment v
  *   (rows seg_row0[v] .. + seg_len[v] of problem seg_group[v]; segments sorted
  *   by problem) contributes ceil(seg_len / 64) steps (row0, v << 7 | rows)
@@ -409,9 +421,11 @@ int dpc_group_sum_f64(const double* x, int B, int n, int stride, const int32_t* 
  *   rows (device int32 [E]) bounds each problem's operand rows; max_rows
  *   bounds rows.  Segments with scale 0 are never read.
  * -------------------------------------------------------------------------*/
+size_t dpc_grouped_gram_workspace_bytes(int n_records, int n_sets);
 int dpc_grouped_gram_sqnorms(const int64_t* a_ptrs, const int64_t* g_ptrs, const int32_t* dims,
                              int n_problems, int dtype, const int32_t* items, int n_items,
-                             int max_rows, const int32_t* seg_item_start, int S, double* seg_sq,
+                             int max_rows, const int32_t* set_items, int n_set_items, int n_sets,
+                             int n_records, const int32_t* seg_item_start, int S, double* seg_sq,
                              double* seg_err, void* ws, size_t ws_bytes, void* stream);
 int dpc_segment_plan(const int32_t* seg_row0, const int32_t* seg_len, const int32_t* seg_group,
                      const float* seg_scale, int S, int E, int max_steps, int32_t* steps,

@@ -44,7 +44,7 @@ _c_u32 = ctypes.c_uint32
 _c_u64 = ctypes.c_uint64
 _c_i64 = ctypes.c_int64
 
-ABI_VERSION = 205  # dpc_version() of the library these signatures describe
+ABI_VERSION = 206  # dpc_version() of the library these signatures describe
 
 # name -> (restype, argtypes)
 SIGNATURES = {
@@ -164,10 +164,12 @@ SIGNATURES = {
         [_c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_u64,
          _c_void_p],
     ),
+    "dpc_grouped_gram_workspace_bytes": (_c_size_t, [_c_int, _c_int]),
     "dpc_grouped_gram_sqnorms": (
         _c_int,
         [_c_void_p, _c_void_p, ctypes.POINTER(_c_int), _c_int, _c_int, _c_void_p, _c_int, _c_int,
-         _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
+         _c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p,
+         _c_size_t, _c_void_p],
     ),
     "dpc_segment_plan": (
         _c_int,

@@ -473,7 +473,8 @@ def ghost_clip_captured(
         for c0 in range(0, len(members_all), cap):
             members = members_all[c0:c0 + cap]
             layout = ops.SegmentLayout([L.cap.segments for L in members], device,
-                                       gram_weights=[L.A.shape[1] + L.G.shape[1] for L in members])
+                                       gram_weights=[L.A.shape[1] + L.G.shape[1] for L in members],
+                                       gram_dims=[(L.A.shape[1], L.G.shape[1]) for L in members])
             seg_sq, seg_err = ops.grouped_gram_sqnorms(
                 [L.A for L in members], [L.G for L in members], layout, return_error=True)
             # Per-group sums over the layers, in layer order: [B, E] columns

@@ -1112,6 +1112,423 @@ gram_grouped_mfma_bf16_kernel(GramItems work, int nblocks, double* __restrict__ 
                lds, red);
 }
 
+// ---------------------------------------------------------------------------
+// Grouped split mode (bf16 MFMA path, segments of 1 .. 320 rows, the common
+// case of mixture-of-experts layers: a top-2-of-8 expert sees ~T / 4 rows of
+// each example).  The dense split kernel's design over one segment: a work
+// item computes the upper triangle of ONE operand's segment Gram matrix, and
+// the segment's two items (A and G) meet through the workspace as a tile set
+// does.  A segment's rows are cut into 32-row units (rows past its end read
+// as zero): up to 8 units are the dense kernel's diagonal set (36 blocks of
+// 32 x 32 over 8 waves); a ninth and a tenth unit (rows 256 .. 319) add their
+// columns' 9 and 10 blocks through fragment slots 4 and 5 (45 or 55 blocks:
+// 11-12 or 13-14 per SIMD, at most 7 per wave).  Each item stages its
+// segment's rows once per K step (16 or 20 KiB), so the launch reads every
+// operand row from memory exactly once:
+// the grouped Gram is bound by HBM (config 5: 1.375 GB of operands for
+// 1.77e11 FLOP).  Records are the pair kernel's, per 128-row tile pair of the
+// segment (3 tiles at most), so segment_finish_kernel folds both kinds.
+// ---------------------------------------------------------------------------
+constexpr int kGsMaxRows = 320;
+constexpr int kGsMaxBlocks = 7;
+constexpr int kGsWaveBytes = kGsMaxBlocks * 16 * 64 * 4;  // 28 KiB of accumulators
+constexpr int kGsSetBytes = kSplitWaves * kGsWaveBytes;   // 224 KiB per operand
+constexpr int kGsMaxPairs = 6;
+constexpr int kGsSlots = 6;
+
+// Modes by the segment's 32-row units: M = 8 (up to 256 rows), 9 (288), 10
+// (320).  Wave w's fragment slots 0..3 hold units lo, lo + 1, hi, hi + 1
+// (the dense diagonal set's roles); slots 4 and 5 hold units 8 and 9.
+DPC_HOST_DEVICE constexpr int gs_unit(int w, int s) {
+  // lo = {0, 2, 4, 2, 0, 0, 0, 4}[w], hi = {2, 4, 6, 6, 4, 6, 2, 6}[w], as
+  // 3-bit fields (no array: every use folds to a constant).
+  return s >= 4 ? 4 + s : (int)(((s < 2 ? 0x800510u : 0xCB4DA2u) >> (3 * w)) & 7u) + (s & 1);
+}
+// Blocks of wave w, as (row slot, column slot):
+//   base  waves 0..2: (0,2) (0,3) (1,2) (1,3) (0,1); wave 3: the four and
+//         (2,3); waves 4, 5: the four; waves 6, 7: (0,0) (1,1) (2,2) (3,3);
+//   M>=9  unit 8's column: wave 3 (4,4); 4: (0,4) (1,4); 5, 6: (2,4) (3,4);
+//         7: (0,4) (1,4);
+//   M=10  unit 9's column: waves 0..2 (0,5) (1,5); 3: (2,5); 4: (4,5);
+//         5: (3,5); 6: (5,5).
+// Blocks per SIMD (waves s and s + 4): 9 | 11 or 12 | 13 or 14.
+DPC_HOST_DEVICE constexpr int gs_nbase(int w) { return w < 4 ? 5 : 4; }
+DPC_HOST_DEVICE constexpr int gs_n9(int w) { return w < 3 ? 0 : (w == 3 ? 1 : 2); }
+DPC_HOST_DEVICE constexpr int gs_n10(int w) { return w < 3 ? 2 : (w == 7 ? 0 : 1); }
+DPC_HOST_DEVICE constexpr int gs_nblocks(int M, int w) {
+  return gs_nbase(w) + (M >= 9 ? gs_n9(w) : 0) + (M >= 10 ? gs_n10(w) : 0);
+}
+// Packed (row slot << 4 | column slot) of block b.
+DPC_HOST_DEVICE constexpr int gs_block(int M, int w, int b) {
+  if (b < gs_nbase(w)) {
+    if (w >= 6) return b << 4 | b;
+    if (b < 4) return (b >> 1) << 4 | (2 + (b & 1));
+    return w < 3 ? (0 << 4 | 1) : (2 << 4 | 3);
+  }
+  const int j9 = b - gs_nbase(w);
+  if (M >= 9 && j9 < gs_n9(w)) {
+    if (w == 3) return 4 << 4 | 4;
+    return ((w == 5 || w == 6) ? 2 + j9 : j9) << 4 | 4;
+  }
+  const int j = j9 - (M >= 9 ? gs_n9(w) : 0);
+  if (w < 3) return j << 4 | 5;
+  return (w == 3 ? 2 : w == 4 ? 4 : w == 5 ? 3 : 5) << 4 | 5;
+}
+DPC_HOST_DEVICE constexpr int gs_row_slot(int M, int w, int b) { return gs_block(M, w, b) >> 4; }
+DPC_HOST_DEVICE constexpr int gs_col_slot(int M, int w, int b) { return gs_block(M, w, b) & 15; }
+DPC_HOST_DEVICE constexpr bool gs_uses_slot(int M, int w, int s) {
+  for (int b = 0; b < gs_nblocks(M, w); ++b)
+    if (gs_row_slot(M, w, b) == s || gs_col_slot(M, w, b) == s) return true;
+  return false;
+}
+// The 128-row tile pair (p <= q) of block b, as a record index q (q + 1) / 2 + p.
+DPC_HOST_DEVICE constexpr int gs_pair(int M, int w, int b) {
+  const int p = gs_unit(w, gs_row_slot(M, w, b)) >> 2, q = gs_unit(w, gs_col_slot(M, w, b)) >> 2;
+  return q * (q + 1) / 2 + p;
+}
+DPC_HOST_DEVICE constexpr bool gs_has_diag(int M, int w) {
+  for (int b = 0; b < gs_nblocks(M, w); ++b)
+    if (gs_unit(w, gs_row_slot(M, w, b)) == gs_unit(w, gs_col_slot(M, w, b))) return true;
+  return false;
+}
+// The wave's distinct tile pairs in order of first appearance: block b's
+// index among them, their number, and the pair of index l.
+DPC_HOST_DEVICE constexpr int gs_local(int M, int w, int b) {
+  int n = 0;
+  for (int i = 0; i < b; ++i) {
+    bool seen = false;
+    for (int j = 0; j < i; ++j) seen = seen || gs_pair(M, w, j) == gs_pair(M, w, i);
+    if (!seen) {
+      if (gs_pair(M, w, i) == gs_pair(M, w, b)) return n;
+      ++n;
+    }
+  }
+  return n;
+}
+DPC_HOST_DEVICE constexpr int gs_nlocal(int M, int w) {
+  int n = 0;
+  for (int b = 0; b < gs_nblocks(M, w); ++b)
+    n = gs_local(M, w, b) + 1 > n ? gs_local(M, w, b) + 1 : n;
+  return n;
+}
+DPC_HOST_DEVICE constexpr int gs_local_pair(int M, int w, int l) {
+  for (int b = 0; b < gs_nblocks(M, w); ++b)
+    if (gs_local(M, w, b) == l) return gs_pair(M, w, b);
+  return 0;
+}
+
+template <int W, int M>
+__device__ __forceinline__ void gsplit_item(const uint16_t* X, int n, int d, int din, int dout,
+                                            int op, int set, double* rec, int32_t* tickets,
+                                            float* __restrict__ xbuf, uint8_t* lds, double* red,
+                                            int* ticket_lds, int my_xcc) {
+  constexpr int kB = gs_nblocks(M, W);
+  // 128-row tiles this wave feeds: tile 2 holds units 8 (rows 0..31) and 9.
+  constexpr int kDma = W < (M - 8) * 2 ? 3 : 2;
+  constexpr int kWords = gs_has_diag(M, W) ? kRecStat : 3;
+  constexpr int kStage = 3 * kGTileBytes;
+  const int tid = threadIdx.x, lane = tid & 63;
+
+  // Staging by DMA: wave W moves rows 16 W .. 16 W + 15 of each 128-row tile
+  // it feeds (one 1 KiB buffer_load ... lds each); rows at or past the
+  // segment's end are past the buffer range and read as zero.
+  const u32x4_t words = rsrc_words(X, (uint32_t)(n * d * 2));
+  const int lchunk = (lane & 3) ^ ((lane >> 4) & 3);
+  const int voff0 = (16 * W + (lane >> 2)) * d * 2 + lchunk * 16;
+  auto dma = [&](uint8_t* stage, int step) __attribute__((always_inline)) {
+    const int bad = step * kGK + lchunk * 8 < d ? 0 : kGramOutOfRange;
+    const uint32_t base = lds_addr(stage) + W * 1024;
+#pragma unroll
+    for (int j = 0; j < kDma; ++j)
+      dma16(words, base + j * kGTileBytes, (voff0 + j * kGramTile * d * 2) | bad, step * kGK * 2);
+  };
+  int foff[kGsSlots];
+#pragma unroll
+  for (int s = 0; s < kGsSlots; ++s) {
+    const int u = gs_unit(W, s);
+    foff[s] = (u >> 2) * kGTileBytes + gtile_off((u & 3) * 32 + (lane & 31), lane >> 5);
+  }
+  struct Frags {
+    bf16x8_t v[kGsSlots];
+  };
+  auto read = [&](const uint8_t* stage, int kk, Frags& fr) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < kGsSlots; ++s)
+      if (gs_uses_slot(M, W, s))
+        fr.v[s] = *reinterpret_cast<const bf16x8_t*>(stage + (foff[s] ^ (32 * kk)));
+  };
+  f32x16_t acc[kB];
+#pragma unroll
+  for (int b = 0; b < kB; ++b) acc[b] = f32x16_t{};
+  auto mma = [&](const Frags& fr) __attribute__((always_inline)) {
+#pragma unroll
+    for (int b = 0; b < kB; ++b)
+      acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr.v[gs_row_slot(M, W, b)],
+                                                       fr.v[gs_col_slot(M, W, b)], acc[b], 0, 0, 0);
+  };
+
+  // The dense split kernel's K loop: four LDS stages, the DMAs of step s + 4
+  // into step s's stage right after the barrier of step s, which waits for
+  // step s + 1's; sub-step 1's fragments read before sub-step 0's MFMAs and
+  // the next step's sub-step 0 before this step's second MFMA group.
+  const int nk = ceil_div(d, kGK);
+  uint8_t* const ring[4] = {lds, lds + kStage, lds + 2 * kStage, lds + 3 * kStage};
+  dma(ring[0], 0);
+  dma(ring[1], 1);
+  dma(ring[2], 2);
+  dma(ring[3], 3);
+  DPC_WAIT_VMCNT(3 * kDma);
+  __syncthreads();
+  Frags fx, fy;
+  read(ring[0], 0, fx);
+  auto step = [&](auto P, int s) __attribute__((always_inline)) {
+    constexpr int p = decltype(P)::value;
+    uint8_t* cur = ring[p];
+    const uint8_t* nxt = ring[(p + 1) % 4];
+    read(cur, 1, fy);
+    mma(fx);
+    __builtin_amdgcn_sched_barrier(0);
+    DPC_WAIT_VMCNT(2 * kDma);  // step s + 1 has landed
+    __syncthreads();
+    dma(cur, s + 4);
+    read(nxt, 0, fx);
+    mma(fy);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int s = 0;
+  for (; s + 4 <= nk; s += 4) {
+    step(StageIdx<0>(), s);
+    step(StageIdx<1>(), s + 1);
+    step(StageIdx<2>(), s + 2);
+    step(StageIdx<3>(), s + 3);
+  }
+  if (s < nk) step(StageIdx<0>(), s);
+  if (s + 1 < nk) step(StageIdx<1>(), s + 1);
+  if (s + 2 < nk) step(StageIdx<2>(), s + 2);
+  DPC_WAIT_VMCNT(0);
+
+  // Meet the segment's other item (see split_item): both publish, the one
+  // with the second ticket reads its partner's accumulators and writes the
+  // segment's records.
+  float4* base = reinterpret_cast<float4*>(xbuf) + (size_t)set * (2 * kGsSetBytes / 16);
+  float4* mine = base + (size_t)op * (kGsSetBytes / 16) + (size_t)W * (kGsWaveBytes / 16);
+  const float4* theirs =
+      base + (size_t)(op ^ 1) * (kGsSetBytes / 16) + (size_t)W * (kGsWaveBytes / 16);
+#pragma unroll
+  for (int b = 0; b < kB; ++b)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4)
+      mine[(b * 4 + r4) * 64 + lane] =
+          make_float4(acc[b][4 * r4], acc[b][4 * r4 + 1], acc[b][4 * r4 + 2], acc[b][4 * r4 + 3]);
+  DPC_WAIT_VMCNT(0);
+  __syncthreads();
+  if (tid == 0) {
+    const int partner = __hip_atomic_load(&tickets[3 * set + 1 + (op ^ 1)], __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+    const bool same = partner == my_xcc + 1;
+    if (!same) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    ticket_lds[0] = __hip_atomic_fetch_add(&tickets[3 * set], 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    ticket_lds[1] = same;
+  }
+  __syncthreads();
+  if (ticket_lds[0] == 0) return;
+  if (ticket_lds[1])
+    asm volatile("buffer_inv sc0" ::: "memory");  // drop stale lines from this CU's L1
+  else
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+
+  const int nka = ceil_div(din, kGK), nkg = ceil_div(dout, kGK);
+  const double gA = dpc_chain_gamma((double)nka * kGK, DPC_GRAM_U_MFMA);
+  const double gQ = dpc_chain_gamma((double)nkg * kGK, DPC_GRAM_U_MFMA);
+  // The statistics are taken with x = this item's entries and y = the
+  // partner's, and the words of the two roles are swapped at the end when
+  // this item holds G (op 1): the A role's row weights come from A's chain.
+  const int kx = op == 0 ? nka : nkg, ky = op == 0 ? nkg : nka;
+  const double etaX = (double)kx * kGK * 0x1.0p-125, etaY = (double)ky * kGK * 0x1.0p-125;
+  const double invX = dpc_row_inv(op == 0 ? gA : gQ), invY = dpc_row_inv(op == 0 ? gQ : gA);
+  if (lane < kGsMaxPairs * kRecStat)
+    red[((lane / kRecStat) * kSplitWaves + W) * kRecStat + lane % kRecStat] = 0.0;
+  // Both items' blocks are read back from the exchange area, one block
+  // ahead of their use: the accumulators are dead after their publication,
+  // and six blocks of both operands would not fit the registers at once.
+  auto load_block = [&](const float4* src, int b) __attribute__((always_inline)) {
+    f32x16_t o;
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const float4 x = src[(b * 4 + r4) * 64 + lane];
+      o[4 * r4] = x.x;
+      o[4 * r4 + 1] = x.y;
+      o[4 * r4 + 2] = x.z;
+      o[4 * r4 + 3] = x.w;
+    }
+    return o;
+  };
+  // Lane-local sums per tile pair (blocks in order), then one cross-lane sum
+  // per pair the wave touches and word its blocks can make non-zero.
+  // Words: 0 sum x y, 1 / 2 off-diagonal x^2 / y^2, 3 wx^2 |y_ss|,
+  // 4 wy^2 |x_ss|, 5 wx^2, 6 wy^2.
+  constexpr int kLocal = gs_nlocal(M, W);
+  double tv[kLocal][kWords];
+#pragma unroll
+  for (int u = 0; u < kLocal; ++u)
+#pragma unroll
+    for (int k = 0; k < kWords; ++k) tv[u][k] = 0.0;
+  // A rolled loop over the blocks: unrolled, the compiler hoists the reads
+  // and fp64 conversions of all blocks and runs out of registers.
+  f32x16_t next_x = load_block(mine, 0), next_y = load_block(theirs, 0);
+#pragma unroll 1
+  for (int b = 0; b < kB; ++b) {
+    const f32x16_t x16 = next_x, y16 = next_y;
+    if (b + 1 < kB) {
+      next_x = load_block(mine, b + 1);
+      next_y = load_block(theirs, b + 1);
+    }
+    const int ru = gs_unit(W, gs_row_slot(M, W, b)), cu = gs_unit(W, gs_col_slot(M, W, b));
+    const bool dblk = ru == cu;
+    // Weight 2 (exact) for a block above a diagonal tile's diagonal: it
+    // stands for its mirror as well.
+    const double wgt = ((ru >> 2) == (cu >> 2) && ru < cu) ? 2.0 : 1.0;
+    double v[kRecStat] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+    float dx = 0.0f, dy = 0.0f;
+    bool has_diag = false;
+    // Four entries at a time (the scheduler would otherwise convert all 32
+    // of the block to fp64 first and run out of registers).
+#pragma unroll
+    for (int r0 = 0; r0 < 16; r0 += 4) {
+#pragma unroll
+      for (int r = r0; r < r0 + 4; ++r) {
+        const double x = x16[r], y = y16[r];
+        v[0] += x * y;
+        const bool on_diag = dblk && ((r >> 2) * 8 + 4 * (lane >> 5) + (r & 3)) == (lane & 31);
+        v[1] += on_diag ? 0.0 : x * x;
+        v[2] += on_diag ? 0.0 : y * y;
+        dx = on_diag ? x16[r] : dx;
+        dy = on_diag ? y16[r] : dy;
+        has_diag = has_diag || on_diag;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (kWords == kRecStat && has_diag) {
+      const double wx = dpc_row_bound_inv(dx, invX, etaX, DPC_GRAM_ROW_SLACK_MFMA);
+      const double wy = dpc_row_bound_inv(dy, invY, etaY, DPC_GRAM_ROW_SLACK_MFMA);
+      v[3] = wx * wx * fabs((double)dy);
+      v[4] = wy * wy * fabs((double)dx);
+      v[5] = wx * wx;
+      v[6] = wy * wy;
+    }
+    v[0] *= wgt;
+    v[1] *= wgt;
+    v[2] *= wgt;
+#pragma unroll
+    for (int u = 0; u < kLocal; ++u) {
+      const bool mine = gs_local(M, W, b) == u;
+#pragma unroll
+      for (int k = 0; k < kWords; ++k) tv[u][k] = mine ? tv[u][k] + v[k] : tv[u][k];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kLocal; ++u) {
+    const int pair = gs_local_pair(M, W, u);
+    if (op == 1) {  // this item holds G: y is A
+      double t = tv[u][1];
+      tv[u][1] = tv[u][2];
+      tv[u][2] = t;
+      if (kWords == kRecStat) {
+        t = tv[u][3];
+        tv[u][3] = tv[u][4];
+        tv[u][4] = t;
+        t = tv[u][5];
+        tv[u][5] = tv[u][6];
+        tv[u][6] = t;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kWords; ++k) {
+      const double x = wave_sum_lane63_f64(tv[u][k]);
+      if (lane == 63) red[(pair * kSplitWaves + W) * kRecStat + k] = x;
+    }
+  }
+  __syncthreads();
+
+  // Records of the segment's tile pairs (nt = 1..3 tiles of 128 rows).
+  const int nt = ceil_div(n, kGramTile), npairs = nt * (nt + 1) / 2;
+  if (tid < npairs * DPC_GRAM_REC_WORDS) {
+    const int u = tid / DPC_GRAM_REC_WORDS, k = tid % DPC_GRAM_REC_WORDS;
+    double val;
+    if (k < kRecStat) {
+      val = 0.0;
+      for (int i = 0; i < kSplitWaves; ++i) val += red[(u * kSplitWaves + i) * kRecStat + k];
+      // The off-diagonal tile pairs (0, 1), (0, 2), (1, 2) count twice (exact).
+      const bool offdiag = u == 1 || u == 3 || u == 4;
+      if (k == 0 && offdiag) val *= 2.0;
+    } else {
+      val = k == 7 ? gA : k == 8 ? gQ : k == 9 ? (double)n : 0.0;
+    }
+    rec[(size_t)u * DPC_GRAM_REC_WORDS + k] = val;
+  }
+}
+
+// Grouped split launch: item l is (problem | op << 8 | set << 9, first row,
+// rows, record slot) -- operand op of the rows-long segment starting at
+// `first row` of problem `problem`, whose records start at `record slot`; the
+// segment's two items share tickets[3 set ..] and their exchange area.  Items
+// of a segment sit on one XCD (the host's placement), padding items are -1.
+__global__ void __launch_bounds__(512, 1)
+gram_gsplit_bf16_kernel(GramItems work, int nblocks, double* __restrict__ records,
+                        int32_t* __restrict__ tickets, float* __restrict__ xbuf) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[4 * 3 * kGTileBytes];
+  __shared__ double red[kGsMaxPairs * kSplitWaves * kRecStat];
+  __shared__ int ticket_lds[2];
+  const int l = xcd_logical_block(gridDim.x, nblocks);
+  if (l < 0) return;  // padding workgroup: exits before any barrier
+  const int32_t* it = work.items + 4 * (size_t)l;
+  const int w0 = __builtin_amdgcn_readfirstlane(it[0]);
+  if (w0 < 0) return;  // empty item: exits before any barrier
+  const int problem = w0 & 0xff, op = (w0 >> 8) & 1, set = w0 >> 9;
+  const int row0 = __builtin_amdgcn_readfirstlane(it[1]);
+  const int n = __builtin_amdgcn_readfirstlane(it[2]);
+  const int slot = __builtin_amdgcn_readfirstlane(it[3]);
+  const int din = work.din[problem], dout = work.dout[problem];
+  const int d = op == 0 ? din : dout;
+  const uint16_t* X =
+      reinterpret_cast<const uint16_t*>(op == 0 ? work.a_ptrs[problem] : work.g_ptrs[problem]) +
+      (size_t)row0 * d;
+  double* rec = records + (size_t)slot * DPC_GRAM_REC_WORDS;
+  int xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  xcc &= 0xf;
+  if (threadIdx.x == 0)
+    __hip_atomic_store(&tickets[3 * set + 1 + op], xcc + 1, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int units = ceil_div(n, 32);
+#define DPC_GS_CASE(Wc)                                                                        \
+  case Wc:                                                                                     \
+    if (units <= 8)                                                                            \
+      gsplit_item<Wc, 8>(X, n, d, din, dout, op, set, rec, tickets, xbuf, lds, red, ticket_lds, \
+                         xcc);                                                                 \
+    else if (units == 9)                                                                       \
+      gsplit_item<Wc, 9>(X, n, d, din, dout, op, set, rec, tickets, xbuf, lds, red, ticket_lds, \
+                         xcc);                                                                 \
+    else                                                                                       \
+      gsplit_item<Wc, 10>(X, n, d, din, dout, op, set, rec, tickets, xbuf, lds, red,           \
+                          ticket_lds, xcc);                                                    \
+    break;
+  switch (w) {
+    DPC_GS_CASE(0)
+    DPC_GS_CASE(1)
+    DPC_GS_CASE(2)
+    DPC_GS_CASE(3)
+    DPC_GS_CASE(4)
+    DPC_GS_CASE(5)
+    DPC_GS_CASE(6)
+    default:
+      DPC_GS_CASE(7)
+  }
+#undef DPC_GS_CASE
+}
+
 // Generic path (float32 inputs, or bf16 with d % 8 != 0): 64 x 64 tiles,
 // fp64 FMA with a 4 x 4 register block per thread (products of fp32 values
 // are exact in fp64, so the Gram entries carry only fp64 summation error).
@@ -1495,19 +1912,39 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
   return DPC_OK;
 }
 
+// Workspace of dpc_grouped_gram_sqnorms: the records, the split kernel's
+// tickets (3 per set) and its accumulator exchange (two operands per set).
+static size_t gs_ticket_offset(int n_records) {
+  return ((size_t)n_records * DPC_GRAM_REC_WORDS * sizeof(double) + 255) & ~(size_t)255;
+}
+static size_t gs_xbuf_offset(int n_records, int n_sets) {
+  return (gs_ticket_offset(n_records) + (size_t)n_sets * 3 * sizeof(int32_t) + 255) &
+         ~(size_t)255;
+}
+
+extern "C" size_t dpc_grouped_gram_workspace_bytes(int n_records, int n_sets) {
+  if (n_records < 0 || n_sets < 0) return 0;
+  return gs_xbuf_offset(n_records, n_sets) + (size_t)n_sets * 2 * kGsSetBytes;
+}
+
 extern "C" int dpc_grouped_gram_sqnorms(const int64_t* a_ptrs, const int64_t* g_ptrs,
                                         const int32_t* dims, int n_problems, int dtype,
                                         const int32_t* items, int n_items, int max_rows,
-                                        const int32_t* seg_item_start, int S, double* seg_sq,
+                                        const int32_t* set_items, int n_set_items, int n_sets,
+                                        int n_records, const int32_t* seg_item_start, int S,
+                                        double* seg_sq,
                                         double* seg_err, void* ws, size_t ws_bytes,
                                         void* stream) {
-  if (n_problems < 1 || !dims || n_items < 0 || S < 0 || max_rows < 0) return DPC_EINVAL;
+  if (n_problems < 1 || !dims || n_items < 0 || S < 0 || max_rows < 0 || n_set_items < 0 ||
+      n_sets < 0 || n_records < 0)
+    return DPC_EINVAL;
   if (dtype != DPC_F32 && dtype != DPC_BF16) return DPC_EINVAL;
   if (n_problems > kMaxGramProblems) return DPC_ENOTSUP;
   if (S == 0) return DPC_OK;
-  if (!seg_item_start || !seg_sq || (n_items > 0 && (!a_ptrs || !g_ptrs || !items || !ws)))
+  if (!seg_item_start || !seg_sq || (n_items > 0 && (!a_ptrs || !g_ptrs || !items || !ws)) ||
+      (n_set_items > 0 && (!a_ptrs || !g_ptrs || !set_items || !ws || n_sets < 1)) ||
+      (n_sets >= (1 << 22)))
     return DPC_EINVAL;
-  if (ws_bytes < (size_t)n_items * DPC_GRAM_REC_WORDS * sizeof(double)) return DPC_ENOSPC;
   GramItems work;
   work.items = items;
   work.a_ptrs = a_ptrs;
@@ -1522,8 +1959,28 @@ extern "C" int dpc_grouped_gram_sqnorms(const int64_t* a_ptrs, const int64_t* g_
     aligned = aligned && work.din[p] % 8 == 0 && work.dout[p] % 8 == 0;
     dmax = max(dmax, max(work.din[p], work.dout[p]));
   }
+  // The split kernel takes bf16 segments of at most kGsMaxRows rows, whose
+  // byte range fits its 32-bit buffer offsets.
+  if (n_set_items > 0 &&
+      (dtype != DPC_BF16 || !aligned || (size_t)kGsMaxRows * (size_t)dmax * 2 >= ((size_t)1 << 31)))
+    return DPC_EINVAL;
   hipStream_t s = (hipStream_t)stream;
   double* records = (double*)ws;
+  if (n_set_items > 0) {
+    if (ws_bytes < dpc_grouped_gram_workspace_bytes(n_records, n_sets)) return DPC_ENOSPC;
+    int32_t* tickets = (int32_t*)((uint8_t*)ws + gs_ticket_offset(n_records));
+    float* xbuf = (float*)((uint8_t*)ws + gs_xbuf_offset(n_records, n_sets));
+    hipLaunchKernelGGL(fill_zero_i32_kernel, dim3(ceil_div(3 * n_sets, kGramThreads)),
+                       dim3(kGramThreads), 0, s, tickets, 3 * n_sets);
+    GramItems sw = work;
+    sw.items = set_items;
+    const int padded = ceil_div(n_set_items, kXcds) * kXcds;
+    hipLaunchKernelGGL(gram_gsplit_bf16_kernel, dim3(padded), dim3(512), 0, s, sw, n_set_items,
+                       records, tickets, xbuf);
+    DPC_HIP_CHECK(hipGetLastError());
+  } else if (ws_bytes < (size_t)n_records * DPC_GRAM_REC_WORDS * sizeof(double)) {
+    return DPC_ENOSPC;
+  }
   if (n_items > 0) {
     const bool fits = ((size_t)max_rows + kGramTile) * (size_t)dmax * 2 < ((size_t)1 << 31);
     if (dtype == DPC_BF16 && aligned && fits) {

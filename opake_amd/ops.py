@@ -493,12 +493,59 @@ class SegmentLayout:
     per problem, e.g. K = batch size).  ``gram_weights[e]`` (default 1) is the
     relative cost of a Gram tile pair of problem e (its din + dout): the Gram
     work items are issued most expensive first, so that a launch over problems
-    of different widths ends evenly.  The device tables (segment first rows and
+    of different widths ends evenly.  ``gram_dims[e]`` (optional) is problem
+    e's (din, dout), which prices the grouped split kernel's items (one per
+    operand) more exactly.  The device tables (segment first rows and
     lengths, Gram work items) are copied in one transfer.
+
+    Two Gram schedules are kept: tile-pair items for every segment (any
+    dtype), and for the bf16 MFMA path the split kernel's items -- two per
+    segment of 1 .. 320 rows (A and G) -- with tile-pair items for the
+    longer segments only.
     """
 
     MAX_GRAM_PROBLEMS = 64
     XCDS = 8
+    SPLIT_MAX_ROWS = 320  # segments the grouped split kernel takes (10 units of 32 rows)
+
+    @classmethod
+    def _split_schedule(cls, seg, seg_len, seg_row0, seg_group, seg_first, k_op):
+        """Items of the grouped split kernel for segments `seg`: per segment
+        (a "set") the A item and the G item, (problem | op << 8 | set << 9,
+        first row, rows, first record slot).  Sets go whole to the 8 XCD bins,
+        most expensive first in snake order (both items of a set on one XCD,
+        where they meet through its L2); within a bin the items run most
+        expensive first.  Returns the padded [8 * per, 4] table."""
+        import numpy as np
+
+        n_sets = len(seg)
+        if n_sets == 0:
+            return np.zeros((0, 4), dtype=np.int64)
+        rows = seg_len[seg]
+        blocks = np.where(rows > 288, 55, np.where(rows > 256, 45, 36))  # 32 x 32 blocks
+        prob = seg_group[seg]
+        cost = np.stack([k_op[prob, 0] * blocks, k_op[prob, 1] * blocks], axis=1)
+        order = np.argsort(-cost.sum(axis=1), kind="stable")
+        r = np.arange(n_sets)
+        lap, pos = r // cls.XCDS, r % cls.XCDS
+        bin_of = np.empty(n_sets, dtype=np.int64)
+        bin_of[order] = np.where(lap % 2 == 0, pos, cls.XCDS - 1 - pos)
+        per = 2 * int(np.bincount(bin_of, minlength=cls.XCDS).max())
+        words = np.stack([
+            np.stack([prob | (op << 8) | (np.arange(n_sets) << 9), seg_row0[seg], rows,
+                      seg_first[seg]], axis=1)
+            for op in (0, 1)], axis=1)  # [n_sets, 2, 4]
+        out = np.zeros((cls.XCDS * per, 4), dtype=np.int64)
+        out[:, 0] = -1
+        for x in range(cls.XCDS):
+            sets = np.nonzero(bin_of == x)[0]
+            if not len(sets):
+                continue
+            it = words[sets].reshape(-1, 4)
+            c = cost[sets].reshape(-1)
+            it = it[np.argsort(-c, kind="stable")]
+            out[x * per:x * per + len(it)] = it
+        return out
 
     @classmethod
     def _xcd_schedule(cls, items, cost, seg_of_item, item_start, xcd_cus=32):
@@ -545,7 +592,7 @@ class SegmentLayout:
             out[x * per:x * per + n] = items[idx]
         return out
 
-    def __init__(self, lengths, device, gram_weights=None):
+    def __init__(self, lengths, device, gram_weights=None, gram_dims=None):
         import numpy as np
 
         lens = np.asarray(lengths, dtype=np.int64)
@@ -585,16 +632,40 @@ class SegmentLayout:
         slot = np.arange(self.n_items)
         items = np.stack([(group[seg_of_item] << 16) | pair, row0[seg_of_item], seg_len, slot],
                          axis=1)
-        items = self._xcd_schedule(items, cost, seg_of_item, item_start, _xcd_cus(device))
+        xcd_cus = _xcd_cus(device)
+        all_items = self._xcd_schedule(items, cost, seg_of_item, item_start, xcd_cus)
+        # The split kernel's schedule: segments of 1 .. SPLIT_MAX_ROWS rows as
+        # sets, tile pairs for the longer ones.
+        short = (flat >= 1) & (flat <= self.SPLIT_MAX_ROWS)
+        if gram_dims is not None:
+            k_op = np.asarray(gram_dims, dtype=np.int64).reshape(self.E, 2)
+        else:
+            k_op = np.repeat(weights[:, None] / 2.0, 2, axis=1)
+        set_items = self._split_schedule(np.nonzero(short)[0], flat, row0, group,
+                                         item_start[:-1], k_op)
+        long_seg = ~short[seg_of_item]
+        if long_seg.any():
+            sub_counts = np.where(short, 0, npairs)
+            sub_start = np.concatenate([[0], np.cumsum(sub_counts)])
+            long_items = self._xcd_schedule(items[long_seg], cost[long_seg],
+                                            seg_of_item[long_seg], sub_start, xcd_cus)
+        else:
+            long_items = np.zeros((0, 4), dtype=np.int64)
+        self.n_sets = int(short.sum())
         self.max_steps = int(((flat + _STEP_ROWS - 1) // _STEP_ROWS).sum())
         # One int32 buffer: row0 [S] | len [S] | group [S] | rows [E] |
-        # item_start [S + 1] | items [n_items * 4].
-        parts = [row0, flat, group, self.rows, item_start, items.reshape(-1)]
+        # item_start [S + 1] | tile-pair items of every segment | tile-pair
+        # items of the long segments | split items.
+        parts = [row0, flat, group, self.rows, item_start, all_items.reshape(-1),
+                 long_items.reshape(-1), set_items.reshape(-1)]
         buf = device_table(np.concatenate(parts), np.int32, device)
         offs = np.cumsum([0] + [len(p) for p in parts])
         (self.seg_row0, self.seg_len, self.seg_group, self.rows_dev, self.item_start,
-         self.items) = [buf[offs[i]:offs[i + 1]] for i in range(len(parts))]
-        self.n_launch_items = len(items)
+         self.items, self.long_items, self.set_items) = [buf[offs[i]:offs[i + 1]]
+                                                         for i in range(len(parts))]
+        self.n_launch_items = len(all_items)
+        self.n_long_items = len(long_items)
+        self.n_set_items = len(set_items)
         self._buf = buf
         self.device = torch.device(device)
 
@@ -639,14 +710,27 @@ def grouped_gram_sqnorms(A_list, G_list, layout: SegmentLayout, *, return_error:
     seg_sq = torch.empty((layout.E, layout.K), dtype=torch.float64, device=dev)
     seg_err = (torch.empty((layout.E, layout.K), dtype=torch.float64, device=dev)
                if return_error else None)
-    ws = torch.empty(max(layout.n_launch_items, 1) * _GRAM_REC_WORDS, dtype=torch.float64,
-                     device=dev)
+    # The grouped split kernel (bf16, widths that are multiples of 8) takes the
+    # segments of up to SPLIT_MAX_ROWS rows; the tile-pair kernel the rest.
+    widths = [w for A, G in zip(A_list, G_list) for w in (A.shape[1], G.shape[1])]
+    split = (dtype == torch.bfloat16 and layout.n_set_items > 0
+             and all(w % 8 == 0 for w in widths)
+             and SegmentLayout.SPLIT_MAX_ROWS * max(widths) * 2 < (1 << 31))
+    if split:
+        items, n_items = layout.long_items, layout.n_long_items
+        sets, n_set_items, n_sets = layout.set_items, layout.n_set_items, layout.n_sets
+    else:
+        items, n_items = layout.items, layout.n_launch_items
+        sets, n_set_items, n_sets = None, 0, 0
+    n_records = layout.n_items
+    nbytes = nat.load().dpc_grouped_gram_workspace_bytes(n_records, n_sets)
+    ws = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=dev)
     a_ptrs, g_ptrs = _ptr_table(A_list, dev), _ptr_table(G_list, dev)
     nat.call(
         "dpc_grouped_gram_sqnorms", nat.ptr(a_ptrs), nat.ptr(g_ptrs), dims, layout.E,
-        nat.dtype_code(dtype), nat.ptr(layout.items), layout.n_launch_items, layout.max_rows,
-        nat.ptr(layout.item_start), layout.S, nat.ptr(seg_sq), nat.ptr(seg_err), nat.ptr(ws),
-        ws.numel() * 8, nat.stream_handle(dev),
+        nat.dtype_code(dtype), nat.ptr(items), n_items, layout.max_rows, nat.ptr(sets),
+        n_set_items, n_sets, n_records, nat.ptr(layout.item_start), layout.S, nat.ptr(seg_sq),
+        nat.ptr(seg_err), nat.ptr(ws), ws.numel(), nat.stream_handle(dev),
     )
     return (seg_sq, seg_err) if return_error else seg_sq
 

@@ -34,8 +34,12 @@ def test_version_and_size_queries():
     if not _native.LIB_PATH.exists():
         pytest.skip("native library not built")
     lib = _native.load()
-    assert lib.dpc_version() == _native.ABI_VERSION == 205
+    assert lib.dpc_version() == _native.ABI_VERSION == 206
     assert lib.dpc_clip_plan_bytes(32) == 16 + 32 * 4
+    # Grouped Gram workspace: the records, then the split kernel's tickets and
+    # accumulator exchange (2 x 224 KiB per set), each 256-byte aligned.
+    assert lib.dpc_grouped_gram_workspace_bytes(10, 0) == 1024
+    assert lib.dpc_grouped_gram_workspace_bytes(10, 3) == 1024 + 256 + 3 * 2 * 229376
     assert lib.dpc_gram_workspace_bytes(0, 5) == 0
     assert lib.dpc_gram_workspace_bytes(2, 128) > 0
 

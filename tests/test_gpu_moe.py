@@ -93,6 +93,67 @@ def test_grouped_gram_mixed_shapes_cost_ordered(dev, dtype, shapes):
             assert abs(got[e, k].item() - want[k].item()) <= tol * want[k].item(), (e, k)
 
 
+# Segments for the grouped split kernel (1 .. 320 rows: up to 8 units of 32
+# rows, a ninth (257 .. 288) and a tenth (289 .. 320)) beside longer ones
+# that take the tile-pair kernel in the same call.
+SPLIT_LENGTHS = [[1, 31, 32, 33, 127, 128, 129, 200, 255, 256],
+                 [257, 270, 287, 288, 289, 0, 64, 96, 160, 321],
+                 [250, 260, 280, 300, 8, 16, 319, 320, 190, 240]]
+
+
+def _all_pairs_sqnorms(dev, As, Gs, layout):
+    """The same call with every segment on the tile-pair kernel."""
+    import ctypes
+
+    dims = (ctypes.c_int * (2 * layout.E))(
+        *[v for A, G in zip(As, Gs) for v in (A.shape[1], G.shape[1])])
+    sq = torch.empty((layout.E, layout.K), dtype=torch.float64, device=dev)
+    err = torch.empty_like(sq)
+    nbytes = nat.load().dpc_grouped_gram_workspace_bytes(layout.n_items, 0)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    a_ptrs = torch.tensor([a.data_ptr() for a in As], dtype=torch.int64, device=dev)
+    g_ptrs = torch.tensor([g.data_ptr() for g in Gs], dtype=torch.int64, device=dev)
+    nat.call("dpc_grouped_gram_sqnorms", nat.ptr(a_ptrs), nat.ptr(g_ptrs), dims, layout.E,
+             nat.DPC_BF16, nat.ptr(layout.items), layout.n_launch_items, layout.max_rows,
+             nat.ptr(None), 0, 0, layout.n_items, nat.ptr(layout.item_start), layout.S,
+             nat.ptr(sq), nat.ptr(err), nat.ptr(ws), ws.numel(), nat.stream_handle(dev))
+    return sq, err
+
+
+@pytest.mark.parametrize("dims", [[(64, 96), (128, 40), (32, 256)],
+                                  [(256, 256), (96, 160), (512, 64)]])
+def test_grouped_split_kernel_matches_exact(dev, dims):
+    """The grouped split kernel's segment norms: within their own error bound
+    of the exact fp64 ||G_v^T A_v||^2 (so the clip factor is DP-sound), and
+    within 2e-2 of it; the tile-pair kernel on the same segments agrees."""
+    gen = torch.Generator().manual_seed(sum(a for a, _ in dims))
+    As, Gs = [], []
+    for lens, (din, dout) in zip(SPLIT_LENGTHS, dims):
+        rows = sum(lens)
+        scale = torch.exp(torch.randn(rows, 1, generator=gen))
+        As.append(torch.randn(rows, din, generator=gen).to(torch.bfloat16))
+        Gs.append((torch.randn(rows, dout, generator=gen) * 0.1 * scale).to(torch.bfloat16))
+    layout = ops.SegmentLayout(SPLIT_LENGTHS, dev, gram_dims=dims)
+    assert layout.n_set_items > 0 and layout.n_long_items > 0
+    Ad, Gd = [a.to(dev) for a in As], [g.to(dev) for g in Gs]
+    for rep in range(2):  # the tickets are cleared for every call
+        sq, err = ops.grouped_gram_sqnorms(Ad, Gd, layout, return_error=True)
+        sq, err = sq.cpu(), err.cpu()
+        for e, lens in enumerate(SPLIT_LENGTHS):
+            exact = (ghost_oracle.segment_grads(As[e], Gs[e], lens, dtype=torch.float64) ** 2
+                     ).sum(dim=(1, 2))
+            for k, n in enumerate(lens):
+                if n == 0:
+                    assert sq[e, k].item() == 0.0 and err[e, k].item() == 0.0
+                    continue
+                d = abs(sq[e, k].item() - exact[k].item())
+                assert d <= err[e, k].item(), (rep, e, k, n, d, err[e, k].item())
+                assert d <= 2e-2 * exact[k].item(), (rep, e, k, n)
+                assert err[e, k].item() <= 1e-2 * exact[k].item(), (rep, e, k, n)
+    psq, perr = _all_pairs_sqnorms(dev, Ad, Gd, layout)
+    torch.testing.assert_close(sq, psq.cpu(), rtol=1e-5, atol=0)
+
+
 @pytest.mark.parametrize("dtype,din,dout", [(torch.float32, 40, 24), (torch.bfloat16, 264, 136),
                                             (torch.bfloat16, 36, 20)])
 @pytest.mark.parametrize("out_dtype", [None, torch.float32])
