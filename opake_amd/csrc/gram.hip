@@ -1226,27 +1226,50 @@ __device__ __forceinline__ void gsplit_item(const uint16_t* X, int n, int d, int
   // 128-row tiles this wave feeds: tile 2 holds units 8 (rows 0..31) and 9.
   constexpr int kDma = W < (M - 8) * 2 ? 3 : 2;
   constexpr int kWords = gs_has_diag(M, W) ? kRecStat : 3;
-  constexpr int kStage = 3 * kGTileBytes;
   const int tid = threadIdx.x, lane = tid & 63;
 
-  // Staging by DMA: wave W moves rows 16 W .. 16 W + 15 of each 128-row tile
-  // it feeds (one 1 KiB buffer_load ... lds each); rows at or past the
-  // segment's end are past the buffer range and read as zero.
+  // 64-deep K steps: each staged row is a whole 128-byte segment of the
+  // operand row (with 32-deep steps the memory system fetched 64 bytes from
+  // every row per step and sustained ~4.3 TB/s).  A staged 128-row tile is
+  // 16 KiB: row r's 16-byte chunk c at r * 128 + ((c ^ ((r >> 1) & 7)) << 4),
+  // so that a fragment read (16 consecutive rows, one chunk) and a DMA write
+  // (8 rows x 8 chunks) each touch 16 distinct 16-byte bank groups.  Three
+  // stages of three tiles (144 KiB): the DMAs of step s + 3 go into step s's
+  // stage after the barrier of step s, which waits for step s + 1's.
+  constexpr int kSK = 64;                     // reduction depth per K step
+  constexpr int kTile = kGramTile * kSK * 2;  // 16 KiB
+  constexpr int kStage = 3 * kTile;
+  constexpr int kInst = 2 * kDma;             // two 8-row DMAs per tile fed
+
+  // Staging by DMA: wave W moves rows 16 W .. 16 W + 15 of each tile it feeds
+  // (two 1 KiB buffer_load ... lds, 8 rows each); lane i the 16 bytes of row
+  // 16 W + 8 h + i / 8 that belong at physical chunk i % 8.  Rows at or past
+  // the segment's end are past the buffer range and read as zero.
   const u32x4_t words = rsrc_words(X, (uint32_t)(n * d * 2));
-  const int lchunk = (lane & 3) ^ ((lane >> 4) & 3);
-  const int voff0 = (16 * W + (lane >> 2)) * d * 2 + lchunk * 16;
+  auto lchunk_of = [&](int h) { return (lane & 7) ^ ((4 * h + (lane >> 4)) & 7); };
+  const int lc0 = lchunk_of(0), lc1 = lchunk_of(1);
+  const int voff0 = (16 * W + (lane >> 3)) * d * 2 + lc0 * 16;
+  const int voff1 = (16 * W + 8 + (lane >> 3)) * d * 2 + lc1 * 16;
   auto dma = [&](uint8_t* stage, int step) __attribute__((always_inline)) {
-    const int bad = step * kGK + lchunk * 8 < d ? 0 : kGramOutOfRange;
-    const uint32_t base = lds_addr(stage) + W * 1024;
+    const int bad0 = step * kSK + lc0 * 8 < d ? 0 : kGramOutOfRange;
+    const int bad1 = step * kSK + lc1 * 8 < d ? 0 : kGramOutOfRange;
+    const uint32_t base = lds_addr(stage) + W * 2048;
 #pragma unroll
-    for (int j = 0; j < kDma; ++j)
-      dma16(words, base + j * kGTileBytes, (voff0 + j * kGramTile * d * 2) | bad, step * kGK * 2);
+    for (int j = 0; j < kDma; ++j) {
+      dma16(words, base + j * kTile, (voff0 + j * kGramTile * d * 2) | bad0, step * kSK * 2);
+      dma16(words, base + j * kTile + 1024, (voff1 + j * kGramTile * d * 2) | bad1,
+            step * kSK * 2);
+    }
   };
+  // Fragment of slot s at 16-deep sub-step kk: lane l reads row l % 32 of
+  // the slot's unit, chunk 2 kk + l / 32; sub-step kk's offset is sub-step
+  // 0's XOR 32 kk.
   int foff[kGsSlots];
 #pragma unroll
   for (int s = 0; s < kGsSlots; ++s) {
     const int u = gs_unit(W, s);
-    foff[s] = (u >> 2) * kGTileBytes + gtile_off((u & 3) * 32 + (lane & 31), lane >> 5);
+    const int r = (u & 3) * 32 + (lane & 31);
+    foff[s] = (u >> 2) * kTile + r * 128 + (((lane >> 5) ^ ((r >> 1) & 7)) << 4);
   }
   struct Frags {
     bf16x8_t v[kGsSlots];
@@ -1267,44 +1290,46 @@ __device__ __forceinline__ void gsplit_item(const uint16_t* X, int n, int d, int
                                                        fr.v[gs_col_slot(M, W, b)], acc[b], 0, 0, 0);
   };
 
-  // The dense split kernel's K loop: four LDS stages, the DMAs of step s + 4
-  // into step s's stage right after the barrier of step s, which waits for
-  // step s + 1's; sub-step 1's fragments read before sub-step 0's MFMAs and
-  // the next step's sub-step 0 before this step's second MFMA group.
-  const int nk = ceil_div(d, kGK);
-  uint8_t* const ring[4] = {lds, lds + kStage, lds + 2 * kStage, lds + 3 * kStage};
+  // Each step: four sub-steps of MFMAs, the fragments of the next read during
+  // the current one's; the barrier sits before the last group, whose MFMAs
+  // run while the next stage's first fragments are read.
+  const int nk = ceil_div(d, kSK);
+  uint8_t* const ring[3] = {lds, lds + kStage, lds + 2 * kStage};
   dma(ring[0], 0);
   dma(ring[1], 1);
   dma(ring[2], 2);
-  dma(ring[3], 3);
-  DPC_WAIT_VMCNT(3 * kDma);
+  DPC_WAIT_VMCNT(2 * kInst);  // step 0 has landed
   __syncthreads();
   Frags fx, fy;
   read(ring[0], 0, fx);
   auto step = [&](auto P, int s) __attribute__((always_inline)) {
     constexpr int p = decltype(P)::value;
     uint8_t* cur = ring[p];
-    const uint8_t* nxt = ring[(p + 1) % 4];
+    const uint8_t* nxt = ring[(p + 1) % 3];
     read(cur, 1, fy);
     mma(fx);
     __builtin_amdgcn_sched_barrier(0);
-    DPC_WAIT_VMCNT(2 * kDma);  // step s + 1 has landed
+    read(cur, 2, fx);
+    mma(fy);
+    __builtin_amdgcn_sched_barrier(0);
+    read(cur, 3, fy);
+    mma(fx);
+    __builtin_amdgcn_sched_barrier(0);
+    DPC_WAIT_VMCNT(kInst);  // step s + 1 has landed
     __syncthreads();
-    dma(cur, s + 4);
+    dma(cur, s + 3);
     read(nxt, 0, fx);
     mma(fy);
     __builtin_amdgcn_sched_barrier(0);
   };
   int s = 0;
-  for (; s + 4 <= nk; s += 4) {
+  for (; s + 3 <= nk; s += 3) {
     step(StageIdx<0>(), s);
     step(StageIdx<1>(), s + 1);
     step(StageIdx<2>(), s + 2);
-    step(StageIdx<3>(), s + 3);
   }
   if (s < nk) step(StageIdx<0>(), s);
   if (s + 1 < nk) step(StageIdx<1>(), s + 1);
-  if (s + 2 < nk) step(StageIdx<2>(), s + 2);
   DPC_WAIT_VMCNT(0);
 
   // Meet the segment's other item (see split_item): both publish, the one
@@ -1477,7 +1502,7 @@ __device__ __forceinline__ void gsplit_item(const uint16_t* X, int n, int d, int
 __global__ void __launch_bounds__(512, 1)
 gram_gsplit_bf16_kernel(GramItems work, int nblocks, double* __restrict__ records,
                         int32_t* __restrict__ tickets, float* __restrict__ xbuf) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[4 * 3 * kGTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * 3 * kGramTile * 64 * 2];
   __shared__ double red[kGsMaxPairs * kSplitWaves * kRecStat];
   __shared__ int ticket_lds[2];
   const int l = xcd_logical_block(gridDim.x, nblocks);
