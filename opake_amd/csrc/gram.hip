@@ -631,31 +631,44 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   constexpr int ntr = diag_set ? 2 : 3;  // staged 128-row blocks
   const int tr_row0[3] = {t * kGramTile, (t + 1) * kGramTile, (diag_set ? t : q) * kGramTile};
-  constexpr int kStage = 3 * kGTileBytes;
+  // 64-deep K steps over 128-byte row segments, three stages of three
+  // 16 KiB tiles: the staging of the grouped split kernel (gsplit_item).
+  constexpr int kSK = 64;
+  constexpr int kTile = kGramTile * kSK * 2;
+  constexpr int kStage = 3 * kTile;
+  constexpr int kInst = 2 * ntr;
 
   // Staging by DMA: wave w moves rows 16 w .. 16 w + 15 of each staged
-  // block per K step (one 1 KiB buffer_load ... lds each); lane i the 16
-  // bytes of row 16 w + i / 4 that belong at physical chunk i % 4.
+  // block per K step (two 1 KiB buffer_load ... lds, 8 rows each); lane i
+  // the 16 bytes of row 16 w + 8 h + i / 8 that belong at physical chunk i % 8.
   const u32x4_t words = rsrc_words(X, (uint32_t)(T * d * 2));
-  const int lrow = 16 * w + (lane >> 2);
-  const int lchunk = (lane & 3) ^ ((lane >> 4) & 3);
-  int dvoff[3];
+  const int lc0 = (lane & 7) ^ ((lane >> 4) & 7), lc1 = (lane & 7) ^ ((4 + (lane >> 4)) & 7);
+  int dvoff0[3], dvoff1[3];
 #pragma unroll
-  for (int j = 0; j < 3; ++j) dvoff[j] = (tr_row0[j] + lrow) * d * 2 + lchunk * 16;
+  for (int j = 0; j < 3; ++j) {
+    dvoff0[j] = (tr_row0[j] + 16 * w + (lane >> 3)) * d * 2 + lc0 * 16;
+    dvoff1[j] = (tr_row0[j] + 16 * w + 8 + (lane >> 3)) * d * 2 + lc1 * 16;
+  }
   auto dma = [&](uint8_t* stage, int step) __attribute__((always_inline)) {
-    const int bad = step * kGK + lchunk * 8 < d ? 0 : kGramOutOfRange;
-    const uint32_t base = lds_addr(stage) + w * 1024;
+    const int bad0 = step * kSK + lc0 * 8 < d ? 0 : kGramOutOfRange;
+    const int bad1 = step * kSK + lc1 * 8 < d ? 0 : kGramOutOfRange;
+    const uint32_t base = lds_addr(stage) + w * 2048;
 #pragma unroll
-    for (int j = 0; j < ntr; ++j)
-      dma16(words, base + j * kGTileBytes, dvoff[j] | bad, step * kGK * 2);
+    for (int j = 0; j < ntr; ++j) {
+      dma16(words, base + j * kTile, dvoff0[j] | bad0, step * kSK * 2);
+      dma16(words, base + j * kTile + 1024, dvoff1[j] | bad1, step * kSK * 2);
+    }
   };
   // Fragment of row block f[k] at 16-deep sub-step kk: lane l reads row l % 32
-  // of the block, k chunk 2 kk + l / 32 (the 32x32x16 operand layout); sub-step
-  // 1's chunk is sub-step 0's with bit 1 set, i.e. its offset XOR 32.
+  // of the block, chunk 2 kk + l / 32 (the 32x32x16 operand layout); row r's
+  // chunk c sits at r * 128 + ((c ^ ((r >> 1) & 7)) << 4), so sub-step kk's
+  // offset is sub-step 0's XOR 32 kk.
   int foff[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k)
-    foff[k] = (f[k] >> 2) * kGTileBytes + gtile_off((f[k] & 3) * 32 + (lane & 31), lane >> 5);
+  for (int k = 0; k < 4; ++k) {
+    const int r = (f[k] & 3) * 32 + (lane & 31);
+    foff[k] = (f[k] >> 2) * kTile + r * 128 + (((lane >> 5) ^ ((r >> 1) & 7)) << 4);
+  }
   struct Frags {
     bf16x8_t v[4];
   };
@@ -674,55 +687,48 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
                                                        0, 0, 0);
   };
 
-  // The K loop of the paired kernel's G-only steps: sub-step 1's fragments
-  // are read before sub-step 0's MFMAs, the next step's rows (loaded two
-  // steps earlier) go into the other stage before the barrier and the
-  // registers are reloaded, and sub-step 0 of the next step is read (from
-  // the other stage) before this step's second MFMA group.  (Storing at the
-  // start of the step measured slower.)
-  // The K loop: four LDS stages; the DMAs of step s + 4 go into step s's
-  // stage right after the barrier of step s (three steps to land; three
-  // stages measured 1-2% slower), and the barrier of step s waits for step
-  // s + 1's.  Sub-step 1's fragments are
-  // read before sub-step 0's MFMAs, and sub-step 0 of the next step (from
-  // the next stage, after the barrier) before this step's second MFMA
-  // group.  (Register staging two steps ahead -- 16-byte loads and LDS
-  // stores -- measured 10% slower at B = 8, 3-7% at B = 32: a wave's load of
-  // 16 rows x 64 bytes moves at half the rate of a DMA of the same rows.)
-  const int nk = ceil_div(d, kGK);
-  uint8_t* const ring[4] = {lds, lds + kStage, lds + 2 * kStage, lds + 3 * kStage};
+  // The K loop: three stages; the DMAs of step s + 3 go into step s's stage
+  // right after the barrier of step s, which waits for step s + 1's.  Each
+  // step is four 16-deep sub-steps whose fragments are read during the
+  // previous sub-step's MFMAs; the barrier sits before the last group, which
+  // runs while the next stage's first fragments are read.
+  const int nk = ceil_div(d, kSK);
+  uint8_t* const ring[3] = {lds, lds + kStage, lds + 2 * kStage};
   dma(ring[0], 0);
   dma(ring[1], 1);
   dma(ring[2], 2);
-  dma(ring[3], 3);
-  DPC_WAIT_VMCNT(3 * ntr);
+  DPC_WAIT_VMCNT(2 * kInst);
   __syncthreads();
   Frags fx, fy;
   read(ring[0], 0, fx);
   auto step = [&](auto P, int s) __attribute__((always_inline)) {
     constexpr int p = decltype(P)::value;
     uint8_t* cur = ring[p];
-    const uint8_t* nxt = ring[(p + 1) % 4];
+    const uint8_t* nxt = ring[(p + 1) % 3];
     read(cur, 1, fy);
     mma(fx);
     __builtin_amdgcn_sched_barrier(0);
-    DPC_WAIT_VMCNT(2 * ntr);  // step s + 1 has landed
+    read(cur, 2, fx);
+    mma(fy);
+    __builtin_amdgcn_sched_barrier(0);
+    read(cur, 3, fy);
+    mma(fx);
+    __builtin_amdgcn_sched_barrier(0);
+    DPC_WAIT_VMCNT(kInst);  // step s + 1 has landed
     __syncthreads();
-    dma(cur, s + 4);
+    dma(cur, s + 3);
     read(nxt, 0, fx);
     mma(fy);
     __builtin_amdgcn_sched_barrier(0);
   };
   int s = 0;
-  for (; s + 4 <= nk; s += 4) {
+  for (; s + 3 <= nk; s += 3) {
     step(StageIdx<0>(), s);
     step(StageIdx<1>(), s + 1);
     step(StageIdx<2>(), s + 2);
-    step(StageIdx<3>(), s + 3);
   }
   if (s < nk) step(StageIdx<0>(), s);
   if (s + 1 < nk) step(StageIdx<1>(), s + 1);
-  if (s + 2 < nk) step(StageIdx<2>(), s + 2);
   DPC_WAIT_VMCNT(0);
 
   // Meet the set's other workgroup.  Both publish their accumulators (1 KiB
@@ -1008,7 +1014,7 @@ __global__ void __launch_bounds__(512, 1)
 gram_split_bf16_kernel(const SplitLayers lay, int B, int T, int npairs, int nsets, int nblocks,
                        double* __restrict__ records, int32_t* __restrict__ tickets,
                        float* __restrict__ xbuf, const SplitTail tail) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[4 * 3 * kGTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * 3 * kGramTile * 64 * 2];
   __shared__ double red[3 * kSplitWaves * kRecStat];
   __shared__ int ticket_lds[2];
   const int l0 = xcd_logical_block(gridDim.x, nblocks);
