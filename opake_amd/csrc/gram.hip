@@ -619,6 +619,34 @@ __device__ __forceinline__ void split_block_tile(bool diag_set, int rb, int cb, 
   }
 }
 
+// The exchange between the two items of a split tile set (or grouped
+// segment): word 1 + op of the set holds item op's XCD + 1 from the kernel's
+// start; the publisher adds kSplitReady once its accumulators are stored.
+constexpr int kSplitReady = 0x100;
+constexpr int kSplitSpinMax = 1 << 22;  // polls of ~64 cycles each: ~0.1 s
+
+// Publisher (one thread, after the workgroup's stores completed).
+__device__ __forceinline__ void split_publish(int32_t* set_words, int op, int my_xcc) {
+  const int partner =
+      __hip_atomic_load(&set_words[1 + (op ^ 1)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 0xff;
+  if (partner != my_xcc + 1) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __hip_atomic_store(&set_words[1 + op], (my_xcc + 1) | kSplitReady, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Reader (one thread): waits for the partner's ready bit; flags[1] = the
+// partner sits on this XCD, flags[2] = the wait gave up.
+__device__ __forceinline__ void split_await(int32_t* set_words, int op, int my_xcc, int* flags) {
+  int v = 0, spins = 0;
+  for (;;) {
+    v = __hip_atomic_load(&set_words[1 + (op ^ 1)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((v & kSplitReady) || ++spins >= kSplitSpinMax) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  flags[1] = (v & 0xff) == my_xcc + 1;
+  flags[2] = (v & kSplitReady) == 0;
+}
+
 template <int kKind, bool diag_set>
 __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int din, int dout,
                                            int t, int q, const int f[4], int op, int slot,
@@ -731,45 +759,51 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
   if (s + 1 < nk) step(StageIdx<1>(), s + 1);
   DPC_WAIT_VMCNT(0);
 
-  // Meet the set's other workgroup.  Both publish their accumulators (1 KiB
-  // per store instruction), wait for their stores to complete, and take an
-  // atomic ticket; the one that takes the second ticket reads its partner's
-  // accumulators and writes the records.  Nobody waits for anybody.  Where
-  // the data meets depends on the XCDs of the two workgroups (published at
-  // their start, see below): on one XCD its L2 cache holds the stores and
-  // the reader only drops stale lines from its CU's L1; otherwise (or when
-  // the partner's XCD is not known yet) the writer's ticket carries a
-  // device-scope release and the reader's a device-scope acquire, which
-  // write the stores back past the writer's L2 and drop the reader's stale
-  // L2 lines.  (The waves of a diagonal set run different instantiations of
-  // this function: the ticket goes through the kernel's LDS words.)
+  // Meet the set's other workgroup.  Each takes an atomic ticket as soon as
+  // its K loop is done.  The first publishes its accumulators (1 KiB per
+  // store instruction), waits for the stores to complete and sets the ready
+  // bit of its word (tickets[3 slot + 1 + op], which holds its XCD + 1 from
+  // the kernel's start); the second, which writes the records, reads the
+  // partner's accumulators once that bit is set -- in practice at once: the
+  // partner took its ticket earlier and only has its stores left.  Where the
+  // data meets depends on the XCDs of the two workgroups: on one XCD its L2
+  // cache holds the stores and the reader only drops stale lines from its
+  // CU's L1; otherwise (or when the partner's XCD is not known yet) the
+  // publisher's flag carries a device-scope release and the reader's wait a
+  // device-scope acquire, which write the stores back past the writer's L2
+  // and drop the reader's stale L2 lines.  The wait is bounded: past
+  // kSplitSpinMax polls (never seen) the records are written as NaN, which
+  // makes the examples' norms non-finite, so they take the non-finite path.
+  // (The waves of a diagonal set run different instantiations of this
+  // function: the ticket goes through the kernel's LDS words.)
   float4* base = reinterpret_cast<float4*>(xbuf) + (size_t)slot * (2 * kSplitSetBytes / 16);
   float4* mine = base + (size_t)op * (kSplitSetBytes / 16) + (size_t)w * (kSplitWaveBytes / 16);
   const float4* theirs =
       base + (size_t)(op ^ 1) * (kSplitSetBytes / 16) + (size_t)w * (kSplitWaveBytes / 16);
-#pragma unroll
-  for (int b = 0; b < kB; ++b)
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4)
-      mine[(b * 4 + r4) * 64 + lane] =
-          make_float4(acc[b][4 * r4], acc[b][4 * r4 + 1], acc[b][4 * r4 + 2], acc[b][4 * r4 + 3]);
-  DPC_WAIT_VMCNT(0);
   __syncthreads();
-  if (tid == 0) {
-    const int partner =
-        __hip_atomic_load(&tickets[3 * slot + 1 + (op ^ 1)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const bool same = partner == my_xcc + 1;
-    if (!same) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  if (tid == 0)
     ticket_lds[0] = __hip_atomic_fetch_add(&tickets[3 * slot], 1, __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT);
-    ticket_lds[1] = same;
-  }
   __syncthreads();
-  if (ticket_lds[0] == 0) return;
+  if (ticket_lds[0] == 0) {
+#pragma unroll
+    for (int b = 0; b < kB; ++b)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        mine[(b * 4 + r4) * 64 + lane] = make_float4(acc[b][4 * r4], acc[b][4 * r4 + 1],
+                                                     acc[b][4 * r4 + 2], acc[b][4 * r4 + 3]);
+    DPC_WAIT_VMCNT(0);
+    __syncthreads();
+    if (tid == 0) split_publish(tickets + 3 * slot, op, my_xcc);
+    return;
+  }
+  if (tid == 0) split_await(tickets + 3 * slot, op, my_xcc, ticket_lds);
+  __syncthreads();
   if (ticket_lds[1])
     asm volatile("buffer_inv sc0" ::: "memory");  // drop stale lines from this CU's L1
   else
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  const bool timed_out = ticket_lds[2] != 0;
 
   // Statistics per tile of the set (the paired kernel's record words; A's
   // Gram is P, G's is Q, each with the gamma of its own chain -- the bound is
@@ -888,6 +922,7 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
       // A device-scope store: written through to memory, where another XCD's
       // workgroup (the launch's tail) reads it without a writeback of this
       // XCD's L2.
+      if (timed_out && k < kRecStat) val = __builtin_nan("");
       __hip_atomic_store(&rec_ex[(size_t)pair[u] * DPC_GRAM_REC_WORDS + k], val, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -1016,7 +1051,7 @@ gram_split_bf16_kernel(const SplitLayers lay, int B, int T, int npairs, int nset
                        float* __restrict__ xbuf, const SplitTail tail) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[3 * 3 * kGramTile * 64 * 2];
   __shared__ double red[3 * kSplitWaves * kRecStat];
-  __shared__ int ticket_lds[2];
+  __shared__ int ticket_lds[3];
   const int l0 = xcd_logical_block(gridDim.x, nblocks);
   if (l0 < 0) return;  // padding workgroup: exits before any barrier
   // Several layers (B % 8 == 0): every XCD's range holds, layer after layer,
@@ -1338,36 +1373,46 @@ __device__ __forceinline__ void gsplit_item(const uint16_t* X, int n, int d, int
   if (s + 1 < nk) step(StageIdx<1>(), s + 1);
   DPC_WAIT_VMCNT(0);
 
-  // Meet the segment's other item (see split_item): both publish, the one
-  // with the second ticket reads its partner's accumulators and writes the
-  // segment's records.
+  // Meet the segment's other item as split_item meets its partner: the
+  // first to finish publishes its accumulators and sets its ready bit, the
+  // second reads them and writes the segment's records.
   float4* base = reinterpret_cast<float4*>(xbuf) + (size_t)set * (2 * kGsSetBytes / 16);
   float4* mine = base + (size_t)op * (kGsSetBytes / 16) + (size_t)W * (kGsWaveBytes / 16);
   const float4* theirs =
       base + (size_t)(op ^ 1) * (kGsSetBytes / 16) + (size_t)W * (kGsWaveBytes / 16);
+  __syncthreads();
+  if (tid == 0)
+    ticket_lds[0] = __hip_atomic_fetch_add(&tickets[3 * set], 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (ticket_lds[0] == 0) {
+#pragma unroll
+    for (int b = 0; b < kB; ++b)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        mine[(b * 4 + r4) * 64 + lane] = make_float4(acc[b][4 * r4], acc[b][4 * r4 + 1],
+                                                     acc[b][4 * r4 + 2], acc[b][4 * r4 + 3]);
+    DPC_WAIT_VMCNT(0);
+    __syncthreads();
+    if (tid == 0) split_publish(tickets + 3 * set, op, my_xcc);
+    return;
+  }
+  // The records phase reads this item's blocks back from its own area as well
+  // (a rolled loop over the blocks cannot index the accumulator registers).
 #pragma unroll
   for (int b = 0; b < kB; ++b)
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4)
-      mine[(b * 4 + r4) * 64 + lane] =
-          make_float4(acc[b][4 * r4], acc[b][4 * r4 + 1], acc[b][4 * r4 + 2], acc[b][4 * r4 + 3]);
+      mine[(b * 4 + r4) * 64 + lane] = make_float4(acc[b][4 * r4], acc[b][4 * r4 + 1],
+                                                   acc[b][4 * r4 + 2], acc[b][4 * r4 + 3]);
+  if (tid == 0) split_await(tickets + 3 * set, op, my_xcc, ticket_lds);
   DPC_WAIT_VMCNT(0);
   __syncthreads();
-  if (tid == 0) {
-    const int partner = __hip_atomic_load(&tickets[3 * set + 1 + (op ^ 1)], __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-    const bool same = partner == my_xcc + 1;
-    if (!same) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    ticket_lds[0] = __hip_atomic_fetch_add(&tickets[3 * set], 1, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-    ticket_lds[1] = same;
-  }
-  __syncthreads();
-  if (ticket_lds[0] == 0) return;
   if (ticket_lds[1])
     asm volatile("buffer_inv sc0" ::: "memory");  // drop stale lines from this CU's L1
   else
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  const bool timed_out = ticket_lds[2] != 0;
 
   const int nka = ceil_div(din, kGK), nkg = ceil_div(dout, kGK);
   const double gA = dpc_chain_gamma((double)nka * kGK, DPC_GRAM_U_MFMA);
@@ -1496,6 +1541,7 @@ __device__ __forceinline__ void gsplit_item(const uint16_t* X, int n, int d, int
     } else {
       val = k == 7 ? gA : k == 8 ? gQ : k == 9 ? (double)n : 0.0;
     }
+    if (timed_out && k < kRecStat) val = __builtin_nan("");
     rec[(size_t)u * DPC_GRAM_REC_WORDS + k] = val;
   }
 }
@@ -1510,7 +1556,7 @@ gram_gsplit_bf16_kernel(GramItems work, int nblocks, double* __restrict__ record
                         int32_t* __restrict__ tickets, float* __restrict__ xbuf) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[3 * 3 * kGramTile * 64 * 2];
   __shared__ double red[kGsMaxPairs * kSplitWaves * kRecStat];
-  __shared__ int ticket_lds[2];
+  __shared__ int ticket_lds[3];
   const int l = xcd_logical_block(gridDim.x, nblocks);
   if (l < 0) return;  // padding workgroup: exits before any barrier
   const int32_t* it = work.items + 4 * (size_t)l;
