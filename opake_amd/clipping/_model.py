@@ -515,7 +515,11 @@ def ghost_clip_captured(
                      key=str)
     guards = [num.guard_constants(dt, torch.promote_types(dt, torch.float32), roundoff)
               for dt in storage]
-    watch = _nf.watch(device, n_groups, nonfinite)
+    # Only Gram and flat norms can come out non-finite (materialised
+    # per-example gradients are sanitised by the leaf kernels), so a step of
+    # direct layers alone never waits for its norm pass on the host.
+    _nf.check_mode(nonfinite)
+    watch = _nf.watch(device, n_groups, nonfinite) if dense or segmented else None
     cfs = [ops.clip_factors(sq[g], num.conservative_bound(bounds[g]), guards, err=err[g],
                             kind=kind, gamma=gamma, count_threshold=num.float32_of(bounds[g]),
                             nonfinite=watch.slot(g) if watch is not None else None)
