@@ -10,7 +10,7 @@ constexpr int kClipThreads = 1024;
 __global__ void __launch_bounds__(kClipThreads)
 clip_factors_kernel(const double* __restrict__ sqnorm, const double* __restrict__ sqerr, int B,
                     const ClipJob job) {
-  __shared__ int shm[3 * (kClipThreads / 64) + 2];
+  __shared__ int shm[clip_block_lds_ints(kClipThreads / 64)];
   clip_factors_block(sqnorm, sqerr, B, job, shm);
 }
 

@@ -76,105 +76,155 @@ DPC_DEVICE double clip_guarded_scale(double sq, double err, double C, int kind, 
 }
 #pragma clang fp contract(on)
 
-// LDS words clip_factors_block needs for a workgroup of `nw` waves.
-DPC_HOST_DEVICE int clip_block_lds_ints(int nw) { return 3 * nw + 2; }
+// What the plans and counts need to know of one example, as flag bits: for
+// guard g, bit 2 g (fast: the GEMM's pipelined path may carry the scale) and
+// bit 2 g + 1 (slow: a positive scale it cannot); the norm above the count
+// threshold; a non-finite squared norm or bound.
+constexpr int kClipFlagClipped = 1 << 8;
+constexpr int kClipFlagNonfinite = 1 << 9;
 
-// The clip-factor pass over B examples by one whole workgroup (every thread
-// calls it; it synchronises the workgroup).  sq / err (err nullable) may be
-// global or LDS arrays.  `shm`: clip_block_lds_ints(waves) ints of LDS.
-//
-// Guard g's pass computes its scales and lists its active examples in plan g
-// (see plan.h): the fast ones from the front of `active` in increasing order,
-// the others from its back, in increasing order read backwards.  Each list is
-// an ordered compaction: a ballot within a wave, wave offsets through LDS.
-// The norms and the clipped count come from guard 0's pass.
-__device__ inline void clip_factors_block(const double* sq, const double* err, int B,
-                                          const ClipJob& job, int* shm) {
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int nw = blockDim.x >> 6;
-  int* wave_counts = shm;
-  int* clipped_counts = shm + nw;
-  int* slow_counts = shm + 2 * nw;
-  int* base = shm + 3 * nw;
-  int* base_slow = base + 1;
-  int clipped_local = 0, nonfinite_local = 0;
-  for (int i = tid; i < B; i += blockDim.x)
-    nonfinite_local += !(isfinite(sq[i]) && (err == nullptr || isfinite(err[i])));
+// One example's clip factors under every guard (the scale s and its value in
+// the multiply dtype sf), its norm estimate and its flag bits, before they
+// are stored.  `err` is ignored without `has_err`.
+struct ClipExample {
+  int flags;
+  float norm;
+  float sf[kClipMaxGuards];
+  double s[kClipMaxGuards];
+};
+
+DPC_DEVICE ClipExample clip_example_eval(double sq, double err, bool has_err, int B,
+                                         const ClipJob& job) {
+  ClipExample e;
+  e.flags = (isfinite(sq) && (!has_err || isfinite(err))) ? 0 : kClipFlagNonfinite;
+  e.norm = 0.0f;
   const bool fast_ok = (double)B * job.C <= (double)DPC_FAST_BC_MAX;
-  for (int g = 0; g < job.n_guards; ++g) {
-    const bool have_plan = job.plans != nullptr;
-    ClipPlanView plan = clip_plan_view((char*)job.plans + (size_t)g * clip_plan_bytes(B), B);
-    if (tid == 0) {
-      *base = 0;
-      *base_slow = 0;
+#pragma unroll
+  for (int g = 0; g < kClipMaxGuards; ++g) {
+    e.s[g] = 0.0;
+    e.sf[g] = 0.0f;
+    if (g >= job.n_guards) continue;
+    double norm;
+    const double s = clip_guarded_scale(sq, has_err ? err : 0.0, job.C, job.kind, job.gamma,
+                                        job.guards.rel[g], job.guards.abs_[g], &norm);
+    const float sf = clip_scale_in(s, job.guards.mult[g]);
+    e.s[g] = s;
+    e.sf[g] = sf;
+    if (g == 0) {
+      e.norm = (float)norm;
+      if ((float)norm > job.count_threshold) e.flags |= kClipFlagClipped;
     }
-    for (int start = 0; start < B; start += blockDim.x) {
-      const int i = start + tid;
-      bool fast = false, slow = false;
-      if (i < B) {
-        double norm;
-        const double s = clip_guarded_scale(sq[i], err ? err[i] : 0.0, job.C, job.kind,
-                                            job.gamma, job.guards.rel[g], job.guards.abs_[g],
-                                            &norm);
-        const float sf = clip_scale_in(s, job.guards.mult[g]);
-        if (job.scale) job.scale[(size_t)g * B + i] = sf;
-        if (job.scale64)
-          job.scale64[(size_t)g * B + i] = job.guards.mult[g] == DPC_F64 ? s : (double)sf;
-        if (g == 0) {
-          if (job.norms_out) job.norms_out[i] = (float)norm;
-          if ((float)norm > job.count_threshold) ++clipped_local;
-        }
-        fast = sf > 0.0f && fast_ok && sf >= DPC_FAST_SCALE_MIN && sf <= DPC_FAST_SCALE_MAX;
-        slow = sf > 0.0f && !fast;
-      }
-      const unsigned long long mf = __ballot(fast), ms = __ballot(slow);
-      const unsigned long long below = (1ull << lane) - 1ull;
-      if (lane == 0) {
-        wave_counts[w] = __popcll(mf);
-        slow_counts[w] = __popcll(ms);
-      }
-      __syncthreads();
-      int of = *base, os = *base_slow;
-      for (int v = 0; v < w; ++v) {
-        of += wave_counts[v];
-        os += slow_counts[v];
-      }
-      if (have_plan && fast) plan.active[of + __popcll(mf & below)] = i;
-      if (have_plan && slow) plan.active[B - 1 - (os + __popcll(ms & below))] = i;
-      __syncthreads();
-      if (tid == 0) {
-        for (int v = 0; v < nw; ++v) {
-          *base += wave_counts[v];
-          *base_slow += slow_counts[v];
-        }
-      }
-      __syncthreads();
-    }
-    if (tid == 0 && have_plan) {
-      *plan.nactive = *base + *base_slow;
-      *plan.nfast = *base;
-    }
-    __syncthreads();
+    const bool fast =
+        sf > 0.0f && fast_ok && sf >= DPC_FAST_SCALE_MIN && sf <= DPC_FAST_SCALE_MAX;
+    const bool slow = sf > 0.0f && !fast;
+    e.flags |= (fast ? 1 : 0) << (2 * g);
+    e.flags |= (slow ? 2 : 0) << (2 * g);
   }
-  for (int off = 32; off > 0; off >>= 1) {
-    clipped_local += __shfl_down(clipped_local, off, 64);
-    nonfinite_local += __shfl_down(nonfinite_local, off, 64);
+  return e;
+}
+
+// Stores example i's factors to the job's scale / scale64 / norms_out.
+DPC_DEVICE void clip_example_store(const ClipExample& e, int i, int B, const ClipJob& job) {
+#pragma unroll
+  for (int g = 0; g < kClipMaxGuards; ++g) {
+    if (g >= job.n_guards) continue;
+    if (job.scale) job.scale[(size_t)g * B + i] = e.sf[g];
+    if (job.scale64)
+      job.scale64[(size_t)g * B + i] = job.guards.mult[g] == DPC_F64 ? e.s[g] : (double)e.sf[g];
+  }
+  if (job.norms_out) job.norms_out[i] = e.norm;
+}
+
+// Both: stores example i's factors and returns its flag bits.
+DPC_DEVICE int clip_example(double sq, double err, bool has_err, int i, int B,
+                            const ClipJob& job) {
+  const ClipExample e = clip_example_eval(sq, err, has_err, B, job);
+  clip_example_store(e, i, B, job);
+  return e.flags;
+}
+
+// The running state of one wave's plan compaction: the size of each guard's
+// fast (2 g) and slow (2 g + 1) list so far, and the counts.
+struct ClipLists {
+  int size[2 * kClipMaxGuards];
+  int clipped;
+  int nonfinite;
+};
+
+// One wave (all 64 lanes, uniform control): places examples i0 .. i0 + n - 1,
+// whose flag bits are flags[0 .. n - 1], in every guard's plan after the
+// examples placed so far, 64 at a time.  Guard g's plan lists its active
+// examples (see plan.h): the fast ones from the front of `active` in
+// increasing order, the others from its back, in increasing order read
+// backwards -- an ordered compaction by ballots, the list sizes uniform.
+// The clipped count is guard 0's.
+DPC_DEVICE void clip_compact_wave(const int* flags, int n, int i0, int B, const ClipJob& job,
+                                  ClipLists& st) {
+  const int lane = threadIdx.x & 63;
+  const unsigned long long below = (1ull << lane) - 1ull;
+  const int nl = 2 * job.n_guards;
+  for (int c = 0; c < n; c += 64) {
+    const int f = c + lane < n ? flags[c + lane] : 0;
+    st.clipped += __popcll(__ballot((f & kClipFlagClipped) != 0));
+    st.nonfinite += __popcll(__ballot((f & kClipFlagNonfinite) != 0));
+#pragma unroll
+    for (int l = 0; l < 2 * kClipMaxGuards; ++l) {
+      if (l >= nl) break;
+      const unsigned long long m = __ballot((f >> l) & 1);
+      if (job.plans && ((f >> l) & 1)) {
+        const int o = st.size[l] + __popcll(m & below);
+        ClipPlanView plan =
+            clip_plan_view((char*)job.plans + (size_t)(l / 2) * clip_plan_bytes(B), B);
+        plan.active[(l & 1) ? B - 1 - o : o] = i0 + c + lane;
+      }
+      st.size[l] += __popcll(m);
+    }
+  }
+}
+
+// One wave, after the last clip_compact_wave: the list lengths and counts.
+DPC_DEVICE void clip_finish_wave(const ClipLists& st, int B, const ClipJob& job) {
+  const int lane = threadIdx.x & 63;
+  if (job.plans && lane < job.n_guards) {
+    int fast = 0, slow = 0;
+#pragma unroll
+    for (int g = 0; g < kClipMaxGuards; ++g) {
+      fast = lane == g ? st.size[2 * g] : fast;
+      slow = lane == g ? st.size[2 * g + 1] : slow;
+    }
+    ClipPlanView plan = clip_plan_view((char*)job.plans + (size_t)lane * clip_plan_bytes(B), B);
+    *plan.nactive = fast + slow;
+    *plan.nfast = fast;
   }
   if (lane == 0) {
-    clipped_counts[w] = clipped_local;
-    wave_counts[w] = nonfinite_local;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int total = 0, bad = 0;
-    for (int v = 0; v < nw; ++v) {
-      total += clipped_counts[v];
-      bad += wave_counts[v];
-    }
-    if (job.nclipped) *job.nclipped = total;
+    if (job.nclipped) *job.nclipped = st.clipped;
     if (job.nonfinite)
-      __hip_atomic_store(job.nonfinite, bad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(job.nonfinite, st.nonfinite, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
   }
+}
+
+// LDS words clip_factors_block needs for a workgroup of `nw` waves.
+DPC_HOST_DEVICE constexpr int clip_block_lds_ints(int nw) { return 64 * nw; }
+
+// The whole clip-factor pass over B examples by one workgroup (every thread
+// calls it; it synchronises the workgroup): the factors of a round of
+// blockDim examples in parallel (clip_example), their flags through LDS,
+// then wave 0 places them in the plans.  The barriers order LDS only, so the
+// output stores are never waited for.  sq / err (err nullable) may be global
+// or LDS arrays.  `shm`: clip_block_lds_ints(waves) ints of LDS.
+__device__ inline void clip_factors_block(const double* sq, const double* err, int B,
+                                          const ClipJob& job, int* shm) {
+  const int tid = threadIdx.x;
+  ClipLists st = {};
+  for (int start = 0; start < B; start += (int)blockDim.x) {
+    const int i = start + tid;
+    if (i < B) shm[tid] = clip_example(sq[i], err ? err[i] : 0.0, err != nullptr, i, B, job);
+    dpc_lds_barrier();
+    if (tid < 64) clip_compact_wave(shm, min((int)blockDim.x, B - start), start, B, job, st);
+    dpc_lds_barrier();
+  }
+  if (tid < 64) clip_finish_wave(st, B, job);
 }
 
 // Host side: the job of a dpc_clip_factors-style call; DPC_OK or DPC_EINVAL.

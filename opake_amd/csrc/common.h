@@ -29,6 +29,16 @@ DPC_DEVICE __attribute__((address_space(1))) T* global_ptr(const void* p) {
 // the compiler does not track.
 #define DPC_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
 
+// A workgroup barrier that orders LDS only.  __syncthreads() is a release /
+// acquire on all memory: after global stores it waits for them to complete
+// (vmcnt(0), a memory round trip).  This one waits for the wave's LDS
+// operations alone, for barriers that only hand LDS words between waves.
+DPC_DEVICE void dpc_lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ---------------------------------------------------------------------------
 // bfloat16 <-> float.  bf16 is the upper half of an IEEE binary32; the
 // narrowing conversion rounds to nearest-even and keeps NaN a NaN.
@@ -207,6 +217,14 @@ DPC_DEVICE double wave_sum_lane63_f64(double v) {
   v += dpp_f64<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
   v += dpp_f64<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
   return v;
+}
+
+// The same total, in every lane (read from lane 63).
+DPC_DEVICE double wave_sum_all_f64(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, wave_sum_lane63_f64(v));
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)b, 63);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(b >> 32), 63);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 
 // A float the compiler must take as given: without it, a float64 -> float32

@@ -963,21 +963,21 @@ struct SplitTail {
 
 __device__ __forceinline__ double gram_bound_wave(const double* rec, int nt, double* sum);
 
-// Largest batch whose squared norms and bounds the tail keeps in the
-// staging LDS (16 bytes per example, plus the clip routine's words).
+// Largest batch whose flags the tail keeps in the staging LDS (4 bytes per
+// example).
 constexpr int kSplitTailMaxB = 1024;
 
-// Device-scope loads of n doubles into LDS by the whole workgroup, eight per
+// Device-scope loads of n words into LDS by the whole workgroup, eight per
 // thread in flight (the data may come from other XCDs: no cache is trusted).
-__device__ __forceinline__ void load_agent_to_lds(const double* __restrict__ src, double* dst,
-                                                  int n) {
+template <typename T>
+__device__ __forceinline__ void load_agent_to_lds(const T* __restrict__ src, T* dst, int n) {
   constexpr int kU = 8;
   for (int i0 = 0; i0 < n; i0 += kU * (int)blockDim.x) {
-    double v[kU];
+    T v[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int i = i0 + u * (int)blockDim.x + (int)threadIdx.x;
-      v[u] = i < n ? __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0;
+      v[u] = i < n ? __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : T(0);
     }
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
@@ -990,7 +990,13 @@ __device__ __forceinline__ void load_agent_to_lds(const double* __restrict__ src
 // Called by every item after its part of the set (`writer`: this item wrote
 // the set's records; its partner has taken its ticket).  Counters advance
 // only after the data they announce has completed at the memory side
-// (device-scope stores and a wait), so no cache writeback is needed.
+// (device-scope stores and a wait), so no cache writeback is needed.  The
+// example's last set folds its records, computes the example's clip
+// factors (clip_example_eval: the same bits as the whole-batch pass), leaves
+// the example's flag bits in its set counter; the last example's finisher
+// builds the plans and counts from every example's flags and clears the
+// counters.  Barriers that only hand LDS words between waves order LDS
+// alone (dpc_lds_barrier), so the output stores are never waited for.
 __device__ void split_tail(const SplitTail& tail, const double* __restrict__ records,
                            int32_t* set_tickets, bool writer, int ex, int B, int nt, int nsets,
                            int nlayers, uint8_t* lds, int* flag) {
@@ -1002,7 +1008,7 @@ __device__ void split_tail(const SplitTail& tail, const double* __restrict__ rec
   if (tid == 0)
     flag[0] = __hip_atomic_fetch_add(&tail.ex_done[ex], 1, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT) == nsets * nlayers - 1;
-  __syncthreads();
+  dpc_lds_barrier();
   if (!flag[0]) return;
   // The example's last set: fold its records (every layer's).
   const size_t np = (size_t)nt * (nt + 1) / 2;
@@ -1011,7 +1017,7 @@ __device__ void split_tail(const SplitTail& tail, const double* __restrict__ rec
   for (int L = 0; L < nlayers; ++L)
     load_agent_to_lds(records + ((size_t)L * B + ex) * ex_words, rec_lds + L * ex_words,
                       ex_words);
-  __syncthreads();
+  dpc_lds_barrier();
   if (tid < 64) {
     double v = 0.0, ev = 0.0;
     for (int L = 0; L < nlayers; ++L) {
@@ -1021,28 +1027,32 @@ __device__ void split_tail(const SplitTail& tail, const double* __restrict__ rec
       ev = L == 0 ? e : ev + e;
     }
     if (lane == 0) {
-      __hip_atomic_store(&tail.sqnorm[ex], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (tail.sqerr)
-        __hip_atomic_store(&tail.sqerr[ex], ev, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      tail.ex_done[ex] = 0;
+      const ClipExample e = clip_example_eval(v, ev, tail.sqerr != nullptr, B, tail.job);
+      // The flags replace the example's set count; they are at memory before
+      // the example is counted.
+      __hip_atomic_store(&tail.ex_done[ex], e.flags, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      DPC_WAIT_VMCNT(0);
+      flag[0] = __hip_atomic_fetch_add(tail.done, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == B - 1;
+      // The outputs are read after the launch only: stored last, not waited for.
+      tail.sqnorm[ex] = v;
+      if (tail.sqerr) tail.sqerr[ex] = ev;
+      clip_example_store(e, ex, B, tail.job);
     }
   }
-  DPC_WAIT_VMCNT(0);
-  __syncthreads();
-  if (tid == 0)
-    flag[0] = __hip_atomic_fetch_add(tail.done, 1, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT) == B - 1;
-  __syncthreads();
+  dpc_lds_barrier();
   if (!flag[0]) return;
-  // The last example: the clip factors of all of them.
+  // The last example: the plans and counts of all of them (wave 0).
   if (tid == 0) *tail.done = 0;
-  double* sq = reinterpret_cast<double*>(lds);
-  double* er = sq + B;
-  load_agent_to_lds(tail.sqnorm, sq, B);
-  if (tail.sqerr) load_agent_to_lds(tail.sqerr, er, B);
-  __syncthreads();
-  clip_factors_block(sq, tail.sqerr ? er : nullptr, B, tail.job,
-                     reinterpret_cast<int*>(er + B));
+  int* fl = reinterpret_cast<int*>(lds);
+  load_agent_to_lds(tail.ex_done, fl, B);
+  dpc_lds_barrier();
+  for (int i = tid; i < B; i += (int)blockDim.x) tail.ex_done[i] = 0;
+  if (tid < 64) {
+    ClipLists st = {};
+    clip_compact_wave(fl, B, 0, B, tail.job, st);
+    clip_finish_wave(st, B, tail.job);
+  }
 }
 
 __global__ void __launch_bounds__(512, 1)
@@ -1725,8 +1735,8 @@ gram_grouped_generic_kernel(GramItems work, double* __restrict__ records) {
 
 // dpc_gram_bound's fold of an example's nt (nt + 1) / 2 records by one wave:
 // lane j takes pairs j, j + 64, ..., and the five partial sums are added by
-// a fixed butterfly (every lane ends with the same totals), so the result
-// does not depend on timing; it differs from the serial fold only in the
+// DPP row moves in a fixed order (wave_sum_all_f64: every lane gets the
+// totals), so the result does not depend on timing; it differs from the serial fold only in the
 // order of its fp64 additions of non-negative terms, which the bound's final
 // 1 + 2^-40 covers.  Returns the bound; *sum = the inner products' sum.
 __device__ __forceinline__ double gram_bound_wave(const double* rec, int nt, double* sum) {
@@ -1751,8 +1761,7 @@ __device__ __forceinline__ double gram_bound_wave(const double* rec, int nt, dou
     }
   }
 #pragma unroll
-  for (int k = 0; k < 5; ++k)
-    for (int off = 32; off > 0; off >>= 1) v[k] += __shfl_xor(v[k], off, 64);
+  for (int k = 0; k < 5; ++k) v[k] = wave_sum_all_f64(v[k]);
   *sum = v[0];
   const double gA = rec[7], gQ = rec[8], T = rec[9];
   const double g64 = (T * T + 256.0) * 0x1.0p-52;
@@ -2255,13 +2264,12 @@ extern "C" int dpc_gram_sqnorms_multi(int n, const void* const* A, const void* c
 namespace {
 bool gram_clip_one_launch(int B, int T, int din, int dout, int dtype, int with_bias) {
   const size_t dmax = (size_t)(din > dout ? din : dout);
-  // The tail's LDS holds one example's records, then 2 B doubles and the
-  // clip routine's words.
+  // The tail's LDS holds one example's records, then B flag words.
   const size_t nt = (size_t)ceil_div(T, kGramTile), np = nt * (nt + 1) / 2;
   const size_t lds_doubles = (size_t)(4 * 3 * kGTileBytes) / sizeof(double);
   return dtype == DPC_BF16 && !with_bias && din % 8 == 0 && dout % 8 == 0 && split_shape(T) &&
          B <= kSplitTailMaxB && ((size_t)T + kGramTile) * dmax * 2 < ((size_t)1 << 31) &&
-         np * DPC_GRAM_REC_WORDS <= lds_doubles && 2 * (size_t)B + 64 <= lds_doubles;
+         np * DPC_GRAM_REC_WORDS <= lds_doubles && (size_t)B <= 2 * lds_doubles;
 }
 }  // namespace
 
