@@ -423,8 +423,8 @@ def run_moe(args) -> dict:
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "clipped_sum_bf16_kernel<true, true> (grouped, G by DMA; 2 grouped "
-                      "GEMMs per step, each with its empty <true, false> companion launch)",
+            "kernel": "clipped_sum_bf16_kernel<true> (grouped; 2 grouped GEMMs per step, "
+                      "one launch each)",
             "achieved": gemm_tflops,
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
@@ -581,7 +581,7 @@ def run_block(args) -> dict:
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "clipped_sum_bf16_kernel<false, true> (dpc_clipped_sum_multi: the 4 "
+            "kernel": "clipped_sum_bf16_kernel<false> (dpc_clipped_sum_multi: the 4 "
                       "linear layers' 1024 output tiles in one launch per step)",
             "achieved": gemm_tflops,
             "peak": MFMA_BF16_PEAK_TFLOPS,

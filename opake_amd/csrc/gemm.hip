@@ -350,6 +350,13 @@ constexpr int kG0Bytes = (kOperandBytes > kEpiPassRows * kEpiLd * 4) ? kOperandB
 
 
 
+// The LDS arrays of the fast kernel, at namespace scope: every instantiation
+// of the tile body in one kernel uses the same four arrays.
+__shared__ __attribute__((aligned(16))) uint8_t lds_g0[kG0Bytes];
+__shared__ __attribute__((aligned(16))) uint8_t lds_g1[kOperandBytes];
+__shared__ __attribute__((aligned(16))) uint8_t lds_a0[kOperandBytes];
+__shared__ __attribute__((aligned(16))) uint8_t lds_a1[kOperandBytes];
+
 // The body of the fast kernel for one 256 x 256 output tile: kWaves = 8
 // waves (2 per SIMD) of 128 x 64, each made of 8 x 4 blocks of 16 x 16
 // (16x16x32 MFMA, fp32 accumulators).  (The 16x16x32 instruction sustains a
@@ -368,10 +375,6 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
   constexpr int kGC = kBK / kRowsPerPass;   // G chunks per thread per K step
   constexpr int kGCSub = kGC / 4;           // ... stored per phase
   constexpr int kDma = 32 / kWaves;         // 1 KiB A transfers per wave per K step
-  __shared__ __attribute__((aligned(16))) uint8_t lds_g0[kG0Bytes];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_g1[kOperandBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_a0[kOperandBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_a1[kOperandBytes];
   int M = args.ep.M, N = args.ep.N;
   const int T = args.T;
   int lin = xcd_linear_id(gridDim.x);
@@ -995,28 +998,24 @@ __device__ __forceinline__ bool grouped_scales_fit(const FastArgs& args) {
   return __syncthreads_and(fit) != 0;
 }
 
-// A grouped launch is a pair of launches over the same grid, kGdma first:
-// each workgroup runs in the launch that matches its problem's scales and
-// returns at once from the other.
-template <bool kGrouped, bool kGdma>
+// Dense mode: G by DMA.  Grouped mode: one launch in which each workgroup
+// takes the body that matches its problem's scales (both bodies share the
+// LDS arrays).
+template <bool kGrouped>
 __global__ void __launch_bounds__(kFastWaves * 64, 1) clipped_sum_bf16_kernel(FastArgs args) {
   if constexpr (kGrouped) {
-    if (grouped_scales_fit(args) != kGdma) return;
+    if (grouped_scales_fit(args))
+      clipped_sum_tile<true, true, kFastWaves>(args);
+    else
+      clipped_sum_tile<true, false, kFastWaves>(args);
+  } else {
+    clipped_sum_tile<false, true, kFastWaves>(args);
   }
-  clipped_sum_tile<kGrouped, kGdma, kFastWaves>(args);
 }
 
 template <bool kGrouped>
 void launch_fast(dim3 grid, hipStream_t s, const FastArgs& args) {
-  if constexpr (kGrouped) {
-    hipLaunchKernelGGL((clipped_sum_bf16_kernel<true, true>), grid, dim3(kFastWaves * 64), 0, s,
-                       args);
-    hipLaunchKernelGGL((clipped_sum_bf16_kernel<true, false>), grid, dim3(kFastWaves * 64), 0, s,
-                       args);
-  } else {
-    hipLaunchKernelGGL((clipped_sum_bf16_kernel<false, true>), grid, dim3(kFastWaves * 64), 0, s,
-                       args);
-  }
+  hipLaunchKernelGGL((clipped_sum_bf16_kernel<kGrouped>), grid, dim3(kFastWaves * 64), 0, s, args);
 }
 
 // Split-K finish: out = epilogue(sum over splits of partial[split], in
