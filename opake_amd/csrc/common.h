@@ -80,12 +80,12 @@ DPC_HOST_DEVICE void philox_mulhilo(uint32_t a, uint32_t b, uint32_t* hi, uint32
 
 // a ^ b ^ c; on the device one v_bitop3_b32 (gfx950's three-input bitwise
 // operation, truth table 0x96 = odd parity), where the compiler emits two
-// XORs.
+// XORs.  The builtin (not inline asm) lets a uniform operand -- the Philox
+// round key -- stay in its scalar register instead of being copied to a
+// vector register for every use.
 DPC_HOST_DEVICE uint32_t xor3_u32(uint32_t a, uint32_t b, uint32_t c) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  uint32_t r;
-  asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x96" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
+  return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
 #else
   return a ^ b ^ c;
 #endif
