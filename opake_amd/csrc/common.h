@@ -49,18 +49,41 @@ DPC_HOST_DEVICE float bf16_bits_to_f32(uint16_t b) {
   return v.f;
 }
 
-// Branch-free (a select, not a divergent branch around the NaN case).
+// On the host, branch-free (a select, not a divergent branch around the NaN
+// case).  On the device, the hardware conversion (v_cvt_pk_bf16_f32), which
+// returns the same bits for every one of the 2^32 inputs, NaNs included
+// (checked exhaustively on the device against the host formula).
 DPC_HOST_DEVICE uint16_t f32_to_bf16_bits(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  // Opaque, so that a float64 -> float32 -> bf16 chain is not folded into one
+  // float64 -> bf16 conversion (one rounding where torch rounds twice).
+  asm("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+#else
   union { uint32_t u; float f; } v;
   v.f = f;
   const uint32_t u = v.u;
   const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
   const uint32_t quiet_nan = (u >> 16) | 0x0040u;
   return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? quiet_nan : rounded);
+#endif
 }
 
 // Round a float to the nearest bf16 and widen it back (one rounding).
 DPC_HOST_DEVICE float round_to_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+// f32_to_bf16_bits of a and b, packed (a in the low half): on the device one
+// conversion of the pair.
+DPC_HOST_DEVICE uint32_t f32x2_to_bf16x2_bits(float a, float b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2_t __attribute__((ext_vector_type(2)));
+  asm("" : "+v"(a), "+v"(b));  // opaque, as in f32_to_bf16_bits
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{a, b}, b2_t));
+#else
+  return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+#endif
+}
 
 // ---------------------------------------------------------------------------
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy
@@ -133,9 +156,12 @@ DPC_HOST_DEVICE Philox4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uin
 // than 1e-6.  The function of (seed, leaf, r, c) does not depend on how a
 // kernel tiles the leaf, so every kernel that writes a leaf draws the same
 // stream.
-DPC_DEVICE float ln_unit_interval(double u) {
+// ln(x 2^escale) for x 2^escale in (0, 1): the exact power-of-two scale goes
+// to the exponent frexp returns, so it costs no float64 operation.
+DPC_DEVICE float ln_unit_interval(double x, int escale) {
   int e;
-  double m = frexp(u, &e);  // m in [0.5, 1)
+  double m = frexp(x, &e);  // m in [0.5, 1)
+  e += escale;
   if (m < 0.70710678118654752) {
     m *= 2.0;
     e -= 1;
@@ -157,11 +183,17 @@ DPC_DEVICE void philox_normal_pair(uint64_t seed, uint32_t leaf, uint64_t block,
   Philox4 w = philox4x32_10((uint32_t)block, (uint32_t)(block >> 32), leaf, 0u,
                             (uint32_t)seed, (uint32_t)(seed >> 32));
   uint64_t bits = ((uint64_t)w.v[0] << 32) | (uint64_t)w.v[1];
-  double u1 = ((double)(bits >> 11) + 0.5) * 0x1.0p-53;
-  float u2 = (float)(((double)w.v[2] + 0.5) * 0x1.0p-32);
+  // u1 = x1 2^-53 and u2 = x2 2^-32 with x1 = k + 1/2, x2 = w2 + 1/2 in
+  // double; the power-of-two scales are exact (u2 >= 2^-33 is a normal
+  // float, so scaling after the rounding to float gives the same float).
+  // k = bits >> 11 as hi 2^32 + lo (21 + 32 bits): lo + 1/2 and hi 2^32 are
+  // exact, so the fused multiply-add rounds k + 1/2 once, as (double)k + 0.5.
+  const double x1 = fma((double)(uint32_t)(bits >> 43), 0x1.0p32,
+                        (double)(uint32_t)(bits >> 11) + 0.5);
+  const float u2 = (float)((double)w.v[2] + 0.5) * 0x1.0p-32f;
   // -2 ln u1 >= 2.2e-16 (u1 <= 1 - 2^-54): a normal float, so the 1-ulp
   // hardware square root needs no scaling.
-  float radius = __builtin_amdgcn_sqrtf(-2.0f * ln_unit_interval(u1));
+  float radius = __builtin_amdgcn_sqrtf(-2.0f * ln_unit_interval(x1, -53));
   *z0 = radius * __builtin_amdgcn_cosf(u2);
   *z1 = radius * __builtin_amdgcn_sinf(u2);
 }

@@ -144,7 +144,7 @@ __device__ __forceinline__ void emit_quad(const Epilogue& ep, int m, int n, cons
     const float b = finish_value(v[r][1], ep, z[r][1]);
     const size_t idx = (size_t)(m + r) * ep.N + n;
     if (ep.out_bf16) {
-      const uint32_t packed = (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+      const uint32_t packed = f32x2_to_bf16x2_bits(a, b);
       *global_ptr<uint32_t>(reinterpret_cast<uint16_t*>(ep.out) + idx) = packed;
     } else {
       *global_ptr<f32x2_t>(reinterpret_cast<float*>(ep.out) + idx) = f32x2_t{a, b};
@@ -200,7 +200,7 @@ __device__ __forceinline__ void emit_quad_t(const Epilogue& ep, int m, int n, co
     const float b = finish_value_t<kBf, kNb, kNoise>(v[r][1], ep, z[r][1]);
     const size_t idx = (size_t)(m + r) * ep.N + n;
     if (kBf) {
-      const uint32_t packed = (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+      const uint32_t packed = f32x2_to_bf16x2_bits(a, b);
       *global_ptr<uint32_t>(reinterpret_cast<uint16_t*>(ep.out) + idx) = packed;
     } else {
       *global_ptr<f32x2_t>(reinterpret_cast<float*>(ep.out) + idx) = f32x2_t{a, b};

@@ -324,10 +324,8 @@ apply_sum_kernel(const int64_t* __restrict__ ptrs, const int64_t* __restrict__ s
       u32x4_t v, v2;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        v[k] = (uint32_t)f32_to_bf16_bits(acc[2 * k]) |
-               ((uint32_t)f32_to_bf16_bits(acc[2 * k + 1]) << 16);
-        v2[k] = (uint32_t)f32_to_bf16_bits(acc2[2 * k]) |
-                ((uint32_t)f32_to_bf16_bits(acc2[2 * k + 1]) << 16);
+        v[k] = f32x2_to_bf16x2_bits(acc[2 * k], acc[2 * k + 1]);
+        v2[k] = f32x2_to_bf16x2_bits(acc2[2 * k], acc2[2 * k + 1]);
       }
       *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(out) + o) = v;
       if (kSecond) *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(out_sq) + o) = v2;

@@ -115,7 +115,7 @@ add_noise_pairs_kernel(const void* __restrict__ x, void* __restrict__ y, int64_t
       const float a = add_scaled<true>(bf16_bits_to_f32((uint16_t)(xv & 0xffffu)), sigma, z[h][0]);
       const float d = add_scaled<true>(bf16_bits_to_f32((uint16_t)(xv >> 16)), sigma, z[h][1]);
       *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(y) + idx) =
-          (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(d) << 16);
+          f32x2_to_bf16x2_bits(a, d);
     } else {
       const float2 xv = *reinterpret_cast<const float2*>(reinterpret_cast<const float*>(x) + idx);
       float2 out;
