@@ -932,49 +932,62 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     // rows; each thread owns a pair of adjacent columns and 32 / (kT / 128) of
     // the slice's rows, walked in even/odd row pairs: coalesced 4- or 8-byte
     // stores, and one Philox block per (row pair, column) in a rolled loop.
+    // The usual choices (bf16 output, no / normalize_by, noise added) have a
+    // copy of their own with no branch per value; the others take the general
+    // one.
     float* tile = reinterpret_cast<float*>(lds_g0);
     constexpr int kEpiRows = kEpiPassRows / (kT / 128);
-    // Unrolled: the accumulator blocks are selected by compile-time indices
-    // (a runtime index would move them to scratch memory).
+    auto epilogue = [&](auto Usual) __attribute__((always_inline)) {
+      // Unrolled: the accumulator blocks are selected by compile-time indices
+      // (a runtime index would move them to scratch memory).
 #pragma unroll
-    for (int e = 0; e < kBM / kEpiPassRows; ++e) {
-      if (wm == (e >> 2)) {
-        // 16x16 block (i, j): lane l holds rows 4 (l / 16) + r of column l % 16.
+      for (int e = 0; e < kBM / kEpiPassRows; ++e) {
+        if (wm == (e >> 2)) {
+          // 16x16 block (i, j): lane l holds rows 4 (l / 16) + r of column l % 16.
 #pragma unroll
-        for (int i2 = 0; i2 < 2; ++i2)
+          for (int i2 = 0; i2 < 2; ++i2)
 #pragma unroll
-          for (int j = 0; j < kCB; ++j)
+            for (int j = 0; j < kCB; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int ml = 16 * i2 + 4 * (lane >> 4) + r;
-              const int nl = wn * kWC + j * 16 + (lane & 15);
-              tile[ml * kEpiLd + nl] = acc[2 * (e & 3) + i2][j][r];
-            }
-      }
-      __syncthreads();
-      const int cl = 2 * (tid & 127);
-      const int rr = (tid >> 7) * kEpiRows;
-      if (!kGrouped && args.splits > 1) {
-        // Split-K: the raw fp32 tile; the reduce kernel finishes it.
-        auto* part = global_ptr<float>(args.partial + (size_t)split * M * N);
-#pragma unroll 2
-        for (int ml = rr; ml < rr + kEpiRows; ++ml) {
-          const int m = m0 + e * kEpiPassRows + ml, n = n0 + cl;
-          if (m < M && n < N)
-            *reinterpret_cast<__attribute__((address_space(1))) f32x2_t*>(part + (size_t)m * N + n) =
-                *reinterpret_cast<const f32x2_t*>(tile + ml * kEpiLd + cl);
+              for (int r = 0; r < 4; ++r) {
+                const int ml = 16 * i2 + 4 * (lane >> 4) + r;
+                const int nl = wn * kWC + j * 16 + (lane & 15);
+                tile[ml * kEpiLd + nl] = acc[2 * (e & 3) + i2][j][r];
+              }
         }
-      } else {
+        __syncthreads();
+        const int cl = 2 * (tid & 127);
+        const int rr = (tid >> 7) * kEpiRows;
+        if (!decltype(Usual)::value && !kGrouped && args.splits > 1) {
+          // Split-K: the raw fp32 tile; the reduce kernel finishes it.
+          auto* part = global_ptr<float>(args.partial + (size_t)split * M * N);
 #pragma unroll 2
-        for (int ml = rr; ml < rr + kEpiRows; ml += 2) {
-          const float2 t0 = *reinterpret_cast<const float2*>(tile + ml * kEpiLd + cl);
-          const float2 t1 = *reinterpret_cast<const float2*>(tile + (ml + 1) * kEpiLd + cl);
-          const float v[2][2] = {{t0.x, t0.y}, {t1.x, t1.y}};
-          emit_quad(ep, m0 + e * kEpiPassRows + ml, n0 + cl, v);
+          for (int ml = rr; ml < rr + kEpiRows; ++ml) {
+            const int m = m0 + e * kEpiPassRows + ml, n = n0 + cl;
+            if (m < M && n < N)
+              *reinterpret_cast<__attribute__((address_space(1))) f32x2_t*>(part + (size_t)m * N +
+                                                                          n) =
+                  *reinterpret_cast<const f32x2_t*>(tile + ml * kEpiLd + cl);
+          }
+        } else {
+#pragma unroll 2
+          for (int ml = rr; ml < rr + kEpiRows; ml += 2) {
+            const float2 t0 = *reinterpret_cast<const float2*>(tile + ml * kEpiLd + cl);
+            const float2 t1 = *reinterpret_cast<const float2*>(tile + (ml + 1) * kEpiLd + cl);
+            const float v[2][2] = {{t0.x, t0.y}, {t1.x, t1.y}};
+            if constexpr (decltype(Usual)::value)
+              emit_quad_t<true, false, true>(ep, m0 + e * kEpiPassRows + ml, n0 + cl, v);
+            else
+              emit_quad(ep, m0 + e * kEpiPassRows + ml, n0 + cl, v);
+          }
         }
+        __syncthreads();
       }
-      __syncthreads();
-    }
+    };
+    if ((kGrouped || args.splits == 1) && ep.out_bf16 && !ep.apply_nb && ep.sigma != 0.0f)
+      epilogue(std::true_type());
+    else
+      epilogue(std::false_type());
   }
 }
 
