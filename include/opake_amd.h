@@ -175,6 +175,20 @@ int dpc_clip_factors(const double* sqnorm, const double* sqerr, int B, double C,
                      double* scale64, float* norms_out, int* nclipped, void* plan,
                      int* nonfinite, void* stream);
 
+/* dpc_clip_factors_groups: dpc_clip_factors for n_groups clipping groups in
+ * one launch -- the per-group clip of _streaming.py:84-108 with each group's
+ * own bound (_pytree.py:345-352) -- bit for bit n_groups calls of
+ * dpc_clip_factors, group g with C[g] and count_threshold[g] (HOST arrays of
+ * n_groups values), sqnorm + g * B and sqerr + g * B, and its outputs at
+ * scale / scale64 + g * n_guards * B, norms_out + g * B, nclipped + g,
+ * plan + g * n_guards * dpc_clip_plan_bytes(B) bytes and nonfinite + g. */
+int dpc_clip_factors_groups(const double* sqnorm, const double* sqerr, int n_groups, int B,
+                            const double* C, int kind, double gamma, const double* guard_rel,
+                            const double* guard_abs, const int* guard_mult, int n_guards,
+                            const float* count_threshold, float* scale, double* scale64,
+                            float* norms_out, int* nclipped, void* plan, int* nonfinite,
+                            void* stream);
+
 /* dpc_gram_clip_factors: the norm pass and the clip factors of one linear
  * layer -- _streaming.py:70-108 for a layer whose per-example gradients are
  * never formed -- exactly
@@ -362,13 +376,17 @@ int dpc_leaves_apply_ex(const int64_t* ptrs, const int64_t* sizes, const int32_t
  * paths clip the examples whose Gram norm is not finite from these. */
 int dpc_sanitize_columns(const void* x, void* out, int n, int T, int d, int dtype, void* stream);
 
-/* Per-group sums of per-leaf squared norms: out[g * B + b] (float64) = sum of
- * x[b * stride + j] over the columns j with col_group[j] == g, in column
- * order -- the per-group accumulation in leaf order of
- * packages/opake-engine/src/opake/api/engine/clipping/_streaming.py:71-80
- * (_accumulate_group_value, _pytree.py:345-352). */
-int dpc_group_sum_f64(const double* x, int B, int n, int stride, const int32_t* col_group,
-                      int n_groups, double* out, void* stream);
+/* Per-group sums of per-leaf squared norms: s = the sum of
+ * x[b * stride + j * col_stride] over the columns j with col_group[j] == g,
+ * in column order (from 0.0), and out[g * B + b] (float64) = s, or
+ * out[g * B + b] + s with `accumulate` -- the per-group accumulation in leaf
+ * order of packages/opake-engine/src/opake/api/engine/clipping/
+ * _streaming.py:71-80 (_accumulate_group_value, _pytree.py:345-352).  x is
+ * [B, n] row-major (col_stride 1, stride >= n) or column-major (stride 1,
+ * col_stride >= B); other layouts are DPC_EINVAL. */
+int dpc_group_sum_f64(const double* x, int B, int n, int stride, int col_stride,
+                      const int32_t* col_group, int n_groups, double* out, int accumulate,
+                      void* stream);
 
 /* ------------------------------------------------------------------------
  * Grouped (segmented) linear layers: E problems of one shape, e.g. the same

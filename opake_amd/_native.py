@@ -44,7 +44,7 @@ _c_u32 = ctypes.c_uint32
 _c_u64 = ctypes.c_uint64
 _c_i64 = ctypes.c_int64
 
-ABI_VERSION = 206  # dpc_version() of the library these signatures describe
+ABI_VERSION = 207  # dpc_version() of the library these signatures describe
 
 # name -> (restype, argtypes)
 SIGNATURES = {
@@ -69,6 +69,13 @@ SIGNATURES = {
          _c_void_p, _c_void_p],
     ),
     "dpc_clip_plan_bytes": (_c_size_t, [_c_int]),
+    "dpc_clip_factors_groups": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_int, _c_int, ctypes.POINTER(_c_double), _c_int, _c_double,
+         ctypes.POINTER(_c_double), ctypes.POINTER(_c_double), ctypes.POINTER(_c_int), _c_int,
+         ctypes.POINTER(_c_float), _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p],
+    ),
     "dpc_clip_factors": (
         _c_int,
         [_c_void_p, _c_void_p, _c_int, _c_double, _c_int, _c_double, ctypes.POINTER(_c_double),
@@ -143,7 +150,9 @@ SIGNATURES = {
          _c_u64, _c_u32, _c_void_p],
     ),
     "dpc_group_sum_f64": (
-        _c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_void_p],
+        _c_int,
+        [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
+         _c_void_p],
     ),
     "dpc_row_sum_f64": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_void_p]),
     "dpc_per_example_grads_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int]),

@@ -340,8 +340,8 @@ def leaves_clip_sum(leaves, clipping_norm, *, kind: str = "fixed", gamma: float 
     if grouped:
         col_group = device_table(leaf_groups, np.int32, device)
         group_sq = torch.empty((n_groups, B), dtype=torch.float64, device=device)
-        nat.call("dpc_group_sum_f64", nat.ptr(leaf_sq), B, L, L, nat.ptr(col_group), n_groups,
-                 nat.ptr(group_sq), stream)
+        nat.call("dpc_group_sum_f64", nat.ptr(leaf_sq), B, L, L, 1, nat.ptr(col_group),
+                 n_groups, nat.ptr(group_sq), 0, stream)
         cfs = [ops.clip_factors(group_sq[k], bound_of(bounds[k]), guards,
                                 kind=scale_kind, gamma=gamma,
                                 count_threshold=num.float32_of(bounds[k]))

@@ -442,8 +442,8 @@ def ghost_clip_captured(
     # Per-group, per-example squared norms and the bounds of their rounding
     # errors (the ghost norms' sq + err bounds ||g||^2; the materialised
     # leaves' norms follow the reference's own roundoff, in the guard).
-    sq = torch.zeros((n_groups, B), dtype=torch.float64, device=device)
-    err = torch.zeros((n_groups, B), dtype=torch.float64, device=device)
+    sq_err = torch.zeros((2, n_groups, B), dtype=torch.float64, device=device)
+    sq, err = sq_err[0], sq_err[1]
     gram_batches = {}
     for L in dense:
         if L.A.shape[1] == 1:
@@ -477,16 +477,13 @@ def ghost_clip_captured(
                                        gram_dims=[(L.A.shape[1], L.G.shape[1]) for L in members])
             seg_sq, seg_err = ops.grouped_gram_sqnorms(
                 [L.A for L in members], [L.G for L in members], layout, return_error=True)
-            # Per-group sums over the layers, in layer order: [B, E] columns
-            # folded by group.
+            # Per-group sums over the layers, in layer order: the [E, B]
+            # columns folded by group and added to the group's running sums.
             cols = device_table([L.group for L in members], np.int32, device)
             for acc, per_seg in ((sq, seg_sq), (err, seg_err)):
-                by_example = per_seg.t().contiguous()
-                gsum = torch.empty((n_groups, B), dtype=torch.float64, device=device)
-                nat.call("dpc_group_sum_f64", nat.ptr(by_example), B, len(members),
-                         len(members), nat.ptr(cols), n_groups, nat.ptr(gsum),
-                         nat.stream_handle(device))
-                acc += gsum
+                per_seg = per_seg.contiguous()
+                nat.call("dpc_group_sum_f64", nat.ptr(per_seg), B, len(members), 1, B,
+                         nat.ptr(cols), n_groups, nat.ptr(acc), 1, nat.stream_handle(device))
     # The clipped sums: one grouped launch per layer shape.
     buckets = {}
     for L in segmented:
@@ -502,10 +499,8 @@ def ghost_clip_captured(
         leaf_sq = direct_batch.sqnorms()
         cols = [leaf_group[n] for n in direct_names]
         col_group = device_table(cols, np.int32, device)
-        gsq = torch.empty((n_groups, B), dtype=torch.float64, device=device)
-        nat.call("dpc_group_sum_f64", nat.ptr(leaf_sq), B, len(cols), len(cols),
-                 nat.ptr(col_group), n_groups, nat.ptr(gsq), nat.stream_handle(device))
-        sq += gsq
+        nat.call("dpc_group_sum_f64", nat.ptr(leaf_sq), B, len(cols), len(cols), 1,
+                 nat.ptr(col_group), n_groups, nat.ptr(sq), 1, nat.stream_handle(device))
 
     # Guards for the materialised leaves the reference would clip.
     sizes = [math.prod(shapes[n]) for n in leaf_names]
@@ -520,10 +515,12 @@ def ghost_clip_captured(
     # direct layers alone never waits for its norm pass on the host.
     _nf.check_mode(nonfinite)
     watch = _nf.watch(device, n_groups, nonfinite) if dense or segmented else None
-    cfs = [ops.clip_factors(sq[g], num.conservative_bound(bounds[g]), guards, err=err[g],
-                            kind=kind, gamma=gamma, count_threshold=num.float32_of(bounds[g]),
-                            nonfinite=watch.slot(g) if watch is not None else None)
-           for g in range(n_groups)]
+    # Every group's clip factors in one launch (group g: row g of each output).
+    cfg = ops.clip_factors_groups(
+        sq, [num.conservative_bound(bounds[g]) for g in range(n_groups)], guards, err=err,
+        kind=kind, gamma=gamma, count_thresholds=[num.float32_of(b) for b in bounds],
+        nonfinite=watch.flags if watch is not None else None)
+    cfs = [cfg.group(g) for g in range(n_groups)]
 
     std = 0.0
     gen = None
@@ -612,7 +609,7 @@ def ghost_clip_captured(
             tree[wn] = w
     for members, layout in bucket_layouts:
         si = storage.index(members[0].A.dtype)
-        seg_scale = torch.stack([cfs[L.group].scale[si] for L in members])
+        seg_scale = _group_rows(cfg.scale, [L.group for L in members], si)
         names = [f"{L.name}.weight" for L in members]
         sigmas = [leaf_std(n) for n in names]
         gnoise = None
@@ -640,7 +637,7 @@ def ghost_clip_captured(
         for i, n in enumerate(names):
             tree[n] = stacked[i]
     if direct_batch is not None:
-        scale_rows = {dt: torch.stack([cf.scale[storage.index(dt)] for cf in cfs])
+        scale_rows = {dt: _group_rows(cfg.scale, list(range(n_groups)), storage.index(dt))
                       for dt in direct_batch.dtypes}
         sum_dtypes = ({dt: (_sum_dtype_of(dt, None), dtype) for dt in direct_batch.dtypes}
                       if dtype is not None else None)
@@ -680,13 +677,23 @@ def ghost_clip_captured(
         aux = GhostGradAux(
             loss_values=None,
             grad_norms=torch.sqrt(total).to(torch.float32) if per_group else cfs[0].norms,
-            clip_scales=torch.stack([cf.scale for cf in cfs]) if per_group else cfs[0].scale,
-            num_clipped=torch.cat([cf.nclipped for cf in cfs]),
+            clip_scales=cfg.scale if per_group else cfs[0].scale,
+            num_clipped=cfg.nclipped,
             batch_size=B, group_norms=group_norms)
         result = (result, aux)
     if noise_fn is None:
         return result
     return result, next_noise_state
+
+
+def _group_rows(scale: torch.Tensor, groups: list[int], guard: int) -> torch.Tensor:
+    """Rows ``scale[g, guard]`` for g in ``groups`` ([len(groups), B], contiguous):
+    a view when they are all the groups in order and the guard's rows are
+    contiguous, else a gather."""
+    G = scale.shape[0]
+    if groups == list(range(G)) and (scale.shape[1] == 1 or G == 1):
+        return scale[:, guard]
+    return scale[:, guard].index_select(0, device_table(groups, np.int32, scale.device))
 
 
 def _scale_kind(auto_s_gamma):

@@ -436,16 +436,18 @@ apply_sum_generic_kernel(const int64_t* __restrict__ ptrs, const int64_t* __rest
 // out[g * B + b] = sum over columns j with col_group[j] == g of x[b, j], in
 // column order (fp64): the reference's per-group accumulation in leaf order.
 __global__ void __launch_bounds__(kThreads)
-group_sum_kernel(const double* __restrict__ x, int B, int n, int stride,
-                 const int32_t* __restrict__ col_group, int n_groups, double* __restrict__ out) {
+group_sum_kernel(const double* __restrict__ x, int B, int n, int stride, int col_stride,
+                 const int32_t* __restrict__ col_group, int n_groups, double* __restrict__ out,
+                 int accumulate) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= B * n_groups) return;
   const int g = idx / B, b = idx % B;
   double s = 0.0;
   for (int j = 0; j < n; ++j) {
-    if (col_group[j] == g) s += x[(size_t)b * stride + j];
+    if (col_group[j] == g) s += x[(size_t)b * stride + (size_t)j * col_stride];
   }
-  out[(size_t)g * B + b] = s;
+  double* o = out + (size_t)g * B + b;
+  *o = accumulate ? *o + s : s;
 }
 
 template <bool kBf16, bool kOutBf16, typename... Args>
@@ -463,15 +465,21 @@ void launch_apply(hipStream_t s, bool second, bool postsq, Args... args) {
 
 }  // namespace
 
-extern "C" int dpc_group_sum_f64(const double* x, int B, int n, int stride,
+extern "C" int dpc_group_sum_f64(const double* x, int B, int n, int stride, int col_stride,
                                  const int32_t* col_group, int n_groups, double* out,
-                                 void* stream) {
-  if (B < 0 || n < 0 || stride < n || n_groups < 1) return DPC_EINVAL;
+                                 int accumulate, void* stream) {
+  if (B < 0 || n < 0 || stride < 1 || col_stride < 1 || n_groups < 1) return DPC_EINVAL;
+  // x is [B, n] with rows `stride` apart and columns `col_stride` apart: one
+  // of the two must step over the whole other dimension.
+  const bool row_major = (int64_t)stride >= (int64_t)n * col_stride;
+  const bool col_major = (int64_t)col_stride >= (int64_t)B * stride;
+  if (!row_major && !col_major) return DPC_EINVAL;
   if (B == 0) return DPC_OK;
   if (!out || (n > 0 && (!x || !col_group))) return DPC_EINVAL;
   const int total = B * n_groups;
   hipLaunchKernelGGL(group_sum_kernel, dim3(ceil_div(total, kThreads)), dim3(kThreads), 0,
-                     (hipStream_t)stream, x, B, n, stride, col_group, n_groups, out);
+                     (hipStream_t)stream, x, B, n, stride, col_stride, col_group, n_groups, out,
+                     accumulate);
   DPC_HIP_CHECK(hipGetLastError());
   return DPC_OK;
 }

@@ -235,6 +235,72 @@ def clip_factors(
     return cf
 
 
+@dataclass
+class ClipFactorGroups:
+    """Outputs of :func:`clip_factors_groups`: group g's are ``group(g)``."""
+
+    scale: torch.Tensor  # float32 [n_groups, n_guards, B]
+    norms: torch.Tensor  # float32 [n_groups, B]
+    nclipped: torch.Tensor  # int32 [n_groups]
+    plan: torch.Tensor  # uint8 [n_groups, n_guards, plan bytes]
+    scale64: torch.Tensor | None = None  # float64 [n_groups, n_guards, B]
+
+    def group(self, g: int) -> ClipFactors:
+        return ClipFactors(scale=self.scale[g], norms=self.norms[g],
+                           nclipped=self.nclipped[g:g + 1], plan=self.plan[g],
+                           scale64=None if self.scale64 is None else self.scale64[g])
+
+
+def clip_factors_groups(
+    sqnorm: torch.Tensor,
+    clipping_norms: list[float],
+    guards: list[tuple[float, float]],
+    *,
+    err: torch.Tensor | None = None,
+    kind: int = nat.SCALE_FIXED,
+    gamma: float = 0.0,
+    count_thresholds: list[float],
+    nonfinite: torch.Tensor | None = None,
+) -> ClipFactorGroups:
+    """:func:`clip_factors` for every row g of ``sqnorm`` (float64 [n_groups,
+    B]) with its own bound ``clipping_norms[g]`` and count threshold, in one
+    launch; the same bits as one call per group.  ``nonfinite``: int32
+    [n_groups] (device or pinned host memory), one count per group."""
+    dev = nat.require_device(sqnorm, err)
+    if sqnorm.dtype != torch.float64 or sqnorm.dim() != 2:
+        raise ConfigurationError("sqnorm must be a float64 [n_groups, B] tensor")
+    G, B = sqnorm.shape
+    if len(clipping_norms) != G or len(count_thresholds) != G:
+        raise ConfigurationError("one clipping norm and count threshold per group")
+    if not 1 <= len(guards) <= 4:
+        raise ConfigurationError("between 1 and 4 guards are supported")
+    if err is not None and (err.dtype != torch.float64 or tuple(err.shape) != (G, B)):
+        raise ConfigurationError("err must be a float64 tensor like sqnorm")
+    if nonfinite is not None and (nonfinite.dtype != torch.int32 or nonfinite.numel() < G):
+        raise ConfigurationError("nonfinite must hold one int32 per group")
+    n = len(guards)
+    rel = (ctypes.c_double * n)(*[g[0] for g in guards])
+    abs_ = (ctypes.c_double * n)(*[g[1] for g in guards])
+    mult, codes = _guard_mults(guards)
+    cs = (ctypes.c_double * G)(*[float(c) for c in clipping_norms])
+    thr = (ctypes.c_float * G)(*[float(t) for t in count_thresholds])
+    lib = nat.load()
+    out = ClipFactorGroups(
+        scale=torch.empty((G, n, B), dtype=torch.float32, device=dev),
+        norms=torch.empty((G, B), dtype=torch.float32, device=dev),
+        nclipped=torch.empty(G, dtype=torch.int32, device=dev),
+        plan=torch.empty((G, n, lib.dpc_clip_plan_bytes(B)), dtype=torch.uint8, device=dev),
+        scale64=(torch.empty((G, n, B), dtype=torch.float64, device=dev)
+                 if nat.DPC_F64 in codes else None))
+    nat.call(
+        "dpc_clip_factors_groups", nat.ptr(_contig(sqnorm)),
+        nat.ptr(None if err is None else _contig(err)), G, B, cs, kind, float(gamma), rel, abs_,
+        mult, n, thr, nat.ptr(out.scale), nat.ptr(out.scale64), nat.ptr(out.norms),
+        nat.ptr(out.nclipped), nat.ptr(out.plan), nat.ptr(nonfinite), nat.stream_handle(dev),
+    )
+    return out
+
+
 def _guard_mults(guards):
     """The guards' multiply dtype codes (third element: a dtype, ``True`` for
     bfloat16, absent for float32) as a ctypes array, and as a list."""
@@ -1002,7 +1068,9 @@ def philox4x32_10(counter: tuple[int, int, int, int], key: tuple[int, int], n: i
 
 
 __all__ = [
+    "ClipFactorGroups",
     "ClipFactors",
+    "clip_factors_groups",
     "gram_clip_factors",
     "sanitize_columns",
     "GroupedNoise",

@@ -34,7 +34,7 @@ def test_version_and_size_queries():
     if not _native.LIB_PATH.exists():
         pytest.skip("native library not built")
     lib = _native.load()
-    assert lib.dpc_version() == _native.ABI_VERSION == 206
+    assert lib.dpc_version() == _native.ABI_VERSION == 207
     assert lib.dpc_clip_plan_bytes(32) == 16 + 32 * 4
     # Grouped Gram workspace: the records, then the split kernel's tickets and
     # accumulator exchange (2 x 224 KiB per set), each 256-byte aligned.

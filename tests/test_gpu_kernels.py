@@ -182,6 +182,83 @@ def test_clip_factors_bit_exact(dev, kind, with_err):
         assert list(active[B - len(slow):][::-1]) == slow
 
 
+def _plan_lists(plan, B):
+    """Per guard: (nactive, nfast, front list, back list) -- the words a plan
+    defines (the rest of its buffer is never written)."""
+    out = []
+    for p in plan.cpu().numpy():
+        w = p.view(np.int32)
+        nact, nfast = int(w[0]), int(w[1])
+        act = w[4:4 + B]
+        out.append((nact, nfast, act[:nfast].tolist(), act[B - (nact - nfast):].tolist()))
+    return out
+
+
+@pytest.mark.parametrize("G,B", [(8, 300), (70, 37)])
+def test_clip_factors_groups_match_per_group_calls(dev, G, B):
+    """One launch over G groups equals G dpc_clip_factors calls bit for bit
+    (scales, float64 scales, norms, counts, plans, non-finite counts), groups
+    past the 64 of one launch included."""
+    g = _gen(23)
+    sq = torch.exp(torch.randn(G, B, generator=g, dtype=torch.float64) * 3)
+    err = sq * torch.rand(G, B, generator=g, dtype=torch.float64) * 0.01
+    sq[0, :3] = torch.tensor([math.nan, math.inf, 0.0], dtype=torch.float64)
+    sq[G - 1, 5] = 2.0 ** 140  # a slow-list example
+    err[1, 4] = math.nan
+    Cs = [0.5 + 0.25 * k for k in range(G)]
+    thr = [float(np.float32(c)) for c in Cs]
+    roundoff = clip_oracle.norm_roundoff(torch.float32, torch.float64, 2, 4096)
+    guards = [(*num.guard_constants(torch.bfloat16, torch.float32, roundoff), True),
+              (*num.guard_constants(torch.float64, torch.float64, roundoff), torch.float64)]
+    sq_d, err_d = sq.to(dev), err.to(dev)
+    nf = torch.full((G,), -1, dtype=torch.int32, device=dev)
+    got = ops.clip_factors_groups(sq_d, Cs, guards, err=err_d, count_thresholds=thr,
+                                  nonfinite=nf)
+    for k in range(G):
+        nf1 = torch.full((1,), -1, dtype=torch.int32, device=dev)
+        want = ops.clip_factors(sq_d[k], Cs[k], guards, err=err_d[k], count_threshold=thr[k],
+                                nonfinite=nf1)
+        one = got.group(k)
+        assert torch.equal(one.scale.cpu(), want.scale.cpu()), k
+        assert torch.equal(one.scale64.cpu(), want.scale64.cpu()), k
+        torch.testing.assert_close(one.norms.cpu(), want.norms.cpu(), rtol=0, atol=0,
+                                   equal_nan=True)
+        assert torch.equal(one.nclipped.cpu(), want.nclipped.cpu()), k
+        assert _plan_lists(one.plan, B) == _plan_lists(want.plan, B), k
+        assert int(nf[k]) == int(nf1[0]), k
+    assert int(nf[0]) == 2 and int(nf[1]) == 1
+
+
+@pytest.mark.parametrize("accumulate", [0, 1])
+def test_group_sum_column_major_and_accumulate(dev, accumulate):
+    """dpc_group_sum_f64 over a column-major [B, n] block: per-group sums in
+    column order from 0.0, added to the output when accumulating -- the same
+    fp64 additions as a sequential host loop."""
+    g = _gen(29)
+    B, n, G = 45, 13, 4
+    x = torch.randn(n, B, generator=g, dtype=torch.float64)  # column j is row j
+    groups = [int(v) for v in torch.randint(0, G, (n,), generator=g)]
+    base = torch.randn(G, B, generator=g, dtype=torch.float64)
+    out = base.clone().to(dev)
+    col_group = torch.tensor(groups, dtype=torch.int32, device=dev)
+    xd = x.to(dev)
+    nat.call("dpc_group_sum_f64", nat.ptr(xd), B, n, 1, B, nat.ptr(col_group), G,
+             nat.ptr(out), accumulate, nat.stream_handle(torch.device(dev)))
+    want = torch.empty(G, B, dtype=torch.float64)
+    for gg in range(G):
+        for b in range(B):
+            s = 0.0
+            for j in range(n):
+                if groups[j] == gg:
+                    s += float(x[j, b])
+            want[gg, b] = base[gg, b] + s if accumulate else s
+    assert torch.equal(out.cpu(), want)
+    # A layout where neither dimension steps over the other is refused.
+    rc = nat.load().dpc_group_sum_f64(nat.ptr(xd), B, n, 2, 2, nat.ptr(col_group), G,
+                                      nat.ptr(out), 0, nat.stream_handle(torch.device(dev)))
+    assert rc == nat.DPC_EINVAL
+
+
 def test_clip_factors_boundary_example(dev):
     # The reference's own boundary pin: [[3,4],[0.6,0.8]], C=1 -> [1.2, 1.6]
     # (an example at ||g|| == C is still scaled by rel < 1).
