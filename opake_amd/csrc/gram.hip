@@ -941,7 +941,42 @@ struct SplitLayers {
   const uint16_t* G[kSplitMaxLayers];
   int din[kSplitMaxLayers], dout[kSplitMaxLayers], region[kSplitMaxLayers];
   int n;
+  int round;  // several layers: the CUs of an XCD (0: layer after layer)
 };
+
+// Several layers: the item at position lx of an XCD's range.  The items fall
+// into classes (layer, operand) of bpx * nsets items, each with its
+// operand's K loop.  An XCD's workgroups go to its CUs in launch order, one
+// per free CU, and a workgroup that finds no free CU holds back the launch's
+// later ones on every XCD; so the classes run in decreasing order of K (ties:
+// layer, then operand), which makes every round of `round` consecutive
+// positions items of one length (no CU waits behind another's long item),
+// in serpentine rounds (odd rounds reversed) so that the CUs' sums even out
+// where a class ends inside a round.
+__device__ __forceinline__ void split_multi_item(const SplitLayers& lay, int nsets, int bpx,
+                                                 int per_xcd, int lx, int* L, int* ex_local,
+                                                 int* set, int* op) {
+  const int W = lay.round;
+  const int r = lx / W, slot = lx - r * W;
+  const bool full = (r + 1) * W <= per_xcd;
+  const int rank = ((r & 1) && full) ? r * W + (W - 1 - slot) : lx;
+  const int per_cls = bpx * nsets;
+  const int c = rank / per_cls, j = rank - c * per_cls;
+  int cls = 0;
+  for (int k = 0; k < 2 * lay.n; ++k) {
+    const int kk = (k & 1) ? lay.dout[k >> 1] : lay.din[k >> 1];
+    int pos = 0;
+    for (int m = 0; m < 2 * lay.n; ++m) {
+      const int km = (m & 1) ? lay.dout[m >> 1] : lay.din[m >> 1];
+      pos += (km > kk || (km == kk && m < k)) ? 1 : 0;
+    }
+    if (pos == c) cls = k;
+  }
+  *L = cls >> 1;
+  *op = cls & 1;
+  *ex_local = j / nsets;
+  *set = j - (j / nsets) * nsets;
+}
 
 // The clip factors folded into a split launch (dpc_gram_clip_factors).  Each
 // tile set's record writer (the item with the second ticket) clears the
@@ -1070,9 +1105,15 @@ gram_split_bf16_kernel(const SplitLayers lay, int B, int T, int npairs, int nset
   if (lay.n > 1) {
     const int per_xcd = nblocks / kXcds, bpx = B / kXcds, per_lx = bpx * 2 * nsets;
     const int x = l0 / per_xcd, lx = l0 - x * per_xcd;
-    L = lx / per_lx;
-    const int r = lx - L * per_lx;
-    l = (x * bpx + r / (2 * nsets)) * 2 * nsets + r % (2 * nsets);
+    if (lay.round > 0) {
+      int e, st, o;
+      split_multi_item(lay, nsets, bpx, per_xcd, lx, &L, &e, &st, &o);
+      l = ((x * bpx + e) * nsets + st) * 2 + o;
+    } else {
+      L = lx / per_lx;
+      const int r = lx - L * per_lx;
+      l = (x * bpx + r / (2 * nsets)) * 2 * nsets + r % (2 * nsets);
+    }
   }
   L = __builtin_amdgcn_readfirstlane(L);
   l = __builtin_amdgcn_readfirstlane(l);
@@ -1948,6 +1989,7 @@ extern "C" int dpc_gram_sqnorms(const void* A, const void* G, int B, int T, int 
                        dim3(kGramThreads), 0, s, tickets, 3 * nsets * B);
     SplitLayers lay;
     lay.n = 1;
+    lay.round = 0;
     for (int i = 0; i < kSplitMaxLayers; ++i) {
       lay.A[i] = (const uint16_t*)A;
       lay.G[i] = (const uint16_t*)G;
@@ -2123,6 +2165,22 @@ extern "C" int dpc_row_sum_f64(const double* x, int B, int n, int accumulate, do
 }
 
 namespace {
+// Compute units per XCD of the current device (cached per device; 32 on
+// MI355X: 256 CUs in 8 XCDs).
+int cus_per_xcd() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 32;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus < kXcds)
+      cus = 32 * kXcds;
+    cached[dev] = cus / kXcds;
+  }
+  return cached[dev];
+}
+
 constexpr int kMaxDevices = 64;
 void* g_scratch_ptr[kMaxDevices];
 std::mutex g_scratch_mu;
@@ -2240,6 +2298,7 @@ extern "C" int dpc_gram_sqnorms_multi(int n, const void* const* A, const void* c
   });
   SplitLayers lay;
   lay.n = n;
+  lay.round = cus_per_xcd();
   for (int k = 0; k < kSplitMaxLayers; ++k) {
     const int i = order[k < n ? k : 0];
     lay.A[k] = (const uint16_t*)A[i];
@@ -2330,6 +2389,7 @@ extern "C" int dpc_gram_clip_factors(const void* A, const void* G, int B, int T,
   const int n_tickets = 3 * nsets * B;
   SplitLayers lay;
   lay.n = 1;
+  lay.round = 0;
   for (int i = 0; i < kSplitMaxLayers; ++i) {
     lay.A[i] = (const uint16_t*)A;
     lay.G[i] = (const uint16_t*)G;
