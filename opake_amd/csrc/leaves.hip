@@ -225,8 +225,9 @@ __device__ __forceinline__ float store_round(float x, float s) {
 // bf16, two for fp32), so each element's fp32 sum runs in example order.
 // With post_sq, each wave's sum of stored^2 over its 512 elements of example
 // b goes to post_sq[b, 4 t + wave] (a fixed shuffle tree over the thread
-// sums, each in element order).
-constexpr int kApplyUnroll = 4;
+// sums, each in element order).  Eight examples ahead rather than four:
+// 206 vs 217 us for a [32, 4096 x 4096] bf16 leaf (sixteen: 212 us).
+constexpr int kApplyUnroll = 8;
 
 #pragma clang fp contract(off)
 template <bool kBf16, bool kOutBf16, bool kSecond, bool kPostSq>
