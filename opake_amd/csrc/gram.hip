@@ -851,17 +851,29 @@ __device__ __forceinline__ void split_item(const uint16_t* X, int T, int d, int 
     double v[kRecStat] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
     float da = 0.0f, dg = 0.0f;
     bool has_diag = false;
+    // x: this item's operand, y: the partner's; the sums of squares are
+    // swapped into place (v[1]: A's, v[2]: G's) after the block.
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const double a = op == 0 ? acc[b][r] : other[r];
-      const double g = op == 0 ? other[r] : acc[b][r];
-      v[0] += a * g;
-      const bool on_diag = dblk && ((r >> 2) * 8 + 4 * (lane >> 5) + (r & 3)) == (lane & 31);
-      v[1] += on_diag ? 0.0 : a * a;
-      v[2] += on_diag ? 0.0 : g * g;
-      da = on_diag ? (float)a : da;
-      dg = on_diag ? (float)g : dg;
+      const double x = acc[b][r], y = other[r];
+      v[0] += x * y;
+      // Only kDiag4 waves hold diagonal blocks (the other kinds pair distinct
+      // row blocks): for them the test folds away at compile time.
+      const bool on_diag = kKind == kDiag4 && dblk &&
+                           ((r >> 2) * 8 + 4 * (lane >> 5) + (r & 3)) == (lane & 31);
+      v[1] += on_diag ? 0.0 : x * x;
+      v[2] += on_diag ? 0.0 : y * y;
+      da = on_diag ? acc[b][r] : da;
+      dg = on_diag ? other[r] : dg;
       has_diag = has_diag || on_diag;
+    }
+    if (op != 0) {
+      const double t = v[1];
+      v[1] = v[2];
+      v[2] = t;
+      const float d = da;
+      da = dg;
+      dg = d;
     }
     if (has_diag) {
       const double ws = dpc_row_bound_inv(da, invA, etaA, DPC_GRAM_ROW_SLACK_MFMA);
