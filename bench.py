@@ -67,6 +67,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
+import opake_amd  # noqa: E402,F401  (first: it sets HIP's options before the GPU is used)
 import torch  # noqa: E402,F401  (every measured path needs it)
 
 METRIC = "DP-step examples/sec at 1 MI355X; TFLOP/s and % of MFMA/HBM roofline"

@@ -7,7 +7,16 @@ types, with the work done by hand-written HIP kernels for gfx950 behind the C
 ABI in ``include/opake_amd.h``.
 """
 
-from opake_amd import exceptions, random, types
+import os as _os
+
+# Kernel arguments in device memory: the first waves of a launch read them
+# without a round trip to host memory (4-5 us less per config-2 step, two
+# launches).  HIP reads this when its runtime starts, so it takes effect
+# only if nothing in the process has used the GPU yet; a value the caller
+# set is kept.
+_os.environ.setdefault("HIP_FORCE_DEV_KERNARG", "1")
+
+from opake_amd import exceptions, random, types  # noqa: E402
 from opake_amd.random import RngKey, fold_in, generator_from_key, key, split
 from opake_amd.types import (
     ClippedPytree,
