@@ -494,8 +494,12 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
         plan_pack = in ? args.grp.steps[2 * (step0 + sl) + 1] : 0;
         plan_sc = in ? args.grp.seg_scale[plan_pack >> 7] : 0.0f;
       } else {
-        plan_ex = sl < nactive ? plan.active[sl] : 0;
-        plan_sc = sl < nactive ? args.scale[plan_ex] : 0.0f;
+        // Only the fast list's slots (the front nfast entries) are walked
+        // here; the entries between it and the slow list at the back are
+        // not written by the plan builder, so neither they nor the scales
+        // they would index are read.
+        plan_ex = sl < nfast ? plan.active[sl] : 0;
+        plan_sc = sl < nfast ? args.scale[plan_ex] : 0.0f;
       }
     };
     // Dense: step t covers rows [active[t / spe] * T + (t % spe) * 64, +64).

@@ -467,6 +467,37 @@ def test_clipped_sum_slow_plan_slots(dev, case):
     torch.testing.assert_close(cf.norms.cpu().double(), res.norms, rtol=2e-2, atol=0)
 
 
+def test_clipped_sum_ignores_the_plan_gap(dev):
+    """A plan with fast, slow and zero-scale examples leaves entries between
+    its two lists unwritten (the buffer is not cleared).  The GEMM reads
+    neither them nor the scales they would index: with the gap filled with an
+    out-of-range index the sum still matches the fp64 reference built from
+    the device's scales."""
+    B, T, din, dout = 6, 128, 256, 264
+    g = _gen(93)
+    A = torch.randn(B, T, din, generator=g).to(torch.bfloat16)
+    G = (torch.randn(B, T, dout, generator=g) * 0.01).to(torch.bfloat16)
+    A_d, G_d = A.to(dev), G.to(dev)
+    sq, err = ops.gram_sqnorms(A_d, G_d, return_error=True)
+    sq[1] = 1e42  # scale ~1e-21 < 2^-64: the slow list
+    sq[3] = float("nan")  # scale 0: in neither list
+    from opake_amd.clipping import guard_for_linear
+    cf = ops.clip_factors(sq, num.conservative_bound(1.0),
+                          [guard_for_linear(A.dtype, din, dout, False)], err=err,
+                          count_threshold=num.float32_of(1.0))
+    plan = cf.plan[0].view(torch.int32)
+    nactive, nfast = int(plan[0]), int(plan[1])
+    assert (nactive, nfast) == (B - 1, B - 2)
+    nslow = nactive - nfast
+    plan[4 + nfast:4 + B - nslow] = 0x7FFFFFFF  # the gap: one entry here
+    torch.cuda.synchronize()
+    w, _ = ops.clipped_sum(A_d, G_d, cf.scale[0], plan=cf.plan[0], out_dtype=torch.float32)
+    s = cf.scale[0].cpu().double()
+    assert s[3] == 0 and 0 < s[1] < 2.0 ** -64
+    want = torch.einsum("b,btm,btk->mk", s, G.double(), A.double())
+    assert _rel_err(w.cpu(), want) < 2e-2
+
+
 @pytest.mark.parametrize("B,T,din,dout", [(8, 256, 512, 264), (16, 128, 256, 256)])
 def test_clipped_sum_split_k(dev, B, T, din, dout):
     """Launches of few output tiles split their K steps (2-8 slices through the
