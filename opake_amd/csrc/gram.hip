@@ -25,6 +25,7 @@
 // the "both Gram matrices" body for A's K range, then a "G G^T only" body
 // that stages G's tiles alone).  The grouped (MoE) kernel runs items of one
 // tile pair on 4 waves.
+#include <atomic>
 #include <mutex>
 
 #include <algorithm>
@@ -2180,17 +2181,19 @@ namespace {
 // Compute units per XCD of the current device (cached per device; 32 on
 // MI355X: 256 CUs in 8 XCDs).
 int cus_per_xcd() {
-  static int cached[64];
+  static std::atomic<int> cached[64];  // 0: not read yet (threads may race to fill it)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 32;
-  if (cached[dev] == 0) {
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus < kXcds)
       cus = 32 * kXcds;
-    cached[dev] = cus / kXcds;
+    v = cus / kXcds;
+    cached[dev].store(v, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return v;
 }
 
 constexpr int kMaxDevices = 64;
