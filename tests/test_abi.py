@@ -83,3 +83,24 @@ def test_err_less_accumulation_must_be_explicit():
         ops._wants_error(out, None, None)
     with pytest.raises(ConfigurationError, match="return_error=False"):
         ops._wants_error(out, err, False)
+
+
+def _kernarg_setting(env_value):
+    """HIP_FORCE_DEV_KERNARG as seen after `import opake_amd` in a fresh
+    interpreter whose environment holds `env_value` (None: unset)."""
+    import os
+    import subprocess
+    import sys
+
+    env = {k: v for k, v in os.environ.items() if k != "HIP_FORCE_DEV_KERNARG"}
+    if env_value is not None:
+        env["HIP_FORCE_DEV_KERNARG"] = env_value
+    code = "import os, opake_amd; print(os.environ.get('HIP_FORCE_DEV_KERNARG'))"
+    out = subprocess.run([sys.executable, "-c", code], env=env, check=True, text=True,
+                         capture_output=True, cwd=Path(__file__).resolve().parents[1])
+    return out.stdout.strip()
+
+
+def test_import_asks_for_device_kernel_arguments_unless_set():
+    assert _kernarg_setting(None) == "1"
+    assert _kernarg_setting("0") == "0"
