@@ -424,7 +424,7 @@ def run_moe(args) -> dict:
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "clipped_sum_bf16_kernel<true> (grouped; 2 grouped GEMMs per step, "
+            "kernel": "clipped_sum_bf16_kernel<true, false> (grouped; 2 grouped GEMMs per step, "
                       "one launch each)",
             "achieved": gemm_tflops,
             "peak": MFMA_BF16_PEAK_TFLOPS,
@@ -582,7 +582,7 @@ def run_block(args) -> dict:
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "clipped_sum_bf16_kernel<false> (dpc_clipped_sum_multi: the 4 "
+            "kernel": "clipped_sum_bf16_kernel<false, false> (dpc_clipped_sum_multi: the 4 "
                       "linear layers' 1024 output tiles in one launch per step)",
             "achieved": gemm_tflops,
             "peak": MFMA_BF16_PEAK_TFLOPS,

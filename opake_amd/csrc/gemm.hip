@@ -42,6 +42,7 @@
 //     every transfer is in range and a lane's DMA offsets are fixed;
 //   * workgroup ids are remapped so that each of the 8 XCDs owns a compact
 //     block of output tiles and re-reads operand tiles from its own L2.
+#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -363,7 +364,7 @@ __shared__ __attribute__((aligned(16))) uint8_t lds_a1[kOperandBytes];
 // higher clock than 32x32x16 on the same data, and 8 waves measure faster
 // than 4 waves of 128 x 128 whose 256 accumulators per lane leave too few
 // registers for the pipeline.)
-template <bool kGrouped, bool kGdma, int kWaves>
+template <bool kGrouped, bool kGdma, int kWaves, bool kHalfDma = false>
 __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
   constexpr int kT = kWaves * 64;           // threads
   constexpr int kWavesN = kWaves / 2;       // waves along the tile columns
@@ -375,6 +376,9 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
   constexpr int kGC = kBK / kRowsPerPass;   // G chunks per thread per K step
   constexpr int kGCSub = kGC / 4;           // ... stored per phase
   constexpr int kDma = 32 / kWaves;         // 1 KiB A transfers per wave per K step
+  // kHalfDma's DMA waves step kWaves rows per instruction: the same swizzle
+  // (row & 7) for every instruction needs kWaves % 8 == 0.
+  static_assert(!kHalfDma || (!kGrouped && kWaves % 8 == 0), "half-wave DMAs: dense, 8k waves");
   int M = args.ep.M, N = args.ep.N;
   const int T = args.T;
   int lin = xcd_linear_id(gridDim.x);
@@ -559,18 +563,41 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
     const int dma_col = tile_slot_col(dma_row, lane & 31);
     const int dma_voff = dma_row * N * 2 + (kGrouped ? n0 + dma_col : min(n0 + dma_col, N - 8)) * 2;
     const int dma_bad = (kGrouped && n0 + dma_col >= N) ? kOutOfRange : 0;
+    // Dense mode with kHalfDma: the first half of the waves issues all the
+    // transfers, as if the workgroup had kWaves / 2 waves (wave w's
+    // instruction j fills tile rows 2 w + kWaves j and the next: the same
+    // swizzle, row & 7, for every j), so the other half never stalls issuing
+    // one.  Measured faster for launches of one round of workgroups (config
+    // 2: GEMM 6 us less) and slower for four rounds (config 3: +1%), so the
+    // host picks it by the number of rounds.
     auto dma_a = [&](uint8_t* astage, int row0, int valid) __attribute__((always_inline)) {
+      if constexpr (kGrouped) {
 #pragma unroll
-      for (int j = 0; j < kDma; ++j) {
-        auto* dst = (__attribute__((address_space(3))) void*)((lds_u8_t*)astage +
-                                                               (w + kWaves * j) * 1024);
-        const int rows = row0 + 2 * kWaves * j;
-        if constexpr (kGrouped) {
+        for (int j = 0; j < kDma; ++j) {
+          auto* dst = (__attribute__((address_space(3))) void*)((lds_u8_t*)astage +
+                                                                 (w + kWaves * j) * 1024);
+          const int rows = row0 + 2 * kWaves * j;
           const int bad = dma_row >= valid - 2 * kWaves * j ? kOutOfRange : dma_bad;
           __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, dst, 16, (rows * N * 2 + dma_voff) | bad,
                                                    0, 0, 0);
-        } else {
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, dst, 16, dma_voff, rows * N * 2, 0, 0);
+        }
+      } else if constexpr (kHalfDma) {
+        if (w < kWaves / 2) {
+#pragma unroll
+          for (int j = 0; j < 2 * kDma; ++j) {
+            auto* dst = (__attribute__((address_space(3))) void*)((lds_u8_t*)astage +
+                                                                   (w + kWaves / 2 * j) * 1024);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, dst, 16, dma_voff,
+                                                     (row0 + kWaves * j) * N * 2, 0, 0);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kDma; ++j) {
+          auto* dst = (__attribute__((address_space(3))) void*)((lds_u8_t*)astage +
+                                                                 (w + kWaves * j) * 1024);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, dst, 16, dma_voff,
+                                                   (row0 + 2 * kWaves * j) * N * 2, 0, 0);
         }
       }
     };
@@ -582,17 +609,33 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
         dma_row * M * 2 + (kGrouped ? m0 + dma_col : min(m0 + dma_col, M - 8)) * 2;
     const int gdma_bad = (kGrouped && m0 + dma_col >= M) ? kOutOfRange : 0;
     auto dma_g = [&](uint8_t* gstage, int row0, int valid) __attribute__((always_inline)) {
+      if constexpr (kGrouped) {
 #pragma unroll
-      for (int j = 0; j < kDma; ++j) {
-        auto* dst = (__attribute__((address_space(3))) void*)((lds_u8_t*)gstage +
-                                                               (w + kWaves * j) * 1024);
-        const int rows = row0 + 2 * kWaves * j;
-        if constexpr (kGrouped) {
+        for (int j = 0; j < kDma; ++j) {
+          auto* dst = (__attribute__((address_space(3))) void*)((lds_u8_t*)gstage +
+                                                                 (w + kWaves * j) * 1024);
+          const int rows = row0 + 2 * kWaves * j;
           const int bad = dma_row >= valid - 2 * kWaves * j ? kOutOfRange : gdma_bad;
           __builtin_amdgcn_raw_ptr_buffer_load_lds(g_rsrc, dst, 16,
                                                    (rows * M * 2 + gdma_voff) | bad, 0, 0, 0);
-        } else {
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(g_rsrc, dst, 16, gdma_voff, rows * M * 2, 0, 0);
+        }
+      } else if constexpr (kHalfDma) {
+        if (w < kWaves / 2) {
+#pragma unroll
+          for (int j = 0; j < 2 * kDma; ++j) {
+            auto* dst = (__attribute__((address_space(3))) void*)((lds_u8_t*)gstage +
+                                                                   (w + kWaves / 2 * j) * 1024);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(g_rsrc, dst, 16, gdma_voff,
+                                                     (row0 + kWaves * j) * M * 2, 0, 0);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kDma; ++j) {
+          auto* dst = (__attribute__((address_space(3))) void*)((lds_u8_t*)gstage +
+                                                                 (w + kWaves * j) * 1024);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(g_rsrc, dst, 16, gdma_voff,
+                                                   (row0 + 2 * kWaves * j) * M * 2, 0, 0);
         }
       }
     };
@@ -805,8 +848,14 @@ __device__ __forceinline__ void clipped_sum_tile(const FastArgs& args) {
 #pragma unroll
         for (int j = 0; j < kGC; ++j) load_chunk(row_next, valid_next, j);
       }
-      // Step 0's transfers have landed (step 1's DMAs and G loads may not).
-      DPC_WAIT_VMCNT(kGdma ? kDma : kDma + kGC);
+      // Step 0's transfers have landed (step 1's DMAs and G loads may not;
+      // with kHalfDma a DMA wave has 2 kDma of step 1's in flight, the
+      // others none).
+      if constexpr (kHalfDma) {
+        DPC_WAIT_VMCNT(2 * kDma);
+      } else {
+        DPC_WAIT_VMCNT(kGdma ? kDma : kDma + kGC);
+      }
       __syncthreads();
       read_g16(g0, 0, 0, gf0);
       read_a16(lds_a0, 0, af0);
@@ -1018,7 +1067,7 @@ __device__ __forceinline__ bool grouped_scales_fit(const FastArgs& args) {
 // Dense mode: G by DMA.  Grouped mode: one launch in which each workgroup
 // takes the body that matches its problem's scales (both bodies share the
 // LDS arrays).
-template <bool kGrouped>
+template <bool kGrouped, bool kHalfDma = false>
 __global__ void __launch_bounds__(kFastWaves * 64, 1) clipped_sum_bf16_kernel(FastArgs args) {
   if constexpr (kGrouped) {
     if (grouped_scales_fit(args))
@@ -1026,13 +1075,35 @@ __global__ void __launch_bounds__(kFastWaves * 64, 1) clipped_sum_bf16_kernel(Fa
     else
       clipped_sum_tile<true, false, kFastWaves>(args);
   } else {
-    clipped_sum_tile<false, true, kFastWaves>(args);
+    clipped_sum_tile<false, true, kFastWaves, kHalfDma>(args);
   }
 }
 
+// Compute units of the current device (cached per device; 256 if unknown).
+int device_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        v <= 0)
+      v = 256;
+    cached[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
+// Dense launches of at most one workgroup per compute unit take the
+// half-wave DMA body (see clipped_sum_tile).
 template <bool kGrouped>
 void launch_fast(dim3 grid, hipStream_t s, const FastArgs& args) {
-  hipLaunchKernelGGL((clipped_sum_bf16_kernel<kGrouped>), grid, dim3(kFastWaves * 64), 0, s, args);
+  if (!kGrouped && (int)grid.x <= device_cus())
+    hipLaunchKernelGGL((clipped_sum_bf16_kernel<false, true>), grid, dim3(kFastWaves * 64), 0, s,
+                       args);
+  else
+    hipLaunchKernelGGL((clipped_sum_bf16_kernel<kGrouped>), grid, dim3(kFastWaves * 64), 0, s,
+                       args);
 }
 
 // Split-K finish: out = epilogue(sum over splits of partial[split], in
